@@ -1,0 +1,292 @@
+/*
+ * q38m -- MI355X-native quantized MoE data plane, C ABI.
+ *
+ * Drop-in boundary for the executor's MoE step (reference caller:
+ * run_moe, cuda/cuda_backend.cu:1516-1605).  Conventions follow the
+ * reference headers: bf16 values travel as raw uint16_t words
+ * (include/q38/cuda_kernels.h:11-12), the stream is an opaque void* and
+ * the device an int so callers never include vendor headers
+ * (include/q38/cuda_transport.h:25-26), every pointer is a device
+ * pointer, the caller owns every buffer and no function allocates
+ * (include/q38/cuda_moe_prefill.h:95-97).  All compute entry points are
+ * asynchronous on the given stream and never read back to the host.
+ *
+ * Errors: every function returns Q38M_OK or an error code; the message
+ * of the last failure on the calling thread is q38m_last_error().  The
+ * C++ wrapper (q38m.hpp) rethrows invalid arguments as
+ * std::invalid_argument and device errors as std::runtime_error, as the
+ * reference does (cuda/q38_moe_prefill.cu:33-68).  Data errors found on
+ * the device (invalid expert id) are reported in the plan header's
+ * status word without a host sync (cuda/q38_moe_prefill.cu:163-191).
+ *
+ * Number formats (the arithmetic contract; bit-exact against the CPU
+ * oracle): int8 per-token activations (s = absmax/127, q = rint(x/s)),
+ * W4 symmetric group-32 or W8 symmetric per-output-channel weights with
+ * fp16 scales, int32 accumulators per group, fp32 epilogue in a fixed
+ * order, bf16 outputs.
+ */
+#ifndef Q38M_H
+#define Q38M_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define Q38M_OK 0
+#define Q38M_ERR_INVALID_ARGUMENT 1
+#define Q38M_ERR_DEVICE 2
+#define Q38M_ERR_UNSUPPORTED 3
+
+/* ---- routing constants: include/q38/cuda_moe_prefill.h:11-16 --------- */
+#define Q38M_ROUTE_EXPERTS 512u
+#define Q38M_ROUTE_TOPK 10u
+#define Q38M_MMQ_M 16u
+#define Q38M_PREFILL_SLAB_MAX_TOKENS 512u
+#define Q38M_ROUTE_PLAN_MAGIC_V1 0x52383351u /* "Q38R" */
+#define Q38M_ROUTE_PLAN_VERSION_V1 1u
+/* Model widths this build's kernels are instantiated for. */
+#define Q38M_HIDDEN 2048u
+#define Q38M_INTERMEDIATE 512u
+
+/* Q38RoutePlanStatusV1, include/q38/cuda_moe_prefill.h:18-22 */
+#define Q38M_PLAN_OK 0u
+#define Q38M_PLAN_INVALID_EXPERT 1u
+#define Q38M_PLAN_INVALID_SHAPE 2u
+
+/* q38m_moe_build_route_plan_v1 flags */
+#define Q38M_PLAN_FLAG_HASHES 1u /* also compute the FNV-1a route/plan hashes */
+
+/* ---- plan ABI (byte-identical to the reference V1 layout) ------------ */
+/* Q38ExpertMmqTaskV1, include/q38/cuda_moe_prefill.h:24-31 */
+typedef struct __attribute__((aligned(8))) q38m_task_v1 {
+    uint32_t packed_begin;
+    uint16_t expert;
+    uint8_t valid_rows;
+    uint8_t flags;
+} q38m_task_v1;
+
+/* Q38RoutePlanHeaderV1, include/q38/cuda_moe_prefill.h:33-48 */
+typedef struct __attribute__((aligned(16))) q38m_route_plan_header_v1 {
+    uint32_t magic;
+    uint32_t version;
+    uint32_t tokens;
+    uint32_t routes;
+    uint32_t active_experts;
+    uint32_t task_count;
+    uint32_t status;
+    uint32_t flags;
+    uint64_t route_hash;
+    uint64_t plan_hash;
+    uint64_t reserved0;
+    uint64_t reserved1;
+} q38m_route_plan_header_v1;
+
+/* Q38RoutePlanStorageV1, include/q38/cuda_moe_prefill.h:50-58 */
+typedef struct q38m_route_plan_v1 {
+    q38m_route_plan_header_v1* header;
+    uint16_t* expert_counts;        /* [512] */
+    uint32_t* expert_offsets;       /* [513] */
+    uint32_t* expert_task_offsets;  /* [513] */
+    uint32_t* packed_assignment;    /* [routes] expert-major, stable */
+    uint32_t* assignment_to_packed; /* [routes] inverse */
+    q38m_task_v1* tasks;            /* [max_tasks] M=16 tiles */
+} q38m_route_plan_v1;
+
+/* ---- expert weight descriptor ---------------------------------------- */
+/* Generalises DeviceWeightFormatV1 (include/q38/device_artifact.h:12-18)
+ * and CudaTensorViewV1/CudaWeightLayoutV1 (include/q38/cuda_weights.h:
+ * 21-38) with the group size and scale dtype of this build's formats. */
+#define Q38M_FORMAT_W4_SYM 2u /* int4 two's complement, even k in the low nibble */
+#define Q38M_FORMAT_W8_SYM 3u /* int8 */
+#define Q38M_SCALE_F16 1u
+#define Q38M_LAYOUT_ROW_MAJOR 0u /* canonical artifact layout */
+#define Q38M_LAYOUT_MFMA16 2u    /* device layout for the 16x16 int8 MFMA kernels */
+
+typedef struct q38m_expert_weights_v1 {
+    const void* data;
+    const void* scales;
+    uint32_t format;      /* Q38M_FORMAT_* */
+    uint32_t group_size;  /* 32, or 0 = one scale per output channel */
+    uint32_t scale_dtype; /* Q38M_SCALE_F16 */
+    uint32_t layout;      /* Q38M_LAYOUT_* */
+    uint32_t experts;     /* 512 */
+    uint32_t rows;        /* output channels: 2*I for gate/up, H for down */
+    uint32_t columns;     /* K: H for gate/up, I for down */
+} q38m_expert_weights_v1;
+
+/* Row-major layouts (artifact): W4 data [E][rows][cols/2], W8 data
+ * [E][rows][cols]; fp16 scales [E][rows][cols/32] (group 32) or [E][rows]
+ * (per channel).  MFMA16 layouts (produced by q38m_repack_expert_weights):
+ *   W4 g32 data  [E][rows/16][cols/128][64 lanes][16 B]; lane l = (q=l/16,
+ *     n=l%16) holds for row 16t+n and groups 4kq+j (j=0..3) one dword each:
+ *     byte i = nib(k0+i) | nib(k0+4+i)<<4, k0 = 32(4kq+j)+8q.
+ *   W4 g32 scales [E][rows/16][cols/128][16 rows][4 groups] fp16.
+ *   W8 data  [E][rows/16][cols/64][64 lanes][16 B]; lane l holds row 16t+n,
+ *     columns 64kb+16q .. +15.   W8 per-channel scales stay [E][rows]. */
+
+/* ---- sizes: include/q38/cuda_moe_prefill.h:73-93 --------------------- */
+uint32_t q38m_moe_prefill_routes_v1(uint32_t tokens);
+uint32_t q38m_moe_prefill_max_tasks_v1(uint32_t tokens);
+size_t q38m_moe_route_plan_bytes_v1(uint32_t tokens);
+
+/* cuda_moe_route_plan_storage_v1, include/q38/cuda_moe_prefill.h:98-99
+ * (cuda/q38_moe_prefill.cu:635-663).  Binds views; never touches memory. */
+int q38m_moe_route_plan_storage_v1(void* allocation, size_t allocation_bytes,
+                                   uint32_t tokens, q38m_route_plan_v1* out);
+
+/* cuda_topk_router_bf16, include/q38/cuda_kernels.h:83-91, with fp32
+ * logits (the BASELINE router output).  Experts must be a multiple of 64
+ * and <= 1024; top_k <= 32. */
+int q38m_topk_router_f32(const float* logits, int32_t* expert_ids,
+                         float* expert_weights, uint32_t tokens,
+                         uint32_t experts, uint32_t top_k, int normalize_top_k,
+                         void* stream, int device);
+
+/* cuda_moe_build_route_plan_v1, include/q38/cuda_moe_prefill.h:101-104.
+ * flags: Q38M_PLAN_FLAG_HASHES computes route_hash/plan_hash exactly as the
+ * reference (a serial pass); without it both hashes are 0. */
+int q38m_moe_build_route_plan_v1(const int32_t* expert_ids, uint32_t tokens,
+                                 const q38m_route_plan_v1* plan, uint32_t flags,
+                                 void* stream, int device);
+
+/* cuda_moe_pack_hidden_v1, include/q38/cuda_moe_prefill.h:106-110.
+ * Kept for callers of the bf16 gather; the int8 path gathers in-kernel. */
+int q38m_moe_pack_hidden_v1(const uint16_t* hidden,
+                            const uint32_t* packed_assignment, uint32_t routes,
+                            uint32_t hidden_width, uint16_t* packed_hidden,
+                            void* stream, int device);
+
+/* Per-row int8 absmax quantisation of a bf16 matrix (no reference
+ * counterpart; rounding convention of tools/q38_artifact_compiler.py:
+ * 214-222).  width is 512, 1024, 2048 or 4096. */
+int q38m_quantize_rows_i8(const uint16_t* x, uint32_t rows, uint32_t width,
+                          int8_t* q, float* scales, void* stream, int device);
+
+/* out = bf16(a + b), the residual add between stacked MoE layers (the
+ * caller's side of the step; cf. the hyper-connection finish around
+ * run_moe, cuda/cuda_backend.cu:1967-1971).  elements % 8 == 0. */
+int q38m_residual_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* out,
+                           uint64_t elements, void* stream, int device);
+
+/* cuda_moe_grouped_gate_up_v1, include/q38/cuda_moe_prefill.h:112-118.
+ * Reads int8 token rows xq[T][H] (scales xs[T]) through packed_assignment
+ * instead of a packed bf16 copy; writes weighted_mid bf16 [routes][I] in
+ * packed order: m = bf16(bf16(silu(g)*u) * w).  gate_up: W4 g32 MFMA16. */
+int q38m_moe_grouped_gate_up_v1(const q38m_expert_weights_v1* gate_up,
+                                const int8_t* xq, const float* xs,
+                                const uint32_t* packed_assignment,
+                                const float* token_rank_weights,
+                                const q38m_task_v1* tasks, uint32_t task_count,
+                                uint16_t* weighted_mid, void* stream, int device);
+
+/* cuda_moe_grouped_down_v1, include/q38/cuda_moe_prefill.h:120-125.
+ * Input: the int8 quantised weighted_mid rows (q38m_quantize_rows_i8).
+ * Output: route_output fp32 [routes][H] in packed order.  down: W8
+ * per-channel or W4 g32, MFMA16 layout. */
+int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down,
+                             const int8_t* mid_q, const float* mid_scales,
+                             const q38m_task_v1* tasks, uint32_t task_count,
+                             float* route_output, void* stream, int device);
+
+/* cuda_moe_reduce_top10_and_combine_shared_v1,
+ * include/q38/cuda_moe_prefill.h:127-131.  shared_output/shared_gate may
+ * both be NULL (no shared expert). */
+int q38m_moe_reduce_top10_and_combine_shared_v1(
+    const float* route_output, const uint32_t* assignment_to_packed,
+    const uint16_t* shared_output, const uint16_t* shared_gate,
+    uint32_t tokens, uint16_t* output, void* stream, int device);
+
+/* cuda_moe_combine_shared_bf16, include/q38/cuda_moe.h:31-37. */
+int q38m_moe_combine_shared_bf16(const uint16_t* routed_output,
+                                 const uint16_t* shared_output,
+                                 const uint16_t* shared_gate, uint16_t* output,
+                                 uint32_t tokens, void* stream, int device);
+
+/* ---- the whole step (the run_moe sequence, cuda_backend.cu:1523-1601) */
+/* Workspace of the whole step, bound once for max_tokens (the reference's
+ * MoE workspace, cuda/cuda_backend.cu:908-946); any slab of
+ * tokens <= max_tokens reuses it. */
+typedef struct q38m_prefill_workspace_v1 {
+    uint32_t max_tokens;
+    q38m_route_plan_v1 plan; /* bound for max_tokens */
+    int32_t* expert_ids;     /* [T*10] */
+    float* expert_weights;   /* [T*10] */
+    int8_t* xq;              /* [T][H] */
+    float* xs;               /* [T] */
+    uint16_t* weighted_mid;  /* [T*10][I] */
+    int8_t* mid_q;           /* [T*10][I] */
+    float* mid_s;            /* [T*10] */
+    float* route_output;     /* [T*10][H] */
+} q38m_prefill_workspace_v1;
+
+/* Bytes of one contiguous workspace for `tokens` (<= 512) and its binding
+ * (allocation 256-byte aligned). */
+size_t q38m_moe_prefill_workspace_bytes(uint32_t tokens);
+int q38m_moe_prefill_workspace_bind(void* allocation, size_t bytes,
+                                    uint32_t tokens,
+                                    q38m_prefill_workspace_v1* out);
+
+/* One MoE layer over a slab of <= 512 tokens: top-k (when logits is not
+ * NULL; else expert_ids/expert_weights in the workspace are inputs),
+ * route plan, int8 quantisation, grouped gate/up, mid quantisation,
+ * grouped down, fixed-order combine. */
+int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up,
+                        const q38m_expert_weights_v1* down,
+                        const uint16_t* hidden, const float* logits,
+                        uint32_t tokens, const q38m_prefill_workspace_v1* ws,
+                        const uint16_t* shared_output,
+                        const uint16_t* shared_gate, uint16_t* output,
+                        void* stream, int device);
+
+/* ---- batch-1 decode: cuda_moe_routed_bf16 (include/q38/cuda_moe.h:
+ * 17-29) tokens == 1 branch.  Streams only the top_k selected experts.
+ * Bit-identical to q38m_moe_prefill_v1 with tokens == 1.  scratch:
+ * q38m_moe_decode_scratch_bytes() bytes, 16-aligned. */
+size_t q38m_moe_decode_scratch_bytes(void);
+int q38m_moe_routed_decode_v1(const q38m_expert_weights_v1* gate_up,
+                              const q38m_expert_weights_v1* down,
+                              const uint16_t* hidden,
+                              const int32_t* expert_ids,
+                              const float* expert_weights, uint32_t top_k,
+                              void* scratch, uint16_t* routed_output,
+                              void* stream, int device);
+
+/* ---- weight layout (cuda/cuda_weights.cu:229-285 re-tiles W4 at load) */
+size_t q38m_expert_weights_bytes(const q38m_expert_weights_v1* w,
+                                 size_t* scale_bytes);
+/* Converts row-major weights into the MFMA16 device layout.  dst
+ * describes the destination buffers (layout MFMA16, same shape/format). */
+int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
+                               const q38m_expert_weights_v1* dst,
+                               void* stream, int device);
+
+/* ---- deterministic synthetic data (counter-based SplitMix64) --------- */
+#define Q38M_SYNTH_NORMAL_F32 1u     /* sigma*N(0,1) (+ bias[i % bias_len]) */
+#define Q38M_SYNTH_NORMAL_BF16 2u    /* bf16(sigma*N(0,1)) */
+#define Q38M_SYNTH_ABS_NORMAL_F16 3u /* f16(|sigma*N(0,1)|) */
+#define Q38M_SYNTH_UNIFORM_W4 4u     /* int4 uniform in [lo,hi], packed pairs */
+#define Q38M_SYNTH_UNIFORM_I8 5u     /* int8 uniform in [lo,hi] */
+int q38m_synth_fill(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count,
+                    float sigma, int32_t lo, int32_t hi, const float* bias,
+                    uint32_t bias_len, void* out, void* stream, int device);
+
+/* cuda_q38_moe_prefill_compiled / cuda_q38_moe_compiled */
+int q38m_moe_compiled(void);
+const char* q38m_last_error(void);
+
+/* Kernel-level self checks used by the tests: the contract's exp and the
+ * int8 MFMA lane layout (one 16x16x32 product, A and B row-major). */
+int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream,
+                    int device);
+int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d,
+                                void* stream, int device);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,428 @@
+// C ABI of the q38m MoE data plane: argument validation, device selection,
+// error reporting and launch sequencing.  Kernels live in the other
+// translation units behind q38m_internal.h.
+//
+// Validation mirrors the reference host wrappers
+// (cuda/q38_moe_prefill.cu:33-68, :635-866; cuda/q38_moe.cu:352-501):
+// invalid arguments return Q38M_ERR_INVALID_ARGUMENT (the reference throws
+// std::invalid_argument), launch failures Q38M_ERR_DEVICE (std::runtime_error).
+#include <stdint.h>
+
+#include <string>
+
+#include "q38m_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* message) {
+    g_last_error = message;
+    return code;
+}
+
+int device_fail(hipError_t status, const char* operation) {
+    g_last_error = std::string(operation) + ": " + hipGetErrorString(status);
+    return Q38M_ERR_DEVICE;
+}
+
+int select_device(int device) {
+    if (device < 0) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid q38m device");
+    const hipError_t status = hipSetDevice(device);
+    if (status != hipSuccess) return device_fail(status, "hipSetDevice(q38m)");
+    return Q38M_OK;
+}
+
+int finish(hipError_t status, const char* operation) {
+    if (status != hipSuccess) return device_fail(status, operation);
+    g_last_error.clear();
+    return Q38M_OK;
+}
+
+hipStream_t as_stream(void* stream) { return reinterpret_cast<hipStream_t>(stream); }
+
+bool aligned(const void* p, uintptr_t alignment) {
+    return (reinterpret_cast<uintptr_t>(p) % alignment) == 0u;
+}
+
+size_t align_up(size_t value, size_t alignment) {
+    return (value + alignment - 1u) / alignment * alignment;
+}
+
+bool valid_plan(const q38m_route_plan_v1* plan) {
+    return plan && plan->header && plan->expert_counts && plan->expert_offsets &&
+           plan->expert_task_offsets && plan->packed_assignment &&
+           plan->assignment_to_packed && plan->tasks;
+}
+
+// Shape/format checks of validate_expert_tensor (q38_moe_prefill.cu:51-62)
+// for this build's formats.
+bool valid_gate_up(const q38m_expert_weights_v1* w) {
+    return w && w->data && w->scales && aligned(w->data, 16) && aligned(w->scales, 8) &&
+           w->format == Q38M_FORMAT_W4_SYM && w->group_size == 32u &&
+           w->scale_dtype == Q38M_SCALE_F16 && w->layout == Q38M_LAYOUT_MFMA16 &&
+           w->experts == Q38M_ROUTE_EXPERTS && w->rows == 2u * Q38M_INTERMEDIATE &&
+           w->columns == Q38M_HIDDEN;
+}
+
+bool valid_down(const q38m_expert_weights_v1* w) {
+    if (!w || !w->data || !w->scales || !aligned(w->data, 16) || !aligned(w->scales, 8) ||
+        w->scale_dtype != Q38M_SCALE_F16 || w->layout != Q38M_LAYOUT_MFMA16 ||
+        w->experts != Q38M_ROUTE_EXPERTS || w->rows != Q38M_HIDDEN ||
+        w->columns != Q38M_INTERMEDIATE)
+        return false;
+    return (w->format == Q38M_FORMAT_W8_SYM && w->group_size == 0u) ||
+           (w->format == Q38M_FORMAT_W4_SYM && w->group_size == 32u);
+}
+
+int check_weights(const q38m_expert_weights_v1* w, bool gate_up) {
+    if (w && w->layout == Q38M_LAYOUT_ROW_MAJOR)
+        return fail(Q38M_ERR_UNSUPPORTED,
+                    "q38m kernels read the MFMA16 layout; convert with q38m_repack_expert_weights");
+    if (gate_up ? !valid_gate_up(w) : !valid_down(w))
+        return fail(Q38M_ERR_INVALID_ARGUMENT,
+                    gate_up ? "invalid grouped gate/up expert tensor"
+                            : "invalid grouped down expert tensor");
+    return Q38M_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t q38m_moe_prefill_routes_v1(uint32_t tokens) { return q38m::routes_v1(tokens); }
+
+uint32_t q38m_moe_prefill_max_tasks_v1(uint32_t tokens) { return q38m::max_tasks_v1(tokens); }
+
+size_t q38m_moe_route_plan_bytes_v1(uint32_t tokens) {
+    const size_t routes = q38m::routes_v1(tokens);
+    return sizeof(q38m_route_plan_header_v1) + Q38M_ROUTE_EXPERTS * sizeof(uint16_t) +
+           2u * (Q38M_ROUTE_EXPERTS + 1u) * sizeof(uint32_t) + 2u * routes * sizeof(uint32_t) +
+           static_cast<size_t>(q38m::max_tasks_v1(tokens)) * sizeof(q38m_task_v1);
+}
+
+int q38m_moe_route_plan_storage_v1(void* allocation, size_t allocation_bytes, uint32_t tokens,
+                                   q38m_route_plan_v1* out) {
+    if (!out || !allocation || tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE route-plan allocation");
+    if (allocation_bytes < q38m_moe_route_plan_bytes_v1(tokens))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "prefill MoE route-plan allocation is too small");
+    if (!aligned(allocation, alignof(q38m_route_plan_header_v1)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "prefill MoE route-plan allocation is unaligned");
+    uint8_t* cursor = static_cast<uint8_t*>(allocation);
+    const size_t routes = q38m::routes_v1(tokens);
+    out->header = reinterpret_cast<q38m_route_plan_header_v1*>(cursor);
+    cursor += sizeof(q38m_route_plan_header_v1);
+    out->expert_counts = reinterpret_cast<uint16_t*>(cursor);
+    cursor += Q38M_ROUTE_EXPERTS * sizeof(uint16_t);
+    out->expert_offsets = reinterpret_cast<uint32_t*>(cursor);
+    cursor += (Q38M_ROUTE_EXPERTS + 1u) * sizeof(uint32_t);
+    out->expert_task_offsets = reinterpret_cast<uint32_t*>(cursor);
+    cursor += (Q38M_ROUTE_EXPERTS + 1u) * sizeof(uint32_t);
+    out->packed_assignment = reinterpret_cast<uint32_t*>(cursor);
+    cursor += routes * sizeof(uint32_t);
+    out->assignment_to_packed = reinterpret_cast<uint32_t*>(cursor);
+    cursor += routes * sizeof(uint32_t);
+    out->tasks = reinterpret_cast<q38m_task_v1*>(cursor);
+    g_last_error.clear();
+    return Q38M_OK;
+}
+
+int q38m_topk_router_f32(const float* logits, int32_t* expert_ids, float* expert_weights,
+                         uint32_t tokens, uint32_t experts, uint32_t top_k,
+                         int normalize_top_k, void* stream, int device) {
+    if (!logits || !expert_ids || !expert_weights || tokens == 0 || experts == 0 ||
+        experts % 64u != 0u || experts > 1024u || top_k == 0 || top_k > experts || top_k > 32u)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid top-k router buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_topk(logits, expert_ids, expert_weights, tokens, experts, top_k,
+                                    normalize_top_k, as_stream(stream)),
+                  "topk_kernel");
+}
+
+int q38m_moe_build_route_plan_v1(const int32_t* expert_ids, uint32_t tokens,
+                                 const q38m_route_plan_v1* plan, uint32_t flags, void* stream,
+                                 int device) {
+    if (!expert_ids || tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS ||
+        (flags & ~Q38M_PLAN_FLAG_HASHES) != 0u)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE route-plan input");
+    if (!valid_plan(plan))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "incomplete prefill MoE route-plan storage");
+    if (!aligned(plan->tasks, 8) || !aligned(plan->header, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "unaligned prefill MoE route-plan storage");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_build_plan(expert_ids, tokens, *plan,
+                                          (flags & Q38M_PLAN_FLAG_HASHES) != 0u,
+                                          as_stream(stream)),
+                  "build_plan_kernel");
+}
+
+int q38m_moe_pack_hidden_v1(const uint16_t* hidden, const uint32_t* packed_assignment,
+                            uint32_t routes, uint32_t hidden_width, uint16_t* packed_hidden,
+                            void* stream, int device) {
+    if (!hidden || !packed_assignment || routes == 0 ||
+        routes > Q38M_PREFILL_SLAB_MAX_TOKENS * Q38M_ROUTE_TOPK || routes % Q38M_ROUTE_TOPK != 0 ||
+        hidden_width == 0 || hidden_width % 8u != 0u || !packed_hidden || !aligned(hidden, 16) ||
+        !aligned(packed_hidden, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE hidden-pack input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_pack_hidden(hidden, packed_assignment, routes, hidden_width,
+                                           packed_hidden, as_stream(stream)),
+                  "pack_hidden_kernel");
+}
+
+int q38m_quantize_rows_i8(const uint16_t* x, uint32_t rows, uint32_t width, int8_t* q,
+                          float* scales, void* stream, int device) {
+    if (!x || !q || !scales || rows == 0 ||
+        (width != 512u && width != 1024u && width != 2048u && width != 4096u) ||
+        !aligned(x, 16) || !aligned(q, 8))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid int8 row quantisation input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_quantize_rows(x, rows, width, q, scales, as_stream(stream)),
+                  "quantize_rows_kernel");
+}
+
+int q38m_residual_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* out,
+                           uint64_t elements, void* stream, int device) {
+    if (!a || !b || !out || elements == 0 || elements % 8u != 0u || !aligned(a, 16) ||
+        !aligned(b, 16) || !aligned(out, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid residual add input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_residual_add(a, b, out, elements, as_stream(stream)),
+                  "residual_add_kernel");
+}
+
+int q38m_moe_grouped_gate_up_v1(const q38m_expert_weights_v1* gate_up, const int8_t* xq,
+                                const float* xs, const uint32_t* packed_assignment,
+                                const float* token_rank_weights, const q38m_task_v1* tasks,
+                                uint32_t task_count, uint16_t* weighted_mid, void* stream,
+                                int device) {
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (!xq || !xs || !packed_assignment || !token_rank_weights || !tasks || task_count == 0 ||
+        task_count > q38m::max_tasks_v1(Q38M_PREFILL_SLAB_MAX_TOKENS) || !weighted_mid ||
+        !aligned(xq, 8) || !aligned(tasks, 8))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill gate/up input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_gate_up_w4g32(gate_up->data, gate_up->scales, xq, xs,
+                                             packed_assignment, token_rank_weights, tasks,
+                                             task_count, weighted_mid, as_stream(stream)),
+                  "gate_up_w4g32_kernel");
+}
+
+int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down, const int8_t* mid_q,
+                             const float* mid_scales, const q38m_task_v1* tasks,
+                             uint32_t task_count, float* route_output, void* stream,
+                             int device) {
+    if (int rc = check_weights(down, false)) return rc;
+    if (!mid_q || !mid_scales || !tasks || task_count == 0 ||
+        task_count > q38m::max_tasks_v1(Q38M_PREFILL_SLAB_MAX_TOKENS) || !route_output ||
+        !aligned(mid_q, 16) || !aligned(tasks, 8))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill down input");
+    if (int rc = select_device(device)) return rc;
+    const hipError_t status =
+        down->format == Q38M_FORMAT_W8_SYM
+            ? q38m::launch_down_w8pc(down->data, down->scales, mid_q, mid_scales, tasks,
+                                     task_count, route_output, as_stream(stream))
+            : q38m::launch_down_w4g32(down->data, down->scales, mid_q, mid_scales, tasks,
+                                      task_count, route_output, as_stream(stream));
+    return finish(status, "grouped_down_kernel");
+}
+
+int q38m_moe_reduce_top10_and_combine_shared_v1(const float* route_output,
+                                                const uint32_t* assignment_to_packed,
+                                                const uint16_t* shared_output,
+                                                const uint16_t* shared_gate, uint32_t tokens,
+                                                uint16_t* output, void* stream, int device) {
+    if (!route_output || !assignment_to_packed || (shared_output == nullptr) != (shared_gate == nullptr) ||
+        tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS || !output ||
+        !aligned(route_output, 16) || !aligned(output, 16) ||
+        (shared_output && !aligned(shared_output, 16)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill reduction input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_combine(route_output, assignment_to_packed, shared_output,
+                                       shared_gate, tokens, output, as_stream(stream)),
+                  "combine_kernel");
+}
+
+int q38m_moe_combine_shared_bf16(const uint16_t* routed_output, const uint16_t* shared_output,
+                                 const uint16_t* shared_gate, uint16_t* output, uint32_t tokens,
+                                 void* stream, int device) {
+    if (!routed_output || !shared_output || !shared_gate || !output || tokens == 0)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid shared MoE buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_combine_shared(routed_output, shared_output, shared_gate, output,
+                                              tokens, as_stream(stream)),
+                  "combine_shared_kernel");
+}
+
+size_t q38m_moe_prefill_workspace_bytes(uint32_t tokens) {
+    if (tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS) return 0;
+    const size_t routes = q38m::routes_v1(tokens);
+    size_t bytes = align_up(q38m_moe_route_plan_bytes_v1(tokens), 256);
+    bytes += align_up(routes * 4u, 256) * 2u;                      // ids, weights
+    bytes += align_up(static_cast<size_t>(tokens) * Q38M_HIDDEN, 256);      // xq
+    bytes += align_up(static_cast<size_t>(tokens) * 4u, 256);               // xs
+    bytes += align_up(routes * Q38M_INTERMEDIATE * 2u, 256);                // weighted_mid
+    bytes += align_up(routes * Q38M_INTERMEDIATE, 256);                     // mid_q
+    bytes += align_up(routes * 4u, 256);                                    // mid_s
+    bytes += align_up(routes * Q38M_HIDDEN * 4u, 256);                      // route_output
+    return bytes;
+}
+
+int q38m_moe_prefill_workspace_bind(void* allocation, size_t bytes, uint32_t tokens,
+                                    q38m_prefill_workspace_v1* out) {
+    if (!allocation || !out || tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS ||
+        bytes < q38m_moe_prefill_workspace_bytes(tokens) || !aligned(allocation, 256))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE workspace allocation");
+    const size_t routes = q38m::routes_v1(tokens);
+    uint8_t* cursor = static_cast<uint8_t*>(allocation);
+    const size_t plan_bytes = q38m_moe_route_plan_bytes_v1(tokens);
+    if (int rc = q38m_moe_route_plan_storage_v1(cursor, plan_bytes, tokens, &out->plan)) return rc;
+    cursor += align_up(plan_bytes, 256);
+    out->max_tokens = tokens;
+    out->expert_ids = reinterpret_cast<int32_t*>(cursor);
+    cursor += align_up(routes * 4u, 256);
+    out->expert_weights = reinterpret_cast<float*>(cursor);
+    cursor += align_up(routes * 4u, 256);
+    out->xq = reinterpret_cast<int8_t*>(cursor);
+    cursor += align_up(static_cast<size_t>(tokens) * Q38M_HIDDEN, 256);
+    out->xs = reinterpret_cast<float*>(cursor);
+    cursor += align_up(static_cast<size_t>(tokens) * 4u, 256);
+    out->weighted_mid = reinterpret_cast<uint16_t*>(cursor);
+    cursor += align_up(routes * Q38M_INTERMEDIATE * 2u, 256);
+    out->mid_q = reinterpret_cast<int8_t*>(cursor);
+    cursor += align_up(routes * Q38M_INTERMEDIATE, 256);
+    out->mid_s = reinterpret_cast<float*>(cursor);
+    cursor += align_up(routes * 4u, 256);
+    out->route_output = reinterpret_cast<float*>(cursor);
+    g_last_error.clear();
+    return Q38M_OK;
+}
+
+int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert_weights_v1* down,
+                        const uint16_t* hidden, const float* logits, uint32_t tokens,
+                        const q38m_prefill_workspace_v1* ws, const uint16_t* shared_output,
+                        const uint16_t* shared_gate, uint16_t* output, void* stream, int device) {
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (int rc = check_weights(down, false)) return rc;
+    if (!hidden || !ws || !output || tokens == 0 || tokens > ws->max_tokens ||
+        !valid_plan(&ws->plan) || !ws->expert_ids || !ws->expert_weights || !ws->xq || !ws->xs ||
+        !ws->weighted_mid || !ws->mid_q || !ws->mid_s || !ws->route_output ||
+        (shared_output == nullptr) != (shared_gate == nullptr) || !aligned(hidden, 16) ||
+        !aligned(output, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE step input");
+    if (int rc = select_device(device)) return rc;
+    const hipStream_t s = as_stream(stream);
+    const uint32_t routes = q38m::routes_v1(tokens);
+    const uint32_t tasks = q38m::max_tasks_v1(tokens);
+    hipError_t status = hipSuccess;
+    if (logits)
+        status = q38m::launch_topk(logits, ws->expert_ids, ws->expert_weights, tokens,
+                                   Q38M_ROUTE_EXPERTS, Q38M_ROUTE_TOPK, 1, s);
+    if (status == hipSuccess)
+        status = q38m::launch_build_plan(ws->expert_ids, tokens, ws->plan, false, s);
+    if (status == hipSuccess)
+        status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws->xq, ws->xs, s);
+    if (status == hipSuccess)
+        status = q38m::launch_gate_up_w4g32(gate_up->data, gate_up->scales, ws->xq, ws->xs,
+                                            ws->plan.packed_assignment, ws->expert_weights,
+                                            ws->plan.tasks, tasks, ws->weighted_mid, s);
+    if (status == hipSuccess)
+        status = q38m::launch_quantize_rows(ws->weighted_mid, routes, Q38M_INTERMEDIATE,
+                                            ws->mid_q, ws->mid_s, s);
+    if (status == hipSuccess)
+        status = down->format == Q38M_FORMAT_W8_SYM
+                     ? q38m::launch_down_w8pc(down->data, down->scales, ws->mid_q, ws->mid_s,
+                                              ws->plan.tasks, tasks, ws->route_output, s)
+                     : q38m::launch_down_w4g32(down->data, down->scales, ws->mid_q, ws->mid_s,
+                                               ws->plan.tasks, tasks, ws->route_output, s);
+    if (status == hipSuccess)
+        status = q38m::launch_combine(ws->route_output, ws->plan.assignment_to_packed,
+                                      shared_output, shared_gate, tokens, output, s);
+    return finish(status, "prefill MoE step");
+}
+
+size_t q38m_moe_decode_scratch_bytes(void) { return q38m::decode_scratch_bytes(); }
+
+int q38m_moe_routed_decode_v1(const q38m_expert_weights_v1* gate_up,
+                              const q38m_expert_weights_v1* down, const uint16_t* hidden,
+                              const int32_t* expert_ids, const float* expert_weights,
+                              uint32_t top_k, void* scratch, uint16_t* routed_output,
+                              void* stream, int device) {
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (int rc = check_weights(down, false)) return rc;
+    if (!hidden || !expert_ids || !expert_weights || top_k == 0 || top_k > Q38M_ROUTE_TOPK ||
+        !scratch || !routed_output || !aligned(hidden, 16) || !aligned(scratch, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid routed MoE buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_decode(*gate_up, *down, hidden, expert_ids, expert_weights, top_k,
+                                      scratch, routed_output, as_stream(stream)),
+                  "decode routed MoE kernels");
+}
+
+size_t q38m_expert_weights_bytes(const q38m_expert_weights_v1* w, size_t* scale_bytes) {
+    if (!w || (w->format != Q38M_FORMAT_W4_SYM && w->format != Q38M_FORMAT_W8_SYM)) {
+        if (scale_bytes) *scale_bytes = 0;
+        return 0;
+    }
+    const uint64_t elements = static_cast<uint64_t>(w->experts) * w->rows * w->columns;
+    if (scale_bytes) {
+        const uint64_t scales = w->group_size ? elements / w->group_size
+                                              : static_cast<uint64_t>(w->experts) * w->rows;
+        *scale_bytes = static_cast<size_t>(scales * 2u);
+    }
+    return static_cast<size_t>(w->format == Q38M_FORMAT_W4_SYM ? elements / 2u : elements);
+}
+
+int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
+                               const q38m_expert_weights_v1* dst, void* stream, int device) {
+    if (!src || !dst || !src->data || !src->scales || !dst->data || !dst->scales ||
+        src->layout != Q38M_LAYOUT_ROW_MAJOR || dst->layout != Q38M_LAYOUT_MFMA16 ||
+        src->format != dst->format || src->group_size != dst->group_size ||
+        src->scale_dtype != Q38M_SCALE_F16 || dst->scale_dtype != Q38M_SCALE_F16 ||
+        src->experts != dst->experts || src->rows != dst->rows || src->columns != dst->columns ||
+        src->experts == 0 || src->rows % 16u != 0u || !aligned(src->data, 16) ||
+        !aligned(dst->data, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid expert weight repack");
+    const bool w4 = src->format == Q38M_FORMAT_W4_SYM && src->group_size == 32u &&
+                    src->columns % 128u == 0u;
+    const bool w8 = src->format == Q38M_FORMAT_W8_SYM && src->group_size == 0u &&
+                    src->columns % 64u == 0u;
+    if (!w4 && !w8)
+        return fail(Q38M_ERR_UNSUPPORTED, "repack supports W4 group-32 and W8 per-channel");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_repack(*src, *dst, as_stream(stream)), "repack kernels");
+}
+
+int q38m_synth_fill(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count, float sigma,
+                    int32_t lo, int32_t hi, const float* bias, uint32_t bias_len, void* out,
+                    void* stream, int device) {
+    if (!out || count == 0 || kind < Q38M_SYNTH_NORMAL_F32 || kind > Q38M_SYNTH_UNIFORM_I8 ||
+        (kind == Q38M_SYNTH_UNIFORM_W4 && (count % 2u != 0u || lo < -8 || hi > 7 || lo > hi)) ||
+        (kind == Q38M_SYNTH_UNIFORM_I8 && (lo < -128 || hi > 127 || lo > hi)) ||
+        (bias && (bias_len == 0 || kind != Q38M_SYNTH_NORMAL_F32)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid synthetic fill");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_synth(kind, seed, tag, count, sigma, lo, hi, bias, bias_len, out,
+                                     as_stream(stream)),
+                  "synth_kernel");
+}
+
+int q38m_moe_compiled(void) { return 1; }
+
+const char* q38m_last_error(void) { return g_last_error.c_str(); }
+
+int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream, int device) {
+    if (!x || !out || n == 0) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug expf input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_debug_expf(x, n, out, as_stream(stream)), "debug_expf_kernel");
+}
+
+int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d, void* stream,
+                                int device) {
+    if (!a || !b || !d) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug mfma input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_debug_mfma(a, b, d, as_stream(stream)), "debug_mfma_kernel");
+}
+
+}  // extern "C"

@@ -1,0 +1,210 @@
+// Device helpers shared by the q38m HIP kernels (gfx950 / CDNA4).
+//
+// The fp32 epilogue is part of the arithmetic contract: every kernel is
+// compiled with -ffp-contract=off and every fused multiply-add is an
+// explicit __builtin_fmaf, so the GPU performs exactly the operations of
+// the CPU restatement in the same order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "q38m.h"
+
+namespace q38m {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---- conversions ---------------------------------------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) {
+    return __uint_as_float(h << 16);
+}
+
+// Round-to-nearest-even bf16 (tools/q38_artifact_compiler.py:61-66).
+__device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+    uint32_t b = __float_as_uint(v);
+    if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 16) | 0x40u;
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return b >> 16;
+}
+
+__device__ __forceinline__ float bf16_round(float v) {
+    return bf16_to_f32(f32_to_bf16(v));
+}
+
+// Exact binary16 -> binary32 through the hardware conversion.
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
+// binary32 -> binary16, round-to-nearest-even, integer-only so the result
+// does not depend on the conversion instruction's mode bits.
+__device__ __forceinline__ uint32_t f32_to_f16(float v) {
+    const uint32_t bits = __float_as_uint(v);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const uint32_t mag = bits & 0x7fffffffu;
+    if (mag > 0x7f800000u) return sign | 0x7e00u;
+    if (mag >= 0x477ff000u) return sign | 0x7c00u;
+    if (mag >= 0x38800000u) {
+        const uint32_t rounded = mag + 0x0fffu + ((mag >> 13) & 1u);
+        return sign | ((rounded >> 13) - (112u << 10));
+    }
+    const uint32_t biased = mag >> 23;
+    if (biased == 0u) return sign;
+    const uint32_t shift = 126u - biased;
+    if (shift > 24u) return sign;
+    const uint32_t mant = (mag & 0x7fffffu) | 0x800000u;
+    uint32_t result = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (rem > half || (rem == half && (result & 1u))) ++result;
+    return sign | result;
+}
+
+// ---- the contract's exp ---------------------------------------------------
+// Cody & Waite reduction x = n*ln2 + r (ln2 split so n*ln2_hi is exact),
+// degree-7 Taylor polynomial of e^r in Horner form, exact 2^n scaling.
+// Results below the smallest normal are flushed to 0 (x < -87.3).
+__device__ __forceinline__ float exp_q(float x) {
+    if (x != x) return x + x;
+    if (x > 88.72283935546875f) return __builtin_huge_valf();
+    if (x < -87.3f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(n, -0.693145751953125f, x);
+    r = __builtin_fmaf(n, -1.42860682030941723212e-6f, r);
+    float p = 1.98412698412698412698e-4f;
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-3f);
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-2f);
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-1f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int e = static_cast<int>(n);
+    if (e > 127) return (p * 2.0f) * __uint_as_float(254u << 23);  // * 2^127
+    return p * __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+}
+
+// SwiGLU with the router-weight fold; rounding sequence of the reference
+// gate/up epilogue (cuda/q38_moe_prefill.cu:449-461).
+__device__ __forceinline__ uint32_t swiglu_fold(float y_gate, float y_up,
+                                                float weight) {
+    const float g = bf16_round(y_gate);
+    const float u = bf16_round(y_up);
+    const float e = exp_q(-g);
+    const float den = 1.0f + e;
+    const float silu = g / den;
+    const float h = bf16_round(silu * u);
+    return f32_to_bf16(h * weight);
+}
+
+// ---- int8 MFMA -------------------------------------------------------------
+// v_mfma_i32_16x16x32_i8: A 16x32 (lane l: row l%16, k 8*(l/16)..+7),
+// B 32x16 (lane l: column l%16, same k), D lane l: rows 4*(l/16)+i,
+// column l%16.  One instruction covers exactly one 32-wide scale group.
+__device__ __forceinline__ v4i mfma_i8_16x16x32(long a, long b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
+}
+
+// v_mfma_i32_16x16x64_i8 (gfx950): 16 int8 per lane per operand.
+__device__ __forceinline__ v4i mfma_i8_16x16x64(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Expands one MFMA16 W4 dword (byte i = k_i | k_{4+i} << 4) into the eight
+// int8 B-operand bytes k_0..k_7, each multiplied by 16: the nibble lands
+// in the high half of its byte, so the sign needs no extension.  The x16
+// is exact and is removed by scaling the group scale by 1/16.
+__device__ __forceinline__ long unpack_w4x16(uint32_t w) {
+    const uint32_t lo = (w << 4) & 0xf0f0f0f0u;
+    const uint32_t hi = w & 0xf0f0f0f0u;
+    return static_cast<long>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ long as_long(uint2 v) {
+    return static_cast<long>((static_cast<uint64_t>(v.y) << 32) | v.x);
+}
+
+__device__ __forceinline__ v4i as_v4i(uint4 v) {
+    v4i r;
+    r.x = static_cast<int>(v.x);
+    r.y = static_cast<int>(v.y);
+    r.z = static_cast<int>(v.z);
+    r.w = static_cast<int>(v.w);
+    return r;
+}
+
+// ---- counter-based SplitMix64 (Steele, Lea, Flood 2014) -------------------
+constexpr uint64_t kGamma = 0x9e3779b97f4a7c15ull;
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z ^= z >> 30;
+    z *= 0xbf58476d1ce4e5b9ull;
+    z ^= z >> 27;
+    z *= 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    return z;
+}
+
+__host__ __device__ inline uint64_t stream_base_host(uint64_t seed, uint64_t tag) {
+    uint64_t z = seed + kGamma * (tag + 1u);
+    z ^= z >> 30;
+    z *= 0xbf58476d1ce4e5b9ull;
+    z ^= z >> 27;
+    z *= 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    return z;
+}
+
+__device__ __forceinline__ uint64_t stream_at(uint64_t base, uint64_t counter) {
+    return mix64(base + kGamma * (counter + 1u));
+}
+
+// Natural log of a positive normal float (synthetic data only).
+__device__ __forceinline__ float log_q(float x) {
+    const uint32_t bits = __float_as_uint(x);
+    int exponent = static_cast<int>(bits >> 23) - 127;
+    float m = __uint_as_float((bits & 0x7fffffu) | 0x3f800000u);
+    if (m > 1.41421353816986083984375f) {
+        m = m * 0.5f;
+        exponent += 1;
+    }
+    const float f = m - 1.0f;
+    const float t = f / (2.0f + f);
+    const float t2 = t * t;
+    float p = 0.181818181818181818f;
+    p = __builtin_fmaf(p, t2, 0.222222222222222222f);
+    p = __builtin_fmaf(p, t2, 0.285714285714285714f);
+    p = __builtin_fmaf(p, t2, 0.4f);
+    p = __builtin_fmaf(p, t2, 0.666666666666666667f);
+    p = __builtin_fmaf(p, t2, 2.0f);
+    return __builtin_fmaf(static_cast<float>(exponent), 0.693147180559945309f, p * t);
+}
+
+// Marsaglia polar method; element i uses counters 32*i + attempt.
+__device__ __forceinline__ float normal_at(uint64_t base, uint64_t index) {
+    for (uint32_t attempt = 0; attempt < 32u; ++attempt) {
+        const uint64_t r = stream_at(base, index * 32u + attempt);
+        const int32_t ia = static_cast<int32_t>(2u * static_cast<uint32_t>(r >> 40)) - 16777215;
+        const int32_t ib =
+            static_cast<int32_t>(2u * static_cast<uint32_t>((r >> 16) & 0xffffffu)) - 16777215;
+        const float a = static_cast<float>(ia) * 5.9604644775390625e-8f;
+        const float b = static_cast<float>(ib) * 5.9604644775390625e-8f;
+        const float s = a * a + b * b;
+        if (s >= 1.0f) continue;
+        float t = -2.0f * log_q(s);
+        t = t / s;
+        t = __builtin_sqrtf(t);
+        return a * t;
+    }
+    return 0.0f;
+}
+
+__device__ __forceinline__ int uniform_at(uint64_t base, uint64_t index, int lo, int hi) {
+    const uint64_t r = stream_at(base, index);
+    const uint64_t span = static_cast<uint64_t>(static_cast<int64_t>(hi - lo + 1));
+    return lo + static_cast<int>(((r >> 32) * span) >> 32);
+}
+
+}  // namespace q38m

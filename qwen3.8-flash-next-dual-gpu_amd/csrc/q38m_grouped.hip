@@ -1,0 +1,351 @@
+// Expert-grouped prefill: gate/up (W4 g32) with fused SwiGLU and router
+// weight, down (W8 per-channel or W4 g32), and the fixed-order combine.
+//
+// Work decomposition: one workgroup per (task, output slice), where a task
+// is one M=16 tile of one expert from the V1 route plan.  Each wave owns a
+// 16-channel tile (gate/up: a gate tile and its matching up tile, so the
+// SwiGLU pair sits in the same lane) and streams the expert's weights
+// straight from HBM into VGPRs in the MFMA16 layout: every wave-wide
+// 16-byte load is 1 KiB contiguous.  Tasks beyond the plan's task_count
+// carry valid_rows == 0 and exit at once (q38_moe_prefill.cu:316-317).
+#include "q38m_device.h"
+#include "q38m_internal.h"
+
+namespace q38m {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Gate/up, W4 group-32 fp16 scales, MFMA16 layout.
+//   acc[r][j][g] = sum_{k in g} xq[token(r)][k] * W[e][j][k]        (int32)
+//   y[r][j]      = fmaf-chain over g = 0..H/32-1 of acc * s[e][j][g]  (fp32)
+//   then y * xs[token(r)] and the SwiGLU fold of the reference epilogue.
+// One v_mfma_i32_16x16x32_i8 per group gives that group's exact int32
+// tile (zero accumulator), so the fp32 chain runs in group order in the
+// same lanes that hold the accumulators.
+// ---------------------------------------------------------------------------
+template <uint32_t H, uint32_t I>
+__global__ __launch_bounds__(256) void gate_up_w4g32_kernel(
+    const uint4* __restrict__ w, const uint2* __restrict__ s,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
+    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    constexpr uint32_t kQuads = H / 128u;
+    constexpr uint32_t kTiles = 2u * I / 16u;
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t gate_tile = blockIdx.x * 4u + wave;
+    const uint32_t up_tile = gate_tile + I / 16u;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+
+    // A operand: lane (n, q) supplies token row n, bytes 8q..8q+7 of each
+    // 32-wide group.  Rows past valid_rows reuse row 0; their D rows are
+    // never stored.
+    const uint32_t a_row = n < rows ? n : 0u;
+    const uint32_t a_token = packed[p0 + a_row] / kTopK;
+    const uint2* xa = reinterpret_cast<const uint2*>(xq + static_cast<size_t>(a_token) * H) + q;
+
+    const uint4* wg = w + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 64u + lane;
+    const uint4* wu = w + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 64u + lane;
+    const uint2* sg = s + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 16u + n;
+    const uint2* su = s + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 16u + n;
+
+    float yg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float yu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const v4i zero = {0, 0, 0, 0};
+
+    uint4 bg = wg[0], bu = wu[0];
+    uint2 cg = sg[0], cu = su[0];
+    uint2 a0 = xa[0], a1 = xa[4], a2 = xa[8], a3 = xa[12];
+#pragma unroll 2
+    for (uint32_t kq = 0; kq < kQuads; ++kq) {
+        // prefetch the next quad while this one is consumed
+        const uint32_t nk = kq + 1u < kQuads ? kq + 1u : kq;
+        const uint4 nbg = wg[nk * 64u], nbu = wu[nk * 64u];
+        const uint2 ncg = sg[nk * 16u], ncu = su[nk * 16u];
+        const uint2 na0 = xa[nk * 16u], na1 = xa[nk * 16u + 4u];
+        const uint2 na2 = xa[nk * 16u + 8u], na3 = xa[nk * 16u + 12u];
+
+        const uint32_t wgw[4] = {bg.x, bg.y, bg.z, bg.w};
+        const uint32_t wuw[4] = {bu.x, bu.y, bu.z, bu.w};
+        const uint32_t sgw[2] = {cg.x, cg.y};
+        const uint32_t suw[2] = {cu.x, cu.y};
+        const long av[4] = {as_long(a0), as_long(a1), as_long(a2), as_long(a3)};
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j) {
+            const v4i dg = mfma_i8_16x16x32(av[j], unpack_w4x16(wgw[j]), zero);
+            const v4i du = mfma_i8_16x16x32(av[j], unpack_w4x16(wuw[j]), zero);
+            const uint32_t hg = (j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu);
+            const uint32_t hu = (j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu);
+            const float scale_g = f16_to_f32(hg) * 0.0625f;
+            const float scale_u = f16_to_f32(hu) * 0.0625f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                yg[i] = __builtin_fmaf(static_cast<float>(dg[i]), scale_g, yg[i]);
+                yu[i] = __builtin_fmaf(static_cast<float>(du[i]), scale_u, yu[i]);
+            }
+        }
+        bg = nbg; bu = nbu; cg = ncg; cu = ncu;
+        a0 = na0; a1 = na1; a2 = na2; a3 = na3;
+    }
+
+    const uint32_t channel = gate_tile * 16u + n;
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        const uint32_t r = 4u * q + i;
+        if (r >= rows) continue;
+        const uint32_t p = p0 + r;
+        const uint32_t a = packed[p];
+        const float st = xs[a / kTopK];
+        const float y_gate = yg[i] * st;
+        const float y_up = yu[i] * st;
+        mid[static_cast<size_t>(p) * I + channel] =
+            static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Down, W8 per output channel, MFMA16 layout (16 int8 per lane per 64-wide
+// K block).  acc = sum_k qm[r][k] * W[e][c][k] over all of K in one int32
+// (exact in fp32, |acc| < 2^24), o = ((float)acc * ws[e][c]) * sm[r].
+// Each wave keeps its 16 A rows (whole K) in registers and sweeps
+// kTilesPerWave output tiles.
+// ---------------------------------------------------------------------------
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave>
+__global__ __launch_bounds__(256) void down_w8pc_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+    const int8_t* __restrict__ mq, const float* __restrict__ ms,
+    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    constexpr uint32_t kBlocks = I / 64u;
+    constexpr uint32_t kTiles = H / 16u;
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+    const uint32_t a_row = n < rows ? n : 0u;
+    const uint4* xa = reinterpret_cast<const uint4*>(mq + static_cast<size_t>(p0 + a_row) * I) + q;
+    v4i a[kBlocks];
+#pragma unroll
+    for (uint32_t kb = 0; kb < kBlocks; ++kb) a[kb] = as_v4i(xa[kb * 4u]);
+    float row_scale[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        const uint32_t r = 4u * q + i;
+        row_scale[i] = ms[p0 + (r < rows ? r : 0u)];
+    }
+    const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
+#pragma unroll
+    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
+        const uint32_t tile = tile0 + t;
+        const uint4* wt = w + static_cast<size_t>(e * kTiles + tile) * kBlocks * 64u + lane;
+        uint4 b[kBlocks];
+#pragma unroll
+        for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = wt[kb * 64u];
+        v4i acc = {0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t kb = 0; kb < kBlocks; ++kb) acc = mfma_i8_16x16x64(a[kb], as_v4i(b[kb]), acc);
+        const uint32_t channel = tile * 16u + n;
+        const float ws = f16_to_f32(s[static_cast<size_t>(e) * H + channel]);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 4u * q + i;
+            if (r >= rows) continue;
+            const float o = (static_cast<float>(acc[i]) * ws) * row_scale[i];
+            out[static_cast<size_t>(p0 + r) * H + channel] = o;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Down, W4 group-32 (the all-W4 layer policy): the gate/up group chain over
+// K = I, then * sm[r].
+// ---------------------------------------------------------------------------
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave>
+__global__ __launch_bounds__(256) void down_w4g32_kernel(
+    const uint4* __restrict__ w, const uint2* __restrict__ s,
+    const int8_t* __restrict__ mq, const float* __restrict__ ms,
+    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    constexpr uint32_t kQuads = I / 128u;
+    constexpr uint32_t kTiles = H / 16u;
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+    const uint32_t a_row = n < rows ? n : 0u;
+    const uint2* xa = reinterpret_cast<const uint2*>(mq + static_cast<size_t>(p0 + a_row) * I) + q;
+    long a[kQuads * 4u];
+#pragma unroll
+    for (uint32_t g = 0; g < kQuads * 4u; ++g) a[g] = as_long(xa[g * 4u]);
+    float row_scale[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        const uint32_t r = 4u * q + i;
+        row_scale[i] = ms[p0 + (r < rows ? r : 0u)];
+    }
+    const v4i zero = {0, 0, 0, 0};
+    const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
+    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
+        const uint32_t tile = tile0 + t;
+        const uint4* wt = w + static_cast<size_t>(e * kTiles + tile) * kQuads * 64u + lane;
+        const uint2* st = s + static_cast<size_t>(e * kTiles + tile) * kQuads * 16u + n;
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t kq = 0; kq < kQuads; ++kq) {
+            const uint4 b = wt[kq * 64u];
+            const uint2 c = st[kq * 16u];
+            const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+            const uint32_t cw[2] = {c.x, c.y};
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j) {
+                const v4i d = mfma_i8_16x16x32(a[kq * 4u + j], unpack_w4x16(bw[j]), zero);
+                const uint32_t h = (j & 1u) ? (cw[j >> 1] >> 16) : (cw[j >> 1] & 0xffffu);
+                const float scale = f16_to_f32(h) * 0.0625f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    y[i] = __builtin_fmaf(static_cast<float>(d[i]), scale, y[i]);
+            }
+        }
+        const uint32_t channel = tile * 16u + n;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 4u * q + i;
+            if (r >= rows) continue;
+            out[static_cast<size_t>(p0 + r) * H + channel] = y[i] * row_scale[i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fixed rank-order reduce from 0.0f plus the optional gated shared term
+// (q38_moe_prefill.cu:601-631).  One workgroup per token, 8 columns/thread.
+// ---------------------------------------------------------------------------
+template <uint32_t H>
+__global__ __launch_bounds__(256) void combine_kernel(
+    const float* __restrict__ route_output, const uint32_t* __restrict__ inverse,
+    const uint16_t* __restrict__ shared_output, const uint16_t* __restrict__ shared_gate,
+    uint16_t* __restrict__ output) {
+    const uint32_t token = blockIdx.x;
+    const bool shared = shared_output != nullptr && shared_gate != nullptr;
+    float multiplier = 0.0f;
+    if (shared) {
+        const float g = bf16_to_f32(shared_gate[token]);
+        multiplier = 1.0f / (1.0f + exp_q(-g));
+    }
+    uint32_t rows[kTopK];
+#pragma unroll
+    for (uint32_t r = 0; r < kTopK; ++r) rows[r] = inverse[token * kTopK + r];
+    for (uint32_t c0 = threadIdx.x * 8u; c0 < H; c0 += 256u * 8u) {
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (uint32_t r = 0; r < kTopK; ++r) {
+            const float4* src = reinterpret_cast<const float4*>(
+                route_output + static_cast<size_t>(rows[r]) * H + c0);
+            const float4 v0 = src[0];
+            const float4 v1 = src[1];
+            acc[0] += v0.x; acc[1] += v0.y; acc[2] += v0.z; acc[3] += v0.w;
+            acc[4] += v1.x; acc[5] += v1.y; acc[6] += v1.z; acc[7] += v1.w;
+        }
+        if (shared) {
+            const uint4 sv = *reinterpret_cast<const uint4*>(
+                shared_output + static_cast<size_t>(token) * H + c0);
+            const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t h = (i & 1) ? (sw[i >> 1] >> 16) : (sw[i >> 1] & 0xffffu);
+                const float term = bf16_to_f32(h) * multiplier;
+                acc[i] = acc[i] + term;
+            }
+        }
+        uint4 packed;
+        packed.x = f32_to_bf16(acc[0]) | (f32_to_bf16(acc[1]) << 16);
+        packed.y = f32_to_bf16(acc[2]) | (f32_to_bf16(acc[3]) << 16);
+        packed.z = f32_to_bf16(acc[4]) | (f32_to_bf16(acc[5]) << 16);
+        packed.w = f32_to_bf16(acc[6]) | (f32_to_bf16(acc[7]) << 16);
+        *reinterpret_cast<uint4*>(output + static_cast<size_t>(token) * H + c0) = packed;
+    }
+}
+
+// Decode combine: routed + shared * sigmoid(gate) (q38_moe.cu:337-350).
+template <uint32_t H>
+__global__ __launch_bounds__(256) void combine_shared_kernel(
+    const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
+    const uint16_t* __restrict__ gate, uint16_t* __restrict__ output, uint64_t elements) {
+    const uint64_t index = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (index >= elements) return;
+    const float g = bf16_to_f32(gate[index / H]);
+    const float sigmoid = 1.0f / (1.0f + exp_q(-g));
+    const float term = bf16_to_f32(shared[index]) * sigmoid;
+    output[index] = static_cast<uint16_t>(f32_to_bf16(bf16_to_f32(routed[index]) + term));
+}
+
+}  // namespace
+
+hipError_t launch_gate_up_w4g32(const void* data, const void* scales,
+                                const int8_t* xq, const float* xs,
+                                const uint32_t* packed, const float* route_weights,
+                                const q38m_task_v1* tasks, uint32_t task_count,
+                                uint16_t* weighted_mid, hipStream_t stream) {
+    const dim3 grid(kInter / 64u, task_count);
+    gate_up_w4g32_kernel<kHidden, kInter><<<grid, 256, 0, stream>>>(
+        static_cast<const uint4*>(data), static_cast<const uint2*>(scales), xq, xs,
+        packed, route_weights, tasks, weighted_mid);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_w8pc(const void* data, const void* scales,
+                            const int8_t* mid_q, const float* mid_s,
+                            const q38m_task_v1* tasks, uint32_t task_count,
+                            float* route_output, hipStream_t stream) {
+    constexpr uint32_t kTilesPerWave = 4;
+    const dim3 grid(kHidden / 16u / (4u * kTilesPerWave), task_count);
+    down_w8pc_kernel<kHidden, kInter, kTilesPerWave><<<grid, 256, 0, stream>>>(
+        static_cast<const uint4*>(data), static_cast<const uint16_t*>(scales), mid_q,
+        mid_s, tasks, route_output);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_w4g32(const void* data, const void* scales,
+                             const int8_t* mid_q, const float* mid_s,
+                             const q38m_task_v1* tasks, uint32_t task_count,
+                             float* route_output, hipStream_t stream) {
+    constexpr uint32_t kTilesPerWave = 4;
+    const dim3 grid(kHidden / 16u / (4u * kTilesPerWave), task_count);
+    down_w4g32_kernel<kHidden, kInter, kTilesPerWave><<<grid, 256, 0, stream>>>(
+        static_cast<const uint4*>(data), static_cast<const uint2*>(scales), mid_q,
+        mid_s, tasks, route_output);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const float* route_output, const uint32_t* inverse,
+                          const uint16_t* shared_output, const uint16_t* shared_gate,
+                          uint32_t tokens, uint16_t* output, hipStream_t stream) {
+    combine_kernel<kHidden><<<tokens, 256, 0, stream>>>(route_output, inverse,
+                                                        shared_output, shared_gate, output);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine_shared(const uint16_t* routed, const uint16_t* shared,
+                                 const uint16_t* gate, uint16_t* output,
+                                 uint32_t tokens, hipStream_t stream) {
+    const uint64_t elements = static_cast<uint64_t>(tokens) * kHidden;
+    combine_shared_kernel<kHidden><<<static_cast<uint32_t>((elements + 255u) / 256u), 256, 0,
+                                     stream>>>(routed, shared, gate, output, elements);
+    return hipGetLastError();
+}
+
+}  // namespace q38m

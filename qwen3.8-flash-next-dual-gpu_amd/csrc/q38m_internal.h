@@ -1,0 +1,85 @@
+// Internal launch interface between the C ABI layer (q38m_api.hip) and the
+// kernel translation units.  Launchers assume validated arguments; each
+// returns hipGetLastError() after its launches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "q38m.h"
+
+namespace q38m {
+
+constexpr uint32_t kExperts = Q38M_ROUTE_EXPERTS;
+constexpr uint32_t kTopK = Q38M_ROUTE_TOPK;
+constexpr uint32_t kMmqM = Q38M_MMQ_M;
+constexpr uint32_t kSlabMaxTokens = Q38M_PREFILL_SLAB_MAX_TOKENS;
+constexpr uint32_t kHidden = Q38M_HIDDEN;
+constexpr uint32_t kInter = Q38M_INTERMEDIATE;
+
+inline uint32_t routes_v1(uint32_t tokens) { return tokens * kTopK; }
+inline uint32_t max_tasks_v1(uint32_t tokens) {
+    const uint32_t routes = routes_v1(tokens);
+    const uint32_t initially = routes < kExperts ? routes : kExperts;
+    return initially + (routes - initially) / kMmqM;
+}
+
+// routing (q38m_routing.hip)
+hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
+                       uint32_t tokens, uint32_t experts, uint32_t top_k,
+                       int normalize, hipStream_t stream);
+hipError_t launch_build_plan(const int32_t* ids, uint32_t tokens,
+                             const q38m_route_plan_v1& plan, bool hashes,
+                             hipStream_t stream);
+
+// quantisation and gathers (q38m_quant.hip)
+hipError_t launch_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
+                                int8_t* q, float* scales, hipStream_t stream);
+hipError_t launch_pack_hidden(const uint16_t* hidden, const uint32_t* packed,
+                              uint32_t routes, uint32_t width, uint16_t* out,
+                              hipStream_t stream);
+hipError_t launch_residual_add(const uint16_t* a, const uint16_t* b, uint16_t* out,
+                               uint64_t elements, hipStream_t stream);
+
+// grouped GEMMs and combine (q38m_grouped.hip)
+hipError_t launch_gate_up_w4g32(const void* data, const void* scales,
+                                const int8_t* xq, const float* xs,
+                                const uint32_t* packed, const float* route_weights,
+                                const q38m_task_v1* tasks, uint32_t task_count,
+                                uint16_t* weighted_mid, hipStream_t stream);
+hipError_t launch_down_w8pc(const void* data, const void* scales,
+                            const int8_t* mid_q, const float* mid_s,
+                            const q38m_task_v1* tasks, uint32_t task_count,
+                            float* route_output, hipStream_t stream);
+hipError_t launch_down_w4g32(const void* data, const void* scales,
+                             const int8_t* mid_q, const float* mid_s,
+                             const q38m_task_v1* tasks, uint32_t task_count,
+                             float* route_output, hipStream_t stream);
+hipError_t launch_combine(const float* route_output, const uint32_t* inverse,
+                          const uint16_t* shared_output, const uint16_t* shared_gate,
+                          uint32_t tokens, uint16_t* output, hipStream_t stream);
+hipError_t launch_combine_shared(const uint16_t* routed, const uint16_t* shared,
+                                 const uint16_t* gate, uint16_t* output,
+                                 uint32_t tokens, hipStream_t stream);
+
+// decode (q38m_decode.hip)
+size_t decode_scratch_bytes();
+hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
+                         const q38m_expert_weights_v1& down,
+                         const uint16_t* hidden, const int32_t* ids,
+                         const float* weights, uint32_t top_k, void* scratch,
+                         uint16_t* output, hipStream_t stream);
+
+// layout and synthetic data (q38m_layout.hip)
+hipError_t launch_repack(const q38m_expert_weights_v1& src,
+                         const q38m_expert_weights_v1& dst, hipStream_t stream);
+hipError_t launch_synth(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count,
+                        float sigma, int32_t lo, int32_t hi, const float* bias,
+                        uint32_t bias_len, void* out, hipStream_t stream);
+hipError_t launch_debug_expf(const float* x, uint32_t n, float* out,
+                             hipStream_t stream);
+hipError_t launch_debug_mfma(const int8_t* a, const int8_t* b, int32_t* d,
+                             hipStream_t stream);
+
+}  // namespace q38m

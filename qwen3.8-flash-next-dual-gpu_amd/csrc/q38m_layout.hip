@@ -1,0 +1,195 @@
+// Device weight layout conversion (the load-time re-tiling of
+// cuda/cuda_weights.cu:229-285, for this build's MFMA16 layout),
+// deterministic synthetic data, and kernel-level self checks.
+#include "q38m_device.h"
+#include "q38m_internal.h"
+
+namespace q38m {
+namespace {
+
+// W4 row-major [E][R][K/2] -> MFMA16 [E][R/16][K/128][64][4 dwords].
+// Output dword (e, rt, kq, lane=(q,n), j) covers row 16rt+n, group g=4kq+j,
+// k0 = 32g+8q: byte i = nib(k0+i) | nib(k0+4+i) << 4.  The source dword at
+// k0/2 holds nibbles k0..k0+7 in order.
+__global__ void repack_w4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                 uint32_t rows, uint32_t cols, uint64_t total) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= total) return;
+    const uint32_t quads = cols / 128u;
+    const uint32_t row_tiles = rows / 16u;
+    const uint32_t j = static_cast<uint32_t>(o & 3u);
+    const uint32_t lane = static_cast<uint32_t>((o >> 2) & 63u);
+    const uint64_t block = o >> 8;
+    const uint32_t kq = static_cast<uint32_t>(block % quads);
+    const uint64_t tmp = block / quads;
+    const uint32_t rt = static_cast<uint32_t>(tmp % row_tiles);
+    const uint64_t e = tmp / row_tiles;
+    const uint32_t n = lane & 15u, q = lane >> 4;
+    const uint32_t row = rt * 16u + n;
+    const uint32_t g = kq * 4u + j;
+    const uint32_t c = src[(e * rows + row) * (cols / 8u) + g * 4u + q];
+    uint32_t out = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        out |= ((c >> (4u * i)) & 0xfu) << (8u * i);
+        out |= ((c >> (16u + 4u * i)) & 0xfu) << (8u * i + 4u);
+    }
+    dst[o] = out;
+}
+
+// W4 g32 scales [E][R][K/32] -> [E][R/16][K/128][16][4].
+__global__ void repack_w4_scales_kernel(const uint16_t* __restrict__ src,
+                                        uint16_t* __restrict__ dst, uint32_t rows,
+                                        uint32_t cols, uint64_t total) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= total) return;
+    const uint32_t quads = cols / 128u;
+    const uint32_t row_tiles = rows / 16u;
+    const uint32_t j = static_cast<uint32_t>(o & 3u);
+    const uint32_t n = static_cast<uint32_t>((o >> 2) & 15u);
+    const uint64_t block = o >> 6;
+    const uint32_t kq = static_cast<uint32_t>(block % quads);
+    const uint64_t tmp = block / quads;
+    const uint32_t rt = static_cast<uint32_t>(tmp % row_tiles);
+    const uint64_t e = tmp / row_tiles;
+    dst[o] = src[(e * rows + rt * 16u + n) * (cols / 32u) + kq * 4u + j];
+}
+
+// W8 row-major [E][R][K] -> MFMA16 [E][R/16][K/64][64][16 B]; lane (q,n)
+// holds row 16rt+n, columns 64kb+16q .. +15.
+__global__ void repack_w8_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                 uint32_t rows, uint32_t cols, uint64_t total) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= total) return;
+    const uint32_t blocks = cols / 64u;
+    const uint32_t row_tiles = rows / 16u;
+    const uint32_t lane = static_cast<uint32_t>(o & 63u);
+    const uint64_t block = o >> 6;
+    const uint32_t kb = static_cast<uint32_t>(block % blocks);
+    const uint64_t tmp = block / blocks;
+    const uint32_t rt = static_cast<uint32_t>(tmp % row_tiles);
+    const uint64_t e = tmp / row_tiles;
+    const uint32_t n = lane & 15u, q = lane >> 4;
+    dst[o] = src[((e * rows + rt * 16u + n) * cols + kb * 64u + q * 16u) / 16u];
+}
+
+__global__ void copy_u16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                uint64_t total) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o < total) dst[o] = src[o];
+}
+
+// Synthetic data, one element (or one packed W4 byte) per thread, grid-
+// stride so any count fits the grid.
+__global__ void synth_kernel(uint32_t kind, uint64_t base, uint64_t count, float sigma,
+                             int32_t lo, int32_t hi, const float* __restrict__ bias,
+                             uint32_t bias_len, void* __restrict__ out) {
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * blockDim.x;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
+         i += stride) {
+        switch (kind) {
+            case Q38M_SYNTH_NORMAL_F32: {
+                float v = normal_at(base, i) * sigma;
+                if (bias) v = v + bias[i % bias_len];
+                static_cast<float*>(out)[i] = v;
+                break;
+            }
+            case Q38M_SYNTH_NORMAL_BF16:
+                static_cast<uint16_t*>(out)[i] =
+                    static_cast<uint16_t>(f32_to_bf16(normal_at(base, i) * sigma));
+                break;
+            case Q38M_SYNTH_ABS_NORMAL_F16:
+                static_cast<uint16_t*>(out)[i] =
+                    static_cast<uint16_t>(f32_to_f16(fabsf(normal_at(base, i) * sigma)));
+                break;
+            case Q38M_SYNTH_UNIFORM_W4: {
+                const int low = uniform_at(base, 2u * i, lo, hi);
+                const int high = uniform_at(base, 2u * i + 1u, lo, hi);
+                static_cast<uint8_t*>(out)[i] = static_cast<uint8_t>(
+                    (static_cast<uint32_t>(low) & 0xfu) | ((static_cast<uint32_t>(high) & 0xfu) << 4));
+                break;
+            }
+            case Q38M_SYNTH_UNIFORM_I8:
+                static_cast<int8_t*>(out)[i] = static_cast<int8_t>(uniform_at(base, i, lo, hi));
+                break;
+            default:
+                break;
+        }
+    }
+}
+
+__global__ void debug_expf_kernel(const float* __restrict__ x, uint32_t n, float* __restrict__ out) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = exp_q(x[i]);
+}
+
+// One v_mfma_i32_16x16x32_i8 with A (16x32) and B (32x16) given row-major
+// in memory, loaded in the operand layout the kernels assume; D (16x16) is
+// written row-major from the assumed result layout.
+__global__ void debug_mfma_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b,
+                                  int32_t* __restrict__ d) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u, q = lane >> 4;
+    uint64_t av = 0, bv = 0;
+    for (uint32_t i = 0; i < 8u; ++i) {
+        av |= static_cast<uint64_t>(static_cast<uint8_t>(a[n * 32u + 8u * q + i])) << (8u * i);
+        bv |= static_cast<uint64_t>(static_cast<uint8_t>(b[(8u * q + i) * 16u + n])) << (8u * i);
+    }
+    const v4i zero = {0, 0, 0, 0};
+    const v4i r = mfma_i8_16x16x32(static_cast<long>(av), static_cast<long>(bv), zero);
+    for (uint32_t i = 0; i < 4u; ++i) d[(4u * q + i) * 16u + n] = r[i];
+}
+
+inline uint32_t blocks_for(uint64_t total, uint32_t threads) {
+    return static_cast<uint32_t>((total + threads - 1u) / threads);
+}
+
+}  // namespace
+
+hipError_t launch_repack(const q38m_expert_weights_v1& src,
+                         const q38m_expert_weights_v1& dst, hipStream_t stream) {
+    const uint64_t elements = static_cast<uint64_t>(src.experts) * src.rows * src.columns;
+    if (src.format == Q38M_FORMAT_W4_SYM) {
+        const uint64_t dwords = elements / 8u;
+        repack_w4_kernel<<<blocks_for(dwords, 256), 256, 0, stream>>>(
+            static_cast<const uint32_t*>(src.data), static_cast<uint32_t*>(const_cast<void*>(dst.data)),
+            src.rows, src.columns, dwords);
+        const uint64_t scales = elements / 32u;
+        repack_w4_scales_kernel<<<blocks_for(scales, 256), 256, 0, stream>>>(
+            static_cast<const uint16_t*>(src.scales),
+            static_cast<uint16_t*>(const_cast<void*>(dst.scales)), src.rows, src.columns, scales);
+    } else {
+        const uint64_t vectors = elements / 16u;
+        repack_w8_kernel<<<blocks_for(vectors, 256), 256, 0, stream>>>(
+            static_cast<const uint4*>(src.data), static_cast<uint4*>(const_cast<void*>(dst.data)),
+            src.rows, src.columns, vectors);
+        const uint64_t scales = static_cast<uint64_t>(src.experts) * src.rows;
+        copy_u16_kernel<<<blocks_for(scales, 256), 256, 0, stream>>>(
+            static_cast<const uint16_t*>(src.scales),
+            static_cast<uint16_t*>(const_cast<void*>(dst.scales)), scales);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_synth(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count,
+                        float sigma, int32_t lo, int32_t hi, const float* bias,
+                        uint32_t bias_len, void* out, hipStream_t stream) {
+    const uint64_t items = kind == Q38M_SYNTH_UNIFORM_W4 ? count / 2u : count;
+    const uint32_t blocks = static_cast<uint32_t>(
+        items / 256u + 1u < 65536u ? items / 256u + 1u : 65536u);
+    synth_kernel<<<blocks, 256, 0, stream>>>(kind, stream_base_host(seed, tag), items, sigma, lo,
+                                             hi, bias, bias_len, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_debug_expf(const float* x, uint32_t n, float* out, hipStream_t stream) {
+    debug_expf_kernel<<<blocks_for(n, 256), 256, 0, stream>>>(x, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_debug_mfma(const int8_t* a, const int8_t* b, int32_t* d, hipStream_t stream) {
+    debug_mfma_kernel<<<1, 64, 0, stream>>>(a, b, d);
+    return hipGetLastError();
+}
+
+}  // namespace q38m

@@ -1,0 +1,118 @@
+// Per-row int8 activation quantisation and the bf16 hidden gather.
+#include "q38m_device.h"
+#include "q38m_internal.h"
+
+namespace q38m {
+namespace {
+
+// One wave per row; lane l owns elements [8l + 512c, 8l + 512c + 8) so
+// every load is a coalesced 16-byte vector.  s = absmax/127 (IEEE
+// division), zero -> 1, q = clamp(rint(x/s), -127, 127): the convention of
+// tools/q38_artifact_compiler.py:214-222 applied per token row.
+template <uint32_t kChunks>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(
+    const uint16_t* __restrict__ x, uint32_t rows, int8_t* __restrict__ q,
+    float* __restrict__ scales) {
+    constexpr uint32_t kWidth = kChunks * 512u;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint4* src = reinterpret_cast<const uint4*>(x + static_cast<size_t>(row) * kWidth);
+    uint4 v[kChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) v[c] = src[c * 64u + lane];
+    float amax = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] & 0xffffu)));
+            amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] >> 16)));
+        }
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        amax = fmaxf(amax, __shfl_xor(amax, offset, 64));
+    float s = amax / 127.0f;
+    if (s == 0.0f) s = 1.0f;
+    uint2* dst = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * kWidth);
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+        uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
+            float r = __builtin_rintf(bf16_to_f32(h) / s);
+            r = fminf(fmaxf(r, -127.0f), 127.0f);
+            const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
+            packed[i >> 2] |= b << (8 * (i & 3));
+        }
+        dst[c * 64u + lane] = make_uint2(packed[0], packed[1]);
+    }
+    if (lane == 0) scales[row] = s;
+}
+
+// Gather hidden[token(packed)] -> packed order (q38_moe_prefill.cu:292-306).
+__global__ __launch_bounds__(256) void pack_hidden_kernel(
+    const uint16_t* __restrict__ hidden, const uint32_t* __restrict__ packed,
+    uint32_t width, uint16_t* __restrict__ out) {
+    const uint32_t p = blockIdx.x;
+    const uint32_t token = packed[p] / kTopK;
+    const uint4* src = reinterpret_cast<const uint4*>(hidden + static_cast<size_t>(token) * width);
+    uint4* dst = reinterpret_cast<uint4*>(out + static_cast<size_t>(p) * width);
+    for (uint32_t i = threadIdx.x; i < width / 8u; i += blockDim.x) dst[i] = src[i];
+}
+
+// out = bf16(a + b) in fp32, 8 elements per thread.
+__global__ __launch_bounds__(256) void residual_add_kernel(
+    const uint4* __restrict__ a, const uint4* __restrict__ b, uint4* __restrict__ out,
+    uint64_t vectors) {
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= vectors) return;
+    const uint4 va = a[i], vb = b[i];
+    const uint32_t wa[4] = {va.x, va.y, va.z, va.w};
+    const uint32_t wb[4] = {vb.x, vb.y, vb.z, vb.w};
+    uint32_t r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float lo = bf16_to_f32(wa[k] & 0xffffu) + bf16_to_f32(wb[k] & 0xffffu);
+        const float hi = bf16_to_f32(wa[k] >> 16) + bf16_to_f32(wb[k] >> 16);
+        r[k] = f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+    }
+    out[i] = make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+}  // namespace
+
+hipError_t launch_residual_add(const uint16_t* a, const uint16_t* b, uint16_t* out,
+                               uint64_t elements, hipStream_t stream) {
+    const uint64_t vectors = elements / 8u;
+    residual_add_kernel<<<static_cast<uint32_t>((vectors + 255u) / 256u), 256, 0, stream>>>(
+        reinterpret_cast<const uint4*>(a), reinterpret_cast<const uint4*>(b),
+        reinterpret_cast<uint4*>(out), vectors);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
+                                int8_t* q, float* scales, hipStream_t stream) {
+    const dim3 grid((rows + 3u) / 4u);
+    switch (width / 512u) {
+        case 1: quantize_rows_kernel<1><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
+        case 2: quantize_rows_kernel<2><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
+        case 4: quantize_rows_kernel<4><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
+        case 8: quantize_rows_kernel<8><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_hidden(const uint16_t* hidden, const uint32_t* packed,
+                              uint32_t routes, uint32_t width, uint16_t* out,
+                              hipStream_t stream) {
+    pack_hidden_kernel<<<routes, 256, 0, stream>>>(hidden, packed, width, out);
+    return hipGetLastError();
+}
+
+}  // namespace q38m

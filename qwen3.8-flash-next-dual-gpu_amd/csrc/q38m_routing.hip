@@ -1,0 +1,336 @@
+// Routing: top-k of the router logits and the deterministic expert-major
+// route plan (V1 byte layout of include/q38/cuda_moe_prefill.h:11-93).
+#include "q38m_device.h"
+#include "q38m_internal.h"
+
+namespace q38m {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Top-k: one wave per token.  Lane l holds experts l, l+64, ...  Each of the
+// top_k rounds takes every lane's best unselected (value desc, id asc) and a
+// six-step butterfly to the wave winner -- the order of the reference's
+// bitonic sort (q38_kernels.cu:431-458).  Numerators exp(l_r - l_0) and the
+// rank-order fp32 denominator follow q38_kernels.cu:460-479.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool better(float v, int id, float ov, int oid) {
+    return v > ov || (v == ov && id < oid);
+}
+
+template <int kPerLane>
+__global__ __launch_bounds__(256) void topk_kernel(
+    const float* __restrict__ logits, uint32_t tokens, uint32_t experts,
+    uint32_t top_k, int normalize, int32_t* __restrict__ ids,
+    float* __restrict__ weights) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t token = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (token >= tokens) return;
+    const float* row = logits + static_cast<size_t>(token) * experts;
+    float v[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const uint32_t e = lane + 64u * j;
+        v[j] = e < experts ? row[e] : -__builtin_huge_valf();
+    }
+    uint32_t taken = 0;
+    float mine_v = 0.0f;
+    int mine_id = 0;
+    float top_v = 0.0f;
+    for (uint32_t rank = 0; rank < top_k; ++rank) {
+        float best_v = -__builtin_huge_valf();
+        int best_id = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < kPerLane; ++j) {
+            const int e = static_cast<int>(lane + 64u * j);
+            if (((taken >> j) & 1u) == 0u && e < static_cast<int>(experts) &&
+                better(v[j], e, best_v, best_id)) {
+                best_v = v[j];
+                best_id = e;
+            }
+        }
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) {
+            const float ov = __shfl_xor(best_v, offset, 64);
+            const int oid = __shfl_xor(best_id, offset, 64);
+            if (better(ov, oid, best_v, best_id)) {
+                best_v = ov;
+                best_id = oid;
+            }
+        }
+        if (static_cast<uint32_t>(best_id & 63) == lane)
+            taken |= 1u << (best_id >> 6);
+        if (lane == rank) {
+            mine_v = best_v;
+            mine_id = best_id;
+        }
+        if (rank == 0) top_v = best_v;
+    }
+    const float numerator = lane < top_k ? exp_q(mine_v - top_v) : 0.0f;
+    float denominator = 0.0f;
+    if (normalize) {
+        for (uint32_t rank = 0; rank < top_k; ++rank)
+            denominator += __shfl(numerator, static_cast<int>(rank), 64);
+    } else {
+        for (int j = 0; j < kPerLane; ++j) {
+            const float ex = (lane + 64u * j) < experts ? exp_q(v[j] - top_v) : 0.0f;
+            for (uint32_t src = 0; src < 64u; ++src) {
+                const float term = __shfl(ex, static_cast<int>(src), 64);
+                if (src + 64u * j < experts) denominator += term;
+            }
+        }
+    }
+    if (lane < top_k) {
+        ids[static_cast<size_t>(token) * top_k + lane] = mine_id;
+        weights[static_cast<size_t>(token) * top_k + lane] = numerator / denominator;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Route plan: one workgroup of 16 waves.  The reference runs one lane per
+// expert over every route (O(routes * experts) LDS compares, then a serial
+// prefix on lane 0; q38_moe_prefill.cu:198-233).  Here:
+//   1. each wave owns a contiguous segment of assignments and, 64 at a time,
+//      finds lanes with equal expert ids with nine ballots (one per id bit);
+//      the stable rank inside the segment is the popcount of equal lanes
+//      below plus the wave's running per-expert count in LDS;
+//   2. a per-expert exclusive scan over the 16 wave histograms gives each
+//      wave's base inside its expert;
+//   3. a 512-wide scan (wave prefix + wave totals) gives expert and task
+//      offsets;
+//   4. scatter: packed = offset[e] + wave_base[w][e] + local rank.
+// The result is the stable counting sort of the reference, byte for byte.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kPlanThreads = 1024;
+constexpr uint32_t kPlanWaves = kPlanThreads / 64;
+constexpr uint32_t kMaxRoutes = kSlabMaxTokens * kTopK;
+
+__global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
+    const int32_t* __restrict__ expert_ids, uint32_t tokens,
+    q38m_route_plan_v1 plan, uint32_t max_tasks) {
+    __shared__ uint16_t key[kMaxRoutes];
+    __shared__ uint16_t local_rank[kMaxRoutes];
+    __shared__ uint16_t hist[kPlanWaves][kExperts];
+    __shared__ uint32_t counts[kExperts];
+    __shared__ uint32_t offsets[kExperts + 1];
+    __shared__ uint32_t task_offsets[kExperts + 1];
+    __shared__ uint32_t wave_totals[2][8];
+    __shared__ uint32_t wave_active[8];
+    __shared__ uint32_t invalid;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
+    const uint32_t routes = tokens * kTopK;
+
+    if (tid == 0) invalid = 0u;
+    for (uint32_t i = tid; i < kPlanWaves * kExperts; i += kPlanThreads)
+        (&hist[0][0])[i] = 0;
+    __syncthreads();
+    for (uint32_t a = tid; a < routes; a += kPlanThreads) {
+        const int32_t id = expert_ids[a];
+        const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
+        key[a] = valid ? static_cast<uint16_t>(id) : static_cast<uint16_t>(0xffffu);
+        if (!valid) invalid = 1u;
+    }
+    __syncthreads();
+
+    // 1. stable local ranks per wave segment
+    const uint32_t segment = ((routes + kPlanWaves * 64u - 1u) / (kPlanWaves * 64u)) * 64u;
+    const uint32_t begin = wave * segment;
+    const uint32_t end = min(begin + segment, routes);
+    const uint64_t below_mask = (1ull << lane) - 1ull;
+    for (uint32_t base = begin; base < end; base += 64u) {
+        const uint32_t a = base + lane;
+        const uint32_t k = a < end ? key[a] : 0xffffu;
+        const bool valid = k != 0xffffu;
+        uint64_t equal = __ballot(valid);
+#pragma unroll
+        for (uint32_t bit = 0; bit < 9u; ++bit) {
+            const bool set = (k >> bit) & 1u;
+            const uint64_t vote = __ballot(set);
+            equal &= set ? vote : ~vote;
+        }
+        const uint32_t below = __popcll(equal & below_mask);
+        const uint32_t running = valid ? hist[wave][k] : 0u;
+        if (valid) local_rank[a] = static_cast<uint16_t>(running + below);
+        if (valid && below == 0u)
+            hist[wave][k] = static_cast<uint16_t>(running + __popcll(equal));
+    }
+    __syncthreads();
+
+    // 2. per-expert base of every wave
+    if (tid < kExperts) {
+        uint32_t running = 0;
+        for (uint32_t w = 0; w < kPlanWaves; ++w) {
+            const uint32_t c = hist[w][tid];
+            hist[w][tid] = static_cast<uint16_t>(running);
+            running += c;
+        }
+        counts[tid] = running;
+        plan.expert_counts[tid] = static_cast<uint16_t>(running);
+    }
+    __syncthreads();
+
+    // 3. expert and task offsets
+    uint32_t count = 0, tasks = 0, inc_count = 0, inc_tasks = 0;
+    if (tid < kExperts) {
+        count = counts[tid];
+        tasks = (count + kMmqM - 1u) / kMmqM;
+        inc_count = count;
+        inc_tasks = tasks;
+#pragma unroll
+        for (int offset = 1; offset < 64; offset <<= 1) {
+            const uint32_t oc = __shfl_up(inc_count, offset, 64);
+            const uint32_t ot = __shfl_up(inc_tasks, offset, 64);
+            if (lane >= static_cast<uint32_t>(offset)) {
+                inc_count += oc;
+                inc_tasks += ot;
+            }
+        }
+        const uint64_t active = __ballot(count != 0u);
+        if (lane == 63u) {
+            wave_totals[0][wave] = inc_count;
+            wave_totals[1][wave] = inc_tasks;
+        }
+        if (lane == 0u) wave_active[wave] = __popcll(active);
+    }
+    __syncthreads();
+    if (tid < kExperts) {
+        uint32_t prefix_count = 0, prefix_tasks = 0;
+        for (uint32_t w = 0; w < wave; ++w) {
+            prefix_count += wave_totals[0][w];
+            prefix_tasks += wave_totals[1][w];
+        }
+        offsets[tid] = prefix_count + inc_count - count;
+        task_offsets[tid] = prefix_tasks + inc_tasks - tasks;
+        if (tid == kExperts - 1u) {
+            offsets[kExperts] = prefix_count + inc_count;
+            task_offsets[kExperts] = prefix_tasks + inc_tasks;
+        }
+    }
+    __syncthreads();
+
+    for (uint32_t i = tid; i <= kExperts; i += kPlanThreads) {
+        plan.expert_offsets[i] = offsets[i];
+        plan.expert_task_offsets[i] = task_offsets[i];
+    }
+    const uint32_t total = offsets[kExperts];
+    const uint32_t task_total = task_offsets[kExperts];
+    if (tid == 0) {
+        uint32_t active = 0;
+        for (uint32_t w = 0; w < 8u; ++w) active += wave_active[w];
+        uint32_t status = Q38M_PLAN_OK;
+        if (invalid)
+            status = Q38M_PLAN_INVALID_EXPERT;
+        else if (total != routes || task_total > max_tasks)
+            status = Q38M_PLAN_INVALID_SHAPE;
+        q38m_route_plan_header_v1* h = plan.header;
+        h->magic = Q38M_ROUTE_PLAN_MAGIC_V1;
+        h->version = Q38M_ROUTE_PLAN_VERSION_V1;
+        h->tokens = tokens;
+        h->routes = routes;
+        h->active_experts = active;
+        h->task_count = task_total;
+        h->status = status;
+        h->flags = 0u;
+        h->route_hash = 0u;
+        h->plan_hash = 0u;
+        h->reserved0 = 0u;
+        h->reserved1 = 0u;
+    }
+
+    // 4. scatter; identity for invalid assignments and unfilled positions
+    for (uint32_t a = tid; a < routes; a += kPlanThreads) {
+        const uint32_t k = key[a];
+        if (k == 0xffffu) {
+            plan.assignment_to_packed[a] = a;
+            continue;
+        }
+        const uint32_t w = a / segment;
+        const uint32_t position = offsets[k] + hist[w][k] + local_rank[a];
+        plan.packed_assignment[position] = a;
+        plan.assignment_to_packed[a] = position;
+    }
+    for (uint32_t p = total + tid; p < routes; p += kPlanThreads)
+        plan.packed_assignment[p] = p;
+
+    uint2* task_words = reinterpret_cast<uint2*>(plan.tasks);
+    if (tid < kExperts) {
+        const uint32_t c = counts[tid];
+        const uint32_t first = task_offsets[tid];
+        const uint32_t n = (c + kMmqM - 1u) / kMmqM;
+        for (uint32_t tile = 0; tile < n; ++tile) {
+            const uint32_t remaining = c - tile * kMmqM;
+            const uint32_t rows = remaining < kMmqM ? remaining : kMmqM;
+            task_words[first + tile] = make_uint2(offsets[tid] + tile * kMmqM,
+                                                  tid | (rows << 16));
+        }
+    }
+    for (uint32_t t = task_total + tid; t < max_tasks; t += kPlanThreads)
+        task_words[t] = make_uint2(0u, 0u);
+}
+
+// FNV-1a over 64-bit words, the serial hash pass of
+// cuda/q38_moe_prefill.cu:262-289.  Requested explicitly: it is a single
+// dependent chain of ~2*routes+1026 multiplies and would dominate the step.
+__global__ void plan_hash_kernel(const int32_t* __restrict__ expert_ids,
+                                 q38m_route_plan_v1 plan) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    constexpr uint64_t kOffset = 1469598103934665603ull;
+    constexpr uint64_t kPrime = 1099511628211ull;
+    const uint32_t routes = plan.header->routes;
+    uint64_t route_hash = kOffset;
+    for (uint32_t a = 0; a < routes; ++a) {
+        const int32_t id = expert_ids[a];
+        const uint64_t k = (id >= 0 && id < static_cast<int32_t>(kExperts))
+                               ? static_cast<uint64_t>(id)
+                               : 0xffffull;
+        route_hash = (route_hash ^ k) * kPrime;
+    }
+    uint64_t plan_hash = kOffset;
+    for (uint32_t e = 0; e <= kExperts; ++e) {
+        plan_hash = (plan_hash ^ plan.expert_offsets[e]) * kPrime;
+        plan_hash = (plan_hash ^ plan.expert_task_offsets[e]) * kPrime;
+    }
+    for (uint32_t p = 0; p < routes; ++p)
+        plan_hash = (plan_hash ^ plan.packed_assignment[p]) * kPrime;
+    const uint32_t task_count = plan.header->task_count;
+    for (uint32_t t = 0; t < task_count; ++t) {
+        const q38m_task_v1 task = plan.tasks[t];
+        const uint64_t low = static_cast<uint64_t>(task.packed_begin) |
+                             (static_cast<uint64_t>(task.expert) << 32);
+        const uint64_t high = static_cast<uint64_t>(task.valid_rows) |
+                              (static_cast<uint64_t>(task.flags) << 8);
+        plan_hash = (plan_hash ^ low) * kPrime;
+        plan_hash = (plan_hash ^ high) * kPrime;
+    }
+    plan.header->route_hash = route_hash;
+    plan.header->plan_hash = plan_hash;
+}
+
+}  // namespace
+
+hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
+                       uint32_t tokens, uint32_t experts, uint32_t top_k,
+                       int normalize, hipStream_t stream) {
+    const dim3 grid((tokens + 3u) / 4u);
+    const uint32_t per_lane = (experts + 63u) / 64u;
+    if (per_lane <= 8u)
+        topk_kernel<8><<<grid, 256, 0, stream>>>(logits, tokens, experts, top_k,
+                                                 normalize, ids, weights);
+    else
+        topk_kernel<16><<<grid, 256, 0, stream>>>(logits, tokens, experts, top_k,
+                                                  normalize, ids, weights);
+    return hipGetLastError();
+}
+
+hipError_t launch_build_plan(const int32_t* ids, uint32_t tokens,
+                             const q38m_route_plan_v1& plan, bool hashes,
+                             hipStream_t stream) {
+    build_plan_kernel<<<1, kPlanThreads, 0, stream>>>(ids, tokens, plan,
+                                                      max_tasks_v1(tokens));
+    if (hashes) plan_hash_kernel<<<1, 64, 0, stream>>>(ids, plan);
+    return hipGetLastError();
+}
+
+}  // namespace q38m

@@ -1,0 +1,133 @@
+"""GPU test plumbing: synthetic layers built on the device with the product's
+generator, host copies for the oracle, and thin wrappers that run the
+product's C ABI on torch-allocated buffers."""
+import ctypes
+import importlib.util
+import os
+
+import numpy as np
+
+from conftest import PACKAGE_DIR, load_product
+
+_spec = importlib.util.spec_from_file_location("q38m_workloads",
+                                               os.path.join(PACKAGE_DIR, "workloads.py"))
+W = importlib.util.module_from_spec(_spec)
+_spec.loader.exec_module(W)
+
+
+def torch():
+    import torch as t
+    return t
+
+
+def host(tensor, dtype):
+    """Device tensor -> numpy array reinterpreted as dtype."""
+    return tensor.detach().cpu().numpy().view(dtype)
+
+
+def device(array):
+    t = torch()
+    a = np.ascontiguousarray(array)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    elif a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return t.from_numpy(a.copy()).cuda()
+
+
+def stream():
+    return torch().cuda.current_stream().cuda_stream
+
+
+class Layer:
+    """One MoE layer's weights: row-major on the device, repacked MFMA16 on
+    the device, and the row-major bytes on the host for the oracle."""
+
+    def __init__(self, q38m, orc, seed, layer, gate_up_fmt, down_fmt, with_host=True):
+        gu_tag, dn_tag, _, _ = W.layer_tags(layer)
+        _, gbits, ggroup, gsigma = gate_up_fmt
+        _, dbits, dgroup, dsigma = down_fmt
+        fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+        self.gu_rm = q38m.synth_weights(seed, gu_tag, fmt[gbits], ggroup, W.EXPERTS,
+                                        2 * W.INTER, W.HIDDEN, gsigma)
+        self.dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dbits], dgroup, W.EXPERTS, W.HIDDEN,
+                                        W.INTER, dsigma)
+        self.gu = q38m.repack(self.gu_rm)
+        self.dn = q38m.repack(self.dn_rm)
+        self.host_gu = self.host_dn = None
+        if with_host:
+            self.host_gu = orc.HostWeights(host(self.gu_rm.data, np.uint8),
+                                           host(self.gu_rm.scales, np.uint16), gbits, ggroup,
+                                           W.EXPERTS, 2 * W.INTER, W.HIDDEN)
+            self.host_dn = orc.HostWeights(host(self.dn_rm.data, np.uint8),
+                                           host(self.dn_rm.scales, np.uint16), dbits, dgroup,
+                                           W.EXPERTS, W.HIDDEN, W.INTER)
+
+    def drop_row_major(self):
+        self.gu_rm = self.dn_rm = None
+
+
+def synth_hidden(q38m, seed, tag, tokens):
+    t = torch()
+    out = t.empty(tokens * W.HIDDEN, dtype=t.int16, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, tag, out.numel(), out)
+    return out.view(tokens, W.HIDDEN)
+
+
+def synth_logits(q38m, seed, tag, tokens, bias=None):
+    t = torch()
+    out = t.empty(tokens * W.EXPERTS, dtype=t.float32, device="cuda")
+    b = None if bias is None else t.tensor(bias, dtype=t.float32, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, tag, out.numel(), out, bias=b)
+    return out.view(tokens, W.EXPERTS)
+
+
+def prefill(q38m, layer, hidden, logits, ws, output=None, shared=None):
+    """Runs q38m_moe_prefill_v1 on device tensors; returns the bf16 output."""
+    t = torch()
+    tokens = hidden.shape[0]
+    if output is None:
+        output = t.empty(tokens, W.HIDDEN, dtype=t.int16, device="cuda")
+    so, sg = (None, None) if shared is None else shared
+    q38m.call("q38m_moe_prefill_v1", ctypes.byref(layer.gu.desc), ctypes.byref(layer.dn.desc),
+              hidden.data_ptr(), None if logits is None else logits.data_ptr(), tokens,
+              ctypes.byref(ws.ws), None if so is None else so.data_ptr(),
+              None if sg is None else sg.data_ptr(), output.data_ptr(), stream(), 0)
+    return output
+
+
+def decode(q38m, layer, hidden, ids, weights, scratch, output=None, top_k=10):
+    t = torch()
+    if output is None:
+        output = t.empty(1, W.HIDDEN, dtype=t.int16, device="cuda")
+    q38m.call("q38m_moe_routed_decode_v1", ctypes.byref(layer.gu.desc),
+              ctypes.byref(layer.dn.desc), hidden.data_ptr(), ids.data_ptr(), weights.data_ptr(),
+              top_k, scratch.data_ptr(), output.data_ptr(), stream(), 0)
+    return output
+
+
+def ws_arrays(ws, tokens):
+    """Workspace regions (views into the workspace's own device buffer)
+    as numpy arrays."""
+    t = torch()
+    t.cuda.synchronize()
+    r = tokens * 10
+    base = ws.buffer.data_ptr()
+
+    def grab(address, count, itemsize, np_dtype):
+        offset = address - base
+        raw = ws.buffer[offset:offset + count * itemsize]
+        return raw.cpu().numpy().view(np_dtype)
+
+    w = ws.ws
+    return {
+        "ids": grab(w.expert_ids, r, 4, np.int32).reshape(tokens, 10),
+        "weights": grab(w.expert_weights, r, 4, np.float32).reshape(tokens, 10),
+        "xq": grab(w.xq, tokens * W.HIDDEN, 1, np.int8).reshape(tokens, W.HIDDEN),
+        "xs": grab(w.xs, tokens, 4, np.float32),
+        "weighted_mid": grab(w.weighted_mid, r * W.INTER, 2, np.uint16).reshape(r, W.INTER),
+        "mid_q": grab(w.mid_q, r * W.INTER, 1, np.int8).reshape(r, W.INTER),
+        "mid_s": grab(w.mid_s, r, 4, np.float32),
+        "route_output": grab(w.route_output, r * W.HIDDEN, 4, np.float32).reshape(r, W.HIDDEN),
+        "plan": grab(w.plan.header, load_product().route_plan_bytes(ws.max_tokens), 1, np.uint8),
+    }

@@ -1,0 +1,226 @@
+"""C ABI checks that need no GPU: libq38m.so loads, exports every function
+include/q38m.h declares, keeps the reference's V1 plan byte layout
+(include/q38/cuda_moe_prefill.h:24-48, 73-93; cuda_kernel_tests.cu:529-533),
+and rejects every invalid argument the reference's host wrappers reject
+(cuda/q38_moe_prefill.cu:44-68, :635-866; cuda/q38_moe.cu:352-385) before
+touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "q38m.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(q38m_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(q38m):
+    lib = q38m.lib()
+    names = declared_functions()
+    assert len(names) >= 25
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(q38m.SIGNATURES), "binding and header disagree"
+    assert lib.q38m_moe_compiled() == 1
+
+
+def test_struct_layouts(q38m):
+    assert ctypes.sizeof(q38m.Task) == 8
+    assert ctypes.sizeof(q38m.PlanHeader) == 64
+    assert q38m.PlanHeader.route_hash.offset == 32
+    assert ctypes.sizeof(q38m.RoutePlan) == 56
+    assert ctypes.sizeof(q38m.ExpertWeights) == 48
+
+
+def test_plan_sizes_match_reference_bounds(q38m):
+    lib = q38m.lib()
+    assert lib.q38m_moe_prefill_routes_v1(512) == 5120
+    assert lib.q38m_moe_prefill_max_tasks_v1(128) == 560
+    assert lib.q38m_moe_prefill_max_tasks_v1(256) == 640
+    assert lib.q38m_moe_prefill_max_tasks_v1(512) == 800
+    assert lib.q38m_moe_prefill_max_tasks_v1(1) == 10
+    assert lib.q38m_moe_route_plan_bytes_v1(512) == 52552
+
+
+def test_plan_sizes_match_oracle(q38m, orc):
+    for t in (1, 3, 64, 128, 500, 512):
+        assert q38m.route_plan_bytes(t) == orc.plan_bytes(t)
+        assert q38m.max_tasks(t) == orc.max_tasks(t)
+
+
+def test_plan_storage_binding_offsets(q38m):
+    base = 0x100000
+    plan = q38m.bind_plan(base, q38m.route_plan_bytes(512), 512)
+    routes = 5120
+    assert plan.header == base
+    assert plan.expert_counts == base + 64
+    assert plan.expert_offsets == base + 64 + 1024
+    assert plan.expert_task_offsets == base + 64 + 1024 + 2052
+    assert plan.packed_assignment == base + 64 + 1024 + 2 * 2052
+    assert plan.assignment_to_packed == plan.packed_assignment + 4 * routes
+    assert plan.tasks == plan.assignment_to_packed + 4 * routes
+
+
+def test_plan_storage_rejects_bad_allocations(q38m):
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.bind_plan(0x100000, q38m.route_plan_bytes(512) - 1, 512)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.bind_plan(0x100008, q38m.route_plan_bytes(512), 512)
+    for tokens in (0, 513):
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.bind_plan(0x100000, 1 << 20, tokens)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.bind_plan(None, 1 << 20, 4)
+
+
+def test_workspace_binding(q38m):
+    lib = q38m.lib()
+    sizes = [lib.q38m_moe_prefill_workspace_bytes(t) for t in (1, 64, 512)]
+    assert sizes[0] < sizes[1] < sizes[2]
+    assert lib.q38m_moe_prefill_workspace_bytes(0) == 0
+    assert lib.q38m_moe_prefill_workspace_bytes(513) == 0
+    ws = q38m.PrefillWorkspace()
+    base = 0x1000000
+    q38m.call("q38m_moe_prefill_workspace_bind", base, sizes[2], 512, ctypes.byref(ws))
+    assert ws.max_tokens == 512 and ws.plan.header == base
+    ptrs = [ws.expert_ids, ws.expert_weights, ws.xq, ws.xs, ws.weighted_mid, ws.mid_q,
+            ws.mid_s, ws.route_output]
+    assert ptrs == sorted(ptrs) and all(p % 256 == 0 for p in ptrs)
+    assert ws.route_output + 5120 * 2048 * 4 <= base + sizes[2]
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_prefill_workspace_bind", base + 16, sizes[2], 512, ctypes.byref(ws))
+
+
+def fake_weights(q38m, fmt=2, group=32, layout=2, rows=1024, cols=2048, experts=512):
+    return q38m.ExpertWeights(0x200000, 0x400000, fmt, group, 1, layout, experts, rows, cols)
+
+
+def test_gate_up_validation(q38m):
+    good = fake_weights(q38m)
+    args = [0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 800, 0x60000, None, 0]
+
+    def call(w, *override):
+        a = list(args)
+        for i, v in override:
+            a[i] = v
+        q38m.call("q38m_moe_grouped_gate_up_v1", ctypes.byref(w), *a)
+
+    with pytest.raises(q38m.Unsupported):
+        call(fake_weights(q38m, layout=0))
+    for bad in (fake_weights(q38m, fmt=3), fake_weights(q38m, group=128),
+                fake_weights(q38m, rows=1280), fake_weights(q38m, cols=2560),
+                fake_weights(q38m, experts=256)):
+        with pytest.raises(q38m.InvalidArgument):
+            call(bad)
+    with pytest.raises(q38m.InvalidArgument):
+        call(good, (5, 0))          # task_count == 0
+    with pytest.raises(q38m.InvalidArgument):
+        call(good, (5, 801))        # above the 512-token bound
+    with pytest.raises(q38m.InvalidArgument):
+        call(good, (0, None))       # null activations
+    with pytest.raises(q38m.InvalidArgument):
+        call(good, (0, 0x10001))    # misaligned activations
+
+
+def test_down_validation(q38m):
+    w8 = fake_weights(q38m, fmt=3, group=0, rows=2048, cols=512)
+    args = [0x10000, 0x20000, 0x30000, 10, 0x40000, None, 0]
+    with pytest.raises(q38m.Unsupported):
+        q38m.call("q38m_moe_grouped_down_v1",
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=0, rows=2048, cols=512)),
+                  *args)
+    with pytest.raises(q38m.InvalidArgument):  # W8 with a group size
+        q38m.call("q38m_moe_grouped_down_v1",
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=32, rows=2048, cols=512)), *args)
+    with pytest.raises(q38m.InvalidArgument):  # transposed shape
+        q38m.call("q38m_moe_grouped_down_v1",
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, rows=512, cols=2048)), *args)
+    args[2] = None
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(w8), *args)
+
+
+def test_routing_and_quant_validation(q38m):
+    plan = q38m.bind_plan(0x100000, q38m.route_plan_bytes(8), 8)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_build_route_plan_v1", 0x1000, 0, ctypes.byref(plan), 0, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_build_route_plan_v1", 0x1000, 513, ctypes.byref(plan), 0, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_build_route_plan_v1", 0x1000, 8, ctypes.byref(plan), 2, None, 0)
+    broken = q38m.RoutePlan()
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_build_route_plan_v1", 0x1000, 8, ctypes.byref(broken), 0, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_topk_router_f32", 0x1000, 0x2000, 0x3000, 4, 512, 33, 1, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_topk_router_f32", 0x1000, 0x2000, 0x3000, 4, 500, 10, 1, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_quantize_rows_i8", 0x1000, 4, 1536, 0x2000, 0x3000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_reduce_top10_and_combine_shared_v1", 0x1000, 0x2000, 0x3000, None,
+                  4, 0x4000, None, 0)  # shared output without its gate
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_pack_hidden_v1", 0x1000, 0x2000, 15, 2048, 0x3000, None, 0)
+
+
+def test_decode_and_step_validation(q38m):
+    gu = fake_weights(q38m)
+    dn = fake_weights(q38m, fmt=3, group=0, rows=2048, cols=512)
+    with pytest.raises(q38m.InvalidArgument):  # top_k above 10
+        q38m.call("q38m_moe_routed_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000,
+                  0x2000, 0x3000, 11, 0x4000, 0x5000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # no scratch
+        q38m.call("q38m_moe_routed_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000,
+                  0x2000, 0x3000, 10, None, 0x5000, None, 0)
+    ws = q38m.PrefillWorkspace()
+    q38m.call("q38m_moe_prefill_workspace_bind", 0x1000000,
+              q38m.lib().q38m_moe_prefill_workspace_bytes(64), 64, ctypes.byref(ws))
+    with pytest.raises(q38m.InvalidArgument):  # more tokens than the workspace holds
+        q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2000, 65,
+                  ctypes.byref(ws), None, None, 0x3000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2000, 64,
+                  ctypes.byref(ws), None, None, 0x3000, None, -1)  # negative device
+
+
+def test_repack_and_synth_validation(q38m):
+    src = fake_weights(q38m, layout=0)
+    dst = fake_weights(q38m, layout=2)
+    with pytest.raises(q38m.InvalidArgument):  # same layout on both sides
+        q38m.call("q38m_repack_expert_weights", ctypes.byref(dst), ctypes.byref(dst), None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # shape mismatch
+        q38m.call("q38m_repack_expert_weights", ctypes.byref(src),
+                  ctypes.byref(fake_weights(q38m, layout=2, rows=2048)), None, 0)
+    with pytest.raises(q38m.Unsupported):  # W4 per-channel has no MFMA16 layout
+        q38m.call("q38m_repack_expert_weights", ctypes.byref(fake_weights(q38m, group=0, layout=0)),
+                  ctypes.byref(fake_weights(q38m, group=0, layout=2)), None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_synth_fill", 9, 1, 1, 16, 1.0, 0, 0, None, 0, 0x1000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # odd W4 count
+        q38m.call("q38m_synth_fill", 4, 1, 1, 15, 1.0, -8, 7, None, 0, 0x1000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # int4 range
+        q38m.call("q38m_synth_fill", 4, 1, 1, 16, 1.0, -9, 7, None, 0, 0x1000, None, 0)
+
+
+def test_weight_byte_counts(q38m):
+    d, s = q38m.weights_bytes(2, 32, 512, 1024, 2048)
+    assert (d, s) == (512 * 1024 * 1024, 512 * 1024 * 64 * 2)
+    d, s = q38m.weights_bytes(3, 0, 512, 2048, 512)
+    assert (d, s) == (512 * 2048 * 512, 512 * 2048 * 2)
+
+
+def test_error_message_is_reported(q38m):
+    try:
+        q38m.bind_plan(0x100000, 10, 512)
+    except q38m.InvalidArgument as exc:
+        assert "too small" in str(exc)
+    else:
+        raise AssertionError("expected InvalidArgument")
