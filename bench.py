@@ -1,0 +1,321 @@
+"""Benchmark of the MI355X MoE data plane.
+
+Headline (BASELINE.json metric): MoE-layer prefill tokens/s on the
+512-token slab of config 2 (hidden 2048, 512 experts, top-10,
+intermediate 512, W4 group-32 gate/up + W8 per-channel down), one step =
+top-k routing, route plan, int8 quantisation, grouped gate/up + SwiGLU,
+mid quantisation, grouped down and the rank-order combine, with inputs
+resident in HBM.  Also reported: per-kernel durations from HIP events on
+the launch stream inside the timed region, the roofline of the dominant
+kernel, the step's fraction of int8 MFMA and HBM peaks, batch-1 decode
+HBM GB/s through config 3's 48-layer stack, and the CPU oracle timed on
+this host as the baseline.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+"""
+import argparse
+import ctypes
+import importlib.util
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PACKAGE_DIR = os.path.join(ROOT, "qwen3.8-flash-next-dual-gpu_amd")
+
+HBM_PEAK_GBPS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, POP/s expressed in TOP/s
+
+
+def load(name, path, package_dir=None):
+    spec = importlib.util.spec_from_file_location(
+        name, path, submodule_search_locations=[package_dir] if package_dir else None)
+    module = importlib.util.module_from_spec(spec)
+    sys.modules[name] = module
+    spec.loader.exec_module(module)
+    return module
+
+
+def main():
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--decode-tokens", type=int, default=16)
+    parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--no-decode", action="store_true")
+    parser.add_argument("--calibrate-copy-mib", type=int, default=0,
+                        help="after the run, copy a buffer of this many MiB 5 times (a plain "
+                             "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the MoE data plane is built and measured on a single "
+              f"MI355X (expert sharding is a design note only); --gpus {args.gpus} is not run.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    q38m = load("q38m_amd", os.path.join(PACKAGE_DIR, "__init__.py"), PACKAGE_DIR)
+    W = load("q38m_workloads", os.path.join(PACKAGE_DIR, "workloads.py"))
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    sh = stream.cuda_stream
+
+    # ---- config 2 inputs, resident in HBM --------------------------------
+    config = 2
+    spec = W.CONFIGS[config]
+    seed, T = spec["seed"], spec["tokens"]
+    gu_tag, dn_tag, h_tag, l_tag = W.layer_tags(0)
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    gu_rm = q38m.synth_weights(seed, gu_tag, fmt[4], 32, W.EXPERTS, 2 * W.INTER, W.HIDDEN, 0.02)
+    dn_rm = q38m.synth_weights(seed, dn_tag, fmt[8], 0, W.EXPERTS, W.HIDDEN, W.INTER, 0.002)
+    gu, dn = q38m.repack(gu_rm), q38m.repack(dn_rm)
+    hidden = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
+    logits = torch.empty(T, W.EXPERTS, dtype=torch.float32, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, h_tag, hidden.numel(), hidden)
+    q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, l_tag, logits.numel(), logits)
+    out = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
+    wsb = q38m.PrefillWorkspace_(T)
+    ws = wsb.ws
+    routes = T * W.TOPK
+    max_tasks = q38m.max_tasks(T)
+
+    stage_names = ["topk", "plan", "quant_x", "gate_up", "quant_mid", "down", "combine"]
+
+    def launch_stage(i):
+        if i == 0:
+            q38m.call("q38m_topk_router_f32", logits.data_ptr(), ws.expert_ids,
+                      ws.expert_weights, T, W.EXPERTS, W.TOPK, 1, sh, 0)
+        elif i == 1:
+            q38m.call("q38m_moe_build_route_plan_v1", ws.expert_ids, T, ctypes.byref(ws.plan), 0,
+                      sh, 0)
+        elif i == 2:
+            q38m.call("q38m_quantize_rows_i8", hidden.data_ptr(), T, W.HIDDEN, ws.xq, ws.xs, sh, 0)
+        elif i == 3:
+            q38m.call("q38m_moe_grouped_gate_up_v1", ctypes.byref(gu.desc), ws.xq, ws.xs,
+                      ws.plan.packed_assignment, ws.expert_weights, ws.plan.tasks, max_tasks,
+                      ws.weighted_mid, sh, 0)
+        elif i == 4:
+            q38m.call("q38m_quantize_rows_i8", ws.weighted_mid, routes, W.INTER, ws.mid_q,
+                      ws.mid_s, sh, 0)
+        elif i == 5:
+            q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(dn.desc), ws.mid_q, ws.mid_s,
+                      ws.plan.tasks, max_tasks, ws.route_output, sh, 0)
+        else:
+            q38m.call("q38m_moe_reduce_top10_and_combine_shared_v1", ws.route_output,
+                      ws.plan.assignment_to_packed, None, None, T, out.data_ptr(), sh, 0)
+
+    def step(events=None):
+        for i in range(len(stage_names)):
+            if events is not None:
+                events[i].record(stream)
+            launch_stage(i)
+        if events is not None:
+            events[-1].record(stream)
+
+    # the fused entry point must agree with the stage sequence
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    staged = out.clone()
+    q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+              hidden.data_ptr(), logits.data_ptr(), T, ctypes.byref(ws), None, None,
+              out.data_ptr(), sh, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(staged, out), "fused and staged prefill disagree"
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stage_names) + 1)]
+              for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(args.steps):
+        step(events[k])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    stage_ms = [statistics.fmean(events[k][i].elapsed_time(events[k][i + 1])
+                                 for k in range(args.steps)) for i in range(len(stage_names))]
+    ms_per_step = elapsed * 1e3 / args.steps
+    tok_per_s = T * args.steps / elapsed
+
+    # algorithmic counts (per launch / per step)
+    ids = torch.empty(routes, dtype=torch.int32, device="cuda")
+    base = wsb.buffer.data_ptr()
+    ids.view(torch.uint8).copy_(wsb.buffer[ws.expert_ids - base:ws.expert_ids - base + 4 * routes])
+    active = int(torch.bincount(ids.long(), minlength=W.EXPERTS).gt(0).sum())
+    gu_bytes_expert = 2 * W.INTER * W.HIDDEN // 2 + 2 * W.INTER * (W.HIDDEN // 32) * 2
+    dn_bytes_expert = W.HIDDEN * W.INTER + W.HIDDEN * 2
+    gate_up_bytes = (active * gu_bytes_expert + T * W.HIDDEN + T * 4 + routes * 8 +
+                     routes * W.INTER * 2)
+    down_bytes = (active * dn_bytes_expert + routes * W.INTER + routes * 4 +
+                  routes * W.HIDDEN * 4)
+    kernels = {
+        "gate_up": (stage_ms[3], gate_up_bytes, "gate_up_w4g32_kernel"),
+        "down": (stage_ms[5], down_bytes, "down_w8pc_kernel"),
+    }
+    dominant = max(kernels, key=lambda k: kernels[k][0])
+    d_ms, d_bytes, d_symbol = kernels[dominant]
+    achieved = d_bytes / (d_ms * 1e-3) / 1e9
+    step_bytes = (active * (gu_bytes_expert + dn_bytes_expert) + T * W.HIDDEN * 2 * 2 +
+                  T * W.EXPERTS * 4)
+    step_ops = routes * W.ops_per_route()
+    step_s = ms_per_step * 1e-3
+    traffic = None
+    pmc_path = os.path.join(ROOT, "profiles", f"{d_symbol}_config2_traffic.json")
+    if os.path.exists(pmc_path):
+        with open(pmc_path) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": "MoE-layer prefill tok/s @512-token slab (% int8 MFMA peak); decode HBM GB/s",
+        "value": round(tok_per_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded SplitMix64: bf16 N(0,1) hidden, fp32 N(0,1) logits, "
+                "int4 U[-8,7] / int8 U[-127,127] weights, fp16 |N| scales)",
+        "config": {"workload": spec["name"], "tokens": T, "hidden": W.HIDDEN,
+                   "intermediate": W.INTER, "experts": W.EXPERTS, "top_k": W.TOPK,
+                   "active_experts": active},
+        "roofline": {"bound": "hbm", "kernel": d_symbol, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "algorithmic_bytes": d_bytes, "avg_ms": round(d_ms, 5)},
+        "step_roofline": {"bytes": step_bytes, "ops": step_ops,
+                          "hbm_frac": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBPS, 4),
+                          "int8_mfma_frac": round(step_ops / step_s / 1e12 / INT8_PEAK_TOPS, 5),
+                          "hbm_bound_mfma_ceiling": round(
+                              (step_ops / (step_bytes / (HBM_PEAK_GBPS * 1e9))) / 1e12 /
+                              INT8_PEAK_TOPS, 4)},
+        "stages_ms": {n: round(v, 5) for n, v in zip(stage_names, stage_ms)},
+    }
+
+    if args.calibrate_copy_mib:
+        src = torch.empty(args.calibrate_copy_mib << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        src.fill_(1)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        result["calibration_copy_bytes"] = src.numel()
+
+    if not args.no_decode:
+        result["decode"] = bench_decode(q38m, W, torch, args.decode_tokens)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
+                                              T)
+    print(json.dumps(result), flush=True)
+
+
+def bench_decode(q38m, W, torch, tokens):
+    """Config 3: one token through 48 MoE layers (W4 g32 gate/up + W8 down),
+    a fresh router draw per layer, residual add between layers.  Reports
+    HBM GB/s over the selected experts' weights."""
+    spec = W.CONFIGS[3]
+    seed, layers = spec["seed"], spec["layers"]
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    sh = torch.cuda.current_stream().cuda_stream
+    stack = []
+    for layer in range(layers):
+        gu_tag, dn_tag, _, _ = W.layer_tags(layer)
+        gu_rm = q38m.synth_weights(seed, gu_tag, fmt[4], 32, W.EXPERTS, 2 * W.INTER, W.HIDDEN,
+                                   0.02)
+        gu = q38m.repack(gu_rm)
+        del gu_rm
+        dn_rm = q38m.synth_weights(seed, dn_tag, fmt[8], 0, W.EXPERTS, W.HIDDEN, W.INTER, 0.002)
+        dn = q38m.repack(dn_rm)
+        del dn_rm
+        stack.append((gu, dn))
+    resident = sum(gu.nbytes + dn.nbytes for gu, dn in stack)
+    logits = torch.empty(tokens + 2, layers, W.EXPERTS, dtype=torch.float32, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, 2, logits.numel(), logits)
+    state = torch.empty(2, W.HIDDEN, dtype=torch.int16, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, 1, W.HIDDEN, state[0])
+    out = torch.empty(W.HIDDEN, dtype=torch.int16, device="cuda")
+    ids = torch.empty(W.TOPK, dtype=torch.int32, device="cuda")
+    wts = torch.empty(W.TOPK, dtype=torch.float32, device="cuda")
+    scratch = torch.empty(q38m.lib().q38m_moe_decode_scratch_bytes() + 256, dtype=torch.uint8,
+                          device="cuda")
+
+    def token(t):
+        for layer, (gu, dn) in enumerate(stack):
+            q38m.call("q38m_topk_router_f32", logits[t, layer].data_ptr(), ids.data_ptr(),
+                      wts.data_ptr(), 1, W.EXPERTS, W.TOPK, 1, sh, 0)
+            q38m.call("q38m_moe_routed_decode_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                      state[0].data_ptr(), ids.data_ptr(), wts.data_ptr(), W.TOPK,
+                      scratch.data_ptr(), out.data_ptr(), sh, 0)
+            q38m.call("q38m_residual_add_bf16", state[0].data_ptr(), out.data_ptr(),
+                      state[0].data_ptr(), W.HIDDEN, sh, 0)
+
+    token(tokens)
+    token(tokens + 1)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for t in range(tokens):
+        token(t)
+    stop.record()
+    torch.cuda.synchronize()
+    ms_token = start.elapsed_time(stop) / tokens
+    bytes_token = layers * W.TOPK * W.algorithmic_bytes_per_expert(W.W4, W.W8)
+    gbps = bytes_token / (ms_token * 1e-3) / 1e9
+    return {"workload": spec["name"], "tokens": tokens, "layers": layers,
+            "resident_weight_GB": round(resident / 1e9, 2),
+            "us_per_token": round(ms_token * 1e3, 2),
+            "us_per_layer": round(ms_token * 1e3 / layers, 3),
+            "algorithmic_bytes_per_token": bytes_token,
+            "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "launches_per_layer": 4, "mode": "eager"}
+
+
+def cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, gpu_out, T):
+    """The CPU oracle (this repository's C + OpenMP restatement of the
+    reference's grouped MoE step; the reference ships no CPU path) timed on
+    this host over the same config-2 slab, using the very bytes the GPU
+    used; also checks the GPU output against it."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    hg = orc.HostWeights(gu_rm.data.cpu().numpy(), gu_rm.scales.cpu().numpy().view(np.uint16), 4,
+                         32, W.EXPERTS, 2 * W.INTER, W.HIDDEN)
+    hd = orc.HostWeights(dn_rm.data.cpu().numpy(), dn_rm.scales.cpu().numpy().view(np.uint16), 8,
+                         0, W.EXPERTS, W.HIDDEN, W.INTER)
+    h = hidden.cpu().numpy().view(np.uint16)
+    lg = logits.cpu().numpy()
+    times = []
+    result = None
+    for i in range(4):
+        t0 = time.perf_counter()
+        result = orc.moe(h, hg, hd, logits=lg)
+        if i > 0:
+            times.append(time.perf_counter() - t0)
+    median = statistics.median(times)
+    match = bool(np.array_equal(result["output"], gpu_out.cpu().numpy().view(np.uint16)))
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(T / median, 1), "unit": "tok/s", "cores": orc.num_threads(),
+            "kind": "port",
+            "sample": f"full config-2 slab ({T} tokens x 10 routes), median of 3 after 1 "
+                      f"warm-up, gcc -O3 -fopenmp restatement in oracle/",
+            "seconds_per_slab": round(median, 4), "cpu_model": model,
+            "gpu_matches_cpu_bitwise": match}
+
+
+if __name__ == "__main__":
+    main()
