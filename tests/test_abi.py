@@ -224,3 +224,48 @@ def test_error_message_is_reported(q38m):
         assert "too small" in str(exc)
     else:
         raise AssertionError("expected InvalidArgument")
+
+
+CPP_PROGRAM = r"""
+#include "q38m.hpp"
+#include <cstdio>
+int main() {
+    static_assert(q38m::q38_moe_route_plan_bytes_v1(512) == 52552, "plan bytes");
+    static_assert(q38m::q38_moe_prefill_max_tasks_v1(128) == 560, "max tasks");
+    if (q38m_moe_route_plan_bytes_v1(512) != 52552) return 2;
+    alignas(16) static unsigned char arena[1 << 16];
+    auto plan = q38m::cuda_moe_route_plan_storage_v1(arena, sizeof(arena), 512);
+    if (reinterpret_cast<unsigned char*>(plan.tasks) != arena + 52552 - 800 * 8) return 3;
+    try {
+        q38m::cuda_moe_route_plan_storage_v1(arena, 100, 512);
+        return 4;
+    } catch (const std::invalid_argument& e) {
+        std::printf("invalid_argument: %s\n", e.what());
+    }
+    q38m_expert_weights_v1 rm{arena, arena, Q38M_FORMAT_W4_SYM, 32, Q38M_SCALE_F16,
+                              Q38M_LAYOUT_ROW_MAJOR, 512, 1024, 2048};
+    try {
+        q38m::cuda_moe_grouped_gate_up_v1(rm, nullptr, nullptr, nullptr, nullptr, nullptr, 1,
+                                          nullptr, nullptr, 0);
+        return 5;
+    } catch (const std::invalid_argument& e) {
+        std::printf("unsupported layout: %s\n", e.what());
+    }
+    std::printf("ok\n");
+    return 0;
+}
+"""
+
+
+def test_cpp_wrapper_compiles_links_and_throws(tmp_path):
+    import subprocess
+    src = tmp_path / "wrapper.cpp"
+    src.write_text(CPP_PROGRAM)
+    exe = tmp_path / "wrapper"
+    pkg = os.path.join(ROOT, "qwen3.8-flash-next-dual-gpu_amd")
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    str(src), "-o", str(exe), "-L", pkg, "-lq38m", f"-Wl,-rpath,{pkg}",
+                    "-Wl,-rpath,/opt/rocm/lib"], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stdout + out.stderr
+    assert "too small" in out.stdout and "MFMA16" in out.stdout and out.stdout.endswith("ok\n")
