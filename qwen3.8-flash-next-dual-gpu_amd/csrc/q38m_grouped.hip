@@ -14,6 +14,31 @@
 namespace q38m {
 namespace {
 
+// One quad (4 scale groups) of the gate/up chain for one gate tile and its
+// up tile: per group one MFMA per tile from a zero accumulator (the group's
+// exact 16*acc), then the fp32 chain y16 = fma(16*acc, s_g, y16).
+__device__ __forceinline__ void gate_up_quad(const uint2* __restrict__ a_quad, uint4 wg, uint4 wu,
+                                             uint2 sg, uint2 su, float (&yg)[4], float (&yu)[4]) {
+    const v4i zero = {0, 0, 0, 0};
+    const uint32_t wgw[4] = {wg.x, wg.y, wg.z, wg.w};
+    const uint32_t wuw[4] = {wu.x, wu.y, wu.z, wu.w};
+    const uint32_t sgw[2] = {sg.x, sg.y};
+    const uint32_t suw[2] = {su.x, su.y};
+#pragma unroll
+    for (uint32_t j = 0; j < 4u; ++j) {
+        const long a = as_long(a_quad[j * 64u]);
+        const v4i dg = mfma_i8_16x16x32(a, unpack_w4x16(wgw[j]), zero);
+        const v4i du = mfma_i8_16x16x32(a, unpack_w4x16(wuw[j]), zero);
+        const float scale_g = f16_to_f32((j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu));
+        const float scale_u = f16_to_f32((j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            yg[i] = __builtin_fmaf(static_cast<float>(dg[i]), scale_g, yg[i]);
+            yu[i] = __builtin_fmaf(static_cast<float>(du[i]), scale_u, yu[i]);
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Gate/up, W4 group-32 fp16 scales, MFMA16 layout.
 //   acc[r][j][g] = sum_{k in g} xq[token(r)][k] * W[e][j][k]        (int32)
@@ -22,76 +47,83 @@ namespace {
 // One v_mfma_i32_16x16x32_i8 per group gives that group's exact int32
 // tile (zero accumulator), so the fp32 chain runs in group order in the
 // same lanes that hold the accumulators.
+//
+// Memory plan: a workgroup of kWaves waves covers kWaves gate tiles and
+// their up tiles of one task.  The task's 16 int8 token rows (32 KiB) are
+// staged into LDS once in the MFMA A-operand order ([group][lane], 8 bytes
+// per lane), so the waves read activations with conflict-free 512-byte
+// ds_read_b64 instead of each re-reading them from L2.  Every wave streams
+// its two weight tiles with a one-quad-ahead register prefetch; with
+// <= 64 VGPRs, eight waves per SIMD keep ~70 KB of weights in flight per CU,
+// which is what ~2 us of loaded HBM latency needs at full bandwidth.
+//
+// The chain runs on 16x-scaled values: the MFMA gives 16*acc (nibbles in the
+// high half of each byte) and the raw fp16 scale feeds the fma, so
+// y16 = 16*y exactly at every step (power-of-two scaling commutes with
+// rounding; all partial sums are multiples of 2^-24, far from the subnormal
+// range).  y = y16 * 0.0625 is then exact and the contract's y * s_t follows.
 // ---------------------------------------------------------------------------
-template <uint32_t H, uint32_t I>
-__global__ __launch_bounds__(256) void gate_up_w4g32_kernel(
+template <uint32_t H, uint32_t I, uint32_t kWaves>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void gate_up_w4g32_kernel(
     const uint4* __restrict__ w, const uint2* __restrict__ s,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
     const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
     constexpr uint32_t kQuads = H / 128u;
+    constexpr uint32_t kGroups = H / 32u;
     constexpr uint32_t kTiles = 2u * I / 16u;
+    constexpr uint32_t kThreads = kWaves * 64u;
+    __shared__ uint2 a_lds[kGroups * 64u];
+
     const q38m_task_v1 task = tasks[blockIdx.y];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
-    const uint32_t gate_tile = blockIdx.x * 4u + wave;
+    const uint32_t gate_tile = blockIdx.x * kWaves + wave;
     const uint32_t up_tile = gate_tile + I / 16u;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
-
-    // A operand: lane (n, q) supplies token row n, bytes 8q..8q+7 of each
-    // 32-wide group.  Rows past valid_rows reuse row 0; their D rows are
-    // never stored.
-    const uint32_t a_row = n < rows ? n : 0u;
-    const uint32_t a_token = packed[p0 + a_row] / kTopK;
-    const uint2* xa = reinterpret_cast<const uint2*>(xq + static_cast<size_t>(a_token) * H) + q;
 
     const uint4* wg = w + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 64u + lane;
     const uint4* wu = w + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 64u + lane;
     const uint2* sg = s + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 16u + n;
     const uint2* su = s + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 16u + n;
 
-    float yg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float yu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const v4i zero = {0, 0, 0, 0};
-
+    // the first quad's weights are in flight while A is staged
     uint4 bg = wg[0], bu = wu[0];
     uint2 cg = sg[0], cu = su[0];
-    uint2 a0 = xa[0], a1 = xa[4], a2 = xa[8], a3 = xa[12];
-#pragma unroll 2
+
+    // Stage A: 16-byte chunk c of token row r holds group c/2 for lane groups
+    // q = 2(c%2) and 2(c%2)+1.  Rows past valid_rows replicate row 0.
+    for (uint32_t i = threadIdx.x; i < 16u * (H / 16u); i += kThreads) {
+        const uint32_t r = i / (H / 16u);
+        const uint32_t chunk = i % (H / 16u);
+        const uint32_t token = packed[p0 + (r < rows ? r : 0u)] / kTopK;
+        const uint4 v = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token) * H)[chunk];
+        const uint32_t base = (chunk >> 1) * 64u + (chunk & 1u) * 32u + r;
+        a_lds[base] = make_uint2(v.x, v.y);
+        a_lds[base + 16u] = make_uint2(v.z, v.w);
+    }
+    __syncthreads();
+
+    float yg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float yu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
     for (uint32_t kq = 0; kq < kQuads; ++kq) {
-        // prefetch the next quad while this one is consumed
-        const uint32_t nk = kq + 1u < kQuads ? kq + 1u : kq;
+        const uint32_t nk = kq + 1u < kQuads ? kq + 1u : kq;  // last prefetch re-reads (L1 hit)
         const uint4 nbg = wg[nk * 64u], nbu = wu[nk * 64u];
         const uint2 ncg = sg[nk * 16u], ncu = su[nk * 16u];
-        const uint2 na0 = xa[nk * 16u], na1 = xa[nk * 16u + 4u];
-        const uint2 na2 = xa[nk * 16u + 8u], na3 = xa[nk * 16u + 12u];
-
-        const uint32_t wgw[4] = {bg.x, bg.y, bg.z, bg.w};
-        const uint32_t wuw[4] = {bu.x, bu.y, bu.z, bu.w};
-        const uint32_t sgw[2] = {cg.x, cg.y};
-        const uint32_t suw[2] = {cu.x, cu.y};
-        const long av[4] = {as_long(a0), as_long(a1), as_long(a2), as_long(a3)};
-#pragma unroll
-        for (uint32_t j = 0; j < 4u; ++j) {
-            const v4i dg = mfma_i8_16x16x32(av[j], unpack_w4x16(wgw[j]), zero);
-            const v4i du = mfma_i8_16x16x32(av[j], unpack_w4x16(wuw[j]), zero);
-            const uint32_t hg = (j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu);
-            const uint32_t hu = (j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu);
-            const float scale_g = f16_to_f32(hg) * 0.0625f;
-            const float scale_u = f16_to_f32(hu) * 0.0625f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                yg[i] = __builtin_fmaf(static_cast<float>(dg[i]), scale_g, yg[i]);
-                yu[i] = __builtin_fmaf(static_cast<float>(du[i]), scale_u, yu[i]);
-            }
-        }
-        bg = nbg; bu = nbu; cg = ncg; cu = ncu;
-        a0 = na0; a1 = na1; a2 = na2; a3 = na3;
+        // the next quad's loads are issued before any of this quad's math
+        __builtin_amdgcn_sched_barrier(0);
+        gate_up_quad(a_lds + 4u * kq * 64u + lane, bg, bu, cg, cu, yg, yu);
+        bg = nbg;
+        bu = nbu;
+        cg = ncg;
+        cu = ncu;
     }
 
     const uint32_t channel = gate_tile * 16u + n;
@@ -102,8 +134,8 @@ __global__ __launch_bounds__(256) void gate_up_w4g32_kernel(
         const uint32_t p = p0 + r;
         const uint32_t a = packed[p];
         const float st = xs[a / kTopK];
-        const float y_gate = yg[i] * st;
-        const float y_up = yu[i] * st;
+        const float y_gate = (yg[i] * 0.0625f) * st;
+        const float y_up = (yu[i] * 0.0625f) * st;
         mid[static_cast<size_t>(p) * I + channel] =
             static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
     }
@@ -300,8 +332,9 @@ hipError_t launch_gate_up_w4g32(const void* data, const void* scales,
                                 const uint32_t* packed, const float* route_weights,
                                 const q38m_task_v1* tasks, uint32_t task_count,
                                 uint16_t* weighted_mid, hipStream_t stream) {
-    const dim3 grid(kInter / 64u, task_count);
-    gate_up_w4g32_kernel<kHidden, kInter><<<grid, 256, 0, stream>>>(
+    constexpr uint32_t kWaves = 8;
+    const dim3 grid(kInter / 16u / kWaves, task_count);
+    gate_up_w4g32_kernel<kHidden, kInter, kWaves><<<grid, kWaves * 64u, 0, stream>>>(
         static_cast<const uint4*>(data), static_cast<const uint2*>(scales), xq, xs,
         packed, route_weights, tasks, weighted_mid);
     return hipGetLastError();
