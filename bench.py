@@ -71,7 +71,7 @@ def main():
     fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
     gu_rm = q38m.synth_weights(seed, gu_tag, fmt[4], 32, W.EXPERTS, 2 * W.INTER, W.HIDDEN, 0.02)
     dn_rm = q38m.synth_weights(seed, dn_tag, fmt[8], 0, W.EXPERTS, W.HIDDEN, W.INTER, 0.002)
-    gu, dn = q38m.repack(gu_rm), q38m.repack(dn_rm)
+    gu, dn = q38m.repack(gu_rm, paired=True), q38m.repack(dn_rm)
     hidden = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
     logits = torch.empty(T, W.EXPERTS, dtype=torch.float32, device="cuda")
     q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, h_tag, hidden.numel(), hidden)
@@ -228,7 +228,7 @@ def bench_decode(q38m, W, torch, tokens):
         gu_tag, dn_tag, _, _ = W.layer_tags(layer)
         gu_rm = q38m.synth_weights(seed, gu_tag, fmt[4], 32, W.EXPERTS, 2 * W.INTER, W.HIDDEN,
                                    0.02)
-        gu = q38m.repack(gu_rm)
+        gu = q38m.repack(gu_rm, paired=True)
         del gu_rm
         dn_rm = q38m.synth_weights(seed, dn_tag, fmt[8], 0, W.EXPERTS, W.HIDDEN, W.INTER, 0.002)
         dn = q38m.repack(dn_rm)

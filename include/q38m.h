@@ -103,8 +103,10 @@ typedef struct q38m_route_plan_v1 {
 #define Q38M_FORMAT_W4_SYM 2u /* int4 two's complement, even k in the low nibble */
 #define Q38M_FORMAT_W8_SYM 3u /* int8 */
 #define Q38M_SCALE_F16 1u
-#define Q38M_LAYOUT_ROW_MAJOR 0u /* canonical artifact layout */
-#define Q38M_LAYOUT_MFMA16 2u    /* device layout for the 16x16 int8 MFMA kernels */
+#define Q38M_LAYOUT_ROW_MAJOR 0u   /* canonical artifact layout */
+#define Q38M_LAYOUT_MFMA16 2u      /* device layout for the 16x16 int8 MFMA kernels */
+#define Q38M_LAYOUT_MFMA16_PAIRED 3u /* MFMA16 with row tile t next to tile t+rows/32
+                                        (the gate/up halves), W4 group-32 only */
 
 typedef struct q38m_expert_weights_v1 {
     const void* data;
@@ -121,10 +123,12 @@ typedef struct q38m_expert_weights_v1 {
 /* Row-major layouts (artifact): W4 data [E][rows][cols/2], W8 data
  * [E][rows][cols]; fp16 scales [E][rows][cols/32] (group 32) or [E][rows]
  * (per channel).  MFMA16 layouts (produced by q38m_repack_expert_weights):
- *   W4 g32 data  [E][rows/16][cols/128][64 lanes][16 B]; lane l = (q=l/16,
- *     n=l%16) holds for row 16t+n and groups 4kq+j (j=0..3) one dword each:
- *     byte i = nib(k0+i) | nib(k0+4+i)<<4, k0 = 32(4kq+j)+8q.
- *   W4 g32 scales [E][rows/16][cols/128][16 rows][4 groups] fp16.
+ *   W4 g32 data  [E][cols/128][slot][64 lanes][16 B], quad-major: for one
+ *     128-wide K block (quad kq) all row tiles are adjacent.  Slot s holds
+ *     row tile s (MFMA16) or, paired, tile s/2 + (s%2)*rows/32.  Lane
+ *     l = (q=l/16, n=l%16) holds for row 16t+n and groups 4kq+j (j=0..3) one
+ *     dword each: byte i = nib(k0+i) | nib(k0+4+i)<<4, k0 = 32(4kq+j)+8q.
+ *   W4 g32 scales [E][cols/128][slot][16 rows][4 groups] fp16 (same order).
  *   W8 data  [E][rows/16][cols/64][64 lanes][16 B]; lane l holds row 16t+n,
  *     columns 64kb+16q .. +15.   W8 per-channel scales stay [E][rows]. */
 

@@ -37,6 +37,7 @@ FORMAT_W8_SYM = 3
 SCALE_F16 = 1
 LAYOUT_ROW_MAJOR = 0
 LAYOUT_MFMA16 = 2
+LAYOUT_MFMA16_PAIRED = 3
 
 SYNTH_NORMAL_F32 = 1
 SYNTH_NORMAL_BF16 = 2
@@ -245,13 +246,15 @@ def synth_weights(seed, tag, fmt, group, experts, rows, columns, scale_sigma, de
     return DeviceWeights(data, scales, fmt, group, LAYOUT_ROW_MAJOR, experts, rows, columns)
 
 
-def repack(weights, stream=None):
-    """Row-major -> MFMA16 device layout (a new allocation)."""
+def repack(weights, paired=False, stream=None):
+    """Row-major -> MFMA16 device layout (a new allocation).  paired=True
+    gives the gate/up layout (tile t next to tile t + rows/32)."""
     torch = _torch()
     data = torch.empty_like(weights.data)
     scales = torch.empty_like(weights.scales)
     d = weights.desc
-    out = DeviceWeights(data, scales, d.format, d.group_size, LAYOUT_MFMA16, d.experts, d.rows,
+    layout = LAYOUT_MFMA16_PAIRED if paired else LAYOUT_MFMA16
+    out = DeviceWeights(data, scales, d.format, d.group_size, layout, d.experts, d.rows,
                         d.columns)
     call("q38m_repack_expert_weights", ctypes.byref(weights.desc), ctypes.byref(out.desc),
          stream_handle(stream), device_index(data))

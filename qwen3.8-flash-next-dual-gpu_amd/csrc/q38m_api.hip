@@ -60,7 +60,7 @@ bool valid_plan(const q38m_route_plan_v1* plan) {
 bool valid_gate_up(const q38m_expert_weights_v1* w) {
     return w && w->data && w->scales && aligned(w->data, 16) && aligned(w->scales, 8) &&
            w->format == Q38M_FORMAT_W4_SYM && w->group_size == 32u &&
-           w->scale_dtype == Q38M_SCALE_F16 && w->layout == Q38M_LAYOUT_MFMA16 &&
+           w->scale_dtype == Q38M_SCALE_F16 && w->layout == Q38M_LAYOUT_MFMA16_PAIRED &&
            w->experts == Q38M_ROUTE_EXPERTS && w->rows == 2u * Q38M_INTERMEDIATE &&
            w->columns == Q38M_HIDDEN;
 }
@@ -78,7 +78,8 @@ bool valid_down(const q38m_expert_weights_v1* w) {
 int check_weights(const q38m_expert_weights_v1* w, bool gate_up) {
     if (w && w->layout == Q38M_LAYOUT_ROW_MAJOR)
         return fail(Q38M_ERR_UNSUPPORTED,
-                    "q38m kernels read the MFMA16 layout; convert with q38m_repack_expert_weights");
+                    "q38m kernels read the MFMA16 layouts (gate/up: MFMA16_PAIRED); convert with "
+                    "q38m_repack_expert_weights");
     if (gate_up ? !valid_gate_up(w) : !valid_down(w))
         return fail(Q38M_ERR_INVALID_ARGUMENT,
                     gate_up ? "invalid grouped gate/up expert tensor"
@@ -377,7 +378,8 @@ size_t q38m_expert_weights_bytes(const q38m_expert_weights_v1* w, size_t* scale_
 int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
                                const q38m_expert_weights_v1* dst, void* stream, int device) {
     if (!src || !dst || !src->data || !src->scales || !dst->data || !dst->scales ||
-        src->layout != Q38M_LAYOUT_ROW_MAJOR || dst->layout != Q38M_LAYOUT_MFMA16 ||
+        src->layout != Q38M_LAYOUT_ROW_MAJOR ||
+        (dst->layout != Q38M_LAYOUT_MFMA16 && dst->layout != Q38M_LAYOUT_MFMA16_PAIRED) ||
         src->format != dst->format || src->group_size != dst->group_size ||
         src->scale_dtype != Q38M_SCALE_F16 || dst->scale_dtype != Q38M_SCALE_F16 ||
         src->experts != dst->experts || src->rows != dst->rows || src->columns != dst->columns ||
@@ -385,11 +387,14 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
         !aligned(dst->data, 16))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid expert weight repack");
     const bool w4 = src->format == Q38M_FORMAT_W4_SYM && src->group_size == 32u &&
-                    src->columns % 128u == 0u;
+                    src->columns % 128u == 0u &&
+                    (dst->layout == Q38M_LAYOUT_MFMA16 || src->rows % 32u == 0u);
     const bool w8 = src->format == Q38M_FORMAT_W8_SYM && src->group_size == 0u &&
-                    src->columns % 64u == 0u;
+                    src->columns % 64u == 0u && dst->layout == Q38M_LAYOUT_MFMA16;
     if (!w4 && !w8)
-        return fail(Q38M_ERR_UNSUPPORTED, "repack supports W4 group-32 and W8 per-channel");
+        return fail(Q38M_ERR_UNSUPPORTED,
+                    "repack supports W4 group-32 (MFMA16 or MFMA16_PAIRED) and W8 per-channel "
+                    "(MFMA16)");
     if (int rc = select_device(device)) return rc;
     return finish(q38m::launch_repack(*src, *dst, as_stream(stream)), "repack kernels");
 }

@@ -40,27 +40,27 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
-    const uint32_t gate_tile = blockIdx.x;
-    const uint32_t up_tile = gate_tile + I / 16u;
+    const uint32_t gate_tile = blockIdx.x;  // = the gate/up pair index
     const uint32_t route = blockIdx.y;
     const int32_t id = ids[route];
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
 
     // weights first: every load of this wave's K quarter is issued now
+    // (paired quad-major layout: gate tile of pair p in slot 2p, up in 2p+1)
     uint4 bg[kQuadsPerWave], bu[kQuadsPerWave];
     uint2 cg[kQuadsPerWave], cu[kQuadsPerWave];
-    const uint4* wg = w + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 64u + lane;
-    const uint4* wu = w + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 64u + lane;
-    const uint2* sg = s + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 16u + n;
-    const uint2* su = s + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 16u + n;
+    const uint4* wg = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u + lane;
+    const uint4* wu = wg + 64u;
+    const uint2* sg = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u + n;
+    const uint2* su = sg + 16u;
 #pragma unroll
     for (uint32_t i = 0; i < kQuadsPerWave; ++i) {
         const uint32_t kq = wave * kQuadsPerWave + i;
-        bg[i] = wg[kq * 64u];
-        bu[i] = wu[kq * 64u];
-        cg[i] = sg[kq * 16u];
-        cu[i] = su[kq * 16u];
+        bg[i] = wg[kq * kTiles * 64u];
+        bu[i] = wu[kq * kTiles * 64u];
+        cg[i] = sg[kq * kTiles * 16u];
+        cu[i] = su[kq * kTiles * 16u];
     }
 
     // int8 quantisation of the token (same arithmetic as the row kernel)
@@ -154,17 +154,20 @@ __global__ __launch_bounds__(640) void decode_down_kernel(
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
 
+    // W8: tile-major [e][tile][kb]; W4: quad-major [e][kq][tile]
     uint4 b[kBlocks];
-    const uint4* wt = w + static_cast<size_t>(e * kTiles + tile) * kBlocks * 64u + lane;
+    const uint4* wt = kW4 ? w + (static_cast<size_t>(e) * kBlocks * kTiles + tile) * 64u + lane
+                          : w + static_cast<size_t>(e * kTiles + tile) * kBlocks * 64u + lane;
+    const uint32_t block_stride = kW4 ? kTiles * 64u : 64u;
 #pragma unroll
-    for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = wt[kb * 64u];
+    for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = wt[kb * block_stride];
     uint2 c[kW4 ? kBlocks : 1];
     float ws = 0.0f;
     if constexpr (kW4) {
         const uint2* st = static_cast<const uint2*>(s) +
-                          static_cast<size_t>(e * kTiles + tile) * kBlocks * 16u + n;
+                          (static_cast<size_t>(e) * kBlocks * kTiles + tile) * 16u + n;
 #pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb) c[kb] = st[kb * 16u];
+        for (uint32_t kb = 0; kb < kBlocks; ++kb) c[kb] = st[kb * kTiles * 16u];
     } else {
         ws = f16_to_f32(static_cast<const uint16_t*>(s)[static_cast<size_t>(e) * H + tile * 16u + n]);
     }

@@ -14,6 +14,11 @@
 namespace q38m {
 namespace {
 
+struct QuadWeights {
+    uint4 g, u;    // gate and up tile data of one quad
+    uint2 sg, su;  // their fp16 scales (4 groups)
+};
+
 // One quad (4 scale groups) of the gate/up chain for one gate tile and its
 // up tile: per group one MFMA per tile from a zero accumulator (the group's
 // exact 16*acc), then the fp32 chain y16 = fma(16*acc, s_g, y16).
@@ -53,9 +58,9 @@ __device__ __forceinline__ void gate_up_quad(const uint2* __restrict__ a_quad, u
 // staged into LDS once in the MFMA A-operand order ([group][lane], 8 bytes
 // per lane), so the waves read activations with conflict-free 512-byte
 // ds_read_b64 instead of each re-reading them from L2.  Every wave streams
-// its two weight tiles with a one-quad-ahead register prefetch; with
-// <= 64 VGPRs, eight waves per SIMD keep ~70 KB of weights in flight per CU,
-// which is what ~2 us of loaded HBM latency needs at full bandwidth.
+// its two weight tiles two quads ahead (4.6 KB in flight per wave); at ~70
+// VGPRs three 8-wave workgroups per CU keep ~110 KB of weights in flight,
+// what ~2 us of loaded HBM latency needs at full bandwidth.
 //
 // The chain runs on 16x-scaled values: the MFMA gives 16*acc (nibbles in the
 // high half of each byte) and the raw fp16 scale feeds the fma, so
@@ -64,7 +69,7 @@ __device__ __forceinline__ void gate_up_quad(const uint2* __restrict__ a_quad, u
 // range).  y = y16 * 0.0625 is then exact and the contract's y * s_t follows.
 // ---------------------------------------------------------------------------
 template <uint32_t H, uint32_t I, uint32_t kWaves>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(8, 8)))
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6, 8)))
 void gate_up_w4g32_kernel(
     const uint4* __restrict__ w, const uint2* __restrict__ s,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
@@ -83,19 +88,27 @@ void gate_up_w4g32_kernel(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
-    const uint32_t gate_tile = blockIdx.x * kWaves + wave;
-    const uint32_t up_tile = gate_tile + I / 16u;
+    const uint32_t gate_tile = blockIdx.x * kWaves + wave;  // = the gate/up pair index
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
 
-    const uint4* wg = w + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 64u + lane;
-    const uint4* wu = w + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 64u + lane;
-    const uint2* sg = s + static_cast<size_t>(e * kTiles + gate_tile) * kQuads * 16u + n;
-    const uint2* su = s + static_cast<size_t>(e * kTiles + up_tile) * kQuads * 16u + n;
+    // Paired quad-major layout: for quad kq the gate tile of pair p is slot
+    // 2p and its up tile slot 2p+1, so a workgroup's step reads one
+    // contiguous span of 2*kWaves KiB of weights and 256*kWaves B of scales.
+    constexpr uint32_t kQuadWords = kTiles * 64u;   // uint4 per quad of one expert
+    constexpr uint32_t kQuadScales = kTiles * 16u;  // uint2 per quad of one expert
+    const uint4* wg = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u + lane;
+    const uint4* wu = wg + 64u;
+    const uint2* sg = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u + n;
+    const uint2* su = sg + 16u;
 
-    // the first quad's weights are in flight while A is staged
-    uint4 bg = wg[0], bu = wu[0];
-    uint2 cg = sg[0], cu = su[0];
+    // the first two quads' weights are in flight while A is staged
+    auto load = [&](uint32_t kq) {
+        const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
+        return QuadWeights{wg[k * kQuadWords], wu[k * kQuadWords], sg[k * kQuadScales],
+                           su[k * kQuadScales]};
+    };
+    QuadWeights r0 = load(0), r1 = load(1), r2;
 
     // Stage A: 16-byte chunk c of token row r holds group c/2 for lane groups
     // q = 2(c%2) and 2(c%2)+1.  Rows past valid_rows replicate row 0.
@@ -112,19 +125,25 @@ void gate_up_w4g32_kernel(
 
     float yg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float yu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Two quads ahead through three register sets in a fixed rotation: each
+    // load lands in the set consumed one step earlier, so no register with a
+    // load in flight is ever copied (a copy would wait for the load).  Each
+    // step issues its load before any of its math (scheduling barrier).
+    static_assert(kQuads % 3u == 1u, "three-set rotation plus one peeled quad");
+    const uint2* a_base = a_lds + lane;
 #pragma unroll 1
-    for (uint32_t kq = 0; kq < kQuads; ++kq) {
-        const uint32_t nk = kq + 1u < kQuads ? kq + 1u : kq;  // last prefetch re-reads (L1 hit)
-        const uint4 nbg = wg[nk * 64u], nbu = wu[nk * 64u];
-        const uint2 ncg = sg[nk * 16u], ncu = su[nk * 16u];
-        // the next quad's loads are issued before any of this quad's math
+    for (uint32_t kq = 0; kq + 3u < kQuads; kq += 3u) {
+        r2 = load(kq + 2u);
         __builtin_amdgcn_sched_barrier(0);
-        gate_up_quad(a_lds + 4u * kq * 64u + lane, bg, bu, cg, cu, yg, yu);
-        bg = nbg;
-        bu = nbu;
-        cg = ncg;
-        cu = ncu;
+        gate_up_quad(a_base + 4u * kq * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
+        r0 = load(kq + 3u);
+        __builtin_amdgcn_sched_barrier(0);
+        gate_up_quad(a_base + 4u * (kq + 1u) * 64u, r1.g, r1.u, r1.sg, r1.su, yg, yu);
+        r1 = load(kq + 4u);
+        __builtin_amdgcn_sched_barrier(0);
+        gate_up_quad(a_base + 4u * (kq + 2u) * 64u, r2.g, r2.u, r2.sg, r2.su, yg, yu);
     }
+    gate_up_quad(a_base + 4u * (kQuads - 1u) * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
 
     const uint32_t channel = gate_tile * 16u + n;
 #pragma unroll
@@ -145,47 +164,79 @@ void gate_up_w4g32_kernel(
 // Down, W8 per output channel, MFMA16 layout (16 int8 per lane per 64-wide
 // K block).  acc = sum_k qm[r][k] * W[e][c][k] over all of K in one int32
 // (exact in fp32, |acc| < 2^24), o = ((float)acc * ws[e][c]) * sm[r].
-// Each wave keeps its 16 A rows (whole K) in registers and sweeps
-// kTilesPerWave output tiles.
+//
+// A workgroup of kWaves waves covers kWaves * kTilesPerWave 16-channel
+// output tiles of one task.  The task's 16 int8 mid rows (8 KiB) are staged
+// into LDS once in the MFMA A-operand order ([k block][lane], 16 bytes per
+// lane).  Each wave streams its tiles in half-tile units (4 K blocks = 4 KiB
+// per wave) with a pinned one-unit-ahead prefetch; at ~60 VGPRs eight waves
+// per SIMD keep ~128 KB of weights in flight per CU.
 // ---------------------------------------------------------------------------
-template <uint32_t H, uint32_t I, uint32_t kTilesPerWave>
-__global__ __launch_bounds__(256) void down_w8pc_kernel(
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
+__global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
     constexpr uint32_t kBlocks = I / 64u;
+    constexpr uint32_t kHalf = kBlocks / 2u;
     constexpr uint32_t kTiles = H / 16u;
+    constexpr uint32_t kThreads = kWaves * 64u;
+    static_assert(kBlocks % 2u == 0u, "half-tile units");
+    __shared__ uint4 a_lds[kBlocks * 64u];
+
     const q38m_task_v1 task = tasks[blockIdx.y];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
-    const uint32_t a_row = n < rows ? n : 0u;
-    const uint4* xa = reinterpret_cast<const uint4*>(mq + static_cast<size_t>(p0 + a_row) * I) + q;
-    v4i a[kBlocks];
+    const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
+    const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
+
+    // first half-tile in flight while A is staged
+    uint4 b[kHalf];
 #pragma unroll
-    for (uint32_t kb = 0; kb < kBlocks; ++kb) a[kb] = as_v4i(xa[kb * 4u]);
+    for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = wt[kb * 64u];
+
+    // Stage A: 16-byte chunk c of mid row r is K block c/4, lane group c%4.
+    for (uint32_t i = threadIdx.x; i < 16u * (I / 16u); i += kThreads) {
+        const uint32_t r = i / (I / 16u);
+        const uint32_t chunk = i % (I / 16u);
+        const uint4 v = reinterpret_cast<const uint4*>(
+            mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[chunk];
+        a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + r] = v;
+    }
     float row_scale[4];
 #pragma unroll
     for (uint32_t i = 0; i < 4u; ++i) {
         const uint32_t r = 4u * q + i;
         row_scale[i] = ms[p0 + (r < rows ? r : 0u)];
     }
-    const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
-#pragma unroll
+    __syncthreads();
+
+#pragma unroll 1
     for (uint32_t t = 0; t < kTilesPerWave; ++t) {
         const uint32_t tile = tile0 + t;
-        const uint4* wt = w + static_cast<size_t>(e * kTiles + tile) * kBlocks * 64u + lane;
-        uint4 b[kBlocks];
+        const uint4* wtile = wt + static_cast<size_t>(t) * kBlocks * 64u;
+        uint4 nb[kHalf];
 #pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = wt[kb * 64u];
+        for (uint32_t kb = 0; kb < kHalf; ++kb) nb[kb] = wtile[(kHalf + kb) * 64u];
+        __builtin_amdgcn_sched_barrier(0);
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb) acc = mfma_i8_16x16x64(a[kb], as_v4i(b[kb]), acc);
+        for (uint32_t kb = 0; kb < kHalf; ++kb)
+            acc = mfma_i8_16x16x64(as_v4i(a_lds[kb * 64u + lane]), as_v4i(b[kb]), acc);
+        // next tile's first half (the last tile re-reads its own: an L1 hit)
+        const uint4* wnext = t + 1u < kTilesPerWave ? wtile + kBlocks * 64u : wtile;
+#pragma unroll
+        for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = wnext[kb * 64u];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t kb = 0; kb < kHalf; ++kb)
+            acc = mfma_i8_16x16x64(as_v4i(a_lds[(kHalf + kb) * 64u + lane]), as_v4i(nb[kb]), acc);
         const uint32_t channel = tile * 16u + n;
         const float ws = f16_to_f32(s[static_cast<size_t>(e) * H + channel]);
 #pragma unroll
@@ -233,13 +284,14 @@ __global__ __launch_bounds__(256) void down_w4g32_kernel(
     const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
     for (uint32_t t = 0; t < kTilesPerWave; ++t) {
         const uint32_t tile = tile0 + t;
-        const uint4* wt = w + static_cast<size_t>(e * kTiles + tile) * kQuads * 64u + lane;
-        const uint2* st = s + static_cast<size_t>(e * kTiles + tile) * kQuads * 16u + n;
+        // quad-major layout: quad kq of tile t is unit (e*kQuads + kq)*kTiles + t
+        const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 64u + lane;
+        const uint2* st = s + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 16u + n;
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t kq = 0; kq < kQuads; ++kq) {
-            const uint4 b = wt[kq * 64u];
-            const uint2 c = st[kq * 16u];
+            const uint4 b = wt[kq * kTiles * 64u];
+            const uint2 c = st[kq * kTiles * 16u];
             const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
             const uint32_t cw[2] = {c.x, c.y};
 #pragma unroll
@@ -344,9 +396,9 @@ hipError_t launch_down_w8pc(const void* data, const void* scales,
                             const int8_t* mid_q, const float* mid_s,
                             const q38m_task_v1* tasks, uint32_t task_count,
                             float* route_output, hipStream_t stream) {
-    constexpr uint32_t kTilesPerWave = 4;
-    const dim3 grid(kHidden / 16u / (4u * kTilesPerWave), task_count);
-    down_w8pc_kernel<kHidden, kInter, kTilesPerWave><<<grid, 256, 0, stream>>>(
+    constexpr uint32_t kWaves = 8, kTilesPerWave = 2;
+    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
+    down_w8pc_kernel<kHidden, kInter, kWaves, kTilesPerWave><<<grid, kWaves * 64u, 0, stream>>>(
         static_cast<const uint4*>(data), static_cast<const uint16_t*>(scales), mid_q,
         mid_s, tasks, route_output);
     return hipGetLastError();

@@ -7,25 +7,31 @@
 namespace q38m {
 namespace {
 
-// W4 row-major [E][R][K/2] -> MFMA16 [E][R/16][K/128][64][4 dwords].
-// Output dword (e, rt, kq, lane=(q,n), j) covers row 16rt+n, group g=4kq+j,
-// k0 = 32g+8q: byte i = nib(k0+i) | nib(k0+4+i) << 4.  The source dword at
-// k0/2 holds nibbles k0..k0+7 in order.
+// Slot -> row tile of the quad-major W4 layouts: identity, or, paired, tile
+// s/2 of the first half and tile s/2 of the second half alternating.
+__device__ __forceinline__ uint32_t slot_tile(uint32_t slot, uint32_t row_tiles, bool paired) {
+    return paired ? (slot >> 1) + (slot & 1u) * (row_tiles >> 1) : slot;
+}
+
+// W4 row-major [E][R][K/2] -> MFMA16 [E][K/128][slot][64][4 dwords].
+// Output dword (e, kq, slot, lane=(q,n), j) covers row 16*tile(slot)+n,
+// group g=4kq+j, k0 = 32g+8q: byte i = nib(k0+i) | nib(k0+4+i) << 4.  The
+// source dword at k0/2 holds nibbles k0..k0+7 in order.
 __global__ void repack_w4_kernel(const uint32_t* __restrict__ src, uint32_t* __restrict__ dst,
-                                 uint32_t rows, uint32_t cols, uint64_t total) {
+                                 uint32_t rows, uint32_t cols, bool paired, uint64_t total) {
     const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (o >= total) return;
     const uint32_t quads = cols / 128u;
     const uint32_t row_tiles = rows / 16u;
     const uint32_t j = static_cast<uint32_t>(o & 3u);
     const uint32_t lane = static_cast<uint32_t>((o >> 2) & 63u);
-    const uint64_t block = o >> 8;
-    const uint32_t kq = static_cast<uint32_t>(block % quads);
-    const uint64_t tmp = block / quads;
-    const uint32_t rt = static_cast<uint32_t>(tmp % row_tiles);
-    const uint64_t e = tmp / row_tiles;
+    const uint64_t unit = o >> 8;
+    const uint32_t slot = static_cast<uint32_t>(unit % row_tiles);
+    const uint64_t tmp = unit / row_tiles;
+    const uint32_t kq = static_cast<uint32_t>(tmp % quads);
+    const uint64_t e = tmp / quads;
     const uint32_t n = lane & 15u, q = lane >> 4;
-    const uint32_t row = rt * 16u + n;
+    const uint32_t row = slot_tile(slot, row_tiles, paired) * 16u + n;
     const uint32_t g = kq * 4u + j;
     const uint32_t c = src[(e * rows + row) * (cols / 8u) + g * 4u + q];
     uint32_t out = 0;
@@ -37,22 +43,23 @@ __global__ void repack_w4_kernel(const uint32_t* __restrict__ src, uint32_t* __r
     dst[o] = out;
 }
 
-// W4 g32 scales [E][R][K/32] -> [E][R/16][K/128][16][4].
+// W4 g32 scales [E][R][K/32] -> [E][K/128][slot][16][4].
 __global__ void repack_w4_scales_kernel(const uint16_t* __restrict__ src,
                                         uint16_t* __restrict__ dst, uint32_t rows,
-                                        uint32_t cols, uint64_t total) {
+                                        uint32_t cols, bool paired, uint64_t total) {
     const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (o >= total) return;
     const uint32_t quads = cols / 128u;
     const uint32_t row_tiles = rows / 16u;
     const uint32_t j = static_cast<uint32_t>(o & 3u);
     const uint32_t n = static_cast<uint32_t>((o >> 2) & 15u);
-    const uint64_t block = o >> 6;
-    const uint32_t kq = static_cast<uint32_t>(block % quads);
-    const uint64_t tmp = block / quads;
-    const uint32_t rt = static_cast<uint32_t>(tmp % row_tiles);
-    const uint64_t e = tmp / row_tiles;
-    dst[o] = src[(e * rows + rt * 16u + n) * (cols / 32u) + kq * 4u + j];
+    const uint64_t unit = o >> 6;
+    const uint32_t slot = static_cast<uint32_t>(unit % row_tiles);
+    const uint64_t tmp = unit / row_tiles;
+    const uint32_t kq = static_cast<uint32_t>(tmp % quads);
+    const uint64_t e = tmp / quads;
+    const uint32_t row = slot_tile(slot, row_tiles, paired) * 16u + n;
+    dst[o] = src[(e * rows + row) * (cols / 32u) + kq * 4u + j];
 }
 
 // W8 row-major [E][R][K] -> MFMA16 [E][R/16][K/64][64][16 B]; lane (q,n)
@@ -150,14 +157,16 @@ hipError_t launch_repack(const q38m_expert_weights_v1& src,
                          const q38m_expert_weights_v1& dst, hipStream_t stream) {
     const uint64_t elements = static_cast<uint64_t>(src.experts) * src.rows * src.columns;
     if (src.format == Q38M_FORMAT_W4_SYM) {
+        const bool paired = dst.layout == Q38M_LAYOUT_MFMA16_PAIRED;
         const uint64_t dwords = elements / 8u;
         repack_w4_kernel<<<blocks_for(dwords, 256), 256, 0, stream>>>(
             static_cast<const uint32_t*>(src.data), static_cast<uint32_t*>(const_cast<void*>(dst.data)),
-            src.rows, src.columns, dwords);
+            src.rows, src.columns, paired, dwords);
         const uint64_t scales = elements / 32u;
         repack_w4_scales_kernel<<<blocks_for(scales, 256), 256, 0, stream>>>(
             static_cast<const uint16_t*>(src.scales),
-            static_cast<uint16_t*>(const_cast<void*>(dst.scales)), src.rows, src.columns, scales);
+            static_cast<uint16_t*>(const_cast<void*>(dst.scales)), src.rows, src.columns, paired,
+            scales);
     } else {
         const uint64_t vectors = elements / 16u;
         repack_w8_kernel<<<blocks_for(vectors, 256), 256, 0, stream>>>(

@@ -52,7 +52,7 @@ class Layer:
                                         2 * W.INTER, W.HIDDEN, gsigma)
         self.dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dbits], dgroup, W.EXPERTS, W.HIDDEN,
                                         W.INTER, dsigma)
-        self.gu = q38m.repack(self.gu_rm)
+        self.gu = q38m.repack(self.gu_rm, paired=True)
         self.dn = q38m.repack(self.dn_rm)
         self.host_gu = self.host_dn = None
         if with_host:

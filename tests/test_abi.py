@@ -98,7 +98,7 @@ def test_workspace_binding(q38m):
         q38m.call("q38m_moe_prefill_workspace_bind", base + 16, sizes[2], 512, ctypes.byref(ws))
 
 
-def fake_weights(q38m, fmt=2, group=32, layout=2, rows=1024, cols=2048, experts=512):
+def fake_weights(q38m, fmt=2, group=32, layout=3, rows=1024, cols=2048, experts=512):
     return q38m.ExpertWeights(0x200000, 0x400000, fmt, group, 1, layout, experts, rows, cols)
 
 
@@ -116,7 +116,8 @@ def test_gate_up_validation(q38m):
         call(fake_weights(q38m, layout=0))
     for bad in (fake_weights(q38m, fmt=3), fake_weights(q38m, group=128),
                 fake_weights(q38m, rows=1280), fake_weights(q38m, cols=2560),
-                fake_weights(q38m, experts=256)):
+                fake_weights(q38m, experts=256),
+                fake_weights(q38m, layout=2)):  # gate/up needs the paired layout
         with pytest.raises(q38m.InvalidArgument):
             call(bad)
     with pytest.raises(q38m.InvalidArgument):
@@ -130,7 +131,7 @@ def test_gate_up_validation(q38m):
 
 
 def test_down_validation(q38m):
-    w8 = fake_weights(q38m, fmt=3, group=0, rows=2048, cols=512)
+    w8 = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)
     args = [0x10000, 0x20000, 0x30000, 10, 0x40000, None, 0]
     with pytest.raises(q38m.Unsupported):
         q38m.call("q38m_moe_grouped_down_v1",
@@ -138,10 +139,10 @@ def test_down_validation(q38m):
                   *args)
     with pytest.raises(q38m.InvalidArgument):  # W8 with a group size
         q38m.call("q38m_moe_grouped_down_v1",
-                  ctypes.byref(fake_weights(q38m, fmt=3, group=32, rows=2048, cols=512)), *args)
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=32, layout=2, rows=2048, cols=512)), *args)
     with pytest.raises(q38m.InvalidArgument):  # transposed shape
         q38m.call("q38m_moe_grouped_down_v1",
-                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, rows=512, cols=2048)), *args)
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=2, rows=512, cols=2048)), *args)
     args[2] = None
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(w8), *args)
@@ -173,7 +174,7 @@ def test_routing_and_quant_validation(q38m):
 
 def test_decode_and_step_validation(q38m):
     gu = fake_weights(q38m)
-    dn = fake_weights(q38m, fmt=3, group=0, rows=2048, cols=512)
+    dn = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)
     with pytest.raises(q38m.InvalidArgument):  # top_k above 10
         q38m.call("q38m_moe_routed_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000,
                   0x2000, 0x3000, 11, 0x4000, 0x5000, None, 0)
@@ -202,6 +203,11 @@ def test_repack_and_synth_validation(q38m):
     with pytest.raises(q38m.Unsupported):  # W4 per-channel has no MFMA16 layout
         q38m.call("q38m_repack_expert_weights", ctypes.byref(fake_weights(q38m, group=0, layout=0)),
                   ctypes.byref(fake_weights(q38m, group=0, layout=2)), None, 0)
+    w8_src = fake_weights(q38m, fmt=3, group=0, layout=0, rows=2048, cols=512)
+    with pytest.raises(q38m.Unsupported):  # the paired layout is W4-only
+        q38m.call("q38m_repack_expert_weights", ctypes.byref(w8_src),
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=3, rows=2048, cols=512)),
+                  None, 0)
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_synth_fill", 9, 1, 1, 16, 1.0, 0, 0, None, 0, 0x1000, None, 0)
     with pytest.raises(q38m.InvalidArgument):  # odd W4 count

@@ -126,7 +126,7 @@ def test_reference_onehot_kat(q38m, orc, down_bits):
     class L:
         pass
     layer = L()
-    layer.gu, layer.dn = q38m.repack(gu), q38m.repack(dn)
+    layer.gu, layer.dn = q38m.repack(gu, paired=True), q38m.repack(dn)
     hidden = np.zeros((2, H), np.float32)
     hidden[0, 0], hidden[1, 0] = kat["hidden_values"]
     ws = q38m.PrefillWorkspace_(2)

@@ -198,16 +198,22 @@ def test_pack_hidden_gather(q38m, orc):
     assert np.array_equal(got, hidden[p["packed"] // 10])
 
 
-def repack_w4_host(data, scales, experts, rows, cols):
-    """numpy restatement of the MFMA16 W4 layout documented in q38m.h."""
+def repack_w4_host(data, scales, experts, rows, cols, paired):
+    """numpy restatement of the quad-major MFMA16 W4 layouts documented in
+    q38m.h: [e][kq][slot][lane=(q,n)][j][byte i], byte i = nib(k0+i) |
+    nib(k0+4+i) << 4; paired slots alternate tiles of the two row halves."""
     nib = np.empty(experts * rows * cols, np.uint8)
     nib[0::2] = data & 0xF
     nib[1::2] = data >> 4
     nib = nib.reshape(experts, rows // 16, 16, cols // 128, 4, 4, 8)  # e,rt,n,kq,j,q,k8
-    # out[e][rt][kq][q][n][j][byte i] = nib(k0+i) | nib(k0+4+i) << 4
-    nib = nib.transpose(0, 1, 3, 5, 2, 4, 6)  # e,rt,kq,q,n,j,k8
+    sc = scales.reshape(experts, rows // 16, 16, cols // 128, 4)      # e,rt,n,kq,j
+    tiles = rows // 16
+    order = np.arange(tiles)
+    if paired:
+        order = np.stack([order[:tiles // 2], order[tiles // 2:]], 1).reshape(-1)
+    nib = nib[:, order].transpose(0, 3, 1, 5, 2, 4, 6)  # e,kq,slot,q,n,j,k8
     out = nib[..., 0:4] | (nib[..., 4:8] << 4)
-    sc = scales.reshape(experts, rows // 16, 16, cols // 128, 4).transpose(0, 1, 3, 2, 4)
+    sc = sc[:, order].transpose(0, 3, 1, 2, 4)          # e,kq,slot,n,j
     return out.reshape(-1), sc.reshape(-1)
 
 
@@ -219,10 +225,12 @@ def repack_w8_host(data, experts, rows, cols):
 def test_repack_layouts(q38m, orc):
     E, R, C = 4, 64, 512
     w4 = q38m.synth_weights(3, 60, q38m.FORMAT_W4_SYM, 32, E, R, C, 0.02)
-    p4 = q38m.repack(w4)
-    d, s = repack_w4_host(host(w4.data, np.uint8), host(w4.scales, np.uint16), E, R, C)
-    assert np.array_equal(host(p4.data, np.uint8), d)
-    assert np.array_equal(host(p4.scales, np.uint16), s)
+    for paired in (False, True):
+        p4 = q38m.repack(w4, paired=paired)
+        d, s = repack_w4_host(host(w4.data, np.uint8), host(w4.scales, np.uint16), E, R, C,
+                              paired)
+        assert np.array_equal(host(p4.data, np.uint8), d)
+        assert np.array_equal(host(p4.scales, np.uint16), s)
     w8 = q38m.synth_weights(3, 62, q38m.FORMAT_W8_SYM, 0, E, R, C, 0.002)
     p8 = q38m.repack(w8)
     assert np.array_equal(host(p8.data, np.uint8), repack_w8_host(host(w8.data, np.uint8), E, R, C))
