@@ -217,12 +217,13 @@ def main():
 
 def bench_decode(q38m, W, torch, tokens):
     """Config 3: one token through 48 MoE layers (W4 g32 gate/up + W8 down),
-    a fresh router draw per layer, residual add between layers.  Reports
-    HBM GB/s over the selected experts' weights."""
+    a fresh router draw per layer, residual add between layers, through the
+    fused q38m_moe_decode_v1 (top-k + experts + residual, two launches per
+    layer).  Timed eagerly and as one HIP graph holding every layer of
+    `tokens` tokens; reports HBM GB/s over the selected experts' weights."""
     spec = W.CONFIGS[3]
     seed, layers = spec["seed"], spec["layers"]
     fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
-    sh = torch.cuda.current_stream().cuda_stream
     stack = []
     for layer in range(layers):
         gu_tag, dn_tag, _, _ = W.layer_tags(layer)
@@ -235,25 +236,22 @@ def bench_decode(q38m, W, torch, tokens):
         del dn_rm
         stack.append((gu, dn))
     resident = sum(gu.nbytes + dn.nbytes for gu, dn in stack)
+    # one fresh router draw per (token, layer); the first two tokens warm up
     logits = torch.empty(tokens + 2, layers, W.EXPERTS, dtype=torch.float32, device="cuda")
     q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, 2, logits.numel(), logits)
-    state = torch.empty(2, W.HIDDEN, dtype=torch.int16, device="cuda")
+    # state[l] is layer l's input; layer l writes bf16(state[l] + moe(state[l])) to state[l+1]
+    state = torch.empty(layers + 1, W.HIDDEN, dtype=torch.int16, device="cuda")
     q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, 1, W.HIDDEN, state[0])
-    out = torch.empty(W.HIDDEN, dtype=torch.int16, device="cuda")
-    ids = torch.empty(W.TOPK, dtype=torch.int32, device="cuda")
-    wts = torch.empty(W.TOPK, dtype=torch.float32, device="cuda")
-    scratch = torch.empty(q38m.lib().q38m_moe_decode_scratch_bytes() + 256, dtype=torch.uint8,
+    scratch = torch.zeros(q38m.lib().q38m_moe_decode_scratch_bytes(), dtype=torch.uint8,
                           device="cuda")
 
     def token(t):
+        sh = torch.cuda.current_stream().cuda_stream
         for layer, (gu, dn) in enumerate(stack):
-            q38m.call("q38m_topk_router_f32", logits[t, layer].data_ptr(), ids.data_ptr(),
-                      wts.data_ptr(), 1, W.EXPERTS, W.TOPK, 1, sh, 0)
-            q38m.call("q38m_moe_routed_decode_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
-                      state[0].data_ptr(), ids.data_ptr(), wts.data_ptr(), W.TOPK,
-                      scratch.data_ptr(), out.data_ptr(), sh, 0)
-            q38m.call("q38m_residual_add_bf16", state[0].data_ptr(), out.data_ptr(),
-                      state[0].data_ptr(), W.HIDDEN, sh, 0)
+            q38m.call("q38m_moe_decode_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                      state[layer].data_ptr(), logits[t, layer].data_ptr(), W.TOPK, None, None,
+                      state[layer].data_ptr(), scratch.data_ptr(), state[layer + 1].data_ptr(),
+                      sh, 0)
 
     token(tokens)
     token(tokens + 1)
@@ -265,16 +263,40 @@ def bench_decode(q38m, W, torch, tokens):
         token(t)
     stop.record()
     torch.cuda.synchronize()
-    ms_token = start.elapsed_time(stop) / tokens
+    ms_eager = start.elapsed_time(stop) / tokens
+    eager_final = state[layers].clone()
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for t in range(tokens):
+            token(t)
+    graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(state[layers], eager_final):
+        raise RuntimeError("decode graph replay differs from the eager run")
+    replays = 3
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    ms_graph = start.elapsed_time(stop) / (replays * tokens)
+    if not torch.equal(state[layers], eager_final):
+        raise RuntimeError("decode graph replays differ from the eager run")
+
     bytes_token = layers * W.TOPK * W.algorithmic_bytes_per_expert(W.W4, W.W8)
-    gbps = bytes_token / (ms_token * 1e-3) / 1e9
+
+    def rate(ms):
+        gbps = bytes_token / (ms * 1e-3) / 1e9
+        return {"us_per_token": round(ms * 1e3, 2), "us_per_layer": round(ms * 1e3 / layers, 3),
+                "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+    graph_rate = rate(ms_graph)
     return {"workload": spec["name"], "tokens": tokens, "layers": layers,
             "resident_weight_GB": round(resident / 1e9, 2),
-            "us_per_token": round(ms_token * 1e3, 2),
-            "us_per_layer": round(ms_token * 1e3 / layers, 3),
-            "algorithmic_bytes_per_token": bytes_token,
-            "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "launches_per_layer": 4, "mode": "eager"}
+            "algorithmic_bytes_per_token": bytes_token, "launches_per_layer": 2,
+            "entry_point": "q38m_moe_decode_v1", **graph_rate, "mode": "hip_graph",
+            "eager": rate(ms_eager)}
 
 
 def cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, gpu_out, T):

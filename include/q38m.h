@@ -259,6 +259,24 @@ int q38m_moe_routed_decode_v1(const q38m_expert_weights_v1* gate_up,
                               void* scratch, uint16_t* routed_output,
                               void* stream, int device);
 
+/* Fused batch-1 decode from fp32 router logits: the whole tokens == 1
+ * sequence of run_moe (cuda/cuda_backend.cu:1516-1605) after the router
+ * GEMV -- cuda_topk_router_bf16 (include/q38/cuda_kernels.h:83-91, here on
+ * 512 experts, normalised), cuda_moe_routed_bf16 (include/q38/cuda_moe.h:
+ * 17-29) and cuda_moe_combine_shared_bf16 (include/q38/cuda_moe.h:31-37)
+ * -- in two launches.  shared_output/shared_gate: both null (no shared
+ * term) or both given.  residual: null, or output = bf16(residual + moe).
+ * Bit-identical to q38m_moe_prefill_v1 with tokens == 1 (then
+ * q38m_residual_add_bf16).  scratch as above; the chosen ids are left in
+ * its first 40 bytes. */
+int q38m_moe_decode_v1(const q38m_expert_weights_v1* gate_up,
+                       const q38m_expert_weights_v1* down,
+                       const uint16_t* hidden, const float* logits,
+                       uint32_t top_k, const uint16_t* shared_output,
+                       const uint16_t* shared_gate, const uint16_t* residual,
+                       void* scratch, uint16_t* output, void* stream,
+                       int device);
+
 /* ---- weight layout (cuda/cuda_weights.cu:229-285 re-tiles W4 at load) */
 size_t q38m_expert_weights_bytes(const q38m_expert_weights_v1* w,
                                  size_t* scale_bytes);

@@ -129,6 +129,19 @@ inline void cuda_moe_routed_bf16(const ExpertWeightsV1& gate_up_experts,
                                     device));
 }
 
+// Fused tokens == 1 MoE step from fp32 router logits: top-k, routed experts
+// and the optional gated shared term (and residual), in two launches.
+inline void moe_decode(const q38m_expert_weights_v1& gate_up_experts,
+                       const q38m_expert_weights_v1& down_experts, const std::uint16_t* hidden,
+                       const float* logits, std::uint32_t top_k,
+                       const std::uint16_t* shared_output, const std::uint16_t* shared_gate,
+                       const std::uint16_t* residual, void* scratch, std::uint16_t* output,
+                       void* stream, int device) {
+    check(q38m_moe_decode_v1(&gate_up_experts, &down_experts, hidden, logits, top_k,
+                             shared_output, shared_gate, residual, scratch, output, stream,
+                             device));
+}
+
 inline void cuda_moe_combine_shared_bf16(const std::uint16_t* routed_output,
                                          const std::uint16_t* shared_output,
                                          const std::uint16_t* shared_gate,

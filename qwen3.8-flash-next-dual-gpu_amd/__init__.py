@@ -133,6 +133,8 @@ SIGNATURES = {
     "q38m_moe_routed_decode_v1": (_INT, [ctypes.POINTER(ExpertWeights),
                                          ctypes.POINTER(ExpertWeights), _P, _P, _P, _U32, _P, _P,
                                          _P, _INT]),
+    "q38m_moe_decode_v1": (_INT, [ctypes.POINTER(ExpertWeights), ctypes.POINTER(ExpertWeights),
+                                  _P, _P, _U32, _P, _P, _P, _P, _P, _P, _INT]),
     "q38m_expert_weights_bytes": (_SZ, [ctypes.POINTER(ExpertWeights), ctypes.POINTER(_SZ)]),
     "q38m_repack_expert_weights": (_INT, [ctypes.POINTER(ExpertWeights),
                                           ctypes.POINTER(ExpertWeights), _P, _INT]),

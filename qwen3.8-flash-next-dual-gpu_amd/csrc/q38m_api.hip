@@ -356,9 +356,28 @@ int q38m_moe_routed_decode_v1(const q38m_expert_weights_v1* gate_up,
         !scratch || !routed_output || !aligned(hidden, 16) || !aligned(scratch, 16))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid routed MoE buffers");
     if (int rc = select_device(device)) return rc;
-    return finish(q38m::launch_decode(*gate_up, *down, hidden, expert_ids, expert_weights, top_k,
-                                      scratch, routed_output, as_stream(stream)),
+    return finish(q38m::launch_decode(*gate_up, *down, hidden, nullptr, expert_ids,
+                                      expert_weights, top_k, nullptr, nullptr, nullptr, scratch,
+                                      routed_output, as_stream(stream)),
                   "decode routed MoE kernels");
+}
+
+int q38m_moe_decode_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert_weights_v1* down,
+                       const uint16_t* hidden, const float* logits, uint32_t top_k,
+                       const uint16_t* shared_output, const uint16_t* shared_gate,
+                       const uint16_t* residual, void* scratch, uint16_t* output, void* stream,
+                       int device) {
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (int rc = check_weights(down, false)) return rc;
+    if (!hidden || !logits || top_k == 0 || top_k > Q38M_ROUTE_TOPK || !scratch || !output ||
+        !aligned(hidden, 16) || !aligned(logits, 16) || !aligned(scratch, 16) ||
+        ((shared_output == nullptr) != (shared_gate == nullptr)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid decode MoE buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_decode(*gate_up, *down, hidden, logits, nullptr, nullptr, top_k,
+                                      shared_output, shared_gate, residual, scratch, output,
+                                      as_stream(stream)),
+                  "decode MoE kernels");
 }
 
 size_t q38m_expert_weights_bytes(const q38m_expert_weights_v1* w, size_t* scale_bytes) {

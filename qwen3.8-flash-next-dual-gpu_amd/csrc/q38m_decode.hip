@@ -1,86 +1,193 @@
 // Batch-1 decode: streams only the top_k selected experts (the tokens == 1
-// branch of cuda_moe_routed_bf16, cuda/q38_moe.cu:388-458).  The
-// arithmetic is the prefill contract evaluated for one token -- int8 token
-// quantisation, per-group int32 accumulators, the fp32 group chain in group
-// order, the SwiGLU fold, per-route mid quantisation, down, and the rank-
-// order sum -- so decode equals the grouped prefill with tokens == 1 bit
-// for bit.  (The reference's decode applies the router weight after down
-// and differs from its prefill by up to 0.075, cuda_kernel_tests.cu:370.)
+// branch of run_moe, cuda/cuda_backend.cu:1516-1605: cuda_topk_router_bf16,
+// cuda_moe_routed_bf16 (cuda/q38_moe.cu:388-458), cuda_moe_combine_shared_bf16).
+// The arithmetic is the prefill contract evaluated for one token -- int8
+// token quantisation, per-group int32 accumulators, the fp32 group chain in
+// group order, the SwiGLU fold, per-route mid quantisation, down, and the
+// rank-order sum -- so decode equals the grouped prefill with tokens == 1
+// bit for bit.  (The reference's decode applies the router weight after
+// down and differs from its prefill by up to 0.075, cuda_kernel_tests.cu:370.)
 //
-// Two launches per layer:
-//   gate/up  grid (I/16 tile pairs, top_k), 4 waves split K in quarters and
-//            every wave issues all of its weight loads before any math, so
-//            the whole 10-expert weight set is in flight at once; the int32
-//            group accumulators meet in LDS for the ordered fp32 chain.
-//   down     grid (H/16 tiles), one wave per route; quantises its route's
-//            mid row, runs the down tile, and the block sums the routes in
-//            rank order.
+// At one token the layer is a latency chain: on MI355X a dependent kernel
+// boundary costs ~1.7 us in a graph and a device-scope grid barrier ~5 us,
+// so the layer is two launches and every byte of each launch is requested
+// as early as its address is known.
+//
+//   gate/up  256 workgroups x 10 waves (one wave per route).  Wave 9 ranks
+//            the 512 router logits (or reads the given ids) while waves 0-3
+//            load the token; then every lane issues its 72 bytes of weights
+//            at once (46 KB per workgroup, the layer's 11.8 MB in flight
+//            together).  Workgroup b owns channels 16p+n0, 16p+n0+1 of all
+//            routes; the eight workgroups sharing a pair tile's 128-byte
+//            lines sit on one XCD (b % 8), so each line crosses HBM once.
+//   down     256 workgroups x 10 waves.  Each wave loads the ids and its
+//            route's mid row together, quantises the row in registers, and
+//            streams 8 output channels x 512 columns; int32 partials meet by
+//            shuffles, routes are summed in rank order, then the optional
+//            gated shared term and residual are applied.
 #include "q38m_device.h"
 #include "q38m_internal.h"
 
 namespace q38m {
 namespace {
 
+constexpr uint32_t kDecodeBlocks = 256;
+constexpr uint32_t kDecodeThreads = 64u * kTopK;
+
+// Monotonic unsigned key of a float: larger key = larger value; -0 and +0
+// share a key (equal under <), NaN maps below every number.
+__device__ __forceinline__ uint32_t order_key(float v) {
+    const uint32_t b = __float_as_uint(v + 0.0f);
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return v == v ? k : 0u;
+}
+
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Wave-wide max: quad swaps, half-row and row mirrors (DPP), then the four
+// row results through scalar registers.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    x = umax(x, dpp_u32<0xB1>(x));   // quad_perm [1,0,3,2]
+    x = umax(x, dpp_u32<0x4E>(x));   // quad_perm [2,3,0,1]
+    x = umax(x, dpp_u32<0x141>(x));  // row_half_mirror
+    x = umax(x, dpp_u32<0x140>(x));  // row_mirror
+    const uint32_t r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
+    const uint32_t r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+    return umax(umax(r0, r1), umax(r2, r3));
+}
+
+__device__ __forceinline__ float wave_max_f32(float x) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) x = fmaxf(x, __shfl_xor(x, offset, 64));
+    return x;
+}
+
+// Top-k of 512 logits by (value desc, id asc), one wave: lane l holds
+// experts 8l..8l+7, so between lanes the lower lane has the lower ids and a
+// tie on the wave maximum goes to the lowest such lane; inside a lane the
+// strict > scan keeps the lowest id.  The weights are exp(l_r - l_0) over
+// the rank-order sum of the numerators (q38_kernels.cu:431-479).  Returns
+// this lane's rank (lane < top_k) id and weight.
+__device__ __forceinline__ void wave_topk512(const float* __restrict__ logits, uint32_t top_k,
+                                             uint32_t lane, int32_t& id_out, float& w_out) {
+    const float4* row = reinterpret_cast<const float4*>(logits) + 2u * lane;
+    const float4 a = row[0], b = row[1];
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t key[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) key[j] = order_key(v[j]);
+    uint32_t taken = 0;
+    float mine_v = 0.0f, top_v = 0.0f;
+    int32_t mine_id = -1;
+    for (uint32_t rank = 0; rank < top_k; ++rank) {
+        // best_j = 512 when a lane has nothing left: an id >= 512 (invalid)
+        // if every remaining logit is NaN
+        uint32_t best = 0, best_j = 512;
+        float best_v = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 8u; ++j) {
+            if (((taken >> j) & 1u) == 0u && key[j] > best) {
+                best = key[j];
+                best_j = j;
+                best_v = v[j];
+            }
+        }
+        const uint32_t m = wave_max_u32(best);
+        const uint64_t tied = __ballot(best == m);
+        const uint32_t win = static_cast<uint32_t>(__builtin_ctzll(tied));
+        const uint32_t win_j = __builtin_amdgcn_readlane(best_j, win);
+        const float win_v = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(best_v), win));
+        if (lane == win && best_j < 8u) taken |= 1u << best_j;
+        if (lane == rank) {
+            mine_v = win_v;
+            mine_id = static_cast<int32_t>(8u * win + win_j);
+        }
+        if (rank == 0) top_v = win_v;
+    }
+    const float numerator = lane < top_k ? exp_q(mine_v - top_v) : 0.0f;
+    float denominator = 0.0f;
+    for (uint32_t rank = 0; rank < top_k; ++rank)
+        denominator += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(numerator), rank));
+    id_out = mine_id;
+    w_out = numerator / denominator;
+}
+
 template <uint32_t H, uint32_t I>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(
+__global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     const uint4* __restrict__ w, const uint2* __restrict__ s,
-    const uint16_t* __restrict__ hidden, const int32_t* __restrict__ ids,
-    const float* __restrict__ route_weights, uint16_t* __restrict__ mid) {
+    const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
+    const int32_t* __restrict__ ids_in, const float* __restrict__ weights_in, uint32_t top_k,
+    int32_t* __restrict__ ids_out, uint16_t* __restrict__ mid) {
     constexpr uint32_t kQuads = H / 128u;
-    constexpr uint32_t kGroups = H / 32u;
-    constexpr uint32_t kTiles = 2u * I / 16u;
-    constexpr uint32_t kQuadsPerWave = kQuads / 4u;
-    static_assert(H == 256u * 8u, "one 8-element chunk of the token per thread");
-    __shared__ float acc_lds[kGroups][32];
-    __shared__ float scale_lds[kGroups][32];
-    __shared__ uint2 xq_lds[H / 8u];
-    __shared__ float wave_max[4];
+    constexpr uint32_t kSlots = 2u * I / 16u;
+    constexpr uint32_t kPairs = I / 16u;
+    constexpr uint32_t kQuadPad = 9u;  // 144-byte rows: the 16 quads hit disjoint banks
+    static_assert(H == 256u * 8u && kQuads == 16u, "16 quads, one 8-element token chunk per thread");
+    static_assert(kPairs * 8u == kDecodeBlocks, "eight workgroups per pair tile");
+    __shared__ int32_t ids_lds[kTopK];
+    __shared__ float wr_lds[kTopK];
+    __shared__ float amax_lds[4];
+    __shared__ uint4 x_lds[kQuads * kQuadPad];
 
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t n = lane & 15u;
-    const uint32_t q = lane >> 4;
-    const uint32_t gate_tile = blockIdx.x;  // = the gate/up pair index
-    const uint32_t route = blockIdx.y;
-    const int32_t id = ids[route];
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t slot8 = blockIdx.x >> 3;
+    const uint32_t pair = 4u * (blockIdx.x & 7u) + (slot8 >> 3);
+    const uint32_t n0 = 2u * (slot8 & 7u);
+
+    uint4 hv = make_uint4(0u, 0u, 0u, 0u);
+    if (wave < 4u) hv = reinterpret_cast<const uint4*>(hidden)[threadIdx.x];
+    if (wave == kTopK - 1u) {
+        int32_t id = -1;
+        float wr = 0.0f;
+        if (logits != nullptr) {
+            wave_topk512(logits, top_k, lane, id, wr);
+        } else if (lane < top_k) {
+            id = ids_in[lane];
+            wr = weights_in[lane];
+        }
+        if (lane < kTopK) {
+            ids_lds[lane] = id;
+            wr_lds[lane] = wr;
+        }
+        if (blockIdx.x == 0 && lane < top_k && ids_out != nullptr) ids_out[lane] = id;
+    }
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    if (wave < 4u) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] & 0xffffu)));
+            amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] >> 16)));
+        }
+        amax = wave_max_f32(amax);
+        if (lane == 0) amax_lds[wave] = amax;
+    }
+    __syncthreads();
+
+    // every lane's weights: lane = kq + 16*(c + 2u), u = gate/up, c = channel
+    const uint32_t route = wave;
+    const int32_t id = route < top_k ? ids_lds[route] : -1;
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
+    const uint32_t kq = lane & 15u;
+    const uint32_t c = (lane >> 4) & 1u;
+    const uint32_t u = lane >> 5;
+    const size_t tile = (static_cast<size_t>(e) * kQuads + kq) * kSlots + 2u * pair + u;
+    const uint4* wp = w + tile * 64u + n0 + c;
+    const uint4 b0 = wp[0], b1 = wp[16], b2 = wp[32], b3 = wp[48];
+    const uint2 sc = s[tile * 16u + n0 + c];
 
-    // weights first: every load of this wave's K quarter is issued now
-    // (paired quad-major layout: gate tile of pair p in slot 2p, up in 2p+1)
-    uint4 bg[kQuadsPerWave], bu[kQuadsPerWave];
-    uint2 cg[kQuadsPerWave], cu[kQuadsPerWave];
-    const uint4* wg = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u + lane;
-    const uint4* wu = wg + 64u;
-    const uint2* sg = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u + n;
-    const uint2* su = sg + 16u;
-#pragma unroll
-    for (uint32_t i = 0; i < kQuadsPerWave; ++i) {
-        const uint32_t kq = wave * kQuadsPerWave + i;
-        bg[i] = wg[kq * kTiles * 64u];
-        bu[i] = wu[kq * kTiles * 64u];
-        cg[i] = sg[kq * kTiles * 16u];
-        cu[i] = su[kq * kTiles * 16u];
-    }
-
-    // int8 quantisation of the token (same arithmetic as the row kernel)
-    const uint4 hv = reinterpret_cast<const uint4*>(hidden)[threadIdx.x];
-    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] & 0xffffu)));
-        amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] >> 16)));
-    }
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, offset, 64));
-    if (lane == 0) wave_max[wave] = amax;
-    __syncthreads();
-    amax = fmaxf(fmaxf(wave_max[0], wave_max[1]), fmaxf(wave_max[2], wave_max[3]));
+    // int8 token (same arithmetic as the row quantiser)
+    const float amax = fmaxf(fmaxf(amax_lds[0], amax_lds[1]), fmaxf(amax_lds[2], amax_lds[3]));
     float xs = amax / 127.0f;
     if (xs == 0.0f) xs = 1.0f;
-    {
+    if (wave < 4u) {
         uint32_t packed[2] = {0u, 0u};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -89,91 +196,111 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(
             r = fminf(fmaxf(r, -127.0f), 127.0f);
             packed[i >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (i & 3));
         }
-        xq_lds[threadIdx.x] = make_uint2(packed[0], packed[1]);
+        const uint32_t k = 8u * threadIdx.x;
+        reinterpret_cast<uint2*>(x_lds)[(k >> 7) * (2u * kQuadPad) + ((k & 127u) >> 3)] =
+            make_uint2(packed[0], packed[1]);
     }
     __syncthreads();
 
-    const v4i zero = {0, 0, 0, 0};
+    // group j of quad kq, chunk q: k = 32(4kq+j) + 8q + {0..3} (low nibbles)
+    // and + {4..7} (high nibbles); nibbles sit in the high half of each byte
+    // (16*w), so acc is 16x the group accumulator.
+    uint32_t xw[32];
 #pragma unroll
-    for (uint32_t i = 0; i < kQuadsPerWave; ++i) {
-        const uint32_t kq = wave * kQuadsPerWave + i;
-        const uint32_t wgw[4] = {bg[i].x, bg[i].y, bg[i].z, bg[i].w};
-        const uint32_t wuw[4] = {bu[i].x, bu[i].y, bu[i].z, bu[i].w};
-        const uint32_t sgw[2] = {cg[i].x, cg[i].y};
-        const uint32_t suw[2] = {cu[i].x, cu[i].y};
+    for (uint32_t i = 0; i < 8u; ++i) {
+        const uint4 xv = x_lds[kq * kQuadPad + i];
+        xw[4 * i] = xv.x; xw[4 * i + 1] = xv.y; xw[4 * i + 2] = xv.z; xw[4 * i + 3] = xv.w;
+    }
+    const uint4 bq[4] = {b0, b1, b2, b3};
+    int acc[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (uint32_t q = 0; q < 4u; ++q) {
+        const uint32_t wq[4] = {bq[q].x, bq[q].y, bq[q].z, bq[q].w};
 #pragma unroll
         for (uint32_t j = 0; j < 4u; ++j) {
-            const uint32_t g = 4u * kq + j;
-            const long a = as_long(xq_lds[4u * g + q]);
-            const v4i dg = mfma_i8_16x16x32(a, unpack_w4x16(wgw[j]), zero);
-            const v4i du = mfma_i8_16x16x32(a, unpack_w4x16(wuw[j]), zero);
-            if (q == 0u) {
-                const uint32_t hg = (j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu);
-                const uint32_t hu = (j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu);
-                acc_lds[g][n] = static_cast<float>(dg[0]);
-                acc_lds[g][16u + n] = static_cast<float>(du[0]);
-                scale_lds[g][n] = f16_to_f32(hg) * 0.0625f;
-                scale_lds[g][16u + n] = f16_to_f32(hu) * 0.0625f;
-            }
+            const uint32_t lo = (wq[j] << 4) & 0xf0f0f0f0u;
+            const uint32_t hi = wq[j] & 0xf0f0f0f0u;
+            acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(xw[8u * j + 2u * q]), acc[j], false);
+            acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xw[8u * j + 2u * q + 1u]), acc[j], false);
         }
     }
-    __syncthreads();
-
-    if (wave == 0u && lane < 32u) {
-        float y = 0.0f;
-        for (uint32_t g = 0; g < kGroups; ++g)
-            y = __builtin_fmaf(acc_lds[g][lane], scale_lds[g][lane], y);
-        const float y_up = __shfl(y, static_cast<int>(lane + 16u), 64);
-        if (lane < 16u) {
-            const float y_gate = y * xs;
-            const float y_u = y_up * xs;
-            const uint32_t value = valid ? swiglu_fold(y_gate, y_u, route_weights[route]) : 0u;
-            mid[static_cast<size_t>(route) * I + gate_tile * 16u + n] =
-                static_cast<uint16_t>(value);
-        }
+    const float s0 = f16_to_f32(sc.x & 0xffffu) * 0.0625f, s1 = f16_to_f32(sc.x >> 16) * 0.0625f;
+    const float s2 = f16_to_f32(sc.y & 0xffffu) * 0.0625f, s3 = f16_to_f32(sc.y >> 16) * 0.0625f;
+    // fp32 chain in group order: lane kq continues lane kq-1's value (row_shr:1
+    // inside each 16-lane row); after 16 steps lane 15 holds the row's y.
+    float y = 0.0f;
+#pragma unroll
+    for (uint32_t step = 0; step < kQuads; ++step) {
+        const float yin = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
+        float t = __builtin_fmaf(static_cast<float>(acc[0]), s0, yin);
+        t = __builtin_fmaf(static_cast<float>(acc[1]), s1, t);
+        t = __builtin_fmaf(static_cast<float>(acc[2]), s2, t);
+        y = __builtin_fmaf(static_cast<float>(acc[3]), s3, t);
+    }
+    const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 15));
+    const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 31));
+    const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 47));
+    const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 63));
+    if (lane == 0 && route < top_k) {
+        const float wr = wr_lds[route];
+        const uint32_t m0 = valid ? swiglu_fold(g0 * xs, u0 * xs, wr) : 0u;
+        const uint32_t m1 = valid ? swiglu_fold(g1 * xs, u1 * xs, wr) : 0u;
+        *reinterpret_cast<uint32_t*>(mid + static_cast<size_t>(route) * I + 16u * pair + n0) =
+            m0 | (m1 << 16);
     }
 }
 
 template <uint32_t H, uint32_t I, bool kW4>
-__global__ __launch_bounds__(640) void decode_down_kernel(
-    const uint4* __restrict__ w, const void* __restrict__ s,
-    const uint16_t* __restrict__ mid, const int32_t* __restrict__ ids,
-    uint32_t top_k, uint16_t* __restrict__ out) {
+__global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
+    const uint4* __restrict__ w, const void* __restrict__ s, const uint16_t* __restrict__ mid,
+    const int32_t* __restrict__ ids, uint32_t top_k, const uint16_t* __restrict__ shared_output,
+    const uint16_t* __restrict__ shared_gate, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out) {
     constexpr uint32_t kTiles = H / 16u;
-    constexpr uint32_t kBlocks = kW4 ? I / 128u : I / 64u;  // W4: quads, W8: 64-wide blocks
     static_assert(I == 64u * 8u, "one 8-element chunk of the mid row per lane");
-    __shared__ uint2 mq_lds[kTopK][I / 8u];
-    __shared__ float o_lds[kTopK][16];
+    static_assert(kTiles * 2u == kDecodeBlocks, "eight output channels per workgroup");
+    __shared__ uint4 mq_lds[kTopK][I / 16u];
+    __shared__ float o_lds[kTopK][8];
 
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t route = threadIdx.x >> 6;
-    const uint32_t n = lane & 15u;
-    const uint32_t q = lane >> 4;
-    const uint32_t tile = blockIdx.x;
-    const int32_t id = ids[route];
+    const uint32_t route = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t slot8 = blockIdx.x >> 3;
+    const uint32_t tile = 16u * (blockIdx.x & 7u) + (slot8 >> 1);
+    const uint32_t n0 = 8u * (slot8 & 1u);
+    const bool active = route < top_k;
+
+    const int32_t id = active ? ids[route] : -1;
+    uint4 mv = make_uint4(0u, 0u, 0u, 0u);
+    if (active) mv = reinterpret_cast<const uint4*>(mid + static_cast<size_t>(route) * I)[lane];
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
 
-    // W8: tile-major [e][tile][kb]; W4: quad-major [e][kq][tile]
-    uint4 b[kBlocks];
-    const uint4* wt = kW4 ? w + (static_cast<size_t>(e) * kBlocks * kTiles + tile) * 64u + lane
-                          : w + static_cast<size_t>(e * kTiles + tile) * kBlocks * 64u + lane;
-    const uint32_t block_stride = kW4 ? kTiles * 64u : 64u;
-#pragma unroll
-    for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = wt[kb * block_stride];
-    uint2 c[kW4 ? kBlocks : 1];
+    const uint32_t c = lane & 7u;
+    uint4 bq[4];
+    uint2 sc = make_uint2(0u, 0u);
     float ws = 0.0f;
     if constexpr (kW4) {
-        const uint2* st = static_cast<const uint2*>(s) +
-                          (static_cast<size_t>(e) * kBlocks * kTiles + tile) * 16u + n;
-#pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb) c[kb] = st[kb * kTiles * 16u];
+        // lane = c + 8*(kq + 4*qh): quad kq, chunks q = 2qh, 2qh+1
+        constexpr uint32_t kQuads = I / 128u;
+        const uint32_t kq = (lane >> 3) & 3u, qh = lane >> 5;
+        const size_t t = (static_cast<size_t>(e) * kQuads + kq) * kTiles + tile;
+        const uint4* wp = w + t * 64u + 32u * qh + n0 + c;
+        bq[0] = wp[0];
+        bq[1] = wp[16];
+        sc = static_cast<const uint2*>(s)[t * 16u + n0 + c];
     } else {
-        ws = f16_to_f32(static_cast<const uint16_t*>(s)[static_cast<size_t>(e) * H + tile * 16u + n]);
+        // lane = c + 8*kb: 64-column block kb, chunks q = 0..3
+        constexpr uint32_t kBlocks = I / 64u;
+        const uint32_t kb = lane >> 3;
+        const uint4* wp = w + ((static_cast<size_t>(e) * kTiles + tile) * kBlocks + kb) * 64u + n0 + c;
+        bq[0] = wp[0];
+        bq[1] = wp[16];
+        bq[2] = wp[32];
+        bq[3] = wp[48];
+        ws = f16_to_f32(static_cast<const uint16_t*>(s)[static_cast<size_t>(e) * H + 16u * tile + n0 + c]);
     }
 
     // quantise this route's mid row (8 elements per lane)
-    const uint4 mv = reinterpret_cast<const uint4*>(mid + static_cast<size_t>(route) * I)[lane];
     const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
     float amax = 0.0f;
 #pragma unroll
@@ -181,9 +308,7 @@ __global__ __launch_bounds__(640) void decode_down_kernel(
         amax = fmaxf(amax, fabsf(bf16_to_f32(mw[i] & 0xffffu)));
         amax = fmaxf(amax, fabsf(bf16_to_f32(mw[i] >> 16)));
     }
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, offset, 64));
+    amax = wave_max_f32(amax);
     float sm = amax / 127.0f;
     if (sm == 0.0f) sm = 1.0f;
     {
@@ -195,67 +320,105 @@ __global__ __launch_bounds__(640) void decode_down_kernel(
             r = fminf(fmaxf(r, -127.0f), 127.0f);
             packed[i >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (i & 3));
         }
-        mq_lds[route][lane] = make_uint2(packed[0], packed[1]);
+        reinterpret_cast<uint2*>(mq_lds[route])[lane] = make_uint2(packed[0], packed[1]);
     }
     __syncthreads();
 
     float o = 0.0f;
     if constexpr (kW4) {
-        const v4i zero = {0, 0, 0, 0};
-        float y = 0.0f;
+        // chunk q of quad kq covers, for group j, k = 32(4kq+j) + 8q + {0..7}
+        const uint32_t kq = (lane >> 3) & 3u, qh = lane >> 5;
+        const uint32_t* mrow = reinterpret_cast<const uint32_t*>(mq_lds[route]);
+        int acc[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (uint32_t kq = 0; kq < kBlocks; ++kq) {
-            const uint32_t bw[4] = {b[kq].x, b[kq].y, b[kq].z, b[kq].w};
-            const uint32_t cw[2] = {c[kq].x, c[kq].y};
+        for (uint32_t h = 0; h < 2u; ++h) {
+            const uint32_t q = 2u * qh + h;
+            const uint32_t wq[4] = {bq[h].x, bq[h].y, bq[h].z, bq[h].w};
 #pragma unroll
             for (uint32_t j = 0; j < 4u; ++j) {
-                const uint32_t g = 4u * kq + j;
-                const long a = as_long(mq_lds[route][4u * g + q]);
-                const v4i d = mfma_i8_16x16x32(a, unpack_w4x16(bw[j]), zero);
-                const uint32_t h = (j & 1u) ? (cw[j >> 1] >> 16) : (cw[j >> 1] & 0xffffu);
-                y = __builtin_fmaf(static_cast<float>(d[0]), f16_to_f32(h) * 0.0625f, y);
+                const uint32_t d = (32u * (4u * kq + j) + 8u * q) >> 2;
+                const uint2 xv = *reinterpret_cast<const uint2*>(mrow + d);
+                acc[j] = __builtin_amdgcn_sdot4(static_cast<int>((wq[j] << 4) & 0xf0f0f0f0u), static_cast<int>(xv.x), acc[j], false);
+                acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(wq[j] & 0xf0f0f0f0u), static_cast<int>(xv.y), acc[j], false);
             }
         }
-        o = y * sm;
-    } else {
-        v4i acc = {0, 0, 0, 0};
 #pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb) {
-            const uint2 lo = mq_lds[route][8u * kb + 2u * q];
-            const uint2 hi = mq_lds[route][8u * kb + 2u * q + 1u];
-            const uint4 a = make_uint4(lo.x, lo.y, hi.x, hi.y);
-            acc = mfma_i8_16x16x64(as_v4i(a), as_v4i(b[kb]), acc);
+        for (uint32_t j = 0; j < 4u; ++j) acc[j] += __shfl_xor(acc[j], 32, 64);
+        const float s0 = f16_to_f32(sc.x & 0xffffu) * 0.0625f, s1 = f16_to_f32(sc.x >> 16) * 0.0625f;
+        const float s2 = f16_to_f32(sc.y & 0xffffu) * 0.0625f, s3 = f16_to_f32(sc.y >> 16) * 0.0625f;
+        // chain over the four quads: lane c + 8kq continues lane c + 8(kq-1)
+        float y = 0.0f;
+#pragma unroll
+        for (uint32_t step = 0; step < 4u; ++step) {
+            float yin = __shfl_up(y, 8, 64);
+            if (kq == 0u) yin = 0.0f;
+            float t = __builtin_fmaf(static_cast<float>(acc[0]), s0, yin);
+            t = __builtin_fmaf(static_cast<float>(acc[1]), s1, t);
+            t = __builtin_fmaf(static_cast<float>(acc[2]), s2, t);
+            y = __builtin_fmaf(static_cast<float>(acc[3]), s3, t);
         }
-        o = (static_cast<float>(acc[0]) * ws) * sm;
+        o = __shfl(y, static_cast<int>(24u + c), 64) * sm;
+    } else {
+        const uint32_t kb = lane >> 3;
+        const uint4* mrow = mq_lds[route] + 4u * kb;
+        int acc = 0;
+#pragma unroll
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint4 xv = mrow[q];
+            acc = __builtin_amdgcn_sdot4(static_cast<int>(bq[q].x), static_cast<int>(xv.x), acc, false);
+            acc = __builtin_amdgcn_sdot4(static_cast<int>(bq[q].y), static_cast<int>(xv.y), acc, false);
+            acc = __builtin_amdgcn_sdot4(static_cast<int>(bq[q].z), static_cast<int>(xv.z), acc, false);
+            acc = __builtin_amdgcn_sdot4(static_cast<int>(bq[q].w), static_cast<int>(xv.w), acc, false);
+        }
+        acc += __shfl_xor(acc, 8, 64);
+        acc += __shfl_xor(acc, 16, 64);
+        acc += __shfl_xor(acc, 32, 64);
+        o = (static_cast<float>(acc) * ws) * sm;
     }
-    if (q == 0u) o_lds[route][n] = valid ? o : 0.0f;
+    if (lane < 8u) o_lds[route][lane] = valid ? o : 0.0f;
     __syncthreads();
-    if (route == 0u && lane < 16u) {
+    if (threadIdx.x < 8u) {
+        const uint32_t channel = 16u * tile + n0 + threadIdx.x;
         float total = 0.0f;
-        for (uint32_t r = 0; r < top_k; ++r) total += o_lds[r][lane];
-        out[tile * 16u + lane] = static_cast<uint16_t>(f32_to_bf16(total));
+        for (uint32_t r = 0; r < top_k; ++r) total += o_lds[r][threadIdx.x];
+        if (shared_output != nullptr && shared_gate != nullptr) {
+            const float g = bf16_to_f32(shared_gate[0]);
+            const float multiplier = 1.0f / (1.0f + exp_q(-g));
+            total = total + bf16_to_f32(shared_output[channel]) * multiplier;
+        }
+        uint32_t result = f32_to_bf16(total);
+        if (residual != nullptr)
+            result = f32_to_bf16(bf16_to_f32(residual[channel]) + bf16_to_f32(result));
+        out[channel] = static_cast<uint16_t>(result);
     }
 }
 
 }  // namespace
 
-size_t decode_scratch_bytes() { return static_cast<size_t>(kTopK) * kInter * sizeof(uint16_t); }
+size_t decode_scratch_bytes() {
+    return 256u + static_cast<size_t>(kTopK) * kInter * sizeof(uint16_t);
+}
 
 hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
-                         const q38m_expert_weights_v1& down,
-                         const uint16_t* hidden, const int32_t* ids,
-                         const float* weights, uint32_t top_k, void* scratch,
+                         const q38m_expert_weights_v1& down, const uint16_t* hidden,
+                         const float* logits, const int32_t* ids, const float* weights,
+                         uint32_t top_k, const uint16_t* shared_output,
+                         const uint16_t* shared_gate, const uint16_t* residual, void* scratch,
                          uint16_t* output, hipStream_t stream) {
-    uint16_t* mid = static_cast<uint16_t*>(scratch);
-    decode_gate_up_kernel<kHidden, kInter><<<dim3(kInter / 16u, top_k), 256, 0, stream>>>(
+    int32_t* scratch_ids = static_cast<int32_t*>(scratch);
+    uint16_t* mid = reinterpret_cast<uint16_t*>(static_cast<char*>(scratch) + 256);
+    decode_gate_up_kernel<kHidden, kInter><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
         static_cast<const uint4*>(gate_up.data), static_cast<const uint2*>(gate_up.scales),
-        hidden, ids, weights, mid);
+        hidden, logits, ids, weights, top_k, logits != nullptr ? scratch_ids : nullptr, mid);
+    const int32_t* down_ids = logits != nullptr ? scratch_ids : ids;
     if (down.format == Q38M_FORMAT_W8_SYM)
-        decode_down_kernel<kHidden, kInter, false><<<kHidden / 16u, 64u * top_k, 0, stream>>>(
-            static_cast<const uint4*>(down.data), down.scales, mid, ids, top_k, output);
+        decode_down_kernel<kHidden, kInter, false><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
+            static_cast<const uint4*>(down.data), down.scales, mid, down_ids, top_k,
+            shared_output, shared_gate, residual, output);
     else
-        decode_down_kernel<kHidden, kInter, true><<<kHidden / 16u, 64u * top_k, 0, stream>>>(
-            static_cast<const uint4*>(down.data), down.scales, mid, ids, top_k, output);
+        decode_down_kernel<kHidden, kInter, true><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
+            static_cast<const uint4*>(down.data), down.scales, mid, down_ids, top_k,
+            shared_output, shared_gate, residual, output);
     return hipGetLastError();
 }
 

@@ -65,10 +65,12 @@ hipError_t launch_combine_shared(const uint16_t* routed, const uint16_t* shared,
 
 // decode (q38m_decode.hip)
 size_t decode_scratch_bytes();
+// logits != null: top-k inside the gate/up launch; else ids/weights given
 hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
-                         const q38m_expert_weights_v1& down,
-                         const uint16_t* hidden, const int32_t* ids,
-                         const float* weights, uint32_t top_k, void* scratch,
+                         const q38m_expert_weights_v1& down, const uint16_t* hidden,
+                         const float* logits, const int32_t* ids, const float* weights,
+                         uint32_t top_k, const uint16_t* shared_output,
+                         const uint16_t* shared_gate, const uint16_t* residual, void* scratch,
                          uint16_t* output, hipStream_t stream);
 
 // layout and synthetic data (q38m_layout.hip)

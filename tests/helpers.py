@@ -106,6 +106,34 @@ def decode(q38m, layer, hidden, ids, weights, scratch, output=None, top_k=10):
     return output
 
 
+def decode_fused(q38m, layer, hidden, logits, scratch, output=None, top_k=10, shared=None,
+                 residual=None):
+    """Runs q38m_moe_decode_v1 (top-k from logits, routed experts, optional
+    gated shared term and residual) on device tensors."""
+    t = torch()
+    if output is None:
+        output = t.empty(1, W.HIDDEN, dtype=t.int16, device="cuda")
+    so, sg = (None, None) if shared is None else shared
+    q38m.call("q38m_moe_decode_v1", ctypes.byref(layer.gu.desc), ctypes.byref(layer.dn.desc),
+              hidden.data_ptr(), logits.data_ptr(), top_k,
+              None if so is None else so.data_ptr(), None if sg is None else sg.data_ptr(),
+              None if residual is None else residual.data_ptr(), scratch.data_ptr(),
+              output.data_ptr(), stream(), 0)
+    return output
+
+
+def decode_scratch(q38m):
+    t = torch()
+    return t.zeros(q38m.lib().q38m_moe_decode_scratch_bytes() // 2 + 64, dtype=t.int16,
+                   device="cuda")
+
+
+def scratch_ids(scratch, top_k=10):
+    """The ids q38m_moe_decode_v1 leaves at the start of its scratch."""
+    torch().cuda.synchronize()
+    return host(scratch[:2 * top_k], np.int32).copy()
+
+
 def ws_arrays(ws, tokens):
     """Workspace regions (views into the workspace's own device buffer)
     as numpy arrays."""

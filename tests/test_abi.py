@@ -181,6 +181,23 @@ def test_decode_and_step_validation(q38m):
     with pytest.raises(q38m.InvalidArgument):  # no scratch
         q38m.call("q38m_moe_routed_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000,
                   0x2000, 0x3000, 10, None, 0x5000, None, 0)
+    # fused decode: gu, dn, hidden, logits, top_k, shared, gate, residual, scratch, out
+    with pytest.raises(q38m.InvalidArgument):  # no logits
+        q38m.call("q38m_moe_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, None, 10,
+                  None, None, None, 0x4000, 0x5000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # top_k 0
+        q38m.call("q38m_moe_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2000, 0,
+                  None, None, None, 0x4000, 0x5000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # shared output without its gate
+        q38m.call("q38m_moe_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2000, 10,
+                  0x6000, None, None, 0x4000, 0x5000, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # misaligned logits
+        q38m.call("q38m_moe_decode_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2004, 10,
+                  None, None, None, 0x4000, 0x5000, None, 0)
+    with pytest.raises(q38m.Unsupported):  # row-major gate/up
+        rm = fake_weights(q38m, layout=0)
+        q38m.call("q38m_moe_decode_v1", ctypes.byref(rm), ctypes.byref(dn), 0x1000, 0x2000, 10,
+                  None, None, None, 0x4000, 0x5000, None, 0)
     ws = q38m.PrefillWorkspace()
     q38m.call("q38m_moe_prefill_workspace_bind", 0x1000000,
               q38m.lib().q38m_moe_prefill_workspace_bytes(64), 64, ctypes.byref(ws))

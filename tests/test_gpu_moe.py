@@ -10,7 +10,9 @@ Cases: config 1 (64 tokens, all-W4) and config 2 (512-token slab, mixed)
 at full size with every intermediate; the committed config-1 golden slice;
 the reference's one-hot KAT (cuda_kernel_tests.cu:613-868) restated;
 double runs over poisoned workspaces; the gated shared-expert combine;
-decode == prefill(tokens=1) == oracle; a reduced config-3 decode stack, a
+decode == prefill(tokens=1) == oracle; the fused logits-in decode (ids,
+ties, signed zeros, fewer routes, shared term, residual); a reduced
+config-3 decode stack (routed and fused), a
 config-4 Zipf 4096-token chunk as 8 slabs (oracle on a token sample) and a
 reduced config-5 alternating-policy stack with residual adds.
 """
@@ -21,8 +23,8 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN_DIR
-from helpers import (Layer, W, decode, device, host, prefill, stream, synth_hidden,
-                     synth_logits, torch, ws_arrays)
+from helpers import (Layer, W, decode, decode_fused, decode_scratch, device, host, prefill,
+                     scratch_ids, stream, synth_hidden, synth_logits, torch, ws_arrays)
 
 pytestmark = pytest.mark.gpu
 
@@ -193,6 +195,99 @@ def test_decode_equals_prefill_and_oracle(q38m, orc, layers, config):
         assert np.array_equal(host(dec, np.uint16), ref["output"])
 
 
+@pytest.mark.parametrize("config", [1, 2])
+def test_fused_decode_from_logits(q38m, orc, layers, config):
+    """q38m_moe_decode_v1: top-k inside the gate/up launch, then down; the
+    ids and the output match the oracle bit for bit."""
+    layer = layers(config)
+    scratch = decode_scratch(q38m)
+    for step in range(6):
+        hidden = synth_hidden(q38m, 177 + step, 1, 1)
+        logits = synth_logits(q38m, 177 + step, 2, 1)
+        out = decode_fused(q38m, layer, hidden, logits, scratch)
+        ref = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn,
+                      logits=host(logits, np.float32), grouped=False)
+        assert np.array_equal(scratch_ids(scratch), ref["ids"].ravel())
+        assert np.array_equal(host(out, np.uint16), ref["output"])
+
+
+def test_fused_decode_topk_ties(q38m, orc, layers):
+    """Ties go to the lower expert id and -0 ties +0: the restated reference
+    tie fixture, a block of equal maxima, and a top-10 made of signed zeros."""
+    layer = layers(2)
+    scratch = decode_scratch(q38m)
+    hidden = synth_hidden(q38m, 5, 1, 1)
+    with open(os.path.join(GOLDEN_DIR, "reference_topk_ties.json")) as f:
+        fixture = json.load(f)
+    cases = [(np.array(row, np.float32), np.array(ids, np.int32))
+             for row, ids in zip(fixture["logits"], fixture["ids"])]
+    rng = np.random.default_rng(11)
+    equal_max = rng.standard_normal(512).astype(np.float32)
+    equal_max[rng.choice(512, 30, replace=False)] = 9.5
+    cases.append((equal_max, None))
+    zeros = (-1.0 - np.abs(rng.standard_normal(512))).astype(np.float32)
+    picks = rng.choice(512, 16, replace=False)
+    zeros[picks] = np.where(np.arange(16) % 2 == 0, np.float32(0.0), np.float32(-0.0))
+    cases.append((zeros, None))
+    for row, expected in cases:
+        logits = device(row.reshape(1, 512))
+        out = decode_fused(q38m, layer, hidden, logits, scratch)
+        ref = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn,
+                      logits=row.reshape(1, 512), grouped=False)
+        got_ids = scratch_ids(scratch)
+        assert np.array_equal(got_ids, ref["ids"].ravel())
+        if expected is not None:
+            assert np.array_equal(got_ids, expected)
+        assert np.array_equal(host(out, np.uint16), ref["output"])
+
+
+def test_fused_decode_shared_and_residual(q38m, orc, layers):
+    layer = layers(2)
+    scratch = decode_scratch(q38m)
+    hidden = synth_hidden(q38m, 31, 1, 1)
+    logits = synth_logits(q38m, 31, 2, 1)
+    so = synth_hidden(q38m, 31, 3, 1)
+    sg = synth_hidden(q38m, 31, 4, 1)[0, :8].contiguous()
+    res = synth_hidden(q38m, 31, 5, 1)
+    ref = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn,
+                  logits=host(logits, np.float32), shared_output=host(so, np.uint16),
+                  shared_gate=host(sg, np.uint16)[:1], grouped=False)
+    out = decode_fused(q38m, layer, hidden, logits, scratch, shared=(so, sg))
+    assert np.array_equal(host(out, np.uint16), ref["output"])
+    out = decode_fused(q38m, layer, hidden, logits, scratch, shared=(so, sg), residual=res)
+    expect = orc.f32_to_bf16(orc.bf16_to_f32(host(res, np.uint16)) +
+                             orc.bf16_to_f32(ref["output"]))
+    assert np.array_equal(host(out, np.uint16), expect)
+    plain = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn,
+                    logits=host(logits, np.float32), grouped=False)
+    out = decode_fused(q38m, layer, hidden, logits, scratch, residual=res)
+    expect = orc.f32_to_bf16(orc.bf16_to_f32(host(res, np.uint16)) +
+                             orc.bf16_to_f32(plain["output"]))
+    assert np.array_equal(host(out, np.uint16), expect)
+
+
+@pytest.mark.parametrize("top_k", [1, 4, 9])
+def test_fused_decode_fewer_routes(q38m, orc, layers, top_k):
+    """top_k < 10: the oracle runs the same routes padded to ten with zero
+    router weights (a zero-weight route contributes exactly +0)."""
+    layer = layers(1)
+    scratch = decode_scratch(q38m)
+    hidden = synth_hidden(q38m, 41, 1, 1)
+    logits = synth_logits(q38m, 41, 2, 1)
+    ids, wts = orc.topk(host(logits, np.float32), top_k=top_k)
+    pad_ids = np.zeros((1, 10), np.int32)
+    pad_w = np.zeros((1, 10), np.float32)
+    pad_ids[0, :top_k], pad_w[0, :top_k] = ids[0], wts[0]
+    ref = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn, ids=pad_ids,
+                  weights=pad_w, grouped=False)
+    out = decode_fused(q38m, layer, hidden, logits, scratch, top_k=top_k)
+    assert np.array_equal(scratch_ids(scratch, top_k), ids.ravel())
+    assert np.array_equal(host(out, np.uint16), ref["output"])
+    routed = decode(q38m, layer, hidden, device(ids.ravel()), device(wts.ravel()), scratch,
+                    top_k=top_k)
+    assert np.array_equal(host(routed, np.uint16), ref["output"])
+
+
 def test_config3_decode_stack_reduced(q38m, orc, layers):
     """Config 3 with 4 of its 48 layers: fresh router draw per layer,
     residual add between layers, decode path."""
@@ -201,6 +296,7 @@ def test_config3_decode_stack_reduced(q38m, orc, layers):
     scratch = t.empty(q38m.lib().q38m_moe_decode_scratch_bytes() // 2 + 64, dtype=t.int16,
                       device="cuda")
     state = synth_hidden(q38m, seed, 1, 1)
+    fused_state = state.clone()
     host_state = host(state, np.uint16).copy()
     ws = q38m.PrefillWorkspace_(1)
     for layer_index in range(4):
@@ -216,9 +312,13 @@ def test_config3_decode_stack_reduced(q38m, orc, layers):
         q38m.call("q38m_residual_add_bf16", state.data_ptr(), out.data_ptr(),
                   new_state.data_ptr(), W.HIDDEN, stream(), 0)
         state = new_state
+        # the fused path: top-k, experts and residual in two launches
+        fused_state = decode_fused(q38m, layer, fused_state, logits, scratch,
+                                   output=t.empty_like(fused_state), residual=fused_state)
         host_state = orc.f32_to_bf16(orc.bf16_to_f32(host_state) +
                                      orc.bf16_to_f32(ref["output"].ravel()))
         assert np.array_equal(host(state, np.uint16).ravel(), host_state.ravel())
+        assert np.array_equal(host(fused_state, np.uint16).ravel(), host_state.ravel())
 
 
 def test_config4_zipf_chunk_as_slabs(q38m, orc, layers):
