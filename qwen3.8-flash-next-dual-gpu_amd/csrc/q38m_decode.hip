@@ -13,9 +13,9 @@
 // so the layer is two launches and every byte of each launch is requested
 // as early as its address is known.
 //
-//   gate/up  256 workgroups x 10 waves (one wave per route).  Wave 9 ranks
-//            the 512 router logits (or reads the given ids) while waves 0-3
-//            load the token; then every lane issues its 72 bytes of weights
+//   gate/up  256 workgroups x 10 waves (one wave per route).  Waves 0-7
+//            rank the 512 router logits (or wave 9 reads the given ids) while
+//            waves 0-3 also load the token; then every lane issues its 72 bytes of weights
 //            at once (46 KB per workgroup, the layer's 11.8 MB in flight
 //            together).  Workgroup b owns channels 16p+n0, 16p+n0+1 of all
 //            routes; the eight workgroups sharing a pair tile's 128-byte
@@ -42,23 +42,17 @@ __device__ __forceinline__ uint32_t order_key(float v) {
     return v == v ? k : 0u;
 }
 
-template <int kCtrl>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), kCtrl, 0xf, 0xf, true));
+// Inverse of order_key for non-NaN keys (-0 comes back as +0).
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
-
-// Wave-wide max: quad swaps, half-row and row mirrors (DPP), then the four
-// row results through scalar registers.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-    x = umax(x, dpp_u32<0xB1>(x));   // quad_perm [1,0,3,2]
-    x = umax(x, dpp_u32<0x4E>(x));   // quad_perm [2,3,0,1]
-    x = umax(x, dpp_u32<0x141>(x));  // row_half_mirror
-    x = umax(x, dpp_u32<0x140>(x));  // row_mirror
-    const uint32_t r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16);
-    const uint32_t r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
-    return umax(umax(r0, r1), umax(r2, r3));
+// Sum over each aligned group of eight lanes, valid in the group's last lane.
+__device__ __forceinline__ uint32_t group8_sum(uint32_t x) {
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xf, 0xf, true));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x112, 0xf, 0xf, true));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x114, 0xf, 0xf, true));
+    return x;
 }
 
 __device__ __forceinline__ float wave_max_f32(float x) {
@@ -67,54 +61,22 @@ __device__ __forceinline__ float wave_max_f32(float x) {
     return x;
 }
 
-// Top-k of 512 logits by (value desc, id asc), one wave: lane l holds
-// experts 8l..8l+7, so between lanes the lower lane has the lower ids and a
-// tie on the wave maximum goes to the lowest such lane; inside a lane the
-// strict > scan keeps the lowest id.  The weights are exp(l_r - l_0) over
-// the rank-order sum of the numerators (q38_kernels.cu:431-479).  Returns
-// this lane's rank (lane < top_k) id and weight.
-__device__ __forceinline__ void wave_topk512(const float* __restrict__ logits, uint32_t top_k,
-                                             uint32_t lane, int32_t& id_out, float& w_out) {
-    const float4* row = reinterpret_cast<const float4*>(logits) + 2u * lane;
-    const float4 a = row[0], b = row[1];
-    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint32_t key[8];
+// Rank of `mine` among `count` unique keys in LDS: the number of larger keys
+// (four independent counts so the compares pipeline).
+template <uint32_t kCount>
+__device__ __forceinline__ uint32_t rank_among(const uint64_t* keys, uint64_t mine) {
+    static_assert(kCount % 4u == 0u, "keys in groups of four");
+    uint32_t r[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) key[j] = order_key(v[j]);
-    uint32_t taken = 0;
-    float mine_v = 0.0f, top_v = 0.0f;
-    int32_t mine_id = -1;
-    for (uint32_t rank = 0; rank < top_k; ++rank) {
-        // best_j = 512 when a lane has nothing left: an id >= 512 (invalid)
-        // if every remaining logit is NaN
-        uint32_t best = 0, best_j = 512;
-        float best_v = 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < 8u; ++j) {
-            if (((taken >> j) & 1u) == 0u && key[j] > best) {
-                best = key[j];
-                best_j = j;
-                best_v = v[j];
-            }
-        }
-        const uint32_t m = wave_max_u32(best);
-        const uint64_t tied = __ballot(best == m);
-        const uint32_t win = static_cast<uint32_t>(__builtin_ctzll(tied));
-        const uint32_t win_j = __builtin_amdgcn_readlane(best_j, win);
-        const float win_v = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(best_v), win));
-        if (lane == win && best_j < 8u) taken |= 1u << best_j;
-        if (lane == rank) {
-            mine_v = win_v;
-            mine_id = static_cast<int32_t>(8u * win + win_j);
-        }
-        if (rank == 0) top_v = win_v;
+    for (uint32_t j = 0; j < kCount; j += 4u) {
+        const ulonglong2 a = *reinterpret_cast<const ulonglong2*>(keys + j);
+        const ulonglong2 b = *reinterpret_cast<const ulonglong2*>(keys + j + 2u);
+        r[0] += a.x > mine ? 1u : 0u;
+        r[1] += a.y > mine ? 1u : 0u;
+        r[2] += b.x > mine ? 1u : 0u;
+        r[3] += b.y > mine ? 1u : 0u;
     }
-    const float numerator = lane < top_k ? exp_q(mine_v - top_v) : 0.0f;
-    float denominator = 0.0f;
-    for (uint32_t rank = 0; rank < top_k; ++rank)
-        denominator += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(numerator), rank));
-    id_out = mine_id;
-    w_out = numerator / denominator;
+    return (r[0] + r[1]) + (r[2] + r[3]);
 }
 
 template <uint32_t H, uint32_t I>
@@ -130,32 +92,33 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     static_assert(H == 256u * 8u && kQuads == 16u, "16 quads, one 8-element token chunk per thread");
     static_assert(kPairs * 8u == kDecodeBlocks, "eight workgroups per pair tile");
     __shared__ int32_t ids_lds[kTopK];
-    __shared__ float wr_lds[kTopK];
+    __shared__ float num_lds[kTopK];
     __shared__ float amax_lds[4];
     __shared__ uint4 x_lds[kQuads * kQuadPad];
+    __shared__ uint64_t key_lds[kExperts];
+    __shared__ uint64_t cand_lds[8u * kTopK];
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t slot8 = blockIdx.x >> 3;
     const uint32_t pair = 4u * (blockIdx.x & 7u) + (slot8 >> 3);
     const uint32_t n0 = 2u * (slot8 & 7u);
+    const bool fused = logits != nullptr;
 
     uint4 hv = make_uint4(0u, 0u, 0u, 0u);
     if (wave < 4u) hv = reinterpret_cast<const uint4*>(hidden)[threadIdx.x];
-    if (wave == kTopK - 1u) {
-        int32_t id = -1;
-        float wr = 0.0f;
-        if (logits != nullptr) {
-            wave_topk512(logits, top_k, lane, id, wr);
-        } else if (lane < top_k) {
-            id = ids_in[lane];
-            wr = weights_in[lane];
-        }
-        if (lane < kTopK) {
-            ids_lds[lane] = id;
-            wr_lds[lane] = wr;
-        }
-        if (blockIdx.x == 0 && lane < top_k && ids_out != nullptr) ids_out[lane] = id;
+    // Top-k of the 512 logits by (value desc, id asc) -- the order of the
+    // reference's sort (q38_kernels.cu:431-458) -- as ranks of unique keys
+    // (order key << 32 | 511 - id):
+    //   1. waves 0-7 rank their 64 keys among themselves; ranks 0-9 of each
+    //      wave (80 candidates, eight sorted lists) hold the top 10;
+    //   2. eight threads per candidate count the larger keys in one list
+    //      each; the thread holding rank r writes id_r and exp(l_r - l_0).
+    float logit = 0.0f;
+    if (fused && wave < 8u) logit = logits[threadIdx.x];
+    if (!fused && wave == kTopK - 1u && lane < top_k) {
+        ids_lds[lane] = ids_in[lane];
+        num_lds[lane] = weights_in[lane];
     }
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
     if (wave < 4u) {
@@ -167,6 +130,45 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
         }
         amax = wave_max_f32(amax);
         if (lane == 0) amax_lds[wave] = amax;
+    }
+    uint64_t key = 0;
+    if (fused && wave < 8u) {
+        key = (static_cast<uint64_t>(order_key(logit)) << 32) | (kExperts - 1u - threadIdx.x);
+        key_lds[threadIdx.x] = key;
+    }
+    __syncthreads();
+    if (fused) {
+        if (wave < 8u) {
+            const uint32_t rank = rank_among<64>(key_lds + 64u * wave, key);
+            if (rank < kTopK) cand_lds[kTopK * wave + rank] = key;
+        }
+        __syncthreads();
+        {
+            const uint32_t c = threadIdx.x >> 3, list = threadIdx.x & 7u;
+            const uint64_t mine = cand_lds[c];
+            const uint64_t* other = cand_lds + kTopK * list;
+            uint32_t larger = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < kTopK; j += 2u) {
+                const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(other + j);
+                larger += pr.x > mine ? 1u : 0u;
+                larger += pr.y > mine ? 1u : 0u;
+            }
+            uint64_t top = cand_lds[0];
+#pragma unroll
+            for (uint32_t w8 = 1; w8 < 8u; ++w8) {
+                const uint64_t head = cand_lds[kTopK * w8];
+                top = head > top ? head : top;
+            }
+            const uint32_t rank = group8_sum(larger);
+            if (list == 7u && rank < kTopK) {
+                const uint32_t id = kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu);
+                ids_lds[rank] = static_cast<int32_t>(id);
+                num_lds[rank] = exp_q(key_value(static_cast<uint32_t>(mine >> 32)) -
+                                      key_value(static_cast<uint32_t>(top >> 32)));
+                if (blockIdx.x == 0 && rank < top_k) ids_out[rank] = static_cast<int32_t>(id);
+            }
+        }
     }
     __syncthreads();
 
@@ -242,7 +244,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 47));
     const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 63));
     if (lane == 0 && route < top_k) {
-        const float wr = wr_lds[route];
+        float wr = num_lds[route];
+        if (fused) {
+            // exp(l_r - l_0) over the rank-order sum (q38_kernels.cu:460-479)
+            float denominator = 0.0f;
+            for (uint32_t r = 0; r < top_k; ++r) denominator += num_lds[r];
+            wr = wr / denominator;
+        }
         const uint32_t m0 = valid ? swiglu_fold(g0 * xs, u0 * xs, wr) : 0u;
         const uint32_t m1 = valid ? swiglu_fold(g1 * xs, u1 * xs, wr) : 0u;
         *reinterpret_cast<uint32_t*>(mid + static_cast<size_t>(route) * I + 16u * pair + n0) =
