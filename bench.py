@@ -82,25 +82,24 @@ def main():
     routes = T * W.TOPK
     max_tasks = q38m.max_tasks(T)
 
-    stage_names = ["topk", "plan", "quant_x", "gate_up", "quant_mid", "down", "combine"]
+    # the kernels of q38m_moe_prefill_v1, launched one entry point at a time
+    stage_names = ["route_quant", "plan", "gate_up", "quant_mid", "down", "combine"]
 
     def launch_stage(i):
         if i == 0:
-            q38m.call("q38m_topk_router_f32", logits.data_ptr(), ws.expert_ids,
-                      ws.expert_weights, T, W.EXPERTS, W.TOPK, 1, sh, 0)
+            q38m.call("q38m_moe_route_quantize_v1", logits.data_ptr(), hidden.data_ptr(), T,
+                      ws.expert_ids, ws.expert_weights, ws.xq, ws.xs, sh, 0)
         elif i == 1:
             q38m.call("q38m_moe_build_route_plan_v1", ws.expert_ids, T, ctypes.byref(ws.plan), 0,
                       sh, 0)
         elif i == 2:
-            q38m.call("q38m_quantize_rows_i8", hidden.data_ptr(), T, W.HIDDEN, ws.xq, ws.xs, sh, 0)
-        elif i == 3:
             q38m.call("q38m_moe_grouped_gate_up_v1", ctypes.byref(gu.desc), ws.xq, ws.xs,
                       ws.plan.packed_assignment, ws.expert_weights, ws.plan.tasks, max_tasks,
                       ws.weighted_mid, sh, 0)
-        elif i == 4:
+        elif i == 3:
             q38m.call("q38m_quantize_rows_i8", ws.weighted_mid, routes, W.INTER, ws.mid_q,
                       ws.mid_s, sh, 0)
-        elif i == 5:
+        elif i == 4:
             q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(dn.desc), ws.mid_q, ws.mid_s,
                       ws.plan.tasks, max_tasks, ws.route_output, sh, 0)
         else:
@@ -151,8 +150,8 @@ def main():
     down_bytes = (active * dn_bytes_expert + routes * W.INTER + routes * 4 +
                   routes * W.HIDDEN * 4)
     kernels = {
-        "gate_up": (stage_ms[3], gate_up_bytes, "gate_up_w4g32_kernel"),
-        "down": (stage_ms[5], down_bytes, "down_w8pc_kernel"),
+        "gate_up": (stage_ms[stage_names.index("gate_up")], gate_up_bytes, "gate_up_w4g32_kernel"),
+        "down": (stage_ms[stage_names.index("down")], down_bytes, "down_w8pc_kernel"),
     }
     dominant = max(kernels, key=lambda k: kernels[k][0])
     d_ms, d_bytes, d_symbol = kernels[dominant]

@@ -150,6 +150,18 @@ int q38m_topk_router_f32(const float* logits, int32_t* expert_ids,
                          uint32_t experts, uint32_t top_k, int normalize_top_k,
                          void* stream, int device);
 
+/* Top-10 routing and int8 activation quantisation in one launch (one
+ * workgroup per token): cuda_topk_router_bf16 (include/q38/cuda_kernels.h:
+ * 83-91; 512 experts, normalised) fused with the per-token quantisation
+ * that feeds cuda_moe_grouped_gate_up_v1 (xq[T][2048] int8 + xs[T] fp32;
+ * the reference gathers bf16 rows, cuda_moe_pack_hidden_v1).  Writes
+ * expert_ids/expert_weights [T][10] as q38m_topk_router_f32 does.
+ * logits and hidden 16-byte aligned, xq 8-byte aligned. */
+int q38m_moe_route_quantize_v1(const float* logits, const uint16_t* hidden,
+                               uint32_t tokens, int32_t* expert_ids,
+                               float* expert_weights, int8_t* xq, float* xs,
+                               void* stream, int device);
+
 /* cuda_moe_build_route_plan_v1, include/q38/cuda_moe_prefill.h:101-104.
  * flags: Q38M_PLAN_FLAG_HASHES computes route_hash/plan_hash exactly as the
  * reference (a serial pass); without it both hashes are 0. */

@@ -136,9 +136,26 @@ int q38m_topk_router_f32(const float* logits, int32_t* expert_ids, float* expert
         experts % 64u != 0u || experts > 1024u || top_k == 0 || top_k > experts || top_k > 32u)
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid top-k router buffers");
     if (int rc = select_device(device)) return rc;
+    if (experts == Q38M_ROUTE_EXPERTS && top_k <= Q38M_ROUTE_TOPK && normalize_top_k)
+        return finish(q38m::launch_route_quantize(logits, nullptr, tokens, top_k, expert_ids,
+                                                  expert_weights, nullptr, nullptr,
+                                                  as_stream(stream)),
+                      "route_quantize_kernel");
     return finish(q38m::launch_topk(logits, expert_ids, expert_weights, tokens, experts, top_k,
                                     normalize_top_k, as_stream(stream)),
                   "topk_kernel");
+}
+
+int q38m_moe_route_quantize_v1(const float* logits, const uint16_t* hidden, uint32_t tokens,
+                               int32_t* expert_ids, float* expert_weights, int8_t* xq, float* xs,
+                               void* stream, int device) {
+    if (!logits || !hidden || !expert_ids || !expert_weights || !xq || !xs || tokens == 0 ||
+        !aligned(logits, 16) || !aligned(hidden, 16) || !aligned(xq, 8))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid route/quantise buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_route_quantize(logits, hidden, tokens, Q38M_ROUTE_TOPK, expert_ids,
+                                              expert_weights, xq, xs, as_stream(stream)),
+                  "route_quantize_kernel");
 }
 
 int q38m_moe_build_route_plan_v1(const int32_t* expert_ids, uint32_t tokens,
@@ -318,12 +335,13 @@ int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert
     const uint32_t tasks = q38m::max_tasks_v1(tokens);
     hipError_t status = hipSuccess;
     if (logits)
-        status = q38m::launch_topk(logits, ws->expert_ids, ws->expert_weights, tokens,
-                                   Q38M_ROUTE_EXPERTS, Q38M_ROUTE_TOPK, 1, s);
+        status = q38m::launch_route_quantize(logits, hidden, tokens, Q38M_ROUTE_TOPK,
+                                             ws->expert_ids, ws->expert_weights, ws->xq, ws->xs,
+                                             s);
+    else
+        status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws->xq, ws->xs, s);
     if (status == hipSuccess)
         status = q38m::launch_build_plan(ws->expert_ids, tokens, ws->plan, false, s);
-    if (status == hipSuccess)
-        status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws->xq, ws->xs, s);
     if (status == hipSuccess)
         status = q38m::launch_gate_up_w4g32(gate_up->data, gate_up->scales, ws->xq, ws->xs,
                                             ws->plan.packed_assignment, ws->expert_weights,

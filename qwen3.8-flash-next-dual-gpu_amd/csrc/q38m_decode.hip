@@ -27,57 +27,13 @@
 //            gated shared term and residual are applied.
 #include "q38m_device.h"
 #include "q38m_internal.h"
+#include "q38m_select.h"
 
 namespace q38m {
 namespace {
 
 constexpr uint32_t kDecodeBlocks = 256;
-constexpr uint32_t kDecodeThreads = 64u * kTopK;
-
-// Monotonic unsigned key of a float: larger key = larger value; -0 and +0
-// share a key (equal under <), NaN maps below every number.
-__device__ __forceinline__ uint32_t order_key(float v) {
-    const uint32_t b = __float_as_uint(v + 0.0f);
-    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-    return v == v ? k : 0u;
-}
-
-// Inverse of order_key for non-NaN keys (-0 comes back as +0).
-__device__ __forceinline__ float key_value(uint32_t k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
-// Sum over each aligned group of eight lanes, valid in the group's last lane.
-__device__ __forceinline__ uint32_t group8_sum(uint32_t x) {
-    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xf, 0xf, true));
-    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x112, 0xf, 0xf, true));
-    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x114, 0xf, 0xf, true));
-    return x;
-}
-
-__device__ __forceinline__ float wave_max_f32(float x) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) x = fmaxf(x, __shfl_xor(x, offset, 64));
-    return x;
-}
-
-// Rank of `mine` among `count` unique keys in LDS: the number of larger keys
-// (four independent counts so the compares pipeline).
-template <uint32_t kCount>
-__device__ __forceinline__ uint32_t rank_among(const uint64_t* keys, uint64_t mine) {
-    static_assert(kCount % 4u == 0u, "keys in groups of four");
-    uint32_t r[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (uint32_t j = 0; j < kCount; j += 4u) {
-        const ulonglong2 a = *reinterpret_cast<const ulonglong2*>(keys + j);
-        const ulonglong2 b = *reinterpret_cast<const ulonglong2*>(keys + j + 2u);
-        r[0] += a.x > mine ? 1u : 0u;
-        r[1] += a.y > mine ? 1u : 0u;
-        r[2] += b.x > mine ? 1u : 0u;
-        r[3] += b.y > mine ? 1u : 0u;
-    }
-    return (r[0] + r[1]) + (r[2] + r[3]);
-}
+constexpr uint32_t kDecodeThreads = kSelectThreads;
 
 template <uint32_t H, uint32_t I>
 __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
@@ -95,8 +51,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     __shared__ float num_lds[kTopK];
     __shared__ float amax_lds[4];
     __shared__ uint4 x_lds[kQuads * kQuadPad];
-    __shared__ uint64_t key_lds[kExperts];
-    __shared__ uint64_t cand_lds[8u * kTopK];
+    __shared__ SelectLds select_lds;
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -107,13 +62,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
 
     uint4 hv = make_uint4(0u, 0u, 0u, 0u);
     if (wave < 4u) hv = reinterpret_cast<const uint4*>(hidden)[threadIdx.x];
-    // Top-k of the 512 logits by (value desc, id asc) -- the order of the
-    // reference's sort (q38_kernels.cu:431-458) -- as ranks of unique keys
-    // (order key << 32 | 511 - id):
-    //   1. waves 0-7 rank their 64 keys among themselves; ranks 0-9 of each
-    //      wave (80 candidates, eight sorted lists) hold the top 10;
-    //   2. eight threads per candidate count the larger keys in one list
-    //      each; the thread holding rank r writes id_r and exp(l_r - l_0).
     float logit = 0.0f;
     if (fused && wave < 8u) logit = logits[threadIdx.x];
     if (!fused && wave == kTopK - 1u && lane < top_k) {
@@ -121,56 +69,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
         num_lds[lane] = weights_in[lane];
     }
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-    if (wave < 4u) {
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] & 0xffffu)));
-            amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] >> 16)));
-        }
-        amax = wave_max_f32(amax);
-        if (lane == 0) amax_lds[wave] = amax;
-    }
-    uint64_t key = 0;
-    if (fused && wave < 8u) {
-        key = (static_cast<uint64_t>(order_key(logit)) << 32) | (kExperts - 1u - threadIdx.x);
-        key_lds[threadIdx.x] = key;
-    }
-    __syncthreads();
+    if (wave < 4u) row_absmax_partial(hw, amax_lds);
     if (fused) {
-        if (wave < 8u) {
-            const uint32_t rank = rank_among<64>(key_lds + 64u * wave, key);
-            if (rank < kTopK) cand_lds[kTopK * wave + rank] = key;
-        }
+        block_topk512(logit, select_lds, ids_lds, num_lds);
+        if (blockIdx.x == 0 && threadIdx.x < top_k) ids_out[threadIdx.x] = ids_lds[threadIdx.x];
+    } else {
         __syncthreads();
-        {
-            const uint32_t c = threadIdx.x >> 3, list = threadIdx.x & 7u;
-            const uint64_t mine = cand_lds[c];
-            const uint64_t* other = cand_lds + kTopK * list;
-            uint32_t larger = 0;
-#pragma unroll
-            for (uint32_t j = 0; j < kTopK; j += 2u) {
-                const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(other + j);
-                larger += pr.x > mine ? 1u : 0u;
-                larger += pr.y > mine ? 1u : 0u;
-            }
-            uint64_t top = cand_lds[0];
-#pragma unroll
-            for (uint32_t w8 = 1; w8 < 8u; ++w8) {
-                const uint64_t head = cand_lds[kTopK * w8];
-                top = head > top ? head : top;
-            }
-            const uint32_t rank = group8_sum(larger);
-            if (list == 7u && rank < kTopK) {
-                const uint32_t id = kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu);
-                ids_lds[rank] = static_cast<int32_t>(id);
-                num_lds[rank] = exp_q(key_value(static_cast<uint32_t>(mine >> 32)) -
-                                      key_value(static_cast<uint32_t>(top >> 32)));
-                if (blockIdx.x == 0 && rank < top_k) ids_out[rank] = static_cast<int32_t>(id);
-            }
-        }
     }
-    __syncthreads();
 
     // every lane's weights: lane = kq + 16*(c + 2u), u = gate/up, c = channel
     const uint32_t route = wave;
@@ -186,21 +91,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     const uint2 sc = s[tile * 16u + n0 + c];
 
     // int8 token (same arithmetic as the row quantiser)
-    const float amax = fmaxf(fmaxf(amax_lds[0], amax_lds[1]), fmaxf(amax_lds[2], amax_lds[3]));
-    float xs = amax / 127.0f;
-    if (xs == 0.0f) xs = 1.0f;
+    const float xs = row_scale(amax_lds);
     if (wave < 4u) {
-        uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t h = (i & 1) ? (hw[i >> 1] >> 16) : (hw[i >> 1] & 0xffffu);
-            float r = __builtin_rintf(bf16_to_f32(h) / xs);
-            r = fminf(fmaxf(r, -127.0f), 127.0f);
-            packed[i >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (i & 3));
-        }
         const uint32_t k = 8u * threadIdx.x;
         reinterpret_cast<uint2*>(x_lds)[(k >> 7) * (2u * kQuadPad) + ((k & 127u) >> 3)] =
-            make_uint2(packed[0], packed[1]);
+            quantize8(hw, xs);
     }
     __syncthreads();
 

@@ -29,6 +29,10 @@ inline uint32_t max_tasks_v1(uint32_t tokens) {
 hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
                        uint32_t tokens, uint32_t experts, uint32_t top_k,
                        int normalize, hipStream_t stream);
+// 512 experts, top_k <= 10, normalised; hidden may be null (top-k only)
+hipError_t launch_route_quantize(const float* logits, const uint16_t* hidden, uint32_t tokens,
+                                uint32_t top_k, int32_t* ids, float* weights, int8_t* xq,
+                                float* xs, hipStream_t stream);
 hipError_t launch_build_plan(const int32_t* ids, uint32_t tokens,
                              const q38m_route_plan_v1& plan, bool hashes,
                              hipStream_t stream);

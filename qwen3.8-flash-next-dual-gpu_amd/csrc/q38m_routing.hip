@@ -2,6 +2,7 @@
 // route plan (V1 byte layout of include/q38/cuda_moe_prefill.h:11-93).
 #include "q38m_device.h"
 #include "q38m_internal.h"
+#include "q38m_select.h"
 
 namespace q38m {
 namespace {
@@ -86,6 +87,49 @@ __global__ __launch_bounds__(256) void topk_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Routing + activation quantisation, one ten-wave workgroup per token: the
+// top-k of the token's 512 logits (block_topk512) with the rank-order
+// normalisation, and -- when hidden is given -- the int8 quantisation of
+// the token's 2048-wide row by waves 0-3 (the same arithmetic as
+// quantize_rows_kernel).  Replaces a top-k launch and a quantisation launch.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kSelectThreads) void route_quantize_kernel(
+    const float* __restrict__ logits, const uint16_t* __restrict__ hidden, uint32_t top_k,
+    int32_t* __restrict__ ids, float* __restrict__ weights, int8_t* __restrict__ xq,
+    float* __restrict__ xs) {
+    __shared__ SelectLds select_lds;
+    __shared__ int32_t ids_lds[kTopK];
+    __shared__ float num_lds[kTopK];
+    __shared__ float amax_lds[4];
+    const uint32_t token = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const bool quantize = hidden != nullptr;
+    float logit = 0.0f;
+    if (wave < 8u) logit = logits[static_cast<size_t>(token) * kExperts + t];
+    uint4 hv = make_uint4(0u, 0u, 0u, 0u);
+    if (quantize && wave < 4u)
+        hv = reinterpret_cast<const uint4*>(hidden + static_cast<size_t>(token) * kHidden)[t];
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    if (quantize && wave < 4u) row_absmax_partial(hw, amax_lds);
+    block_topk512(logit, select_lds, ids_lds, num_lds);
+    if (quantize && wave < 4u) {
+        const float s = row_scale(amax_lds);
+        reinterpret_cast<uint2*>(xq + static_cast<size_t>(token) * kHidden)[t] = quantize8(hw, s);
+        if (t == 0) xs[token] = s;
+    }
+    if (wave == kTopK - 1u) {
+        const uint32_t lane = t & 63u;
+        float denominator = 0.0f;
+        for (uint32_t r = 0; r < top_k; ++r) denominator += num_lds[r];
+        if (lane < top_k) {
+            ids[static_cast<size_t>(token) * top_k + lane] = ids_lds[lane];
+            weights[static_cast<size_t>(token) * top_k + lane] = num_lds[lane] / denominator;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Route plan: one workgroup of 16 waves.  The reference runs one lane per
 // expert over every route (O(routes * experts) LDS compares, then a serial
 // prefix on lane 0; q38_moe_prefill.cu:198-233).  Here:
@@ -123,14 +167,26 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     const uint32_t routes = tokens * kTopK;
 
     if (tid == 0) invalid = 0u;
-    for (uint32_t i = tid; i < kPlanWaves * kExperts; i += kPlanThreads)
-        (&hist[0][0])[i] = 0;
+    static_assert(kPlanWaves * kExperts * 2u == kPlanThreads * 16u, "one 16-byte clear per thread");
+    reinterpret_cast<uint4*>(&hist[0][0])[tid] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
-    for (uint32_t a = tid; a < routes; a += kPlanThreads) {
-        const int32_t id = expert_ids[a];
-        const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
-        key[a] = valid ? static_cast<uint16_t>(id) : static_cast<uint16_t>(0xffffu);
-        if (!valid) invalid = 1u;
+    // every id load is issued before the first is used (one round trip)
+    constexpr uint32_t kPerThread = (kMaxRoutes + kPlanThreads - 1u) / kPlanThreads;
+    int32_t loaded[kPerThread];
+#pragma unroll
+    for (uint32_t i = 0; i < kPerThread; ++i) {
+        const uint32_t a = tid + i * kPlanThreads;
+        loaded[i] = a < routes ? expert_ids[a] : 0;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kPerThread; ++i) {
+        const uint32_t a = tid + i * kPlanThreads;
+        if (a < routes) {
+            const int32_t id = loaded[i];
+            const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
+            key[a] = valid ? static_cast<uint16_t>(id) : static_cast<uint16_t>(0xffffu);
+            if (!valid) invalid = 1u;
+        }
     }
     __syncthreads();
 
@@ -160,11 +216,14 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
 
     // 2. per-expert base of every wave
     if (tid < kExperts) {
+        uint32_t c[kPlanWaves];
+#pragma unroll
+        for (uint32_t w = 0; w < kPlanWaves; ++w) c[w] = hist[w][tid];
         uint32_t running = 0;
+#pragma unroll
         for (uint32_t w = 0; w < kPlanWaves; ++w) {
-            const uint32_t c = hist[w][tid];
             hist[w][tid] = static_cast<uint16_t>(running);
-            running += c;
+            running += c[w];
         }
         counts[tid] = running;
         plan.expert_counts[tid] = static_cast<uint16_t>(running);
@@ -321,6 +380,14 @@ hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
     else
         topk_kernel<16><<<grid, 256, 0, stream>>>(logits, tokens, experts, top_k,
                                                   normalize, ids, weights);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_quantize(const float* logits, const uint16_t* hidden, uint32_t tokens,
+                                uint32_t top_k, int32_t* ids, float* weights, int8_t* xq,
+                                float* xs, hipStream_t stream) {
+    route_quantize_kernel<<<tokens, kSelectThreads, 0, stream>>>(logits, hidden, top_k, ids,
+                                                                 weights, xq, xs);
     return hipGetLastError();
 }
 

@@ -1,0 +1,155 @@
+// Block-wide top-k of one 512-logit router row, shared by the prefill
+// routing kernel and the fused decode.
+//
+// Order: value descending, expert id ascending on ties (the order of the
+// reference's sort, cuda/q38_kernels.cu:431-458), expressed as unique
+// 64-bit keys (order key << 32 | 511 - id) so that "larger key" is "ranked
+// first".  Two levels of rank counting:
+//   1. each of waves 0-7 ranks its 64 keys among themselves; ranks 0-9 of
+//      every wave (80 candidates in eight sorted lists) contain the top 10,
+//      because every key above a top-10 key is itself in its wave's top 10;
+//   2. eight threads per candidate count the larger keys in one list each
+//      and a DPP sum adds the eight counts: the global rank.
+// The thread holding rank r writes id_r and exp(l_r - l_0); values come
+// back from the keys (exactly, -0 as +0, which leaves every difference
+// l_r - l_0 unchanged).  The caller forms the rank-order denominator
+// (cuda/q38_kernels.cu:460-479).
+#pragma once
+
+#include "q38m_device.h"
+#include "q38m_internal.h"
+
+namespace q38m {
+
+constexpr uint32_t kSelectThreads = 64u * kTopK;  // ten waves
+
+struct SelectLds {
+    uint64_t key[kExperts];
+    uint64_t cand[8u * kTopK];
+};
+
+// Monotonic unsigned key of a float: larger key = larger value; -0 and +0
+// share a key (equal under <), NaN maps below every number.
+__device__ __forceinline__ uint32_t order_key(float v) {
+    const uint32_t b = __float_as_uint(v + 0.0f);
+    const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return v == v ? k : 0u;
+}
+
+// Inverse of order_key for non-NaN keys (-0 comes back as +0).
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Sum over each aligned group of eight lanes, valid in the group's last lane.
+__device__ __forceinline__ uint32_t group8_sum(uint32_t x) {
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xf, 0xf, true));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x112, 0xf, 0xf, true));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x114, 0xf, 0xf, true));
+    return x;
+}
+
+__device__ __forceinline__ float wave_max_f32(float x) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) x = fmaxf(x, __shfl_xor(x, offset, 64));
+    return x;
+}
+
+// Rank of `mine` among `count` unique keys in LDS: the number of larger keys
+// (four independent counts so the compares pipeline).
+template <uint32_t kCount>
+__device__ __forceinline__ uint32_t rank_among(const uint64_t* keys, uint64_t mine) {
+    static_assert(kCount % 4u == 0u, "keys in groups of four");
+    uint32_t r[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (uint32_t j = 0; j < kCount; j += 4u) {
+        const ulonglong2 a = *reinterpret_cast<const ulonglong2*>(keys + j);
+        const ulonglong2 b = *reinterpret_cast<const ulonglong2*>(keys + j + 2u);
+        r[0] += a.x > mine ? 1u : 0u;
+        r[1] += a.y > mine ? 1u : 0u;
+        r[2] += b.x > mine ? 1u : 0u;
+        r[3] += b.y > mine ? 1u : 0u;
+    }
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
+// Called by all kSelectThreads threads of the block; `logit` is the row
+// entry of threads 0..511.  LDS writes the caller made before the call are
+// visible to the whole block on return.  On return ids[r] and num[r]
+// (r < 10) hold the rank-r expert and exp(l_r - l_0).
+__device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32_t* ids,
+                                              float* num) {
+    const uint32_t t = threadIdx.x;
+    uint64_t key = 0;
+    if (t < kExperts) {
+        key = (static_cast<uint64_t>(order_key(logit)) << 32) | (kExperts - 1u - t);
+        lds.key[t] = key;
+    }
+    __syncthreads();
+    if (t < kExperts) {
+        const uint32_t rank = rank_among<64>(lds.key + (t & ~63u), key);
+        if (rank < kTopK) lds.cand[kTopK * (t >> 6) + rank] = key;
+    }
+    __syncthreads();
+    {
+        const uint32_t c = t >> 3, list = t & 7u;
+        const uint64_t mine = lds.cand[c];
+        const uint64_t* other = lds.cand + kTopK * list;
+        uint32_t larger = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kTopK; j += 2u) {
+            const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(other + j);
+            larger += pr.x > mine ? 1u : 0u;
+            larger += pr.y > mine ? 1u : 0u;
+        }
+        uint64_t top = lds.cand[0];
+#pragma unroll
+        for (uint32_t w8 = 1; w8 < 8u; ++w8) {
+            const uint64_t head = lds.cand[kTopK * w8];
+            top = head > top ? head : top;
+        }
+        const uint32_t rank = group8_sum(larger);
+        if (list == 7u && rank < kTopK) {
+            ids[rank] = static_cast<int32_t>(kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu));
+            num[rank] = exp_q(key_value(static_cast<uint32_t>(mine >> 32)) -
+                              key_value(static_cast<uint32_t>(top >> 32)));
+        }
+    }
+    __syncthreads();
+}
+
+// int8 quantisation of one 2048-wide bf16 row held by threads 0..255 (eight
+// elements each): s = absmax/127 (1 if zero), q = clamp(rint(x/s), +-127)
+// (tools/q38_artifact_compiler.py:214-222).  Step 1 (before a barrier):
+// the per-wave absmax of waves 0..3 into amax_lds.
+__device__ __forceinline__ void row_absmax_partial(const uint32_t (&hw)[4], float* amax_lds) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] & 0xffffu)));
+        amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] >> 16)));
+    }
+    amax = wave_max_f32(amax);
+    if ((threadIdx.x & 63u) == 0u) amax_lds[threadIdx.x >> 6] = amax;
+}
+
+// Step 2 (after the barrier): the row scale and this thread's eight int8s.
+__device__ __forceinline__ float row_scale(const float* amax_lds) {
+    const float amax = fmaxf(fmaxf(amax_lds[0], amax_lds[1]), fmaxf(amax_lds[2], amax_lds[3]));
+    const float s = amax / 127.0f;
+    return s == 0.0f ? 1.0f : s;
+}
+
+__device__ __forceinline__ uint2 quantize8(const uint32_t (&hw)[4], float s) {
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t h = (i & 1) ? (hw[i >> 1] >> 16) : (hw[i >> 1] & 0xffffu);
+        float r = __builtin_rintf(bf16_to_f32(h) / s);
+        r = fminf(fmaxf(r, -127.0f), 127.0f);
+        packed[i >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (i & 3));
+    }
+    return make_uint2(packed[0], packed[1]);
+}
+
+}  // namespace q38m

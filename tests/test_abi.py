@@ -172,6 +172,17 @@ def test_routing_and_quant_validation(q38m):
         q38m.call("q38m_moe_pack_hidden_v1", 0x1000, 0x2000, 15, 2048, 0x3000, None, 0)
 
 
+def test_route_quantize_validation(q38m):
+    # logits, hidden, tokens, ids, weights, xq, xs
+    good = [0x1000, 0x2000, 8, 0x3000, 0x4000, 0x5000, 0x6000]
+    for i, bad in [(0, None), (1, None), (2, 0), (3, None), (4, None), (5, None), (6, None),
+                   (0, 0x1004), (1, 0x2008), (5, 0x5004)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_route_quantize_v1", *args, None, 0)
+
+
 def test_decode_and_step_validation(q38m):
     gu = fake_weights(q38m)
     dn = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)

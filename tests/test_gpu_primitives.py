@@ -111,8 +111,37 @@ def run_topk(q38m, logits, top_k=10, normalize=True):
     return host(ids, np.int32).reshape(tokens, top_k), host(w, np.float32).reshape(tokens, top_k)
 
 
-@pytest.mark.parametrize("case", ["synthetic", "zipf", "ties", "reference_ties", "unnormalised"])
+@pytest.mark.parametrize("case", ["synthetic", "zipf", "ties", "reference_ties", "unnormalised",
+                                  "signed_zeros", "top4", "experts256"])
 def test_topk_bitwise(q38m, orc, case):
+    """512 experts with top_k <= 10 (normalised) run the ranked-key
+    kernel; other shapes the wave-per-token kernel."""
+    top_k, normalize = 10, case != "unnormalised"
+    if case == "signed_zeros":
+        rng = np.random.default_rng(12)
+        logits = (-1.0 - np.abs(rng.standard_normal((64, 512)))).astype(np.float32)
+        for row in logits:
+            picks = rng.choice(512, 14, replace=False)
+            row[picks] = np.where(rng.random(14) < 0.5, np.float32(0.0), np.float32(-0.0))
+        ids, w = run_topk(q38m, logits)
+        wids, ww = orc.topk(logits)
+        assert np.array_equal(ids, wids)
+        assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
+        return
+    if case == "top4":
+        logits = orc.synth_logits(7, 2, 200)
+        ids, w = run_topk(q38m, logits, top_k=4)
+        wids, ww = orc.topk(logits, top_k=4)
+        assert np.array_equal(ids, wids)
+        assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
+        return
+    if case == "experts256":
+        logits = orc.synth_logits(8, 2, 100)[:, :256].copy()
+        ids, w = run_topk(q38m, logits, top_k=8)
+        wids, ww = orc.topk(logits, top_k=8)
+        assert np.array_equal(ids, wids)
+        assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
+        return
     if case == "synthetic":
         logits = orc.synth_logits(5, 2, 512)
     elif case == "zipf":
@@ -129,6 +158,33 @@ def test_topk_bitwise(q38m, orc, case):
     wids, ww = orc.topk(logits, normalize=normalize)
     assert np.array_equal(ids, wids)
     assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
+
+
+@pytest.mark.parametrize("tokens", [1, 64, 512])
+def test_route_quantize_bitwise(q38m, orc, tokens):
+    """q38m_moe_route_quantize_v1: top-10 ids and weights and the int8
+    rows equal the oracle's top-k and row quantiser bit for bit."""
+    t = torch()
+    logits = orc.synth_logits(21, 2, tokens)
+    logits[0, 17] = logits[0].max()  # a tie at the top
+    rng = np.random.default_rng(tokens)
+    x = (rng.standard_normal((tokens, 2048)) * rng.uniform(1e-3, 50, (tokens, 1))).astype(np.float32)
+    if tokens > 3:
+        x[3] = 0.0
+    h = orc.f32_to_bf16(x)
+    ld, hd = device(logits), device(h)
+    ids = t.empty(tokens * 10, dtype=t.int32, device="cuda")
+    w = t.empty(tokens * 10, dtype=t.float32, device="cuda")
+    xq = t.empty(tokens * 2048, dtype=t.int8, device="cuda")
+    xs = t.empty(tokens, dtype=t.float32, device="cuda")
+    q38m.call("q38m_moe_route_quantize_v1", ld.data_ptr(), hd.data_ptr(), tokens, ids.data_ptr(),
+              w.data_ptr(), xq.data_ptr(), xs.data_ptr(), stream(), 0)
+    wids, ww = orc.topk(logits)
+    wq, ws = orc.quantize_rows(h, 2048)
+    assert np.array_equal(host(ids, np.int32).reshape(tokens, 10), wids)
+    assert np.array_equal(host(w, np.float32).reshape(tokens, 10).view(np.uint32), ww.view(np.uint32))
+    assert np.array_equal(host(xq, np.int8).reshape(tokens, 2048), wq)
+    assert np.array_equal(host(xs, np.float32).view(np.uint32), ws.view(np.uint32))
 
 
 def run_plan(q38m, ids, tokens, hashes, poison=None):
