@@ -154,6 +154,7 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     __shared__ uint16_t key[kMaxRoutes];
     __shared__ uint16_t local_rank[kMaxRoutes];
     __shared__ uint16_t hist[kPlanWaves][kExperts];
+    __shared__ unsigned long long peers[kPlanWaves][kExperts + 1u];  // slot 512: invalid ids
     __shared__ uint32_t counts[kExperts];
     __shared__ uint32_t offsets[kExperts + 1];
     __shared__ uint32_t task_offsets[kExperts + 1];
@@ -169,6 +170,8 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     if (tid == 0) invalid = 0u;
     static_assert(kPlanWaves * kExperts * 2u == kPlanThreads * 16u, "one 16-byte clear per thread");
     reinterpret_cast<uint4*>(&hist[0][0])[tid] = make_uint4(0u, 0u, 0u, 0u);
+    for (uint32_t i = tid; i < kPlanWaves * (kExperts + 1u); i += kPlanThreads)
+        (&peers[0][0])[i] = 0ull;
     __syncthreads();
     // every id load is issued before the first is used (one round trip)
     constexpr uint32_t kPerThread = (kMaxRoutes + kPlanThreads - 1u) / kPlanThreads;
@@ -195,22 +198,35 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     const uint32_t begin = wave * segment;
     const uint32_t end = min(begin + segment, routes);
     const uint64_t below_mask = (1ull << lane) - 1ull;
-    for (uint32_t base = begin; base < end; base += 64u) {
-        const uint32_t a = base + lane;
-        const uint32_t k = a < end ? key[a] : 0xffffu;
-        const bool valid = k != 0xffffu;
-        uint64_t equal = __ballot(valid);
+    // Lanes of a 64-route chunk with equal ids: each lane ORs its bit into
+    // its id's slot of the wave's table, reads the slot back and clears it
+    // (one wave's LDS operations execute in order).  Then the stable rank
+    // inside the wave's segment is the wave's running count for the id plus
+    // the equal lanes below.
+    constexpr uint32_t kChunks = (kMaxRoutes + kPlanThreads - 1u) / kPlanThreads;
+    unsigned long long* table = peers[wave];
 #pragma unroll
-        for (uint32_t bit = 0; bit < 9u; ++bit) {
-            const bool set = (k >> bit) & 1u;
-            const uint64_t vote = __ballot(set);
-            equal &= set ? vote : ~vote;
-        }
+    for (uint32_t i = 0; i < kChunks; ++i) {
+        const uint32_t a = begin + 64u * i + lane;
+        const bool in = 64u * i < segment && a < end;
+        const uint32_t raw = key[a < kMaxRoutes ? a : kMaxRoutes - 1u];
+        const uint32_t k = in ? raw : 0xffffu;
+        const bool valid = k != 0xffffu;
+        const uint32_t slot = valid ? k : kExperts;
+        atomicOr(&table[slot], 1ull << lane);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const unsigned long long equal = table[slot];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        table[slot] = 0ull;
         const uint32_t below = __popcll(equal & below_mask);
         const uint32_t running = valid ? hist[wave][k] : 0u;
         if (valid) local_rank[a] = static_cast<uint16_t>(running + below);
         if (valid && below == 0u)
             hist[wave][k] = static_cast<uint16_t>(running + __popcll(equal));
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
     }
     __syncthreads();
 
@@ -256,9 +272,11 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     __syncthreads();
     if (tid < kExperts) {
         uint32_t prefix_count = 0, prefix_tasks = 0;
-        for (uint32_t w = 0; w < wave; ++w) {
-            prefix_count += wave_totals[0][w];
-            prefix_tasks += wave_totals[1][w];
+#pragma unroll
+        for (uint32_t w = 0; w < 8u; ++w) {
+            const uint32_t c = wave_totals[0][w], t = wave_totals[1][w];
+            prefix_count += w < wave ? c : 0u;
+            prefix_tasks += w < wave ? t : 0u;
         }
         offsets[tid] = prefix_count + inc_count - count;
         task_offsets[tid] = prefix_tasks + inc_tasks - tasks;
@@ -299,7 +317,10 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     }
 
     // 4. scatter; identity for invalid assignments and unfilled positions
-    for (uint32_t a = tid; a < routes; a += kPlanThreads) {
+#pragma unroll
+    for (uint32_t i = 0; i < kPerThread; ++i) {
+        const uint32_t a = tid + i * kPlanThreads;
+        if (a >= routes) continue;
         const uint32_t k = key[a];
         if (k == 0xffffu) {
             plan.assignment_to_packed[a] = a;
