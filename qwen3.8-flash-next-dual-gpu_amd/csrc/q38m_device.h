@@ -15,6 +15,23 @@ namespace q38m {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// ---- streaming loads -----------------------------------------------------
+
+// Expert weights are read once per launch: non-temporal loads keep that
+// stream from evicting the activations every workgroup re-reads from L2.
+typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint4 load_stream(const uint4* p) {
+    const v4u_t v = __builtin_nontemporal_load(reinterpret_cast<const v4u_t*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 load_stream(const uint2* p) {
+    const v2u_t v = __builtin_nontemporal_load(reinterpret_cast<const v2u_t*>(p));
+    return make_uint2(v.x, v.y);
+}
+
 // ---- conversions ---------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) {

@@ -105,8 +105,8 @@ void gate_up_w4g32_kernel(
     // the first two quads' weights are in flight while A is staged
     auto load = [&](uint32_t kq) {
         const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
-        return QuadWeights{wg[k * kQuadWords], wu[k * kQuadWords], sg[k * kQuadScales],
-                           su[k * kQuadScales]};
+        return QuadWeights{load_stream(wg + k * kQuadWords), load_stream(wu + k * kQuadWords),
+                           load_stream(sg + k * kQuadScales), load_stream(su + k * kQuadScales)};
     };
     QuadWeights r0 = load(0), r1 = load(1), r2;
 
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
     // first half-tile in flight while A is staged
     uint4 b[kHalf];
 #pragma unroll
-    for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = wt[kb * 64u];
+    for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
 
     // Stage A: 16-byte chunk c of mid row r is K block c/4, lane group c%4.
     for (uint32_t i = threadIdx.x; i < 16u * (I / 16u); i += kThreads) {
@@ -217,22 +217,24 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
     }
     __syncthreads();
 
-#pragma unroll 1
+#pragma unroll
     for (uint32_t t = 0; t < kTilesPerWave; ++t) {
         const uint32_t tile = tile0 + t;
         const uint4* wtile = wt + static_cast<size_t>(t) * kBlocks * 64u;
         uint4 nb[kHalf];
 #pragma unroll
-        for (uint32_t kb = 0; kb < kHalf; ++kb) nb[kb] = wtile[(kHalf + kb) * 64u];
+        for (uint32_t kb = 0; kb < kHalf; ++kb) nb[kb] = load_stream(wtile + (kHalf + kb) * 64u);
         __builtin_amdgcn_sched_barrier(0);
         v4i acc = {0, 0, 0, 0};
 #pragma unroll
         for (uint32_t kb = 0; kb < kHalf; ++kb)
             acc = mfma_i8_16x16x64(as_v4i(a_lds[kb * 64u + lane]), as_v4i(b[kb]), acc);
-        // next tile's first half (the last tile re-reads its own: an L1 hit)
-        const uint4* wnext = t + 1u < kTilesPerWave ? wtile + kBlocks * 64u : wtile;
+        // next tile's first half (unrolled: the last tile issues none)
+        if (t + 1u < kTilesPerWave) {
 #pragma unroll
-        for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = wnext[kb * 64u];
+            for (uint32_t kb = 0; kb < kHalf; ++kb)
+                b[kb] = load_stream(wtile + (kBlocks + kb) * 64u);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (uint32_t kb = 0; kb < kHalf; ++kb)
@@ -290,8 +292,8 @@ __global__ __launch_bounds__(256) void down_w4g32_kernel(
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t kq = 0; kq < kQuads; ++kq) {
-            const uint4 b = wt[kq * kTiles * 64u];
-            const uint2 c = st[kq * kTiles * 16u];
+            const uint4 b = load_stream(wt + kq * kTiles * 64u);
+            const uint2 c = load_stream(st + kq * kTiles * 16u);
             const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
             const uint32_t cw[2] = {c.x, c.y};
 #pragma unroll
