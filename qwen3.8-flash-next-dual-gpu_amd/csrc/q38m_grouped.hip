@@ -97,29 +97,44 @@ void gate_up_w4g32_kernel(
     // contiguous span of 2*kWaves KiB of weights and 256*kWaves B of scales.
     constexpr uint32_t kQuadWords = kTiles * 64u;   // uint4 per quad of one expert
     constexpr uint32_t kQuadScales = kTiles * 16u;  // uint2 per quad of one expert
-    const uint4* wg = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u + lane;
-    const uint4* wu = wg + 64u;
-    const uint2* sg = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u + n;
-    const uint2* su = sg + 16u;
-
-    // the first two quads' weights are in flight while A is staged
+    // uniform bases (scalar registers) plus 32-bit per-lane offsets
+    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u;
+    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u;
     auto load = [&](uint32_t kq) {
         const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
-        return QuadWeights{load_stream(wg + k * kQuadWords), load_stream(wu + k * kQuadWords),
-                           load_stream(sg + k * kQuadScales), load_stream(su + k * kQuadScales)};
+        const uint32_t wi = k * kQuadWords + lane;
+        const uint32_t si = k * kQuadScales + n;
+        return QuadWeights{load_stream(wbase + wi), load_stream(wbase + wi + 64u),
+                           load_stream(sbase + si), load_stream(sbase + si + 16u)};
     };
-    QuadWeights r0 = load(0), r1 = load(1), r2;
 
     // Stage A: 16-byte chunk c of token row r holds group c/2 for lane groups
-    // q = 2(c%2) and 2(c%2)+1.  Rows past valid_rows replicate row 0.
-    for (uint32_t i = threadIdx.x; i < 16u * (H / 16u); i += kThreads) {
-        const uint32_t r = i / (H / 16u);
+    // q = 2(c%2) and 2(c%2)+1.  Rows past valid_rows replicate row 0.  The
+    // row indices are loaded first, then the first two quads of weights and
+    // all row chunks, so A costs two round trips and the weights stay in
+    // flight meanwhile.
+    constexpr uint32_t kChunks = 16u * (H / 16u) / kThreads;
+    static_assert(16u * (H / 16u) % kThreads == 0u, "whole chunks per thread");
+    uint32_t token[kChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t r = (threadIdx.x + c * kThreads) / (H / 16u);
+        token[c] = packed[p0 + (r < rows ? r : 0u)];
+    }
+    QuadWeights r0 = load(0), r1 = load(1), r2;
+    uint4 v[kChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t chunk = (threadIdx.x + c * kThreads) % (H / 16u);
+        v[c] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token[c] / kTopK) * H)[chunk];
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t i = threadIdx.x + c * kThreads;
         const uint32_t chunk = i % (H / 16u);
-        const uint32_t token = packed[p0 + (r < rows ? r : 0u)] / kTopK;
-        const uint4 v = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token) * H)[chunk];
-        const uint32_t base = (chunk >> 1) * 64u + (chunk & 1u) * 32u + r;
-        a_lds[base] = make_uint2(v.x, v.y);
-        a_lds[base + 16u] = make_uint2(v.z, v.w);
+        const uint32_t base = (chunk >> 1) * 64u + (chunk & 1u) * 32u + i / (H / 16u);
+        a_lds[base] = make_uint2(v[c].x, v[c].y);
+        a_lds[base + 16u] = make_uint2(v[c].z, v[c].w);
     }
     __syncthreads();
 
