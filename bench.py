@@ -43,8 +43,8 @@ def load(name, path, package_dir=None):
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=100)
-    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--decode-tokens", type=int, default=16)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-decode", action="store_true")
