@@ -48,6 +48,7 @@ def main():
     parser.add_argument("--decode-tokens", type=int, default=16)
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-decode", action="store_true")
+    parser.add_argument("--no-quantizer", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
@@ -229,6 +230,9 @@ def main():
     if not args.no_decode:
         result["decode"] = bench_decode(q38m, W, torch, args.decode_tokens)
 
+    if not args.no_quantizer:
+        result["weight_pipeline"] = bench_weight_pipeline(q38m, W, torch)
+
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
                                               T)
@@ -317,6 +321,57 @@ def bench_decode(q38m, W, torch, tokens):
             "algorithmic_bytes_per_token": bytes_token, "launches_per_layer": 2,
             "entry_point": "q38m_moe_decode_v1", **graph_rate, "mode": "hip_graph",
             "eager": rate(ms_eager)}
+
+
+def bench_weight_pipeline(q38m, W, torch, reps=5):
+    """The load-time weight path of one layer: bf16
+    expert weights quantised on the device (quantize_groupwise: W4 g32
+    gate/up, W8 per-channel down, fp16 scales) and repacked into the MFMA
+    layouts.  HBM-bound; bytes = read + written."""
+    sh = torch.cuda.current_stream().cuda_stream
+    shapes = {"gate_up": (q38m.FORMAT_W4_SYM, 32, 2 * W.INTER, W.HIDDEN),
+              "down": (q38m.FORMAT_W8_SYM, 0, W.HIDDEN, W.INTER)}
+    out = {}
+    for name, (fmt, group, rows, cols) in shapes.items():
+        elems = W.EXPERTS * rows * cols
+        src = torch.empty(elems, dtype=torch.int16, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, 9, 30 + len(name), elems, src, sigma=0.05)
+        nbytes, sbytes = q38m.weights_bytes(fmt, group, W.EXPERTS, rows, cols)
+        data = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+        scales = torch.empty(sbytes // 2, dtype=torch.int16, device="cuda")
+        rm = q38m.DeviceWeights(data, scales, fmt, group, q38m.LAYOUT_ROW_MAJOR, W.EXPERTS, rows,
+                                cols)
+
+        def quantize():
+            q38m.call("q38m_quantize_expert_weights", src.data_ptr(), ctypes.byref(rm.desc), sh, 0)
+
+        quantize()
+        packed = q38m.repack(rm, paired=(name == "gate_up"))
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            quantize()
+        stop.record()
+        torch.cuda.synchronize()
+        q_ms = start.elapsed_time(stop) / reps
+        start.record()
+        for _ in range(reps):
+            q38m.call("q38m_repack_expert_weights", ctypes.byref(rm.desc),
+                      ctypes.byref(packed.desc), sh, 0)
+        stop.record()
+        torch.cuda.synchronize()
+        r_ms = start.elapsed_time(stop) / reps
+        q_bytes = elems * 2 + nbytes + sbytes
+        r_bytes = 2 * (nbytes + sbytes)
+        out[name] = {"format": "W4 g32" if fmt == q38m.FORMAT_W4_SYM else "W8 per-channel",
+                     "quantize_ms": round(q_ms, 4),
+                     "quantize_GBps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
+                     "quantize_hbm_frac": round(q_bytes / (q_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "repack_ms": round(r_ms, 4),
+                     "repack_GBps": round(r_bytes / (r_ms * 1e-3) / 1e9, 1)}
+        del src, data, scales, rm, packed
+    return out
 
 
 def cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, gpu_out, T):

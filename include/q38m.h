@@ -298,6 +298,18 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
                                const q38m_expert_weights_v1* dst,
                                void* stream, int device);
 
+/* Weight quantiser of the artifact pipeline: quantize_groupwise
+ * (tools/q38_artifact_compiler.py:193-253) on the device.  src: bf16
+ * weights [experts*rows][columns]; dst: row-major layout, fp16 scales,
+ * W4 (groups 32/64/128) or W8 (groups 32/64/128, or group 0 = per output
+ * channel with columns % 512 == 0).  Per group s = max|w|/qmax (qmax 7 for
+ * W4, 127 for W8), s == 0 -> 1, q = clamp(rint(w/s), +-qmax); W4 packs
+ * column 2i in the low nibble.  The reference stores bf16 scales; here they
+ * are fp16 (BASELINE's format).  Follow with q38m_repack_expert_weights. */
+int q38m_quantize_expert_weights(const uint16_t* src_bf16,
+                                 const q38m_expert_weights_v1* dst,
+                                 void* stream, int device);
+
 /* ---- deterministic synthetic data (counter-based SplitMix64) --------- */
 #define Q38M_SYNTH_NORMAL_F32 1u     /* sigma*N(0,1) (+ bias[i % bias_len]) */
 #define Q38M_SYNTH_NORMAL_BF16 2u    /* bf16(sigma*N(0,1)) */

@@ -68,6 +68,7 @@ _SIGS = {
     "q38o_plan_bytes": (_SZ, [_U32]),
     "q38o_build_plan": (_INT, [_P, _U32, _INT, _P]),
     "q38o_quantize_rows": (None, [_P, _U32, _U32, _P, _P]),
+    "q38o_quantize_weights": (ctypes.c_int, [_P, ctypes.c_uint64, _U32, ctypes.c_int, _U32, _P, _P]),
     "q38o_row_value": (_F, [ctypes.POINTER(Weights), _U32, _U32, _P]),
     "q38o_row_accumulators": (None, [ctypes.POINTER(Weights), _U32, _U32, _P, _P]),
     "q38o_gate_up": (None, [ctypes.POINTER(Weights), _U32, _U32, _P, _P, _P, _P, _P]),
@@ -284,6 +285,20 @@ def quantize_rows(x_bf16, width):
     s = np.empty(rows, dtype=np.float32)
     lib().q38o_quantize_rows(_p(x), rows, width, _p(q), _p(s))
     return q, s
+
+
+def quantize_weights(w_bf16, bits, group):
+    """Weight quantiser (quantize_groupwise restated): bf16 words [rows][cols]
+    -> (data bytes [rows][cols*bits/8], fp16 scale words [rows][cols/group])."""
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    rows, cols = w.reshape(-1, w.shape[-1]).shape
+    g = group or cols
+    data = np.zeros((rows, cols * bits // 8), dtype=np.uint8)
+    scales = np.empty((rows, cols // g), dtype=np.uint16)
+    rc = lib().q38o_quantize_weights(_p(w), rows, cols, bits, group, _p(data), _p(scales))
+    if rc:
+        raise ValueError(f"invalid quantiser shape rows={rows} cols={cols} bits={bits} group={group}")
+    return data, scales
 
 
 def row_accumulators(w, expert, row, x_i8):

@@ -487,6 +487,51 @@ void q38o_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
 }
 
 /* ------------------------------------------------------------------ */
+/* Weight quantiser: tools/q38_artifact_compiler.py:193-253            */
+/* ------------------------------------------------------------------ */
+
+int q38o_quantize_weights(const uint16_t* src_bf16, uint64_t rows, uint32_t cols,
+                          int bits, uint32_t group, uint8_t* data, uint16_t* scales_f16) {
+    const uint32_t g = group ? group : cols;
+    if (!src_bf16 || !data || !scales_f16 || rows == 0 || cols == 0 || (bits != 4 && bits != 8) ||
+        cols % g != 0 || (bits == 4 && (g % 2 != 0 || cols % 2 != 0)))
+        return 1;
+    const float qmax = bits == 4 ? 7.0f : 127.0f;
+    const uint32_t groups = cols / g;
+#pragma omp parallel for schedule(static)
+    for (int64_t r = 0; r < (int64_t)rows; ++r) {
+        const uint16_t* row = src_bf16 + (size_t)r * cols;
+        for (uint32_t gi = 0; gi < groups; ++gi) {
+            const uint16_t* w = row + (size_t)gi * g;
+            float amax = 0.0f;
+            for (uint32_t k = 0; k < g; ++k) {
+                const float a = fabsf(q38o_bf16_to_f32(w[k]));
+                if (a > amax) amax = a;
+            }
+            float s = amax / qmax;
+            if (s == 0.0f) s = 1.0f;
+            scales_f16[(size_t)r * groups + gi] = q38o_f32_to_f16(s);
+            for (uint32_t k = 0; k < g; ++k) {
+                float v = rintf(q38o_bf16_to_f32(w[k]) / s);
+                if (v > qmax) v = qmax;
+                if (v < -qmax) v = -qmax;
+                const int q = (int)v;
+                const size_t col = (size_t)gi * g + k;
+                if (bits == 8) {
+                    data[(size_t)r * cols + col] = (uint8_t)(int8_t)q;
+                } else {
+                    uint8_t* byte = data + (size_t)r * (cols / 2) + col / 2;
+                    const uint8_t nib = (uint8_t)(q & 0xf);
+                    *byte = (col & 1) ? (uint8_t)((*byte & 0x0f) | (nib << 4))
+                                      : (uint8_t)((*byte & 0xf0) | nib);
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* Weights and the scaled row value                                    */
 /* ------------------------------------------------------------------ */
 

@@ -107,6 +107,17 @@ int q38o_build_plan(const int32_t* expert_ids, uint32_t tokens,
 void q38o_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
                         int8_t* q, float* scales);
 
+/* Weight quantiser (tools/q38_artifact_compiler.py:193-253,
+ * quantize_groupwise) over `rows` bf16 rows of `cols` columns: per group
+ * of `group` columns (0: the whole row) s = max|w| / qmax (fp32; qmax 7 for
+ * bits 4, 127 for bits 8), s == 0 -> 1, q = clip(rint(w / s), +-qmax).  W4
+ * packs column 2i in the low and 2i+1 in the high nibble (:240-243).
+ * Scales are written as fp16 (RNE) -- the reference writes bf16; fp16 is
+ * the BASELINE scale format.  Returns 0, or 1 for an invalid shape. */
+int q38o_quantize_weights(const uint16_t* src_bf16, uint64_t rows,
+                          uint32_t cols, int bits, uint32_t group,
+                          uint8_t* data, uint16_t* scales_f16);
+
 /* ---- weights -------------------------------------------------------- */
 typedef struct q38o_weights {
     const uint8_t* data;     /* canonical row-major: W4 [E][rows][cols/2]

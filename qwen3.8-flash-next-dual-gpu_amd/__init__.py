@@ -139,6 +139,7 @@ SIGNATURES = {
     "q38m_expert_weights_bytes": (_SZ, [ctypes.POINTER(ExpertWeights), ctypes.POINTER(_SZ)]),
     "q38m_repack_expert_weights": (_INT, [ctypes.POINTER(ExpertWeights),
                                           ctypes.POINTER(ExpertWeights), _P, _INT]),
+    "q38m_quantize_expert_weights": (_INT, [_P, ctypes.POINTER(ExpertWeights), _P, _INT]),
     "q38m_synth_fill": (_INT, [_U32, _U64, _U64, _U64, _F, _I32, _I32, _P, _U32, _P, _P, _INT]),
     "q38m_moe_compiled": (_INT, []),
     "q38m_last_error": (ctypes.c_char_p, []),

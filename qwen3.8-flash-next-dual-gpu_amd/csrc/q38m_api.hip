@@ -436,6 +436,27 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
     return finish(q38m::launch_repack(*src, *dst, as_stream(stream)), "repack kernels");
 }
 
+int q38m_quantize_expert_weights(const uint16_t* src_bf16, const q38m_expert_weights_v1* dst,
+                                 void* stream, int device) {
+    if (!src_bf16 || !dst || !dst->data || !dst->scales || dst->layout != Q38M_LAYOUT_ROW_MAJOR ||
+        dst->scale_dtype != Q38M_SCALE_F16 || dst->experts == 0 || dst->rows == 0 ||
+        dst->columns == 0 || !aligned(src_bf16, 16) || !aligned(dst->data, 16) ||
+        !aligned(dst->scales, 2))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid weight quantiser buffers");
+    const uint32_t g = dst->group_size;
+    const bool grouped = (g == 32u || g == 64u || g == 128u) && dst->columns % g == 0u;
+    const bool w4 = dst->format == Q38M_FORMAT_W4_SYM && grouped;
+    const bool w8 = dst->format == Q38M_FORMAT_W8_SYM &&
+                    (grouped || (g == 0u && dst->columns % 512u == 0u));
+    if (!w4 && !w8)
+        return fail(Q38M_ERR_UNSUPPORTED,
+                    "quantiser supports W4 groups 32/64/128 and W8 groups 32/64/128 or per "
+                    "channel (columns a multiple of 512)");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_quantize_weights(src_bf16, *dst, as_stream(stream)),
+                  "quantize_weights kernels");
+}
+
 int q38m_synth_fill(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count, float sigma,
                     int32_t lo, int32_t hi, const float* bias, uint32_t bias_len, void* out,
                     void* stream, int device) {

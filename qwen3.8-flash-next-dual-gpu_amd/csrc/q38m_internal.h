@@ -80,6 +80,9 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
 // layout and synthetic data (q38m_layout.hip)
 hipError_t launch_repack(const q38m_expert_weights_v1& src,
                          const q38m_expert_weights_v1& dst, hipStream_t stream);
+// bf16 [experts*rows][columns] -> dst (row-major, fp16 scales)
+hipError_t launch_quantize_weights(const uint16_t* src, const q38m_expert_weights_v1& dst,
+                                  hipStream_t stream);
 hipError_t launch_synth(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count,
                         float sigma, int32_t lo, int32_t hi, const float* bias,
                         uint32_t bias_len, void* out, hipStream_t stream);

@@ -80,6 +80,120 @@ __global__ void repack_w8_kernel(const uint4* __restrict__ src, uint4* __restric
     dst[o] = src[((e * rows + rt * 16u + n) * cols + kb * 64u + q * 16u) / 16u];
 }
 
+// ---------------------------------------------------------------------------
+// Weight quantiser (tools/q38_artifact_compiler.py:193-253, quantize_groupwise):
+// per group s = max|w| / qmax (qmax 7 for W4, 127 for W8), s == 0 -> 1,
+// q = clamp(rint(w / s), +-qmax); W4 packs column 2i in the low nibble.
+// Scales are stored as fp16 (round to nearest even, subnormals kept).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v)));
+}
+
+template <uint32_t kBits>
+__device__ __forceinline__ uint32_t quant_weight(uint32_t bf16, float s) {
+    constexpr float kMax = kBits == 4u ? 7.0f : 127.0f;
+    float v = __builtin_rintf(bf16_to_f32(bf16) / s);
+    v = fminf(fmaxf(v, -kMax), kMax);
+    return static_cast<uint32_t>(static_cast<int32_t>(v)) & (kBits == 4u ? 0xfu : 0xffu);
+}
+
+// One thread per group of kGroup columns (groups are contiguous in memory).
+template <uint32_t kBits, uint32_t kGroup>
+__global__ __launch_bounds__(256) void quantize_weights_group_kernel(
+    const uint4* __restrict__ src, uint64_t groups, uint8_t* __restrict__ data,
+    uint16_t* __restrict__ scales) {
+    constexpr uint32_t kVec = kGroup / 8u;  // uint4 of 8 bf16
+    constexpr float kMax = kBits == 4u ? 7.0f : 127.0f;
+    const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    uint32_t w[kGroup / 2u];
+#pragma unroll
+    for (uint32_t i = 0; i < kVec; ++i) {
+        const uint4 v = src[g * kVec + i];
+        w[4 * i] = v.x; w[4 * i + 1] = v.y; w[4 * i + 2] = v.z; w[4 * i + 3] = v.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < kGroup / 2u; ++i) {
+        amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] & 0xffffu)));
+        amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] >> 16)));
+    }
+    float s = amax / kMax;
+    if (s == 0.0f) s = 1.0f;
+    scales[g] = static_cast<uint16_t>(f32_to_f16_bits(s));
+    if constexpr (kBits == 4u) {
+        // two bf16 per word -> one byte (low nibble = even column)
+        uint32_t packed[kGroup / 8u];
+#pragma unroll
+        for (uint32_t i = 0; i < kGroup / 8u; ++i) {
+            uint32_t b = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j) {
+                const uint32_t word = w[4 * i + j];
+                const uint32_t byte = quant_weight<4>(word & 0xffffu, s) |
+                                      (quant_weight<4>(word >> 16, s) << 4);
+                b |= byte << (8 * j);
+            }
+            packed[i] = b;
+        }
+        uint4* out = reinterpret_cast<uint4*>(data + g * (kGroup / 2u));
+#pragma unroll
+        for (uint32_t i = 0; i < kGroup / 32u; ++i)
+            out[i] = make_uint4(packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]);
+    } else {
+        uint32_t packed[kGroup / 4u];
+#pragma unroll
+        for (uint32_t i = 0; i < kGroup / 4u; ++i) {
+            const uint32_t lo = w[2 * i], hi = w[2 * i + 1];
+            packed[i] = quant_weight<8>(lo & 0xffffu, s) | (quant_weight<8>(lo >> 16, s) << 8) |
+                        (quant_weight<8>(hi & 0xffffu, s) << 16) | (quant_weight<8>(hi >> 16, s) << 24);
+        }
+        uint4* out = reinterpret_cast<uint4*>(data + g * kGroup);
+#pragma unroll
+        for (uint32_t i = 0; i < kGroup / 16u; ++i)
+            out[i] = make_uint4(packed[4 * i], packed[4 * i + 1], packed[4 * i + 2], packed[4 * i + 3]);
+    }
+}
+
+// W8 per output channel: one wave per row (columns % 512 == 0), two passes.
+__global__ __launch_bounds__(256) void quantize_weights_row_w8_kernel(
+    const uint16_t* __restrict__ src, uint64_t rows, uint32_t cols, uint8_t* __restrict__ data,
+    uint16_t* __restrict__ scales) {
+    const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4u + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint4* r = reinterpret_cast<const uint4*>(src + row * cols);
+    float amax = 0.0f;
+    for (uint32_t c = lane; c < cols / 8u; c += 64u) {
+        const uint4 v = r[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] & 0xffffu)));
+            amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] >> 16)));
+        }
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) amax = fmaxf(amax, __shfl_xor(amax, offset, 64));
+    float s = amax / 127.0f;
+    if (s == 0.0f) s = 1.0f;
+    if (lane == 0) scales[row] = static_cast<uint16_t>(f32_to_f16_bits(s));
+    uint2* out = reinterpret_cast<uint2*>(data + row * cols);
+    for (uint32_t c = lane; c < cols / 8u; c += 64u) {
+        const uint4 v = r[c];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t packed[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            packed[i] = quant_weight<8>(w[2 * i] & 0xffffu, s) |
+                        (quant_weight<8>(w[2 * i] >> 16, s) << 8) |
+                        (quant_weight<8>(w[2 * i + 1] & 0xffffu, s) << 16) |
+                        (quant_weight<8>(w[2 * i + 1] >> 16, s) << 24);
+        out[c] = make_uint2(packed[0], packed[1]);
+    }
+}
+
 __global__ void copy_u16_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
                                 uint64_t total) {
     const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -177,6 +291,33 @@ hipError_t launch_repack(const q38m_expert_weights_v1& src,
             static_cast<const uint16_t*>(src.scales),
             static_cast<uint16_t*>(const_cast<void*>(dst.scales)), scales);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_weights(const uint16_t* src, const q38m_expert_weights_v1& dst,
+                                  hipStream_t stream) {
+    const uint64_t rows = static_cast<uint64_t>(dst.experts) * dst.rows;
+    uint8_t* data = static_cast<uint8_t*>(const_cast<void*>(dst.data));
+    uint16_t* scales = static_cast<uint16_t*>(const_cast<void*>(dst.scales));
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    const uint32_t g = dst.group_size;
+    const bool w4 = dst.format == Q38M_FORMAT_W4_SYM;
+    if (g == 0u) {
+        quantize_weights_row_w8_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(
+            src, rows, dst.columns, data, scales);
+        return hipGetLastError();
+    }
+    const uint64_t groups = rows * (dst.columns / g);
+    const uint32_t grid = blocks_for(groups, 256);
+#define Q38M_QUANT(BITS, G)                                                                  \
+    quantize_weights_group_kernel<BITS, G><<<grid, 256, 0, stream>>>(s4, groups, data, scales)
+    if (w4 && g == 32u) Q38M_QUANT(4u, 32u);
+    else if (w4 && g == 64u) Q38M_QUANT(4u, 64u);
+    else if (w4) Q38M_QUANT(4u, 128u);
+    else if (g == 32u) Q38M_QUANT(8u, 32u);
+    else if (g == 64u) Q38M_QUANT(8u, 64u);
+    else Q38M_QUANT(8u, 128u);
+#undef Q38M_QUANT
     return hipGetLastError();
 }
 

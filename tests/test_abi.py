@@ -172,6 +172,24 @@ def test_routing_and_quant_validation(q38m):
         q38m.call("q38m_moe_pack_hidden_v1", 0x1000, 0x2000, 15, 2048, 0x3000, None, 0)
 
 
+def test_weight_quantizer_validation(q38m):
+    def desc(fmt=2, group=32, scale=1, layout=0, rows=1024, cols=2048, data=0x200000,
+             scales=0x400000):
+        return q38m.ExpertWeights(data, scales, fmt, group, scale, layout, 512, rows, cols)
+
+    for d, err in [(desc(layout=2), q38m.InvalidArgument),        # not row-major
+                   (desc(scale=2), q38m.InvalidArgument),         # scale dtype
+                   (desc(data=0x200008), q38m.InvalidArgument),   # misaligned data
+                   (desc(group=16), q38m.Unsupported),            # W4 group 16
+                   (desc(group=0), q38m.Unsupported),             # W4 per channel
+                   (desc(fmt=3, group=0, cols=500), q38m.Unsupported),  # per channel, 500 cols
+                   (desc(group=128, cols=2000), q38m.Unsupported)]:     # 2000 % 128
+        with pytest.raises(err):
+            q38m.call("q38m_quantize_expert_weights", 0x100000, ctypes.byref(d), None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # no source
+        q38m.call("q38m_quantize_expert_weights", None, ctypes.byref(desc()), None, 0)
+
+
 def test_route_quantize_validation(q38m):
     # logits, hidden, tokens, ids, weights, xq, xs
     good = [0x1000, 0x2000, 8, 0x3000, 0x4000, 0x5000, 0x6000]
