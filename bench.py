@@ -29,6 +29,7 @@ PACKAGE_DIR = os.path.join(ROOT, "qwen3.8-flash-next-dual-gpu_amd")
 
 HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # dense int8 MFMA, POP/s expressed in TOP/s
+BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
 
 
 def load(name, path, package_dir=None):
@@ -49,6 +50,7 @@ def main():
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-decode", action="store_true")
     parser.add_argument("--no-quantizer", action="store_true")
+    parser.add_argument("--no-dense", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
@@ -233,6 +235,9 @@ def main():
     if not args.no_quantizer:
         result["weight_pipeline"] = bench_weight_pipeline(q38m, W, torch)
 
+    if not args.no_dense:
+        result["router_shared"] = bench_router_shared(q38m, W, torch, hidden, args.steps)
+
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
                                               T)
@@ -321,6 +326,68 @@ def bench_decode(q38m, W, torch, tokens):
             "algorithmic_bytes_per_token": bytes_token, "launches_per_layer": 2,
             "entry_point": "q38m_moe_decode_v1", **graph_rate, "mode": "hip_graph",
             "eager": rate(ms_eager)}
+
+
+def bench_router_shared(q38m, W, torch, hidden, steps):
+    """The dense bf16 GEMMs either side of the routed experts on the same
+    512-token slab: the router (hidden x [512][2048] -> fp32 logits) and the
+    shared expert (gate/up [512][2048], SiLU multiply, down [2048][512],
+    scalar output gate).  Flops are 2 per multiply-add; bytes are every
+    operand read once plus every result written once."""
+    sh = torch.cuda.current_stream().cuda_stream
+    T = hidden.shape[0]
+    I = W.INTER
+    rng = torch.Generator(device="cuda").manual_seed(5)
+
+    def weight(rows, cols):
+        w = (torch.randn(rows, cols, generator=rng, device="cuda") * 0.02).to(torch.bfloat16)
+        return w.view(torch.int16)
+
+    router = weight(W.EXPERTS, W.HIDDEN)
+    wg, wu, wd, wo = weight(I, W.HIDDEN), weight(I, W.HIDDEN), weight(W.HIDDEN, I), weight(1, W.HIDDEN)
+    logits = torch.empty(T, W.EXPERTS, dtype=torch.float32, device="cuda")
+    scratch = torch.empty(q38m.lib().q38m_moe_shared_expert_scratch_bytes(T, I) // 2,
+                          dtype=torch.int16, device="cuda")
+    so = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
+    sg = torch.empty(T, dtype=torch.int16, device="cuda")
+
+    def run_router():
+        q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), T,
+                  logits.data_ptr(), sh, 0)
+
+    def run_shared():
+        q38m.call("q38m_moe_shared_expert_v1", hidden.data_ptr(), wg.data_ptr(), wu.data_ptr(),
+                  wd.data_ptr(), wo.data_ptr(), T, I, scratch.data_ptr(), so.data_ptr(),
+                  sg.data_ptr(), sh, 0)
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / steps
+
+    r_ms, s_ms = timed(run_router), timed(run_shared)
+    r_flops = 2 * T * W.EXPERTS * W.HIDDEN
+    r_bytes = 2 * T * W.HIDDEN + 2 * W.EXPERTS * W.HIDDEN + 4 * T * W.EXPERTS
+    s_flops = 2 * T * W.HIDDEN * (3 * I + 1)
+    s_bytes = (2 * T * W.HIDDEN + 2 * (3 * I * W.HIDDEN + W.HIDDEN) + 3 * 2 * T * I * 2 +
+               2 * T * W.HIDDEN + 2 * T)
+    out = {}
+    for name, ms, flops, nbytes in (("router", r_ms, r_flops, r_bytes),
+                                    ("shared_expert", s_ms, s_flops, s_bytes)):
+        s = ms * 1e-3
+        out[name] = {"ms": round(ms, 5), "TFLOPs": round(flops / s / 1e12, 2),
+                     "bf16_mfma_frac": round(flops / s / 1e12 / BF16_PEAK_TFLOPS, 4),
+                     "GBps": round(nbytes / s / 1e9, 1),
+                     "hbm_frac": round(nbytes / s / 1e9 / HBM_PEAK_GBPS, 4)}
+    out["tokens"] = T
+    return out
 
 
 def bench_weight_pipeline(q38m, W, torch, reps=5):

@@ -298,6 +298,40 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
                                const q38m_expert_weights_v1* dst,
                                void* stream, int device);
 
+/* ---- dense bf16 GEMMs on either side of the routed experts ----------
+ * C[m][n] = A[m][k] * B[n][k]^T (both K-contiguous: activation rows and
+ * [out][in] weight rows), bf16 in, fp32 accumulation (MFMA), exactly one of
+ * c_f32 / c_bf16 (round to nearest even) out.  k % 32 == 0; a, b 16-byte
+ * aligned.  Floating-point parity: a tolerance, not bit-exact. */
+int q38m_dense_gemm_bf16(const uint16_t* a, const uint16_t* b, uint32_t m,
+                         uint32_t n, uint32_t k, float* c_f32,
+                         uint16_t* c_bf16, void* stream, int device);
+
+/* Router logits: hidden bf16 [T][2048] times the bf16 router [512][2048]
+ * (the "preserved" router format, tools/q38_quant_policy.py:205) -> fp32
+ * logits [T][512], the input of q38m_moe_route_quantize_v1 /
+ * q38m_moe_prefill_v1 / q38m_moe_decode_v1.  Replaces the router GEMV/GEMM
+ * of run_moe (cuda/cuda_backend.cu:1518-1519; the reference rounds the
+ * logits to bf16). */
+int q38m_moe_router_v1(const uint16_t* hidden, const uint16_t* router,
+                       uint32_t tokens, float* logits, void* stream, int device);
+
+/* Shared expert of the MoE block (cuda/cuda_backend.cu:1573-1590), bf16
+ * weights: g = bf16(x Wg^T), u = bf16(x Wu^T) [T][inter],
+ * h = bf16(g / (1 + exp(-g)) * u) (cuda_silu_multiply_bf16,
+ * cuda/q38_kernels.cu:286-296), shared_output = bf16(h Wd^T) [T][2048],
+ * shared_gate = bf16(x Wo^T) [T] -- the two inputs of the gated combine
+ * (q38m_moe_prefill_v1 / q38m_moe_decode_v1 / combine entry points).
+ * Wg, Wu [inter][2048]; Wd [2048][inter]; Wo [1][2048]; inter % 32 == 0.
+ * scratch: q38m_moe_shared_expert_scratch_bytes(T, inter) bytes. */
+size_t q38m_moe_shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter);
+int q38m_moe_shared_expert_v1(const uint16_t* hidden, const uint16_t* w_gate,
+                              const uint16_t* w_up, const uint16_t* w_down,
+                              const uint16_t* w_out_gate, uint32_t tokens,
+                              uint32_t inter, void* scratch,
+                              uint16_t* shared_output, uint16_t* shared_gate,
+                              void* stream, int device);
+
 /* Weight quantiser of the artifact pipeline: quantize_groupwise
  * (tools/q38_artifact_compiler.py:193-253) on the device.  src: bf16
  * weights [experts*rows][columns]; dst: row-major layout, fp16 scales,

@@ -171,6 +171,23 @@ inline void run_moe_prefill(const ExpertWeightsV1& gate_up, const ExpertWeightsV
                               shared_output, shared_gate, output, stream, device));
 }
 
+// Router logits (cuda_backend.cu:1518-1519): fp32 [tokens][512].
+inline void moe_router(const std::uint16_t* hidden, const std::uint16_t* router,
+                       std::uint32_t tokens, float* logits, void* stream, int device) {
+    check(q38m_moe_router_v1(hidden, router, tokens, logits, stream, device));
+}
+
+// Shared expert (cuda_backend.cu:1573-1590): shared_output bf16 [tokens][2048]
+// and shared_gate bf16 [tokens] for the gated combine.
+inline void moe_shared_expert(const std::uint16_t* hidden, const std::uint16_t* w_gate,
+                              const std::uint16_t* w_up, const std::uint16_t* w_down,
+                              const std::uint16_t* w_out_gate, std::uint32_t tokens,
+                              std::uint32_t inter, void* scratch, std::uint16_t* shared_output,
+                              std::uint16_t* shared_gate, void* stream, int device) {
+    check(q38m_moe_shared_expert_v1(hidden, w_gate, w_up, w_down, w_out_gate, tokens, inter,
+                                    scratch, shared_output, shared_gate, stream, device));
+}
+
 inline bool cuda_q38_moe_prefill_compiled() { return q38m_moe_compiled() == 1; }
 inline bool cuda_q38_moe_compiled() { return q38m_moe_compiled() == 1; }
 

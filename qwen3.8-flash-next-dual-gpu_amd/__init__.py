@@ -140,6 +140,10 @@ SIGNATURES = {
     "q38m_repack_expert_weights": (_INT, [ctypes.POINTER(ExpertWeights),
                                           ctypes.POINTER(ExpertWeights), _P, _INT]),
     "q38m_quantize_expert_weights": (_INT, [_P, ctypes.POINTER(ExpertWeights), _P, _INT]),
+    "q38m_dense_gemm_bf16": (_INT, [_P, _P, _U32, _U32, _U32, _P, _P, _P, _INT]),
+    "q38m_moe_router_v1": (_INT, [_P, _P, _U32, _P, _P, _INT]),
+    "q38m_moe_shared_expert_scratch_bytes": (_SZ, [_U32, _U32]),
+    "q38m_moe_shared_expert_v1": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _INT]),
     "q38m_synth_fill": (_INT, [_U32, _U64, _U64, _U64, _F, _I32, _I32, _P, _U32, _P, _P, _INT]),
     "q38m_moe_compiled": (_INT, []),
     "q38m_last_error": (ctypes.c_char_p, []),

@@ -436,6 +436,51 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
     return finish(q38m::launch_repack(*src, *dst, as_stream(stream)), "repack kernels");
 }
 
+// the GEMM grid's y dimension holds one 64-row tile per block
+constexpr uint32_t kDenseMaxRows = 65535u * 64u;
+
+int q38m_dense_gemm_bf16(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
+                         uint32_t k, float* c_f32, uint16_t* c_bf16, void* stream, int device) {
+    if (!a || !b || m == 0 || n == 0 || k == 0 || k % 32u != 0u || m > kDenseMaxRows ||
+        (c_f32 == nullptr) == (c_bf16 == nullptr) || !aligned(a, 16) || !aligned(b, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid dense GEMM buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_dense_gemm(a, b, m, n, k, c_f32, c_bf16, as_stream(stream)),
+                  "dense_gemm_kernel");
+}
+
+int q38m_moe_router_v1(const uint16_t* hidden, const uint16_t* router, uint32_t tokens,
+                       float* logits, void* stream, int device) {
+    if (!hidden || !router || !logits || tokens == 0 || tokens > kDenseMaxRows ||
+        !aligned(hidden, 16) || !aligned(router, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid router buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_dense_gemm(hidden, router, tokens, Q38M_ROUTE_EXPERTS,
+                                          Q38M_HIDDEN, logits, nullptr, as_stream(stream)),
+                  "router GEMM");
+}
+
+size_t q38m_moe_shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter) {
+    return q38m::shared_expert_scratch_bytes(tokens, inter);
+}
+
+int q38m_moe_shared_expert_v1(const uint16_t* hidden, const uint16_t* w_gate,
+                              const uint16_t* w_up, const uint16_t* w_down,
+                              const uint16_t* w_out_gate, uint32_t tokens, uint32_t inter,
+                              void* scratch, uint16_t* shared_output, uint16_t* shared_gate,
+                              void* stream, int device) {
+    if (!hidden || !w_gate || !w_up || !w_down || !w_out_gate || !scratch || !shared_output ||
+        !shared_gate || tokens == 0 || tokens > kDenseMaxRows || inter == 0 || inter % 32u != 0u ||
+        !aligned(hidden, 16) || !aligned(w_gate, 16) || !aligned(w_up, 16) ||
+        !aligned(w_down, 16) || !aligned(w_out_gate, 16) || !aligned(scratch, 16))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid shared expert buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_shared_expert(hidden, w_gate, w_up, w_down, w_out_gate, tokens,
+                                             inter, scratch, shared_output, shared_gate,
+                                             as_stream(stream)),
+                  "shared expert kernels");
+}
+
 int q38m_quantize_expert_weights(const uint16_t* src_bf16, const q38m_expert_weights_v1* dst,
                                  void* stream, int device) {
     if (!src_bf16 || !dst || !dst->data || !dst->scales || dst->layout != Q38M_LAYOUT_ROW_MAJOR ||

@@ -1,0 +1,292 @@
+// Dense bf16 GEMMs of the MoE block on either side of the routed experts:
+// the router (cuda_backend.cu:1518-1519, cuda_gemv_bf16 over the
+// "preserved" bf16 router, tools/q38_quant_policy.py:205) and the shared
+// expert (cuda_backend.cu:1573-1590: gate and up projections, SiLU
+// multiply, down projection, the scalar output gate).
+//
+// C[M][N] = A[M][K] * B[N][K]^T: both operands keep K contiguous (the
+// activation rows and the weight matrices' [out][in] rows), bf16 in, fp32
+// accumulation on v_mfma_f32_16x16x32_bf16, fp32 or bf16 (round to nearest
+// even) out.  These are floating-point results: their parity with a CPU
+// restatement is a stated tolerance (the MFMA's internal summation order is
+// not specified), unlike the integer expert GEMMs.  The order of the
+// partial sums is fixed, so a launch's results are the same on every run.
+#include "q38m_device.h"
+#include "q38m_internal.h"
+
+namespace q38m {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+constexpr uint32_t kDenseWaves = 4;
+
+// Lane pointer into a 16-row panel starting at `row`: lane l reads row l%16
+// (clamped to the last row, never stored) at k = 8*(l/16) .. +7 of each
+// 32-wide K step, one 16-byte load per step, which is the bf16 MFMA
+// operand layout.
+__device__ __forceinline__ const uint4* panel_ptr(const uint16_t* base, uint32_t row,
+                                                  uint32_t rows, uint32_t k, uint32_t lane) {
+    const uint32_t r = min(row + (lane & 15u), rows - 1u);
+    return reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * k + (lane >> 4) * 8u);
+}
+
+// One wave's partial products over K steps [s0, s1) for kTM A panels
+// against kNB x kTN B panels.  Steps go in batches of kBatch with the next
+// batch's loads issued before the current batch's MFMAs, so a wave has a
+// batch of loads in flight while it multiplies.
+template <uint32_t kTM, uint32_t kTN, uint32_t kNB, uint32_t kBatch>
+__device__ __forceinline__ void wave_partial(const uint4* const (&pa)[kTM],
+                                             const uint4* const (&pb)[kNB][kTN], uint32_t s0,
+                                             uint32_t s1, f32x4 (&acc)[kNB][kTM][kTN]) {
+    struct Batch {
+        uint4 a[kBatch][kTM];
+        uint4 b[kBatch][kNB][kTN];
+    };
+    auto load = [&](Batch& x, uint32_t s, uint32_t count) {
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) {
+            if (q >= count) break;
+#pragma unroll
+            for (uint32_t i = 0; i < kTM; ++i) x.a[q][i] = pa[i][4u * (s + q)];
+#pragma unroll
+            for (uint32_t v = 0; v < kNB; ++v)
+#pragma unroll
+                for (uint32_t j = 0; j < kTN; ++j) x.b[q][v][j] = pb[v][j][4u * (s + q)];
+        }
+    };
+    auto multiply = [&](const Batch& x, uint32_t count) {
+#pragma unroll
+        for (uint32_t q = 0; q < kBatch; ++q) {
+            if (q >= count) break;
+#pragma unroll
+            for (uint32_t v = 0; v < kNB; ++v)
+#pragma unroll
+                for (uint32_t i = 0; i < kTM; ++i)
+#pragma unroll
+                    for (uint32_t j = 0; j < kTN; ++j)
+                        acc[v][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            as_bf16x8(x.a[q][i]), as_bf16x8(x.b[q][v][j]), acc[v][i][j], 0, 0,
+                            0);
+        }
+    };
+    uint32_t s = s0;
+    if (s + kBatch <= s1) {
+        Batch cur;
+        load(cur, s, kBatch);
+        s += kBatch;
+        while (s + kBatch <= s1) {
+            Batch next;
+            load(next, s, kBatch);
+            multiply(cur, kBatch);
+            cur = next;
+            s += kBatch;
+        }
+        multiply(cur, kBatch);
+    }
+    for (; s < s1; ++s) {
+        Batch one;
+        load(one, s, 1u);
+        multiply(one, 1u);
+    }
+}
+
+constexpr uint32_t batch_for(uint32_t loads_per_step) {
+    return loads_per_step <= 2u ? 8u : (loads_per_step <= 4u ? 4u : 2u);
+}
+
+// The four waves of a block split K; their partial tiles meet in LDS and
+// are summed in wave order (((w0 + w1) + w2) + w3), the same for every
+// launch.  acc holds kTiles tiles as kTiles / per_b groups of per_b (one
+// group per B matrix); wave w finishes output tiles o = w, w + 4, ... of
+// every group, calling finish(o, group, sum).
+template <uint32_t kTiles, uint32_t kPerB, typename Finish>
+__device__ __forceinline__ void reduce_waves(f32x4* lds, const f32x4* acc, uint32_t wave,
+                                             uint32_t lane, Finish finish) {
+#pragma unroll
+    for (uint32_t t = 0; t < kTiles; ++t) lds[(wave * kTiles + t) * 64u + lane] = acc[t];
+    __syncthreads();
+#pragma unroll
+    for (uint32_t o = 0; o < kPerB; ++o) {
+        if (o % kDenseWaves != wave) continue;
+#pragma unroll
+        for (uint32_t v = 0; v < kTiles / kPerB; ++v) {
+            const uint32_t t = v * kPerB + o;
+            f32x4 sum = lds[t * 64u + lane];
+#pragma unroll
+            for (uint32_t w = 1; w < kDenseWaves; ++w) sum += lds[(w * kTiles + t) * 64u + lane];
+            finish(o, v, sum);
+        }
+    }
+}
+
+// C[M][N] = A[M][K] * B[N][K]^T for a (16 kTM) x (16 kTN) tile of C per
+// workgroup of four waves that split K.  The D layout of each 16 x 16 MFMA
+// tile: lane l holds rows 4*(l/16) + e, e = 0..3, of column l%16.
+template <uint32_t kTM, uint32_t kTN, bool kBf16Out>
+__global__ __launch_bounds__(256) void dense_gemm_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m, uint32_t n,
+    uint32_t k, float* __restrict__ c_f32, uint16_t* __restrict__ c_bf16) {
+    __shared__ f32x4 lds[kDenseWaves * kTM * kTN * 64];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t m0 = blockIdx.y * 16u * kTM;
+    const uint32_t n0 = blockIdx.x * 16u * kTN;
+    const uint4* pa[kTM];
+    const uint4* pb[1][kTN];
+#pragma unroll
+    for (uint32_t i = 0; i < kTM; ++i) pa[i] = panel_ptr(a, m0 + 16u * i, m, k, lane);
+#pragma unroll
+    for (uint32_t j = 0; j < kTN; ++j) pb[0][j] = panel_ptr(b, n0 + 16u * j, n, k, lane);
+    f32x4 acc[1][kTM][kTN];
+#pragma unroll
+    for (uint32_t i = 0; i < kTM; ++i)
+#pragma unroll
+        for (uint32_t j = 0; j < kTN; ++j) acc[0][i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t steps = k / 32u;
+    wave_partial<kTM, kTN, 1, batch_for(kTM + kTN)>(pa, pb, wave * steps / kDenseWaves,
+                                                    (wave + 1u) * steps / kDenseWaves, acc);
+    reduce_waves<kTM * kTN, kTM * kTN>(lds, &acc[0][0][0], wave, lane,
+                                       [&](uint32_t o, uint32_t, f32x4 sum) {
+        const uint32_t col = n0 + 16u * (o % kTN) + (lane & 15u);
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const uint32_t row = m0 + 16u * (o / kTN) + 4u * (lane >> 4) + e;
+            if (row >= m || col >= n) continue;
+            const size_t at = static_cast<size_t>(row) * n + col;
+            if constexpr (kBf16Out)
+                c_bf16[at] = static_cast<uint16_t>(f32_to_bf16(sum[e]));
+            else
+                c_f32[at] = sum[e];
+        }
+    });
+}
+
+// h = bf16(g / (1 + exp(-g)) * u) on bf16 g and u (q38_kernels.cu:286-296,
+// with this library's exp).
+__device__ __forceinline__ uint32_t silu_multiply(uint32_t g_bits, uint32_t u_bits) {
+    const float g = bf16_to_f32(g_bits);
+    return f32_to_bf16((g / (1.0f + exp_q(-g))) * bf16_to_f32(u_bits));
+}
+
+// The shared expert's first half in one launch: block (x, y) with x below
+// the last column computes the 32 x 32 tiles (y, x) of g = bf16(X Wg^T) and
+// u = bf16(X Wu^T) and h = silu_multiply(g, u) from them; the last column
+// of blocks computes the scalar output gate bf16(X wo^T) of its 32 rows.
+__global__ __launch_bounds__(256) void shared_gate_up_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w_gate,
+    const uint16_t* __restrict__ w_up, const uint16_t* __restrict__ w_out_gate, uint32_t m,
+    uint32_t inter, uint16_t* __restrict__ g_out, uint16_t* __restrict__ u_out,
+    uint16_t* __restrict__ h_out, uint16_t* __restrict__ gate_out) {
+    constexpr uint32_t kTM = 2, kTN = 2;
+    __shared__ f32x4 lds[kDenseWaves * 2 * kTM * kTN * 64];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t m0 = blockIdx.y * 16u * kTM;
+    const uint32_t steps = kHidden / 32u;
+    const uint32_t s0 = wave * steps / kDenseWaves, s1 = (wave + 1u) * steps / kDenseWaves;
+    const uint4* pa[kTM];
+#pragma unroll
+    for (uint32_t i = 0; i < kTM; ++i) pa[i] = panel_ptr(x, m0 + 16u * i, m, kHidden, lane);
+    if (blockIdx.x == gridDim.x - 1u) {
+        const uint4* pb[1][1] = {{panel_ptr(w_out_gate, 0, 1, kHidden, lane)}};
+        f32x4 acc[1][kTM][1];
+#pragma unroll
+        for (uint32_t i = 0; i < kTM; ++i) acc[0][i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        wave_partial<kTM, 1, 1, batch_for(kTM + 1)>(pa, pb, s0, s1, acc);
+        reduce_waves<kTM, kTM>(lds, &acc[0][0][0], wave, lane,
+                               [&](uint32_t o, uint32_t, f32x4 sum) {
+            if ((lane & 15u) != 0u) return;  // column 0 holds the gate
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) {
+                const uint32_t row = m0 + 16u * o + 4u * (lane >> 4) + e;
+                if (row < m) gate_out[row] = static_cast<uint16_t>(f32_to_bf16(sum[e]));
+            }
+        });
+        return;
+    }
+    const uint32_t n0 = blockIdx.x * 16u * kTN;
+    const uint4* pb[2][kTN];
+#pragma unroll
+    for (uint32_t j = 0; j < kTN; ++j) {
+        pb[0][j] = panel_ptr(w_gate, n0 + 16u * j, inter, kHidden, lane);
+        pb[1][j] = panel_ptr(w_up, n0 + 16u * j, inter, kHidden, lane);
+    }
+    f32x4 acc[2][kTM][kTN];
+#pragma unroll
+    for (uint32_t v = 0; v < 2u; ++v)
+#pragma unroll
+        for (uint32_t i = 0; i < kTM; ++i)
+#pragma unroll
+            for (uint32_t j = 0; j < kTN; ++j) acc[v][i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    wave_partial<kTM, kTN, 2, batch_for(kTM + 2 * kTN)>(pa, pb, s0, s1, acc);
+    uint32_t g_bits[4] = {0u, 0u, 0u, 0u};
+    reduce_waves<2 * kTM * kTN, kTM * kTN>(lds, &acc[0][0][0], wave, lane,
+                                           [&](uint32_t o, uint32_t v, f32x4 sum) {
+        const uint32_t col = n0 + 16u * (o % kTN) + (lane & 15u);
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) {
+            const uint32_t row = m0 + 16u * (o / kTN) + 4u * (lane >> 4) + e;
+            const uint32_t bits = f32_to_bf16(sum[e]);
+            if (v == 0u) {  // the g tile comes first, then the u tile
+                g_bits[e] = bits;
+                continue;
+            }
+            if (row >= m) continue;
+            const size_t at = static_cast<size_t>(row) * inter + col;
+            g_out[at] = static_cast<uint16_t>(g_bits[e]);
+            u_out[at] = static_cast<uint16_t>(bits);
+            h_out[at] = static_cast<uint16_t>(silu_multiply(g_bits[e], bits));
+        }
+    });
+}
+
+}  // namespace
+
+hipError_t launch_dense_gemm(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
+                             uint32_t k, float* c_f32, uint16_t* c_bf16, hipStream_t stream) {
+    const uint32_t tm = m <= 16u ? 1u : 2u;
+    const uint32_t tn = (m <= 16u || n <= 16u) ? 1u : 2u;
+    const dim3 grid((n + 16u * tn - 1u) / (16u * tn), (m + 16u * tm - 1u) / (16u * tm));
+    const bool bf = c_bf16 != nullptr;
+    if (tm == 1u && bf)
+        dense_gemm_kernel<1, 1, true><<<grid, 256, 0, stream>>>(a, b, m, n, k, nullptr, c_bf16);
+    else if (tm == 1u)
+        dense_gemm_kernel<1, 1, false><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, nullptr);
+    else if (tn == 1u && bf)
+        dense_gemm_kernel<2, 1, true><<<grid, 256, 0, stream>>>(a, b, m, n, k, nullptr, c_bf16);
+    else if (tn == 1u)
+        dense_gemm_kernel<2, 1, false><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, nullptr);
+    else if (bf)
+        dense_gemm_kernel<2, 2, true><<<grid, 256, 0, stream>>>(a, b, m, n, k, nullptr, c_bf16);
+    else
+        dense_gemm_kernel<2, 2, false><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, nullptr);
+    return hipGetLastError();
+}
+
+size_t shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter) {
+    return 3u * static_cast<size_t>(tokens) * inter * sizeof(uint16_t);
+}
+
+hipError_t launch_shared_expert(const uint16_t* hidden, const uint16_t* w_gate,
+                                const uint16_t* w_up, const uint16_t* w_down,
+                                const uint16_t* w_out_gate, uint32_t tokens, uint32_t inter,
+                                void* scratch, uint16_t* shared_output, uint16_t* shared_gate,
+                                hipStream_t stream) {
+    const size_t elements = static_cast<size_t>(tokens) * inter;
+    uint16_t* g = static_cast<uint16_t*>(scratch);
+    uint16_t* u = g + elements;
+    uint16_t* h = u + elements;
+    const dim3 grid(inter / 32u + 1u, (tokens + 31u) / 32u);
+    shared_gate_up_kernel<<<grid, 256, 0, stream>>>(hidden, w_gate, w_up, w_out_gate, tokens,
+                                                    inter, g, u, h, shared_gate);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess)
+        e = launch_dense_gemm(h, w_down, tokens, kHidden, inter, nullptr, shared_output, stream);
+    return e;
+}
+
+}  // namespace q38m

@@ -77,6 +77,16 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
                          const uint16_t* shared_gate, const uint16_t* residual, void* scratch,
                          uint16_t* output, hipStream_t stream);
 
+// dense bf16 GEMMs (q38m_dense.hip): C = A * B^T, K contiguous in both
+hipError_t launch_dense_gemm(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
+                             uint32_t k, float* c_f32, uint16_t* c_bf16, hipStream_t stream);
+size_t shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter);
+hipError_t launch_shared_expert(const uint16_t* hidden, const uint16_t* w_gate,
+                                const uint16_t* w_up, const uint16_t* w_down,
+                                const uint16_t* w_out_gate, uint32_t tokens, uint32_t inter,
+                                void* scratch, uint16_t* shared_output, uint16_t* shared_gate,
+                                hipStream_t stream);
+
 // layout and synthetic data (q38m_layout.hip)
 hipError_t launch_repack(const q38m_expert_weights_v1& src,
                          const q38m_expert_weights_v1& dst, hipStream_t stream);

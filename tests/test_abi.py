@@ -201,6 +201,35 @@ def test_route_quantize_validation(q38m):
             q38m.call("q38m_moe_route_quantize_v1", *args, None, 0)
 
 
+def test_dense_validation(q38m):
+    # a, b, m, n, k, c_f32, c_bf16
+    good = [0x1000, 0x2000, 64, 512, 2048, 0x3000, None]
+    for i, bad in [(0, None), (1, None), (2, 0), (3, 0), (4, 0), (4, 48), (5, None),
+                   (2, 65535 * 64 + 1), (0, 0x1008), (1, 0x2002)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_dense_gemm_bf16", *args, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # both outputs
+        q38m.call("q38m_dense_gemm_bf16", 0x1000, 0x2000, 64, 512, 2048, 0x3000, 0x4000, None, 0)
+    # hidden, router, tokens, logits
+    good = [0x1000, 0x2000, 8, 0x3000]
+    for i, bad in [(0, None), (1, None), (2, 0), (3, None), (0, 0x1004)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_router_v1", *args, None, 0)
+    # hidden, wg, wu, wd, wo, tokens, inter, scratch, shared_output, shared_gate
+    good = [0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 8, 512, 0x6000, 0x7000, 0x8000]
+    for i, bad in [(0, None), (4, None), (5, 0), (6, 0), (6, 520), (7, None), (8, None),
+                   (9, None), (3, 0x4008), (7, 0x6004)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_shared_expert_v1", *args, None, 0)
+    assert q38m.lib().q38m_moe_shared_expert_scratch_bytes(8, 512) == 3 * 8 * 512 * 2
+
+
 def test_decode_and_step_validation(q38m):
     gu = fake_weights(q38m)
     dn = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)

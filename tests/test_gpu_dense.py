@@ -1,0 +1,153 @@
+"""The dense bf16 GEMMs on either side of the routed experts (SURVEY 8(f)
+ranks 1 and 2): the router logits and the shared expert.  They are
+floating-point results, checked against a float64 CPU evaluation within a
+tolerance written here; the shared expert's SiLU multiply and everything
+downstream of the logits / shared inputs are bit-exact.
+
+Tolerances: an fp32 accumulation of K products is within
+TOL_SUM * sum_k |a_k b_k| of the exact value (TOL_SUM = 2^-16, far above
+the ~sqrt(K) * 2^-24 typical error, far below any layout mistake); bf16
+outputs additionally within one bf16 step (2^-8 relative)."""
+import numpy as np
+import pytest
+
+from helpers import Layer, W, device, host, prefill, stream, synth_hidden, torch
+
+pytestmark = pytest.mark.gpu
+
+TOL_SUM = 2.0 ** -16
+BF16_STEP = 2.0 ** -8
+
+
+def bf16_matrix(orc, rng, rows, cols, sigma):
+    return orc.f32_to_bf16((rng.standard_normal((rows, cols)) * sigma).astype(np.float32))
+
+
+def gemm(q38m, a_dev, b_dev, m, n, k, out_bf16):
+    t = torch()
+    if out_bf16:
+        c = t.empty(m * n, dtype=t.int16, device="cuda")
+        q38m.call("q38m_dense_gemm_bf16", a_dev.data_ptr(), b_dev.data_ptr(), m, n, k, None,
+                  c.data_ptr(), stream(), 0)
+    else:
+        c = t.empty(m * n, dtype=t.float32, device="cuda")
+        q38m.call("q38m_dense_gemm_bf16", a_dev.data_ptr(), b_dev.data_ptr(), m, n, k,
+                  c.data_ptr(), None, stream(), 0)
+    t.cuda.synchronize()
+    return c
+
+
+def check_close(orc, got, a, b, out_bf16):
+    af = orc.bf16_to_f32(a).astype(np.float64)
+    bf = orc.bf16_to_f32(b).astype(np.float64)
+    exact = af @ bf.T
+    bound = TOL_SUM * (np.abs(af) @ np.abs(bf).T)
+    if out_bf16:
+        got = orc.bf16_to_f32(got).astype(np.float64)
+        bound = bound + BF16_STEP * np.abs(exact)
+    assert np.all(np.abs(got - exact) <= bound)
+
+
+@pytest.mark.parametrize("m,n,k", [(40, 512, 2048), (512, 2048, 512), (1, 512, 2048),
+                                   (33, 1, 2048), (64, 96, 64), (130, 70, 96)])
+@pytest.mark.parametrize("out_bf16", [False, True])
+def test_dense_gemm(q38m, orc, m, n, k, out_bf16):
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    a = bf16_matrix(orc, rng, m, k, 1.0)
+    b = bf16_matrix(orc, rng, n, k, 0.05)
+    c = gemm(q38m, device(a), device(b), m, n, k, out_bf16)
+    got = host(c, np.uint16 if out_bf16 else np.float32).reshape(m, n)
+    check_close(orc, got, a, b, out_bf16)
+
+
+def test_router_logits_and_routes(q38m, orc):
+    t = torch()
+    rng = np.random.default_rng(5)
+    tokens = 96
+    hidden = bf16_matrix(orc, rng, tokens, W.HIDDEN, 1.0)
+    router = bf16_matrix(orc, rng, W.EXPERTS, W.HIDDEN, 0.02)
+    logits = t.empty(tokens * W.EXPERTS, dtype=t.float32, device="cuda")
+    hd, rd = device(hidden), device(router)
+    q38m.call("q38m_moe_router_v1", hd.data_ptr(), rd.data_ptr(), tokens, logits.data_ptr(),
+              stream(), 0)
+    t.cuda.synchronize()
+    got = host(logits, np.float32).reshape(tokens, W.EXPERTS)
+    check_close(orc, got, hidden, router, False)
+    # routes: the top-10 of the GPU logits equals the top-10 of the exact
+    # logits wherever ranks 10 and 11 are further apart than the tolerance
+    hf = orc.bf16_to_f32(hidden).astype(np.float64)
+    rf = orc.bf16_to_f32(router).astype(np.float64)
+    exact = hf @ rf.T
+    bound = TOL_SUM * (np.abs(hf) @ np.abs(rf).T).max(axis=1)
+    ids_gpu, _ = orc.topk(got)
+    order = np.argsort(-exact, axis=1, kind="stable")
+    decided = 0
+    for tok in range(tokens):
+        s = np.sort(exact[tok])[::-1]
+        if s[9] - s[10] > 2 * bound[tok]:
+            assert set(ids_gpu[tok]) == set(order[tok, :10])
+            decided += 1
+    assert decided >= tokens * 0.9
+
+
+def test_shared_expert(q38m, orc):
+    t = torch()
+    rng = np.random.default_rng(9)
+    tokens, inter = 40, W.INTER
+    x = bf16_matrix(orc, rng, tokens, W.HIDDEN, 1.0)
+    wg = bf16_matrix(orc, rng, inter, W.HIDDEN, 0.02)
+    wu = bf16_matrix(orc, rng, inter, W.HIDDEN, 0.02)
+    wd = bf16_matrix(orc, rng, W.HIDDEN, inter, 0.02)
+    wo = bf16_matrix(orc, rng, 1, W.HIDDEN, 0.02)
+    scratch = t.empty(q38m.lib().q38m_moe_shared_expert_scratch_bytes(tokens, inter) // 2,
+                      dtype=t.int16, device="cuda")
+    so = t.empty(tokens * W.HIDDEN, dtype=t.int16, device="cuda")
+    sg = t.empty(tokens, dtype=t.int16, device="cuda")
+    devs = [device(v) for v in (x, wg, wu, wd, wo)]
+    q38m.call("q38m_moe_shared_expert_v1", *[d.data_ptr() for d in devs], tokens, inter,
+              scratch.data_ptr(), so.data_ptr(), sg.data_ptr(), stream(), 0)
+    t.cuda.synchronize()
+    words = host(scratch, np.uint16)
+    g = words[:tokens * inter].reshape(tokens, inter)
+    u = words[tokens * inter:2 * tokens * inter].reshape(tokens, inter)
+    h = words[2 * tokens * inter:].reshape(tokens, inter)
+    check_close(orc, g, x, wg, True)
+    check_close(orc, u, x, wu, True)
+    # the SiLU multiply is exact given g and u: bf16((g / (1 + exp(-g))) * u)
+    gf = orc.bf16_to_f32(g)
+    uf = orc.bf16_to_f32(u)
+    denom = (np.float32(1.0) + orc.expf(-gf)).astype(np.float32)
+    want_h = orc.f32_to_bf16(((gf / denom).astype(np.float32) * uf).astype(np.float32))
+    assert np.array_equal(h, want_h)
+    check_close(orc, host(so, np.uint16).reshape(tokens, W.HIDDEN), h, wd, True)
+    check_close(orc, host(sg, np.uint16).reshape(tokens, 1), x, wo, True)
+
+
+def test_moe_block_router_routed_shared(q38m, orc):
+    """The whole MoE block on the device -- router logits, the routed
+    experts, the shared expert and the gated combine -- equals the oracle's
+    step on the same logits and shared inputs, bit for bit."""
+    t = torch()
+    gfmt, dfmt = W.layer_policy(2, 0)
+    layer = Layer(q38m, orc, W.CONFIGS[2]["seed"], 0, gfmt, dfmt)
+    rng = np.random.default_rng(17)
+    tokens = 64
+    hidden = synth_hidden(q38m, 17, 1, tokens)
+    router = device(bf16_matrix(orc, rng, W.EXPERTS, W.HIDDEN, 0.02))
+    weights = [device(bf16_matrix(orc, rng, r, c, 0.02)) for r, c in
+               ((W.INTER, W.HIDDEN), (W.INTER, W.HIDDEN), (W.HIDDEN, W.INTER), (1, W.HIDDEN))]
+    logits = t.empty(tokens, W.EXPERTS, dtype=t.float32, device="cuda")
+    q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), tokens,
+              logits.data_ptr(), stream(), 0)
+    scratch = t.empty(q38m.lib().q38m_moe_shared_expert_scratch_bytes(tokens, W.INTER) // 2,
+                      dtype=t.int16, device="cuda")
+    so = t.empty(tokens, W.HIDDEN, dtype=t.int16, device="cuda")
+    sg = t.empty(tokens, dtype=t.int16, device="cuda")
+    q38m.call("q38m_moe_shared_expert_v1", hidden.data_ptr(), *[w.data_ptr() for w in weights],
+              tokens, W.INTER, scratch.data_ptr(), so.data_ptr(), sg.data_ptr(), stream(), 0)
+    ws = q38m.PrefillWorkspace_(tokens)
+    out = prefill(q38m, layer, hidden, logits, ws, shared=(so, sg))
+    ref = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn,
+                  logits=host(logits, np.float32), shared_output=host(so, np.uint16),
+                  shared_gate=host(sg, np.uint16))
+    assert np.array_equal(host(out, np.uint16), ref["output"])
