@@ -48,6 +48,12 @@ extern "C" {
 #define Q38M_PREFILL_SLAB_MAX_TOKENS 512u
 #define Q38M_ROUTE_PLAN_MAGIC_V1 0x52383351u /* "Q38R" */
 #define Q38M_ROUTE_PLAN_VERSION_V1 1u
+/* Chunks above the slab (no reference counterpart: the reference prefills
+ * in slabs of <= 512 tokens).  The chunk plan keeps the V1 layout, packed
+ * order and status codes with tasks of up to 128 rows and version 2. */
+#define Q38M_WIDE_MAX_TOKENS 32768u
+#define Q38M_WIDE_TASK_ROWS 128u
+#define Q38M_ROUTE_PLAN_VERSION_WIDE 2u
 /* Model widths this build's kernels are instantiated for. */
 #define Q38M_HIDDEN 2048u
 #define Q38M_INTERMEDIATE 512u
@@ -257,6 +263,44 @@ int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up,
                         const uint16_t* shared_output,
                         const uint16_t* shared_gate, uint16_t* output,
                         void* stream, int device);
+
+/* ---- one layer over a chunk of up to 32,768 tokens ------------------
+ * No reference counterpart: the reference runs run_moe per slab of <= 512
+ * tokens (cuda/cuda_backend.cu:1529-1559).  Same inputs, outputs and
+ * arithmetic as q38m_moe_prefill_v1 -- every token's output is
+ * bit-identical to running its slab through that entry point -- with the
+ * route plan built over the whole chunk, so each active expert's weights
+ * are streamed once per 128 routed rows instead of once per 16.  The
+ * plan's packed order is the V1 order (expert-major, stable in route
+ * index); its tasks are 128-row tiles (header version 2). */
+typedef struct q38m_wide_workspace_v1 {
+    q38m_prefill_workspace_v1 step; /* bound for max_tokens <= 32768 */
+    uint32_t* plan_scratch;         /* per-chunk expert counts */
+} q38m_wide_workspace_v1;
+
+/* Chunk plan alone: bytes of the plan views and of their build scratch. */
+uint32_t q38m_moe_wide_max_tasks(uint32_t tokens);
+size_t q38m_moe_wide_plan_bytes(uint32_t tokens);
+size_t q38m_moe_wide_plan_scratch_bytes(uint32_t tokens);
+int q38m_moe_wide_plan_storage(void* allocation, size_t allocation_bytes,
+                               uint32_t tokens, q38m_route_plan_v1* out);
+/* Builds the chunk plan of expert_ids [tokens][10] into a plan bound by
+ * q38m_moe_wide_plan_storage for >= tokens; scratch holds
+ * q38m_moe_wide_plan_scratch_bytes(tokens) bytes, 4-byte aligned. */
+int q38m_moe_build_route_plan_wide(const int32_t* expert_ids, uint32_t tokens,
+                                   const q38m_route_plan_v1* plan, uint32_t* scratch,
+                                   void* stream, int device);
+
+size_t q38m_moe_wide_workspace_bytes(uint32_t tokens);
+int q38m_moe_wide_workspace_bind(void* allocation, size_t bytes, uint32_t tokens,
+                                 q38m_wide_workspace_v1* out);
+int q38m_moe_prefill_wide_v1(const q38m_expert_weights_v1* gate_up,
+                             const q38m_expert_weights_v1* down,
+                             const uint16_t* hidden, const float* logits,
+                             uint32_t tokens, const q38m_wide_workspace_v1* ws,
+                             const uint16_t* shared_output,
+                             const uint16_t* shared_gate, uint16_t* output,
+                             void* stream, int device);
 
 /* ---- batch-1 decode: cuda_moe_routed_bf16 (include/q38/cuda_moe.h:
  * 17-29) tokens == 1 branch.  Streams only the top_k selected experts.

@@ -99,6 +99,10 @@ class PrefillWorkspace(ctypes.Structure):
                 ("mid_s", ctypes.c_void_p), ("route_output", ctypes.c_void_p)]
 
 
+class WideWorkspace(ctypes.Structure):
+    _fields_ = [("step", PrefillWorkspace), ("plan_scratch", ctypes.c_void_p)]
+
+
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
 _U64 = ctypes.c_uint64
@@ -130,6 +134,16 @@ SIGNATURES = {
     "q38m_moe_prefill_v1": (_INT, [ctypes.POINTER(ExpertWeights), ctypes.POINTER(ExpertWeights),
                                    _P, _P, _U32, ctypes.POINTER(PrefillWorkspace), _P, _P, _P,
                                    _P, _INT]),
+    "q38m_moe_wide_max_tasks": (_U32, [_U32]),
+    "q38m_moe_wide_plan_bytes": (_SZ, [_U32]),
+    "q38m_moe_wide_plan_scratch_bytes": (_SZ, [_U32]),
+    "q38m_moe_wide_plan_storage": (_INT, [_P, _SZ, _U32, ctypes.POINTER(RoutePlan)]),
+    "q38m_moe_build_route_plan_wide": (_INT, [_P, _U32, ctypes.POINTER(RoutePlan), _P, _P, _INT]),
+    "q38m_moe_wide_workspace_bytes": (_SZ, [_U32]),
+    "q38m_moe_wide_workspace_bind": (_INT, [_P, _SZ, _U32, ctypes.POINTER(WideWorkspace)]),
+    "q38m_moe_prefill_wide_v1": (_INT, [ctypes.POINTER(ExpertWeights),
+                                        ctypes.POINTER(ExpertWeights), _P, _P, _U32,
+                                        ctypes.POINTER(WideWorkspace), _P, _P, _P, _P, _INT]),
     "q38m_moe_decode_scratch_bytes": (_SZ, []),
     "q38m_moe_routed_decode_v1": (_INT, [ctypes.POINTER(ExpertWeights),
                                          ctypes.POINTER(ExpertWeights), _P, _P, _P, _U32, _P, _P,
@@ -283,6 +297,24 @@ class PrefillWorkspace_:
         self.ws = PrefillWorkspace()
         call("q38m_moe_prefill_workspace_bind", aligned, nbytes, max_tokens,
              ctypes.byref(self.ws))
+        self.max_tokens = max_tokens
+
+
+class WideWorkspace_:
+    """One device allocation bound as the chunk (up to 32,768 tokens) workspace."""
+
+    def __init__(self, max_tokens, device="cuda"):
+        torch = _torch()
+        nbytes = lib().q38m_moe_wide_workspace_bytes(max_tokens)
+        if nbytes == 0:
+            raise InvalidArgument(f"invalid chunk workspace token count {max_tokens}")
+        self.buffer = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
+        base = self.buffer.data_ptr()
+        aligned = (base + 255) // 256 * 256
+        self.wide = WideWorkspace()
+        call("q38m_moe_wide_workspace_bind", aligned, nbytes, max_tokens,
+             ctypes.byref(self.wide))
+        self.ws = self.wide.step
         self.max_tokens = max_tokens
 
 

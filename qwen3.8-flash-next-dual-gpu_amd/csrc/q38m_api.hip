@@ -95,21 +95,10 @@ uint32_t q38m_moe_prefill_routes_v1(uint32_t tokens) { return q38m::routes_v1(to
 
 uint32_t q38m_moe_prefill_max_tasks_v1(uint32_t tokens) { return q38m::max_tasks_v1(tokens); }
 
-size_t q38m_moe_route_plan_bytes_v1(uint32_t tokens) {
-    const size_t routes = q38m::routes_v1(tokens);
-    return sizeof(q38m_route_plan_header_v1) + Q38M_ROUTE_EXPERTS * sizeof(uint16_t) +
-           2u * (Q38M_ROUTE_EXPERTS + 1u) * sizeof(uint32_t) + 2u * routes * sizeof(uint32_t) +
-           static_cast<size_t>(q38m::max_tasks_v1(tokens)) * sizeof(q38m_task_v1);
-}
-
-int q38m_moe_route_plan_storage_v1(void* allocation, size_t allocation_bytes, uint32_t tokens,
-                                   q38m_route_plan_v1* out) {
-    if (!out || !allocation || tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS)
-        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE route-plan allocation");
-    if (allocation_bytes < q38m_moe_route_plan_bytes_v1(tokens))
-        return fail(Q38M_ERR_INVALID_ARGUMENT, "prefill MoE route-plan allocation is too small");
-    if (!aligned(allocation, alignof(q38m_route_plan_header_v1)))
-        return fail(Q38M_ERR_INVALID_ARGUMENT, "prefill MoE route-plan allocation is unaligned");
+namespace {
+// The V1 plan's views in one allocation (cuda/q38_moe_prefill.cu:635-663);
+// the chunk plan uses the same order with its own task count after them.
+void bind_plan_views(void* allocation, uint32_t tokens, q38m_route_plan_v1* out) {
     uint8_t* cursor = static_cast<uint8_t*>(allocation);
     const size_t routes = q38m::routes_v1(tokens);
     out->header = reinterpret_cast<q38m_route_plan_header_v1*>(cursor);
@@ -125,6 +114,26 @@ int q38m_moe_route_plan_storage_v1(void* allocation, size_t allocation_bytes, ui
     out->assignment_to_packed = reinterpret_cast<uint32_t*>(cursor);
     cursor += routes * sizeof(uint32_t);
     out->tasks = reinterpret_cast<q38m_task_v1*>(cursor);
+}
+
+}  // namespace
+
+size_t q38m_moe_route_plan_bytes_v1(uint32_t tokens) {
+    const size_t routes = q38m::routes_v1(tokens);
+    return sizeof(q38m_route_plan_header_v1) + Q38M_ROUTE_EXPERTS * sizeof(uint16_t) +
+           2u * (Q38M_ROUTE_EXPERTS + 1u) * sizeof(uint32_t) + 2u * routes * sizeof(uint32_t) +
+           static_cast<size_t>(q38m::max_tasks_v1(tokens)) * sizeof(q38m_task_v1);
+}
+
+int q38m_moe_route_plan_storage_v1(void* allocation, size_t allocation_bytes, uint32_t tokens,
+                                   q38m_route_plan_v1* out) {
+    if (!out || !allocation || tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE route-plan allocation");
+    if (allocation_bytes < q38m_moe_route_plan_bytes_v1(tokens))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "prefill MoE route-plan allocation is too small");
+    if (!aligned(allocation, alignof(q38m_route_plan_header_v1)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "prefill MoE route-plan allocation is unaligned");
+    bind_plan_views(allocation, tokens, out);
     g_last_error.clear();
     return Q38M_OK;
 }
@@ -359,6 +368,152 @@ int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert
         status = q38m::launch_combine(ws->route_output, ws->plan.assignment_to_packed,
                                       shared_output, shared_gate, tokens, output, s);
     return finish(status, "prefill MoE step");
+}
+
+// ---- chunks above the slab ----------------------------------------------
+
+uint32_t q38m_moe_wide_max_tasks(uint32_t tokens) {
+    if (tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS) return 0;
+    return q38m::max_tasks_wide(tokens);
+}
+
+size_t q38m_moe_wide_plan_bytes(uint32_t tokens) {
+    if (tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS) return 0;
+    const size_t routes = q38m::routes_v1(tokens);
+    return sizeof(q38m_route_plan_header_v1) + Q38M_ROUTE_EXPERTS * sizeof(uint16_t) +
+           2u * (Q38M_ROUTE_EXPERTS + 1u) * sizeof(uint32_t) + 2u * routes * sizeof(uint32_t) +
+           static_cast<size_t>(q38m::max_tasks_wide(tokens)) * sizeof(q38m_task_v1);
+}
+
+size_t q38m_moe_wide_plan_scratch_bytes(uint32_t tokens) {
+    if (tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS) return 0;
+    return static_cast<size_t>(q38m::wide_chunks(tokens)) * (Q38M_ROUTE_EXPERTS + 1u) *
+           sizeof(uint32_t);
+}
+
+int q38m_moe_wide_plan_storage(void* allocation, size_t allocation_bytes, uint32_t tokens,
+                               q38m_route_plan_v1* out) {
+    if (!out || !allocation || tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid chunk route-plan allocation");
+    if (allocation_bytes < q38m_moe_wide_plan_bytes(tokens))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "chunk route-plan allocation is too small");
+    if (!aligned(allocation, alignof(q38m_route_plan_header_v1)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "chunk route-plan allocation is unaligned");
+    bind_plan_views(allocation, tokens, out);
+    g_last_error.clear();
+    return Q38M_OK;
+}
+
+int q38m_moe_build_route_plan_wide(const int32_t* expert_ids, uint32_t tokens,
+                                   const q38m_route_plan_v1* plan, uint32_t* scratch,
+                                   void* stream, int device) {
+    if (!expert_ids || !valid_plan(plan) || !scratch || tokens == 0 ||
+        tokens > Q38M_WIDE_MAX_TOKENS || !aligned(scratch, 4))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid chunk route-plan input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_build_wide_plan(expert_ids, tokens, *plan, scratch,
+                                               as_stream(stream)),
+                  "chunk route-plan kernels");
+}
+
+size_t q38m_moe_wide_workspace_bytes(uint32_t tokens) {
+    if (tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS) return 0;
+    const size_t routes = q38m::routes_v1(tokens);
+    size_t bytes = align_up(q38m_moe_wide_plan_bytes(tokens), 256);
+    bytes += align_up(q38m_moe_wide_plan_scratch_bytes(tokens), 256);
+    bytes += align_up(routes * 4u, 256) * 2u;                                // ids, weights
+    bytes += align_up(static_cast<size_t>(tokens) * Q38M_HIDDEN, 256);      // xq
+    bytes += align_up(static_cast<size_t>(tokens) * 4u, 256);               // xs
+    bytes += align_up(routes * Q38M_INTERMEDIATE * 2u, 256);                // weighted_mid
+    bytes += align_up(routes * Q38M_INTERMEDIATE, 256);                     // mid_q
+    bytes += align_up(routes * 4u, 256);                                    // mid_s
+    bytes += align_up(routes * Q38M_HIDDEN * 4u, 256);                      // route_output
+    return bytes;
+}
+
+int q38m_moe_wide_workspace_bind(void* allocation, size_t bytes, uint32_t tokens,
+                                 q38m_wide_workspace_v1* out) {
+    if (!allocation || !out || tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS ||
+        bytes < q38m_moe_wide_workspace_bytes(tokens) || !aligned(allocation, 256))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid chunk workspace allocation");
+    const size_t routes = q38m::routes_v1(tokens);
+    uint8_t* cursor = static_cast<uint8_t*>(allocation);
+    q38m_prefill_workspace_v1& w = out->step;
+    bind_plan_views(cursor, tokens, &w.plan);
+    cursor += align_up(q38m_moe_wide_plan_bytes(tokens), 256);
+    out->plan_scratch = reinterpret_cast<uint32_t*>(cursor);
+    cursor += align_up(q38m_moe_wide_plan_scratch_bytes(tokens), 256);
+    w.max_tokens = tokens;
+    w.expert_ids = reinterpret_cast<int32_t*>(cursor);
+    cursor += align_up(routes * 4u, 256);
+    w.expert_weights = reinterpret_cast<float*>(cursor);
+    cursor += align_up(routes * 4u, 256);
+    w.xq = reinterpret_cast<int8_t*>(cursor);
+    cursor += align_up(static_cast<size_t>(tokens) * Q38M_HIDDEN, 256);
+    w.xs = reinterpret_cast<float*>(cursor);
+    cursor += align_up(static_cast<size_t>(tokens) * 4u, 256);
+    w.weighted_mid = reinterpret_cast<uint16_t*>(cursor);
+    cursor += align_up(routes * Q38M_INTERMEDIATE * 2u, 256);
+    w.mid_q = reinterpret_cast<int8_t*>(cursor);
+    cursor += align_up(routes * Q38M_INTERMEDIATE, 256);
+    w.mid_s = reinterpret_cast<float*>(cursor);
+    cursor += align_up(routes * 4u, 256);
+    w.route_output = reinterpret_cast<float*>(cursor);
+    g_last_error.clear();
+    return Q38M_OK;
+}
+
+int q38m_moe_prefill_wide_v1(const q38m_expert_weights_v1* gate_up,
+                             const q38m_expert_weights_v1* down, const uint16_t* hidden,
+                             const float* logits, uint32_t tokens,
+                             const q38m_wide_workspace_v1* wide,
+                             const uint16_t* shared_output, const uint16_t* shared_gate,
+                             uint16_t* output, void* stream, int device) {
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (int rc = check_weights(down, false)) return rc;
+    if (!wide || !wide->plan_scratch)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid chunk MoE workspace");
+    const q38m_prefill_workspace_v1* ws = &wide->step;
+    if (!hidden || !output || tokens == 0 || tokens > ws->max_tokens ||
+        tokens > Q38M_WIDE_MAX_TOKENS || !valid_plan(&ws->plan) || !ws->expert_ids ||
+        !ws->expert_weights || !ws->xq || !ws->xs || !ws->weighted_mid || !ws->mid_q ||
+        !ws->mid_s || !ws->route_output ||
+        (shared_output == nullptr) != (shared_gate == nullptr) || !aligned(hidden, 16) ||
+        !aligned(output, 16) || (logits && !aligned(logits, 16)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid chunk MoE step input");
+    if (int rc = select_device(device)) return rc;
+    const hipStream_t s = as_stream(stream);
+    const uint32_t routes = q38m::routes_v1(tokens);
+    const uint32_t tasks = q38m::max_tasks_wide(tokens);
+    hipError_t status = hipSuccess;
+    if (logits)
+        status = q38m::launch_route_quantize(logits, hidden, tokens, Q38M_ROUTE_TOPK,
+                                             ws->expert_ids, ws->expert_weights, ws->xq, ws->xs,
+                                             s);
+    else
+        status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws->xq, ws->xs, s);
+    if (status == hipSuccess)
+        status = q38m::launch_build_wide_plan(ws->expert_ids, tokens, ws->plan,
+                                              wide->plan_scratch, s);
+    if (status == hipSuccess)
+        status = q38m::launch_gate_up_w4g32_wide(gate_up->data, gate_up->scales, ws->xq, ws->xs,
+                                                 ws->plan.packed_assignment, ws->expert_weights,
+                                                 ws->plan.tasks, tasks, ws->weighted_mid, s);
+    if (status == hipSuccess)
+        status = q38m::launch_quantize_rows(ws->weighted_mid, routes, Q38M_INTERMEDIATE,
+                                            ws->mid_q, ws->mid_s, s);
+    if (status == hipSuccess)
+        status = down->format == Q38M_FORMAT_W8_SYM
+                     ? q38m::launch_down_w8pc_wide(down->data, down->scales, ws->mid_q,
+                                                   ws->mid_s, ws->plan.tasks, tasks,
+                                                   ws->route_output, s)
+                     : q38m::launch_down_w4g32_wide(down->data, down->scales, ws->mid_q,
+                                                    ws->mid_s, ws->plan.tasks, tasks,
+                                                    ws->route_output, s);
+    if (status == hipSuccess)
+        status = q38m::launch_combine(ws->route_output, ws->plan.assignment_to_packed,
+                                      shared_output, shared_gate, tokens, output, s);
+    return finish(status, "chunk MoE step");
 }
 
 size_t q38m_moe_decode_scratch_bytes(void) { return q38m::decode_scratch_bytes(); }

@@ -25,6 +25,31 @@ inline uint32_t max_tasks_v1(uint32_t tokens) {
     return initially + (routes - initially) / kMmqM;
 }
 
+// chunks above the slab (q38m_wide.hip): 128-row tasks, plans built from
+// per-chunk expert histograms of kWideChunkRoutes routes each
+constexpr uint32_t kWideChunkRoutes = 2048;
+inline uint32_t max_tasks_wide(uint32_t tokens) {
+    const uint32_t routes = routes_v1(tokens);
+    const uint32_t initially = routes < kExperts ? routes : kExperts;
+    return initially + (routes - initially) / Q38M_WIDE_TASK_ROWS;
+}
+uint32_t wide_chunks(uint32_t tokens);
+// chunk_counts: wide_chunks(tokens) * 513 uint32 of scratch
+hipError_t launch_build_wide_plan(const int32_t* ids, uint32_t tokens,
+                                  const q38m_route_plan_v1& plan, uint32_t* chunk_counts,
+                                  hipStream_t stream);
+hipError_t launch_gate_up_w4g32_wide(const void* data, const void* scales, const int8_t* xq,
+                                     const float* xs, const uint32_t* packed,
+                                     const float* route_weights, const q38m_task_v1* tasks,
+                                     uint32_t task_count, uint16_t* weighted_mid,
+                                     hipStream_t stream);
+hipError_t launch_down_w8pc_wide(const void* data, const void* scales, const int8_t* mid_q,
+                                 const float* mid_s, const q38m_task_v1* tasks,
+                                 uint32_t task_count, float* route_output, hipStream_t stream);
+hipError_t launch_down_w4g32_wide(const void* data, const void* scales, const int8_t* mid_q,
+                                  const float* mid_s, const q38m_task_v1* tasks,
+                                  uint32_t task_count, float* route_output, hipStream_t stream);
+
 // routing (q38m_routing.hip)
 hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
                        uint32_t tokens, uint32_t experts, uint32_t top_k,

@@ -1,0 +1,623 @@
+// Chunks above the 512-token slab: one MoE layer over up to 32,768 tokens
+// in a single pass, so that every active expert's weights are streamed once
+// per 128 routed rows instead of once per 16.  The reference prefills in
+// slabs of at most 512 tokens (include/q38/cuda_moe_prefill.h:14, the V1
+// plan); this path keeps the V1 plan's packed order (expert-major, stable
+// in route index, q38_moe_prefill.cu:192-262) and per-route arithmetic, so
+// every route's weighted_mid and route_output row and every token's output
+// are bit-identical to the slab path's, and changes only the task height
+// (128 rows) and how the plan is built (three launches instead of one
+// workgroup).
+//
+// Plan: (1) per-chunk expert histograms, (2) one workgroup scans them into
+// expert offsets, per-chunk bases and 128-row tasks, (3) one wave per chunk
+// assigns stable positions with an LDS table of equal-id lane masks.
+//
+// GEMMs: the slab kernels' decomposition (gate/up: a workgroup of 8 waves
+// covers 8 gate/up tile pairs of one task; down: 16-channel output tiles)
+// with up to 8 MFMA row tiles per weight fragment.  The gate/up chain costs
+// a v_cvt and a v_fma per accumulator element and group, so at 128 rows the
+// kernel is VALU-bound (~1/4 of int8 MFMA peak); down W8 is MFMA/HBM-bound.
+#include "q38m_device.h"
+#include "q38m_internal.h"
+
+namespace q38m {
+namespace {
+
+constexpr uint32_t kWideRows = Q38M_WIDE_TASK_ROWS;
+constexpr uint32_t kRowTiles = kWideRows / 16u;
+constexpr uint32_t kCountSlots = kExperts + 1u;  // slot 512 counts invalid ids
+
+// ---- plan -------------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void wide_count_kernel(const int32_t* __restrict__ ids,
+                                                         uint32_t routes,
+                                                         uint32_t* __restrict__ chunk_counts) {
+    __shared__ uint32_t hist[kCountSlots];
+    for (uint32_t i = threadIdx.x; i < kCountSlots; i += 256u) hist[i] = 0u;
+    __syncthreads();
+    const uint32_t begin = blockIdx.x * kWideChunkRoutes;
+    const uint32_t end = min(begin + kWideChunkRoutes, routes);
+    for (uint32_t a = begin + threadIdx.x; a < end; a += 256u) {
+        const int32_t id = ids[a];
+        const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
+        atomicAdd(&hist[valid ? static_cast<uint32_t>(id) : kExperts], 1u);
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < kCountSlots; i += 256u)
+        chunk_counts[static_cast<size_t>(blockIdx.x) * kCountSlots + i] = hist[i];
+}
+
+// One workgroup of 512 threads, thread e = expert e.  Turns the per-chunk
+// counts into per-chunk bases within each expert's segment (in place) and
+// writes the plan's counts, offsets, task offsets, tasks and header.
+__global__ __launch_bounds__(512) void wide_scan_kernel(uint32_t* __restrict__ chunk_counts,
+                                                        uint32_t chunks, uint32_t tokens,
+                                                        q38m_route_plan_v1 plan,
+                                                        uint32_t max_tasks) {
+    __shared__ uint32_t wave_totals[2][8];
+    __shared__ uint32_t wave_active[8];
+    __shared__ uint32_t offsets[kExperts + 1u];
+    __shared__ uint32_t task_offsets[kExperts + 1u];
+    __shared__ uint32_t invalid;
+    const uint32_t e = threadIdx.x;
+    const uint32_t lane = e & 63u;
+    const uint32_t wave = e >> 6;
+    const uint32_t routes = tokens * kTopK;
+
+    // 1. running count of expert e over the chunks, in chunk order; each
+    // chunk's slot becomes the expert's count in the chunks before it.  The
+    // loads of 32 chunks are issued before their sums.
+    uint32_t count = 0;
+    for (uint32_t c0 = 0; c0 < chunks; c0 += 32u) {
+        uint32_t v[32];
+#pragma unroll
+        for (uint32_t j = 0; j < 32u; ++j)
+            v[j] = c0 + j < chunks ? chunk_counts[static_cast<size_t>(c0 + j) * kCountSlots + e]
+                                   : 0u;
+#pragma unroll
+        for (uint32_t j = 0; j < 32u; ++j) {
+            if (c0 + j < chunks)
+                chunk_counts[static_cast<size_t>(c0 + j) * kCountSlots + e] = count;
+            count += v[j];
+        }
+    }
+    // invalid ids: wave 0 sums slot 512 of every chunk
+    if (wave == 0u) {
+        uint32_t bad = 0;
+        for (uint32_t c = lane; c < chunks; c += 64u)
+            bad += chunk_counts[static_cast<size_t>(c) * kCountSlots + kExperts];
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) bad += __shfl_xor(bad, offset, 64);
+        if (lane == 0u) invalid = bad;
+    }
+    plan.expert_counts[e] = static_cast<uint16_t>(count);
+
+    // 2. exclusive scans of counts and task counts over experts
+    const uint32_t tasks = (count + kWideRows - 1u) / kWideRows;
+    uint32_t inc_count = count, inc_tasks = tasks;
+#pragma unroll
+    for (int offset = 1; offset < 64; offset <<= 1) {
+        const uint32_t oc = __shfl_up(inc_count, offset, 64);
+        const uint32_t ot = __shfl_up(inc_tasks, offset, 64);
+        if (lane >= static_cast<uint32_t>(offset)) {
+            inc_count += oc;
+            inc_tasks += ot;
+        }
+    }
+    const uint64_t active = __ballot(count != 0u);
+    if (lane == 63u) {
+        wave_totals[0][wave] = inc_count;
+        wave_totals[1][wave] = inc_tasks;
+    }
+    if (lane == 0u) wave_active[wave] = __popcll(active);
+    __syncthreads();
+    uint32_t prefix_count = 0, prefix_tasks = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 8u; ++w) {
+        prefix_count += w < wave ? wave_totals[0][w] : 0u;
+        prefix_tasks += w < wave ? wave_totals[1][w] : 0u;
+    }
+    const uint32_t offset = prefix_count + inc_count - count;
+    const uint32_t task_offset = prefix_tasks + inc_tasks - tasks;
+    offsets[e] = offset;
+    task_offsets[e] = task_offset;
+    if (e == kExperts - 1u) {
+        offsets[kExperts] = prefix_count + inc_count;
+        task_offsets[kExperts] = prefix_tasks + inc_tasks;
+    }
+    __syncthreads();
+    plan.expert_offsets[e] = offset;
+    plan.expert_task_offsets[e] = task_offset;
+    if (e == 0u) {
+        plan.expert_offsets[kExperts] = offsets[kExperts];
+        plan.expert_task_offsets[kExperts] = task_offsets[kExperts];
+    }
+    const uint32_t total = offsets[kExperts];
+    const uint32_t task_total = task_offsets[kExperts];
+
+    // 3. tasks: 128-row tiles of each expert's segment, zero past the count
+    uint2* task_words = reinterpret_cast<uint2*>(plan.tasks);
+    for (uint32_t t = 0; t < tasks; ++t) {
+        const uint32_t remaining = count - t * kWideRows;
+        const uint32_t rows = remaining < kWideRows ? remaining : kWideRows;
+        task_words[task_offset + t] = make_uint2(offset + t * kWideRows, e | (rows << 16));
+    }
+    for (uint32_t t = task_total + e; t < max_tasks; t += 512u) task_words[t] = make_uint2(0u, 0u);
+    // packed positions no valid route fills hold their own index
+    for (uint32_t p = total + e; p < routes; p += 512u) plan.packed_assignment[p] = p;
+
+    if (e == 0u) {
+        uint32_t active_experts = 0;
+        for (uint32_t w = 0; w < 8u; ++w) active_experts += wave_active[w];
+        uint32_t status = Q38M_PLAN_OK;
+        if (invalid != 0u)
+            status = Q38M_PLAN_INVALID_EXPERT;
+        else if (total != routes || task_total > max_tasks)
+            status = Q38M_PLAN_INVALID_SHAPE;
+        q38m_route_plan_header_v1* h = plan.header;
+        h->magic = Q38M_ROUTE_PLAN_MAGIC_V1;
+        h->version = Q38M_ROUTE_PLAN_VERSION_WIDE;
+        h->tokens = tokens;
+        h->routes = routes;
+        h->active_experts = active_experts;
+        h->task_count = task_total;
+        h->status = status;
+        h->flags = 0u;
+        h->route_hash = 0u;
+        h->plan_hash = 0u;
+        h->reserved0 = 0u;
+        h->reserved1 = 0u;
+    }
+}
+
+// One wave per chunk walks its routes 64 at a time in route order, from
+// the expert offsets plus the chunk's bases within each segment.  Lanes
+// with equal ids find each other through an LDS table of lane masks (each
+// lane ORs its bit into its id's slot, reads the slot back, clears it; one
+// wave's LDS operations execute in order); the stable position is the
+// chunk's running base for the id plus the equal lanes below.
+__global__ __launch_bounds__(64) void wide_scatter_kernel(const int32_t* __restrict__ ids,
+                                                          uint32_t routes,
+                                                          const uint32_t* __restrict__ bases,
+                                                          q38m_route_plan_v1 plan) {
+    __shared__ uint32_t running[kExperts];
+    __shared__ unsigned long long table[kCountSlots];
+    const uint32_t lane = threadIdx.x;
+    const uint32_t* base = bases + static_cast<size_t>(blockIdx.x) * kCountSlots;
+    for (uint32_t i = lane; i < kExperts; i += 64u) running[i] = plan.expert_offsets[i] + base[i];
+    for (uint32_t i = lane; i < kCountSlots; i += 64u) table[i] = 0ull;
+    __syncthreads();
+    const uint64_t below_mask = (1ull << lane) - 1ull;
+    const uint32_t begin = blockIdx.x * kWideChunkRoutes;
+    const uint32_t end = min(begin + kWideChunkRoutes, routes);
+    for (uint32_t a0 = begin; a0 < end; a0 += 64u) {
+        const uint32_t a = a0 + lane;
+        const bool in = a < end;
+        const int32_t id = in ? ids[a] : -1;
+        const bool valid = in && id >= 0 && id < static_cast<int32_t>(kExperts);
+        const uint32_t slot = valid ? static_cast<uint32_t>(id) : kExperts;
+        atomicOr(&table[slot], 1ull << lane);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        const unsigned long long equal = table[slot];
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        table[slot] = 0ull;
+        const uint32_t below = __popcll(equal & below_mask);
+        const uint32_t run = valid ? running[valid ? slot : 0u] : 0u;
+        if (valid && below == 0u) running[slot] = run + __popcll(equal);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        if (valid) {
+            const uint32_t position = run + below;
+            plan.packed_assignment[position] = a;
+            plan.assignment_to_packed[a] = position;
+        } else if (in) {
+            plan.assignment_to_packed[a] = a;
+        }
+    }
+}
+
+// ---- gate/up ----------------------------------------------------------------
+
+struct QuadWeights {
+    uint4 g, u;    // gate and up tile data of one quad
+    uint2 sg, su;  // their fp16 scales (4 groups)
+};
+
+// Gate/up over a 128-row task: the slab kernel's chain (per group one
+// v_mfma_i32_16x16x32_i8 from a zero accumulator, then
+// y16 = fma(16*acc, s_g, y16) in group order) for every active 16-row tile
+// against the same unpacked weight fragment.  A is staged one quad (128 K)
+// at a time into a double-buffered LDS image [group][row tile][lane] of
+// 8-byte MFMA fragments; the next quad's rows are loaded into registers
+// while the current quad is multiplied.  Weights stream two quads ahead as
+// in the slab kernel.
+template <uint32_t H, uint32_t I, uint32_t kWaves>
+__global__ __launch_bounds__(kWaves * 64) void gate_up_w4g32_wide_kernel(
+    const uint4* __restrict__ w, const uint2* __restrict__ s,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
+    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    constexpr uint32_t kQuads = H / 128u;
+    constexpr uint32_t kTiles = 2u * I / 16u;
+    constexpr uint32_t kThreads = kWaves * 64u;
+    constexpr uint32_t kChunksPerQuad = kWideRows * 8u;  // 16-byte row pieces per quad
+    constexpr uint32_t kPerThread = kChunksPerQuad / kThreads;
+    static_assert(kChunksPerQuad % kThreads == 0u, "whole pieces per thread");
+    constexpr uint32_t kQuadFragments = 4u * kRowTiles * 64u;
+    __shared__ uint2 a_lds[2][kQuadFragments];
+
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t active_tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t gate_tile = blockIdx.x * kWaves + wave;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+
+    constexpr uint32_t kQuadWords = kTiles * 64u;
+    constexpr uint32_t kQuadScales = kTiles * 16u;
+    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u;
+    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u;
+    auto load = [&](uint32_t kq) {
+        const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
+        const uint32_t wi = k * kQuadWords + lane;
+        const uint32_t si = k * kQuadScales + n;
+        return QuadWeights{load_stream(wbase + wi), load_stream(wbase + wi + 64u),
+                           load_stream(sbase + si), load_stream(sbase + si + 16u)};
+    };
+
+    // Piece i of a quad: row r = i/8, 16-byte piece c = i%8 of the row's 128
+    // bytes, i.e. group c/2, lane groups 2(c%2) and 2(c%2)+1.  Rows past
+    // valid_rows stage zeros.
+    const uint4* row_src[kPerThread];
+    uint32_t lds_at[kPerThread];
+    bool alive[kPerThread];
+#pragma unroll
+    for (uint32_t u = 0; u < kPerThread; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / 8u, c = i % 8u;
+        alive[u] = r < rows;
+        const uint32_t token = alive[u] ? packed[p0 + r] / kTopK : 0u;
+        row_src[u] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token) * H) + c;
+        lds_at[u] = ((c >> 1) * kRowTiles + r / 16u) * 64u + (c & 1u) * 32u + r % 16u;
+    }
+    uint4 pieces[kPerThread];
+    auto load_a = [&](uint32_t kq) {
+#pragma unroll
+        for (uint32_t u = 0; u < kPerThread; ++u)
+            pieces[u] = alive[u] ? row_src[u][kq * 8u] : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto store_a = [&](uint32_t buffer) {
+#pragma unroll
+        for (uint32_t u = 0; u < kPerThread; ++u) {
+            a_lds[buffer][lds_at[u]] = make_uint2(pieces[u].x, pieces[u].y);
+            a_lds[buffer][lds_at[u] + 16u] = make_uint2(pieces[u].z, pieces[u].w);
+        }
+    };
+
+    float yg[kRowTiles][4], yu[kRowTiles][4];
+#pragma unroll
+    for (uint32_t t = 0; t < kRowTiles; ++t)
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) yg[t][i] = yu[t][i] = 0.0f;
+
+    auto multiply = [&](uint32_t kq, const QuadWeights& b) {
+        const uint2* abuf = a_lds[kq & 1u] + lane;
+        const v4i zero = {0, 0, 0, 0};
+        const uint32_t wgw[4] = {b.g.x, b.g.y, b.g.z, b.g.w};
+        const uint32_t wuw[4] = {b.u.x, b.u.y, b.u.z, b.u.w};
+        const uint32_t sgw[2] = {b.sg.x, b.sg.y};
+        const uint32_t suw[2] = {b.su.x, b.su.y};
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j) {
+            const long bg = unpack_w4x16(wgw[j]);
+            const long bu = unpack_w4x16(wuw[j]);
+            const float scale_g = f16_to_f32((j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu));
+            const float scale_u = f16_to_f32((j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu));
+#pragma unroll
+            for (uint32_t t = 0; t < kRowTiles; ++t) {
+                if (t >= active_tiles) break;
+                const long a = as_long(abuf[(j * kRowTiles + t) * 64u]);
+                const v4i dg = mfma_i8_16x16x32(a, bg, zero);
+                const v4i du = mfma_i8_16x16x32(a, bu, zero);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    yg[t][i] = __builtin_fmaf(static_cast<float>(dg[i]), scale_g, yg[t][i]);
+                    yu[t][i] = __builtin_fmaf(static_cast<float>(du[i]), scale_u, yu[t][i]);
+                }
+            }
+        }
+    };
+    // one quad: weights two ahead into the set just consumed, A one ahead
+    auto step = [&](uint32_t kq, const QuadWeights& cur, QuadWeights& refill) {
+        refill = load(kq + 2u);
+        if (kq + 1u < kQuads) load_a(kq + 1u);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(kq, cur);
+        if (kq + 1u < kQuads) store_a((kq + 1u) & 1u);
+        __syncthreads();
+    };
+
+    load_a(0);
+    QuadWeights r0 = load(0), r1 = load(1), r2;
+    store_a(0);
+    __syncthreads();
+    static_assert(kQuads % 3u == 1u, "three-set rotation plus one peeled quad");
+#pragma unroll 1
+    for (uint32_t kq = 0; kq + 3u < kQuads; kq += 3u) {
+        step(kq, r0, r2);
+        step(kq + 1u, r1, r0);
+        step(kq + 2u, r2, r1);
+    }
+    multiply(kQuads - 1u, r0);
+
+    const uint32_t channel = gate_tile * 16u + n;
+#pragma unroll
+    for (uint32_t t = 0; t < kRowTiles; ++t) {
+        if (t >= active_tiles) break;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 16u * t + 4u * q + i;
+            if (r >= rows) continue;
+            const uint32_t p = p0 + r;
+            const uint32_t a = packed[p];
+            const float st = xs[a / kTopK];
+            const float y_gate = (yg[t][i] * 0.0625f) * st;
+            const float y_up = (yu[t][i] * 0.0625f) * st;
+            mid[static_cast<size_t>(p) * I + channel] =
+                static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
+        }
+    }
+}
+
+// ---- down -------------------------------------------------------------------
+
+// Down, W8 per output channel, over a 128-row task: the task's mid rows
+// (contiguous in packed order, 64 KiB) are staged once into LDS as
+// [K block][row tile][lane] 16-byte MFMA fragments; each wave streams its
+// 16-channel tiles (8 KiB each, next tile prefetched) and runs one
+// v_mfma_i32_16x16x64_i8 per (K block, active row tile).
+// o = ((float)acc * ws[e][c]) * sm[r], as the slab kernel.
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
+__global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+    const int8_t* __restrict__ mq, const float* __restrict__ ms,
+    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    constexpr uint32_t kBlocks = I / 64u;
+    constexpr uint32_t kTiles = H / 16u;
+    constexpr uint32_t kThreads = kWaves * 64u;
+    constexpr uint32_t kPieces = kWideRows * (I / 16u);
+    static_assert(kPieces % kThreads == 0u, "whole pieces per thread");
+    __shared__ uint4 a_lds[kBlocks * kRowTiles * 64u];
+    __shared__ float row_scale[kWideRows];
+
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t active_tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+    const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
+    const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
+
+    uint4 b[kBlocks];
+#pragma unroll
+    for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = load_stream(wt + kb * 64u);
+
+    // Piece i: row r = i / (I/16), 16-byte piece c: K block c/4, lane group c%4.
+#pragma unroll
+    for (uint32_t u = 0; u < kPieces / kThreads; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / (I / 16u), c = i % (I / 16u);
+        const uint4 v = r < rows ? reinterpret_cast<const uint4*>(
+                                       mq + static_cast<size_t>(p0 + r) * I)[c]
+                                 : make_uint4(0u, 0u, 0u, 0u);
+        a_lds[((c >> 2) * kRowTiles + r / 16u) * 64u + (c & 3u) * 16u + r % 16u] = v;
+    }
+    if (threadIdx.x < kWideRows)
+        row_scale[threadIdx.x] = threadIdx.x < rows ? ms[p0 + threadIdx.x] : 0.0f;
+    __syncthreads();
+
+#pragma unroll 1
+    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
+        uint4 nb[kBlocks];
+        const uint4* next = wt + static_cast<size_t>(t + 1u < kTilesPerWave ? t + 1u : t) *
+                                     kBlocks * 64u;
+#pragma unroll
+        for (uint32_t kb = 0; kb < kBlocks; ++kb) nb[kb] = load_stream(next + kb * 64u);
+        __builtin_amdgcn_sched_barrier(0);
+        v4i acc[kRowTiles];
+#pragma unroll
+        for (uint32_t rt = 0; rt < kRowTiles; ++rt) acc[rt] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (uint32_t kb = 0; kb < kBlocks; ++kb)
+#pragma unroll
+            for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
+                if (rt >= active_tiles) break;
+                acc[rt] = mfma_i8_16x16x64(as_v4i(a_lds[(kb * kRowTiles + rt) * 64u + lane]),
+                                           as_v4i(b[kb]), acc[rt]);
+            }
+        const uint32_t channel = (tile0 + t) * 16u + n;
+        const float ws = f16_to_f32(s[static_cast<size_t>(e) * H + channel]);
+#pragma unroll
+        for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
+            if (rt >= active_tiles) break;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) {
+                const uint32_t r = 16u * rt + 4u * q + i;
+                if (r >= rows) continue;
+                out[static_cast<size_t>(p0 + r) * H + channel] =
+                    (static_cast<float>(acc[rt][i]) * ws) * row_scale[r];
+            }
+        }
+#pragma unroll
+        for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = nb[kb];
+    }
+}
+
+// Down, W4 group-32 (the all-W4 layer policy), over a 128-row task: the
+// gate/up group chain over K = I with every active row tile against the
+// same weight fragment; the mid rows are staged once in LDS as
+// [group][row tile][lane] 8-byte fragments.
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
+__global__ __launch_bounds__(kWaves * 64) void down_w4g32_wide_kernel(
+    const uint4* __restrict__ w, const uint2* __restrict__ s,
+    const int8_t* __restrict__ mq, const float* __restrict__ ms,
+    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    constexpr uint32_t kQuads = I / 128u;
+    constexpr uint32_t kGroups = I / 32u;
+    constexpr uint32_t kTiles = H / 16u;
+    constexpr uint32_t kThreads = kWaves * 64u;
+    constexpr uint32_t kPieces = kWideRows * (I / 16u);
+    static_assert(kPieces % kThreads == 0u, "whole pieces per thread");
+    __shared__ uint2 a_lds[kGroups * kRowTiles * 64u];
+    __shared__ float row_scale[kWideRows];
+
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t active_tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+
+    // Piece i: row r, 16-byte piece c = group c/2, lane groups 2(c%2), 2(c%2)+1.
+#pragma unroll
+    for (uint32_t u = 0; u < kPieces / kThreads; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / (I / 16u), c = i % (I / 16u);
+        const uint4 v = r < rows ? reinterpret_cast<const uint4*>(
+                                       mq + static_cast<size_t>(p0 + r) * I)[c]
+                                 : make_uint4(0u, 0u, 0u, 0u);
+        const uint32_t at = ((c >> 1) * kRowTiles + r / 16u) * 64u + (c & 1u) * 32u + r % 16u;
+        a_lds[at] = make_uint2(v.x, v.y);
+        a_lds[at + 16u] = make_uint2(v.z, v.w);
+    }
+    if (threadIdx.x < kWideRows)
+        row_scale[threadIdx.x] = threadIdx.x < rows ? ms[p0 + threadIdx.x] : 0.0f;
+    __syncthreads();
+
+    const v4i zero = {0, 0, 0, 0};
+    const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
+#pragma unroll 1
+    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
+        const uint32_t tile = tile0 + t;
+        const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 64u + lane;
+        const uint2* st = s + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 16u + n;
+        uint4 bq[kQuads];
+        uint2 cq[kQuads];
+#pragma unroll
+        for (uint32_t kq = 0; kq < kQuads; ++kq) {
+            bq[kq] = load_stream(wt + kq * kTiles * 64u);
+            cq[kq] = load_stream(st + kq * kTiles * 16u);
+        }
+        float y[kRowTiles][4];
+#pragma unroll
+        for (uint32_t rt = 0; rt < kRowTiles; ++rt)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) y[rt][i] = 0.0f;
+#pragma unroll
+        for (uint32_t kq = 0; kq < kQuads; ++kq) {
+            const uint32_t bw[4] = {bq[kq].x, bq[kq].y, bq[kq].z, bq[kq].w};
+            const uint32_t cw[2] = {cq[kq].x, cq[kq].y};
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j) {
+                const long bj = unpack_w4x16(bw[j]);
+                const uint32_t h = (j & 1u) ? (cw[j >> 1] >> 16) : (cw[j >> 1] & 0xffffu);
+                const float scale = f16_to_f32(h) * 0.0625f;
+                const uint32_t g = kq * 4u + j;
+#pragma unroll
+                for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
+                    if (rt >= active_tiles) break;
+                    const v4i d = mfma_i8_16x16x32(
+                        as_long(a_lds[(g * kRowTiles + rt) * 64u + lane]), bj, zero);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        y[rt][i] = __builtin_fmaf(static_cast<float>(d[i]), scale, y[rt][i]);
+                }
+            }
+        }
+        const uint32_t channel = tile * 16u + n;
+#pragma unroll
+        for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
+            if (rt >= active_tiles) break;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) {
+                const uint32_t r = 16u * rt + 4u * q + i;
+                if (r >= rows) continue;
+                out[static_cast<size_t>(p0 + r) * H + channel] = y[rt][i] * row_scale[r];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+uint32_t wide_chunks(uint32_t tokens) {
+    return (routes_v1(tokens) + kWideChunkRoutes - 1u) / kWideChunkRoutes;
+}
+
+hipError_t launch_build_wide_plan(const int32_t* ids, uint32_t tokens,
+                                  const q38m_route_plan_v1& plan, uint32_t* chunk_counts,
+                                  hipStream_t stream) {
+    const uint32_t routes = routes_v1(tokens);
+    const uint32_t chunks = wide_chunks(tokens);
+    wide_count_kernel<<<chunks, 256, 0, stream>>>(ids, routes, chunk_counts);
+    wide_scan_kernel<<<1, 512, 0, stream>>>(chunk_counts, chunks, tokens, plan,
+                                            max_tasks_wide(tokens));
+    wide_scatter_kernel<<<chunks, 64, 0, stream>>>(ids, routes, chunk_counts, plan);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate_up_w4g32_wide(const void* data, const void* scales, const int8_t* xq,
+                                     const float* xs, const uint32_t* packed,
+                                     const float* route_weights, const q38m_task_v1* tasks,
+                                     uint32_t task_count, uint16_t* weighted_mid,
+                                     hipStream_t stream) {
+    constexpr uint32_t kWaves = 8;
+    const dim3 grid(kInter / 16u / kWaves, task_count);
+    gate_up_w4g32_wide_kernel<kHidden, kInter, kWaves><<<grid, kWaves * 64u, 0, stream>>>(
+        static_cast<const uint4*>(data), static_cast<const uint2*>(scales), xq, xs, packed,
+        route_weights, tasks, weighted_mid);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_w8pc_wide(const void* data, const void* scales, const int8_t* mid_q,
+                                 const float* mid_s, const q38m_task_v1* tasks,
+                                 uint32_t task_count, float* route_output, hipStream_t stream) {
+    constexpr uint32_t kWaves = 8, kTilesPerWave = 4;
+    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
+    down_w8pc_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave>
+        <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(data),
+                                            static_cast<const uint16_t*>(scales), mid_q, mid_s,
+                                            tasks, route_output);
+    return hipGetLastError();
+}
+
+hipError_t launch_down_w4g32_wide(const void* data, const void* scales, const int8_t* mid_q,
+                                  const float* mid_s, const q38m_task_v1* tasks,
+                                  uint32_t task_count, float* route_output, hipStream_t stream) {
+    constexpr uint32_t kWaves = 8, kTilesPerWave = 4;
+    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
+    down_w4g32_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave>
+        <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(data),
+                                            static_cast<const uint2*>(scales), mid_q, mid_s,
+                                            tasks, route_output);
+    return hipGetLastError();
+}
+
+}  // namespace q38m

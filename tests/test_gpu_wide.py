@@ -1,0 +1,253 @@
+"""GPU parity of the chunk path (q38m_moe_prefill_wide_v1: one layer over up
+to 32,768 tokens with 128-row tasks).
+
+- the chunk plan against numpy's stable argsort of the expert ids (the
+  expert-major stable order of cuda/q38_moe_prefill.cu:192-262), its counts,
+  offsets, 128-row tasks and header; for T <= 512 its packed order, counts
+  and offsets equal the oracle's V1 plan; invalid ids fail closed as V1;
+- the whole step bit-exact against the slab path on the same inputs (every
+  token of a 4096-token Zipf chunk) and against the oracle token by token
+  on samples; at T = 512 every intermediate equals the slab path's;
+- all-W4 layers (W4 down), the gated shared term and ragged sizes.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from helpers import (Layer, W, host, prefill, stream, synth_hidden, synth_logits, torch,
+                     ws_arrays)
+
+pytestmark = pytest.mark.gpu
+
+ROWS = 128
+
+
+def wide_plan(q38m, ids_host, tokens):
+    """Builds the chunk plan on the device; returns its arrays."""
+    t = torch()
+    nbytes = q38m.lib().q38m_moe_wide_plan_bytes(tokens)
+    buf = t.full((nbytes + 256,), 0xA5, dtype=t.uint8, device="cuda")
+    base = (buf.data_ptr() + 255) // 256 * 256
+    plan = q38m.RoutePlan()
+    q38m.call("q38m_moe_wide_plan_storage", base, nbytes, tokens, ctypes.byref(plan))
+    scratch = t.empty(q38m.lib().q38m_moe_wide_plan_scratch_bytes(tokens) // 4,
+                      dtype=t.int32, device="cuda")
+    ids = t.from_numpy(np.ascontiguousarray(ids_host, dtype=np.int32).ravel()).cuda()
+    q38m.call("q38m_moe_build_route_plan_wide", ids.data_ptr(), tokens, ctypes.byref(plan),
+              scratch.data_ptr(), stream(), 0)
+    t.cuda.synchronize()
+    off = base - buf.data_ptr()
+    raw = buf[off:off + nbytes].cpu().numpy()
+    routes = tokens * 10
+    max_tasks = q38m.lib().q38m_moe_wide_max_tasks(tokens)
+
+    def take(ptr, count, dtype):
+        start = ptr - base
+        return raw[start:start + count * np.dtype(dtype).itemsize].view(dtype)
+
+    header = take(plan.header, 16, np.uint32)
+    return {
+        "magic": header[0], "version": header[1], "tokens": header[2], "routes": header[3],
+        "active": header[4], "task_count": header[5], "status": header[6],
+        "counts": take(plan.expert_counts, 512, np.uint16),
+        "offsets": take(plan.expert_offsets, 513, np.uint32),
+        "task_offsets": take(plan.expert_task_offsets, 513, np.uint32),
+        "packed": take(plan.packed_assignment, routes, np.uint32),
+        "inverse": take(plan.assignment_to_packed, routes, np.uint32),
+        "tasks": take(plan.tasks, 2 * max_tasks, np.uint32).reshape(max_tasks, 2),
+        "max_tasks": max_tasks,
+    }
+
+
+def expected_plan(ids_host, tokens):
+    """The chunk plan restated with numpy: stable argsort by expert id,
+    128-row tiles of each expert's segment."""
+    flat = np.ascontiguousarray(ids_host, dtype=np.int64).ravel()
+    valid = (flat >= 0) & (flat < 512)
+    order = np.argsort(np.where(valid, flat, 1 << 20), kind="stable")[:valid.sum()]
+    counts = np.bincount(flat[valid], minlength=512)
+    offsets = np.concatenate([[0], np.cumsum(counts)])
+    ntasks = (counts + ROWS - 1) // ROWS
+    task_offsets = np.concatenate([[0], np.cumsum(ntasks)])
+    tasks = []
+    for e in range(512):
+        for k in range(ntasks[e]):
+            rows = min(ROWS, counts[e] - k * ROWS)
+            tasks.append((offsets[e] + k * ROWS, e | (rows << 16)))
+    return order, counts, offsets, task_offsets, np.array(tasks, dtype=np.uint32).reshape(-1, 2)
+
+
+def zipf_ids(seed, tokens, s=1.1):
+    rng = np.random.default_rng(seed)
+    p = 1.0 / np.arange(1, 513) ** s
+    p /= p.sum()
+    perm = rng.permutation(512)
+    out = np.empty((tokens, 10), np.int32)
+    for t_ in range(tokens):
+        out[t_] = perm[rng.choice(512, 10, replace=False, p=p)]
+    return out
+
+
+@pytest.mark.parametrize("tokens,kind", [(1, "uniform"), (3, "uniform"), (512, "uniform"),
+                                         (2053, "zipf"), (4096, "zipf"), (32768, "uniform")])
+def test_wide_plan_matches_stable_sort(q38m, orc, tokens, kind):
+    rng = np.random.default_rng(tokens)
+    if kind == "zipf":
+        ids = zipf_ids(tokens, tokens)
+    else:
+        ids = np.stack([rng.choice(512, 10, replace=False) for _ in range(tokens)]).astype(np.int32)
+    got = wide_plan(q38m, ids, tokens)
+    order, counts, offsets, task_offsets, tasks = expected_plan(ids, tokens)
+    routes = tokens * 10
+    assert got["magic"] == 0x52383351 and got["version"] == 2 and got["status"] == 0
+    assert got["tokens"] == tokens and got["routes"] == routes
+    assert got["active"] == (counts > 0).sum()
+    assert np.array_equal(got["packed"], order)
+    assert np.array_equal(got["inverse"][order], np.arange(routes))
+    assert np.array_equal(got["counts"], counts)
+    assert np.array_equal(got["offsets"], offsets)
+    assert np.array_equal(got["task_offsets"], task_offsets)
+    assert got["task_count"] == len(tasks) <= got["max_tasks"]
+    assert np.array_equal(got["tasks"][:len(tasks)], tasks)
+    assert not got["tasks"][len(tasks):].any()
+    if tokens <= 512:
+        v1 = orc.parse_plan(orc.build_plan(ids.ravel(), tokens), tokens)
+        assert np.array_equal(got["packed"], v1["packed"])
+        assert np.array_equal(got["inverse"], v1["inverse"])
+
+
+def test_wide_plan_invalid_ids_fail_closed(q38m):
+    tokens = 300
+    ids = ((np.arange(tokens * 10) * 19 + 5) % 512).astype(np.int32)
+    ids[4] = -1
+    ids[2500] = 600
+    got = wide_plan(q38m, ids, tokens)
+    assert got["status"] == 1
+    valid = (ids >= 0) & (ids < 512)
+    order = np.argsort(np.where(valid, ids, 1 << 20), kind="stable")[:valid.sum()]
+    nvalid = valid.sum()
+    assert np.array_equal(got["packed"][:nvalid], order)
+    assert np.array_equal(got["packed"][nvalid:], np.arange(nvalid, tokens * 10))
+    assert got["inverse"][4] == 4 and got["inverse"][2500] == 2500
+
+
+def prefill_wide(q38m, layer, hidden, logits, ws, output=None, shared=None):
+    t = torch()
+    tokens = hidden.shape[0]
+    if output is None:
+        output = t.empty(tokens, W.HIDDEN, dtype=t.int16, device="cuda")
+    so, sg = (None, None) if shared is None else shared
+    q38m.call("q38m_moe_prefill_wide_v1", ctypes.byref(layer.gu.desc),
+              ctypes.byref(layer.dn.desc), hidden.data_ptr(),
+              None if logits is None else logits.data_ptr(), tokens, ctypes.byref(ws.wide),
+              None if so is None else so.data_ptr(), None if sg is None else sg.data_ptr(),
+              output.data_ptr(), stream(), 0)
+    return output
+
+
+@pytest.fixture(scope="module")
+def wide_layers(q38m, orc):
+    cache = {}
+
+    def get(config, layer=0):
+        key = (config, layer)
+        if key not in cache:
+            gfmt, dfmt = W.layer_policy(config, layer)
+            cache[key] = Layer(q38m, orc, W.CONFIGS[config]["seed"], layer, gfmt, dfmt)
+        return cache[key]
+
+    yield get
+    cache.clear()
+
+
+def test_wide_slab_equals_v1_with_intermediates(q38m, orc, wide_layers):
+    """At T = 512 the chunk plan's packed order is the V1 order, so every
+    intermediate of the chunk path equals the slab path's."""
+    layer = wide_layers(2)
+    seed = W.CONFIGS[2]["seed"]
+    hidden = synth_hidden(q38m, seed, 7, 512)
+    logits = synth_logits(q38m, seed, 8, 512)
+    ws1 = q38m.PrefillWorkspace_(512)
+    out1 = prefill(q38m, layer, hidden, logits, ws1)
+    wsw = q38m.WideWorkspace_(512)
+    outw = prefill_wide(q38m, layer, hidden, logits, wsw)
+    a, b = ws_arrays(ws1, 512), ws_arrays(wsw, 512)
+    for name in ("ids", "xq", "weighted_mid", "mid_q", "route_output"):
+        assert np.array_equal(a[name], b[name]), name
+    assert np.array_equal(a["weights"].view(np.uint32), b["weights"].view(np.uint32))
+    assert np.array_equal(host(out1, np.uint16), host(outw, np.uint16))
+
+
+def test_wide_config4_chunk(q38m, orc, wide_layers):
+    """Config 4 (4096 tokens, Zipf s=1.1) in one chunk: every token equals
+    the slab path's result, and a sample equals the oracle token by token."""
+    t = torch()
+    layer = wide_layers(4)
+    seed = W.CONFIGS[4]["seed"]
+    bias = W.bias_for(4, 0)
+    hidden = synth_hidden(q38m, seed, 1, 4096)
+    logits = synth_logits(q38m, seed, 2, 4096, bias)
+    wsw = q38m.WideWorkspace_(4096)
+    outw = prefill_wide(q38m, layer, hidden, logits, wsw)
+    ws1 = q38m.PrefillWorkspace_(512)
+    out1 = t.empty(4096, W.HIDDEN, dtype=t.int16, device="cuda")
+    for s in range(8):
+        sl = slice(s * 512, (s + 1) * 512)
+        prefill(q38m, layer, hidden[sl], logits[sl], ws1, output=out1[sl])
+    got = host(outw, np.uint16)
+    assert np.array_equal(got, host(out1, np.uint16))
+    rng = np.random.default_rng(44)
+    sample = np.sort(rng.choice(4096, 64, replace=False))
+    ref = orc.moe(host(hidden, np.uint16)[sample], layer.host_gu, layer.host_dn,
+                  logits=host(logits, np.float32)[sample], grouped=False)
+    assert np.array_equal(got[sample], ref["output"])
+    # hot experts really span several 128-row tasks
+    counts = wide_plan_counts(wsw)
+    assert counts.max() > 2 * ROWS
+
+
+def wide_plan_counts(wsw):
+    torch().cuda.synchronize()
+    base = wsw.buffer.data_ptr()
+    start = wsw.ws.plan.expert_counts - base
+    return wsw.buffer[start:start + 1024].cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("tokens", [1, 77, 1000])
+def test_wide_all_w4_layer_and_shared(q38m, orc, wide_layers, tokens):
+    """Config 5's all-W4 layer policy (W4 g32 down) with the gated shared
+    term, at ragged chunk sizes, against the oracle token by token."""
+    t = torch()
+    layer = wide_layers(5, 0)
+    seed = W.CONFIGS[5]["seed"]
+    hidden = synth_hidden(q38m, seed, 11, tokens)
+    logits = synth_logits(q38m, seed, 12, tokens, W.bias_for(5, 0))
+    so = synth_hidden(q38m, seed, 13, tokens)
+    sg = t.empty(tokens, dtype=t.int16, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, 14, tokens, sg)
+    wsw = q38m.WideWorkspace_(tokens)
+    out = prefill_wide(q38m, layer, hidden, logits, wsw, shared=(so, sg))
+    sample = np.arange(tokens) if tokens <= 100 else np.arange(0, tokens, 7)
+    ref = orc.moe(host(hidden, np.uint16)[sample], layer.host_gu, layer.host_dn,
+                  logits=host(logits, np.float32)[sample],
+                  shared_output=host(so, np.uint16)[sample],
+                  shared_gate=host(sg, np.uint16)[sample], grouped=False)
+    assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
+
+
+def test_wide_config5_layer_full_chunk(q38m, orc, wide_layers):
+    """One config-5 layer (W4/W8) over all 32,768 tokens of the stack in one
+    chunk, against the oracle on a 64-token sample."""
+    layer = wide_layers(5, 1)
+    seed = W.CONFIGS[5]["seed"]
+    tokens = 32768
+    _, _, h_tag, l_tag = W.layer_tags(1)
+    hidden = synth_hidden(q38m, seed, h_tag, tokens)
+    logits = synth_logits(q38m, seed, l_tag, tokens, W.bias_for(5, 1))
+    wsw = q38m.WideWorkspace_(tokens)
+    out = prefill_wide(q38m, layer, hidden, logits, wsw)
+    sample = np.arange(0, tokens, 512) + np.arange(64) % 7
+    ref = orc.moe(host(hidden[sample.tolist()], np.uint16), layer.host_gu, layer.host_dn,
+                  logits=host(logits[sample.tolist()], np.float32), grouped=False)
+    assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
