@@ -51,6 +51,7 @@ def main():
     parser.add_argument("--no-decode", action="store_true")
     parser.add_argument("--no-quantizer", action="store_true")
     parser.add_argument("--no-dense", action="store_true")
+    parser.add_argument("--no-chunks", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
@@ -238,6 +239,9 @@ def main():
     if not args.no_dense:
         result["router_shared"] = bench_router_shared(q38m, W, torch, hidden, args.steps)
 
+    if not args.no_chunks:
+        result["chunks"] = bench_chunks(q38m, W, torch)
+
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
                                               T)
@@ -387,6 +391,81 @@ def bench_router_shared(q38m, W, torch, hidden, steps):
                      "GBps": round(nbytes / s / 1e9, 1),
                      "hbm_frac": round(nbytes / s / 1e9 / HBM_PEAK_GBPS, 4)}
     out["tokens"] = T
+    return out
+
+
+def bench_chunks(q38m, W, torch):
+    """Workloads above the slab through q38m_moe_prefill_wide_v1 (one plan
+    over the whole chunk, 128-row tasks): config 4 (4096 tokens, Zipf 1.1)
+    and one config-5 layer of each policy over all 32,768 tokens of the
+    stack (Zipf 0.8).  The same tokens through the slab entry point
+    (q38m_moe_prefill_v1, 512 tokens per call) are timed beside it; both
+    results are compared token for token.  ops = 2*(2*I*H + H*I) per route."""
+    sh = torch.cuda.current_stream().cuda_stream
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    out = {}
+    cases = (("config4", 4, 0, 4096, 10), ("config5_layer_w4_w8", 5, 1, 32768, 5),
+             ("config5_layer_w4_w4", 5, 0, 32768, 5))
+    for name, config, layer_index, tokens, reps in cases:
+        spec = W.CONFIGS[config]
+        seed = spec["seed"]
+        gfmt, dfmt = W.layer_policy(config, layer_index)
+        gu_tag, dn_tag, h_tag, l_tag = W.layer_tags(layer_index)
+        gu_rm = q38m.synth_weights(seed, gu_tag, fmt[gfmt[1]], gfmt[2], W.EXPERTS, 2 * W.INTER,
+                                   W.HIDDEN, gfmt[3])
+        dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dfmt[1]], dfmt[2], W.EXPERTS, W.HIDDEN,
+                                   W.INTER, dfmt[3])
+        gu, dn = q38m.repack(gu_rm, paired=True), q38m.repack(dn_rm)
+        del gu_rm, dn_rm
+        hidden = torch.empty(tokens, W.HIDDEN, dtype=torch.int16, device="cuda")
+        logits = torch.empty(tokens, W.EXPERTS, dtype=torch.float32, device="cuda")
+        bias = W.bias_for(config, layer_index)
+        bias_t = torch.tensor(bias, dtype=torch.float32, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, h_tag, hidden.numel(), hidden)
+        q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, l_tag, logits.numel(), logits, bias=bias_t)
+        wide = q38m.WideWorkspace_(tokens)
+        slab = q38m.PrefillWorkspace_(512)
+        out_w = torch.empty(tokens, W.HIDDEN, dtype=torch.int16, device="cuda")
+        out_s = torch.empty_like(out_w)
+
+        def run_wide():
+            q38m.call("q38m_moe_prefill_wide_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                      hidden.data_ptr(), logits.data_ptr(), tokens, ctypes.byref(wide.wide),
+                      None, None, out_w.data_ptr(), sh, 0)
+
+        def run_slabs():
+            for s0 in range(0, tokens, 512):
+                q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                          hidden[s0:].data_ptr(), logits[s0:].data_ptr(), 512,
+                          ctypes.byref(slab.ws), None, None, out_s[s0:].data_ptr(), sh, 0)
+
+        def timed(fn):
+            fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) * 1e3 / reps
+
+        wide_ms, slab_ms = timed(run_wide), timed(run_slabs)
+        same = bool(torch.equal(out_w, out_s))
+        base = wide.buffer.data_ptr()
+        start = wide.ws.plan.expert_counts - base
+        counts = wide.buffer[start:start + 1024].view(torch.int16).to(torch.int32) & 0xFFFF
+        active = int((counts > 0).sum())
+        ops = tokens * W.TOPK * W.ops_per_route()
+        weight_bytes = active * W.algorithmic_bytes_per_expert(gfmt, dfmt)
+        out[name] = {"tokens": tokens, "policy": f"{gfmt[0]}/{dfmt[0]}",
+                     "active_experts": active, "hottest_expert_routes": int(counts.max()),
+                     "wide_ms": round(wide_ms, 4), "wide_tok_s": round(tokens / wide_ms * 1e3, 1),
+                     "slab_ms": round(slab_ms, 4), "slab_tok_s": round(tokens / slab_ms * 1e3, 1),
+                     "speedup": round(slab_ms / wide_ms, 2),
+                     "wide_int8_mfma_frac": round(ops / (wide_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                                                  4),
+                     "active_weight_bytes": weight_bytes, "outputs_equal": same}
+        del gu, dn, hidden, logits, wide, slab, out_w, out_s
+        torch.cuda.empty_cache()
     return out
 
 

@@ -13,6 +13,10 @@
 // expert offsets, per-chunk bases and 128-row tasks, (3) one wave per chunk
 // assigns stable positions with an LDS table of equal-id lane masks.
 //
+// Weights are read with ordinary (cached) loads, unlike the slab kernels'
+// non-temporal streams: a hot expert's 128-row tasks run side by side and
+// share its weights through L2.
+//
 // GEMMs: the slab kernels' decomposition (gate/up: a workgroup of 8 waves
 // covers 8 gate/up tile pairs of one task; down: 16-channel output tiles)
 // with up to 8 MFMA row tiles per weight fragment.  The gate/up chain costs
@@ -226,64 +230,52 @@ struct QuadWeights {
     uint2 sg, su;  // their fp16 scales (4 groups)
 };
 
-// Gate/up over a 128-row task: the slab kernel's chain (per group one
-// v_mfma_i32_16x16x32_i8 from a zero accumulator, then
-// y16 = fma(16*acc, s_g, y16) in group order) for every active 16-row tile
-// against the same unpacked weight fragment.  A is staged one quad (128 K)
+// Gate/up over a task of up to 128 rows: the slab kernel's chain (per group
+// one v_mfma_i32_16x16x32_i8 from a zero accumulator, then
+// y16 = fma(16*acc, s_g, y16) in group order) for kTiles 16-row tiles
+// against the same unpacked weight fragment.  kTiles is a compile-time
+// count picked per task from its row count (8, 4, 2 or 1 tiles), so the
+// tile loop has no branches and the compiler interleaves one tile's MFMAs
+// with the previous tile's v_cvt/v_fma chain.  A is staged one quad (128 K)
 // at a time into a double-buffered LDS image [group][row tile][lane] of
-// 8-byte MFMA fragments; the next quad's rows are loaded into registers
-// while the current quad is multiplied.  Weights stream two quads ahead as
-// in the slab kernel.
-template <uint32_t H, uint32_t I, uint32_t kWaves>
-__global__ __launch_bounds__(kWaves * 64) void gate_up_w4g32_wide_kernel(
-    const uint4* __restrict__ w, const uint2* __restrict__ s,
+// 8-byte MFMA fragments, the next quad's rows loaded into registers while
+// the current quad is multiplied; weights run two quads ahead.
+template <uint32_t H, uint32_t I, uint32_t kThreads, uint32_t kTiles>
+__device__ __forceinline__ void gate_up_wide_rows(
+    const uint4* __restrict__ wbase, const uint2* __restrict__ sbase,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
-    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    uint16_t* __restrict__ mid, uint2 (*a_lds)[4u * kRowTiles * 64u], uint32_t rows,
+    uint32_t p0, uint32_t gate_tile) {
     constexpr uint32_t kQuads = H / 128u;
-    constexpr uint32_t kTiles = 2u * I / 16u;
-    constexpr uint32_t kThreads = kWaves * 64u;
-    constexpr uint32_t kChunksPerQuad = kWideRows * 8u;  // 16-byte row pieces per quad
-    constexpr uint32_t kPerThread = kChunksPerQuad / kThreads;
-    static_assert(kChunksPerQuad % kThreads == 0u, "whole pieces per thread");
-    constexpr uint32_t kQuadFragments = 4u * kRowTiles * 64u;
-    __shared__ uint2 a_lds[2][kQuadFragments];
-
-    const q38m_task_v1 task = tasks[blockIdx.y];
-    const uint32_t rows = task.valid_rows;
-    if (rows == 0u) return;
-    const uint32_t active_tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
+    constexpr uint32_t kTilesAll = 2u * I / 16u;
+    constexpr uint32_t kQuadWords = kTilesAll * 64u;
+    constexpr uint32_t kQuadScales = kTilesAll * 16u;
+    constexpr uint32_t kPieces = kTiles * 16u * 8u;  // 16-byte row pieces per quad
+    constexpr uint32_t kPerThread = (kPieces + kThreads - 1u) / kThreads;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
-    const uint32_t gate_tile = blockIdx.x * kWaves + wave;
-    const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
 
-    constexpr uint32_t kQuadWords = kTiles * 64u;
-    constexpr uint32_t kQuadScales = kTiles * 16u;
-    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u;
-    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u;
     auto load = [&](uint32_t kq) {
         const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
         const uint32_t wi = k * kQuadWords + lane;
         const uint32_t si = k * kQuadScales + n;
-        return QuadWeights{load_stream(wbase + wi), load_stream(wbase + wi + 64u),
-                           load_stream(sbase + si), load_stream(sbase + si + 16u)};
+        return QuadWeights{wbase[wi], wbase[wi + 64u], sbase[si], sbase[si + 16u]};
     };
 
-    // Piece i of a quad: row r = i/8, 16-byte piece c = i%8 of the row's 128
-    // bytes, i.e. group c/2, lane groups 2(c%2) and 2(c%2)+1.  Rows past
+    // Piece i: row r = i/8, 16-byte piece c = i%8 of the row's 128 bytes of
+    // the quad, i.e. group c/2, lane groups 2(c%2) and 2(c%2)+1.  Rows past
     // valid_rows stage zeros.
     const uint4* row_src[kPerThread];
     uint32_t lds_at[kPerThread];
-    bool alive[kPerThread];
+    bool alive[kPerThread], staged[kPerThread];
 #pragma unroll
     for (uint32_t u = 0; u < kPerThread; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
         const uint32_t r = i / 8u, c = i % 8u;
-        alive[u] = r < rows;
+        staged[u] = i < kPieces;
+        alive[u] = staged[u] && r < rows;
         const uint32_t token = alive[u] ? packed[p0 + r] / kTopK : 0u;
         row_src[u] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token) * H) + c;
         lds_at[u] = ((c >> 1) * kRowTiles + r / 16u) * 64u + (c & 1u) * 32u + r % 16u;
@@ -297,14 +289,15 @@ __global__ __launch_bounds__(kWaves * 64) void gate_up_w4g32_wide_kernel(
     auto store_a = [&](uint32_t buffer) {
 #pragma unroll
         for (uint32_t u = 0; u < kPerThread; ++u) {
+            if (!staged[u]) continue;
             a_lds[buffer][lds_at[u]] = make_uint2(pieces[u].x, pieces[u].y);
             a_lds[buffer][lds_at[u] + 16u] = make_uint2(pieces[u].z, pieces[u].w);
         }
     };
 
-    float yg[kRowTiles][4], yu[kRowTiles][4];
+    float yg[kTiles][4], yu[kTiles][4];
 #pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t)
+    for (uint32_t t = 0; t < kTiles; ++t)
 #pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) yg[t][i] = yu[t][i] = 0.0f;
 
@@ -315,23 +308,44 @@ __global__ __launch_bounds__(kWaves * 64) void gate_up_w4g32_wide_kernel(
         const uint32_t wuw[4] = {b.u.x, b.u.y, b.u.z, b.u.w};
         const uint32_t sgw[2] = {b.sg.x, b.sg.y};
         const uint32_t suw[2] = {b.su.x, b.su.y};
+        // A fragments of group j+1 are read from LDS while group j computes
+        long frag[2][kTiles];
+#pragma unroll
+        for (uint32_t t = 0; t < kTiles; ++t) frag[0][t] = as_long(abuf[t * 64u]);
 #pragma unroll
         for (uint32_t j = 0; j < 4u; ++j) {
+            if (j + 1u < 4u) {
+#pragma unroll
+                for (uint32_t t = 0; t < kTiles; ++t)
+                    frag[(j + 1u) & 1u][t] = as_long(abuf[((j + 1u) * kRowTiles + t) * 64u]);
+            }
+            const long* a = frag[j & 1u];
             const long bg = unpack_w4x16(wgw[j]);
             const long bu = unpack_w4x16(wuw[j]);
             const float scale_g = f16_to_f32((j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu));
             const float scale_u = f16_to_f32((j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu));
+            // tile t+1's MFMAs are issued before tile t's chain; scheduling
+            // barriers and an empty asm on each tile's accumulators keep
+            // that order, so two tiles' results are live at a time
+            v4i dg[2], du[2];
+            dg[0] = mfma_i8_16x16x32(a[0], bg, zero);
+            du[0] = mfma_i8_16x16x32(a[0], bu, zero);
 #pragma unroll
-            for (uint32_t t = 0; t < kRowTiles; ++t) {
-                if (t >= active_tiles) break;
-                const long a = as_long(abuf[(j * kRowTiles + t) * 64u]);
-                const v4i dg = mfma_i8_16x16x32(a, bg, zero);
-                const v4i du = mfma_i8_16x16x32(a, bu, zero);
+            for (uint32_t t = 0; t < kTiles; ++t) {
+                if (t + 1u < kTiles) {
+                    dg[(t + 1u) & 1u] = mfma_i8_16x16x32(a[t + 1u], bg, zero);
+                    du[(t + 1u) & 1u] = mfma_i8_16x16x32(a[t + 1u], bu, zero);
+                }
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    yg[t][i] = __builtin_fmaf(static_cast<float>(dg[i]), scale_g, yg[t][i]);
-                    yu[t][i] = __builtin_fmaf(static_cast<float>(du[i]), scale_u, yu[t][i]);
+                    yg[t][i] = __builtin_fmaf(static_cast<float>(dg[t & 1u][i]), scale_g, yg[t][i]);
+                    yu[t][i] = __builtin_fmaf(static_cast<float>(du[t & 1u][i]), scale_u, yu[t][i]);
                 }
+                // the chain is materialised here, not sunk past later tiles
+                asm volatile("" : "+v"(yg[t][0]), "+v"(yg[t][1]), "+v"(yg[t][2]), "+v"(yg[t][3]),
+                                  "+v"(yu[t][0]), "+v"(yu[t][1]), "+v"(yu[t][2]), "+v"(yu[t][3]));
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     };
@@ -360,8 +374,7 @@ __global__ __launch_bounds__(kWaves * 64) void gate_up_w4g32_wide_kernel(
 
     const uint32_t channel = gate_tile * 16u + n;
 #pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-        if (t >= active_tiles) break;
+    for (uint32_t t = 0; t < kTiles; ++t) {
 #pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) {
             const uint32_t r = 16u * t + 4u * q + i;
@@ -377,14 +390,106 @@ __global__ __launch_bounds__(kWaves * 64) void gate_up_w4g32_wide_kernel(
     }
 }
 
+template <uint32_t H, uint32_t I, uint32_t kWaves>
+__global__ __launch_bounds__(kWaves * 64)
+void gate_up_w4g32_wide_kernel(
+    const uint4* __restrict__ w, const uint2* __restrict__ s,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
+    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    constexpr uint32_t kQuads = H / 128u;
+    constexpr uint32_t kTilesAll = 2u * I / 16u;
+    constexpr uint32_t kThreads = kWaves * 64u;
+    __shared__ uint2 a_lds[2][4u * kRowTiles * 64u];
+
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t gate_tile = blockIdx.x * kWaves + wave;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+    // Paired quad-major layout: for quad kq the gate tile of pair p is slot
+    // 2p and its up tile slot 2p+1.
+    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTilesAll + 2u * gate_tile) * 64u;
+    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTilesAll + 2u * gate_tile) * 16u;
+    const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
+    if (tiles > 4u)
+        gate_up_wide_rows<H, I, kThreads, 8>(wbase, sbase, xq, xs, packed, route_weights, mid,
+                                             a_lds, rows, p0, gate_tile);
+    else if (tiles > 2u)
+        gate_up_wide_rows<H, I, kThreads, 4>(wbase, sbase, xq, xs, packed, route_weights, mid,
+                                             a_lds, rows, p0, gate_tile);
+    else if (tiles == 2u)
+        gate_up_wide_rows<H, I, kThreads, 2>(wbase, sbase, xq, xs, packed, route_weights, mid,
+                                             a_lds, rows, p0, gate_tile);
+    else
+        gate_up_wide_rows<H, I, kThreads, 1>(wbase, sbase, xq, xs, packed, route_weights, mid,
+                                             a_lds, rows, p0, gate_tile);
+}
+
 // ---- down -------------------------------------------------------------------
 
-// Down, W8 per output channel, over a 128-row task: the task's mid rows
-// (contiguous in packed order, 64 KiB) are staged once into LDS as
-// [K block][row tile][lane] 16-byte MFMA fragments; each wave streams its
-// 16-channel tiles (8 KiB each, next tile prefetched) and runs one
-// v_mfma_i32_16x16x64_i8 per (K block, active row tile).
-// o = ((float)acc * ws[e][c]) * sm[r], as the slab kernel.
+// Down, W8 per output channel, over a task of up to 128 rows: the mid rows
+// (contiguous in packed order) are staged once into LDS as [K block][row
+// tile][lane] 16-byte MFMA fragments.  Each wave owns kTilesPerWave
+// 16-channel output tiles and walks K in the outer loop: a K block's kRows
+// A fragments are read from LDS once and multiplied into every owned tile
+// (v_mfma_i32_16x16x64_i8), with the tiles' weight fragments two K blocks
+// ahead.  kRows (8, 4, 2 or 1 row tiles) is picked per task from its row
+// count.  o = ((float)acc * ws[e][c]) * sm[r], as the slab kernel.
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kRows>
+__device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
+                                                  const uint16_t* __restrict__ ws_row,
+                                                  const uint4* a_lds, const float* row_scale,
+                                                  uint32_t rows, uint32_t p0, uint32_t tile0,
+                                                  float* __restrict__ out) {
+    constexpr uint32_t kBlocks = I / 64u;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    v4i acc[kTilesPerWave][kRows];
+#pragma unroll
+    for (uint32_t t = 0; t < kTilesPerWave; ++t)
+#pragma unroll
+        for (uint32_t r = 0; r < kRows; ++r) acc[t][r] = v4i{0, 0, 0, 0};
+    // tile t's K block kb: wt[(t * kBlocks + kb) * 64]
+    uint4 wq[3][kTilesPerWave];
+    auto load_w = [&](uint32_t kb, uint4 (&dst)[kTilesPerWave]) {
+        const uint32_t k = kb < kBlocks ? kb : kBlocks - 1u;
+#pragma unroll
+        for (uint32_t t = 0; t < kTilesPerWave; ++t) dst[t] = wt[(t * kBlocks + k) * 64u];
+    };
+    load_w(0, wq[0]);
+    load_w(1, wq[1]);
+#pragma unroll
+    for (uint32_t kb = 0; kb < kBlocks; ++kb) {
+        load_w(kb + 2u, wq[(kb + 2u) % 3u]);
+        v4i a[kRows];
+#pragma unroll
+        for (uint32_t r = 0; r < kRows; ++r) a[r] = as_v4i(a_lds[(kb * kRowTiles + r) * 64u + lane]);
+#pragma unroll
+        for (uint32_t t = 0; t < kTilesPerWave; ++t)
+#pragma unroll
+            for (uint32_t r = 0; r < kRows; ++r)
+                acc[t][r] = mfma_i8_16x16x64(a[r], as_v4i(wq[kb % 3u][t]), acc[t][r]);
+    }
+#pragma unroll
+    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
+        const uint32_t channel = (tile0 + t) * 16u + n;
+        const float ws = f16_to_f32(ws_row[channel]);
+#pragma unroll
+        for (uint32_t r = 0; r < kRows; ++r)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) {
+                const uint32_t row = 16u * r + 4u * q + i;
+                if (row >= rows) continue;
+                out[static_cast<size_t>(p0 + row) * H + channel] =
+                    (static_cast<float>(acc[t][r][i]) * ws) * row_scale[row];
+            }
+    }
+}
+
 template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
 __global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
@@ -401,69 +506,47 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
     const q38m_task_v1 task = tasks[blockIdx.y];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
-    const uint32_t active_tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t n = lane & 15u;
-    const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
     const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
     const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
+    const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
 
-    uint4 b[kBlocks];
+    // Piece i: row r = i / (I/16), 16-byte piece c: K block c/4, lane group
+    // c%4.  Every load is issued before the first store (rows past the task
+    // re-read its first row and stage zeros), so staging is one round trip.
+    constexpr uint32_t kPer = kPieces / kThreads;
+    uint4 v[kPer];
 #pragma unroll
-    for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = load_stream(wt + kb * 64u);
-
-    // Piece i: row r = i / (I/16), 16-byte piece c: K block c/4, lane group c%4.
-#pragma unroll
-    for (uint32_t u = 0; u < kPieces / kThreads; ++u) {
+    for (uint32_t u = 0; u < kPer; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
         const uint32_t r = i / (I / 16u), c = i % (I / 16u);
-        const uint4 v = r < rows ? reinterpret_cast<const uint4*>(
-                                       mq + static_cast<size_t>(p0 + r) * I)[c]
-                                 : make_uint4(0u, 0u, 0u, 0u);
-        a_lds[((c >> 2) * kRowTiles + r / 16u) * 64u + (c & 3u) * 16u + r % 16u] = v;
+        v[u] = reinterpret_cast<const uint4*>(mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) *
+                                                       I)[c];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / (I / 16u), c = i % (I / 16u);
+        if (r < 16u * tiles)
+            a_lds[((c >> 2) * kRowTiles + r / 16u) * 64u + (c & 3u) * 16u + r % 16u] =
+                r < rows ? v[u] : make_uint4(0u, 0u, 0u, 0u);
     }
     if (threadIdx.x < kWideRows)
         row_scale[threadIdx.x] = threadIdx.x < rows ? ms[p0 + threadIdx.x] : 0.0f;
     __syncthreads();
 
-#pragma unroll 1
-    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
-        uint4 nb[kBlocks];
-        const uint4* next = wt + static_cast<size_t>(t + 1u < kTilesPerWave ? t + 1u : t) *
-                                     kBlocks * 64u;
-#pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb) nb[kb] = load_stream(next + kb * 64u);
-        __builtin_amdgcn_sched_barrier(0);
-        v4i acc[kRowTiles];
-#pragma unroll
-        for (uint32_t rt = 0; rt < kRowTiles; ++rt) acc[rt] = v4i{0, 0, 0, 0};
-#pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb)
-#pragma unroll
-            for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
-                if (rt >= active_tiles) break;
-                acc[rt] = mfma_i8_16x16x64(as_v4i(a_lds[(kb * kRowTiles + rt) * 64u + lane]),
-                                           as_v4i(b[kb]), acc[rt]);
-            }
-        const uint32_t channel = (tile0 + t) * 16u + n;
-        const float ws = f16_to_f32(s[static_cast<size_t>(e) * H + channel]);
-#pragma unroll
-        for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
-            if (rt >= active_tiles) break;
-#pragma unroll
-            for (uint32_t i = 0; i < 4u; ++i) {
-                const uint32_t r = 16u * rt + 4u * q + i;
-                if (r >= rows) continue;
-                out[static_cast<size_t>(p0 + r) * H + channel] =
-                    (static_cast<float>(acc[rt][i]) * ws) * row_scale[r];
-            }
-        }
-#pragma unroll
-        for (uint32_t kb = 0; kb < kBlocks; ++kb) b[kb] = nb[kb];
-    }
+    const uint16_t* ws_row = s + static_cast<size_t>(e) * H;
+    if (tiles > 4u)
+        down_w8_wide_rows<H, I, kTilesPerWave, 8>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
+    else if (tiles > 2u)
+        down_w8_wide_rows<H, I, kTilesPerWave, 4>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
+    else if (tiles == 2u)
+        down_w8_wide_rows<H, I, kTilesPerWave, 2>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
+    else
+        down_w8_wide_rows<H, I, kTilesPerWave, 1>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
 }
 
 // Down, W4 group-32 (the all-W4 layer policy), over a 128-row task: the
@@ -495,17 +578,25 @@ __global__ __launch_bounds__(kWaves * 64) void down_w4g32_wide_kernel(
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
 
-    // Piece i: row r, 16-byte piece c = group c/2, lane groups 2(c%2), 2(c%2)+1.
+    // Piece i: row r, 16-byte piece c = group c/2, lane groups 2(c%2),
+    // 2(c%2)+1; all loads before the first store, as in the W8 kernel.
+    constexpr uint32_t kPer = kPieces / kThreads;
+    uint4 v[kPer];
 #pragma unroll
-    for (uint32_t u = 0; u < kPieces / kThreads; ++u) {
+    for (uint32_t u = 0; u < kPer; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
         const uint32_t r = i / (I / 16u), c = i % (I / 16u);
-        const uint4 v = r < rows ? reinterpret_cast<const uint4*>(
-                                       mq + static_cast<size_t>(p0 + r) * I)[c]
-                                 : make_uint4(0u, 0u, 0u, 0u);
+        v[u] = reinterpret_cast<const uint4*>(mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) *
+                                                       I)[c];
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < kPer; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / (I / 16u), c = i % (I / 16u);
+        const uint4 x = r < rows ? v[u] : make_uint4(0u, 0u, 0u, 0u);
         const uint32_t at = ((c >> 1) * kRowTiles + r / 16u) * 64u + (c & 1u) * 32u + r % 16u;
-        a_lds[at] = make_uint2(v.x, v.y);
-        a_lds[at + 16u] = make_uint2(v.z, v.w);
+        a_lds[at] = make_uint2(x.x, x.y);
+        a_lds[at + 16u] = make_uint2(x.z, x.w);
     }
     if (threadIdx.x < kWideRows)
         row_scale[threadIdx.x] = threadIdx.x < rows ? ms[p0 + threadIdx.x] : 0.0f;
@@ -522,8 +613,8 @@ __global__ __launch_bounds__(kWaves * 64) void down_w4g32_wide_kernel(
         uint2 cq[kQuads];
 #pragma unroll
         for (uint32_t kq = 0; kq < kQuads; ++kq) {
-            bq[kq] = load_stream(wt + kq * kTiles * 64u);
-            cq[kq] = load_stream(st + kq * kTiles * 16u);
+            bq[kq] = wt[kq * kTiles * 64u];
+            cq[kq] = st[kq * kTiles * 16u];
         }
         float y[kRowTiles][4];
 #pragma unroll
