@@ -225,28 +225,35 @@ __global__ __launch_bounds__(64) void wide_scatter_kernel(const int32_t* __restr
 
 // ---- gate/up ----------------------------------------------------------------
 
-struct QuadWeights {
-    uint4 g, u;    // gate and up tile data of one quad
-    uint2 sg, su;  // their fp16 scales (4 groups)
+struct TileQuad {
+    uint4 w;  // one 16-channel tile's data of one quad
+    uint2 s;  // its fp16 scales (4 groups)
 };
 
-// Gate/up over a task of up to 128 rows: the slab kernel's chain (per group
-// one v_mfma_i32_16x16x32_i8 from a zero accumulator, then
+// Gate/up over a task of up to 128 rows.  A workgroup of 16 waves covers 8
+// gate/up tile pairs: waves 0-7 run the gate tiles, waves 8-15 the matching
+// up tiles, so each wave holds one tile's accumulators (32 VGPRs at 128
+// rows) and four waves fit on a SIMD.  Each wave runs the slab kernel's
+// chain (per group one v_mfma_i32_16x16x32_i8 from a zero accumulator, then
 // y16 = fma(16*acc, s_g, y16) in group order) for kTiles 16-row tiles
-// against the same unpacked weight fragment.  kTiles is a compile-time
-// count picked per task from its row count (8, 4, 2 or 1 tiles), so the
-// tile loop has no branches and the compiler interleaves one tile's MFMAs
-// with the previous tile's v_cvt/v_fma chain.  A is staged one quad (128 K)
-// at a time into a double-buffered LDS image [group][row tile][lane] of
-// 8-byte MFMA fragments, the next quad's rows loaded into registers while
-// the current quad is multiplied; weights run two quads ahead.
+// against the same unpacked weight fragment; kTiles (8, 4, 2 or 1) is
+// picked per task from its row count, so the tile loop has no branches.
+// Within a group, tile t+1's MFMA is issued before tile t's v_cvt/v_fma
+// chain, and an empty asm on each tile's accumulators keeps that order (the
+// compiler would otherwise issue every MFMA first and spill their results).
+// A is staged one quad (128 K) at a time into a double-buffered LDS image
+// [group][row tile][lane] of 8-byte MFMA fragments, the next quad loaded
+// into registers while the current one is multiplied, and a group's
+// fragments read from LDS while the previous group computes; weights run
+// two quads ahead.  The gate waves hand their y16 to the up waves through
+// LDS for the SwiGLU epilogue.
 template <uint32_t H, uint32_t I, uint32_t kThreads, uint32_t kTiles>
 __device__ __forceinline__ void gate_up_wide_rows(
     const uint4* __restrict__ wbase, const uint2* __restrict__ sbase,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
-    uint16_t* __restrict__ mid, uint2 (*a_lds)[4u * kRowTiles * 64u], uint32_t rows,
-    uint32_t p0, uint32_t gate_tile) {
+    uint16_t* __restrict__ mid, uint2 (*a_lds)[4u * kRowTiles * 64u], float* gate_lds,
+    uint32_t rows, uint32_t p0, uint32_t pair, bool up) {
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kTilesAll = 2u * I / 16u;
     constexpr uint32_t kQuadWords = kTilesAll * 64u;
@@ -256,12 +263,11 @@ __device__ __forceinline__ void gate_up_wide_rows(
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
+    const uint32_t wave_in_half = (threadIdx.x >> 6) & 7u;
 
     auto load = [&](uint32_t kq) {
         const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
-        const uint32_t wi = k * kQuadWords + lane;
-        const uint32_t si = k * kQuadScales + n;
-        return QuadWeights{wbase[wi], wbase[wi + 64u], sbase[si], sbase[si + 16u]};
+        return TileQuad{wbase[k * kQuadWords + lane], sbase[k * kQuadScales + n]};
     };
 
     // Piece i: row r = i/8, 16-byte piece c = i%8 of the row's 128 bytes of
@@ -295,20 +301,17 @@ __device__ __forceinline__ void gate_up_wide_rows(
         }
     };
 
-    float yg[kTiles][4], yu[kTiles][4];
+    float y[kTiles][4];
 #pragma unroll
     for (uint32_t t = 0; t < kTiles; ++t)
 #pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) yg[t][i] = yu[t][i] = 0.0f;
+        for (uint32_t i = 0; i < 4u; ++i) y[t][i] = 0.0f;
 
-    auto multiply = [&](uint32_t kq, const QuadWeights& b) {
+    auto multiply = [&](uint32_t kq, const TileQuad& b) {
         const uint2* abuf = a_lds[kq & 1u] + lane;
         const v4i zero = {0, 0, 0, 0};
-        const uint32_t wgw[4] = {b.g.x, b.g.y, b.g.z, b.g.w};
-        const uint32_t wuw[4] = {b.u.x, b.u.y, b.u.z, b.u.w};
-        const uint32_t sgw[2] = {b.sg.x, b.sg.y};
-        const uint32_t suw[2] = {b.su.x, b.su.y};
-        // A fragments of group j+1 are read from LDS while group j computes
+        const uint32_t ww[4] = {b.w.x, b.w.y, b.w.z, b.w.w};
+        const uint32_t sw[2] = {b.s.x, b.s.y};
         long frag[2][kTiles];
 #pragma unroll
         for (uint32_t t = 0; t < kTiles; ++t) frag[0][t] = as_long(abuf[t * 64u]);
@@ -320,37 +323,24 @@ __device__ __forceinline__ void gate_up_wide_rows(
                     frag[(j + 1u) & 1u][t] = as_long(abuf[((j + 1u) * kRowTiles + t) * 64u]);
             }
             const long* a = frag[j & 1u];
-            const long bg = unpack_w4x16(wgw[j]);
-            const long bu = unpack_w4x16(wuw[j]);
-            const float scale_g = f16_to_f32((j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu));
-            const float scale_u = f16_to_f32((j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu));
-            // tile t+1's MFMAs are issued before tile t's chain; scheduling
-            // barriers and an empty asm on each tile's accumulators keep
-            // that order, so two tiles' results are live at a time
-            v4i dg[2], du[2];
-            dg[0] = mfma_i8_16x16x32(a[0], bg, zero);
-            du[0] = mfma_i8_16x16x32(a[0], bu, zero);
+            const long bj = unpack_w4x16(ww[j]);
+            const float scale = f16_to_f32((j & 1u) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu));
+            v4i d[2];
+            d[0] = mfma_i8_16x16x32(a[0], bj, zero);
 #pragma unroll
             for (uint32_t t = 0; t < kTiles; ++t) {
-                if (t + 1u < kTiles) {
-                    dg[(t + 1u) & 1u] = mfma_i8_16x16x32(a[t + 1u], bg, zero);
-                    du[(t + 1u) & 1u] = mfma_i8_16x16x32(a[t + 1u], bu, zero);
-                }
+                if (t + 1u < kTiles) d[(t + 1u) & 1u] = mfma_i8_16x16x32(a[t + 1u], bj, zero);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    yg[t][i] = __builtin_fmaf(static_cast<float>(dg[t & 1u][i]), scale_g, yg[t][i]);
-                    yu[t][i] = __builtin_fmaf(static_cast<float>(du[t & 1u][i]), scale_u, yu[t][i]);
-                }
-                // the chain is materialised here, not sunk past later tiles
-                asm volatile("" : "+v"(yg[t][0]), "+v"(yg[t][1]), "+v"(yg[t][2]), "+v"(yg[t][3]),
-                                  "+v"(yu[t][0]), "+v"(yu[t][1]), "+v"(yu[t][2]), "+v"(yu[t][3]));
+                for (int i = 0; i < 4; ++i)
+                    y[t][i] = __builtin_fmaf(static_cast<float>(d[t & 1u][i]), scale, y[t][i]);
+                asm volatile("" : "+v"(y[t][0]), "+v"(y[t][1]), "+v"(y[t][2]), "+v"(y[t][3]));
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
     };
     // one quad: weights two ahead into the set just consumed, A one ahead
-    auto step = [&](uint32_t kq, const QuadWeights& cur, QuadWeights& refill) {
+    auto step = [&](uint32_t kq, const TileQuad& cur, TileQuad& refill) {
         refill = load(kq + 2u);
         if (kq + 1u < kQuads) load_a(kq + 1u);
         __builtin_amdgcn_sched_barrier(0);
@@ -360,7 +350,7 @@ __device__ __forceinline__ void gate_up_wide_rows(
     };
 
     load_a(0);
-    QuadWeights r0 = load(0), r1 = load(1), r2;
+    TileQuad r0 = load(0), r1 = load(1), r2;
     store_a(0);
     __syncthreads();
     static_assert(kQuads % 3u == 1u, "three-set rotation plus one peeled quad");
@@ -372,7 +362,19 @@ __device__ __forceinline__ void gate_up_wide_rows(
     }
     multiply(kQuads - 1u, r0);
 
-    const uint32_t channel = gate_tile * 16u + n;
+    // gate waves hand y16 over: gate_lds[pair in workgroup][row][channel],
+    // over the A image, once every wave has finished reading it
+    float* handoff = gate_lds + wave_in_half * (kWideRows * 16u);
+    __syncthreads();
+    if (!up) {
+#pragma unroll
+        for (uint32_t t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) handoff[(16u * t + 4u * q + i) * 16u + n] = y[t][i];
+    }
+    __syncthreads();
+    if (!up) return;
+    const uint32_t channel = pair * 16u + n;
 #pragma unroll
     for (uint32_t t = 0; t < kTiles; ++t) {
 #pragma unroll
@@ -382,16 +384,16 @@ __device__ __forceinline__ void gate_up_wide_rows(
             const uint32_t p = p0 + r;
             const uint32_t a = packed[p];
             const float st = xs[a / kTopK];
-            const float y_gate = (yg[t][i] * 0.0625f) * st;
-            const float y_up = (yu[t][i] * 0.0625f) * st;
+            const float y_gate = (handoff[r * 16u + n] * 0.0625f) * st;
+            const float y_up = (y[t][i] * 0.0625f) * st;
             mid[static_cast<size_t>(p) * I + channel] =
                 static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
         }
     }
 }
 
-template <uint32_t H, uint32_t I, uint32_t kWaves>
-__global__ __launch_bounds__(kWaves * 64)
+template <uint32_t H, uint32_t I, uint32_t kPairs>
+__global__ __launch_bounds__(kPairs * 128) __attribute__((amdgpu_waves_per_eu(4)))
 void gate_up_w4g32_wide_kernel(
     const uint4* __restrict__ w, const uint2* __restrict__ s,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
@@ -399,33 +401,40 @@ void gate_up_w4g32_wide_kernel(
     const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kTilesAll = 2u * I / 16u;
-    constexpr uint32_t kThreads = kWaves * 64u;
-    __shared__ uint2 a_lds[2][4u * kRowTiles * 64u];
+    constexpr uint32_t kThreads = kPairs * 128u;
+    // the A image (two quads) and, after the K loop, the gate hand-off
+    constexpr uint32_t kABytes = 2u * 4u * kRowTiles * 64u * 8u;
+    constexpr uint32_t kHandoffBytes = kPairs * kWideRows * 16u * 4u;
+    __shared__ __align__(16) uint8_t lds[kABytes > kHandoffBytes ? kABytes : kHandoffBytes];
+    auto a_lds = reinterpret_cast<uint2 (*)[4u * kRowTiles * 64u]>(lds);
+    float* gate_lds = reinterpret_cast<float*>(lds);
 
     const q38m_task_v1 task = tasks[blockIdx.y];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t gate_tile = blockIdx.x * kWaves + wave;
+    const bool up = wave >= kPairs;
+    const uint32_t pair = blockIdx.x * kPairs + (wave % kPairs);
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
     // Paired quad-major layout: for quad kq the gate tile of pair p is slot
     // 2p and its up tile slot 2p+1.
-    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTilesAll + 2u * gate_tile) * 64u;
-    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTilesAll + 2u * gate_tile) * 16u;
+    const uint32_t slot = 2u * pair + (up ? 1u : 0u);
+    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTilesAll + slot) * 64u;
+    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTilesAll + slot) * 16u;
     const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
     if (tiles > 4u)
         gate_up_wide_rows<H, I, kThreads, 8>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, rows, p0, gate_tile);
+                                             a_lds, gate_lds, rows, p0, pair, up);
     else if (tiles > 2u)
         gate_up_wide_rows<H, I, kThreads, 4>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, rows, p0, gate_tile);
+                                             a_lds, gate_lds, rows, p0, pair, up);
     else if (tiles == 2u)
         gate_up_wide_rows<H, I, kThreads, 2>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, rows, p0, gate_tile);
+                                             a_lds, gate_lds, rows, p0, pair, up);
     else
         gate_up_wide_rows<H, I, kThreads, 1>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, rows, p0, gate_tile);
+                                             a_lds, gate_lds, rows, p0, pair, up);
 }
 
 // ---- down -------------------------------------------------------------------
@@ -679,9 +688,9 @@ hipError_t launch_gate_up_w4g32_wide(const void* data, const void* scales, const
                                      const float* route_weights, const q38m_task_v1* tasks,
                                      uint32_t task_count, uint16_t* weighted_mid,
                                      hipStream_t stream) {
-    constexpr uint32_t kWaves = 8;
-    const dim3 grid(kInter / 16u / kWaves, task_count);
-    gate_up_w4g32_wide_kernel<kHidden, kInter, kWaves><<<grid, kWaves * 64u, 0, stream>>>(
+    constexpr uint32_t kPairs = 8;
+    const dim3 grid(kInter / 16u / kPairs, task_count);
+    gate_up_w4g32_wide_kernel<kHidden, kInter, kPairs><<<grid, kPairs * 128u, 0, stream>>>(
         static_cast<const uint4*>(data), static_cast<const uint2*>(scales), xq, xs, packed,
         route_weights, tasks, weighted_mid);
     return hipGetLastError();
