@@ -558,12 +558,88 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
         down_w8_wide_rows<H, I, kTilesPerWave, 1>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
 }
 
-// Down, W4 group-32 (the all-W4 layer policy), over a 128-row task: the
-// gate/up group chain over K = I with every active row tile against the
-// same weight fragment; the mid rows are staged once in LDS as
-// [group][row tile][lane] 8-byte fragments.
+// Down, W4 group-32 (the all-W4 layer policy), over a task of up to 128
+// rows: the gate/up chain over K = I.  The mid rows are staged once in LDS
+// as [group][row tile][lane] 8-byte fragments; a workgroup of 16 waves
+// covers 32 output tiles, two per wave.  A wave streams its tiles' weights
+// one quad ahead and runs the chain group by group with the
+// same pinned MFMA/v_cvt/v_fma interleave as the gate/up kernel, over kRows
+// (8, 4, 2 or 1) row tiles picked per task.
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kRows>
+__device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
+                                                  const uint2* __restrict__ st,
+                                                  const uint2* a_lds, const float* row_scale,
+                                                  uint32_t rows, uint32_t p0, uint32_t tile0,
+                                                  float* __restrict__ out) {
+    constexpr uint32_t kQuads = I / 128u;
+    constexpr uint32_t kTiles = H / 16u;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint2* abuf = a_lds + lane;
+    const v4i zero = {0, 0, 0, 0};
+    // quad-major layout: quad kq of tile t is unit kq*kTiles + t of the
+    // expert; weights stream one quad ahead, across tile boundaries too
+    auto load = [&](uint32_t t, uint32_t kq) {
+        const uint32_t tt = t < kTilesPerWave ? t : kTilesPerWave - 1u;
+        return TileQuad{wt[(kq * kTiles + tt) * 64u], st[(kq * kTiles + tt) * 16u]};
+    };
+    TileQuad cur = load(0, 0);
+#pragma unroll 1
+    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
+        float y[kRows][4];
+#pragma unroll
+        for (uint32_t r = 0; r < kRows; ++r)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) y[r][i] = 0.0f;
+#pragma unroll 1
+        for (uint32_t kq = 0; kq < kQuads; ++kq) {
+          const TileQuad next = kq + 1u < kQuads ? load(t, kq + 1u) : load(t + 1u, 0);
+          const uint32_t bw[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
+          const uint32_t cw[2] = {cur.s.x, cur.s.y};
+#pragma unroll
+          for (uint32_t j = 0; j < 4u; ++j) {
+            const uint32_t g = kq * 4u + j;
+            long a[kRows];
+#pragma unroll
+            for (uint32_t r = 0; r < kRows; ++r) a[r] = as_long(abuf[(g * kRowTiles + r) * 64u]);
+            const long bj = unpack_w4x16(bw[j]);
+            const uint32_t h = (j & 1u) ? (cw[j >> 1] >> 16) : (cw[j >> 1] & 0xffffu);
+            const float scale = f16_to_f32(h) * 0.0625f;
+            v4i d[2];
+            d[0] = mfma_i8_16x16x32(a[0], bj, zero);
+#pragma unroll
+            for (uint32_t r = 0; r < kRows; ++r) {
+                if (r + 1u < kRows) d[(r + 1u) & 1u] = mfma_i8_16x16x32(a[r + 1u], bj, zero);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    y[r][i] = __builtin_fmaf(static_cast<float>(d[r & 1u][i]), scale, y[r][i]);
+                asm volatile("" : "+v"(y[r][0]), "+v"(y[r][1]), "+v"(y[r][2]), "+v"(y[r][3]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+          cur = next;
+        }
+        const uint32_t channel = (tile0 + t) * 16u + n;
+        // re-derived in every tile, so the 32 output addresses are not
+        // hoisted out of the tile loop into registers
+        uint32_t lane_row = 4u * q;
+        asm volatile("" : "+v"(lane_row));
+#pragma unroll
+        for (uint32_t r = 0; r < kRows; ++r)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) {
+                const uint32_t row = 16u * r + lane_row + i;
+                if (row >= rows) continue;
+                out[static_cast<size_t>(p0 + row) * H + channel] = y[r][i] * row_scale[row];
+            }
+    }
+}
+
 template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
-__global__ __launch_bounds__(kWaves * 64) void down_w4g32_wide_kernel(
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4)))
+void down_w4g32_wide_kernel(
     const uint4* __restrict__ w, const uint2* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
@@ -579,16 +655,14 @@ __global__ __launch_bounds__(kWaves * 64) void down_w4g32_wide_kernel(
     const q38m_task_v1 task = tasks[blockIdx.y];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
-    const uint32_t active_tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
-    const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
 
     // Piece i: row r, 16-byte piece c = group c/2, lane groups 2(c%2),
-    // 2(c%2)+1; all loads before the first store, as in the W8 kernel.
+    // 2(c%2)+1; all loads before the first store.
     constexpr uint32_t kPer = kPieces / kThreads;
     uint4 v[kPer];
 #pragma unroll
@@ -611,58 +685,18 @@ __global__ __launch_bounds__(kWaves * 64) void down_w4g32_wide_kernel(
         row_scale[threadIdx.x] = threadIdx.x < rows ? ms[p0 + threadIdx.x] : 0.0f;
     __syncthreads();
 
-    const v4i zero = {0, 0, 0, 0};
     const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
-#pragma unroll 1
-    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
-        const uint32_t tile = tile0 + t;
-        const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 64u + lane;
-        const uint2* st = s + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 16u + n;
-        uint4 bq[kQuads];
-        uint2 cq[kQuads];
-#pragma unroll
-        for (uint32_t kq = 0; kq < kQuads; ++kq) {
-            bq[kq] = wt[kq * kTiles * 64u];
-            cq[kq] = st[kq * kTiles * 16u];
-        }
-        float y[kRowTiles][4];
-#pragma unroll
-        for (uint32_t rt = 0; rt < kRowTiles; ++rt)
-#pragma unroll
-            for (uint32_t i = 0; i < 4u; ++i) y[rt][i] = 0.0f;
-#pragma unroll
-        for (uint32_t kq = 0; kq < kQuads; ++kq) {
-            const uint32_t bw[4] = {bq[kq].x, bq[kq].y, bq[kq].z, bq[kq].w};
-            const uint32_t cw[2] = {cq[kq].x, cq[kq].y};
-#pragma unroll
-            for (uint32_t j = 0; j < 4u; ++j) {
-                const long bj = unpack_w4x16(bw[j]);
-                const uint32_t h = (j & 1u) ? (cw[j >> 1] >> 16) : (cw[j >> 1] & 0xffffu);
-                const float scale = f16_to_f32(h) * 0.0625f;
-                const uint32_t g = kq * 4u + j;
-#pragma unroll
-                for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
-                    if (rt >= active_tiles) break;
-                    const v4i d = mfma_i8_16x16x32(
-                        as_long(a_lds[(g * kRowTiles + rt) * 64u + lane]), bj, zero);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        y[rt][i] = __builtin_fmaf(static_cast<float>(d[i]), scale, y[rt][i]);
-                }
-            }
-        }
-        const uint32_t channel = tile * 16u + n;
-#pragma unroll
-        for (uint32_t rt = 0; rt < kRowTiles; ++rt) {
-            if (rt >= active_tiles) break;
-#pragma unroll
-            for (uint32_t i = 0; i < 4u; ++i) {
-                const uint32_t r = 16u * rt + 4u * q + i;
-                if (r >= rows) continue;
-                out[static_cast<size_t>(p0 + r) * H + channel] = y[rt][i] * row_scale[r];
-            }
-        }
-    }
+    const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile0) * 64u + lane;
+    const uint2* st = s + (static_cast<size_t>(e) * kQuads * kTiles + tile0) * 16u + n;
+    const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
+    if (tiles > 4u)
+        down_w4_wide_rows<H, I, kTilesPerWave, 8>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
+    else if (tiles > 2u)
+        down_w4_wide_rows<H, I, kTilesPerWave, 4>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
+    else if (tiles == 2u)
+        down_w4_wide_rows<H, I, kTilesPerWave, 2>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
+    else
+        down_w4_wide_rows<H, I, kTilesPerWave, 1>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
 }
 
 }  // namespace
@@ -711,7 +745,7 @@ hipError_t launch_down_w8pc_wide(const void* data, const void* scales, const int
 hipError_t launch_down_w4g32_wide(const void* data, const void* scales, const int8_t* mid_q,
                                   const float* mid_s, const q38m_task_v1* tasks,
                                   uint32_t task_count, float* route_output, hipStream_t stream) {
-    constexpr uint32_t kWaves = 8, kTilesPerWave = 4;
+    constexpr uint32_t kWaves = 16, kTilesPerWave = 2;
     const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
     down_w4g32_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave>
         <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(data),
