@@ -10,10 +10,13 @@ q38m_moe_prefill_v1.  Also reported: per-kernel durations from HIP events
 on the launch stream over a second timed run of the same kernels launched
 one entry point at a time, the roofline of the dominant
 kernel, the step's fraction of int8 MFMA and HBM peaks, batch-1 decode
-HBM GB/s through config 3's 48-layer stack, and the CPU oracle timed on
-this host as the baseline.
+HBM GB/s through config 3's 48-layer stack, the router and shared-expert
+GEMMs, the chunk path (q38m_moe_prefill_wide_v1) on config 4 and one
+config-5 layer beside the slab path, and the CPU oracle timed on this host
+as the baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+       [--no-quantizer] [--no-dense] [--no-chunks]
 """
 import argparse
 import ctypes
