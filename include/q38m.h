@@ -403,10 +403,13 @@ int q38m_moe_compiled(void);
 const char* q38m_last_error(void);
 
 /* Kernel-level self checks used by the tests: the contract's exp and the
- * int8 MFMA lane layout (one 16x16x32 product, A and B row-major). */
+ * int8 MFMA lane layouts (one 16x16x32 or 32x32x32 product, A and B
+ * row-major). */
 int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream,
                     int device);
 int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d,
+                                void* stream, int device);
+int q38m_debug_mfma_32x32x32_i8(const int8_t* a, const int8_t* b, int32_t* d,
                                 void* stream, int device);
 
 #ifdef __cplusplus

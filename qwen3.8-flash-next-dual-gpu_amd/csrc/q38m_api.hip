@@ -688,4 +688,11 @@ int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d, vo
     return finish(q38m::launch_debug_mfma(a, b, d, as_stream(stream)), "debug_mfma_kernel");
 }
 
+int q38m_debug_mfma_32x32x32_i8(const int8_t* a, const int8_t* b, int32_t* d, void* stream,
+                                int device) {
+    if (!a || !b || !d) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug mfma input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_debug_mfma32(a, b, d, as_stream(stream)), "debug_mfma32_kernel");
+}
+
 }  // extern "C"

@@ -129,6 +129,15 @@ __device__ __forceinline__ v4i mfma_i8_16x16x64(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_i32_32x32x32_i8 (gfx950): A 32x32 (lane l: row l%32, k
+// 16*(l/32)..+15), B 32x32 (lane l: column l%32, same k), D lane l:
+// column l%32, rows 8*(i/4) + 4*(l/32) + i%4 for i = 0..15.  Like the
+// 16x16x32 form it covers one 32-wide scale group, at twice its MAC rate.
+typedef int v16i __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ v16i mfma_i8_32x32x32(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
 // Expands one MFMA16 W4 dword (byte i = k_i | k_{4+i} << 4) into the eight
 // int8 B-operand bytes k_0..k_7, each multiplied by 16: the nibble lands
 // in the high half of its byte, so the sign needs no extension.  The x16

@@ -125,5 +125,7 @@ hipError_t launch_debug_expf(const float* x, uint32_t n, float* out,
                              hipStream_t stream);
 hipError_t launch_debug_mfma(const int8_t* a, const int8_t* b, int32_t* d,
                              hipStream_t stream);
+hipError_t launch_debug_mfma32(const int8_t* a, const int8_t* b, int32_t* d,
+                               hipStream_t stream);
 
 }  // namespace q38m

@@ -261,6 +261,25 @@ __global__ void debug_mfma_kernel(const int8_t* __restrict__ a, const int8_t* __
     for (uint32_t i = 0; i < 4u; ++i) d[(4u * q + i) * 16u + n] = r[i];
 }
 
+__global__ void debug_mfma32_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b,
+                                    int32_t* __restrict__ d) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = lane & 31u, h = lane >> 5;
+    uint32_t av[4] = {0u, 0u, 0u, 0u}, bv[4] = {0u, 0u, 0u, 0u};
+    for (uint32_t i = 0; i < 16u; ++i) {
+        av[i / 4u] |= static_cast<uint32_t>(static_cast<uint8_t>(a[c * 32u + 16u * h + i])) << (8u * (i % 4u));
+        bv[i / 4u] |= static_cast<uint32_t>(static_cast<uint8_t>(b[(16u * h + i) * 32u + c])) << (8u * (i % 4u));
+    }
+    const v4i at = {static_cast<int>(av[0]), static_cast<int>(av[1]), static_cast<int>(av[2]),
+                    static_cast<int>(av[3])};
+    const v4i bt = {static_cast<int>(bv[0]), static_cast<int>(bv[1]), static_cast<int>(bv[2]),
+                    static_cast<int>(bv[3])};
+    v16i zero;
+    for (int i = 0; i < 16; ++i) zero[i] = 0;
+    const v16i r = mfma_i8_32x32x32(at, bt, zero);
+    for (uint32_t i = 0; i < 16u; ++i) d[(8u * (i / 4u) + 4u * h + i % 4u) * 32u + c] = r[i];
+}
+
 inline uint32_t blocks_for(uint64_t total, uint32_t threads) {
     return static_cast<uint32_t>((total + threads - 1u) / threads);
 }
@@ -339,6 +358,11 @@ hipError_t launch_debug_expf(const float* x, uint32_t n, float* out, hipStream_t
 
 hipError_t launch_debug_mfma(const int8_t* a, const int8_t* b, int32_t* d, hipStream_t stream) {
     debug_mfma_kernel<<<1, 64, 0, stream>>>(a, b, d);
+    return hipGetLastError();
+}
+
+hipError_t launch_debug_mfma32(const int8_t* a, const int8_t* b, int32_t* d, hipStream_t stream) {
+    debug_mfma32_kernel<<<1, 64, 0, stream>>>(a, b, d);
     return hipGetLastError();
 }
 

@@ -35,6 +35,19 @@ def test_mfma_i8_lane_layout(q38m):
     assert np.array_equal(got, a.astype(np.int64) @ b.astype(np.int64))
 
 
+def test_mfma_i8_32x32_lane_layout(q38m):
+    rng = np.random.default_rng(3)
+    a = rng.integers(-128, 128, (32, 32)).astype(np.int8)
+    b = rng.integers(-128, 128, (32, 32)).astype(np.int8)
+    t = torch()
+    d = t.zeros(1024, dtype=t.int32, device="cuda")
+    da, db = device(a), device(b)
+    q38m.call("q38m_debug_mfma_32x32x32_i8", da.data_ptr(), db.data_ptr(), d.data_ptr(),
+              stream(), 0)
+    got = host(d, np.int32).reshape(32, 32)
+    assert np.array_equal(got, a.astype(np.int64) @ b.astype(np.int64))
+
+
 def test_expf_bitwise(q38m, orc):
     rng = np.random.default_rng(1)
     x = np.concatenate([
