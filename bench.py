@@ -12,11 +12,12 @@ one entry point at a time, the roofline of the dominant
 kernel, the step's fraction of int8 MFMA and HBM peaks, batch-1 decode
 HBM GB/s through config 3's 48-layer stack, the router and shared-expert
 GEMMs, the chunk path (q38m_moe_prefill_wide_v1) on config 4 and one
-config-5 layer beside the slab path, and the CPU oracle timed on this host
-as the baseline.
+config-5 layer beside the slab path, the hyper-connection prepare/finish
+around the MoE step (q38m_hyper_prepare_v1, q38m_hyper_inject_bf16) on the
+512-token slab, and the CPU oracle timed on this host as the baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
-       [--no-quantizer] [--no-dense] [--no-chunks]
+       [--no-quantizer] [--no-dense] [--no-chunks] [--no-hyper]
 """
 import argparse
 import ctypes
@@ -55,6 +56,7 @@ def main():
     parser.add_argument("--no-quantizer", action="store_true")
     parser.add_argument("--no-dense", action="store_true")
     parser.add_argument("--no-chunks", action="store_true")
+    parser.add_argument("--no-hyper", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
@@ -245,6 +247,9 @@ def main():
     if not args.no_chunks:
         result["chunks"] = bench_chunks(q38m, W, torch)
 
+    if not args.no_hyper:
+        result["hyper"] = bench_hyper(q38m, torch, T, args.steps)
+
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
                                               T)
@@ -394,6 +399,71 @@ def bench_router_shared(q38m, W, torch, hidden, steps):
                      "GBps": round(nbytes / s / 1e9, 1),
                      "hbm_frac": round(nbytes / s / 1e9 / HBM_PEAK_GBPS, 4)}
     out["tokens"] = T
+    return out
+
+
+def bench_hyper(q38m, torch, T, steps, low_rank=320):
+    """Hyper-connection prepare (group RMSNorm + inject dots, the two
+    low-rank GEMMs with SiLU / sigmoid epilogues, the stream mix) and finish
+    (inject) on a T-token slab, at this layer's hidden 2048 and the
+    reference model's 2560.  Algorithmic bytes: every operand read once and
+    every result written once, intermediates included (prepare: the 4-stream
+    state in, normalized out and in twice, mix out and in, low out and in,
+    mixed and injection out, the three weight matrices; inject: state and
+    block output in, state out)."""
+    sh = torch.cuda.current_stream().cuda_stream
+    rng = torch.Generator(device="cuda").manual_seed(11)
+
+    def bf16(*shape, scale=1.0):
+        x = (torch.randn(*shape, generator=rng, device="cuda") * scale).to(torch.bfloat16)
+        return x.view(torch.int16)
+
+    out = {"tokens": T, "low_rank": low_rank}
+    for H in (2048, 2560):
+        width = 4 * H
+        state = bf16(T, width)
+        norm_w, down = bf16(width, scale=0.1), bf16(low_rank, width, scale=0.03)
+        up, inj = bf16(width, low_rank, scale=0.2), bf16(4, width, scale=0.03)
+        block = bf16(T, H)
+        scratch = torch.empty(q38m.lib().q38m_hyper_prepare_scratch_bytes(T, H, low_rank) // 2,
+                              dtype=torch.int16, device="cuda")
+        mixed = torch.empty(T, H, dtype=torch.int16, device="cuda")
+        injection = torch.empty(T, 4, dtype=torch.int16, device="cuda")
+        new_state = torch.empty_like(state)
+
+        def prepare():
+            q38m.call("q38m_hyper_prepare_v1", state.data_ptr(), norm_w.data_ptr(),
+                      down.data_ptr(), up.data_ptr(), inj.data_ptr(), T, H, low_rank,
+                      scratch.data_ptr(), mixed.data_ptr(), injection.data_ptr(), sh, 0)
+
+        def finish():
+            q38m.call("q38m_hyper_inject_bf16", state.data_ptr(), block.data_ptr(),
+                      injection.data_ptr(), new_state.data_ptr(), T, H, sh, 0)
+
+        def timed(fn):
+            for _ in range(5):
+                fn()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(steps):
+                fn()
+            stop.record()
+            torch.cuda.synchronize()
+            return start.elapsed_time(stop) / steps
+
+        p_ms, f_ms = timed(prepare), timed(finish)
+        p_bytes = 2 * (T * width * 6 + T * low_rank * 2 + T * H + T * 4 +
+                       width * (1 + 2 * low_rank + 4))
+        f_bytes = 2 * (2 * T * width + T * H + T * 4)
+        p_flops = 2 * T * width * (2 * low_rank + 4)
+        res = {}
+        for name, ms, nbytes in (("prepare", p_ms, p_bytes), ("finish", f_ms, f_bytes)):
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            res[name] = {"us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                         "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+        res["prepare"]["TFLOPs"] = round(p_flops / (p_ms * 1e-3) / 1e12, 2)
+        out[f"hidden_{H}"] = res
     return out
 
 

@@ -54,6 +54,8 @@ extern "C" {
 #define Q38M_WIDE_MAX_TOKENS 32768u
 #define Q38M_WIDE_TASK_ROWS 128u
 #define Q38M_ROUTE_PLAN_VERSION_WIDE 2u
+/* Hyper-connection streams per token (include/q38/cuda_hyper.h:9). */
+#define Q38M_HYPER_STREAMS 4u
 /* Model widths this build's kernels are instantiated for. */
 #define Q38M_HIDDEN 2048u
 #define Q38M_INTERMEDIATE 512u
@@ -332,6 +334,43 @@ int q38m_moe_decode_v1(const q38m_expert_weights_v1* gate_up,
                        const uint16_t* shared_gate, const uint16_t* residual,
                        void* scratch, uint16_t* output, void* stream,
                        int device);
+
+/* ---- hyper-connection prepare/finish around the MoE step -------------
+ * include/q38/cuda_hyper.h:15-58 (kernels cuda/q38_hyper.cu:52-114; call
+ * sequence cuda_backend.cu:1219-1252).  The hidden state is
+ * Q38M_HYPER_STREAMS streams of `hidden` bf16 values per token ([T][4][H]);
+ * the reference fixes hidden = 2560 (cuda_hyper.h:9-12), here it is a
+ * parameter (multiple of 8, <= 8192) so the prepare can feed this library's
+ * H = 2048 MoE.  Floating-point results (fp32 inside a step, bf16 between
+ * steps as the reference, this library's exp): parity is a tolerance.
+ * Elementwise entry points need tokens * width to be a multiple of 8. */
+int q38m_hyper_repeat_embedding_bf16(const uint16_t* embedding, uint16_t* hyper,
+                                     uint32_t tokens, uint32_t hidden, void* stream,
+                                     int device);
+int q38m_hyper_group_rmsnorm_bf16(const uint16_t* hyper, const uint16_t* norm_weight,
+                                  uint16_t* normalized, uint32_t tokens, uint32_t hidden,
+                                  void* stream, int device);
+int q38m_hyper_silu_scaled_bf16(const uint16_t* input, uint16_t* output, uint32_t tokens,
+                                uint32_t width, float divisor, void* stream, int device);
+int q38m_hyper_sigmoid_bf16(const uint16_t* input, uint16_t* output, uint32_t tokens,
+                            uint32_t width, float input_divisor, float output_scale,
+                            void* stream, int device);
+int q38m_hyper_mix_bf16(const uint16_t* normalized_hyper, const uint16_t* mix_weights,
+                        uint16_t* mixed, uint32_t tokens, uint32_t hidden, void* stream,
+                        int device);
+int q38m_hyper_inject_bf16(const uint16_t* original_hyper, const uint16_t* block_output,
+                           const uint16_t* injection_weights, uint16_t* output_hyper,
+                           uint32_t tokens, uint32_t hidden, void* stream, int device);
+/* The whole prepare_hyper sequence (cuda_backend.cu:1219-1243) in four
+ * launches: mix_down [low_rank][4H], mix_up [4H][low_rank], inject [4][4H]
+ * or NULL (then injection is not written).  low_rank % 32 == 0.  Outputs
+ * mixed [T][H] (the MoE input) and injection [T][4] (for the finish). */
+size_t q38m_hyper_prepare_scratch_bytes(uint32_t tokens, uint32_t hidden, uint32_t low_rank);
+int q38m_hyper_prepare_v1(const uint16_t* hyper, const uint16_t* norm_weight,
+                          const uint16_t* mix_down, const uint16_t* mix_up,
+                          const uint16_t* inject, uint32_t tokens, uint32_t hidden,
+                          uint32_t low_rank, void* scratch, uint16_t* mixed,
+                          uint16_t* injection, void* stream, int device);
 
 /* ---- weight layout (cuda/cuda_weights.cu:229-285 re-tiles W4 at load) */
 size_t q38m_expert_weights_bytes(const q38m_expert_weights_v1* w,

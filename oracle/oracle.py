@@ -367,3 +367,93 @@ def set_threads(n):
 
 def num_threads():
     return lib().q38o_num_threads()
+
+
+# ---- hyper-connection prepare/finish (floating point) ---------------------
+# Restatement of cuda/q38_hyper.cu:52-114 and the prepare_hyper /
+# finish_hyper sequences of cuda/cuda_backend.cu:1219-1252, in float32 with
+# bf16 rounding between steps as the reference stores bf16 after every
+# kernel.  exp is this library's expf (the reference calls CUDA's expf);
+# a * b + c written in the reference is evaluated as one rounding (fma),
+# emulated exactly in float64 since every product here is of bf16 values.
+# Pins: tests/test_oracle_hyper.py (closed forms and a float64 evaluation).
+HYPER_STREAMS = 4
+
+
+def _bf(x):
+    return bf16_to_f32(f32_to_bf16(np.asarray(x, dtype=np.float32)))
+
+
+def _fma(a, b, c):
+    return (np.asarray(a, np.float64) * np.asarray(b, np.float64) +
+            np.asarray(c, np.float64)).astype(np.float32)
+
+
+def hyper_repeat_embedding(embedding_bf16):
+    """[T][H] -> [T][4][H] (q38_hyper.cu:52-61)."""
+    e = np.asarray(embedding_bf16, np.uint16)
+    return np.repeat(e[:, None, :], HYPER_STREAMS, axis=1)
+
+
+def hyper_group_rmsnorm(hyper_bf16, weight_bf16):
+    """[T][4][H], weight [4][H] -> bf16 [T][4][H] (q38_hyper.cu:63-85):
+    x * rsqrt(mean(x^2) + 1e-6) * (1 + w) per (token, stream).  The sum of
+    squares is evaluated in float64 (the reference's tree order is not part
+    of its contract; parity is a tolerance)."""
+    x = bf16_to_f32(np.asarray(hyper_bf16, np.uint16))
+    w = bf16_to_f32(np.asarray(weight_bf16, np.uint16))
+    hidden = x.shape[-1]
+    mean = (np.square(x.astype(np.float64)).sum(axis=-1) / hidden).astype(np.float32)
+    inverse = (np.float32(1.0) / np.sqrt(mean + np.float32(1e-6))).astype(np.float32)
+    y = (x * inverse[..., None]).astype(np.float32) * (np.float32(1.0) + w)
+    return f32_to_bf16(y.astype(np.float32))
+
+
+def hyper_activation(x_bf16, divisor, scale, silu):
+    """bf16(f(x / divisor) * scale), f = silu or sigmoid (q38_hyper.cu:87-97)."""
+    v = (bf16_to_f32(np.asarray(x_bf16, np.uint16)) / np.float32(divisor)).astype(np.float32)
+    sigmoid = (np.float32(1.0) / (np.float32(1.0) + expf(-v))).astype(np.float32)
+    out = (v * sigmoid if silu else sigmoid).astype(np.float32) * np.float32(scale)
+    return f32_to_bf16(out.astype(np.float32))
+
+
+def hyper_mix(normalized_bf16, mix_bf16):
+    """[T][4][H] x [T][4][H] -> bf16 [T][H]: the stream sum in stream order,
+    then / 4 (q38_hyper.cu:99-114)."""
+    n = bf16_to_f32(np.asarray(normalized_bf16, np.uint16))
+    m = bf16_to_f32(np.asarray(mix_bf16, np.uint16))
+    acc = np.zeros(n.shape[:1] + n.shape[2:], np.float32)
+    for s in range(HYPER_STREAMS):
+        acc = _fma(n[:, s], m[:, s], acc)
+    return f32_to_bf16((acc / np.float32(HYPER_STREAMS)).astype(np.float32))
+
+
+def hyper_inject(original_bf16, block_bf16, injection_bf16):
+    """bf16(original[s][i] + block[i] * injection[s]) (q38_hyper.cu:116-135)."""
+    o = bf16_to_f32(np.asarray(original_bf16, np.uint16))
+    b = bf16_to_f32(np.asarray(block_bf16, np.uint16))
+    g = bf16_to_f32(np.asarray(injection_bf16, np.uint16))
+    return f32_to_bf16(_fma(b[:, None, :], g[:, :, None], o))
+
+
+def hyper_gemv(x_bf16, w_bf16):
+    """cuda_gemv_bf16 over a preserved bf16 matrix [N][K]: bf16 of the dot
+    product (evaluated in float64; the reference's order is cuBLAS's)."""
+    x = bf16_to_f32(np.asarray(x_bf16, np.uint16)).astype(np.float64)
+    w = bf16_to_f32(np.asarray(w_bf16, np.uint16)).astype(np.float64)
+    return f32_to_bf16((x @ w.T).astype(np.float32))
+
+
+def hyper_prepare(hyper_bf16, norm_bf16, mix_down_bf16, mix_up_bf16, inject_bf16=None):
+    """prepare_hyper (cuda_backend.cu:1219-1243): returns (mixed [T][H],
+    injection [T][4] or None, and the intermediates for tests)."""
+    t = hyper_bf16.shape[0]
+    normalized = hyper_group_rmsnorm(hyper_bf16, norm_bf16)
+    flat = normalized.reshape(t, -1)
+    low = hyper_activation(hyper_gemv(flat, mix_down_bf16), HYPER_STREAMS, 1.0, True)
+    mix = hyper_activation(hyper_gemv(low, mix_up_bf16), 1.0, 1.0, False)
+    mixed = hyper_mix(normalized, mix.reshape(normalized.shape))
+    injection = None
+    if inject_bf16 is not None:
+        injection = hyper_activation(hyper_gemv(flat, inject_bf16), HYPER_STREAMS, 2.0, False)
+    return mixed, injection, {"normalized": normalized, "low": low, "mix": mix}

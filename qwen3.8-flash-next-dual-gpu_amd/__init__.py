@@ -158,6 +158,14 @@ SIGNATURES = {
     "q38m_moe_router_v1": (_INT, [_P, _P, _U32, _P, _P, _INT]),
     "q38m_moe_shared_expert_scratch_bytes": (_SZ, [_U32, _U32]),
     "q38m_moe_shared_expert_v1": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _INT]),
+    "q38m_hyper_repeat_embedding_bf16": (_INT, [_P, _P, _U32, _U32, _P, _INT]),
+    "q38m_hyper_group_rmsnorm_bf16": (_INT, [_P, _P, _P, _U32, _U32, _P, _INT]),
+    "q38m_hyper_silu_scaled_bf16": (_INT, [_P, _P, _U32, _U32, _F, _P, _INT]),
+    "q38m_hyper_sigmoid_bf16": (_INT, [_P, _P, _U32, _U32, _F, _F, _P, _INT]),
+    "q38m_hyper_mix_bf16": (_INT, [_P, _P, _P, _U32, _U32, _P, _INT]),
+    "q38m_hyper_inject_bf16": (_INT, [_P, _P, _P, _P, _U32, _U32, _P, _INT]),
+    "q38m_hyper_prepare_scratch_bytes": (_SZ, [_U32, _U32, _U32]),
+    "q38m_hyper_prepare_v1": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P, _INT]),
     "q38m_synth_fill": (_INT, [_U32, _U64, _U64, _U64, _F, _I32, _I32, _P, _U32, _P, _P, _INT]),
     "q38m_moe_compiled": (_INT, []),
     "q38m_last_error": (ctypes.c_char_p, []),

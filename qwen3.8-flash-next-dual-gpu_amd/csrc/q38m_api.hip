@@ -12,6 +12,8 @@
 
 #include "q38m_internal.h"
 
+#include <initializer_list>
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -591,8 +593,9 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
     return finish(q38m::launch_repack(*src, *dst, as_stream(stream)), "repack kernels");
 }
 
-// the GEMM grid's y dimension holds one 64-row tile per block
-constexpr uint32_t kDenseMaxRows = 65535u * 64u;
+// the GEMM grid's y dimension holds one 32-row tile per block and stays
+// within 65535 blocks
+constexpr uint32_t kDenseMaxRows = 65535u * 32u;
 
 int q38m_dense_gemm_bf16(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
                          uint32_t k, float* c_f32, uint16_t* c_bf16, void* stream, int device) {
@@ -674,6 +677,105 @@ int q38m_synth_fill(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count, 
 int q38m_moe_compiled(void) { return 1; }
 
 const char* q38m_last_error(void) { return g_last_error.c_str(); }
+
+// ---- hyper-connection prepare/finish ----------------------------------
+
+namespace {
+bool valid_hidden(uint32_t hidden) { return hidden != 0u && hidden % 8u == 0u && hidden <= 8192u; }
+bool all16(std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs)
+        if (!p || !aligned(p, 16)) return false;
+    return true;
+}
+}  // namespace
+
+int q38m_hyper_repeat_embedding_bf16(const uint16_t* embedding, uint16_t* hyper, uint32_t tokens,
+                                     uint32_t hidden, void* stream, int device) {
+    if (!all16({embedding, hyper}) || tokens == 0 || !valid_hidden(hidden))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid hyper repeat buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_hyper_repeat(embedding, hyper, tokens, hidden, as_stream(stream)),
+                  "hyper_repeat_kernel");
+}
+
+int q38m_hyper_group_rmsnorm_bf16(const uint16_t* hyper, const uint16_t* norm_weight,
+                                  uint16_t* normalized, uint32_t tokens, uint32_t hidden,
+                                  void* stream, int device) {
+    if (!all16({hyper, norm_weight, normalized}) || tokens == 0 || !valid_hidden(hidden))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid hyper norm buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_hyper_norm(hyper, norm_weight, nullptr, tokens, hidden, normalized,
+                                          nullptr, as_stream(stream)),
+                  "hyper_norm_kernel");
+}
+
+int q38m_hyper_silu_scaled_bf16(const uint16_t* input, uint16_t* output, uint32_t tokens,
+                                uint32_t width, float divisor, void* stream, int device) {
+    const uint64_t elements = static_cast<uint64_t>(tokens) * width;
+    if (!all16({input, output}) || elements == 0 || elements % 8u != 0u || !(divisor > 0.0f))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid hyper elementwise buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_hyper_elementwise(input, output, elements, divisor, 1.0f, true,
+                                                 as_stream(stream)),
+                  "hyper_elementwise_kernel");
+}
+
+int q38m_hyper_sigmoid_bf16(const uint16_t* input, uint16_t* output, uint32_t tokens,
+                            uint32_t width, float input_divisor, float output_scale,
+                            void* stream, int device) {
+    const uint64_t elements = static_cast<uint64_t>(tokens) * width;
+    if (!all16({input, output}) || elements == 0 || elements % 8u != 0u ||
+        !(input_divisor > 0.0f))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid hyper elementwise buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_hyper_elementwise(input, output, elements, input_divisor,
+                                                 output_scale, false, as_stream(stream)),
+                  "hyper_elementwise_kernel");
+}
+
+int q38m_hyper_mix_bf16(const uint16_t* normalized_hyper, const uint16_t* mix_weights,
+                        uint16_t* mixed, uint32_t tokens, uint32_t hidden, void* stream,
+                        int device) {
+    if (!all16({normalized_hyper, mix_weights, mixed}) || tokens == 0 || !valid_hidden(hidden))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid hyper mix buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_hyper_mix(normalized_hyper, mix_weights, mixed, tokens, hidden,
+                                         as_stream(stream)),
+                  "hyper_mix_kernel");
+}
+
+int q38m_hyper_inject_bf16(const uint16_t* original_hyper, const uint16_t* block_output,
+                           const uint16_t* injection_weights, uint16_t* output_hyper,
+                           uint32_t tokens, uint32_t hidden, void* stream, int device) {
+    if (!all16({original_hyper, block_output, output_hyper}) || !injection_weights ||
+        !aligned(injection_weights, 2) || tokens == 0 || !valid_hidden(hidden))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid hyper injection buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_hyper_inject(original_hyper, block_output, injection_weights,
+                                            output_hyper, tokens, hidden, as_stream(stream)),
+                  "hyper_inject_kernel");
+}
+
+size_t q38m_hyper_prepare_scratch_bytes(uint32_t tokens, uint32_t hidden, uint32_t low_rank) {
+    return q38m::hyper_prepare_scratch_bytes(tokens, hidden, low_rank);
+}
+
+int q38m_hyper_prepare_v1(const uint16_t* hyper, const uint16_t* norm_weight,
+                          const uint16_t* mix_down, const uint16_t* mix_up,
+                          const uint16_t* inject, uint32_t tokens, uint32_t hidden,
+                          uint32_t low_rank, void* scratch, uint16_t* mixed,
+                          uint16_t* injection, void* stream, int device) {
+    if (!all16({hyper, norm_weight, mix_down, mix_up, scratch, mixed}) || tokens == 0 ||
+        tokens > 65535u * 32u || !valid_hidden(hidden) || low_rank == 0u ||
+        low_rank % 32u != 0u || (inject != nullptr && (!aligned(inject, 16) || !injection)) ||
+        (injection != nullptr && !aligned(injection, 2)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid hyper prepare input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_hyper_prepare(hyper, norm_weight, mix_down, mix_up, inject, tokens,
+                                             hidden, low_rank, scratch, mixed, injection,
+                                             as_stream(stream)),
+                  "hyper prepare kernels");
+}
 
 int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream, int device) {
     if (!x || !out || n == 0) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug expf input");

@@ -123,13 +123,28 @@ __device__ __forceinline__ void reduce_waves(f32x4* lds, const f32x4* acc, uint3
     }
 }
 
+// Output of the dense GEMM: fp32, bf16, or bf16 through the hyper-connection
+// elementwise step applied to the bf16-rounded product v
+// (q38_hyper.cu:87-97): bf16(silu(v / divisor) * scale) or
+// bf16(sigmoid(v / divisor) * scale), sigmoid(x) = 1 / (1 + exp(-x)).
+enum class DenseOut { kF32, kBf16, kBf16Silu, kBf16Sigmoid };
+
+__device__ __forceinline__ uint32_t dense_epilogue(DenseOut mode, float acc, float divisor,
+                                                   float scale) {
+    if (mode == DenseOut::kBf16) return f32_to_bf16(acc);
+    const float v = bf16_round(acc) / divisor;
+    const float sigmoid = 1.0f / (1.0f + exp_q(-v));
+    return f32_to_bf16((mode == DenseOut::kBf16Silu ? v * sigmoid : sigmoid) * scale);
+}
+
 // C[M][N] = A[M][K] * B[N][K]^T for a (16 kTM) x (16 kTN) tile of C per
 // workgroup of four waves that split K.  The D layout of each 16 x 16 MFMA
 // tile: lane l holds rows 4*(l/16) + e, e = 0..3, of column l%16.
-template <uint32_t kTM, uint32_t kTN, bool kBf16Out>
+template <uint32_t kTM, uint32_t kTN, DenseOut kOut>
 __global__ __launch_bounds__(256) void dense_gemm_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m, uint32_t n,
-    uint32_t k, float* __restrict__ c_f32, uint16_t* __restrict__ c_bf16) {
+    uint32_t k, float* __restrict__ c_f32, uint16_t* __restrict__ c_bf16, float divisor,
+    float scale) {
     __shared__ f32x4 lds[kDenseWaves * kTM * kTN * 64];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
@@ -157,10 +172,10 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(
             const uint32_t row = m0 + 16u * (o / kTN) + 4u * (lane >> 4) + e;
             if (row >= m || col >= n) continue;
             const size_t at = static_cast<size_t>(row) * n + col;
-            if constexpr (kBf16Out)
-                c_bf16[at] = static_cast<uint16_t>(f32_to_bf16(sum[e]));
-            else
+            if constexpr (kOut == DenseOut::kF32)
                 c_f32[at] = sum[e];
+            else
+                c_bf16[at] = static_cast<uint16_t>(dense_epilogue(kOut, sum[e], divisor, scale));
         }
     });
 }
@@ -246,24 +261,46 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
 
 }  // namespace
 
-hipError_t launch_dense_gemm(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
-                             uint32_t k, float* c_f32, uint16_t* c_bf16, hipStream_t stream) {
+namespace {
+
+template <DenseOut kOut>
+void launch_dense_tiles(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n, uint32_t k,
+                        float* c_f32, uint16_t* c_bf16, float divisor, float scale,
+                        hipStream_t stream) {
     const uint32_t tm = m <= 16u ? 1u : 2u;
     const uint32_t tn = (m <= 16u || n <= 16u) ? 1u : 2u;
     const dim3 grid((n + 16u * tn - 1u) / (16u * tn), (m + 16u * tm - 1u) / (16u * tm));
-    const bool bf = c_bf16 != nullptr;
-    if (tm == 1u && bf)
-        dense_gemm_kernel<1, 1, true><<<grid, 256, 0, stream>>>(a, b, m, n, k, nullptr, c_bf16);
-    else if (tm == 1u)
-        dense_gemm_kernel<1, 1, false><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, nullptr);
-    else if (tn == 1u && bf)
-        dense_gemm_kernel<2, 1, true><<<grid, 256, 0, stream>>>(a, b, m, n, k, nullptr, c_bf16);
+    if (tm == 1u)
+        dense_gemm_kernel<1, 1, kOut><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, c_bf16,
+                                                               divisor, scale);
     else if (tn == 1u)
-        dense_gemm_kernel<2, 1, false><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, nullptr);
-    else if (bf)
-        dense_gemm_kernel<2, 2, true><<<grid, 256, 0, stream>>>(a, b, m, n, k, nullptr, c_bf16);
+        dense_gemm_kernel<2, 1, kOut><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, c_bf16,
+                                                               divisor, scale);
     else
-        dense_gemm_kernel<2, 2, false><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, nullptr);
+        dense_gemm_kernel<2, 2, kOut><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, c_bf16,
+                                                               divisor, scale);
+}
+
+}  // namespace
+
+hipError_t launch_dense_gemm(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
+                             uint32_t k, float* c_f32, uint16_t* c_bf16, hipStream_t stream) {
+    if (c_bf16 != nullptr)
+        launch_dense_tiles<DenseOut::kBf16>(a, b, m, n, k, nullptr, c_bf16, 1.0f, 1.0f, stream);
+    else
+        launch_dense_tiles<DenseOut::kF32>(a, b, m, n, k, c_f32, nullptr, 1.0f, 1.0f, stream);
+    return hipGetLastError();
+}
+
+hipError_t launch_dense_gemm_act(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
+                                 uint32_t k, bool silu, float divisor, float scale,
+                                 uint16_t* c_bf16, hipStream_t stream) {
+    if (silu)
+        launch_dense_tiles<DenseOut::kBf16Silu>(a, b, m, n, k, nullptr, c_bf16, divisor, scale,
+                                                stream);
+    else
+        launch_dense_tiles<DenseOut::kBf16Sigmoid>(a, b, m, n, k, nullptr, c_bf16, divisor,
+                                                   scale, stream);
     return hipGetLastError();
 }
 

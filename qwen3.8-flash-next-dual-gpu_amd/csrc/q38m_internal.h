@@ -105,12 +105,36 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
 // dense bf16 GEMMs (q38m_dense.hip): C = A * B^T, K contiguous in both
 hipError_t launch_dense_gemm(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
                              uint32_t k, float* c_f32, uint16_t* c_bf16, hipStream_t stream);
+// C = act(bf16(A * B^T)): silu or sigmoid of the bf16 product / divisor, * scale
+hipError_t launch_dense_gemm_act(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
+                                 uint32_t k, bool silu, float divisor, float scale,
+                                 uint16_t* c_bf16, hipStream_t stream);
 size_t shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter);
 hipError_t launch_shared_expert(const uint16_t* hidden, const uint16_t* w_gate,
                                 const uint16_t* w_up, const uint16_t* w_down,
                                 const uint16_t* w_out_gate, uint32_t tokens, uint32_t inter,
                                 void* scratch, uint16_t* shared_output, uint16_t* shared_gate,
                                 hipStream_t stream);
+
+// hyper-connection prepare/finish (q38m_hyper.hip); hidden % 8 == 0
+hipError_t launch_hyper_repeat(const uint16_t* embedding, uint16_t* hyper, uint32_t tokens,
+                               uint32_t hidden, hipStream_t stream);
+hipError_t launch_hyper_norm(const uint16_t* hyper, const uint16_t* weight,
+                             const uint16_t* inject, uint32_t tokens, uint32_t hidden,
+                             uint16_t* normalized, uint16_t* injection, hipStream_t stream);
+hipError_t launch_hyper_elementwise(const uint16_t* in, uint16_t* out, uint64_t elements,
+                                    float divisor, float scale, bool silu, hipStream_t stream);
+hipError_t launch_hyper_mix(const uint16_t* normalized, const uint16_t* mix, uint16_t* mixed,
+                            uint32_t tokens, uint32_t hidden, hipStream_t stream);
+hipError_t launch_hyper_inject(const uint16_t* original, const uint16_t* block,
+                               const uint16_t* injection, uint16_t* output, uint32_t tokens,
+                               uint32_t hidden, hipStream_t stream);
+size_t hyper_prepare_scratch_bytes(uint32_t tokens, uint32_t hidden, uint32_t low_rank);
+hipError_t launch_hyper_prepare(const uint16_t* hyper, const uint16_t* norm_weight,
+                                const uint16_t* mix_down, const uint16_t* mix_up,
+                                const uint16_t* inject, uint32_t tokens, uint32_t hidden,
+                                uint32_t low_rank, void* scratch, uint16_t* mixed,
+                                uint16_t* injection, hipStream_t stream);
 
 // layout and synthetic data (q38m_layout.hip)
 hipError_t launch_repack(const q38m_expert_weights_v1& src,

@@ -205,7 +205,7 @@ def test_dense_validation(q38m):
     # a, b, m, n, k, c_f32, c_bf16
     good = [0x1000, 0x2000, 64, 512, 2048, 0x3000, None]
     for i, bad in [(0, None), (1, None), (2, 0), (3, 0), (4, 0), (4, 48), (5, None),
-                   (2, 65535 * 64 + 1), (0, 0x1008), (1, 0x2002)]:
+                   (2, 65535 * 32 + 1), (0, 0x1008), (1, 0x2002)]:
         args = list(good)
         args[i] = bad
         with pytest.raises(q38m.InvalidArgument):
@@ -228,6 +228,24 @@ def test_dense_validation(q38m):
         with pytest.raises(q38m.InvalidArgument):
             q38m.call("q38m_moe_shared_expert_v1", *args, None, 0)
     assert q38m.lib().q38m_moe_shared_expert_scratch_bytes(8, 512) == 3 * 8 * 512 * 2
+
+
+def test_hyper_validation(q38m):
+    # hyper, norm_weight, mix_down, mix_up, inject, tokens, hidden, low_rank, scratch, mixed, injection
+    good = [0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 8, 2560, 320, 0x6000, 0x7000, 0x8000]
+    for i, bad in [(0, None), (2, None), (5, 0), (6, 0), (6, 2564), (6, 8200), (7, 0), (7, 300),
+                   (8, None), (9, None), (10, None), (0, 0x1008), (4, 0x5004)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_hyper_prepare_v1", *args, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # element count not a multiple of 8
+        q38m.call("q38m_hyper_sigmoid_bf16", 0x1000, 0x2000, 3, 5, 1.0, 1.0, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # divisor must be positive
+        q38m.call("q38m_hyper_silu_scaled_bf16", 0x1000, 0x2000, 8, 320, 0.0, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_hyper_inject_bf16", 0x1000, 0x2000, None, 0x3000, 8, 2560, None, 0)
+    assert q38m.lib().q38m_hyper_prepare_scratch_bytes(8, 2560, 320) == 2 * 8 * 4 * 2560 * 2 + 8 * 320 * 2
 
 
 def test_decode_and_step_validation(q38m):
