@@ -158,6 +158,16 @@ int q38m_topk_router_f32(const float* logits, int32_t* expert_ids,
                          uint32_t experts, uint32_t top_k, int normalize_top_k,
                          void* stream, int device);
 
+/* cuda_topk_router_bf16, include/q38/cuda_kernels.h:83-91: the same
+ * selection and weights as q38m_topk_router_f32 on bf16 logits (raw words),
+ * the type the reference's router GEMM writes.  bf16 widens to fp32
+ * exactly, so the result equals q38m_topk_router_f32 on the widened
+ * logits.  Same limits as q38m_topk_router_f32. */
+int q38m_topk_router_bf16(const uint16_t* logits, int32_t* expert_ids,
+                          float* expert_weights, uint32_t tokens,
+                          uint32_t experts, uint32_t top_k, int normalize_top_k,
+                          void* stream, int device);
+
 /* Top-10 routing and int8 activation quantisation in one launch (one
  * workgroup per token): cuda_topk_router_bf16 (include/q38/cuda_kernels.h:
  * 83-91; 512 experts, normalised) fused with the per-token quantisation

@@ -151,7 +151,17 @@ inline void cuda_moe_combine_shared_bf16(const std::uint16_t* routed_output,
                                        stream, device));
 }
 
-// Router top-k over fp32 logits (the reference takes bf16 logits).
+// cuda_topk_router_bf16 (include/q38/cuda_kernels.h:83-91): same name and
+// arguments as the reference.
+inline void cuda_topk_router_bf16(const std::uint16_t* logits, std::int32_t* expert_ids,
+                                  float* expert_weights, std::uint32_t tokens,
+                                  std::uint32_t experts, std::uint32_t top_k,
+                                  bool normalize_top_k, void* stream, int device) {
+    check(q38m_topk_router_bf16(logits, expert_ids, expert_weights, tokens, experts, top_k,
+                                normalize_top_k ? 1 : 0, stream, device));
+}
+
+// Router top-k over fp32 logits (the BASELINE router output).
 inline void cuda_topk_router_f32(const float* logits, std::int32_t* expert_ids,
                                  float* expert_weights, std::uint32_t tokens,
                                  std::uint32_t experts, std::uint32_t top_k,

@@ -118,6 +118,7 @@ SIGNATURES = {
     "q38m_moe_route_plan_bytes_v1": (_SZ, [_U32]),
     "q38m_moe_route_plan_storage_v1": (_INT, [_P, _SZ, _U32, ctypes.POINTER(RoutePlan)]),
     "q38m_topk_router_f32": (_INT, [_P, _P, _P, _U32, _U32, _U32, _INT, _P, _INT]),
+    "q38m_topk_router_bf16": (_INT, [_P, _P, _P, _U32, _U32, _U32, _INT, _P, _INT]),
     "q38m_moe_route_quantize_v1": (_INT, [_P, _P, _U32, _P, _P, _P, _P, _P, _INT]),
     "q38m_moe_build_route_plan_v1": (_INT, [_P, _U32, ctypes.POINTER(RoutePlan), _U32, _P, _INT]),
     "q38m_moe_pack_hidden_v1": (_INT, [_P, _P, _U32, _U32, _P, _P, _INT]),

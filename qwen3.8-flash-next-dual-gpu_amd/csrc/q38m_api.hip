@@ -157,6 +157,22 @@ int q38m_topk_router_f32(const float* logits, int32_t* expert_ids, float* expert
                   "topk_kernel");
 }
 
+int q38m_topk_router_bf16(const uint16_t* logits, int32_t* expert_ids, float* expert_weights,
+                          uint32_t tokens, uint32_t experts, uint32_t top_k,
+                          int normalize_top_k, void* stream, int device) {
+    if (!logits || !expert_ids || !expert_weights || tokens == 0 || experts == 0 ||
+        experts % 64u != 0u || experts > 1024u || top_k == 0 || top_k > experts || top_k > 32u)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid top-k router buffers");
+    if (int rc = select_device(device)) return rc;
+    if (experts == Q38M_ROUTE_EXPERTS && top_k <= Q38M_ROUTE_TOPK && normalize_top_k)
+        return finish(q38m::launch_route_bf16(logits, tokens, top_k, expert_ids, expert_weights,
+                                              as_stream(stream)),
+                      "route_quantize_kernel");
+    return finish(q38m::launch_topk(logits, expert_ids, expert_weights, tokens, experts, top_k,
+                                    normalize_top_k, as_stream(stream)),
+                  "topk_kernel");
+}
+
 int q38m_moe_route_quantize_v1(const float* logits, const uint16_t* hidden, uint32_t tokens,
                                int32_t* expert_ids, float* expert_weights, int8_t* xq, float* xs,
                                void* stream, int device) {

@@ -54,6 +54,13 @@ hipError_t launch_down_w4g32_wide(const void* data, const void* scales, const in
 hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
                        uint32_t tokens, uint32_t experts, uint32_t top_k,
                        int normalize, hipStream_t stream);
+// bf16 logits (uint16_t words)
+hipError_t launch_topk(const uint16_t* logits, int32_t* ids, float* weights,
+                       uint32_t tokens, uint32_t experts, uint32_t top_k,
+                       int normalize, hipStream_t stream);
+// 512 bf16 logits per token, top_k <= 10, normalised (ranked-key kernel)
+hipError_t launch_route_bf16(const uint16_t* logits, uint32_t tokens, uint32_t top_k,
+                             int32_t* ids, float* weights, hipStream_t stream);
 // 512 experts, top_k <= 10, normalised; hidden may be null (top-k only)
 hipError_t launch_route_quantize(const float* logits, const uint16_t* hidden, uint32_t tokens,
                                 uint32_t top_k, int32_t* ids, float* weights, int8_t* xq,

@@ -18,20 +18,28 @@ __device__ __forceinline__ bool better(float v, int id, float ov, int oid) {
     return v > ov || (v == ov && id < oid);
 }
 
-template <int kPerLane>
+// Router logits are fp32 (the BASELINE router output) or bf16 words (the
+// reference's router writes bf16 logits, cuda_topk_router_bf16); bf16 widens
+// to fp32 exactly, so both run the same fp32 selection.
+__device__ __forceinline__ float logit_at(const float* row, size_t i) { return row[i]; }
+__device__ __forceinline__ float logit_at(const uint16_t* row, size_t i) {
+    return bf16_to_f32(row[i]);
+}
+
+template <int kPerLane, typename Logit>
 __global__ __launch_bounds__(256) void topk_kernel(
-    const float* __restrict__ logits, uint32_t tokens, uint32_t experts,
+    const Logit* __restrict__ logits, uint32_t tokens, uint32_t experts,
     uint32_t top_k, int normalize, int32_t* __restrict__ ids,
     float* __restrict__ weights) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t token = blockIdx.x * 4u + (threadIdx.x >> 6);
     if (token >= tokens) return;
-    const float* row = logits + static_cast<size_t>(token) * experts;
+    const Logit* row = logits + static_cast<size_t>(token) * experts;
     float v[kPerLane];
 #pragma unroll
     for (int j = 0; j < kPerLane; ++j) {
         const uint32_t e = lane + 64u * j;
-        v[j] = e < experts ? row[e] : -__builtin_huge_valf();
+        v[j] = e < experts ? logit_at(row, e) : -__builtin_huge_valf();
     }
     uint32_t taken = 0;
     float mine_v = 0.0f;
@@ -93,8 +101,9 @@ __global__ __launch_bounds__(256) void topk_kernel(
 // the token's 2048-wide row by waves 0-3 (the same arithmetic as
 // quantize_rows_kernel).  Replaces a top-k launch and a quantisation launch.
 // ---------------------------------------------------------------------------
+template <typename Logit>
 __global__ __launch_bounds__(kSelectThreads) void route_quantize_kernel(
-    const float* __restrict__ logits, const uint16_t* __restrict__ hidden, uint32_t top_k,
+    const Logit* __restrict__ logits, const uint16_t* __restrict__ hidden, uint32_t top_k,
     int32_t* __restrict__ ids, float* __restrict__ weights, int8_t* __restrict__ xq,
     float* __restrict__ xs) {
     __shared__ SelectLds select_lds;
@@ -106,7 +115,7 @@ __global__ __launch_bounds__(kSelectThreads) void route_quantize_kernel(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const bool quantize = hidden != nullptr;
     float logit = 0.0f;
-    if (wave < 8u) logit = logits[static_cast<size_t>(token) * kExperts + t];
+    if (wave < 8u) logit = logit_at(logits, static_cast<size_t>(token) * kExperts + t);
     uint4 hv = make_uint4(0u, 0u, 0u, 0u);
     if (quantize && wave < 4u)
         hv = reinterpret_cast<const uint4*>(hidden + static_cast<size_t>(token) * kHidden)[t];
@@ -390,9 +399,12 @@ __global__ void plan_hash_kernel(const int32_t* __restrict__ expert_ids,
 
 }  // namespace
 
-hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
-                       uint32_t tokens, uint32_t experts, uint32_t top_k,
-                       int normalize, hipStream_t stream) {
+namespace {
+
+template <typename Logit>
+hipError_t launch_topk_any(const Logit* logits, int32_t* ids, float* weights, uint32_t tokens,
+                           uint32_t experts, uint32_t top_k, int normalize,
+                           hipStream_t stream) {
     const dim3 grid((tokens + 3u) / 4u);
     const uint32_t per_lane = (experts + 63u) / 64u;
     if (per_lane <= 8u)
@@ -404,11 +416,33 @@ hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
     return hipGetLastError();
 }
 
+}  // namespace
+
+hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
+                       uint32_t tokens, uint32_t experts, uint32_t top_k,
+                       int normalize, hipStream_t stream) {
+    return launch_topk_any(logits, ids, weights, tokens, experts, top_k, normalize, stream);
+}
+
+hipError_t launch_topk(const uint16_t* logits, int32_t* ids, float* weights,
+                       uint32_t tokens, uint32_t experts, uint32_t top_k,
+                       int normalize, hipStream_t stream) {
+    return launch_topk_any(logits, ids, weights, tokens, experts, top_k, normalize, stream);
+}
+
 hipError_t launch_route_quantize(const float* logits, const uint16_t* hidden, uint32_t tokens,
                                 uint32_t top_k, int32_t* ids, float* weights, int8_t* xq,
                                 float* xs, hipStream_t stream) {
     route_quantize_kernel<<<tokens, kSelectThreads, 0, stream>>>(logits, hidden, top_k, ids,
                                                                  weights, xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_bf16(const uint16_t* logits, uint32_t tokens, uint32_t top_k,
+                             int32_t* ids, float* weights, hipStream_t stream) {
+    route_quantize_kernel<<<tokens, kSelectThreads, 0, stream>>>(
+        logits, static_cast<const uint16_t*>(nullptr), top_k, ids, weights,
+        static_cast<int8_t*>(nullptr), static_cast<float*>(nullptr));
     return hipGetLastError();
 }
 

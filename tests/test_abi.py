@@ -164,6 +164,12 @@ def test_routing_and_quant_validation(q38m):
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_topk_router_f32", 0x1000, 0x2000, 0x3000, 4, 500, 10, 1, None, 0)
     with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_topk_router_bf16", 0x1000, 0x2000, 0x3000, 4, 512, 33, 1, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_topk_router_bf16", 0x1000, 0x2000, 0x3000, 4, 500, 10, 1, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call("q38m_topk_router_bf16", None, 0x2000, 0x3000, 4, 512, 10, 1, None, 0)
+    with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_quantize_rows_i8", 0x1000, 4, 1536, 0x2000, 0x3000, None, 0)
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_moe_reduce_top10_and_combine_shared_v1", 0x1000, 0x2000, 0x3000, None,

@@ -124,6 +124,52 @@ def run_topk(q38m, logits, top_k=10, normalize=True):
     return host(ids, np.int32).reshape(tokens, top_k), host(w, np.float32).reshape(tokens, top_k)
 
 
+def run_topk_bf16(q38m, words, top_k=10, normalize=True):
+    t = torch()
+    tokens, experts = words.shape
+    ids = t.empty(tokens * top_k, dtype=t.int32, device="cuda")
+    w = t.empty(tokens * top_k, dtype=t.float32, device="cuda")
+    ld = device(words.view(np.int16))
+    q38m.call("q38m_topk_router_bf16", ld.data_ptr(), ids.data_ptr(), w.data_ptr(),
+              tokens, experts, top_k, int(normalize), stream(), 0)
+    return host(ids, np.int32).reshape(tokens, top_k), host(w, np.float32).reshape(tokens, top_k)
+
+
+@pytest.mark.parametrize("case", ["synthetic", "ties", "reference_ties", "unnormalised",
+                                  "signed_zeros", "top4", "experts256"])
+def test_topk_bf16_bitwise(q38m, orc, case):
+    """cuda_topk_router_bf16's surface: bf16 logits (the reference router's
+    output type).  bf16 -> fp32 is exact, so the oracle runs on the widened
+    values; rounding fp32 logits to bf16 also creates many exact ties."""
+    rng = np.random.default_rng(31)
+    top_k, normalize, experts = 10, case != "unnormalised", 512
+    if case == "synthetic" or case == "unnormalised":
+        logits = orc.synth_logits(11, 2, 256)
+    elif case == "ties":
+        logits = rng.integers(-3, 3, (200, 512)).astype(np.float32) * np.float32(0.125)
+    elif case == "reference_ties":
+        with open(os.path.join(GOLDEN_DIR, "reference_topk_ties.json")) as f:
+            logits = np.array(json.load(f)["logits"], np.float32)
+    elif case == "signed_zeros":
+        logits = (-1.0 - np.abs(rng.standard_normal((64, 512)))).astype(np.float32)
+        for row in logits:
+            picks = rng.choice(512, 14, replace=False)
+            row[picks] = np.where(rng.random(14) < 0.5, np.float32(0.0), np.float32(-0.0))
+    elif case == "top4":
+        logits, top_k = orc.synth_logits(12, 2, 100), 4
+    else:
+        logits, top_k, experts = orc.synth_logits(13, 2, 100)[:, :256].copy(), 8, 256
+    words = orc.f32_to_bf16(logits).reshape(logits.shape[0], experts)
+    widened = (words.astype(np.uint32) << 16).view(np.float32)
+    ids, w = run_topk_bf16(q38m, words, top_k=top_k, normalize=normalize)
+    wids, ww = orc.topk(widened, top_k=top_k, normalize=normalize)
+    assert np.array_equal(ids, wids)
+    assert np.array_equal(w.view(np.uint32), ww.view(np.uint32))
+    fids, fw = run_topk(q38m, widened, top_k=top_k, normalize=normalize)
+    assert np.array_equal(ids, fids)
+    assert np.array_equal(w.view(np.uint32), fw.view(np.uint32))
+
+
 @pytest.mark.parametrize("case", ["synthetic", "zipf", "ties", "reference_ties", "unnormalised",
                                   "signed_zeros", "top4", "experts256"])
 def test_topk_bitwise(q38m, orc, case):
