@@ -12,12 +12,13 @@ one entry point at a time, the roofline of the dominant
 kernel, the step's fraction of int8 MFMA and HBM peaks, batch-1 decode
 HBM GB/s through config 3's 48-layer stack, the router and shared-expert
 GEMMs, the chunk path (q38m_moe_prefill_wide_v1) on config 4 and one
-config-5 layer beside the slab path, the hyper-connection prepare/finish
+config-5 layer beside the slab path, config 5 end to end (32,768 tokens
+through all 48 layers, layer-major and slab-major), the hyper-connection prepare/finish
 around the MoE step (q38m_hyper_prepare_v1, q38m_hyper_inject_bf16) on the
 512-token slab, and the CPU oracle timed on this host as the baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
-       [--no-quantizer] [--no-dense] [--no-chunks] [--no-hyper]
+       [--no-quantizer] [--no-dense] [--no-chunks] [--no-stack] [--no-hyper]
 """
 import argparse
 import ctypes
@@ -57,6 +58,8 @@ def main():
     parser.add_argument("--no-dense", action="store_true")
     parser.add_argument("--no-chunks", action="store_true")
     parser.add_argument("--no-hyper", action="store_true")
+    parser.add_argument("--no-stack", action="store_true",
+                        help="skip the full 48-layer config-5 stack")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
@@ -246,6 +249,9 @@ def main():
 
     if not args.no_chunks:
         result["chunks"] = bench_chunks(q38m, W, torch)
+
+    if not args.no_stack:
+        result["config5_stack"] = bench_config5_stack(q38m, W, torch)
 
     if not args.no_hyper:
         result["hyper"] = bench_hyper(q38m, torch, T, args.steps)
@@ -540,6 +546,96 @@ def bench_chunks(q38m, W, torch):
         del gu, dn, hidden, logits, wide, slab, out_w, out_s
         torch.cuda.empty_cache()
     return out
+
+
+def bench_config5_stack(q38m, W, torch, passes=2):
+    """Config 5 end to end: 32,768 tokens through all 48 MoE layers
+    (even layers all-W4 g32, odd layers W4 g32 gate/up + W8 down; per-layer
+    N(0,1) router logits with the Zipf 0.8 bias; hidden = bf16(hidden +
+    moe(hidden)) between layers).  Timed layer-major through
+    q38m_moe_prefill_wide_v1 (one call per layer over all tokens) and
+    slab-major as BASELINE describes it (64 slabs x 512 tokens through
+    q38m_moe_prefill_v1 per layer); the two schedules must give the same
+    final hidden states bit for bit.  ops = 48 x 10T x 2(2IH + HI)."""
+    spec = W.CONFIGS[5]
+    seed, layers, tokens = spec["seed"], spec["layers"], spec["tokens"]
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    sh = torch.cuda.current_stream().cuda_stream
+    stack, weight_bytes = [], 0
+    logits = torch.empty(layers, tokens, W.EXPERTS, dtype=torch.float32, device="cuda")
+    for layer in range(layers):
+        gfmt, dfmt = W.layer_policy(5, layer)
+        gu_tag, dn_tag, _, l_tag = W.layer_tags(layer)
+        gu_rm = q38m.synth_weights(seed, gu_tag, fmt[gfmt[1]], gfmt[2], W.EXPERTS, 2 * W.INTER,
+                                   W.HIDDEN, gfmt[3])
+        gu = q38m.repack(gu_rm, paired=True)
+        del gu_rm
+        dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dfmt[1]], dfmt[2], W.EXPERTS, W.HIDDEN,
+                                   W.INTER, dfmt[3])
+        dn = q38m.repack(dn_rm)
+        del dn_rm
+        stack.append((gu, dn))
+        weight_bytes += gu.nbytes + dn.nbytes
+        bias_t = torch.tensor(W.bias_for(5, layer), dtype=torch.float32, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, l_tag, logits[layer].numel(), logits[layer],
+                        bias=bias_t)
+    _, _, h_tag, _ = W.layer_tags(0)
+    h0 = torch.empty(tokens, W.HIDDEN, dtype=torch.int16, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, h_tag, h0.numel(), h0)
+    state = [torch.empty_like(h0), torch.empty_like(h0)]
+    moe_out = torch.empty_like(h0)
+    wide = q38m.WideWorkspace_(tokens)
+    slab = q38m.PrefillWorkspace_(512)
+
+    def layer_major():
+        state[0].copy_(h0)
+        for layer, (gu, dn) in enumerate(stack):
+            src, dst = state[layer % 2], state[(layer + 1) % 2]
+            q38m.call("q38m_moe_prefill_wide_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                      src.data_ptr(), logits[layer].data_ptr(), tokens, ctypes.byref(wide.wide),
+                      None, None, moe_out.data_ptr(), sh, 0)
+            q38m.call("q38m_residual_add_bf16", src.data_ptr(), moe_out.data_ptr(),
+                      dst.data_ptr(), src.numel(), sh, 0)
+        return state[layers % 2]
+
+    def slab_major():
+        state[0].copy_(h0)
+        for layer, (gu, dn) in enumerate(stack):
+            src, dst = state[layer % 2], state[(layer + 1) % 2]
+            for s0 in range(0, tokens, 512):
+                q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                          src[s0:].data_ptr(), logits[layer, s0:].data_ptr(), 512,
+                          ctypes.byref(slab.ws), None, None, moe_out[s0:].data_ptr(), sh, 0)
+            q38m.call("q38m_residual_add_bf16", src.data_ptr(), moe_out.data_ptr(),
+                      dst.data_ptr(), src.numel(), sh, 0)
+        return state[layers % 2]
+
+    def timed(fn, reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            result = fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / reps, result
+
+    layer_major()  # warm-up
+    chunk_ms, final = timed(layer_major, passes)
+    chunk_final = final.clone()
+    slab_ms, final = timed(slab_major, 1)
+    same = bool(torch.equal(chunk_final, final))
+    ops = layers * tokens * W.TOPK * W.ops_per_route()
+    del stack, logits, state, moe_out, wide, slab
+    torch.cuda.empty_cache()
+    return {"workload": spec["name"], "tokens": tokens, "layers": layers,
+            "policy": "even layers all-W4 g32, odd layers W4 g32 gate/up + W8 down",
+            "resident_weight_GB": round(weight_bytes / 1e9, 2), "ops": ops,
+            "layer_major_ms": round(chunk_ms, 2),
+            "layer_major_tok_s": round(tokens / chunk_ms * 1e3, 1),
+            "layer_major_int8_mfma_frac": round(ops / (chunk_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+                                                4),
+            "slab_major_ms": round(slab_ms, 2),
+            "slab_major_tok_s": round(tokens / slab_ms * 1e3, 1),
+            "speedup": round(slab_ms / chunk_ms, 2), "outputs_equal": same}
 
 
 def bench_weight_pipeline(q38m, W, torch, reps=5):
