@@ -445,7 +445,9 @@ void gate_up_w4g32_wide_kernel(
 // 16-channel output tiles and walks K in the outer loop: a K block's kRows
 // A fragments are read from LDS once and multiplied into every owned tile
 // (v_mfma_i32_16x16x64_i8), with the tiles' weight fragments two K blocks
-// ahead.  kRows (8, 4, 2 or 1 row tiles) is picked per task from its row
+// ahead.  One A fragment is live at a time (row by row): holding all kRows
+// of them took the kernel to 256 VGPRs with spills (1.07 ms vs 1.00 ms on
+// a config-5 layer).  kRows (8, 4, 2 or 1 row tiles) is picked per task from its row
 // count.  o = ((float)acc * ws[e][c]) * sm[r], as the slab kernel.
 template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kRows>
 __device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
@@ -474,14 +476,13 @@ __device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
 #pragma unroll
     for (uint32_t kb = 0; kb < kBlocks; ++kb) {
         load_w(kb + 2u, wq[(kb + 2u) % 3u]);
-        v4i a[kRows];
 #pragma unroll
-        for (uint32_t r = 0; r < kRows; ++r) a[r] = as_v4i(a_lds[(kb * kRowTiles + r) * 64u + lane]);
+        for (uint32_t r = 0; r < kRows; ++r) {
+            const v4i a = as_v4i(a_lds[(kb * kRowTiles + r) * 64u + lane]);
 #pragma unroll
-        for (uint32_t t = 0; t < kTilesPerWave; ++t)
-#pragma unroll
-            for (uint32_t r = 0; r < kRows; ++r)
-                acc[t][r] = mfma_i8_16x16x64(a[r], as_v4i(wq[kb % 3u][t]), acc[t][r]);
+            for (uint32_t t = 0; t < kTilesPerWave; ++t)
+                acc[t][r] = mfma_i8_16x16x64(a, as_v4i(wq[kb % 3u][t]), acc[t][r]);
+        }
     }
 #pragma unroll
     for (uint32_t t = 0; t < kTilesPerWave; ++t) {
