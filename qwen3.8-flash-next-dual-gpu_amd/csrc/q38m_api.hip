@@ -505,9 +505,8 @@ int q38m_moe_prefill_wide_v1(const q38m_expert_weights_v1* gate_up,
     const uint32_t tasks = q38m::max_tasks_wide(tokens);
     hipError_t status = hipSuccess;
     if (logits)
-        status = q38m::launch_route_quantize(logits, hidden, tokens, Q38M_ROUTE_TOPK,
-                                             ws->expert_ids, ws->expert_weights, ws->xq, ws->xs,
-                                             s);
+        status = q38m::launch_route_quantize_wave(logits, hidden, tokens, ws->expert_ids,
+                                                  ws->expert_weights, ws->xq, ws->xs, s);
     else
         status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws->xq, ws->xs, s);
     if (status == hipSuccess)

@@ -58,6 +58,11 @@ hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
 hipError_t launch_topk(const uint16_t* logits, int32_t* ids, float* weights,
                        uint32_t tokens, uint32_t experts, uint32_t top_k,
                        int normalize, hipStream_t stream);
+// 512 logits per token, top-10, normalised, plus the token's int8 row: one
+// wave per token (the throughput form for chunks)
+hipError_t launch_route_quantize_wave(const float* logits, const uint16_t* hidden,
+                                     uint32_t tokens, int32_t* ids, float* weights, int8_t* xq,
+                                     float* xs, hipStream_t stream);
 // 512 bf16 logits per token, top_k <= 10, normalised (ranked-key kernel)
 hipError_t launch_route_bf16(const uint16_t* logits, uint32_t tokens, uint32_t top_k,
                              int32_t* ids, float* weights, hipStream_t stream);

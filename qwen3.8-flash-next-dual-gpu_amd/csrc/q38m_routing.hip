@@ -26,25 +26,17 @@ __device__ __forceinline__ float logit_at(const uint16_t* row, size_t i) {
     return bf16_to_f32(row[i]);
 }
 
-template <int kPerLane, typename Logit>
-__global__ __launch_bounds__(256) void topk_kernel(
-    const Logit* __restrict__ logits, uint32_t tokens, uint32_t experts,
-    uint32_t top_k, int normalize, int32_t* __restrict__ ids,
-    float* __restrict__ weights) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t token = blockIdx.x * 4u + (threadIdx.x >> 6);
-    if (token >= tokens) return;
-    const Logit* row = logits + static_cast<size_t>(token) * experts;
-    float v[kPerLane];
-#pragma unroll
-    for (int j = 0; j < kPerLane; ++j) {
-        const uint32_t e = lane + 64u * j;
-        v[j] = e < experts ? logit_at(row, e) : -__builtin_huge_valf();
-    }
+// The wave's top_k by (value desc, id asc) over v[j] = logit of expert
+// lane + 64j: lane r < top_k receives the rank-r value and id; every lane
+// receives the rank-0 value.
+template <int kPerLane>
+__device__ __forceinline__ void wave_topk(const float (&v)[kPerLane], uint32_t experts,
+                                          uint32_t top_k, uint32_t lane, float& mine_v,
+                                          int& mine_id, float& top_v) {
     uint32_t taken = 0;
-    float mine_v = 0.0f;
-    int mine_id = 0;
-    float top_v = 0.0f;
+    mine_v = 0.0f;
+    mine_id = 0;
+    top_v = 0.0f;
     for (uint32_t rank = 0; rank < top_k; ++rank) {
         float best_v = -__builtin_huge_valf();
         int best_id = 0x7fffffff;
@@ -74,6 +66,26 @@ __global__ __launch_bounds__(256) void topk_kernel(
         }
         if (rank == 0) top_v = best_v;
     }
+}
+
+template <int kPerLane, typename Logit>
+__global__ __launch_bounds__(256) void topk_kernel(
+    const Logit* __restrict__ logits, uint32_t tokens, uint32_t experts,
+    uint32_t top_k, int normalize, int32_t* __restrict__ ids,
+    float* __restrict__ weights) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t token = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (token >= tokens) return;
+    const Logit* row = logits + static_cast<size_t>(token) * experts;
+    float v[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+        const uint32_t e = lane + 64u * j;
+        v[j] = e < experts ? logit_at(row, e) : -__builtin_huge_valf();
+    }
+    float mine_v, top_v;
+    int mine_id;
+    wave_topk<kPerLane>(v, experts, top_k, lane, mine_v, mine_id, top_v);
     const float numerator = lane < top_k ? exp_q(mine_v - top_v) : 0.0f;
     float denominator = 0.0f;
     if (normalize) {
@@ -92,6 +104,63 @@ __global__ __launch_bounds__(256) void topk_kernel(
         ids[static_cast<size_t>(token) * top_k + lane] = mine_id;
         weights[static_cast<size_t>(token) * top_k + lane] = numerator / denominator;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Routing + activation quantisation for chunks, one wave per token (four per
+// workgroup): the top-10 of the token's 512 logits by wave_topk, normalised
+// in rank order, and the int8 quantisation of its 2048-wide row, lane l
+// owning elements 8l + 512c .. +7 (c = 0..3).  The logit and hidden loads
+// go out together.  Same results as route_quantize_kernel bit for bit;
+// at tens of thousands of tokens it keeps 32 tokens in flight per CU where
+// the ten-wave workgroups of route_quantize_kernel keep three.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void route_quantize_wave_kernel(
+    const float* __restrict__ logits, const uint16_t* __restrict__ hidden, uint32_t tokens,
+    int32_t* __restrict__ ids, float* __restrict__ weights, int8_t* __restrict__ xq,
+    float* __restrict__ xs) {
+    constexpr uint32_t kChunks = kHidden / 512u;
+    constexpr int kPerLane = static_cast<int>(kExperts / 64u);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t token = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (token >= tokens) return;
+    const float* row = logits + static_cast<size_t>(token) * kExperts;
+    const uint4* src = reinterpret_cast<const uint4*>(hidden + static_cast<size_t>(token) * kHidden);
+    float v[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) v[j] = row[lane + 64u * j];
+    uint4 h[kChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) h[c] = src[c * 64u + lane];
+
+    float mine_v, top_v;
+    int mine_id;
+    wave_topk<kPerLane>(v, kExperts, kTopK, lane, mine_v, mine_id, top_v);
+    const float numerator = lane < kTopK ? exp_q(mine_v - top_v) : 0.0f;
+    float denominator = 0.0f;
+    for (uint32_t rank = 0; rank < kTopK; ++rank)
+        denominator += __shfl(numerator, static_cast<int>(rank), 64);
+    if (lane < kTopK) {
+        ids[static_cast<size_t>(token) * kTopK + lane] = mine_id;
+        weights[static_cast<size_t>(token) * kTopK + lane] = numerator / denominator;
+    }
+
+    float amax = 0.0f;
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t w[4] = {h[c].x, h[c].y, h[c].z, h[c].w};
+        amax = fmaxf(amax, row_absmax8(w));
+    }
+    amax = wave_max_f32(amax);
+    float s = amax / 127.0f;
+    if (s == 0.0f) s = 1.0f;
+    uint2* dst = reinterpret_cast<uint2*>(xq + static_cast<size_t>(token) * kHidden);
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t w[4] = {h[c].x, h[c].y, h[c].z, h[c].w};
+        dst[c * 64u + lane] = quantize8(w, s);
+    }
+    if (lane == 0) xs[token] = s;
 }
 
 // ---------------------------------------------------------------------------
@@ -435,6 +504,14 @@ hipError_t launch_route_quantize(const float* logits, const uint16_t* hidden, ui
                                 float* xs, hipStream_t stream) {
     route_quantize_kernel<<<tokens, kSelectThreads, 0, stream>>>(logits, hidden, top_k, ids,
                                                                  weights, xq, xs);
+    return hipGetLastError();
+}
+
+hipError_t launch_route_quantize_wave(const float* logits, const uint16_t* hidden,
+                                     uint32_t tokens, int32_t* ids, float* weights, int8_t* xq,
+                                     float* xs, hipStream_t stream) {
+    route_quantize_wave_kernel<<<(tokens + 3u) / 4u, 256, 0, stream>>>(logits, hidden, tokens,
+                                                                      ids, weights, xq, xs);
     return hipGetLastError();
 }
 

@@ -118,18 +118,23 @@ __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32
     __syncthreads();
 }
 
-// int8 quantisation of one 2048-wide bf16 row held by threads 0..255 (eight
-// elements each): s = absmax/127 (1 if zero), q = clamp(rint(x/s), +-127)
-// (tools/q38_artifact_compiler.py:214-222).  Step 1 (before a barrier):
-// the per-wave absmax of waves 0..3 into amax_lds.
-__device__ __forceinline__ void row_absmax_partial(const uint32_t (&hw)[4], float* amax_lds) {
+// max |x| over eight bf16 values (one 16-byte chunk)
+__device__ __forceinline__ float row_absmax8(const uint32_t (&hw)[4]) {
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] & 0xffffu)));
         amax = fmaxf(amax, fabsf(bf16_to_f32(hw[i] >> 16)));
     }
-    amax = wave_max_f32(amax);
+    return amax;
+}
+
+// int8 quantisation of one 2048-wide bf16 row held by threads 0..255 (eight
+// elements each): s = absmax/127 (1 if zero), q = clamp(rint(x/s), +-127)
+// (tools/q38_artifact_compiler.py:214-222).  Step 1 (before a barrier):
+// the per-wave absmax of waves 0..3 into amax_lds.
+__device__ __forceinline__ void row_absmax_partial(const uint32_t (&hw)[4], float* amax_lds) {
+    const float amax = wave_max_f32(row_absmax8(hw));
     if ((threadIdx.x & 63u) == 0u) amax_lds[threadIdx.x >> 6] = amax;
 }
 
