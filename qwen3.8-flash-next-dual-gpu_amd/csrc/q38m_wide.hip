@@ -484,20 +484,23 @@ __device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
                 acc[t][r] = mfma_i8_16x16x64(a, as_v4i(wq[kb % 3u][t]), acc[t][r]);
         }
     }
+    // a row's kTilesPerWave adjacent 16-channel pieces go out in consecutive
+    // stores, so its 64*kTilesPerWave bytes meet in L2 as whole lines
+    float ws[kTilesPerWave];
 #pragma unroll
-    for (uint32_t t = 0; t < kTilesPerWave; ++t) {
-        const uint32_t channel = (tile0 + t) * 16u + n;
-        const float ws = f16_to_f32(ws_row[channel]);
+    for (uint32_t t = 0; t < kTilesPerWave; ++t) ws[t] = f16_to_f32(ws_row[(tile0 + t) * 16u + n]);
 #pragma unroll
-        for (uint32_t r = 0; r < kRows; ++r)
+    for (uint32_t r = 0; r < kRows; ++r)
 #pragma unroll
-            for (uint32_t i = 0; i < 4u; ++i) {
-                const uint32_t row = 16u * r + 4u * q + i;
-                if (row >= rows) continue;
-                out[static_cast<size_t>(p0 + row) * H + channel] =
-                    (static_cast<float>(acc[t][r][i]) * ws) * row_scale[row];
-            }
-    }
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t row = 16u * r + 4u * q + i;
+            if (row >= rows) continue;
+            const float sm = row_scale[row];
+            float* dst = out + static_cast<size_t>(p0 + row) * H + tile0 * 16u + n;
+#pragma unroll
+            for (uint32_t t = 0; t < kTilesPerWave; ++t)
+                dst[16u * t] = (static_cast<float>(acc[t][r][i]) * ws[t]) * sm;
+        }
 }
 
 template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
@@ -562,11 +565,15 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
 // Down, W4 group-32 (the all-W4 layer policy), over a task of up to 128
 // rows: the gate/up chain over K = I.  The mid rows are staged once in LDS
 // as [group][row tile][lane] 8-byte fragments; a workgroup of 16 waves
-// covers 32 output tiles, two per wave.  A wave streams its tiles' weights
+// covers 32 output tiles, two per wave, kStride tiles apart: the two
+// 64-byte halves of an output line come from neighbouring waves at about
+// the same time and meet in L2 (adjacent tiles in one wave were stored a
+// whole tile's chain apart, and 9 % of the route-output bytes went to HBM
+// twice).  A wave streams its tiles' weights
 // one quad ahead and runs the chain group by group with the
 // same pinned MFMA/v_cvt/v_fma interleave as the gate/up kernel, over kRows
 // (8, 4, 2 or 1) row tiles picked per task.
-template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kRows>
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kStride, uint32_t kRows>
 __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
                                                   const uint2* __restrict__ st,
                                                   const uint2* a_lds, const float* row_scale,
@@ -583,7 +590,8 @@ __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
     // expert; weights stream one quad ahead, across tile boundaries too
     auto load = [&](uint32_t t, uint32_t kq) {
         const uint32_t tt = t < kTilesPerWave ? t : kTilesPerWave - 1u;
-        return TileQuad{wt[(kq * kTiles + tt) * 64u], st[(kq * kTiles + tt) * 16u]};
+        return TileQuad{wt[(kq * kTiles + tt * kStride) * 64u],
+                        st[(kq * kTiles + tt * kStride) * 16u]};
     };
     TileQuad cur = load(0, 0);
 #pragma unroll 1
@@ -622,7 +630,7 @@ __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
           }
           cur = next;
         }
-        const uint32_t channel = (tile0 + t) * 16u + n;
+        const uint32_t channel = (tile0 + t * kStride) * 16u + n;
         // re-derived in every tile, so the 32 output addresses are not
         // hoisted out of the tile loop into registers
         uint32_t lane_row = 4u * q;
@@ -686,18 +694,23 @@ void down_w4g32_wide_kernel(
         row_scale[threadIdx.x] = threadIdx.x < rows ? ms[p0 + threadIdx.x] : 0.0f;
     __syncthreads();
 
-    const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
+    // wave w: tiles tile0 + t * kWaves
+    const uint32_t tile0 = blockIdx.x * kWaves * kTilesPerWave + wave;
     const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile0) * 64u + lane;
     const uint2* st = s + (static_cast<size_t>(e) * kQuads * kTiles + tile0) * 16u + n;
     const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
     if (tiles > 4u)
-        down_w4_wide_rows<H, I, kTilesPerWave, 8>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
+        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 8>(wt, st, a_lds, row_scale, rows, p0,
+                                                           tile0, out);
     else if (tiles > 2u)
-        down_w4_wide_rows<H, I, kTilesPerWave, 4>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
+        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 4>(wt, st, a_lds, row_scale, rows, p0,
+                                                           tile0, out);
     else if (tiles == 2u)
-        down_w4_wide_rows<H, I, kTilesPerWave, 2>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
+        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 2>(wt, st, a_lds, row_scale, rows, p0,
+                                                           tile0, out);
     else
-        down_w4_wide_rows<H, I, kTilesPerWave, 1>(wt, st, a_lds, row_scale, rows, p0, tile0, out);
+        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 1>(wt, st, a_lds, row_scale, rows, p0,
+                                                           tile0, out);
 }
 
 }  // namespace
