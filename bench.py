@@ -10,7 +10,8 @@ q38m_moe_prefill_v1.  Also reported: per-kernel durations from HIP events
 on the launch stream over a second timed run of the same kernels launched
 one entry point at a time, the roofline of the dominant
 kernel, the step's fraction of int8 MFMA and HBM peaks, batch-1 decode
-HBM GB/s through config 3's 48-layer stack, the router and shared-expert
+HBM GB/s through config 3's 48-layer stack, config 1 (64 tokens, all-W4)
+through the same entry point, the router and shared-expert
 GEMMs, the chunk path (q38m_moe_prefill_wide_v1) on config 4 and one
 config-5 layer beside the slab path, config 5 end to end (32,768 tokens
 through all 48 layers, layer-major and slab-major), the hyper-connection prepare/finish
@@ -238,6 +239,8 @@ def main():
         torch.cuda.synchronize()
         result["calibration_copy_bytes"] = src.numel()
 
+    result["config1"] = bench_config1(q38m, W, torch, args.steps)
+
     if not args.no_decode:
         result["decode"] = bench_decode(q38m, W, torch, args.decode_tokens)
 
@@ -344,6 +347,55 @@ def bench_decode(q38m, W, torch, tokens):
             "algorithmic_bytes_per_token": bytes_token, "launches_per_layer": 2,
             "entry_point": "q38m_moe_decode_v1", **graph_rate, "mode": "hip_graph",
             "eager": rate(ms_eager)}
+
+
+def bench_config1(q38m, W, torch, steps):
+    """Config 1: the 64-token all-W4 g32 layer (the reference's CPU-runnable
+    case) through q38m_moe_prefill_v1, K calls timed by wall clock.  Bytes:
+    every active expert's weights + hidden in/out + fp32 logits."""
+    spec = W.CONFIGS[1]
+    seed, T = spec["seed"], spec["tokens"]
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    gfmt, dfmt = W.layer_policy(1, 0)
+    gu_tag, dn_tag, h_tag, l_tag = W.layer_tags(0)
+    gu = q38m.repack(q38m.synth_weights(seed, gu_tag, fmt[gfmt[1]], gfmt[2], W.EXPERTS,
+                                        2 * W.INTER, W.HIDDEN, gfmt[3]), paired=True)
+    dn = q38m.repack(q38m.synth_weights(seed, dn_tag, fmt[dfmt[1]], dfmt[2], W.EXPERTS,
+                                        W.HIDDEN, W.INTER, dfmt[3]))
+    hidden = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
+    logits = torch.empty(T, W.EXPERTS, dtype=torch.float32, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, h_tag, hidden.numel(), hidden)
+    q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, l_tag, logits.numel(), logits)
+    wsb = q38m.PrefillWorkspace_(T)
+    out = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
+    sh = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                  hidden.data_ptr(), logits.data_ptr(), T, ctypes.byref(wsb.ws), None, None,
+                  out.data_ptr(), sh, 0)
+
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    base = wsb.buffer.data_ptr()
+    routes = T * W.TOPK
+    ids = wsb.buffer[wsb.ws.expert_ids - base:wsb.ws.expert_ids - base + 4 * routes]
+    active = int(torch.bincount(ids.view(torch.int32).long(), minlength=W.EXPERTS).gt(0).sum())
+    nbytes = (active * W.algorithmic_bytes_per_expert(gfmt, dfmt) + T * W.HIDDEN * 2 * 2 +
+              T * W.EXPERTS * 4)
+    ops = routes * W.ops_per_route()
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": spec["name"], "tokens": T, "active_experts": active,
+            "ms_per_step": round(ms, 4), "tok_s": round(T / ms * 1e3, 1),
+            "algorithmic_bytes": nbytes, "GBps": round(gbps, 1),
+            "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "int8_mfma_frac": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 5)}
 
 
 def bench_router_shared(q38m, W, torch, hidden, steps):
