@@ -110,35 +110,47 @@ typedef struct q38m_route_plan_v1 {
  * 21-38) with the group size and scale dtype of this build's formats. */
 #define Q38M_FORMAT_W4_SYM 2u /* int4 two's complement, even k in the low nibble */
 #define Q38M_FORMAT_W8_SYM 3u /* int8 */
-#define Q38M_SCALE_F16 1u
+#define Q38M_SCALE_F16 1u  /* IEEE binary16 scale words (the BASELINE format) */
+#define Q38M_SCALE_BF16 2u /* bfloat16 scale words (the reference artifact format,
+                              tools/q38_artifact_compiler.py:232) */
 #define Q38M_LAYOUT_ROW_MAJOR 0u   /* canonical artifact layout */
 #define Q38M_LAYOUT_MFMA16 2u      /* device layout for the 16x16 int8 MFMA kernels */
 #define Q38M_LAYOUT_MFMA16_PAIRED 3u /* MFMA16 with row tile t next to tile t+rows/32
-                                        (the gate/up halves), W4 group-32 only */
+                                        (the gate/up halves), W4 only */
 
 typedef struct q38m_expert_weights_v1 {
     const void* data;
     const void* scales;
     uint32_t format;      /* Q38M_FORMAT_* */
-    uint32_t group_size;  /* 32, or 0 = one scale per output channel */
-    uint32_t scale_dtype; /* Q38M_SCALE_F16 */
+    uint32_t group_size;  /* 32, 64, 128, or 0 = one scale per output channel */
+    uint32_t scale_dtype; /* Q38M_SCALE_F16 or Q38M_SCALE_BF16 */
     uint32_t layout;      /* Q38M_LAYOUT_* */
     uint32_t experts;     /* 512 */
     uint32_t rows;        /* output channels: 2*I for gate/up, H for down */
     uint32_t columns;     /* K: H for gate/up, I for down */
 } q38m_expert_weights_v1;
 
-/* Row-major layouts (artifact): W4 data [E][rows][cols/2], W8 data
- * [E][rows][cols]; fp16 scales [E][rows][cols/32] (group 32) or [E][rows]
- * (per channel).  MFMA16 layouts (produced by q38m_repack_expert_weights):
- *   W4 g32 data  [E][cols/128][slot][64 lanes][16 B], quad-major: for one
+/* Formats the grouped kernels run (prefill, chunk and decode alike):
+ * gate/up W4 in groups of 32, 64 or 128 (MFMA16_PAIRED); down W8 per
+ * channel or in groups of 64 or 128, or W4 in groups of 32, 64 or 128
+ * (MFMA16); fp16 or bf16 scale words.  The reference model's routed
+ * experts are W4 group-128 (interior layers) and W8 group-128 (edge layers,
+ * gate/up too) with bf16 scales (tools/q38_quant_policy.py:164-190); the
+ * BASELINE formats are W4 g32 / W8 per channel with fp16 scales.
+ * Per group g: y = fmaf((float)acc_g, s_g, y) in group order from 0, acc_g
+ * the group's exact int32 sum; per channel: y = (float)acc * s.
+ * Row-major layouts (artifact): W4 data [E][rows][cols/2], W8 data
+ * [E][rows][cols]; scales [E][rows][cols/group] or [E][rows] (per
+ * channel).  MFMA16 layouts (produced by q38m_repack_expert_weights):
+ *   W4 data  [E][cols/128][slot][64 lanes][16 B], quad-major: for one
  *     128-wide K block (quad kq) all row tiles are adjacent.  Slot s holds
  *     row tile s (MFMA16) or, paired, tile s/2 + (s%2)*rows/32.  Lane
  *     l = (q=l/16, n=l%16) holds for row 16t+n and groups 4kq+j (j=0..3) one
  *     dword each: byte i = nib(k0+i) | nib(k0+4+i)<<4, k0 = 32(4kq+j)+8q.
- *   W4 g32 scales [E][cols/128][slot][16 rows][4 groups] fp16 (same order).
+ *   W4 scales [E][cols/128][slot][16 rows][128/group] (same order: 4, 2
+ *     or 1 words per row and quad for groups of 32, 64, 128).
  *   W8 data  [E][rows/16][cols/64][64 lanes][16 B]; lane l holds row 16t+n,
- *     columns 64kb+16q .. +15.   W8 per-channel scales stay [E][rows]. */
+ *     columns 64kb+16q .. +15.   W8 scales stay in the artifact order. */
 
 /* ---- sizes: include/q38/cuda_moe_prefill.h:73-93 --------------------- */
 uint32_t q38m_moe_prefill_routes_v1(uint32_t tokens);

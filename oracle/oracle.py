@@ -21,7 +21,7 @@ class Weights(ctypes.Structure):
     _fields_ = [("data", ctypes.c_void_p), ("scales", ctypes.c_void_p),
                 ("bits", ctypes.c_uint32), ("group", ctypes.c_uint32),
                 ("experts", ctypes.c_uint32), ("rows", ctypes.c_uint32),
-                ("cols", ctypes.c_uint32)]
+                ("cols", ctypes.c_uint32), ("scale_bf16", ctypes.c_uint32)]
 
 
 class MoeIO(ctypes.Structure):
@@ -68,7 +68,8 @@ _SIGS = {
     "q38o_plan_bytes": (_SZ, [_U32]),
     "q38o_build_plan": (_INT, [_P, _U32, _INT, _P]),
     "q38o_quantize_rows": (None, [_P, _U32, _U32, _P, _P]),
-    "q38o_quantize_weights": (ctypes.c_int, [_P, ctypes.c_uint64, _U32, ctypes.c_int, _U32, _P, _P]),
+    "q38o_quantize_weights": (ctypes.c_int, [_P, ctypes.c_uint64, _U32, ctypes.c_int, _U32, _P, _P,
+                                             ctypes.c_int]),
     "q38o_row_value": (_F, [ctypes.POINTER(Weights), _U32, _U32, _P]),
     "q38o_row_accumulators": (None, [ctypes.POINTER(Weights), _U32, _U32, _P, _P]),
     "q38o_gate_up": (None, [ctypes.POINTER(Weights), _U32, _U32, _P, _P, _P, _P, _P]),
@@ -180,12 +181,14 @@ def synth_uniform_i8(seed, tag, n, lo=-127, hi=127):
 class HostWeights:
     """Canonical row-major weights in host memory."""
 
-    def __init__(self, data, scales, bits, group, experts, rows, cols):
+    def __init__(self, data, scales, bits, group, experts, rows, cols, scale_bf16=False):
         self.data = np.ascontiguousarray(data, dtype=np.uint8)
         self.scales = np.ascontiguousarray(scales, dtype=np.uint16)
         self.bits, self.group = bits, group
         self.experts, self.rows, self.cols = experts, rows, cols
-        self.desc = Weights(_p(self.data), _p(self.scales), bits, group, experts, rows, cols)
+        self.scale_bf16 = bool(scale_bf16)
+        self.desc = Weights(_p(self.data), _p(self.scales), bits, group, experts, rows, cols,
+                            int(self.scale_bf16))
 
     def unpacked(self, expert):
         """int8 [rows][cols] of one expert."""
@@ -208,17 +211,22 @@ class HostWeights:
         """fp32 scales [rows][groups] (groups = 1 for per-channel)."""
         g = self.cols // self.group if self.group else 1
         per = self.rows * g
-        return f16_to_f32(self.scales[expert * per:(expert + 1) * per]).reshape(self.rows, g)
+        words = self.scales[expert * per:(expert + 1) * per]
+        f = bf16_to_f32(words) if self.scale_bf16 else f16_to_f32(words)
+        return f.reshape(self.rows, g)
 
 
-def synth_weights(seed, tag, bits, group, experts, rows, cols, scale_sigma):
+def synth_weights(seed, tag, bits, group, experts, rows, cols, scale_sigma, scale_bf16=False):
     """Host twin of the product's synth_weights (same counter streams)."""
     n = experts * rows * cols
     data = synth_uniform_w4(seed, tag, n) if bits == 4 else \
         synth_uniform_i8(seed, tag, n).view(np.uint8)
     nscales = n // group if group else experts * rows
-    scales = synth_abs_normal_f16(seed, tag + 1, nscales, scale_sigma)
-    return HostWeights(data, scales, bits, group, experts, rows, cols)
+    if scale_bf16:
+        scales = synth_normal_bf16(seed, tag + 1, nscales, scale_sigma) & np.uint16(0x7FFF)
+    else:
+        scales = synth_abs_normal_f16(seed, tag + 1, nscales, scale_sigma)
+    return HostWeights(data, scales, bits, group, experts, rows, cols, scale_bf16)
 
 
 # ---- routing ---------------------------------------------------------------
@@ -287,15 +295,17 @@ def quantize_rows(x_bf16, width):
     return q, s
 
 
-def quantize_weights(w_bf16, bits, group):
+def quantize_weights(w_bf16, bits, group, scale_bf16=False):
     """Weight quantiser (quantize_groupwise restated): bf16 words [rows][cols]
-    -> (data bytes [rows][cols*bits/8], fp16 scale words [rows][cols/group])."""
+    -> (data bytes [rows][cols*bits/8], fp16 (or bf16) scale words
+    [rows][cols/group])."""
     w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
     rows, cols = w.reshape(-1, w.shape[-1]).shape
     g = group or cols
     data = np.zeros((rows, cols * bits // 8), dtype=np.uint8)
     scales = np.empty((rows, cols // g), dtype=np.uint16)
-    rc = lib().q38o_quantize_weights(_p(w), rows, cols, bits, group, _p(data), _p(scales))
+    rc = lib().q38o_quantize_weights(_p(w), rows, cols, bits, group, _p(data), _p(scales),
+                                     int(scale_bf16))
     if rc:
         raise ValueError(f"invalid quantiser shape rows={rows} cols={cols} bits={bits} group={group}")
     return data, scales

@@ -491,9 +491,10 @@ void q38o_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
 /* ------------------------------------------------------------------ */
 
 int q38o_quantize_weights(const uint16_t* src_bf16, uint64_t rows, uint32_t cols,
-                          int bits, uint32_t group, uint8_t* data, uint16_t* scales_f16) {
+                          int bits, uint32_t group, uint8_t* data, uint16_t* scales,
+                          int scale_bf16) {
     const uint32_t g = group ? group : cols;
-    if (!src_bf16 || !data || !scales_f16 || rows == 0 || cols == 0 || (bits != 4 && bits != 8) ||
+    if (!src_bf16 || !data || !scales || rows == 0 || cols == 0 || (bits != 4 && bits != 8) ||
         cols % g != 0 || (bits == 4 && (g % 2 != 0 || cols % 2 != 0)))
         return 1;
     const float qmax = bits == 4 ? 7.0f : 127.0f;
@@ -510,7 +511,7 @@ int q38o_quantize_weights(const uint16_t* src_bf16, uint64_t rows, uint32_t cols
             }
             float s = amax / qmax;
             if (s == 0.0f) s = 1.0f;
-            scales_f16[(size_t)r * groups + gi] = q38o_f32_to_f16(s);
+            scales[(size_t)r * groups + gi] = scale_bf16 ? q38o_f32_to_bf16(s) : q38o_f32_to_f16(s);
             for (uint32_t k = 0; k < g; ++k) {
                 float v = rintf(q38o_bf16_to_f32(w[k]) / s);
                 if (v > qmax) v = qmax;
@@ -554,15 +555,19 @@ static void unpack_row(const q38o_weights* w, uint32_t e, uint32_t row,
     }
 }
 
+static float scale_word(const q38o_weights* w, uint16_t word) {
+    return w->scale_bf16 ? q38o_bf16_to_f32(word) : q38o_f16_to_f32(word);
+}
+
 static void row_scales(const q38o_weights* w, uint32_t e, uint32_t row,
                        float* out) {
     if (w->group == 0u) {
-        out[0] = q38o_f16_to_f32(w->scales[(size_t)e * w->rows + row]);
+        out[0] = scale_word(w, w->scales[(size_t)e * w->rows + row]);
         return;
     }
     const uint32_t groups = w->cols / w->group;
     const uint16_t* s = w->scales + ((size_t)e * w->rows + row) * groups;
-    for (uint32_t g = 0; g < groups; ++g) out[g] = q38o_f16_to_f32(s[g]);
+    for (uint32_t g = 0; g < groups; ++g) out[g] = scale_word(w, s[g]);
 }
 
 static float chain_row(const int8_t* wrow, const float* scales, uint32_t cols,

@@ -110,23 +110,26 @@ void q38o_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
 /* Weight quantiser (tools/q38_artifact_compiler.py:193-253,
  * quantize_groupwise) over `rows` bf16 rows of `cols` columns: per group
  * of `group` columns (0: the whole row) s = max|w| / qmax (fp32; qmax 7 for
- * bits 4, 127 for bits 8), s == 0 -> 1, q = clip(rint(w / s), +-qmax).  W4
- * packs column 2i in the low and 2i+1 in the high nibble (:240-243).
- * Scales are written as fp16 (RNE) -- the reference writes bf16; fp16 is
- * the BASELINE scale format.  Returns 0, or 1 for an invalid shape. */
+ * bits 4, 127 for bits 8), s == 0 -> 1, q = clip(rint(w / s), +-qmax) from
+ * the fp32 s.  W4 packs column 2i in the low and 2i+1 in the high nibble
+ * (:240-243).  Scales are written as RNE fp16 (scale_bf16 == 0, the
+ * BASELINE scale format) or RNE bf16 (scale_bf16 != 0, what the reference
+ * writes, f32_to_bf16_rne at :232).  Returns 0, or 1 for an invalid shape. */
 int q38o_quantize_weights(const uint16_t* src_bf16, uint64_t rows,
                           uint32_t cols, int bits, uint32_t group,
-                          uint8_t* data, uint16_t* scales_f16);
+                          uint8_t* data, uint16_t* scales, int scale_bf16);
 
 /* ---- weights -------------------------------------------------------- */
 typedef struct q38o_weights {
     const uint8_t* data;     /* canonical row-major: W4 [E][rows][cols/2]
                                 (low nibble = even column); W8 [E][rows][cols] */
-    const uint16_t* scales;  /* fp16: group g: [E][rows][cols/g];
+    const uint16_t* scales;  /* group g: [E][rows][cols/g];
                                 per channel (group 0): [E][rows] */
     uint32_t bits;           /* 4 or 8 */
     uint32_t group;          /* 32, 64, 128 ... or 0 = per output channel */
     uint32_t experts, rows, cols;
+    uint32_t scale_bf16;     /* scale words: 0 = fp16, 1 = bf16 (both
+                                widen to fp32 exactly) */
 } q38o_weights;
 
 /* Scaled row value before the activation scale:

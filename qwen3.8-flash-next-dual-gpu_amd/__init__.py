@@ -35,6 +35,7 @@ PLAN_FLAG_HASHES = 1
 FORMAT_W4_SYM = 2
 FORMAT_W8_SYM = 3
 SCALE_F16 = 1
+SCALE_BF16 = 2
 LAYOUT_ROW_MAJOR = 0
 LAYOUT_MFMA16 = 2
 LAYOUT_MFMA16_PAIRED = 3
@@ -235,10 +236,11 @@ def device_index(tensor):
 class DeviceWeights:
     """Expert weights resident in device memory plus their descriptor."""
 
-    def __init__(self, data, scales, fmt, group, layout, experts, rows, columns):
+    def __init__(self, data, scales, fmt, group, layout, experts, rows, columns,
+                 scale_dtype=SCALE_F16):
         self.data = data
         self.scales = scales
-        self.desc = ExpertWeights(ptr(data), ptr(scales), fmt, group, SCALE_F16, layout,
+        self.desc = ExpertWeights(ptr(data), ptr(scales), fmt, group, scale_dtype, layout,
                                   experts, rows, columns)
 
     @property
@@ -261,9 +263,10 @@ def synth_fill(kind, seed, tag, count, out, sigma=1.0, lo=0, hi=0, bias=None, st
 
 
 def synth_weights(seed, tag, fmt, group, experts, rows, columns, scale_sigma, device="cuda",
-                  stream=None):
+                  stream=None, scale_dtype=SCALE_F16):
     """Row-major synthetic weights: int4 U[-8,7] / int8 U[-127,127] and
-    fp16 |N(0, scale_sigma)| scales (counter streams tag and tag+1)."""
+    |N(0, scale_sigma)| scales (counter streams tag and tag+1): fp16, or
+    bf16 (the bf16 normal stream with its sign bit cleared)."""
     torch = _torch()
     data_bytes, scale_bytes = weights_bytes(fmt, group, experts, rows, columns)
     data = torch.empty(data_bytes, dtype=torch.uint8, device=device)
@@ -273,9 +276,15 @@ def synth_weights(seed, tag, fmt, group, experts, rows, columns, scale_sigma, de
         synth_fill(SYNTH_UNIFORM_W4, seed, tag, elements, data, lo=-8, hi=7, stream=stream)
     else:
         synth_fill(SYNTH_UNIFORM_I8, seed, tag, elements, data, lo=-127, hi=127, stream=stream)
-    synth_fill(SYNTH_ABS_NORMAL_F16, seed, tag + 1, scales.numel(), scales, sigma=scale_sigma,
-               stream=stream)
-    return DeviceWeights(data, scales, fmt, group, LAYOUT_ROW_MAJOR, experts, rows, columns)
+    if scale_dtype == SCALE_BF16:
+        synth_fill(SYNTH_NORMAL_BF16, seed, tag + 1, scales.numel(), scales, sigma=scale_sigma,
+                   stream=stream)
+        scales.bitwise_and_(0x7FFF)
+    else:
+        synth_fill(SYNTH_ABS_NORMAL_F16, seed, tag + 1, scales.numel(), scales,
+                   sigma=scale_sigma, stream=stream)
+    return DeviceWeights(data, scales, fmt, group, LAYOUT_ROW_MAJOR, experts, rows, columns,
+                         scale_dtype)
 
 
 def repack(weights, paired=False, stream=None):
@@ -287,7 +296,7 @@ def repack(weights, paired=False, stream=None):
     d = weights.desc
     layout = LAYOUT_MFMA16_PAIRED if paired else LAYOUT_MFMA16
     out = DeviceWeights(data, scales, d.format, d.group_size, layout, d.experts, d.rows,
-                        d.columns)
+                        d.columns, d.scale_dtype)
     call("q38m_repack_expert_weights", ctypes.byref(weights.desc), ctypes.byref(out.desc),
          stream_handle(stream), device_index(data))
     return out

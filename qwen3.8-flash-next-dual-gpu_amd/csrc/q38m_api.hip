@@ -59,22 +59,28 @@ bool valid_plan(const q38m_route_plan_v1* plan) {
 
 // Shape/format checks of validate_expert_tensor (q38_moe_prefill.cu:51-62)
 // for this build's formats.
+bool valid_scale_dtype(uint32_t dtype) {
+    return dtype == Q38M_SCALE_F16 || dtype == Q38M_SCALE_BF16;
+}
+bool w4_group(uint32_t g) { return g == 32u || g == 64u || g == 128u; }
+
 bool valid_gate_up(const q38m_expert_weights_v1* w) {
     return w && w->data && w->scales && aligned(w->data, 16) && aligned(w->scales, 8) &&
-           w->format == Q38M_FORMAT_W4_SYM && w->group_size == 32u &&
-           w->scale_dtype == Q38M_SCALE_F16 && w->layout == Q38M_LAYOUT_MFMA16_PAIRED &&
+           w->format == Q38M_FORMAT_W4_SYM && w4_group(w->group_size) &&
+           valid_scale_dtype(w->scale_dtype) && w->layout == Q38M_LAYOUT_MFMA16_PAIRED &&
            w->experts == Q38M_ROUTE_EXPERTS && w->rows == 2u * Q38M_INTERMEDIATE &&
            w->columns == Q38M_HIDDEN;
 }
 
 bool valid_down(const q38m_expert_weights_v1* w) {
     if (!w || !w->data || !w->scales || !aligned(w->data, 16) || !aligned(w->scales, 8) ||
-        w->scale_dtype != Q38M_SCALE_F16 || w->layout != Q38M_LAYOUT_MFMA16 ||
+        !valid_scale_dtype(w->scale_dtype) || w->layout != Q38M_LAYOUT_MFMA16 ||
         w->experts != Q38M_ROUTE_EXPERTS || w->rows != Q38M_HIDDEN ||
         w->columns != Q38M_INTERMEDIATE)
         return false;
-    return (w->format == Q38M_FORMAT_W8_SYM && w->group_size == 0u) ||
-           (w->format == Q38M_FORMAT_W4_SYM && w->group_size == 32u);
+    return (w->format == Q38M_FORMAT_W8_SYM &&
+            (w->group_size == 0u || w->group_size == 64u || w->group_size == 128u)) ||
+           (w->format == Q38M_FORMAT_W4_SYM && w4_group(w->group_size));
 }
 
 int check_weights(const q38m_expert_weights_v1* w, bool gate_up) {
@@ -248,10 +254,9 @@ int q38m_moe_grouped_gate_up_v1(const q38m_expert_weights_v1* gate_up, const int
         !aligned(xq, 8) || !aligned(tasks, 8))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill gate/up input");
     if (int rc = select_device(device)) return rc;
-    return finish(q38m::launch_gate_up_w4g32(gate_up->data, gate_up->scales, xq, xs,
-                                             packed_assignment, token_rank_weights, tasks,
-                                             task_count, weighted_mid, as_stream(stream)),
-                  "gate_up_w4g32_kernel");
+    return finish(q38m::launch_gate_up(*gate_up, xq, xs, packed_assignment, token_rank_weights,
+                                       tasks, task_count, weighted_mid, as_stream(stream)),
+                  "grouped gate/up kernel");
 }
 
 int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down, const int8_t* mid_q,
@@ -264,13 +269,9 @@ int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down, const int8_t* m
         !aligned(mid_q, 16) || !aligned(tasks, 8))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill down input");
     if (int rc = select_device(device)) return rc;
-    const hipError_t status =
-        down->format == Q38M_FORMAT_W8_SYM
-            ? q38m::launch_down_w8pc(down->data, down->scales, mid_q, mid_scales, tasks,
-                                     task_count, route_output, as_stream(stream))
-            : q38m::launch_down_w4g32(down->data, down->scales, mid_q, mid_scales, tasks,
-                                      task_count, route_output, as_stream(stream));
-    return finish(status, "grouped_down_kernel");
+    return finish(q38m::launch_down(*down, mid_q, mid_scales, tasks, task_count, route_output,
+                                    as_stream(stream)),
+                  "grouped down kernel");
 }
 
 int q38m_moe_reduce_top10_and_combine_shared_v1(const float* route_output,
@@ -370,18 +371,15 @@ int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert
     if (status == hipSuccess)
         status = q38m::launch_build_plan(ws->expert_ids, tokens, ws->plan, false, s);
     if (status == hipSuccess)
-        status = q38m::launch_gate_up_w4g32(gate_up->data, gate_up->scales, ws->xq, ws->xs,
-                                            ws->plan.packed_assignment, ws->expert_weights,
-                                            ws->plan.tasks, tasks, ws->weighted_mid, s);
+        status = q38m::launch_gate_up(*gate_up, ws->xq, ws->xs, ws->plan.packed_assignment,
+                                      ws->expert_weights, ws->plan.tasks, tasks,
+                                      ws->weighted_mid, s);
     if (status == hipSuccess)
         status = q38m::launch_quantize_rows(ws->weighted_mid, routes, Q38M_INTERMEDIATE,
                                             ws->mid_q, ws->mid_s, s);
     if (status == hipSuccess)
-        status = down->format == Q38M_FORMAT_W8_SYM
-                     ? q38m::launch_down_w8pc(down->data, down->scales, ws->mid_q, ws->mid_s,
-                                              ws->plan.tasks, tasks, ws->route_output, s)
-                     : q38m::launch_down_w4g32(down->data, down->scales, ws->mid_q, ws->mid_s,
-                                               ws->plan.tasks, tasks, ws->route_output, s);
+        status = q38m::launch_down(*down, ws->mid_q, ws->mid_s, ws->plan.tasks, tasks,
+                                   ws->route_output, s);
     if (status == hipSuccess)
         status = q38m::launch_combine(ws->route_output, ws->plan.assignment_to_packed,
                                       shared_output, shared_gate, tokens, output, s);
@@ -513,20 +511,15 @@ int q38m_moe_prefill_wide_v1(const q38m_expert_weights_v1* gate_up,
         status = q38m::launch_build_wide_plan(ws->expert_ids, tokens, ws->plan,
                                               wide->plan_scratch, s);
     if (status == hipSuccess)
-        status = q38m::launch_gate_up_w4g32_wide(gate_up->data, gate_up->scales, ws->xq, ws->xs,
-                                                 ws->plan.packed_assignment, ws->expert_weights,
-                                                 ws->plan.tasks, tasks, ws->weighted_mid, s);
+        status = q38m::launch_gate_up_wide(*gate_up, ws->xq, ws->xs, ws->plan.packed_assignment,
+                                           ws->expert_weights, ws->plan.tasks, tasks,
+                                           ws->weighted_mid, s);
     if (status == hipSuccess)
         status = q38m::launch_quantize_rows(ws->weighted_mid, routes, Q38M_INTERMEDIATE,
                                             ws->mid_q, ws->mid_s, s);
     if (status == hipSuccess)
-        status = down->format == Q38M_FORMAT_W8_SYM
-                     ? q38m::launch_down_w8pc_wide(down->data, down->scales, ws->mid_q,
-                                                   ws->mid_s, ws->plan.tasks, tasks,
-                                                   ws->route_output, s)
-                     : q38m::launch_down_w4g32_wide(down->data, down->scales, ws->mid_q,
-                                                    ws->mid_s, ws->plan.tasks, tasks,
-                                                    ws->route_output, s);
+        status = q38m::launch_down_wide(*down, ws->mid_q, ws->mid_s, ws->plan.tasks, tasks,
+                                        ws->route_output, s);
     if (status == hipSuccess)
         status = q38m::launch_combine(ws->route_output, ws->plan.assignment_to_packed,
                                       shared_output, shared_gate, tokens, output, s);
@@ -590,20 +583,24 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
         src->layout != Q38M_LAYOUT_ROW_MAJOR ||
         (dst->layout != Q38M_LAYOUT_MFMA16 && dst->layout != Q38M_LAYOUT_MFMA16_PAIRED) ||
         src->format != dst->format || src->group_size != dst->group_size ||
-        src->scale_dtype != Q38M_SCALE_F16 || dst->scale_dtype != Q38M_SCALE_F16 ||
+        !valid_scale_dtype(src->scale_dtype) || dst->scale_dtype != src->scale_dtype ||
         src->experts != dst->experts || src->rows != dst->rows || src->columns != dst->columns ||
         src->experts == 0 || src->rows % 16u != 0u || !aligned(src->data, 16) ||
         !aligned(dst->data, 16))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid expert weight repack");
-    const bool w4 = src->format == Q38M_FORMAT_W4_SYM && src->group_size == 32u &&
+    const bool w4 = src->format == Q38M_FORMAT_W4_SYM && w4_group(src->group_size) &&
                     src->columns % 128u == 0u &&
                     (dst->layout == Q38M_LAYOUT_MFMA16 || src->rows % 32u == 0u);
-    const bool w8 = src->format == Q38M_FORMAT_W8_SYM && src->group_size == 0u &&
-                    src->columns % 64u == 0u && dst->layout == Q38M_LAYOUT_MFMA16;
+    const bool w8 = src->format == Q38M_FORMAT_W8_SYM &&
+                    (src->group_size == 0u || src->group_size == 64u ||
+                     src->group_size == 128u) &&
+                    src->columns % 64u == 0u &&
+                    (src->group_size == 0u || src->columns % src->group_size == 0u) &&
+                    dst->layout == Q38M_LAYOUT_MFMA16;
     if (!w4 && !w8)
         return fail(Q38M_ERR_UNSUPPORTED,
-                    "repack supports W4 group-32 (MFMA16 or MFMA16_PAIRED) and W8 per-channel "
-                    "(MFMA16)");
+                    "repack supports W4 groups 32/64/128 (MFMA16 or MFMA16_PAIRED) and W8 per "
+                    "channel or groups 64/128 (MFMA16)");
     if (int rc = select_device(device)) return rc;
     return finish(q38m::launch_repack(*src, *dst, as_stream(stream)), "repack kernels");
 }
@@ -657,7 +654,7 @@ int q38m_moe_shared_expert_v1(const uint16_t* hidden, const uint16_t* w_gate,
 int q38m_quantize_expert_weights(const uint16_t* src_bf16, const q38m_expert_weights_v1* dst,
                                  void* stream, int device) {
     if (!src_bf16 || !dst || !dst->data || !dst->scales || dst->layout != Q38M_LAYOUT_ROW_MAJOR ||
-        dst->scale_dtype != Q38M_SCALE_F16 || dst->experts == 0 || dst->rows == 0 ||
+        !valid_scale_dtype(dst->scale_dtype) || dst->experts == 0 || dst->rows == 0 ||
         dst->columns == 0 || !aligned(src_bf16, 16) || !aligned(dst->data, 16) ||
         !aligned(dst->scales, 2))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid weight quantiser buffers");

@@ -35,9 +35,12 @@ namespace {
 constexpr uint32_t kDecodeBlocks = 256;
 constexpr uint32_t kDecodeThreads = kSelectThreads;
 
-template <uint32_t H, uint32_t I>
+// kSub: 32-column sub-blocks per W4 group (1, 2 or 4: groups of 32, 64,
+// 128).  A group's sub-block accumulators add exactly in int32 before the
+// fp32 chain; bf16: scale words are bf16 (else fp16).
+template <uint32_t H, uint32_t I, uint32_t kSub>
 __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
-    const uint4* __restrict__ w, const uint2* __restrict__ s,
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s, bool bf16,
     const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
     const int32_t* __restrict__ ids_in, const float* __restrict__ weights_in, uint32_t top_k,
     int32_t* __restrict__ ids_out, uint16_t* __restrict__ mid) {
@@ -88,7 +91,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     const size_t tile = (static_cast<size_t>(e) * kQuads + kq) * kSlots + 2u * pair + u;
     const uint4* wp = w + tile * 64u + n0 + c;
     const uint4 b0 = wp[0], b1 = wp[16], b2 = wp[32], b3 = wp[48];
-    const uint2 sc = s[tile * 16u + n0 + c];
+    const uint2 sc = load_quad_scales<kSub, false>(s + (tile * 16u + n0 + c) * (4u / kSub));
 
     // int8 token (same arithmetic as the row quantiser)
     const float xs = row_scale(amax_lds);
@@ -121,18 +124,25 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
             acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xw[8u * j + 2u * q + 1u]), acc[j], false);
         }
     }
-    const float s0 = f16_to_f32(sc.x & 0xffffu) * 0.0625f, s1 = f16_to_f32(sc.x >> 16) * 0.0625f;
-    const float s2 = f16_to_f32(sc.y & 0xffffu) * 0.0625f, s3 = f16_to_f32(sc.y >> 16) * 0.0625f;
+    float gs[4u / kSub];
+    int gacc[4u / kSub];
+#pragma unroll
+    for (uint32_t gi = 0; gi < 4u / kSub; ++gi) {
+        gs[gi] = scale_to_f32(quad_scale_word(sc, gi), bf16) * 0.0625f;
+        gacc[gi] = acc[gi * kSub];
+#pragma unroll
+        for (uint32_t j = 1; j < kSub; ++j) gacc[gi] += acc[gi * kSub + j];
+    }
     // fp32 chain in group order: lane kq continues lane kq-1's value (row_shr:1
     // inside each 16-lane row); after 16 steps lane 15 holds the row's y.
     float y = 0.0f;
 #pragma unroll
     for (uint32_t step = 0; step < kQuads; ++step) {
-        const float yin = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
-        float t = __builtin_fmaf(static_cast<float>(acc[0]), s0, yin);
-        t = __builtin_fmaf(static_cast<float>(acc[1]), s1, t);
-        t = __builtin_fmaf(static_cast<float>(acc[2]), s2, t);
-        y = __builtin_fmaf(static_cast<float>(acc[3]), s3, t);
+        float t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
+#pragma unroll
+        for (uint32_t gi = 0; gi < 4u / kSub; ++gi)
+            t = __builtin_fmaf(static_cast<float>(gacc[gi]), gs[gi], t);
+        y = t;
     }
     const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 15));
     const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 31));
@@ -153,9 +163,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     }
 }
 
-template <uint32_t H, uint32_t I, bool kW4>
+// kPerGroup: W4, 32-column sub-blocks per group (1, 2, 4); W8, 64-column
+// K blocks per group (1, 2; I/64 = per output channel).
+template <uint32_t H, uint32_t I, bool kW4, uint32_t kPerGroup>
 __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
-    const uint4* __restrict__ w, const void* __restrict__ s, const uint16_t* __restrict__ mid,
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s, bool bf16,
+    const uint16_t* __restrict__ mid,
     const int32_t* __restrict__ ids, uint32_t top_k, const uint16_t* __restrict__ shared_output,
     const uint16_t* __restrict__ shared_gate, const uint16_t* __restrict__ residual,
     uint16_t* __restrict__ out) {
@@ -179,6 +192,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
 
     const uint32_t c = lane & 7u;
+    constexpr uint32_t kBlocks = I / 64u;  // W8
+    constexpr uint32_t kW8Groups = kBlocks / kPerGroup;
     uint4 bq[4];
     uint2 sc = make_uint2(0u, 0u);
     float ws = 0.0f;
@@ -190,17 +205,19 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
         const uint4* wp = w + t * 64u + 32u * qh + n0 + c;
         bq[0] = wp[0];
         bq[1] = wp[16];
-        sc = static_cast<const uint2*>(s)[t * 16u + n0 + c];
+        sc = load_quad_scales<kPerGroup, false>(s + (t * 16u + n0 + c) * (4u / kPerGroup));
     } else {
         // lane = c + 8*kb: 64-column block kb, chunks q = 0..3
-        constexpr uint32_t kBlocks = I / 64u;
         const uint32_t kb = lane >> 3;
         const uint4* wp = w + ((static_cast<size_t>(e) * kTiles + tile) * kBlocks + kb) * 64u + n0 + c;
         bq[0] = wp[0];
         bq[1] = wp[16];
         bq[2] = wp[32];
         bq[3] = wp[48];
-        ws = f16_to_f32(static_cast<const uint16_t*>(s)[static_cast<size_t>(e) * H + 16u * tile + n0 + c]);
+        // this lane's group (per channel: the one scale), artifact order
+        ws = scale_to_f32(s[(static_cast<size_t>(e) * H + 16u * tile + n0 + c) * kW8Groups +
+                            kb / kPerGroup],
+                          bf16);
     }
 
     // quantise this route's mid row (8 elements per lane)
@@ -247,18 +264,25 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
         }
 #pragma unroll
         for (uint32_t j = 0; j < 4u; ++j) acc[j] += __shfl_xor(acc[j], 32, 64);
-        const float s0 = f16_to_f32(sc.x & 0xffffu) * 0.0625f, s1 = f16_to_f32(sc.x >> 16) * 0.0625f;
-        const float s2 = f16_to_f32(sc.y & 0xffffu) * 0.0625f, s3 = f16_to_f32(sc.y >> 16) * 0.0625f;
+        float gs[4u / kPerGroup];
+        int gacc[4u / kPerGroup];
+#pragma unroll
+        for (uint32_t gi = 0; gi < 4u / kPerGroup; ++gi) {
+            gs[gi] = scale_to_f32(quad_scale_word(sc, gi), bf16) * 0.0625f;
+            gacc[gi] = acc[gi * kPerGroup];
+#pragma unroll
+            for (uint32_t j = 1; j < kPerGroup; ++j) gacc[gi] += acc[gi * kPerGroup + j];
+        }
         // chain over the four quads: lane c + 8kq continues lane c + 8(kq-1)
         float y = 0.0f;
 #pragma unroll
         for (uint32_t step = 0; step < 4u; ++step) {
-            float yin = __shfl_up(y, 8, 64);
-            if (kq == 0u) yin = 0.0f;
-            float t = __builtin_fmaf(static_cast<float>(acc[0]), s0, yin);
-            t = __builtin_fmaf(static_cast<float>(acc[1]), s1, t);
-            t = __builtin_fmaf(static_cast<float>(acc[2]), s2, t);
-            y = __builtin_fmaf(static_cast<float>(acc[3]), s3, t);
+            float t = __shfl_up(y, 8, 64);
+            if (kq == 0u) t = 0.0f;
+#pragma unroll
+            for (uint32_t gi = 0; gi < 4u / kPerGroup; ++gi)
+                t = __builtin_fmaf(static_cast<float>(gacc[gi]), gs[gi], t);
+            y = t;
         }
         o = __shfl(y, static_cast<int>(24u + c), 64) * sm;
     } else {
@@ -273,10 +297,25 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
             acc = __builtin_amdgcn_sdot4(static_cast<int>(bq[q].z), static_cast<int>(xv.z), acc, false);
             acc = __builtin_amdgcn_sdot4(static_cast<int>(bq[q].w), static_cast<int>(xv.w), acc, false);
         }
-        acc += __shfl_xor(acc, 8, 64);
-        acc += __shfl_xor(acc, 16, 64);
-        acc += __shfl_xor(acc, 32, 64);
-        o = (static_cast<float>(acc) * ws) * sm;
+        if constexpr (kPerGroup == kBlocks) {
+            acc += __shfl_xor(acc, 8, 64);
+            acc += __shfl_xor(acc, 16, 64);
+            acc += __shfl_xor(acc, 32, 64);
+            o = (static_cast<float>(acc) * ws) * sm;
+        } else {
+            // group g = kb / kPerGroup: its blocks' sum, then the chain over
+            // groups (lane c + 8*kPerGroup*g continues the previous group)
+            if constexpr (kPerGroup == 2u) acc += __shfl_xor(acc, 8, 64);
+            const uint32_t g = kb / kPerGroup;
+            float y = 0.0f;
+#pragma unroll
+            for (uint32_t step = 0; step < kW8Groups; ++step) {
+                float t = __shfl_up(y, static_cast<int>(8u * kPerGroup), 64);
+                if (g == 0u) t = 0.0f;
+                y = __builtin_fmaf(static_cast<float>(acc), ws, t);
+            }
+            o = __shfl(y, static_cast<int>(8u * kPerGroup * (kW8Groups - 1u) + c), 64) * sm;
+        }
     }
     if (lane < 8u) o_lds[route][lane] = valid ? o : 0.0f;
     __syncthreads();
@@ -302,6 +341,21 @@ size_t decode_scratch_bytes() {
     return 256u + static_cast<size_t>(kTopK) * kInter * sizeof(uint16_t);
 }
 
+namespace {
+
+template <bool kW4, uint32_t kPerGroup>
+void launch_decode_down(const q38m_expert_weights_v1& down, const uint16_t* mid,
+                        const int32_t* ids, uint32_t top_k, const uint16_t* shared_output,
+                        const uint16_t* shared_gate, const uint16_t* residual, uint16_t* output,
+                        hipStream_t stream) {
+    decode_down_kernel<kHidden, kInter, kW4, kPerGroup><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
+        static_cast<const uint4*>(down.data), static_cast<const uint16_t*>(down.scales),
+        down.scale_dtype == Q38M_SCALE_BF16, mid, ids, top_k, shared_output, shared_gate,
+        residual, output);
+}
+
+}  // namespace
+
 hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
                          const q38m_expert_weights_v1& down, const uint16_t* hidden,
                          const float* logits, const int32_t* ids, const float* weights,
@@ -310,18 +364,57 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
                          uint16_t* output, hipStream_t stream) {
     int32_t* scratch_ids = static_cast<int32_t*>(scratch);
     uint16_t* mid = reinterpret_cast<uint16_t*>(static_cast<char*>(scratch) + 256);
-    decode_gate_up_kernel<kHidden, kInter><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
-        static_cast<const uint4*>(gate_up.data), static_cast<const uint2*>(gate_up.scales),
-        hidden, logits, ids, weights, top_k, logits != nullptr ? scratch_ids : nullptr, mid);
+    const uint4* gw = static_cast<const uint4*>(gate_up.data);
+    const uint16_t* gs = static_cast<const uint16_t*>(gate_up.scales);
+    const bool gbf16 = gate_up.scale_dtype == Q38M_SCALE_BF16;
+    int32_t* ids_out = logits != nullptr ? scratch_ids : nullptr;
+    switch (gate_up.group_size) {
+        case 32u:
+            decode_gate_up_kernel<kHidden, kInter, 1><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
+                gw, gs, gbf16, hidden, logits, ids, weights, top_k, ids_out, mid);
+            break;
+        case 64u:
+            decode_gate_up_kernel<kHidden, kInter, 2><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
+                gw, gs, gbf16, hidden, logits, ids, weights, top_k, ids_out, mid);
+            break;
+        case 128u:
+            decode_gate_up_kernel<kHidden, kInter, 4><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
+                gw, gs, gbf16, hidden, logits, ids, weights, top_k, ids_out, mid);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     const int32_t* down_ids = logits != nullptr ? scratch_ids : ids;
-    if (down.format == Q38M_FORMAT_W8_SYM)
-        decode_down_kernel<kHidden, kInter, false><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
-            static_cast<const uint4*>(down.data), down.scales, mid, down_ids, top_k,
-            shared_output, shared_gate, residual, output);
-    else
-        decode_down_kernel<kHidden, kInter, true><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
-            static_cast<const uint4*>(down.data), down.scales, mid, down_ids, top_k,
-            shared_output, shared_gate, residual, output);
+    constexpr uint32_t kBlocks = kInter / 64u;
+    const bool w8 = down.format == Q38M_FORMAT_W8_SYM;
+    switch (down.group_size) {
+        case 0u:
+            if (!w8) return hipErrorInvalidValue;
+            launch_decode_down<false, kBlocks>(down, mid, down_ids, top_k, shared_output,
+                                               shared_gate, residual, output, stream);
+            break;
+        case 32u:
+            if (w8) return hipErrorInvalidValue;
+            launch_decode_down<true, 1>(down, mid, down_ids, top_k, shared_output, shared_gate,
+                                        residual, output, stream);
+            break;
+        case 64u:
+            if (w8)
+                launch_decode_down<false, 1>(down, mid, down_ids, top_k, shared_output,
+                                             shared_gate, residual, output, stream);
+            else
+                launch_decode_down<true, 2>(down, mid, down_ids, top_k, shared_output,
+                                            shared_gate, residual, output, stream);
+            break;
+        case 128u:
+            if (w8)
+                launch_decode_down<false, 2>(down, mid, down_ids, top_k, shared_output,
+                                             shared_gate, residual, output, stream);
+            else
+                launch_decode_down<true, 4>(down, mid, down_ids, top_k, shared_output,
+                                            shared_gate, residual, output, stream);
+            break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -124,6 +124,42 @@ __device__ __forceinline__ v4i mfma_i8_16x16x32(long a, long b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
 }
 
+// ---- group scales ----------------------------------------------------------
+// Scale words are fp16 (Q38M_SCALE_F16) or bf16 (Q38M_SCALE_BF16); both
+// widen to fp32 exactly.
+__device__ __forceinline__ float scale_to_f32(uint32_t word, bool bf16) {
+    return bf16 ? bf16_to_f32(word & 0xffffu) : f16_to_f32(word & 0xffffu);
+}
+
+// The scale words of one row for one W4 quad (128 columns) in the MFMA16
+// layouts ([E][K/128][slot][16 rows][128/group] words): 4, 2 or 1 words for
+// groups of 32, 64 or 128 columns, i.e. kSub = group/32 sub-blocks of 32
+// per group.  Word gi of the quad is quad_scale_word(result, gi).  kStream:
+// non-temporal loads (weights read once per call) or ordinary cached loads
+// (weights re-read by several tasks of one expert).
+template <uint32_t kSub, bool kStream = true>
+__device__ __forceinline__ uint2 load_quad_scales(const uint16_t* row_words) {
+    static_assert(kSub == 1u || kSub == 2u || kSub == 4u, "groups of 32, 64 or 128");
+    if constexpr (!kStream) {
+        if constexpr (kSub == 1u) return *reinterpret_cast<const uint2*>(row_words);
+        else if constexpr (kSub == 2u)
+            return make_uint2(*reinterpret_cast<const uint32_t*>(row_words), 0u);
+        else return make_uint2(*row_words, 0u);
+    } else if constexpr (kSub == 1u) {
+        const v2u_t v = __builtin_nontemporal_load(reinterpret_cast<const v2u_t*>(row_words));
+        return make_uint2(v.x, v.y);
+    } else if constexpr (kSub == 2u) {
+        return make_uint2(__builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(row_words)),
+                          0u);
+    } else {
+        return make_uint2(__builtin_nontemporal_load(row_words), 0u);
+    }
+}
+__device__ __forceinline__ uint32_t quad_scale_word(uint2 words, uint32_t gi) {
+    const uint32_t d = gi < 2u ? words.x : words.y;
+    return (gi & 1u) ? d >> 16 : d & 0xffffu;
+}
+
 // v_mfma_i32_16x16x64_i8 (gfx950): 16 int8 per lane per operand.
 __device__ __forceinline__ v4i mfma_i8_16x16x64(v4i a, v4i b, v4i c) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);

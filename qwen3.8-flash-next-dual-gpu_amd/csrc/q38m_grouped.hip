@@ -16,26 +16,36 @@ namespace {
 
 struct QuadWeights {
     uint4 g, u;    // gate and up tile data of one quad
-    uint2 sg, su;  // their fp16 scales (4 groups)
+    uint2 sg, su;  // their scale words (load_quad_scales)
 };
 
-// One quad (4 scale groups) of the gate/up chain for one gate tile and its
-// up tile: per group one MFMA per tile from a zero accumulator (the group's
-// exact 16*acc), then the fp32 chain y16 = fma(16*acc, s_g, y16).
+// One quad (128 columns) of the gate/up chain for one gate tile and its up
+// tile.  Per 32-wide sub-block one MFMA per tile; the kSub sub-blocks of a
+// group chain through the int32 accumulator input (the first from zero),
+// giving the group's exact 16*acc; then the fp32 chain
+// y16 = fma(16*acc, s_g, y16) (fp16 scales) or y = fma(16*acc, s_g/16, y)
+// (bf16 scales).
+template <uint32_t kSub, bool kBf16>
 __device__ __forceinline__ void gate_up_quad(const uint2* __restrict__ a_quad, uint4 wg, uint4 wu,
-                                             uint2 sg, uint2 su, float (&yg)[4], float (&yu)[4]) {
+                                             uint2 sg, uint2 su, float (&yg)[4],
+                                             float (&yu)[4]) {
     const v4i zero = {0, 0, 0, 0};
     const uint32_t wgw[4] = {wg.x, wg.y, wg.z, wg.w};
     const uint32_t wuw[4] = {wu.x, wu.y, wu.z, wu.w};
-    const uint32_t sgw[2] = {sg.x, sg.y};
-    const uint32_t suw[2] = {su.x, su.y};
+    v4i cg = zero, cu = zero;  // kSub > 1: the group's running int32 tiles
 #pragma unroll
     for (uint32_t j = 0; j < 4u; ++j) {
         const long a = as_long(a_quad[j * 64u]);
-        const v4i dg = mfma_i8_16x16x32(a, unpack_w4x16(wgw[j]), zero);
-        const v4i du = mfma_i8_16x16x32(a, unpack_w4x16(wuw[j]), zero);
-        const float scale_g = f16_to_f32((j & 1u) ? (sgw[j >> 1] >> 16) : (sgw[j >> 1] & 0xffffu));
-        const float scale_u = f16_to_f32((j & 1u) ? (suw[j >> 1] >> 16) : (suw[j >> 1] & 0xffffu));
+        const v4i dg = mfma_i8_16x16x32(a, unpack_w4x16(wgw[j]), j % kSub == 0u ? zero : cg);
+        const v4i du = mfma_i8_16x16x32(a, unpack_w4x16(wuw[j]), j % kSub == 0u ? zero : cu);
+        if (j % kSub != kSub - 1u) {
+            cg = dg;
+            cu = du;
+            continue;
+        }
+        const uint32_t wsg = quad_scale_word(sg, j / kSub), wsu = quad_scale_word(su, j / kSub);
+        const float scale_g = kBf16 ? bf16_to_f32(wsg) * 0.0625f : f16_to_f32(wsg);
+        const float scale_u = kBf16 ? bf16_to_f32(wsu) * 0.0625f : f16_to_f32(wsu);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             yg[i] = __builtin_fmaf(static_cast<float>(dg[i]), scale_g, yg[i]);
@@ -62,16 +72,18 @@ __device__ __forceinline__ void gate_up_quad(const uint2* __restrict__ a_quad, u
 // VGPRs three 8-wave workgroups per CU keep ~110 KB of weights in flight,
 // what ~2 us of loaded HBM latency needs at full bandwidth.
 //
-// The chain runs on 16x-scaled values: the MFMA gives 16*acc (nibbles in the
-// high half of each byte) and the raw fp16 scale feeds the fma, so
-// y16 = 16*y exactly at every step (power-of-two scaling commutes with
-// rounding; all partial sums are multiples of 2^-24, far from the subnormal
-// range).  y = y16 * 0.0625 is then exact and the contract's y * s_t follows.
+// The MFMA gives 16*acc (nibbles in the high half of each byte).  fp16
+// scales: the raw scale feeds the fma, so y16 = 16*y exactly at every step
+// (power-of-two scaling commutes with rounding; all partial sums are
+// multiples of 2^-24, far from the subnormal range), and y = y16 * 0.0625.
+// bf16 scale words can sit near the subnormal range, so the fma takes s/16
+// (exact in fp32, subnormals included; |16*acc| < 2^24): each product is
+// acc*s exactly and the chain holds y itself.  Then y * s_t.
 // ---------------------------------------------------------------------------
-template <uint32_t H, uint32_t I, uint32_t kWaves>
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kSub, bool kBf16>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6, 8)))
-void gate_up_w4g32_kernel(
-    const uint4* __restrict__ w, const uint2* __restrict__ s,
+void gate_up_w4_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
     const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
@@ -95,17 +107,21 @@ void gate_up_w4g32_kernel(
     // Paired quad-major layout: for quad kq the gate tile of pair p is slot
     // 2p and its up tile slot 2p+1, so a workgroup's step reads one
     // contiguous span of 2*kWaves KiB of weights and 256*kWaves B of scales.
-    constexpr uint32_t kQuadWords = kTiles * 64u;   // uint4 per quad of one expert
-    constexpr uint32_t kQuadScales = kTiles * 16u;  // uint2 per quad of one expert
+    constexpr uint32_t kQuadWords = kTiles * 64u;  // uint4 per quad of one expert
+    constexpr uint32_t kRowScales = 4u / kSub;     // scale words per row and quad
+    constexpr uint32_t kSlotScales = 16u * kRowScales;
+    constexpr uint32_t kQuadScales = kTiles * kSlotScales;
     // uniform bases (scalar registers) plus 32-bit per-lane offsets
     const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u;
-    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 16u;
+    const uint16_t* sbase =
+        s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * kSlotScales;
     auto load = [&](uint32_t kq) {
         const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
         const uint32_t wi = k * kQuadWords + lane;
-        const uint32_t si = k * kQuadScales + n;
+        const uint32_t si = k * kQuadScales + n * kRowScales;
         return QuadWeights{load_stream(wbase + wi), load_stream(wbase + wi + 64u),
-                           load_stream(sbase + si), load_stream(sbase + si + 16u)};
+                           load_quad_scales<kSub>(sbase + si),
+                           load_quad_scales<kSub>(sbase + si + kSlotScales)};
     };
 
     // Stage A: 16-byte chunk c of token row r holds group c/2 for lane groups
@@ -150,15 +166,15 @@ void gate_up_w4g32_kernel(
     for (uint32_t kq = 0; kq + 3u < kQuads; kq += 3u) {
         r2 = load(kq + 2u);
         __builtin_amdgcn_sched_barrier(0);
-        gate_up_quad(a_base + 4u * kq * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
+        gate_up_quad<kSub, kBf16>(a_base + 4u * kq * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
         r0 = load(kq + 3u);
         __builtin_amdgcn_sched_barrier(0);
-        gate_up_quad(a_base + 4u * (kq + 1u) * 64u, r1.g, r1.u, r1.sg, r1.su, yg, yu);
+        gate_up_quad<kSub, kBf16>(a_base + 4u * (kq + 1u) * 64u, r1.g, r1.u, r1.sg, r1.su, yg, yu);
         r1 = load(kq + 4u);
         __builtin_amdgcn_sched_barrier(0);
-        gate_up_quad(a_base + 4u * (kq + 2u) * 64u, r2.g, r2.u, r2.sg, r2.su, yg, yu);
+        gate_up_quad<kSub, kBf16>(a_base + 4u * (kq + 2u) * 64u, r2.g, r2.u, r2.sg, r2.su, yg, yu);
     }
-    gate_up_quad(a_base + 4u * (kQuads - 1u) * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
+    gate_up_quad<kSub, kBf16>(a_base + 4u * (kQuads - 1u) * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
 
     const uint32_t channel = gate_tile * 16u + n;
 #pragma unroll
@@ -168,17 +184,23 @@ void gate_up_w4g32_kernel(
         const uint32_t p = p0 + r;
         const uint32_t a = packed[p];
         const float st = xs[a / kTopK];
-        const float y_gate = (yg[i] * 0.0625f) * st;
-        const float y_up = (yu[i] * 0.0625f) * st;
+        const float unscale = kBf16 ? 1.0f : 0.0625f;
+        const float y_gate = (yg[i] * unscale) * st;
+        const float y_up = (yu[i] * unscale) * st;
         mid[static_cast<size_t>(p) * I + channel] =
             static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
     }
 }
 
 // ---------------------------------------------------------------------------
-// Down, W8 per output channel, MFMA16 layout (16 int8 per lane per 64-wide
-// K block).  acc = sum_k qm[r][k] * W[e][c][k] over all of K in one int32
-// (exact in fp32, |acc| < 2^24), o = ((float)acc * ws[e][c]) * sm[r].
+// Down, W8, MFMA16 layout (16 int8 per lane per 64-wide K block), per output
+// channel or in groups of kBlocksPerGroup K blocks (64 or 128 columns).
+// Per channel (kBlocksPerGroup == I/64): acc = sum_k qm[r][k] * W[e][c][k]
+// over all of K in one int32 (exact in fp32, |acc| < 2^24),
+// o = ((float)acc * ws[e][c]) * sm[r].  Grouped: one int32 per group
+// (its blocks chain through the MFMA accumulator input), the fp32 chain
+// y = fmaf((float)acc_g, s[e][c][g], y) in group order from 0, o = y * sm[r].
+// Group scales stay in the artifact order [E][rows][K/group].
 //
 // A workgroup of kWaves waves covers kWaves * kTilesPerWave 16-channel
 // output tiles of one task.  The task's 16 int8 mid rows (8 KiB) are staged
@@ -187,8 +209,9 @@ void gate_up_w4g32_kernel(
 // per wave) with a pinned one-unit-ahead prefetch; at ~60 VGPRs eight waves
 // per SIMD keep ~128 KB of weights in flight per CU.
 // ---------------------------------------------------------------------------
-template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
-__global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave,
+          uint32_t kBlocksPerGroup, bool kBf16>
+__global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
@@ -196,7 +219,10 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
     constexpr uint32_t kHalf = kBlocks / 2u;
     constexpr uint32_t kTiles = H / 16u;
     constexpr uint32_t kThreads = kWaves * 64u;
+    constexpr bool kPerChannel = kBlocksPerGroup == kBlocks;
+    constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
     static_assert(kBlocks % 2u == 0u, "half-tile units");
+    static_assert(kPerChannel || kHalf % kBlocksPerGroup == 0u, "groups within half tiles");
     __shared__ uint4 a_lds[kBlocks * 64u];
 
     const q38m_task_v1 task = tasks[blockIdx.y];
@@ -232,6 +258,7 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
     }
     __syncthreads();
 
+    const v4i zero = {0, 0, 0, 0};
 #pragma unroll
     for (uint32_t t = 0; t < kTilesPerWave; ++t) {
         const uint32_t tile = tile0 + t;
@@ -239,11 +266,35 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
         uint4 nb[kHalf];
 #pragma unroll
         for (uint32_t kb = 0; kb < kHalf; ++kb) nb[kb] = load_stream(wtile + (kHalf + kb) * 64u);
-        __builtin_amdgcn_sched_barrier(0);
-        v4i acc = {0, 0, 0, 0};
+        // grouped: the row's group scales up front; per channel: after the
+        // K loop (fewer live registers across it)
+        float gs[kGroups];
+        auto load_scales = [&]() {
 #pragma unroll
-        for (uint32_t kb = 0; kb < kHalf; ++kb)
-            acc = mfma_i8_16x16x64(as_v4i(a_lds[kb * 64u + lane]), as_v4i(b[kb]), acc);
+            for (uint32_t g = 0; g < kGroups; ++g)
+                gs[g] = scale_to_f32(
+                    s[(static_cast<size_t>(e) * H + tile * 16u + n) * kGroups + g], kBf16);
+        };
+        if constexpr (!kPerChannel) load_scales();
+        __builtin_amdgcn_sched_barrier(0);
+        v4i acc = zero;
+        float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        // K block kb of the tile: acc restarts at each group's first block
+        // and, grouped, joins the chain at its last
+        auto block = [&](uint32_t kb, uint4 bv) {
+            acc = mfma_i8_16x16x64(as_v4i(a_lds[kb * 64u + lane]), as_v4i(bv),
+                                   kb % kBlocksPerGroup == 0u ? zero : acc);
+            if constexpr (!kPerChannel) {
+                if (kb % kBlocksPerGroup == kBlocksPerGroup - 1u) {
+#pragma unroll
+                    for (uint32_t i = 0; i < 4u; ++i)
+                        y[i] = __builtin_fmaf(static_cast<float>(acc[i]), gs[kb / kBlocksPerGroup],
+                                              y[i]);
+                }
+            }
+        };
+#pragma unroll
+        for (uint32_t kb = 0; kb < kHalf; ++kb) block(kb, b[kb]);
         // next tile's first half (unrolled: the last tile issues none)
         if (t + 1u < kTilesPerWave) {
 #pragma unroll
@@ -252,31 +303,33 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (uint32_t kb = 0; kb < kHalf; ++kb)
-            acc = mfma_i8_16x16x64(as_v4i(a_lds[(kHalf + kb) * 64u + lane]), as_v4i(nb[kb]), acc);
+        for (uint32_t kb = 0; kb < kHalf; ++kb) block(kHalf + kb, nb[kb]);
+        if constexpr (kPerChannel) load_scales();
         const uint32_t channel = tile * 16u + n;
-        const float ws = f16_to_f32(s[static_cast<size_t>(e) * H + channel]);
 #pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) {
             const uint32_t r = 4u * q + i;
             if (r >= rows) continue;
-            const float o = (static_cast<float>(acc[i]) * ws) * row_scale[i];
+            const float o = kPerChannel ? (static_cast<float>(acc[i]) * gs[0]) * row_scale[i]
+                                        : y[i] * row_scale[i];
             out[static_cast<size_t>(p0 + r) * H + channel] = o;
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Down, W4 group-32 (the all-W4 layer policy): the gate/up group chain over
-// K = I, then * sm[r].
+// Down, W4 in groups of 32, 64 or 128 columns (kSub sub-blocks of 32 per
+// group; the all-W4 layer policy): the gate/up group chain over K = I, then
+// * sm[r].
 // ---------------------------------------------------------------------------
-template <uint32_t H, uint32_t I, uint32_t kTilesPerWave>
-__global__ __launch_bounds__(256) void down_w4g32_kernel(
-    const uint4* __restrict__ w, const uint2* __restrict__ s,
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kSub, bool kBf16>
+__global__ __launch_bounds__(256) void down_w4_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
     constexpr uint32_t kQuads = I / 128u;
     constexpr uint32_t kTiles = H / 16u;
+    constexpr uint32_t kRowScales = 4u / kSub;
     const q38m_task_v1 task = tasks[blockIdx.y];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
@@ -303,19 +356,20 @@ __global__ __launch_bounds__(256) void down_w4g32_kernel(
         const uint32_t tile = tile0 + t;
         // quad-major layout: quad kq of tile t is unit (e*kQuads + kq)*kTiles + t
         const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 64u + lane;
-        const uint2* st = s + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 16u + n;
+        const uint16_t* st =
+            s + ((static_cast<size_t>(e) * kQuads * kTiles + tile) * 16u + n) * kRowScales;
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t kq = 0; kq < kQuads; ++kq) {
             const uint4 b = load_stream(wt + kq * kTiles * 64u);
-            const uint2 c = load_stream(st + kq * kTiles * 16u);
+            const uint2 c = load_quad_scales<kSub>(st + kq * kTiles * 16u * kRowScales);
             const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
-            const uint32_t cw[2] = {c.x, c.y};
+            v4i d = zero;
 #pragma unroll
             for (uint32_t j = 0; j < 4u; ++j) {
-                const v4i d = mfma_i8_16x16x32(a[kq * 4u + j], unpack_w4x16(bw[j]), zero);
-                const uint32_t h = (j & 1u) ? (cw[j >> 1] >> 16) : (cw[j >> 1] & 0xffffu);
-                const float scale = f16_to_f32(h) * 0.0625f;
+                d = mfma_i8_16x16x32(a[kq * 4u + j], unpack_w4x16(bw[j]), j % kSub == 0u ? zero : d);
+                if (j % kSub != kSub - 1u) continue;
+                const float scale = scale_to_f32(quad_scale_word(c, j / kSub), kBf16) * 0.0625f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     y[i] = __builtin_fmaf(static_cast<float>(d[i]), scale, y[i]);
@@ -396,40 +450,100 @@ __global__ __launch_bounds__(256) void combine_shared_kernel(
 
 }  // namespace
 
-hipError_t launch_gate_up_w4g32(const void* data, const void* scales,
-                                const int8_t* xq, const float* xs,
-                                const uint32_t* packed, const float* route_weights,
-                                const q38m_task_v1* tasks, uint32_t task_count,
-                                uint16_t* weighted_mid, hipStream_t stream) {
+namespace {
+
+template <uint32_t kSub>
+void launch_gate_up_sub(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
+                        const uint32_t* packed, const float* route_weights,
+                        const q38m_task_v1* tasks, uint32_t task_count, uint16_t* weighted_mid,
+                        hipStream_t stream) {
     constexpr uint32_t kWaves = 8;
     const dim3 grid(kInter / 16u / kWaves, task_count);
-    gate_up_w4g32_kernel<kHidden, kInter, kWaves><<<grid, kWaves * 64u, 0, stream>>>(
-        static_cast<const uint4*>(data), static_cast<const uint2*>(scales), xq, xs,
-        packed, route_weights, tasks, weighted_mid);
-    return hipGetLastError();
+    const auto* data = static_cast<const uint4*>(w.data);
+    const auto* scales = static_cast<const uint16_t*>(w.scales);
+    if (w.scale_dtype == Q38M_SCALE_BF16)
+        gate_up_w4_kernel<kHidden, kInter, kWaves, kSub, true><<<grid, kWaves * 64u, 0, stream>>>(
+            data, scales, xq, xs, packed, route_weights, tasks, weighted_mid);
+    else
+        gate_up_w4_kernel<kHidden, kInter, kWaves, kSub, false><<<grid, kWaves * 64u, 0, stream>>>(
+            data, scales, xq, xs, packed, route_weights, tasks, weighted_mid);
 }
 
-hipError_t launch_down_w8pc(const void* data, const void* scales,
-                            const int8_t* mid_q, const float* mid_s,
-                            const q38m_task_v1* tasks, uint32_t task_count,
-                            float* route_output, hipStream_t stream) {
+template <uint32_t kBlocksPerGroup>
+void launch_down_w8_groups(const q38m_expert_weights_v1& w, const int8_t* mid_q,
+                           const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+                           float* route_output, hipStream_t stream) {
     constexpr uint32_t kWaves = 8, kTilesPerWave = 2;
     const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
-    down_w8pc_kernel<kHidden, kInter, kWaves, kTilesPerWave><<<grid, kWaves * 64u, 0, stream>>>(
-        static_cast<const uint4*>(data), static_cast<const uint16_t*>(scales), mid_q,
-        mid_s, tasks, route_output);
+    const auto* data = static_cast<const uint4*>(w.data);
+    const auto* scales = static_cast<const uint16_t*>(w.scales);
+    if (w.scale_dtype == Q38M_SCALE_BF16)
+        down_w8_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, true>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid_q, mid_s, tasks, route_output);
+    else
+        down_w8_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, false>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid_q, mid_s, tasks, route_output);
+}
+
+template <uint32_t kSub>
+void launch_down_w4_sub(const q38m_expert_weights_v1& w, const int8_t* mid_q,
+                        const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+                        float* route_output, hipStream_t stream) {
+    constexpr uint32_t kTilesPerWave = 4;
+    const dim3 grid(kHidden / 16u / (4u * kTilesPerWave), task_count);
+    const auto* data = static_cast<const uint4*>(w.data);
+    const auto* scales = static_cast<const uint16_t*>(w.scales);
+    if (w.scale_dtype == Q38M_SCALE_BF16)
+        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, true><<<grid, 256, 0, stream>>>(
+            data, scales, mid_q, mid_s, tasks, route_output);
+    else
+        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, false><<<grid, 256, 0, stream>>>(
+            data, scales, mid_q, mid_s, tasks, route_output);
+}
+
+}  // namespace
+
+hipError_t launch_gate_up(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
+                          const uint32_t* packed, const float* route_weights,
+                          const q38m_task_v1* tasks, uint32_t task_count, uint16_t* weighted_mid,
+                          hipStream_t stream) {
+    switch (w.group_size) {
+        case 32u: launch_gate_up_sub<1>(w, xq, xs, packed, route_weights, tasks, task_count,
+                                        weighted_mid, stream); break;
+        case 64u: launch_gate_up_sub<2>(w, xq, xs, packed, route_weights, tasks, task_count,
+                                        weighted_mid, stream); break;
+        case 128u: launch_gate_up_sub<4>(w, xq, xs, packed, route_weights, tasks, task_count,
+                                         weighted_mid, stream); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_down_w4g32(const void* data, const void* scales,
-                             const int8_t* mid_q, const float* mid_s,
-                             const q38m_task_v1* tasks, uint32_t task_count,
-                             float* route_output, hipStream_t stream) {
-    constexpr uint32_t kTilesPerWave = 4;
-    const dim3 grid(kHidden / 16u / (4u * kTilesPerWave), task_count);
-    down_w4g32_kernel<kHidden, kInter, kTilesPerWave><<<grid, 256, 0, stream>>>(
-        static_cast<const uint4*>(data), static_cast<const uint2*>(scales), mid_q,
-        mid_s, tasks, route_output);
+hipError_t launch_down(const q38m_expert_weights_v1& w, const int8_t* mid_q, const float* mid_s,
+                       const q38m_task_v1* tasks, uint32_t task_count, float* route_output,
+                       hipStream_t stream) {
+    constexpr uint32_t kBlocks = kInter / 64u;
+    if (w.format == Q38M_FORMAT_W8_SYM) {
+        switch (w.group_size) {
+            case 0u: launch_down_w8_groups<kBlocks>(w, mid_q, mid_s, tasks, task_count,
+                                                    route_output, stream); break;
+            case 64u: launch_down_w8_groups<1>(w, mid_q, mid_s, tasks, task_count, route_output,
+                                               stream); break;
+            case 128u: launch_down_w8_groups<2>(w, mid_q, mid_s, tasks, task_count, route_output,
+                                                stream); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (w.group_size) {
+            case 32u: launch_down_w4_sub<1>(w, mid_q, mid_s, tasks, task_count, route_output,
+                                            stream); break;
+            case 64u: launch_down_w4_sub<2>(w, mid_q, mid_s, tasks, task_count, route_output,
+                                            stream); break;
+            case 128u: launch_down_w4_sub<4>(w, mid_q, mid_s, tasks, task_count, route_output,
+                                             stream); break;
+            default: return hipErrorInvalidValue;
+        }
+    }
     return hipGetLastError();
 }
 

@@ -38,17 +38,15 @@ uint32_t wide_chunks(uint32_t tokens);
 hipError_t launch_build_wide_plan(const int32_t* ids, uint32_t tokens,
                                   const q38m_route_plan_v1& plan, uint32_t* chunk_counts,
                                   hipStream_t stream);
-hipError_t launch_gate_up_w4g32_wide(const void* data, const void* scales, const int8_t* xq,
-                                     const float* xs, const uint32_t* packed,
-                                     const float* route_weights, const q38m_task_v1* tasks,
-                                     uint32_t task_count, uint16_t* weighted_mid,
-                                     hipStream_t stream);
-hipError_t launch_down_w8pc_wide(const void* data, const void* scales, const int8_t* mid_q,
-                                 const float* mid_s, const q38m_task_v1* tasks,
-                                 uint32_t task_count, float* route_output, hipStream_t stream);
-hipError_t launch_down_w4g32_wide(const void* data, const void* scales, const int8_t* mid_q,
-                                  const float* mid_s, const q38m_task_v1* tasks,
-                                  uint32_t task_count, float* route_output, hipStream_t stream);
+// the grouped GEMMs over 128-row tasks, for the formats launch_gate_up /
+// launch_down take
+hipError_t launch_gate_up_wide(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
+                               const uint32_t* packed, const float* route_weights,
+                               const q38m_task_v1* tasks, uint32_t task_count,
+                               uint16_t* weighted_mid, hipStream_t stream);
+hipError_t launch_down_wide(const q38m_expert_weights_v1& w, const int8_t* mid_q,
+                            const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+                            float* route_output, hipStream_t stream);
 
 // routing (q38m_routing.hip)
 hipError_t launch_topk(const float* logits, int32_t* ids, float* weights,
@@ -84,19 +82,16 @@ hipError_t launch_residual_add(const uint16_t* a, const uint16_t* b, uint16_t* o
                                uint64_t elements, hipStream_t stream);
 
 // grouped GEMMs and combine (q38m_grouped.hip)
-hipError_t launch_gate_up_w4g32(const void* data, const void* scales,
-                                const int8_t* xq, const float* xs,
-                                const uint32_t* packed, const float* route_weights,
-                                const q38m_task_v1* tasks, uint32_t task_count,
-                                uint16_t* weighted_mid, hipStream_t stream);
-hipError_t launch_down_w8pc(const void* data, const void* scales,
-                            const int8_t* mid_q, const float* mid_s,
-                            const q38m_task_v1* tasks, uint32_t task_count,
-                            float* route_output, hipStream_t stream);
-hipError_t launch_down_w4g32(const void* data, const void* scales,
-                             const int8_t* mid_q, const float* mid_s,
-                             const q38m_task_v1* tasks, uint32_t task_count,
-                             float* route_output, hipStream_t stream);
+// weights validated by the API layer: gate/up W4 (groups 32/64/128,
+// MFMA16_PAIRED); down W8 (per channel, groups 64/128) or W4 (groups
+// 32/64/128); fp16 or bf16 scale words
+hipError_t launch_gate_up(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
+                          const uint32_t* packed, const float* route_weights,
+                          const q38m_task_v1* tasks, uint32_t task_count, uint16_t* weighted_mid,
+                          hipStream_t stream);
+hipError_t launch_down(const q38m_expert_weights_v1& w, const int8_t* mid_q, const float* mid_s,
+                       const q38m_task_v1* tasks, uint32_t task_count, float* route_output,
+                       hipStream_t stream);
 hipError_t launch_combine(const float* route_output, const uint32_t* inverse,
                           const uint16_t* shared_output, const uint16_t* shared_gate,
                           uint32_t tokens, uint16_t* output, hipStream_t stream);

@@ -43,23 +43,25 @@ __global__ void repack_w4_kernel(const uint32_t* __restrict__ src, uint32_t* __r
     dst[o] = out;
 }
 
-// W4 g32 scales [E][R][K/32] -> [E][K/128][slot][16][4].
+// W4 scales [E][R][K/g] -> [E][K/128][slot][16][128/g] (g = 32, 64, 128:
+// per_quad = 4, 2, 1 words per row and quad).
 __global__ void repack_w4_scales_kernel(const uint16_t* __restrict__ src,
                                         uint16_t* __restrict__ dst, uint32_t rows,
-                                        uint32_t cols, bool paired, uint64_t total) {
+                                        uint32_t cols, uint32_t per_quad, bool paired,
+                                        uint64_t total) {
     const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (o >= total) return;
     const uint32_t quads = cols / 128u;
     const uint32_t row_tiles = rows / 16u;
-    const uint32_t j = static_cast<uint32_t>(o & 3u);
-    const uint32_t n = static_cast<uint32_t>((o >> 2) & 15u);
-    const uint64_t unit = o >> 6;
+    const uint32_t j = static_cast<uint32_t>(o % per_quad);
+    const uint32_t n = static_cast<uint32_t>((o / per_quad) & 15u);
+    const uint64_t unit = o / (16u * per_quad);
     const uint32_t slot = static_cast<uint32_t>(unit % row_tiles);
     const uint64_t tmp = unit / row_tiles;
     const uint32_t kq = static_cast<uint32_t>(tmp % quads);
     const uint64_t e = tmp / quads;
     const uint32_t row = slot_tile(slot, row_tiles, paired) * 16u + n;
-    dst[o] = src[(e * rows + row) * (cols / 32u) + kq * 4u + j];
+    dst[o] = src[(e * rows + row) * (quads * per_quad) + kq * per_quad + j];
 }
 
 // W8 row-major [E][R][K] -> MFMA16 [E][R/16][K/64][64][16 B]; lane (q,n)
@@ -84,7 +86,9 @@ __global__ void repack_w8_kernel(const uint4* __restrict__ src, uint4* __restric
 // Weight quantiser (tools/q38_artifact_compiler.py:193-253, quantize_groupwise):
 // per group s = max|w| / qmax (qmax 7 for W4, 127 for W8), s == 0 -> 1,
 // q = clamp(rint(w / s), +-qmax); W4 packs column 2i in the low nibble.
-// Scales are stored as fp16 (round to nearest even, subnormals kept).
+// Scales are stored as fp16 (round to nearest even, subnormals kept) or,
+// as the reference does (f32_to_bf16_rne, :232), as RNE bf16; q always
+// comes from the fp32 s.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float v) {
     return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(v)));
@@ -102,7 +106,7 @@ __device__ __forceinline__ uint32_t quant_weight(uint32_t bf16, float s) {
 template <uint32_t kBits, uint32_t kGroup>
 __global__ __launch_bounds__(256) void quantize_weights_group_kernel(
     const uint4* __restrict__ src, uint64_t groups, uint8_t* __restrict__ data,
-    uint16_t* __restrict__ scales) {
+    uint16_t* __restrict__ scales, bool scale_bf16) {
     constexpr uint32_t kVec = kGroup / 8u;  // uint4 of 8 bf16
     constexpr float kMax = kBits == 4u ? 7.0f : 127.0f;
     const uint64_t g = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -121,7 +125,7 @@ __global__ __launch_bounds__(256) void quantize_weights_group_kernel(
     }
     float s = amax / kMax;
     if (s == 0.0f) s = 1.0f;
-    scales[g] = static_cast<uint16_t>(f32_to_f16_bits(s));
+    scales[g] = static_cast<uint16_t>(scale_bf16 ? f32_to_bf16(s) : f32_to_f16_bits(s));
     if constexpr (kBits == 4u) {
         // two bf16 per word -> one byte (low nibble = even column)
         uint32_t packed[kGroup / 8u];
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(256) void quantize_weights_group_kernel(
 // W8 per output channel: one wave per row (columns % 512 == 0), two passes.
 __global__ __launch_bounds__(256) void quantize_weights_row_w8_kernel(
     const uint16_t* __restrict__ src, uint64_t rows, uint32_t cols, uint8_t* __restrict__ data,
-    uint16_t* __restrict__ scales) {
+    uint16_t* __restrict__ scales, bool scale_bf16) {
     const uint64_t row = static_cast<uint64_t>(blockIdx.x) * 4u + (threadIdx.x >> 6);
     if (row >= rows) return;
     const uint32_t lane = threadIdx.x & 63u;
@@ -178,7 +182,8 @@ __global__ __launch_bounds__(256) void quantize_weights_row_w8_kernel(
     for (int offset = 32; offset > 0; offset >>= 1) amax = fmaxf(amax, __shfl_xor(amax, offset, 64));
     float s = amax / 127.0f;
     if (s == 0.0f) s = 1.0f;
-    if (lane == 0) scales[row] = static_cast<uint16_t>(f32_to_f16_bits(s));
+    if (lane == 0)
+        scales[row] = static_cast<uint16_t>(scale_bf16 ? f32_to_bf16(s) : f32_to_f16_bits(s));
     uint2* out = reinterpret_cast<uint2*>(data + row * cols);
     for (uint32_t c = lane; c < cols / 8u; c += 64u) {
         const uint4 v = r[c];
@@ -295,17 +300,19 @@ hipError_t launch_repack(const q38m_expert_weights_v1& src,
         repack_w4_kernel<<<blocks_for(dwords, 256), 256, 0, stream>>>(
             static_cast<const uint32_t*>(src.data), static_cast<uint32_t*>(const_cast<void*>(dst.data)),
             src.rows, src.columns, paired, dwords);
-        const uint64_t scales = elements / 32u;
+        const uint64_t scales = elements / src.group_size;
         repack_w4_scales_kernel<<<blocks_for(scales, 256), 256, 0, stream>>>(
             static_cast<const uint16_t*>(src.scales),
-            static_cast<uint16_t*>(const_cast<void*>(dst.scales)), src.rows, src.columns, paired,
-            scales);
+            static_cast<uint16_t*>(const_cast<void*>(dst.scales)), src.rows, src.columns,
+            128u / src.group_size, paired, scales);
     } else {
         const uint64_t vectors = elements / 16u;
         repack_w8_kernel<<<blocks_for(vectors, 256), 256, 0, stream>>>(
             static_cast<const uint4*>(src.data), static_cast<uint4*>(const_cast<void*>(dst.data)),
             src.rows, src.columns, vectors);
-        const uint64_t scales = static_cast<uint64_t>(src.experts) * src.rows;
+        // W8 scales keep the artifact order (per channel or [E][R][K/g])
+        const uint64_t scales = src.group_size ? elements / src.group_size
+                                               : static_cast<uint64_t>(src.experts) * src.rows;
         copy_u16_kernel<<<blocks_for(scales, 256), 256, 0, stream>>>(
             static_cast<const uint16_t*>(src.scales),
             static_cast<uint16_t*>(const_cast<void*>(dst.scales)), scales);
@@ -321,15 +328,17 @@ hipError_t launch_quantize_weights(const uint16_t* src, const q38m_expert_weight
     const uint4* s4 = reinterpret_cast<const uint4*>(src);
     const uint32_t g = dst.group_size;
     const bool w4 = dst.format == Q38M_FORMAT_W4_SYM;
+    const bool bf16 = dst.scale_dtype == Q38M_SCALE_BF16;
     if (g == 0u) {
         quantize_weights_row_w8_kernel<<<blocks_for(rows, 4), 256, 0, stream>>>(
-            src, rows, dst.columns, data, scales);
+            src, rows, dst.columns, data, scales, bf16);
         return hipGetLastError();
     }
     const uint64_t groups = rows * (dst.columns / g);
     const uint32_t grid = blocks_for(groups, 256);
 #define Q38M_QUANT(BITS, G)                                                                  \
-    quantize_weights_group_kernel<BITS, G><<<grid, 256, 0, stream>>>(s4, groups, data, scales)
+    quantize_weights_group_kernel<BITS, G><<<grid, 256, 0, stream>>>(s4, groups, data, scales, \
+                                                                     bf16)
     if (w4 && g == 32u) Q38M_QUANT(4u, 32u);
     else if (w4 && g == 64u) Q38M_QUANT(4u, 64u);
     else if (w4) Q38M_QUANT(4u, 128u);

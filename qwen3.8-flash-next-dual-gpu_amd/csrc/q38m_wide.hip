@@ -227,17 +227,21 @@ __global__ __launch_bounds__(64) void wide_scatter_kernel(const int32_t* __restr
 
 struct TileQuad {
     uint4 w;  // one 16-channel tile's data of one quad
-    uint2 s;  // its fp16 scales (4 groups)
+    uint2 s;  // its scale words (4, 2 or 1 groups; load_quad_scales)
 };
 
 // Gate/up over a task of up to 128 rows.  A workgroup of 16 waves covers 8
 // gate/up tile pairs: waves 0-7 run the gate tiles, waves 8-15 the matching
 // up tiles, so each wave holds one tile's accumulators (32 VGPRs at 128
-// rows) and four waves fit on a SIMD.  Each wave runs the slab kernel's
-// chain (per group one v_mfma_i32_16x16x32_i8 from a zero accumulator, then
-// y16 = fma(16*acc, s_g, y16) in group order) for kTiles 16-row tiles
+// rows) and four waves fit on a SIMD.  Each wave runs the group chain (per
+// group one v_mfma_i32_16x16x32_i8 from a zero accumulator, then
+// y16 = fma(16*acc, s_g, y16) in group order for fp16 scales) for kTiles 16-row tiles
 // against the same unpacked weight fragment; kTiles (8, 4, 2 or 1) is
 // picked per task from its row count, so the tile loop has no branches.
+// Groups of 64 or 128 columns (kSub = 2 or 4 sub-blocks of 32): the
+// sub-blocks before a group's last chain every tile's int32 accumulator
+// through the MFMA C input, and the last one runs the pinned MFMA/fma
+// interleave from those accumulators.
 // Within a group, tile t+1's MFMA is issued before tile t's v_cvt/v_fma
 // chain, and an empty asm on each tile's accumulators keeps that order (the
 // compiler would otherwise issue every MFMA first and spill their results).
@@ -247,9 +251,9 @@ struct TileQuad {
 // fragments read from LDS while the previous group computes; weights run
 // two quads ahead.  The gate waves hand their y16 to the up waves through
 // LDS for the SwiGLU epilogue.
-template <uint32_t H, uint32_t I, uint32_t kThreads, uint32_t kTiles>
+template <uint32_t H, uint32_t I, uint32_t kThreads, uint32_t kTiles, uint32_t kSub, bool kBf16>
 __device__ __forceinline__ void gate_up_wide_rows(
-    const uint4* __restrict__ wbase, const uint2* __restrict__ sbase,
+    const uint4* __restrict__ wbase, const uint16_t* __restrict__ sbase,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
     uint16_t* __restrict__ mid, uint2 (*a_lds)[4u * kRowTiles * 64u], float* gate_lds,
@@ -258,6 +262,7 @@ __device__ __forceinline__ void gate_up_wide_rows(
     constexpr uint32_t kTilesAll = 2u * I / 16u;
     constexpr uint32_t kQuadWords = kTilesAll * 64u;
     constexpr uint32_t kQuadScales = kTilesAll * 16u;
+    constexpr uint32_t kRowScales = 4u / kSub;       // scale words per row per quad
     constexpr uint32_t kPieces = kTiles * 16u * 8u;  // 16-byte row pieces per quad
     constexpr uint32_t kPerThread = (kPieces + kThreads - 1u) / kThreads;
     const uint32_t lane = threadIdx.x & 63u;
@@ -267,7 +272,8 @@ __device__ __forceinline__ void gate_up_wide_rows(
 
     auto load = [&](uint32_t kq) {
         const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
-        return TileQuad{wbase[k * kQuadWords + lane], sbase[k * kQuadScales + n]};
+        return TileQuad{wbase[k * kQuadWords + lane],
+                        load_quad_scales<kSub, false>(sbase + (k * kQuadScales + n) * kRowScales)};
     };
 
     // Piece i: row r = i/8, 16-byte piece c = i%8 of the row's 128 bytes of
@@ -311,8 +317,8 @@ __device__ __forceinline__ void gate_up_wide_rows(
         const uint2* abuf = a_lds[kq & 1u] + lane;
         const v4i zero = {0, 0, 0, 0};
         const uint32_t ww[4] = {b.w.x, b.w.y, b.w.z, b.w.w};
-        const uint32_t sw[2] = {b.s.x, b.s.y};
         long frag[2][kTiles];
+        v4i chain[kTiles];  // kSub > 1: the group's running int32 tiles
 #pragma unroll
         for (uint32_t t = 0; t < kTiles; ++t) frag[0][t] = as_long(abuf[t * 64u]);
 #pragma unroll
@@ -324,16 +330,35 @@ __device__ __forceinline__ void gate_up_wide_rows(
             }
             const long* a = frag[j & 1u];
             const long bj = unpack_w4x16(ww[j]);
-            const float scale = f16_to_f32((j & 1u) ? (sw[j >> 1] >> 16) : (sw[j >> 1] & 0xffffu));
+            if (j % kSub != kSub - 1u) {
+#pragma unroll
+                for (uint32_t t = 0; t < kTiles; ++t)
+                    chain[t] = mfma_i8_16x16x32(a[t], bj, j % kSub == 0u ? zero : chain[t]);
+                continue;
+            }
+            const uint32_t word = quad_scale_word(b.s, j / kSub);
+            // fp16: y16 = 16*y exactly (partial sums are multiples of 2^-24,
+            // far from the subnormal range).  bf16 words can sit near it, so
+            // they take s/16 (exact) and the chain holds y itself.
+            const float scale = kBf16 ? bf16_to_f32(word) * 0.0625f : f16_to_f32(word);
+            // the group's int32 tile t: d[t & 1] (kSub == 1) or chain[t] in place
             v4i d[2];
-            d[0] = mfma_i8_16x16x32(a[0], bj, zero);
+            auto issue = [&](uint32_t t) {
+                if constexpr (kSub == 1u) d[t & 1u] = mfma_i8_16x16x32(a[t], bj, zero);
+                else chain[t] = mfma_i8_16x16x32(a[t], bj, chain[t]);
+            };
+            auto tile = [&](uint32_t t) -> const v4i& {
+                if constexpr (kSub == 1u) return d[t & 1u];
+                else return chain[t];
+            };
+            issue(0);
 #pragma unroll
             for (uint32_t t = 0; t < kTiles; ++t) {
-                if (t + 1u < kTiles) d[(t + 1u) & 1u] = mfma_i8_16x16x32(a[t + 1u], bj, zero);
+                if (t + 1u < kTiles) issue(t + 1u);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    y[t][i] = __builtin_fmaf(static_cast<float>(d[t & 1u][i]), scale, y[t][i]);
+                    y[t][i] = __builtin_fmaf(static_cast<float>(tile(t)[i]), scale, y[t][i]);
                 asm volatile("" : "+v"(y[t][0]), "+v"(y[t][1]), "+v"(y[t][2]), "+v"(y[t][3]));
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -384,18 +409,19 @@ __device__ __forceinline__ void gate_up_wide_rows(
             const uint32_t p = p0 + r;
             const uint32_t a = packed[p];
             const float st = xs[a / kTopK];
-            const float y_gate = (handoff[r * 16u + n] * 0.0625f) * st;
-            const float y_up = (y[t][i] * 0.0625f) * st;
+            const float unscale = kBf16 ? 1.0f : 0.0625f;
+            const float y_gate = (handoff[r * 16u + n] * unscale) * st;
+            const float y_up = (y[t][i] * unscale) * st;
             mid[static_cast<size_t>(p) * I + channel] =
                 static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
         }
     }
 }
 
-template <uint32_t H, uint32_t I, uint32_t kPairs>
+template <uint32_t H, uint32_t I, uint32_t kPairs, uint32_t kSub, bool kBf16>
 __global__ __launch_bounds__(kPairs * 128) __attribute__((amdgpu_waves_per_eu(4)))
-void gate_up_w4g32_wide_kernel(
-    const uint4* __restrict__ w, const uint2* __restrict__ s,
+void gate_up_w4_wide_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
     const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
@@ -421,20 +447,25 @@ void gate_up_w4g32_wide_kernel(
     // 2p and its up tile slot 2p+1.
     const uint32_t slot = 2u * pair + (up ? 1u : 0u);
     const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTilesAll + slot) * 64u;
-    const uint2* sbase = s + (static_cast<size_t>(e) * kQuads * kTilesAll + slot) * 16u;
+    const uint16_t* sbase =
+        s + (static_cast<size_t>(e) * kQuads * kTilesAll + slot) * 16u * (4u / kSub);
     const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
     if (tiles > 4u)
-        gate_up_wide_rows<H, I, kThreads, 8>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, gate_lds, rows, p0, pair, up);
+        gate_up_wide_rows<H, I, kThreads, 8, kSub, kBf16>(wbase, sbase, xq, xs, packed,
+                                                           route_weights, mid, a_lds, gate_lds,
+                                                           rows, p0, pair, up);
     else if (tiles > 2u)
-        gate_up_wide_rows<H, I, kThreads, 4>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, gate_lds, rows, p0, pair, up);
+        gate_up_wide_rows<H, I, kThreads, 4, kSub, kBf16>(wbase, sbase, xq, xs, packed,
+                                                           route_weights, mid, a_lds, gate_lds,
+                                                           rows, p0, pair, up);
     else if (tiles == 2u)
-        gate_up_wide_rows<H, I, kThreads, 2>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, gate_lds, rows, p0, pair, up);
+        gate_up_wide_rows<H, I, kThreads, 2, kSub, kBf16>(wbase, sbase, xq, xs, packed,
+                                                           route_weights, mid, a_lds, gate_lds,
+                                                           rows, p0, pair, up);
     else
-        gate_up_wide_rows<H, I, kThreads, 1>(wbase, sbase, xq, xs, packed, route_weights, mid,
-                                             a_lds, gate_lds, rows, p0, pair, up);
+        gate_up_wide_rows<H, I, kThreads, 1, kSub, kBf16>(wbase, sbase, xq, xs, packed,
+                                                           route_weights, mid, a_lds, gate_lds,
+                                                           rows, p0, pair, up);
 }
 
 // ---- down -------------------------------------------------------------------
@@ -448,22 +479,48 @@ void gate_up_w4g32_wide_kernel(
 // ahead.  One A fragment is live at a time (row by row): holding all kRows
 // of them took the kernel to 256 VGPRs with spills (1.07 ms vs 1.00 ms on
 // a config-5 layer).  kRows (8, 4, 2 or 1 row tiles) is picked per task from its row
-// count.  o = ((float)acc * ws[e][c]) * sm[r], as the slab kernel.
-template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kRows>
+// count.  Per channel (kBlocksPerGroup == I/64): o = ((float)acc * ws[e][c])
+// * sm[r], as the slab kernel.  Groups of 64 or 128 columns (kBlocksPerGroup
+// 1 or 2 K blocks): acc restarts at each group's first block and, at its
+// last, joins the fp32 chain y = fma((float)acc, s[e][c][g], y) in group
+// order; o = y * sm[r].
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kRows,
+          uint32_t kBlocksPerGroup, bool kBf16>
 __device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
-                                                  const uint16_t* __restrict__ ws_row,
+                                                  const uint16_t* __restrict__ ws_expert,
                                                   const uint4* a_lds, const float* row_scale,
                                                   uint32_t rows, uint32_t p0, uint32_t tile0,
                                                   float* __restrict__ out) {
     constexpr uint32_t kBlocks = I / 64u;
+    constexpr bool kPerChannel = kBlocksPerGroup == kBlocks;
+    constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
+    const v4i zero = {0, 0, 0, 0};
+    // the tiles' scales of channel 16*(tile0+t)+n, artifact order
+    // [E][rows][groups]; per channel read after the K loop (fewer live VGPRs)
+    float ws[kTilesPerWave][kGroups];
+    auto load_scales = [&]() {
+#pragma unroll
+        for (uint32_t t = 0; t < kTilesPerWave; ++t)
+#pragma unroll
+            for (uint32_t g = 0; g < kGroups; ++g) {
+                const uint32_t word = ws_expert[((tile0 + t) * 16u + n) * kGroups + g];
+                ws[t][g] = kBf16 ? bf16_to_f32(word) : f16_to_f32(word);
+            }
+    };
+    if constexpr (!kPerChannel) load_scales();
     v4i acc[kTilesPerWave][kRows];
+    float y[kTilesPerWave][kRows][4];  // grouped: the fp32 chain
 #pragma unroll
     for (uint32_t t = 0; t < kTilesPerWave; ++t)
 #pragma unroll
-        for (uint32_t r = 0; r < kRows; ++r) acc[t][r] = v4i{0, 0, 0, 0};
+        for (uint32_t r = 0; r < kRows; ++r) {
+            acc[t][r] = zero;
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) y[t][r][i] = 0.0f;
+        }
     // tile t's K block kb: wt[(t * kBlocks + kb) * 64]
     uint4 wq[3][kTilesPerWave];
     auto load_w = [&](uint32_t kb, uint4 (&dst)[kTilesPerWave]) {
@@ -481,14 +538,30 @@ __device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
             const v4i a = as_v4i(a_lds[(kb * kRowTiles + r) * 64u + lane]);
 #pragma unroll
             for (uint32_t t = 0; t < kTilesPerWave; ++t)
-                acc[t][r] = mfma_i8_16x16x64(a, as_v4i(wq[kb % 3u][t]), acc[t][r]);
+                acc[t][r] = mfma_i8_16x16x64(a, as_v4i(wq[kb % 3u][t]),
+                                             !kPerChannel && kb % kBlocksPerGroup == 0u
+                                                 ? zero
+                                                 : acc[t][r]);
+        }
+        if constexpr (!kPerChannel) {
+            if (kb % kBlocksPerGroup == kBlocksPerGroup - 1u) {
+#pragma unroll
+                for (uint32_t t = 0; t < kTilesPerWave; ++t)
+#pragma unroll
+                    for (uint32_t r = 0; r < kRows; ++r)
+#pragma unroll
+                        for (uint32_t i = 0; i < 4u; ++i)
+                            y[t][r][i] = __builtin_fmaf(static_cast<float>(acc[t][r][i]),
+                                                        ws[t][kb / kBlocksPerGroup], y[t][r][i]);
+            }
+            // one K block's tiles live at a time (unpinned, the zero-started
+            // blocks would all be issued at once)
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    if constexpr (kPerChannel) load_scales();
     // a row's kTilesPerWave adjacent 16-channel pieces go out in consecutive
     // stores, so its 64*kTilesPerWave bytes meet in L2 as whole lines
-    float ws[kTilesPerWave];
-#pragma unroll
-    for (uint32_t t = 0; t < kTilesPerWave; ++t) ws[t] = f16_to_f32(ws_row[(tile0 + t) * 16u + n]);
 #pragma unroll
     for (uint32_t r = 0; r < kRows; ++r)
 #pragma unroll
@@ -499,12 +572,14 @@ __device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
             float* dst = out + static_cast<size_t>(p0 + row) * H + tile0 * 16u + n;
 #pragma unroll
             for (uint32_t t = 0; t < kTilesPerWave; ++t)
-                dst[16u * t] = (static_cast<float>(acc[t][r][i]) * ws[t]) * sm;
+                dst[16u * t] = kPerChannel ? (static_cast<float>(acc[t][r][i]) * ws[t][0]) * sm
+                                           : y[t][r][i] * sm;
         }
 }
 
-template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
-__global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave,
+          uint32_t kBlocksPerGroup, bool kBf16>
+__global__ __launch_bounds__(kWaves * 64) void down_w8_wide_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
@@ -551,15 +626,19 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
         row_scale[threadIdx.x] = threadIdx.x < rows ? ms[p0 + threadIdx.x] : 0.0f;
     __syncthreads();
 
-    const uint16_t* ws_row = s + static_cast<size_t>(e) * H;
+    const uint16_t* ws_expert = s + static_cast<size_t>(e) * H * (kBlocks / kBlocksPerGroup);
+    auto run = [&](auto row_tiles) {
+        down_w8_wide_rows<H, I, kTilesPerWave, decltype(row_tiles)::value, kBlocksPerGroup,
+                          kBf16>(wt, ws_expert, a_lds, row_scale, rows, p0, tile0, out);
+    };
     if (tiles > 4u)
-        down_w8_wide_rows<H, I, kTilesPerWave, 8>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
+        run(std::integral_constant<uint32_t, 8>{});
     else if (tiles > 2u)
-        down_w8_wide_rows<H, I, kTilesPerWave, 4>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
+        run(std::integral_constant<uint32_t, 4>{});
     else if (tiles == 2u)
-        down_w8_wide_rows<H, I, kTilesPerWave, 2>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
+        run(std::integral_constant<uint32_t, 2>{});
     else
-        down_w8_wide_rows<H, I, kTilesPerWave, 1>(wt, ws_row, a_lds, row_scale, rows, p0, tile0, out);
+        run(std::integral_constant<uint32_t, 1>{});
 }
 
 // Down, W4 group-32 (the all-W4 layer policy), over a task of up to 128
@@ -572,10 +651,12 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8pc_wide_kernel(
 // twice).  A wave streams its tiles' weights
 // one quad ahead and runs the chain group by group with the
 // same pinned MFMA/v_cvt/v_fma interleave as the gate/up kernel, over kRows
-// (8, 4, 2 or 1) row tiles picked per task.
-template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kStride, uint32_t kRows>
+// (8, 4, 2 or 1) row tiles picked per task; groups of 64 or 128 columns
+// chain their sub-blocks' int32 tiles as the gate/up kernel does.
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kStride, uint32_t kRows,
+          uint32_t kSub, bool kBf16>
 __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
-                                                  const uint2* __restrict__ st,
+                                                  const uint16_t* __restrict__ st,
                                                   const uint2* a_lds, const float* row_scale,
                                                   uint32_t rows, uint32_t p0, uint32_t tile0,
                                                   float* __restrict__ out) {
@@ -591,7 +672,8 @@ __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
     auto load = [&](uint32_t t, uint32_t kq) {
         const uint32_t tt = t < kTilesPerWave ? t : kTilesPerWave - 1u;
         return TileQuad{wt[(kq * kTiles + tt * kStride) * 64u],
-                        st[(kq * kTiles + tt * kStride) * 16u]};
+                        load_quad_scales<kSub, false>(st + (kq * kTiles + tt * kStride) * 16u *
+                                                               (4u / kSub))};
     };
     TileQuad cur = load(0, 0);
 #pragma unroll 1
@@ -605,7 +687,7 @@ __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
         for (uint32_t kq = 0; kq < kQuads; ++kq) {
           const TileQuad next = kq + 1u < kQuads ? load(t, kq + 1u) : load(t + 1u, 0);
           const uint32_t bw[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
-          const uint32_t cw[2] = {cur.s.x, cur.s.y};
+          v4i chain[kRows];  // kSub > 1: the group's running int32 tiles
 #pragma unroll
           for (uint32_t j = 0; j < 4u; ++j) {
             const uint32_t g = kq * 4u + j;
@@ -613,17 +695,32 @@ __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
 #pragma unroll
             for (uint32_t r = 0; r < kRows; ++r) a[r] = as_long(abuf[(g * kRowTiles + r) * 64u]);
             const long bj = unpack_w4x16(bw[j]);
-            const uint32_t h = (j & 1u) ? (cw[j >> 1] >> 16) : (cw[j >> 1] & 0xffffu);
-            const float scale = f16_to_f32(h) * 0.0625f;
+            if (j % kSub != kSub - 1u) {
+#pragma unroll
+              for (uint32_t r = 0; r < kRows; ++r)
+                chain[r] = mfma_i8_16x16x32(a[r], bj, j % kSub == 0u ? zero : chain[r]);
+              continue;
+            }
+            const uint32_t word = quad_scale_word(cur.s, j / kSub);
+            const float scale = (kBf16 ? bf16_to_f32(word) : f16_to_f32(word)) * 0.0625f;
+            // the group's int32 tile r: d[r & 1] (kSub == 1) or chain[r] in place
             v4i d[2];
-            d[0] = mfma_i8_16x16x32(a[0], bj, zero);
+            auto issue = [&](uint32_t r) {
+                if constexpr (kSub == 1u) d[r & 1u] = mfma_i8_16x16x32(a[r], bj, zero);
+                else chain[r] = mfma_i8_16x16x32(a[r], bj, chain[r]);
+            };
+            auto tile = [&](uint32_t r) -> const v4i& {
+                if constexpr (kSub == 1u) return d[r & 1u];
+                else return chain[r];
+            };
+            issue(0);
 #pragma unroll
             for (uint32_t r = 0; r < kRows; ++r) {
-                if (r + 1u < kRows) d[(r + 1u) & 1u] = mfma_i8_16x16x32(a[r + 1u], bj, zero);
+                if (r + 1u < kRows) issue(r + 1u);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    y[r][i] = __builtin_fmaf(static_cast<float>(d[r & 1u][i]), scale, y[r][i]);
+                    y[r][i] = __builtin_fmaf(static_cast<float>(tile(r)[i]), scale, y[r][i]);
                 asm volatile("" : "+v"(y[r][0]), "+v"(y[r][1]), "+v"(y[r][2]), "+v"(y[r][3]));
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -646,10 +743,11 @@ __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
     }
 }
 
-template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave>
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave, uint32_t kSub,
+          bool kBf16>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4)))
-void down_w4g32_wide_kernel(
-    const uint4* __restrict__ w, const uint2* __restrict__ s,
+void down_w4_wide_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
     constexpr uint32_t kQuads = I / 128u;
@@ -697,20 +795,21 @@ void down_w4g32_wide_kernel(
     // wave w: tiles tile0 + t * kWaves
     const uint32_t tile0 = blockIdx.x * kWaves * kTilesPerWave + wave;
     const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile0) * 64u + lane;
-    const uint2* st = s + (static_cast<size_t>(e) * kQuads * kTiles + tile0) * 16u + n;
+    const uint16_t* st =
+        s + ((static_cast<size_t>(e) * kQuads * kTiles + tile0) * 16u + n) * (4u / kSub);
     const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
+    auto run = [&](auto row_tiles) {
+        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, decltype(row_tiles)::value, kSub, kBf16>(
+            wt, st, a_lds, row_scale, rows, p0, tile0, out);
+    };
     if (tiles > 4u)
-        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 8>(wt, st, a_lds, row_scale, rows, p0,
-                                                           tile0, out);
+        run(std::integral_constant<uint32_t, 8>{});
     else if (tiles > 2u)
-        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 4>(wt, st, a_lds, row_scale, rows, p0,
-                                                           tile0, out);
+        run(std::integral_constant<uint32_t, 4>{});
     else if (tiles == 2u)
-        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 2>(wt, st, a_lds, row_scale, rows, p0,
-                                                           tile0, out);
+        run(std::integral_constant<uint32_t, 2>{});
     else
-        down_w4_wide_rows<H, I, kTilesPerWave, kWaves, 1>(wt, st, a_lds, row_scale, rows, p0,
-                                                           tile0, out);
+        run(std::integral_constant<uint32_t, 1>{});
 }
 
 }  // namespace
@@ -731,41 +830,117 @@ hipError_t launch_build_wide_plan(const int32_t* ids, uint32_t tokens,
     return hipGetLastError();
 }
 
-hipError_t launch_gate_up_w4g32_wide(const void* data, const void* scales, const int8_t* xq,
+namespace {
+
+template <uint32_t kSub, bool kBf16>
+void launch_gate_up_wide_sub(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
+                             const uint32_t* packed, const float* route_weights,
+                             const q38m_task_v1* tasks, uint32_t task_count,
+                             uint16_t* weighted_mid, hipStream_t stream) {
+    constexpr uint32_t kPairs = 8;
+    const dim3 grid(kInter / 16u / kPairs, task_count);
+    gate_up_w4_wide_kernel<kHidden, kInter, kPairs, kSub, kBf16>
+        <<<grid, kPairs * 128u, 0, stream>>>(static_cast<const uint4*>(w.data),
+                                             static_cast<const uint16_t*>(w.scales), xq, xs,
+                                             packed, route_weights, tasks, weighted_mid);
+}
+
+// Per channel: four tiles per wave (the tuned BASELINE shape).  Grouped:
+// the fp32 chain doubles the live accumulator state, so one tile per wave.
+template <uint32_t kBlocksPerGroup, bool kBf16>
+void launch_down_w8_wide_groups(const q38m_expert_weights_v1& w, const int8_t* mid_q,
+                                const float* mid_s, const q38m_task_v1* tasks,
+                                uint32_t task_count, float* route_output, hipStream_t stream) {
+    constexpr uint32_t kWaves = 8;
+    constexpr uint32_t kTilesPerWave = kBlocksPerGroup == kInter / 64u ? 4u : 1u;
+    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
+    down_w8_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, kBf16>
+        <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(w.data),
+                                            static_cast<const uint16_t*>(w.scales), mid_q, mid_s,
+                                            tasks, route_output);
+}
+
+template <uint32_t kSub, bool kBf16>
+void launch_down_w4_wide_sub(const q38m_expert_weights_v1& w, const int8_t* mid_q,
+                             const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+                             float* route_output, hipStream_t stream) {
+    constexpr uint32_t kWaves = 16, kTilesPerWave = 2;
+    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
+    down_w4_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave, kSub, kBf16>
+        <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(w.data),
+                                            static_cast<const uint16_t*>(w.scales), mid_q, mid_s,
+                                            tasks, route_output);
+}
+
+template <bool kBf16>
+hipError_t launch_gate_up_wide_dtype(const q38m_expert_weights_v1& w, const int8_t* xq,
                                      const float* xs, const uint32_t* packed,
                                      const float* route_weights, const q38m_task_v1* tasks,
                                      uint32_t task_count, uint16_t* weighted_mid,
                                      hipStream_t stream) {
-    constexpr uint32_t kPairs = 8;
-    const dim3 grid(kInter / 16u / kPairs, task_count);
-    gate_up_w4g32_wide_kernel<kHidden, kInter, kPairs><<<grid, kPairs * 128u, 0, stream>>>(
-        static_cast<const uint4*>(data), static_cast<const uint2*>(scales), xq, xs, packed,
-        route_weights, tasks, weighted_mid);
+    switch (w.group_size) {
+        case 32u: launch_gate_up_wide_sub<1, kBf16>(w, xq, xs, packed, route_weights, tasks,
+                                                    task_count, weighted_mid, stream); break;
+        case 64u: launch_gate_up_wide_sub<2, kBf16>(w, xq, xs, packed, route_weights, tasks,
+                                                    task_count, weighted_mid, stream); break;
+        case 128u: launch_gate_up_wide_sub<4, kBf16>(w, xq, xs, packed, route_weights, tasks,
+                                                     task_count, weighted_mid, stream); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
-hipError_t launch_down_w8pc_wide(const void* data, const void* scales, const int8_t* mid_q,
-                                 const float* mid_s, const q38m_task_v1* tasks,
-                                 uint32_t task_count, float* route_output, hipStream_t stream) {
-    constexpr uint32_t kWaves = 8, kTilesPerWave = 4;
-    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
-    down_w8pc_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave>
-        <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(data),
-                                            static_cast<const uint16_t*>(scales), mid_q, mid_s,
-                                            tasks, route_output);
-    return hipGetLastError();
-}
-
-hipError_t launch_down_w4g32_wide(const void* data, const void* scales, const int8_t* mid_q,
+template <bool kBf16>
+hipError_t launch_down_wide_dtype(const q38m_expert_weights_v1& w, const int8_t* mid_q,
                                   const float* mid_s, const q38m_task_v1* tasks,
                                   uint32_t task_count, float* route_output, hipStream_t stream) {
-    constexpr uint32_t kWaves = 16, kTilesPerWave = 2;
-    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
-    down_w4g32_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave>
-        <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(data),
-                                            static_cast<const uint2*>(scales), mid_q, mid_s,
-                                            tasks, route_output);
+    constexpr uint32_t kBlocks = kInter / 64u;
+    if (w.format == Q38M_FORMAT_W8_SYM) {
+        switch (w.group_size) {
+            case 0u: launch_down_w8_wide_groups<kBlocks, kBf16>(w, mid_q, mid_s, tasks,
+                                                                task_count, route_output,
+                                                                stream); break;
+            case 64u: launch_down_w8_wide_groups<1, kBf16>(w, mid_q, mid_s, tasks, task_count,
+                                                           route_output, stream); break;
+            case 128u: launch_down_w8_wide_groups<2, kBf16>(w, mid_q, mid_s, tasks, task_count,
+                                                            route_output, stream); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (w.group_size) {
+            case 32u: launch_down_w4_wide_sub<1, kBf16>(w, mid_q, mid_s, tasks, task_count,
+                                                        route_output, stream); break;
+            case 64u: launch_down_w4_wide_sub<2, kBf16>(w, mid_q, mid_s, tasks, task_count,
+                                                        route_output, stream); break;
+            case 128u: launch_down_w4_wide_sub<4, kBf16>(w, mid_q, mid_s, tasks, task_count,
+                                                         route_output, stream); break;
+            default: return hipErrorInvalidValue;
+        }
+    }
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gate_up_wide(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
+                               const uint32_t* packed, const float* route_weights,
+                               const q38m_task_v1* tasks, uint32_t task_count,
+                               uint16_t* weighted_mid, hipStream_t stream) {
+    return w.scale_dtype == Q38M_SCALE_BF16
+               ? launch_gate_up_wide_dtype<true>(w, xq, xs, packed, route_weights, tasks,
+                                                 task_count, weighted_mid, stream)
+               : launch_gate_up_wide_dtype<false>(w, xq, xs, packed, route_weights, tasks,
+                                                  task_count, weighted_mid, stream);
+}
+
+hipError_t launch_down_wide(const q38m_expert_weights_v1& w, const int8_t* mid_q,
+                            const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+                            float* route_output, hipStream_t stream) {
+    return w.scale_dtype == Q38M_SCALE_BF16
+               ? launch_down_wide_dtype<true>(w, mid_q, mid_s, tasks, task_count, route_output,
+                                              stream)
+               : launch_down_wide_dtype<false>(w, mid_q, mid_s, tasks, task_count,
+                                               route_output, stream);
 }
 
 }  // namespace q38m

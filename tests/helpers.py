@@ -43,25 +43,28 @@ class Layer:
     """One MoE layer's weights: row-major on the device, repacked MFMA16 on
     the device, and the row-major bytes on the host for the oracle."""
 
-    def __init__(self, q38m, orc, seed, layer, gate_up_fmt, down_fmt, with_host=True):
+    def __init__(self, q38m, orc, seed, layer, gate_up_fmt, down_fmt, with_host=True,
+                 gate_up_bf16=False, down_bf16=False):
         gu_tag, dn_tag, _, _ = W.layer_tags(layer)
         _, gbits, ggroup, gsigma = gate_up_fmt
         _, dbits, dgroup, dsigma = down_fmt
         fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+        dtype = {False: q38m.SCALE_F16, True: q38m.SCALE_BF16}
         self.gu_rm = q38m.synth_weights(seed, gu_tag, fmt[gbits], ggroup, W.EXPERTS,
-                                        2 * W.INTER, W.HIDDEN, gsigma)
+                                        2 * W.INTER, W.HIDDEN, gsigma,
+                                        scale_dtype=dtype[gate_up_bf16])
         self.dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dbits], dgroup, W.EXPERTS, W.HIDDEN,
-                                        W.INTER, dsigma)
+                                        W.INTER, dsigma, scale_dtype=dtype[down_bf16])
         self.gu = q38m.repack(self.gu_rm, paired=True)
         self.dn = q38m.repack(self.dn_rm)
         self.host_gu = self.host_dn = None
         if with_host:
             self.host_gu = orc.HostWeights(host(self.gu_rm.data, np.uint8),
                                            host(self.gu_rm.scales, np.uint16), gbits, ggroup,
-                                           W.EXPERTS, 2 * W.INTER, W.HIDDEN)
+                                           W.EXPERTS, 2 * W.INTER, W.HIDDEN, gate_up_bf16)
             self.host_dn = orc.HostWeights(host(self.dn_rm.data, np.uint8),
                                            host(self.dn_rm.scales, np.uint16), dbits, dgroup,
-                                           W.EXPERTS, W.HIDDEN, W.INTER)
+                                           W.EXPERTS, W.HIDDEN, W.INTER, down_bf16)
 
     def drop_row_major(self):
         self.gu_rm = self.dn_rm = None

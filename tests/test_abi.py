@@ -98,8 +98,10 @@ def test_workspace_binding(q38m):
         q38m.call("q38m_moe_prefill_workspace_bind", base + 16, sizes[2], 512, ctypes.byref(ws))
 
 
-def fake_weights(q38m, fmt=2, group=32, layout=3, rows=1024, cols=2048, experts=512):
-    return q38m.ExpertWeights(0x200000, 0x400000, fmt, group, 1, layout, experts, rows, cols)
+def fake_weights(q38m, fmt=2, group=32, layout=3, rows=1024, cols=2048, experts=512,
+                 scale_dtype=1):
+    return q38m.ExpertWeights(0x200000, 0x400000, fmt, group, scale_dtype, layout, experts, rows,
+                              cols)
 
 
 def test_gate_up_validation(q38m):
@@ -114,7 +116,11 @@ def test_gate_up_validation(q38m):
 
     with pytest.raises(q38m.Unsupported):
         call(fake_weights(q38m, layout=0))
-    for bad in (fake_weights(q38m, fmt=3), fake_weights(q38m, group=128),
+    # groups of 32, 64 and 128 with fp16 or bf16 scales are formats; these are not
+    for bad in (fake_weights(q38m, fmt=3), fake_weights(q38m, group=16),
+                fake_weights(q38m, group=96), fake_weights(q38m, group=256),
+                fake_weights(q38m, group=0), fake_weights(q38m, scale_dtype=0),
+                fake_weights(q38m, scale_dtype=3),
                 fake_weights(q38m, rows=1280), fake_weights(q38m, cols=2560),
                 fake_weights(q38m, experts=256),
                 fake_weights(q38m, layout=2)):  # gate/up needs the paired layout
@@ -137,9 +143,20 @@ def test_down_validation(q38m):
         q38m.call("q38m_moe_grouped_down_v1",
                   ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=0, rows=2048, cols=512)),
                   *args)
-    with pytest.raises(q38m.InvalidArgument):  # W8 with a group size
+    for group in (32, 96, 256):  # W8 down: per channel or groups of 64/128 only
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_grouped_down_v1",
+                      ctypes.byref(fake_weights(q38m, fmt=3, group=group, layout=2, rows=2048,
+                                                cols=512)), *args)
+    for group in (0, 16, 256):  # W4 down: groups of 32/64/128 only
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_grouped_down_v1",
+                      ctypes.byref(fake_weights(q38m, fmt=2, group=group, layout=2, rows=2048,
+                                                cols=512)), *args)
+    with pytest.raises(q38m.InvalidArgument):  # unknown scale dtype
         q38m.call("q38m_moe_grouped_down_v1",
-                  ctypes.byref(fake_weights(q38m, fmt=3, group=32, layout=2, rows=2048, cols=512)), *args)
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512,
+                                            scale_dtype=7)), *args)
     with pytest.raises(q38m.InvalidArgument):  # transposed shape
         q38m.call("q38m_moe_grouped_down_v1",
                   ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=2, rows=512, cols=2048)), *args)
@@ -184,7 +201,8 @@ def test_weight_quantizer_validation(q38m):
         return q38m.ExpertWeights(data, scales, fmt, group, scale, layout, 512, rows, cols)
 
     for d, err in [(desc(layout=2), q38m.InvalidArgument),        # not row-major
-                   (desc(scale=2), q38m.InvalidArgument),         # scale dtype
+                   (desc(scale=0), q38m.InvalidArgument),         # scale dtype
+                   (desc(scale=3), q38m.InvalidArgument),         # scale dtype
                    (desc(data=0x200008), q38m.InvalidArgument),   # misaligned data
                    (desc(group=16), q38m.Unsupported),            # W4 group 16
                    (desc(group=0), q38m.Unsupported),             # W4 per channel
@@ -302,6 +320,17 @@ def test_repack_and_synth_validation(q38m):
     with pytest.raises(q38m.Unsupported):  # W4 per-channel has no MFMA16 layout
         q38m.call("q38m_repack_expert_weights", ctypes.byref(fake_weights(q38m, group=0, layout=0)),
                   ctypes.byref(fake_weights(q38m, group=0, layout=2)), None, 0)
+    with pytest.raises(q38m.Unsupported):  # W4 groups of 32/64/128 only
+        q38m.call("q38m_repack_expert_weights", ctypes.byref(fake_weights(q38m, group=256, layout=0)),
+                  ctypes.byref(fake_weights(q38m, group=256, layout=3)), None, 0)
+    with pytest.raises(q38m.Unsupported):  # W8 per channel or groups of 64/128 only
+        q38m.call("q38m_repack_expert_weights",
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=32, layout=0, rows=2048, cols=512)),
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=32, layout=2, rows=2048, cols=512)),
+                  None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # the scale dtype is kept
+        q38m.call("q38m_repack_expert_weights", ctypes.byref(src),
+                  ctypes.byref(fake_weights(q38m, layout=3, scale_dtype=2)), None, 0)
     w8_src = fake_weights(q38m, fmt=3, group=0, layout=0, rows=2048, cols=512)
     with pytest.raises(q38m.Unsupported):  # the paired layout is W4-only
         q38m.call("q38m_repack_expert_weights", ctypes.byref(w8_src),

@@ -3,15 +3,19 @@
 - int8 quantisation: numpy float32 IEEE division + rint (a library
   routine) and the invariants |q| <= 127, absmax element -> +-127, zero
   row -> q = 0 with scale 1.
-- int32 accumulators: numpy int64 matmul per 32-wide group (brute force)
-  for W4 g32 and per row for W8 per-channel.
+- int32 accumulators: numpy int64 matmul per group (brute force) for W4
+  and W8 in groups of 32, 64 and 128 and per row (per channel), with fp16
+  and bf16 scale words decoded independently of the oracle (numpy float16;
+  bf16 as the high half of a float32).
 - gate/up epilogue: the oracle's weighted_mid against a float64 evaluation
   of y = sum_g acc_g*s_g * s_t followed by the reference's bf16 rounding
   sequence: >= 99% of words exact and every word within 2 bf16 ulps (the
   fp32 group chain rounds differently from float64 only in the last bits).
 - down + combine: the oracle's output against a float64 evaluation of the
   whole layer from the oracle's own mid_q (exact int64 accumulators,
-  float64 scales and rank-order sum), within 2 bf16 ulps.
+  float64 scales and rank-order sum), within 2 bf16 ulps; for the BASELINE
+  formats and for groups of 64/128 with bf16 scales (a wrong group index
+  or scale decode moves whole rows, far beyond the tolerance).
 - the reference's one-hot KAT (cuda/cuda_kernel_tests.cu:823-846),
   restated for the int8 contract, bit-exact, for W4 and W8 down.
 - grouped (plan) evaluation equals per-token evaluation bit for bit.
@@ -46,10 +50,25 @@ def test_quantize_rows_numpy_and_invariants(orc):
     assert (np.abs(q[np.arange(64), arg]) == 127)[np.arange(64) != 3].all()
 
 
-@pytest.mark.parametrize("bits,group", [(4, 32), (8, 0), (4, 0), (8, 32)])
-def test_row_accumulators_brute_force(orc, bits, group):
+def decode_scales(w, expert):
+    """float64 [rows][groups] from the scale words, without the oracle."""
+    g = w.cols // w.group if w.group else 1
+    per = w.rows * g
+    words = w.scales[expert * per:(expert + 1) * per]
+    if w.scale_bf16:
+        f = (words.astype(np.uint32) << 16).view(np.float32)
+    else:
+        f = words.view(np.float16)
+    return f.astype(np.float64).reshape(w.rows, g)
+
+
+@pytest.mark.parametrize("scale_bf16", [False, True])
+@pytest.mark.parametrize("bits,group", [(4, 32), (8, 0), (4, 0), (8, 32), (4, 64), (4, 128),
+                                        (8, 64), (8, 128)])
+def test_row_accumulators_brute_force(orc, bits, group, scale_bf16):
     E, R, K = 3, 32, 512
-    w = orc.synth_weights(9, 40, bits, group, E, R, K, 0.02)
+    w = orc.synth_weights(9, 40, bits, group, E, R, K, 0.02, scale_bf16)
+    assert np.array_equal(w.scale_matrix(0), decode_scales(w, 0).astype(np.float32))
     rng = np.random.default_rng(bits + group)
     x = rng.integers(-127, 128, K).astype(np.int8)
     for e in range(E):
@@ -60,17 +79,20 @@ def test_row_accumulators_brute_force(orc, bits, group):
             want = (W[row].reshape(-1, g) * x.astype(np.int64).reshape(-1, g)).sum(axis=1)
             assert np.array_equal(got, want)
             # the scaled row value: the fp32 chain vs float64 within 1e-5 relative
-            scales = w.scale_matrix(e)[row].astype(np.float64)
+            scales = decode_scales(w, e)[row]
             ref = float((want * scales).sum())
             val = orc.row_value(w, e, row, x)
             assert abs(val - ref) <= 1e-5 * max(1.0, np.abs(want * scales).sum())
 
 
-def small_layer(orc, seed, T, down_bits):
+def small_layer(orc, seed, T, down_bits, gate_group=32, gate_bf16=False, down_group=None,
+                down_bf16=False):
     H, I = 2048, 512
-    gu = orc.synth_weights(seed, 10, 4, 32, 512, 2 * I, H, 0.02)
-    dn = orc.synth_weights(seed, 20, down_bits, 32 if down_bits == 4 else 0, 512, H, I,
-                           0.02 if down_bits == 4 else 0.002)
+    if down_group is None:
+        down_group = 32 if down_bits == 4 else 0
+    gu = orc.synth_weights(seed, 10, 4, gate_group, 512, 2 * I, H, 0.02, gate_bf16)
+    dn = orc.synth_weights(seed, 20, down_bits, down_group, 512, H, I,
+                           0.02 if down_bits == 4 else 0.002, down_bf16)
     hid = orc.synth_normal_bf16(seed, 1, T * H).reshape(T, H)
     lg = orc.synth_logits(seed, 2, T)
     return gu, dn, hid, lg
@@ -93,10 +115,16 @@ def bf16_close(orc, got_words, want_words, ulps=2, atol=1e-4):
     return np.abs(got - want) <= ulps * ulp + atol
 
 
-@pytest.mark.parametrize("down_bits", [4, 8])
-def test_layer_against_float64(orc, down_bits):
+# (down bits, gate/up group, gate/up bf16 scales, down group, down bf16 scales)
+LAYER_FORMATS = [(4, 32, False, 32, False), (8, 32, False, 0, False),
+                 (8, 128, True, 128, True), (4, 64, False, 64, True), (8, 64, True, 64, False),
+                 (4, 128, True, 128, False)]
+
+
+@pytest.mark.parametrize("down_bits,ggroup,gbf16,dgroup,dbf16", LAYER_FORMATS)
+def test_layer_against_float64(orc, down_bits, ggroup, gbf16, dgroup, dbf16):
     T = 6
-    gu, dn, hid, lg = small_layer(orc, 31, T, down_bits)
+    gu, dn, hid, lg = small_layer(orc, 31, T, down_bits, ggroup, gbf16, dgroup, dbf16)
     r = orc.moe(hid, gu, dn, logits=lg, intermediates=True)
     p = orc.parse_plan(r["plan"], T)
     xq, xs = r["xq"], r["xs"]
@@ -109,8 +137,9 @@ def test_layer_against_float64(orc, down_bits):
         a = int(packed[pos])
         t, e = a // 10, int(r["ids"].ravel()[a])
         W = gu.unpacked(e).astype(np.int64)
-        S = gu.scale_matrix(e).astype(np.float64)
-        acc = (W.reshape(2 * I, 64, 32) * xq[t].astype(np.int64).reshape(1, 64, 32)).sum(-1)
+        S = decode_scales(gu, e)
+        acc = (W.reshape(2 * I, H // ggroup, ggroup) *
+               xq[t].astype(np.int64).reshape(1, H // ggroup, ggroup)).sum(-1)
         y = (acc * S).sum(-1) * float(xs[t])
         g = orc.bf16_to_f32(orc.f32_to_bf16(y[:I].astype(np.float32))).astype(np.float64)
         u = orc.bf16_to_f32(orc.f32_to_bf16(y[I:].astype(np.float32))).astype(np.float64)
@@ -129,12 +158,13 @@ def test_layer_against_float64(orc, down_bits):
             pos = int(p["inverse"][a])
             e = int(r["ids"].ravel()[a])
             W = dn.unpacked(e).astype(np.int64)
-            S = dn.scale_matrix(e).astype(np.float64)
+            S = decode_scales(dn, e)
             qm = r["mid_q"][pos].astype(np.int64)
-            if down_bits == 8:
+            if dgroup == 0:
                 o = (W @ qm) * S[:, 0]
             else:
-                o = ((W.reshape(H, 16, 32) * qm.reshape(1, 16, 32)).sum(-1) * S).sum(-1)
+                o = ((W.reshape(H, I // dgroup, dgroup) *
+                      qm.reshape(1, I // dgroup, dgroup)).sum(-1) * S).sum(-1)
             out64[t] += o * float(r["mid_s"][pos])
     want = orc.f32_to_bf16(out64.astype(np.float32))
     assert bf16_close(orc, r["output"], want).all()

@@ -8,7 +8,8 @@ Pins:
 - per group: |q| <= qmax; the element of largest magnitude quantises to
   +-qmax with its sign; an all-zero group has scale 1 (fp16 0x3C00) and q = 0;
   every |w/s - q| <= 1/2 (round to nearest), except where clipping binds;
-- the stored scale is numpy's float16 of the float32 absmax / qmax;
+- the stored scale is numpy's float16 (or torch's bfloat16, the reference's
+  f32_to_bf16_rne at :61-66, :232) of the float32 absmax / qmax;
 - q equals numpy's float32 rint(w / s) clipped (an independent float32 evaluation).
 """
 import numpy as np
@@ -38,8 +39,17 @@ def test_reference_int4_packing_kat():
     assert scales.tolist() == [[0x3C00]]
 
 
-@pytest.mark.parametrize("bits,group,cols", [(4, 32, 256), (4, 128, 512), (8, 0, 512), (8, 128, 256)])
-def test_quantiser_invariants(bits, group, cols):
+def bf16_words(x32):
+    """torch's round-to-nearest-even bfloat16 of float32 values, as words."""
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(x32, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("scale_bf16", [False, True])
+@pytest.mark.parametrize("bits,group,cols", [(4, 32, 256), (4, 64, 256), (4, 128, 512),
+                                             (8, 0, 512), (8, 64, 256), (8, 128, 256)])
+def test_quantiser_invariants(bits, group, cols, scale_bf16):
     rng = np.random.default_rng(bits * 1000 + group + cols)
     rows = 64
     w32 = (rng.standard_normal((rows, cols)) * rng.uniform(1e-3, 3.0, (rows, 1))).astype(np.float32)
@@ -47,7 +57,7 @@ def test_quantiser_invariants(bits, group, cols):
     w32[5, :g] = 0.0  # one all-zero group
     w = orc.f32_to_bf16(w32)
     wf = orc.bf16_to_f32(w)
-    data, scales = orc.quantize_weights(w, bits, group)
+    data, scales = orc.quantize_weights(w, bits, group, scale_bf16)
     qmax = 7 if bits == 4 else 127
     q = unpack_w4(data, cols) if bits == 4 else data.view(np.int8)
     assert np.abs(q).max() <= qmax
@@ -56,10 +66,13 @@ def test_quantiser_invariants(bits, group, cols):
     amax = np.abs(grouped).max(axis=2)
     s32 = amax / np.float32(qmax)
     s32 = np.where(s32 == 0, np.float32(1.0), s32).astype(np.float32)
-    # stored scale: numpy's float16 of the float32 scale
-    assert np.array_equal(scales, s32.astype(np.float16).view(np.uint16))
+    # stored scale: numpy's float16 (torch's bfloat16) of the float32 scale
+    if scale_bf16:
+        assert np.array_equal(scales, bf16_words(s32))
+    else:
+        assert np.array_equal(scales, s32.astype(np.float16).view(np.uint16))
     # zero group
-    assert scales[5, 0] == 0x3C00 and not qg[5, 0].any()
+    assert scales[5, 0] == (0x3F80 if scale_bf16 else 0x3C00) and not qg[5, 0].any()
     # the largest element maps to +-qmax with its sign
     idx = np.abs(grouped).argmax(axis=2)
     top_w = np.take_along_axis(grouped, idx[..., None], 2)[..., 0]
