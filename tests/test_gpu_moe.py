@@ -178,8 +178,7 @@ def test_shared_expert_combine(q38m, orc, layers):
 def test_decode_equals_prefill_and_oracle(q38m, orc, layers, config):
     layer = layers(config)
     t = torch()
-    scratch = t.empty(q38m.lib().q38m_moe_decode_scratch_bytes() // 2 + 64, dtype=t.int16,
-                      device="cuda")
+    scratch = decode_scratch(q38m)
     ws = q38m.PrefillWorkspace_(1)
     for step in range(6):
         hidden = synth_hidden(q38m, 77 + step, 1, 1)
@@ -293,8 +292,7 @@ def test_config3_decode_stack_reduced(q38m, orc, layers):
     residual add between layers, decode path."""
     t = torch()
     seed = W.CONFIGS[3]["seed"]
-    scratch = t.empty(q38m.lib().q38m_moe_decode_scratch_bytes() // 2 + 64, dtype=t.int16,
-                      device="cuda")
+    scratch = decode_scratch(q38m)
     state = synth_hidden(q38m, seed, 1, 1)
     fused_state = state.clone()
     host_state = host(state, np.uint16).copy()
@@ -319,6 +317,48 @@ def test_config3_decode_stack_reduced(q38m, orc, layers):
                                      orc.bf16_to_f32(ref["output"].ravel()))
         assert np.array_equal(host(state, np.uint16).ravel(), host_state.ravel())
         assert np.array_equal(host(fused_state, np.uint16).ravel(), host_state.ravel())
+
+
+def test_decode_graph_replays(q38m, orc, layers):
+    """The decode under a HIP graph: three layers of three tokens captured
+    once and replayed three times, with eager decode calls on the same
+    scratch between the replays; every replay equals the eager run."""
+    t = torch()
+    seed = W.CONFIGS[3]["seed"]
+    stack = [layers(3, i) for i in range(3)]
+    logits = [[synth_logits(q38m, seed, 50 + 3 * k + i, 1) for i in range(3)] for k in range(3)]
+    start = synth_hidden(q38m, seed, 49, 1)
+    scratch = decode_scratch(q38m)
+    states = [t.empty_like(start) for _ in range(10)]
+
+    def run():
+        states[0].copy_(start)
+        for k in range(3):
+            for i, layer in enumerate(stack):
+                j = 3 * k + i
+                decode_fused(q38m, layer, states[j], logits[k][i], scratch, output=states[j + 1],
+                             residual=states[j])
+
+    run()
+    eager = states[9].clone()
+    # the oracle agrees on the first layer
+    ref = orc.moe(host(start, np.uint16), stack[0].host_gu, stack[0].host_dn,
+                  logits=host(logits[0][0], np.float32), grouped=False)
+    want = orc.f32_to_bf16(orc.bf16_to_f32(host(start, np.uint16)) +
+                           orc.bf16_to_f32(ref["output"]))
+    assert np.array_equal(host(states[1], np.uint16), want)
+    graph = t.cuda.CUDAGraph()
+    with t.cuda.graph(graph):
+        run()
+    for replay in range(3):
+        states[9].zero_()
+        graph.replay()
+        t.cuda.synchronize()
+        assert t.equal(states[9], eager), replay
+        # eager work on the same scratch between replays
+        other = decode_fused(q38m, stack[1], start, logits[2][2], scratch)
+        t.cuda.synchronize()
+        assert other.shape == start.shape
 
 
 def test_config4_zipf_chunk_as_slabs(q38m, orc, layers):
