@@ -116,7 +116,7 @@ typedef struct q38m_route_plan_v1 {
 #define Q38M_LAYOUT_ROW_MAJOR 0u   /* canonical artifact layout */
 #define Q38M_LAYOUT_MFMA16 2u      /* device layout for the 16x16 int8 MFMA kernels */
 #define Q38M_LAYOUT_MFMA16_PAIRED 3u /* MFMA16 with row tile t next to tile t+rows/32
-                                        (the gate/up halves), W4 only */
+                                        (the gate/up halves) */
 
 typedef struct q38m_expert_weights_v1 {
     const void* data;
@@ -130,10 +130,10 @@ typedef struct q38m_expert_weights_v1 {
     uint32_t columns;     /* K: H for gate/up, I for down */
 } q38m_expert_weights_v1;
 
-/* Formats the grouped kernels run (prefill, chunk and decode alike):
- * gate/up W4 in groups of 32, 64 or 128 (MFMA16_PAIRED); down W8 per
- * channel or in groups of 64 or 128, or W4 in groups of 32, 64 or 128
- * (MFMA16); fp16 or bf16 scale words.  The reference model's routed
+/* Formats the grouped kernels run (prefill, chunk and decode alike), for
+ * gate/up (MFMA16_PAIRED) and down (MFMA16) alike: W4 in groups of 32, 64
+ * or 128; W8 per channel or in groups of 64 or 128; fp16 or bf16 scale
+ * words.  The reference model's routed
  * experts are W4 group-128 (interior layers) and W8 group-128 (edge layers,
  * gate/up too) with bf16 scales (tools/q38_quant_policy.py:164-190); the
  * BASELINE formats are W4 g32 / W8 per channel with fp16 scales.
@@ -150,7 +150,10 @@ typedef struct q38m_expert_weights_v1 {
  *   W4 scales [E][cols/128][slot][16 rows][128/group] (same order: 4, 2
  *     or 1 words per row and quad for groups of 32, 64, 128).
  *   W8 data  [E][rows/16][cols/64][64 lanes][16 B]; lane l holds row 16t+n,
- *     columns 64kb+16q .. +15.   W8 scales stay in the artifact order. */
+ *     columns 64kb+16q .. +15.   W8 scales stay in the artifact order.
+ *   W8 paired (gate/up) [E][cols/64][slot][64 lanes][16 B], K-block-major:
+ *     for one 64-wide K block every slot is adjacent; slot s holds row tile
+ *     s/2 + (s%2)*rows/32, lanes as W8. */
 
 /* ---- sizes: include/q38/cuda_moe_prefill.h:73-93 --------------------- */
 uint32_t q38m_moe_prefill_routes_v1(uint32_t tokens);

@@ -64,9 +64,12 @@ bool valid_scale_dtype(uint32_t dtype) {
 }
 bool w4_group(uint32_t g) { return g == 32u || g == 64u || g == 128u; }
 
+bool w8_group(uint32_t g) { return g == 0u || g == 64u || g == 128u; }
+
 bool valid_gate_up(const q38m_expert_weights_v1* w) {
     return w && w->data && w->scales && aligned(w->data, 16) && aligned(w->scales, 8) &&
-           w->format == Q38M_FORMAT_W4_SYM && w4_group(w->group_size) &&
+           ((w->format == Q38M_FORMAT_W4_SYM && w4_group(w->group_size)) ||
+            (w->format == Q38M_FORMAT_W8_SYM && w8_group(w->group_size))) &&
            valid_scale_dtype(w->scale_dtype) && w->layout == Q38M_LAYOUT_MFMA16_PAIRED &&
            w->experts == Q38M_ROUTE_EXPERTS && w->rows == 2u * Q38M_INTERMEDIATE &&
            w->columns == Q38M_HIDDEN;
@@ -596,11 +599,11 @@ int q38m_repack_expert_weights(const q38m_expert_weights_v1* src,
                      src->group_size == 128u) &&
                     src->columns % 64u == 0u &&
                     (src->group_size == 0u || src->columns % src->group_size == 0u) &&
-                    dst->layout == Q38M_LAYOUT_MFMA16;
+                    (dst->layout == Q38M_LAYOUT_MFMA16 || src->rows % 32u == 0u);
     if (!w4 && !w8)
         return fail(Q38M_ERR_UNSUPPORTED,
-                    "repack supports W4 groups 32/64/128 (MFMA16 or MFMA16_PAIRED) and W8 per "
-                    "channel or groups 64/128 (MFMA16)");
+                    "repack supports W4 groups 32/64/128 and W8 per channel or groups 64/128 "
+                    "(MFMA16 or MFMA16_PAIRED)");
     if (int rc = select_device(device)) return rc;
     return finish(q38m::launch_repack(*src, *dst, as_stream(stream)), "repack kernels");
 }

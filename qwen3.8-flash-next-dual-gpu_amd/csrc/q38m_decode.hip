@@ -35,10 +35,13 @@ namespace {
 constexpr uint32_t kDecodeBlocks = 256;
 constexpr uint32_t kDecodeThreads = kSelectThreads;
 
-// kSub: 32-column sub-blocks per W4 group (1, 2 or 4: groups of 32, 64,
-// 128).  A group's sub-block accumulators add exactly in int32 before the
-// fp32 chain; bf16: scale words are bf16 (else fp16).
-template <uint32_t H, uint32_t I, uint32_t kSub>
+// W4 (kW8 false): kPer = 32-column sub-blocks per group (1, 2 or 4: groups
+// of 32, 64, 128), the MFMA16 quad-major layout.  W8: kPer = 64-column K
+// blocks per group (1, 2, or H/64 = per output channel), the paired
+// K-block-major layout, scales in the artifact order.  A group's partial
+// accumulators add exactly in int32 before the fp32 chain; bf16: scale
+// words are bf16 (else fp16).
+template <uint32_t H, uint32_t I, bool kW8, uint32_t kPer>
 __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, bool bf16,
     const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
@@ -88,10 +91,38 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     const uint32_t kq = lane & 15u;
     const uint32_t c = (lane >> 4) & 1u;
     const uint32_t u = lane >> 5;
-    const size_t tile = (static_cast<size_t>(e) * kQuads + kq) * kSlots + 2u * pair + u;
-    const uint4* wp = w + tile * 64u + n0 + c;
-    const uint4 b0 = wp[0], b1 = wp[16], b2 = wp[32], b3 = wp[48];
-    const uint2 sc = load_quad_scales<kSub, false>(s + (tile * 16u + n0 + c) * (4u / kSub));
+    // W4: quad kq of the slot's tile, 16 bytes per row per 32-column group.
+    // W8: blocks 2kq and 2kq+1 (the same 128 columns), 16 bytes per row and
+    // lane group q: bq[4*block + q].
+    uint4 bq[kW8 ? 8 : 4];
+    uint2 sc = make_uint2(0u, 0u);
+    uint32_t sw = 0;
+    if constexpr (!kW8) {
+        const size_t tile = (static_cast<size_t>(e) * kQuads + kq) * kSlots + 2u * pair + u;
+        const uint4* wp = w + tile * 64u + n0 + c;
+        bq[0] = wp[0];
+        bq[1] = wp[16];
+        bq[2] = wp[32];
+        bq[3] = wp[48];
+        sc = load_quad_scales<kPer, false>(s + (tile * 16u + n0 + c) * (4u / kPer));
+    } else {
+        constexpr uint32_t kBlocks = H / 64u;
+        const uint32_t slot = 2u * pair + u;
+#pragma unroll
+        for (uint32_t b = 0; b < 2u; ++b) {
+            const uint4* wp = w + ((static_cast<size_t>(e) * kBlocks + 2u * kq + b) * kSlots + slot) *
+                                      64u + n0 + c;
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) bq[4u * b + q] = wp[16u * q];
+        }
+        const size_t row = static_cast<size_t>(e) * 2u * I + (u ? I : 0u) + 16u * pair + n0 + c;
+        if constexpr (kPer == kBlocks)
+            sw = s[row];
+        else if constexpr (kPer == 1u)
+            sw = *reinterpret_cast<const uint32_t*>(s + row * kBlocks + 2u * kq);
+        else
+            sw = s[row * (kBlocks / 2u) + kq];
+    }
 
     // int8 token (same arithmetic as the row quantiser)
     const float xs = row_scale(amax_lds);
@@ -102,6 +133,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     }
     __syncthreads();
 
+    float y = 0.0f;
+    if constexpr (!kW8) {
     // group j of quad kq, chunk q: k = 32(4kq+j) + 8q + {0..3} (low nibbles)
     // and + {4..7} (high nibbles); nibbles sit in the high half of each byte
     // (16*w), so acc is 16x the group accumulator.
@@ -111,7 +144,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
         const uint4 xv = x_lds[kq * kQuadPad + i];
         xw[4 * i] = xv.x; xw[4 * i + 1] = xv.y; xw[4 * i + 2] = xv.z; xw[4 * i + 3] = xv.w;
     }
-    const uint4 bq[4] = {b0, b1, b2, b3};
     int acc[4] = {0, 0, 0, 0};
 #pragma unroll
     for (uint32_t q = 0; q < 4u; ++q) {
@@ -124,25 +156,67 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
             acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xw[8u * j + 2u * q + 1u]), acc[j], false);
         }
     }
-    float gs[4u / kSub];
-    int gacc[4u / kSub];
+    float gs[4u / kPer];
+    int gacc[4u / kPer];
 #pragma unroll
-    for (uint32_t gi = 0; gi < 4u / kSub; ++gi) {
+    for (uint32_t gi = 0; gi < 4u / kPer; ++gi) {
         gs[gi] = scale_to_f32(quad_scale_word(sc, gi), bf16) * 0.0625f;
-        gacc[gi] = acc[gi * kSub];
+        gacc[gi] = acc[gi * kPer];
 #pragma unroll
-        for (uint32_t j = 1; j < kSub; ++j) gacc[gi] += acc[gi * kSub + j];
+        for (uint32_t j = 1; j < kPer; ++j) gacc[gi] += acc[gi * kPer + j];
     }
     // fp32 chain in group order: lane kq continues lane kq-1's value (row_shr:1
     // inside each 16-lane row); after 16 steps lane 15 holds the row's y.
-    float y = 0.0f;
 #pragma unroll
     for (uint32_t step = 0; step < kQuads; ++step) {
         float t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
 #pragma unroll
-        for (uint32_t gi = 0; gi < 4u / kSub; ++gi)
+        for (uint32_t gi = 0; gi < 4u / kPer; ++gi)
             t = __builtin_fmaf(static_cast<float>(gacc[gi]), gs[gi], t);
         y = t;
+    }
+    } else {
+        // block b (= 2kq + b), lane group q: columns 64(2kq+b) + 16q .. +15
+        int acc[2] = {0, 0};
+#pragma unroll
+        for (uint32_t b = 0; b < 2u; ++b)
+#pragma unroll
+            for (uint32_t q = 0; q < 4u; ++q) {
+                const uint4 xv = x_lds[kq * kQuadPad + 4u * b + q];
+                const uint4 wv = bq[4u * b + q];
+                acc[b] = __builtin_amdgcn_sdot4(static_cast<int>(wv.x), static_cast<int>(xv.x), acc[b], false);
+                acc[b] = __builtin_amdgcn_sdot4(static_cast<int>(wv.y), static_cast<int>(xv.y), acc[b], false);
+                acc[b] = __builtin_amdgcn_sdot4(static_cast<int>(wv.z), static_cast<int>(xv.z), acc[b], false);
+                acc[b] = __builtin_amdgcn_sdot4(static_cast<int>(wv.w), static_cast<int>(xv.w), acc[b], false);
+            }
+        if constexpr (kPer == H / 64u) {
+            // per channel: one int32 over the row (16 lanes), y = (float)acc * s
+            int sum = acc[0] + acc[1];
+#pragma unroll
+            for (int offset = 8; offset > 0; offset >>= 1) sum += __shfl_xor(sum, offset, 16);
+            y = static_cast<float>(sum) * scale_to_f32(sw, bf16);
+        } else {
+            float gs[2];
+            int gacc[2];
+            if constexpr (kPer == 1u) {
+                gs[0] = scale_to_f32(sw & 0xffffu, bf16);
+                gs[1] = scale_to_f32(sw >> 16, bf16);
+                gacc[0] = acc[0];
+                gacc[1] = acc[1];
+            } else {
+                gs[0] = scale_to_f32(sw, bf16);
+                gacc[0] = acc[0] + acc[1];
+            }
+            // the same chain over the 16 lanes of the row, 128 columns per lane
+#pragma unroll
+            for (uint32_t step = 0; step < kQuads; ++step) {
+                float t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
+#pragma unroll
+                for (uint32_t gi = 0; gi < 2u / kPer; ++gi)
+                    t = __builtin_fmaf(static_cast<float>(gacc[gi]), gs[gi], t);
+                y = t;
+            }
+        }
     }
     const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 15));
     const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 31));
@@ -368,20 +442,27 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
     const uint16_t* gs = static_cast<const uint16_t*>(gate_up.scales);
     const bool gbf16 = gate_up.scale_dtype == Q38M_SCALE_BF16;
     int32_t* ids_out = logits != nullptr ? scratch_ids : nullptr;
-    switch (gate_up.group_size) {
-        case 32u:
-            decode_gate_up_kernel<kHidden, kInter, 1><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
-                gw, gs, gbf16, hidden, logits, ids, weights, top_k, ids_out, mid);
-            break;
-        case 64u:
-            decode_gate_up_kernel<kHidden, kInter, 2><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
-                gw, gs, gbf16, hidden, logits, ids, weights, top_k, ids_out, mid);
-            break;
-        case 128u:
-            decode_gate_up_kernel<kHidden, kInter, 4><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
-                gw, gs, gbf16, hidden, logits, ids, weights, top_k, ids_out, mid);
-            break;
-        default: return hipErrorInvalidValue;
+    auto gate_up_launch = [&](auto w8, auto per) {
+        decode_gate_up_kernel<kHidden, kInter, decltype(w8)::value, decltype(per)::value>
+            <<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(gw, gs, gbf16, hidden, logits, ids,
+                                                           weights, top_k, ids_out, mid);
+    };
+    using W4 = std::false_type;
+    using W8 = std::true_type;
+    if (gate_up.format == Q38M_FORMAT_W8_SYM) {
+        switch (gate_up.group_size) {
+            case 0u: gate_up_launch(W8{}, std::integral_constant<uint32_t, kHidden / 64u>{}); break;
+            case 64u: gate_up_launch(W8{}, std::integral_constant<uint32_t, 1>{}); break;
+            case 128u: gate_up_launch(W8{}, std::integral_constant<uint32_t, 2>{}); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (gate_up.group_size) {
+            case 32u: gate_up_launch(W4{}, std::integral_constant<uint32_t, 1>{}); break;
+            case 64u: gate_up_launch(W4{}, std::integral_constant<uint32_t, 2>{}); break;
+            case 128u: gate_up_launch(W4{}, std::integral_constant<uint32_t, 4>{}); break;
+            default: return hipErrorInvalidValue;
+        }
     }
     const int32_t* down_ids = logits != nullptr ? scratch_ids : ids;
     constexpr uint32_t kBlocks = kInter / 64u;

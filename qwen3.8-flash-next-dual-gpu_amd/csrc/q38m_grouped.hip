@@ -193,6 +193,147 @@ void gate_up_w4_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Gate/up, W8 (the reference's edge-layer format, tools/q38_quant_policy.py:
+// 164-190), paired K-block-major MFMA16 layout: per 64-wide K block one
+// v_mfma_i32_16x16x64_i8 per tile.  Groups of kBlocksPerGroup blocks (64 or
+// 128 columns): the group's blocks chain through the accumulator input and
+// at its last block y = fmaf((float)acc_g, s_g, y) in group order; per
+// channel (kBlocksPerGroup == H/64): one int32 over K, y = (float)acc * s.
+// Scales stay in the artifact order [E][rows][K/G] (gate rows 0..I-1, up
+// rows I..2I-1).  Then y * s_t and the SwiGLU fold, as the W4 kernel.
+// Same plan as the W4 kernel: the task's 16 token rows (32 KiB) staged once
+// in LDS in the A-operand order ([block][lane], 16 bytes per lane), weights
+// two blocks ahead through three register sets, one contiguous span of
+// 2*kWaves KiB per step.
+// ---------------------------------------------------------------------------
+struct BlockWeights {
+    uint4 g, u;       // gate and up tile data of one K block
+    uint32_t sg, su;  // their scale words for the block's group
+};
+
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kBlocksPerGroup, bool kBf16>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6, 8)))
+void gate_up_w8_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
+    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    constexpr uint32_t kBlocks = H / 64u;
+    constexpr uint32_t kTiles = 2u * I / 16u;
+    constexpr uint32_t kThreads = kWaves * 64u;
+    constexpr bool kPerChannel = kBlocksPerGroup == kBlocks;
+    constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
+    __shared__ uint4 a_lds[kBlocks * 64u];
+
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t pair = blockIdx.x * kWaves + wave;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+
+    constexpr uint32_t kBlockWords = kTiles * 64u;  // uint4 per K block of one expert
+    const uint4* wbase = w + (static_cast<size_t>(e) * kBlocks * kTiles + 2u * pair) * 64u;
+    // this lane's gate row 16p+n and up row I+16p+n
+    const uint16_t* sg_row = s + (static_cast<size_t>(e) * 2u * I + pair * 16u + n) * kGroups;
+    const uint16_t* su_row = sg_row + static_cast<size_t>(I) * kGroups;
+    auto load = [&](uint32_t kb) {
+        const uint32_t k = kb < kBlocks ? kb : kBlocks - 1u;  // past the end: re-read (L1 hit)
+        const uint32_t wi = k * kBlockWords + lane;
+        const uint32_t g = kPerChannel ? 0u : k / kBlocksPerGroup;
+        return BlockWeights{load_stream(wbase + wi), load_stream(wbase + wi + 64u),
+                            static_cast<uint32_t>(sg_row[g]), static_cast<uint32_t>(su_row[g])};
+    };
+
+    // Stage A: 16-byte chunk c of token row r is K block c/4, lane group c%4;
+    // rows past valid_rows replicate row 0.
+    constexpr uint32_t kChunks = 16u * (H / 16u) / kThreads;
+    static_assert(16u * (H / 16u) % kThreads == 0u, "whole chunks per thread");
+    uint32_t token[kChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t r = (threadIdx.x + c * kThreads) / (H / 16u);
+        token[c] = packed[p0 + (r < rows ? r : 0u)];
+    }
+    BlockWeights r0 = load(0), r1 = load(1), r2;
+    uint4 v[kChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t chunk = (threadIdx.x + c * kThreads) % (H / 16u);
+        v[c] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token[c] / kTopK) * H)[chunk];
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < kChunks; ++c) {
+        const uint32_t i = threadIdx.x + c * kThreads;
+        const uint32_t chunk = i % (H / 16u);
+        a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + i / (H / 16u)] = v[c];
+    }
+    __syncthreads();
+
+    const v4i zero = {0, 0, 0, 0};
+    v4i cg = zero, cu = zero;
+    float yg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float yu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto block = [&](uint32_t kb, const BlockWeights& b) {
+        const v4i a = as_v4i(a_lds[kb * 64u + lane]);
+        const bool first = kb % kBlocksPerGroup == 0u;
+        cg = mfma_i8_16x16x64(a, as_v4i(b.g), first ? zero : cg);
+        cu = mfma_i8_16x16x64(a, as_v4i(b.u), first ? zero : cu);
+        if constexpr (!kPerChannel) {
+            if (kb % kBlocksPerGroup == kBlocksPerGroup - 1u) {
+                const float scale_g = scale_to_f32(b.sg, kBf16);
+                const float scale_u = scale_to_f32(b.su, kBf16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    yg[i] = __builtin_fmaf(static_cast<float>(cg[i]), scale_g, yg[i]);
+                    yu[i] = __builtin_fmaf(static_cast<float>(cu[i]), scale_u, yu[i]);
+                }
+            }
+        }
+    };
+    static_assert(kBlocks % 3u == 2u, "three-set rotation plus two peeled blocks");
+#pragma unroll 1
+    for (uint32_t kb = 0; kb + 2u < kBlocks; kb += 3u) {
+        r2 = load(kb + 2u);
+        __builtin_amdgcn_sched_barrier(0);
+        block(kb, r0);
+        r0 = load(kb + 3u);
+        __builtin_amdgcn_sched_barrier(0);
+        block(kb + 1u, r1);
+        r1 = load(kb + 4u);
+        __builtin_amdgcn_sched_barrier(0);
+        block(kb + 2u, r2);
+    }
+    block(kBlocks - 2u, r0);
+    block(kBlocks - 1u, r1);
+    if constexpr (kPerChannel) {
+        const float scale_g = scale_to_f32(r1.sg, kBf16);
+        const float scale_u = scale_to_f32(r1.su, kBf16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            yg[i] = static_cast<float>(cg[i]) * scale_g;
+            yu[i] = static_cast<float>(cu[i]) * scale_u;
+        }
+    }
+
+    const uint32_t channel = pair * 16u + n;
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        const uint32_t r = 4u * q + i;
+        if (r >= rows) continue;
+        const uint32_t p = p0 + r;
+        const uint32_t a = packed[p];
+        const float st = xs[a / kTopK];
+        mid[static_cast<size_t>(p) * I + channel] =
+            static_cast<uint16_t>(swiglu_fold(yg[i] * st, yu[i] * st, route_weights[a]));
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Down, W8, MFMA16 layout (16 int8 per lane per 64-wide K block), per output
 // channel or in groups of kBlocksPerGroup K blocks (64 or 128 columns).
 // Per channel (kBlocksPerGroup == I/64): acc = sum_k qm[r][k] * W[e][c][k]
@@ -470,6 +611,25 @@ void launch_gate_up_sub(const q38m_expert_weights_v1& w, const int8_t* xq, const
 }
 
 template <uint32_t kBlocksPerGroup>
+void launch_gate_up_w8_groups(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
+                              const uint32_t* packed, const float* route_weights,
+                              const q38m_task_v1* tasks, uint32_t task_count,
+                              uint16_t* weighted_mid, hipStream_t stream) {
+    constexpr uint32_t kWaves = 8;
+    const dim3 grid(kInter / 16u / kWaves, task_count);
+    const auto* data = static_cast<const uint4*>(w.data);
+    const auto* scales = static_cast<const uint16_t*>(w.scales);
+    if (w.scale_dtype == Q38M_SCALE_BF16)
+        gate_up_w8_kernel<kHidden, kInter, kWaves, kBlocksPerGroup, true>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, xq, xs, packed, route_weights, tasks,
+                                                weighted_mid);
+    else
+        gate_up_w8_kernel<kHidden, kInter, kWaves, kBlocksPerGroup, false>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, xq, xs, packed, route_weights, tasks,
+                                                weighted_mid);
+}
+
+template <uint32_t kBlocksPerGroup>
 void launch_down_w8_groups(const q38m_expert_weights_v1& w, const int8_t* mid_q,
                            const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
                            float* route_output, hipStream_t stream) {
@@ -507,6 +667,19 @@ hipError_t launch_gate_up(const q38m_expert_weights_v1& w, const int8_t* xq, con
                           const uint32_t* packed, const float* route_weights,
                           const q38m_task_v1* tasks, uint32_t task_count, uint16_t* weighted_mid,
                           hipStream_t stream) {
+    if (w.format == Q38M_FORMAT_W8_SYM) {
+        constexpr uint32_t kBlocks = kHidden / 64u;
+        switch (w.group_size) {
+            case 0u: launch_gate_up_w8_groups<kBlocks>(w, xq, xs, packed, route_weights, tasks,
+                                                       task_count, weighted_mid, stream); break;
+            case 64u: launch_gate_up_w8_groups<1>(w, xq, xs, packed, route_weights, tasks,
+                                                  task_count, weighted_mid, stream); break;
+            case 128u: launch_gate_up_w8_groups<2>(w, xq, xs, packed, route_weights, tasks,
+                                                   task_count, weighted_mid, stream); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (w.group_size) {
         case 32u: launch_gate_up_sub<1>(w, xq, xs, packed, route_weights, tasks, task_count,
                                         weighted_mid, stream); break;

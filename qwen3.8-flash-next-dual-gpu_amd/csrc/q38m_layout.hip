@@ -82,6 +82,27 @@ __global__ void repack_w8_kernel(const uint4* __restrict__ src, uint4* __restric
     dst[o] = src[((e * rows + rt * 16u + n) * cols + kb * 64u + q * 16u) / 16u];
 }
 
+// W8 gate/up row-major [E][R][K] -> paired K-block-major MFMA16
+// [E][K/64][slot][64][16 B]: for block kb every slot (1 KiB) is adjacent,
+// slot s holding row tile s/2 + (s%2)*R/32 (the gate tile of channel block
+// p next to its up tile), lane (q,n) row 16t+n, columns 64kb+16q .. +15.
+__global__ void repack_w8_paired_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                        uint32_t rows, uint32_t cols, uint64_t total) {
+    const uint64_t o = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (o >= total) return;
+    const uint32_t blocks = cols / 64u;
+    const uint32_t row_tiles = rows / 16u;
+    const uint32_t lane = static_cast<uint32_t>(o & 63u);
+    const uint64_t unit = o >> 6;
+    const uint32_t slot = static_cast<uint32_t>(unit % row_tiles);
+    const uint64_t tmp = unit / row_tiles;
+    const uint32_t kb = static_cast<uint32_t>(tmp % blocks);
+    const uint64_t e = tmp / blocks;
+    const uint32_t n = lane & 15u, q = lane >> 4;
+    const uint32_t row = slot_tile(slot, row_tiles, true) * 16u + n;
+    dst[o] = src[((e * rows + row) * cols + kb * 64u + q * 16u) / 16u];
+}
+
 // ---------------------------------------------------------------------------
 // Weight quantiser (tools/q38_artifact_compiler.py:193-253, quantize_groupwise):
 // per group s = max|w| / qmax (qmax 7 for W4, 127 for W8), s == 0 -> 1,
@@ -307,9 +328,14 @@ hipError_t launch_repack(const q38m_expert_weights_v1& src,
             128u / src.group_size, paired, scales);
     } else {
         const uint64_t vectors = elements / 16u;
-        repack_w8_kernel<<<blocks_for(vectors, 256), 256, 0, stream>>>(
-            static_cast<const uint4*>(src.data), static_cast<uint4*>(const_cast<void*>(dst.data)),
-            src.rows, src.columns, vectors);
+        if (dst.layout == Q38M_LAYOUT_MFMA16_PAIRED)
+            repack_w8_paired_kernel<<<blocks_for(vectors, 256), 256, 0, stream>>>(
+                static_cast<const uint4*>(src.data),
+                static_cast<uint4*>(const_cast<void*>(dst.data)), src.rows, src.columns, vectors);
+        else
+            repack_w8_kernel<<<blocks_for(vectors, 256), 256, 0, stream>>>(
+                static_cast<const uint4*>(src.data),
+                static_cast<uint4*>(const_cast<void*>(dst.data)), src.rows, src.columns, vectors);
         // W8 scales keep the artifact order (per channel or [E][R][K/g])
         const uint64_t scales = src.group_size ? elements / src.group_size
                                                : static_cast<uint64_t>(src.experts) * src.rows;

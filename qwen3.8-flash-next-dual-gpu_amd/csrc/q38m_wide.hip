@@ -468,6 +468,223 @@ void gate_up_w4_wide_kernel(
                                                            rows, p0, pair, up);
 }
 
+// Gate/up, W8 (paired K-block-major layout; the reference's edge-layer
+// format) over a task of up to 128 rows: the W4 kernel's plan with 64-wide
+// K blocks -- 16 waves (8 gate tiles, 8 up tiles), one tile per wave for
+// kTiles 16-row tiles, A staged one K block (8 KiB) at a time into a
+// double-buffered LDS image [row tile][lane] of 16-byte fragments, weights
+// two blocks ahead.  Groups of one block (64 columns): per tile one
+// v_mfma_i32_16x16x64_i8 from zero, then y = fma((float)acc, s_g, y) with
+// the MFMA/fma interleave pinned; groups of two blocks or per channel: each
+// tile's int32 accumulator chains through the MFMA input (kTiles more
+// registers) and joins the chain at the group's last block (per channel:
+// y = (float)acc * s at the end).  Scales in the artifact order.
+template <uint32_t H, uint32_t I, uint32_t kThreads, uint32_t kTiles, uint32_t kBlocksPerGroup,
+          bool kBf16>
+__device__ __forceinline__ void gate_up_w8_wide_rows(
+    const uint4* __restrict__ wbase, const uint16_t* __restrict__ srow,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
+    uint16_t* __restrict__ mid, uint4 (*a_lds)[kRowTiles * 64u], float* gate_lds,
+    uint32_t rows, uint32_t p0, uint32_t pair, bool up) {
+    constexpr uint32_t kBlocks = H / 64u;
+    constexpr uint32_t kBlockWords = 2u * I / 16u * 64u;  // uint4 per K block of one expert
+    constexpr bool kPerChannel = kBlocksPerGroup == kBlocks;
+    constexpr uint32_t kPieces = kTiles * 16u * 4u;  // 16-byte row pieces per block
+    constexpr uint32_t kPerThread = (kPieces + kThreads - 1u) / kThreads;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u;
+    const uint32_t q = lane >> 4;
+    const uint32_t wave_in_half = (threadIdx.x >> 6) & 7u;
+    const v4i zero = {0, 0, 0, 0};
+
+    struct Block {
+        uint4 w;     // the tile's 16 bytes of one K block
+        uint32_t s;  // the scale word of the block's group
+    };
+    auto load = [&](uint32_t kb) {
+        const uint32_t k = kb < kBlocks ? kb : kBlocks - 1u;  // past the end: re-read (L1 hit)
+        const uint32_t g = kPerChannel ? 0u : k / kBlocksPerGroup;
+        return Block{wbase[k * kBlockWords + lane], static_cast<uint32_t>(srow[g])};
+    };
+
+    // Piece i: row r = i/4, 16-byte piece c = i%4 of the row's 64 bytes of
+    // the block (lane group c).  Rows past valid_rows stage zeros.
+    const uint4* row_src[kPerThread];
+    uint32_t lds_at[kPerThread];
+    bool alive[kPerThread], staged[kPerThread];
+#pragma unroll
+    for (uint32_t u = 0; u < kPerThread; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / 4u, c = i % 4u;
+        staged[u] = i < kPieces;
+        alive[u] = staged[u] && r < rows;
+        const uint32_t token = alive[u] ? packed[p0 + r] / kTopK : 0u;
+        row_src[u] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token) * H) + c;
+        lds_at[u] = (r / 16u) * 64u + c * 16u + r % 16u;
+    }
+    uint4 pieces[kPerThread];
+    auto load_a = [&](uint32_t kb) {
+#pragma unroll
+        for (uint32_t u = 0; u < kPerThread; ++u)
+            pieces[u] = alive[u] ? row_src[u][kb * 4u] : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto store_a = [&](uint32_t buffer) {
+#pragma unroll
+        for (uint32_t u = 0; u < kPerThread; ++u)
+            if (staged[u]) a_lds[buffer][lds_at[u]] = pieces[u];
+    };
+
+    float y[kTiles][4];
+    v4i acc[kTiles];  // groups of two blocks / per channel: the running int32 tiles
+#pragma unroll
+    for (uint32_t t = 0; t < kTiles; ++t) {
+        acc[t] = zero;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) y[t][i] = 0.0f;
+    }
+
+    auto multiply = [&](uint32_t kb, const Block& b) {
+        const uint4* abuf = a_lds[kb & 1u] + lane;
+        const v4i bw = as_v4i(b.w);
+        const float scale = kBf16 ? bf16_to_f32(b.s) : f16_to_f32(b.s);
+        if constexpr (kBlocksPerGroup == 1u) {
+            v4i d[2];
+            d[0] = mfma_i8_16x16x64(as_v4i(abuf[0]), bw, zero);
+#pragma unroll
+            for (uint32_t t = 0; t < kTiles; ++t) {
+                if (t + 1u < kTiles)
+                    d[(t + 1u) & 1u] = mfma_i8_16x16x64(as_v4i(abuf[(t + 1u) * 64u]), bw, zero);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    y[t][i] = __builtin_fmaf(static_cast<float>(d[t & 1u][i]), scale, y[t][i]);
+                asm volatile("" : "+v"(y[t][0]), "+v"(y[t][1]), "+v"(y[t][2]), "+v"(y[t][3]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+            const bool first = kb % kBlocksPerGroup == 0u;
+#pragma unroll
+            for (uint32_t t = 0; t < kTiles; ++t)
+                acc[t] = mfma_i8_16x16x64(as_v4i(abuf[t * 64u]), bw, first ? zero : acc[t]);
+            if constexpr (!kPerChannel) {
+                if (kb % kBlocksPerGroup == kBlocksPerGroup - 1u) {
+#pragma unroll
+                    for (uint32_t t = 0; t < kTiles; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            y[t][i] = __builtin_fmaf(static_cast<float>(acc[t][i]), scale, y[t][i]);
+                }
+            }
+        }
+    };
+    // one block: weights two ahead into the set just consumed, A one ahead
+    auto step = [&](uint32_t kb, const Block& cur, Block& refill) {
+        refill = load(kb + 2u);
+        if (kb + 1u < kBlocks) load_a(kb + 1u);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(kb, cur);
+        if (kb + 1u < kBlocks) store_a((kb + 1u) & 1u);
+        __syncthreads();
+    };
+
+    load_a(0);
+    Block r0 = load(0), r1 = load(1), r2;
+    store_a(0);
+    __syncthreads();
+    static_assert(kBlocks % 3u == 2u, "three-set rotation plus two peeled blocks");
+#pragma unroll 1
+    for (uint32_t kb = 0; kb + 2u < kBlocks; kb += 3u) {
+        step(kb, r0, r2);
+        step(kb + 1u, r1, r0);
+        step(kb + 2u, r2, r1);
+    }
+    step(kBlocks - 2u, r0, r2);
+    multiply(kBlocks - 1u, r1);
+    if constexpr (kPerChannel) {
+        const float scale = kBf16 ? bf16_to_f32(r1.s) : f16_to_f32(r1.s);
+#pragma unroll
+        for (uint32_t t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[t][i] = static_cast<float>(acc[t][i]) * scale;
+    }
+
+    // gate waves hand y over: gate_lds[pair in workgroup][row][channel],
+    // over the A image, once every wave has finished reading it
+    float* handoff = gate_lds + wave_in_half * (kWideRows * 16u);
+    __syncthreads();
+    if (!up) {
+#pragma unroll
+        for (uint32_t t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) handoff[(16u * t + 4u * q + i) * 16u + n] = y[t][i];
+    }
+    __syncthreads();
+    if (!up) return;
+    const uint32_t channel = pair * 16u + n;
+#pragma unroll
+    for (uint32_t t = 0; t < kTiles; ++t) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 16u * t + 4u * q + i;
+            if (r >= rows) continue;
+            const uint32_t p = p0 + r;
+            const uint32_t a = packed[p];
+            const float st = xs[a / kTopK];
+            mid[static_cast<size_t>(p) * I + channel] = static_cast<uint16_t>(
+                swiglu_fold(handoff[r * 16u + n] * st, y[t][i] * st, route_weights[a]));
+        }
+    }
+}
+
+template <uint32_t H, uint32_t I, uint32_t kPairs, uint32_t kBlocksPerGroup, bool kBf16>
+__global__ __launch_bounds__(kPairs * 128) __attribute__((amdgpu_waves_per_eu(4)))
+void gate_up_w8_wide_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
+    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    constexpr uint32_t kBlocks = H / 64u;
+    constexpr uint32_t kSlots = 2u * I / 16u;
+    constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
+    constexpr uint32_t kThreads = kPairs * 128u;
+    // the A image (two blocks) and, after the K loop, the gate hand-off
+    constexpr uint32_t kABytes = 2u * kRowTiles * 64u * 16u;
+    constexpr uint32_t kHandoffBytes = kPairs * kWideRows * 16u * 4u;
+    __shared__ __align__(16) uint8_t lds[kABytes > kHandoffBytes ? kABytes : kHandoffBytes];
+    auto a_lds = reinterpret_cast<uint4 (*)[kRowTiles * 64u]>(lds);
+    float* gate_lds = reinterpret_cast<float*>(lds);
+
+    const q38m_task_v1 task = tasks[blockIdx.y];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool up = wave >= kPairs;
+    const uint32_t pair = blockIdx.x * kPairs + (wave % kPairs);
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+    const uint32_t n = threadIdx.x & 15u;
+    // paired K-block-major layout: for block kb the gate tile of pair p is
+    // slot 2p and its up tile slot 2p+1
+    const uint32_t slot = 2u * pair + (up ? 1u : 0u);
+    const uint4* wbase = w + (static_cast<size_t>(e) * kBlocks * kSlots + slot) * 64u;
+    const uint16_t* srow =
+        s + (static_cast<size_t>(e) * 2u * I + (up ? I : 0u) + pair * 16u + n) * kGroups;
+    const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
+    auto run = [&](auto row_tiles) {
+        gate_up_w8_wide_rows<H, I, kThreads, decltype(row_tiles)::value, kBlocksPerGroup, kBf16>(
+            wbase, srow, xq, xs, packed, route_weights, mid, a_lds, gate_lds, rows, p0, pair, up);
+    };
+    if (tiles > 4u)
+        run(std::integral_constant<uint32_t, 8>{});
+    else if (tiles > 2u)
+        run(std::integral_constant<uint32_t, 4>{});
+    else if (tiles == 2u)
+        run(std::integral_constant<uint32_t, 2>{});
+    else
+        run(std::integral_constant<uint32_t, 1>{});
+}
+
 // ---- down -------------------------------------------------------------------
 
 // Down, W8 per output channel, over a task of up to 128 rows: the mid rows
@@ -872,12 +1089,41 @@ void launch_down_w4_wide_sub(const q38m_expert_weights_v1& w, const int8_t* mid_
                                             tasks, route_output);
 }
 
+template <uint32_t kBlocksPerGroup, bool kBf16>
+void launch_gate_up_w8_wide_groups(const q38m_expert_weights_v1& w, const int8_t* xq,
+                                   const float* xs, const uint32_t* packed,
+                                   const float* route_weights, const q38m_task_v1* tasks,
+                                   uint32_t task_count, uint16_t* weighted_mid,
+                                   hipStream_t stream) {
+    constexpr uint32_t kPairs = 8;
+    const dim3 grid(kInter / 16u / kPairs, task_count);
+    gate_up_w8_wide_kernel<kHidden, kInter, kPairs, kBlocksPerGroup, kBf16>
+        <<<grid, kPairs * 128u, 0, stream>>>(static_cast<const uint4*>(w.data),
+                                             static_cast<const uint16_t*>(w.scales), xq, xs,
+                                             packed, route_weights, tasks, weighted_mid);
+}
+
 template <bool kBf16>
 hipError_t launch_gate_up_wide_dtype(const q38m_expert_weights_v1& w, const int8_t* xq,
                                      const float* xs, const uint32_t* packed,
                                      const float* route_weights, const q38m_task_v1* tasks,
                                      uint32_t task_count, uint16_t* weighted_mid,
                                      hipStream_t stream) {
+    if (w.format == Q38M_FORMAT_W8_SYM) {
+        switch (w.group_size) {
+            case 0u: launch_gate_up_w8_wide_groups<kHidden / 64u, kBf16>(
+                         w, xq, xs, packed, route_weights, tasks, task_count, weighted_mid,
+                         stream); break;
+            case 64u: launch_gate_up_w8_wide_groups<1, kBf16>(w, xq, xs, packed, route_weights,
+                                                              tasks, task_count, weighted_mid,
+                                                              stream); break;
+            case 128u: launch_gate_up_w8_wide_groups<2, kBf16>(w, xq, xs, packed, route_weights,
+                                                               tasks, task_count, weighted_mid,
+                                                               stream); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (w.group_size) {
         case 32u: launch_gate_up_wide_sub<1, kBf16>(w, xq, xs, packed, route_weights, tasks,
                                                     task_count, weighted_mid, stream); break;

@@ -331,10 +331,10 @@ def test_repack_and_synth_validation(q38m):
     with pytest.raises(q38m.InvalidArgument):  # the scale dtype is kept
         q38m.call("q38m_repack_expert_weights", ctypes.byref(src),
                   ctypes.byref(fake_weights(q38m, layout=3, scale_dtype=2)), None, 0)
-    w8_src = fake_weights(q38m, fmt=3, group=0, layout=0, rows=2048, cols=512)
-    with pytest.raises(q38m.Unsupported):  # the paired layout is W4-only
+    w8_src = fake_weights(q38m, fmt=3, group=0, layout=0, rows=2064, cols=512)
+    with pytest.raises(q38m.Unsupported):  # pairing needs an even number of row tiles
         q38m.call("q38m_repack_expert_weights", ctypes.byref(w8_src),
-                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=3, rows=2048, cols=512)),
+                  ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=3, rows=2064, cols=512)),
                   None, 0)
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_synth_fill", 9, 1, 1, 16, 1.0, 0, 0, None, 0, 0x1000, None, 0)

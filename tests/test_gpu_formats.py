@@ -1,8 +1,8 @@
 """GPU parity of the weight formats beyond the BASELINE pair (W4 g32 fp16
 gate/up with W8 per-channel or W4 g32 fp16 down): W4 in groups of 64 and
-128 columns, W8 down in groups of 64 and 128, and bf16 scale words (the
-reference artifact's scale dtype, tools/q38_artifact_compiler.py:232, with
-groups of 128).  The weight descriptor the reference's validate_expert_tensor
+128 columns, W8 in groups of 64 and 128 or per channel for either
+projection, and bf16 scale words (the reference artifact's scale dtype,
+tools/q38_artifact_compiler.py:232, with groups of 128).  The weight descriptor the reference's validate_expert_tensor
 checks (cuda/q38_moe_prefill.cu:51-62) carries the format; every entry point
 that takes expert weights runs each pair bit-exact against the oracle:
 
@@ -14,10 +14,7 @@ that takes expert weights runs each pair bit-exact against the oracle:
   kernels runs): every token equals the slab step over two 512-token slabs,
   and a sample equals the oracle token by token.
 
-Scale magnitudes are |N(0, sigma)| as in the BASELINE synthesis; the
-arithmetic equals the oracle's for every scale word of magnitude 2^-110 or
-more (and zero), which covers every scale the weight quantiser writes for
-weights above 2^-107.
+Scale magnitudes are |N(0, sigma)| as in the BASELINE synthesis.
 """
 import numpy as np
 import pytest
@@ -36,6 +33,11 @@ FORMATS = {
     "w4g32bf16-w8g64bf16": (((4, 32, 0.02), True), ((8, 64, 0.002), True)),
     "w4g64bf16-w8pcbf16": (((4, 64, 0.02), True), ((8, 0, 0.002), True)),
     "w4g128-w4g32": (((4, 128, 0.02), False), ((4, 32, 0.02), False)),
+    # W8 gate/up: the reference's edge layers (0, 1, 46, 47) and MTP experts
+    # are W8 g128 bf16 in both projections (tools/q38_quant_policy.py:164-190)
+    "w8g128bf16-w8g128bf16": (((8, 128, 0.002), True), ((8, 128, 0.002), True)),
+    "w8pc-w8pc": (((8, 0, 0.002), False), ((8, 0, 0.002), False)),
+    "w8g64-w4g32": (((8, 64, 0.002), False), ((4, 32, 0.02), False)),
 }
 SEED = 9
 

@@ -10,7 +10,10 @@
 - gate/up epilogue: the oracle's weighted_mid against a float64 evaluation
   of y = sum_g acc_g*s_g * s_t followed by the reference's bf16 rounding
   sequence: >= 99% of words exact and every word within 2 bf16 ulps (the
-  fp32 group chain rounds differently from float64 only in the last bits).
+  fp32 group chain rounds differently from float64 only in the last bits),
+  or within 2 ulps of the result with y_gate / y_up moved by 2^-16
+  relative (a y at a bf16 rounding tie may round either way, and silu's
+  tail turns that one-ulp step into a few ulps of a small mid word).
 - down + combine: the oracle's output against a float64 evaluation of the
   whole layer from the oracle's own mid_q (exact int64 accumulators,
   float64 scales and rank-order sum), within 2 bf16 ulps; for the BASELINE
@@ -86,11 +89,12 @@ def test_row_accumulators_brute_force(orc, bits, group, scale_bf16):
 
 
 def small_layer(orc, seed, T, down_bits, gate_group=32, gate_bf16=False, down_group=None,
-                down_bf16=False):
+                down_bf16=False, gate_bits=4):
     H, I = 2048, 512
     if down_group is None:
         down_group = 32 if down_bits == 4 else 0
-    gu = orc.synth_weights(seed, 10, 4, gate_group, 512, 2 * I, H, 0.02, gate_bf16)
+    gu = orc.synth_weights(seed, 10, gate_bits, gate_group, 512, 2 * I, H,
+                           0.02 if gate_bits == 4 else 0.002, gate_bf16)
     dn = orc.synth_weights(seed, 20, down_bits, down_group, 512, H, I,
                            0.02 if down_bits == 4 else 0.002, down_bf16)
     hid = orc.synth_normal_bf16(seed, 1, T * H).reshape(T, H)
@@ -115,16 +119,19 @@ def bf16_close(orc, got_words, want_words, ulps=2, atol=1e-4):
     return np.abs(got - want) <= ulps * ulp + atol
 
 
-# (down bits, gate/up group, gate/up bf16 scales, down group, down bf16 scales)
-LAYER_FORMATS = [(4, 32, False, 32, False), (8, 32, False, 0, False),
-                 (8, 128, True, 128, True), (4, 64, False, 64, True), (8, 64, True, 64, False),
-                 (4, 128, True, 128, False)]
+# (down bits, gate/up group, gate/up bf16 scales, down group, down bf16 scales,
+# gate/up bits)
+LAYER_FORMATS = [(4, 32, False, 32, False, 4), (8, 32, False, 0, False, 4),
+                 (8, 128, True, 128, True, 4), (4, 64, False, 64, True, 4),
+                 (8, 64, True, 64, False, 4), (4, 128, True, 128, False, 4),
+                 (8, 128, True, 128, True, 8), (8, 0, False, 0, False, 8),
+                 (4, 64, False, 32, False, 8)]
 
 
-@pytest.mark.parametrize("down_bits,ggroup,gbf16,dgroup,dbf16", LAYER_FORMATS)
-def test_layer_against_float64(orc, down_bits, ggroup, gbf16, dgroup, dbf16):
+@pytest.mark.parametrize("down_bits,ggroup,gbf16,dgroup,dbf16,gbits", LAYER_FORMATS)
+def test_layer_against_float64(orc, down_bits, ggroup, gbf16, dgroup, dbf16, gbits):
     T = 6
-    gu, dn, hid, lg = small_layer(orc, 31, T, down_bits, ggroup, gbf16, dgroup, dbf16)
+    gu, dn, hid, lg = small_layer(orc, 31, T, down_bits, ggroup, gbf16, dgroup, dbf16, gbits)
     r = orc.moe(hid, gu, dn, logits=lg, intermediates=True)
     p = orc.parse_plan(r["plan"], T)
     xq, xs = r["xq"], r["xs"]
@@ -138,16 +145,29 @@ def test_layer_against_float64(orc, down_bits, ggroup, gbf16, dgroup, dbf16):
         t, e = a // 10, int(r["ids"].ravel()[a])
         W = gu.unpacked(e).astype(np.int64)
         S = decode_scales(gu, e)
-        acc = (W.reshape(2 * I, H // ggroup, ggroup) *
-               xq[t].astype(np.int64).reshape(1, H // ggroup, ggroup)).sum(-1)
+        g = ggroup or H
+        acc = (W.reshape(2 * I, H // g, g) *
+               xq[t].astype(np.int64).reshape(1, H // g, g)).sum(-1)
         y = (acc * S).sum(-1) * float(xs[t])
-        g = orc.bf16_to_f32(orc.f32_to_bf16(y[:I].astype(np.float32))).astype(np.float64)
-        u = orc.bf16_to_f32(orc.f32_to_bf16(y[I:].astype(np.float32))).astype(np.float64)
-        hval = orc.bf16_to_f32(orc.f32_to_bf16((g / (1 + np.exp(-g)) * u).astype(np.float32)))
-        m = orc.f32_to_bf16((hval.astype(np.float64) * float(r["weights"].ravel()[a])).astype(
-            np.float32))
-        exact += int((m == r["weighted_mid"][pos]).sum())
-        worst = max(worst, int((~bf16_close(orc, r["weighted_mid"][pos], m)).sum()))
+        wr = float(r["weights"].ravel()[a])
+
+        def mid_words(yg, yu):
+            g = orc.bf16_to_f32(orc.f32_to_bf16(yg.astype(np.float32))).astype(np.float64)
+            u = orc.bf16_to_f32(orc.f32_to_bf16(yu.astype(np.float32))).astype(np.float64)
+            hval = orc.bf16_to_f32(orc.f32_to_bf16((g / (1 + np.exp(-g)) * u).astype(np.float32)))
+            return orc.f32_to_bf16((hval.astype(np.float64) * wr).astype(np.float32))
+
+        m = mid_words(y[:I], y[I:])
+        got = r["weighted_mid"][pos]
+        exact += int((m == got).sum())
+        ok = bf16_close(orc, got, m)
+        # a y within the fp32 chain's error (relative 2^-16 is far above it)
+        # of a bf16 rounding tie may round either way; silu near its tail
+        # then moves a small mid word by several ulps -- accept either side
+        for yg_side in (1.0 - 2.0 ** -16, 1.0 + 2.0 ** -16):
+            for yu_side in (1.0 - 2.0 ** -16, 1.0 + 2.0 ** -16):
+                ok |= bf16_close(orc, got, mid_words(y[:I] * yg_side, y[I:] * yu_side))
+        worst = max(worst, int((~ok).sum()))
     assert worst == 0
     assert exact >= 0.99 * T * 10 * I
     # down + combine in float64 from the oracle's own quantised mid rows
