@@ -180,8 +180,8 @@ def main():
     down_bytes = (active * dn_bytes_expert + routes * W.INTER + routes * 4 +
                   routes * W.HIDDEN * 4)
     kernels = {
-        "gate_up": (stage_ms[stage_names.index("gate_up")], gate_up_bytes, "gate_up_w4g32_kernel"),
-        "down": (stage_ms[stage_names.index("down")], down_bytes, "down_w8pc_kernel"),
+        "gate_up": (stage_ms[stage_names.index("gate_up")], gate_up_bytes, "gate_up_w4_kernel"),
+        "down": (stage_ms[stage_names.index("down")], down_bytes, "down_w8_kernel"),
     }
     dominant = max(kernels, key=lambda k: kernels[k][0])
     d_ms, d_bytes, d_symbol = kernels[dominant]
