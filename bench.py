@@ -59,6 +59,7 @@ def main():
     parser.add_argument("--no-dense", action="store_true")
     parser.add_argument("--no-chunks", action="store_true")
     parser.add_argument("--no-hyper", action="store_true")
+    parser.add_argument("--no-formats", action="store_true")
     parser.add_argument("--no-stack", action="store_true",
                         help="skip the full 48-layer config-5 stack")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -259,6 +260,9 @@ def main():
     if not args.no_hyper:
         result["hyper"] = bench_hyper(q38m, torch, T, args.steps)
 
+    if not args.no_formats:
+        result["reference_formats"] = bench_reference_formats(q38m, W, torch, args.steps)
+
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
                                               T)
@@ -347,6 +351,121 @@ def bench_decode(q38m, W, torch, tokens):
             "algorithmic_bytes_per_token": bytes_token, "launches_per_layer": 2,
             "entry_point": "q38m_moe_decode_v1", **graph_rate, "mode": "hip_graph",
             "eager": rate(ms_eager)}
+
+
+# The reference artifact's routed-expert formats (tools/q38_quant_policy.py:
+# 164-190): groups of 128 with bf16 scale words; W4 in the interior layers,
+# W8 in both projections of layers 0, 1, 46, 47 and the MTP head.
+REFERENCE_FORMATS = {
+    "interior: W4 g128 bf16 gate/up + down": (("w4", 4, 128, 0.02), ("w4", 4, 128, 0.02)),
+    "edge: W8 g128 bf16 gate/up + down": (("w8", 8, 128, 0.002), ("w8", 8, 128, 0.002)),
+}
+
+
+def bench_reference_formats(q38m, W, torch, steps, layers=8, tokens=8):
+    """The reference artifact's own formats through the same entry points:
+    the config-2 slab step (512 tokens, q38m_moe_prefill_v1, K calls by wall
+    clock) and batch-1 decode (q38m_moe_decode_v1, fresh router draw per
+    layer, residual add) through a stack of `layers` layers of distinct
+    weights captured in one HIP graph.  Bytes: active experts' packed weights
+    and scales (+ hidden in/out and logits for the slab)."""
+    spec = W.CONFIGS[2]
+    seed, T = spec["seed"], spec["tokens"]
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    sh = torch.cuda.current_stream().cuda_stream
+    results = {}
+    for name, (gfmt, dfmt) in REFERENCE_FORMATS.items():
+        stack = []
+        for layer in range(layers):
+            gu_tag, dn_tag, _, _ = W.layer_tags(layer)
+            gu_rm = q38m.synth_weights(seed, gu_tag, fmt[gfmt[1]], gfmt[2], W.EXPERTS,
+                                       2 * W.INTER, W.HIDDEN, gfmt[3],
+                                       scale_dtype=q38m.SCALE_BF16)
+            gu = q38m.repack(gu_rm, paired=True)
+            del gu_rm
+            dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dfmt[1]], dfmt[2], W.EXPERTS, W.HIDDEN,
+                                       W.INTER, dfmt[3], scale_dtype=q38m.SCALE_BF16)
+            dn = q38m.repack(dn_rm)
+            del dn_rm
+            stack.append((gu, dn))
+        expert_bytes = W.algorithmic_bytes_per_expert(gfmt, dfmt)
+
+        # slab step on layer 0
+        _, _, h_tag, l_tag = W.layer_tags(0)
+        hidden = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
+        logits = torch.empty(T, W.EXPERTS, dtype=torch.float32, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, h_tag, hidden.numel(), hidden)
+        q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, l_tag, logits.numel(), logits)
+        wsb = q38m.PrefillWorkspace_(T)
+        out = torch.empty(T, W.HIDDEN, dtype=torch.int16, device="cuda")
+        gu, dn = stack[0]
+
+        def step():
+            q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                      hidden.data_ptr(), logits.data_ptr(), T, ctypes.byref(wsb.ws), None, None,
+                      out.data_ptr(), sh, 0)
+
+        for _ in range(5):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        base = wsb.buffer.data_ptr()
+        routes = T * W.TOPK
+        ids = wsb.buffer[wsb.ws.expert_ids - base:wsb.ws.expert_ids - base + 4 * routes]
+        active = int(torch.bincount(ids.view(torch.int32).long(), minlength=W.EXPERTS).gt(0).sum())
+        slab_bytes = active * expert_bytes + T * W.HIDDEN * 2 * 2 + T * W.EXPERTS * 4
+        slab_gbps = slab_bytes / (ms * 1e-3) / 1e9
+
+        # decode through the stack, one graph over `tokens` tokens
+        dlogits = torch.empty(tokens, layers, W.EXPERTS, dtype=torch.float32, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, 12, dlogits.numel(), dlogits)
+        state = torch.empty(layers + 1, W.HIDDEN, dtype=torch.int16, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, 11, W.HIDDEN, state[0])
+        scratch = torch.zeros(q38m.lib().q38m_moe_decode_scratch_bytes(), dtype=torch.uint8,
+                              device="cuda")
+
+        def token(t):
+            s = torch.cuda.current_stream().cuda_stream
+            for layer, (lgu, ldn) in enumerate(stack):
+                q38m.call("q38m_moe_decode_v1", ctypes.byref(lgu.desc), ctypes.byref(ldn.desc),
+                          state[layer].data_ptr(), dlogits[t, layer].data_ptr(), W.TOPK, None,
+                          None, state[layer].data_ptr(), scratch.data_ptr(),
+                          state[layer + 1].data_ptr(), s, 0)
+
+        token(0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for t in range(tokens):
+                token(t)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        replays = 4
+        start.record()
+        for _ in range(replays):
+            graph.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        us_layer = start.elapsed_time(stop) * 1e3 / (replays * tokens * layers)
+        dec_gbps = W.TOPK * expert_bytes / (us_layer * 1e-6) / 1e9
+        results[name] = {
+            "expert_bytes": expert_bytes,
+            "slab": {"tokens": T, "active_experts": active, "ms_per_step": round(ms, 4),
+                     "tok_s": round(T / ms * 1e3, 1), "GBps": round(slab_gbps, 1),
+                     "hbm_frac": round(slab_gbps / HBM_PEAK_GBPS, 4)},
+            "decode": {"layers": layers, "tokens": tokens, "us_per_layer": round(us_layer, 3),
+                       "GBps": round(dec_gbps, 1),
+                       "hbm_frac": round(dec_gbps / HBM_PEAK_GBPS, 4)},
+        }
+        del stack, graph
+        torch.cuda.empty_cache()
+    return results
 
 
 def bench_config1(q38m, W, torch, steps):
