@@ -119,3 +119,18 @@ def test_format_chunk_step_bitwise(q38m, orc, format_layer, name):
     # hot experts span several 128-row tasks
     ids = ws_arrays(wsw, tokens)["ids"].ravel()
     assert np.bincount(ids, minlength=W.EXPERTS).max() > 2 * 128
+
+
+@pytest.mark.parametrize("tokens", [1, 77, 600])
+def test_edge_format_ragged_chunks(q38m, orc, format_layer, tokens):
+    """The reference's edge-layer format (W8 g128 bf16 in both projections)
+    through the chunk step at ragged sizes (one token, a partial first task,
+    more than one slab), against the oracle token by token."""
+    layer = format_layer("w8g128bf16-w8g128bf16")
+    hidden = synth_hidden(q38m, SEED, 51, tokens)
+    logits = synth_logits(q38m, SEED, 52, tokens, W.bias_for(4, 0))
+    out = prefill_wide(q38m, layer, hidden, logits, q38m.WideWorkspace_(tokens))
+    sample = np.arange(tokens) if tokens <= 100 else np.arange(0, tokens, 9)
+    ref = orc.moe(host(hidden, np.uint16)[sample], layer.host_gu, layer.host_dn,
+                  logits=host(logits, np.float32)[sample], grouped=False)
+    assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
