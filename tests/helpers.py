@@ -99,6 +99,45 @@ def prefill(q38m, layer, hidden, logits, ws, output=None, shared=None):
     return output
 
 
+def staged_step(q38m, layer, hidden, logits):
+    """The reference's staged call sequence (run_moe, cuda_backend.cu:
+    1516-1605) through the single-purpose entry points: top-k, route plan,
+    token quantisation, grouped gate/up, mid quantisation, grouped down and
+    the rank-order combine.  Returns the bf16 output."""
+    t = torch()
+    T = hidden.shape[0]
+    R = T * W.TOPK
+    s = stream()
+    ids = t.empty(R, dtype=t.int32, device="cuda")
+    wts = t.empty(R, dtype=t.float32, device="cuda")
+    q38m.call("q38m_topk_router_f32", logits.data_ptr(), ids.data_ptr(), wts.data_ptr(), T,
+              W.EXPERTS, W.TOPK, 1, s, 0)
+    nbytes = q38m.route_plan_bytes(T)
+    buf = t.empty(nbytes + 256, dtype=t.uint8, device="cuda")
+    plan = q38m.bind_plan((buf.data_ptr() + 255) // 256 * 256, nbytes, T)
+    q38m.call("q38m_moe_build_route_plan_v1", ids.data_ptr(), T, ctypes.byref(plan), 0, s, 0)
+    xq = t.empty(T, W.HIDDEN, dtype=t.int8, device="cuda")
+    xs = t.empty(T, dtype=t.float32, device="cuda")
+    q38m.call("q38m_quantize_rows_i8", hidden.data_ptr(), T, W.HIDDEN, xq.data_ptr(),
+              xs.data_ptr(), s, 0)
+    tasks = q38m.max_tasks(T)
+    mid = t.empty(R, W.INTER, dtype=t.int16, device="cuda")
+    q38m.call("q38m_moe_grouped_gate_up_v1", ctypes.byref(layer.gu.desc), xq.data_ptr(),
+              xs.data_ptr(), plan.packed_assignment, wts.data_ptr(), plan.tasks, tasks,
+              mid.data_ptr(), s, 0)
+    mq = t.empty(R, W.INTER, dtype=t.int8, device="cuda")
+    ms = t.empty(R, dtype=t.float32, device="cuda")
+    q38m.call("q38m_quantize_rows_i8", mid.data_ptr(), R, W.INTER, mq.data_ptr(), ms.data_ptr(),
+              s, 0)
+    route_output = t.empty(R, W.HIDDEN, dtype=t.float32, device="cuda")
+    q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(layer.dn.desc), mq.data_ptr(),
+              ms.data_ptr(), plan.tasks, tasks, route_output.data_ptr(), s, 0)
+    out = t.empty(T, W.HIDDEN, dtype=t.int16, device="cuda")
+    q38m.call("q38m_moe_reduce_top10_and_combine_shared_v1", route_output.data_ptr(),
+              plan.assignment_to_packed, None, None, T, out.data_ptr(), s, 0)
+    return out
+
+
 def decode(q38m, layer, hidden, ids, weights, scratch, output=None, top_k=10):
     t = torch()
     if output is None:

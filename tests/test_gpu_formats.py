@@ -19,8 +19,8 @@ Scale magnitudes are |N(0, sigma)| as in the BASELINE synthesis.
 import numpy as np
 import pytest
 
-from helpers import (Layer, W, decode_fused, decode_scratch, host, prefill, synth_hidden,
-                     synth_logits, torch, ws_arrays)
+from helpers import (Layer, W, decode_fused, decode_scratch, host, prefill, staged_step,
+                     synth_hidden, synth_logits, torch, ws_arrays)
 from test_gpu_wide import prefill_wide
 
 pytestmark = pytest.mark.gpu
@@ -134,3 +134,15 @@ def test_edge_format_ragged_chunks(q38m, orc, format_layer, tokens):
     ref = orc.moe(host(hidden, np.uint16)[sample], layer.host_gu, layer.host_dn,
                   logits=host(logits, np.float32)[sample], grouped=False)
     assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
+
+
+@pytest.mark.parametrize("name", ["w8g128bf16-w8g128bf16", "w4g128-w4g128bf16"])
+def test_format_staged_call_sequence(q38m, orc, format_layer, name):
+    """The staged entry points (grouped gate/up, grouped down) take the
+    descriptor's format too: the staged sequence equals the fused step."""
+    layer = format_layer(name)
+    hidden = synth_hidden(q38m, SEED, 61, 100)
+    logits = synth_logits(q38m, SEED, 62, 100)
+    fused = prefill(q38m, layer, hidden, logits, q38m.PrefillWorkspace_(100))
+    staged = staged_step(q38m, layer, hidden, logits)
+    assert np.array_equal(host(staged, np.uint16), host(fused, np.uint16))

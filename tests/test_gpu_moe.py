@@ -24,7 +24,8 @@ import pytest
 
 from conftest import GOLDEN_DIR
 from helpers import (Layer, W, decode, decode_fused, decode_scratch, device, host, prefill,
-                     scratch_ids, stream, synth_hidden, synth_logits, torch, ws_arrays)
+                     scratch_ids, staged_step, stream, synth_hidden, synth_logits, torch,
+                     ws_arrays)
 
 pytestmark = pytest.mark.gpu
 
@@ -88,6 +89,20 @@ def test_full_config_step_bitwise(q38m, orc, layers, config):
     assert np.array_equal(gpu_out, ref["output"])
     assert_baseline_tolerance(orc, gpu_out, ref["output"])
     assert orc.bf16_to_f32(gpu_out).std() > 1.0
+
+
+@pytest.mark.parametrize("config", [1, 2])
+def test_staged_call_sequence(q38m, orc, layers, config):
+    """The reference's staged sequence through the single-purpose entry
+    points equals the fused step and the oracle bit for bit."""
+    tokens = W.CONFIGS[config]["tokens"]
+    layer = layers(config)
+    hidden, logits, ws, fused = run_config_layer(q38m, orc, layer, config, tokens)
+    staged = host(staged_step(q38m, layer, hidden, logits), np.uint16)
+    assert np.array_equal(staged, host(fused, np.uint16))
+    ref = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn,
+                  logits=host(logits, np.float32))
+    assert np.array_equal(staged, ref["output"])
 
 
 def test_config1_golden_slice(q38m, orc, layers):
