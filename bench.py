@@ -420,6 +420,32 @@ def bench_reference_formats(q38m, W, torch, steps, layers=8, tokens=8):
         slab_bytes = active * expert_bytes + T * W.HIDDEN * 2 * 2 + T * W.EXPERTS * 4
         slab_gbps = slab_bytes / (ms * 1e-3) / 1e9
 
+        # the chunk step (q38m_moe_prefill_wide_v1) over config 4's 4096
+        # Zipf-routed tokens
+        CT = W.CONFIGS[4]["tokens"]
+        c_hidden = torch.empty(CT, W.HIDDEN, dtype=torch.int16, device="cuda")
+        c_logits = torch.empty(CT, W.EXPERTS, dtype=torch.float32, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, 21, c_hidden.numel(), c_hidden)
+        bias_t = torch.tensor(W.bias_for(4, 0), dtype=torch.float32, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, 22, c_logits.numel(), c_logits, bias=bias_t)
+        wsw = q38m.WideWorkspace_(CT)
+        c_out = torch.empty(CT, W.HIDDEN, dtype=torch.int16, device="cuda")
+
+        def chunk():
+            q38m.call("q38m_moe_prefill_wide_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                      c_hidden.data_ptr(), c_logits.data_ptr(), CT, ctypes.byref(wsw.wide), None,
+                      None, c_out.data_ptr(), sh, 0)
+
+        for _ in range(3):
+            chunk()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(20):
+            chunk()
+        torch.cuda.synchronize()
+        chunk_ms = (time.perf_counter() - t0) * 1e3 / 20
+        del wsw
+
         # decode through the stack, one graph over `tokens` tokens
         dlogits = torch.empty(tokens, layers, W.EXPERTS, dtype=torch.float32, device="cuda")
         q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, 12, dlogits.numel(), dlogits)
@@ -459,6 +485,9 @@ def bench_reference_formats(q38m, W, torch, steps, layers=8, tokens=8):
             "slab": {"tokens": T, "active_experts": active, "ms_per_step": round(ms, 4),
                      "tok_s": round(T / ms * 1e3, 1), "GBps": round(slab_gbps, 1),
                      "hbm_frac": round(slab_gbps / HBM_PEAK_GBPS, 4)},
+            "chunk": {"tokens": CT, "routing": "config 4 (Zipf s=1.1)",
+                      "ms_per_step": round(chunk_ms, 4),
+                      "tok_s": round(CT / chunk_ms * 1e3, 1)},
             "decode": {"layers": layers, "tokens": tokens, "us_per_layer": round(us_layer, 3),
                        "GBps": round(dec_gbps, 1),
                        "hbm_frac": round(dec_gbps / HBM_PEAK_GBPS, 4)},
