@@ -111,13 +111,13 @@ def main():
         elif i == 2:
             q38m.call("q38m_moe_grouped_gate_up_v1", ctypes.byref(gu.desc), ws.xq, ws.xs,
                       ws.plan.packed_assignment, ws.expert_weights, ws.plan.tasks, max_tasks,
-                      ws.weighted_mid, sh, 0)
+                      ws.weighted_mid, q38m.MODE_GROUPED_MMQ, sh, 0)
         elif i == 3:
             q38m.call("q38m_quantize_rows_i8", ws.weighted_mid, routes, W.INTER, ws.mid_q,
                       ws.mid_s, sh, 0)
         elif i == 4:
             q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(dn.desc), ws.mid_q, ws.mid_s,
-                      ws.plan.tasks, max_tasks, ws.route_output, sh, 0)
+                      ws.plan.tasks, max_tasks, ws.route_output, q38m.MODE_GROUPED_MMQ, sh, 0)
         else:
             q38m.call("q38m_moe_reduce_top10_and_combine_shared_v1", ws.route_output,
                       ws.plan.assignment_to_packed, None, None, T, out.data_ptr(), sh, 0)
@@ -261,7 +261,8 @@ def main():
         result["hyper"] = bench_hyper(q38m, torch, T, args.steps)
 
     if not args.no_formats:
-        result["reference_formats"] = bench_reference_formats(q38m, W, torch, args.steps)
+        result["reference_formats_at_baseline_dims"] = bench_reference_formats(
+            q38m, W, torch, args.steps)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
@@ -353,9 +354,12 @@ def bench_decode(q38m, W, torch, tokens):
             "eager": rate(ms_eager)}
 
 
-# The reference artifact's routed-expert formats (tools/q38_quant_policy.py:
-# 164-190): groups of 128 with bf16 scale words; W4 in the interior layers,
-# W8 in both projections of layers 0, 1, 46, 47 and the MTP head.
+# The reference artifact's routed-expert number formats (tools/
+# q38_quant_policy.py:164-190): groups of 128 with bf16 scale words; W4 in
+# the interior layers, W8 in both projections of layers 0, 1, 46, 47 and the
+# MTP head.  They run here at the BASELINE dimensions (hidden 2048,
+# intermediate 512); the reference model's own tensors ([512][1280][2560],
+# [512][2560][640]) are wider than the kernels are built for.
 REFERENCE_FORMATS = {
     "interior: W4 g128 bf16 gate/up + down": (("w4", 4, 128, 0.02), ("w4", 4, 128, 0.02)),
     "edge: W8 g128 bf16 gate/up + down": (("w8", 8, 128, 0.002), ("w8", 8, 128, 0.002)),
@@ -363,7 +367,8 @@ REFERENCE_FORMATS = {
 
 
 def bench_reference_formats(q38m, W, torch, steps, layers=8, tokens=8):
-    """The reference artifact's own formats through the same entry points:
+    """The reference artifact's formats, at the BASELINE dimensions, through
+    the same entry points:
     the config-2 slab step (512 tokens, q38m_moe_prefill_v1, K calls by wall
     clock) and batch-1 decode (q38m_moe_decode_v1, fresh router draw per
     layer, residual add) through a stack of `layers` layers of distinct
@@ -570,12 +575,12 @@ def bench_router_shared(q38m, W, torch, hidden, steps):
     sg = torch.empty(T, dtype=torch.int16, device="cuda")
 
     def run_router():
-        q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), T,
+        q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), T, W.HIDDEN,
                   logits.data_ptr(), sh, 0)
 
     def run_shared():
         q38m.call("q38m_moe_shared_expert_v1", hidden.data_ptr(), wg.data_ptr(), wu.data_ptr(),
-                  wd.data_ptr(), wo.data_ptr(), T, I, scratch.data_ptr(), so.data_ptr(),
+                  wd.data_ptr(), wo.data_ptr(), T, W.HIDDEN, I, scratch.data_ptr(), so.data_ptr(),
                   sg.data_ptr(), sh, 0)
 
     def timed(fn):
@@ -611,8 +616,8 @@ def bench_router_shared(q38m, W, torch, hidden, steps):
 def bench_hyper(q38m, torch, T, steps, low_rank=320):
     """Hyper-connection prepare (group RMSNorm + inject dots, the two
     low-rank GEMMs with SiLU / sigmoid epilogues, the stream mix) and finish
-    (inject) on a T-token slab, at this layer's hidden 2048 and the
-    reference model's 2560.  Algorithmic bytes: every operand read once and
+    (inject) on a T-token slab at the MoE's hidden width 2048 (the width
+    of the mixed rows the MoE entry points take).  Algorithmic bytes: every operand read once and
     every result written once, intermediates included (prepare: the 4-stream
     state in, normalized out and in twice, mix out and in, low out and in,
     mixed and injection out, the three weight matrices; inject: state and
@@ -625,7 +630,7 @@ def bench_hyper(q38m, torch, T, steps, low_rank=320):
         return x.view(torch.int16)
 
     out = {"tokens": T, "low_rank": low_rank}
-    for H in (2048, 2560):
+    for H in (2048,):
         width = 4 * H
         state = bf16(T, width)
         norm_w, down = bf16(width, scale=0.1), bf16(low_rank, width, scale=0.03)

@@ -65,6 +65,15 @@ extern "C" {
 #define Q38M_PLAN_INVALID_EXPERT 1u
 #define Q38M_PLAN_INVALID_SHAPE 2u
 
+/* Q38PrefillMoeModeV1, include/q38/cuda_moe_prefill.h:67-71.  The grouped
+ * gate/up and down entry points take the mode argument of the reference and
+ * accept the two grouped modes (identical kernels; "safe" is only the
+ * validation label, cuda/q38_moe_prefill.cu:64-68); the legacy atomic
+ * diagnostic is not built and is rejected as an invalid argument. */
+#define Q38M_MOE_MODE_GROUPED_MMQ 1u
+#define Q38M_MOE_MODE_GROUPED_MMQ_SAFE 2u
+#define Q38M_MOE_MODE_LEGACY_ATOMIC_DIAGNOSTIC 3u
+
 /* q38m_moe_build_route_plan_v1 flags */
 #define Q38M_PLAN_FLAG_HASHES 1u /* also compute the FNV-1a route/plan hashes */
 
@@ -224,22 +233,24 @@ int q38m_residual_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* out,
 /* cuda_moe_grouped_gate_up_v1, include/q38/cuda_moe_prefill.h:112-118.
  * Reads int8 token rows xq[T][H] (scales xs[T]) through packed_assignment
  * instead of a packed bf16 copy; writes weighted_mid bf16 [routes][I] in
- * packed order: m = bf16(bf16(silu(g)*u) * w).  gate_up: W4 g32 MFMA16. */
+ * packed order: m = bf16(bf16(silu(g)*u) * w).  gate_up: MFMA16_PAIRED.
+ * mode: Q38M_MOE_MODE_GROUPED_MMQ or _SAFE (validate_grouped_mode). */
 int q38m_moe_grouped_gate_up_v1(const q38m_expert_weights_v1* gate_up,
                                 const int8_t* xq, const float* xs,
                                 const uint32_t* packed_assignment,
                                 const float* token_rank_weights,
                                 const q38m_task_v1* tasks, uint32_t task_count,
-                                uint16_t* weighted_mid, void* stream, int device);
+                                uint16_t* weighted_mid, uint32_t mode, void* stream,
+                                int device);
 
 /* cuda_moe_grouped_down_v1, include/q38/cuda_moe_prefill.h:120-125.
  * Input: the int8 quantised weighted_mid rows (q38m_quantize_rows_i8).
- * Output: route_output fp32 [routes][H] in packed order.  down: W8
- * per-channel or W4 g32, MFMA16 layout. */
+ * Output: route_output fp32 [routes][H] in packed order.  down: MFMA16.
+ * mode as for gate/up. */
 int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down,
                              const int8_t* mid_q, const float* mid_scales,
                              const q38m_task_v1* tasks, uint32_t task_count,
-                             float* route_output, void* stream, int device);
+                             float* route_output, uint32_t mode, void* stream, int device);
 
 /* cuda_moe_reduce_top10_and_combine_shared_v1,
  * include/q38/cuda_moe_prefill.h:127-131.  shared_output/shared_gate may
@@ -415,14 +426,17 @@ int q38m_dense_gemm_bf16(const uint16_t* a, const uint16_t* b, uint32_t m,
                          uint32_t n, uint32_t k, float* c_f32,
                          uint16_t* c_bf16, void* stream, int device);
 
-/* Router logits: hidden bf16 [T][2048] times the bf16 router [512][2048]
- * (the "preserved" router format, tools/q38_quant_policy.py:205) -> fp32
- * logits [T][512], the input of q38m_moe_route_quantize_v1 /
- * q38m_moe_prefill_v1 / q38m_moe_decode_v1.  Replaces the router GEMV/GEMM
- * of run_moe (cuda/cuda_backend.cu:1518-1519; the reference rounds the
- * logits to bf16). */
+/* Router logits: hidden bf16 [T][hidden_width] times the bf16 router
+ * [512][hidden_width] (the "preserved" router format,
+ * tools/q38_quant_policy.py:205) -> fp32 logits [T][512], the input of
+ * q38m_moe_route_quantize_v1 / q38m_moe_prefill_v1 / q38m_moe_decode_v1.
+ * Replaces the router GEMV/GEMM of run_moe (cuda/cuda_backend.cu:1518-1519;
+ * the reference rounds the logits to bf16).  hidden_width must be the
+ * MoE's Q38M_HIDDEN (2048): any other width is rejected, so a caller
+ * cannot feed it rows of another stride. */
 int q38m_moe_router_v1(const uint16_t* hidden, const uint16_t* router,
-                       uint32_t tokens, float* logits, void* stream, int device);
+                       uint32_t tokens, uint32_t hidden_width, float* logits,
+                       void* stream, int device);
 
 /* Shared expert of the MoE block (cuda/cuda_backend.cu:1573-1590), bf16
  * weights: g = bf16(x Wg^T), u = bf16(x Wu^T) [T][inter],
@@ -431,12 +445,13 @@ int q38m_moe_router_v1(const uint16_t* hidden, const uint16_t* router,
  * shared_gate = bf16(x Wo^T) [T] -- the two inputs of the gated combine
  * (q38m_moe_prefill_v1 / q38m_moe_decode_v1 / combine entry points).
  * Wg, Wu [inter][2048]; Wd [2048][inter]; Wo [1][2048]; inter % 32 == 0.
+ * hidden_width must be Q38M_HIDDEN (2048), as for the router.
  * scratch: q38m_moe_shared_expert_scratch_bytes(T, inter) bytes. */
 size_t q38m_moe_shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter);
 int q38m_moe_shared_expert_v1(const uint16_t* hidden, const uint16_t* w_gate,
                               const uint16_t* w_up, const uint16_t* w_down,
                               const uint16_t* w_out_gate, uint32_t tokens,
-                              uint32_t inter, void* scratch,
+                              uint32_t hidden_width, uint32_t inter, void* scratch,
                               uint16_t* shared_output, uint16_t* shared_gate,
                               void* stream, int device);
 
@@ -465,16 +480,6 @@ int q38m_synth_fill(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count,
 /* cuda_q38_moe_prefill_compiled / cuda_q38_moe_compiled */
 int q38m_moe_compiled(void);
 const char* q38m_last_error(void);
-
-/* Kernel-level self checks used by the tests: the contract's exp and the
- * int8 MFMA lane layouts (one 16x16x32 or 32x32x32 product, A and B
- * row-major). */
-int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream,
-                    int device);
-int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d,
-                                void* stream, int device);
-int q38m_debug_mfma_32x32x32_i8(const int8_t* a, const int8_t* b, int32_t* d,
-                                void* stream, int device);
 
 #ifdef __cplusplus
 }

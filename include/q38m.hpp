@@ -2,9 +2,24 @@
 // argument order and error behaviour (include/q38/cuda_moe_prefill.h:98-133,
 // include/q38/cuda_moe.h:17-39, include/q38/cuda_kernels.h:83-91): invalid
 // arguments throw std::invalid_argument, device failures throw
-// std::runtime_error (cuda/q38_moe_prefill.cu:33-68).  A caller of the
-// reference switches by including this header and qualifying calls with
-// q38m:: instead of q38::.
+// std::runtime_error (cuda/q38_moe_prefill.cu:33-68).
+//
+// A caller of the reference switches by including this header and
+// qualifying calls with q38m:: instead of q38::, with these differences
+// (the activation format of this data plane is int8 per token, not bf16):
+//  - cuda_moe_grouped_gate_up_v1 takes the int8 token rows xq[T][2048] and
+//    their scales xs[T] (from q38m_moe_route_quantize_v1 or
+//    quantize_rows_i8) instead of the packed bf16 rows of
+//    cuda_moe_pack_hidden_v1; it gathers the rows through
+//    packed_assignment itself, so the pack step is not needed;
+//  - cuda_moe_grouped_down_v1 takes weighted_mid quantised to int8 rows
+//    (one quantize_rows_i8 call between gate/up and down);
+//  - expert tensors are q38m_expert_weights_v1 descriptors in the MFMA16
+//    device layouts instead of CudaTensorViewV1;
+//  - cuda_moe_routed_bf16 serves tokens == 1 only (the legacy route-wise
+//    atomic path for tokens > 1 is not built);
+//  - both grouped modes are accepted and the legacy atomic mode is
+//    rejected, as validate_grouped_mode does.
 #ifndef Q38M_HPP
 #define Q38M_HPP
 
@@ -22,6 +37,13 @@ using Q38RoutePlanHeaderV1 = q38m_route_plan_header_v1;
 using Q38RoutePlanStorageV1 = q38m_route_plan_v1;
 using ExpertWeightsV1 = q38m_expert_weights_v1;
 using PrefillWorkspaceV1 = q38m_prefill_workspace_v1;
+
+// Q38PrefillMoeModeV1, include/q38/cuda_moe_prefill.h:67-71
+enum class Q38PrefillMoeModeV1 : std::uint32_t {
+    kGroupedMmq = Q38M_MOE_MODE_GROUPED_MMQ,
+    kGroupedMmqSafe = Q38M_MOE_MODE_GROUPED_MMQ_SAFE,
+    kLegacyAtomicDiagnostic = Q38M_MOE_MODE_LEGACY_ATOMIC_DIAGNOSTIC,
+};
 
 static_assert(sizeof(Q38ExpertMmqTaskV1) == 8, "Q38ExpertMmqTaskV1 ABI changed");
 static_assert(sizeof(Q38RoutePlanHeaderV1) == 64, "Q38RoutePlanHeaderV1 ABI changed");
@@ -90,18 +112,20 @@ inline void cuda_moe_grouped_gate_up_v1(const ExpertWeightsV1& gate_up_experts,
                                         const float* token_rank_weights,
                                         const Q38ExpertMmqTaskV1* tasks,
                                         std::uint32_t task_count, std::uint16_t* weighted_mid,
-                                        void* stream, int device) {
+                                        Q38PrefillMoeModeV1 mode, void* stream, int device) {
     check(q38m_moe_grouped_gate_up_v1(&gate_up_experts, xq, xs, packed_assignment,
                                       token_rank_weights, tasks, task_count, weighted_mid,
-                                      stream, device));
+                                      static_cast<std::uint32_t>(mode), stream, device));
 }
 
 inline void cuda_moe_grouped_down_v1(const ExpertWeightsV1& down_experts,
                                      const std::int8_t* mid_q, const float* mid_scales,
                                      const Q38ExpertMmqTaskV1* tasks, std::uint32_t task_count,
-                                     float* route_output, void* stream, int device) {
+                                     float* route_output, Q38PrefillMoeModeV1 mode, void* stream,
+                                     int device) {
     check(q38m_moe_grouped_down_v1(&down_experts, mid_q, mid_scales, tasks, task_count,
-                                   route_output, stream, device));
+                                   route_output, static_cast<std::uint32_t>(mode), stream,
+                                   device));
 }
 
 inline void cuda_moe_reduce_top10_and_combine_shared_v1(
@@ -181,10 +205,12 @@ inline void run_moe_prefill(const ExpertWeightsV1& gate_up, const ExpertWeightsV
                               shared_output, shared_gate, output, stream, device));
 }
 
-// Router logits (cuda_backend.cu:1518-1519): fp32 [tokens][512].
+// Router logits (cuda_backend.cu:1518-1519): fp32 [tokens][512] from
+// hidden rows of hidden_width (must be 2048) values.
 inline void moe_router(const std::uint16_t* hidden, const std::uint16_t* router,
-                       std::uint32_t tokens, float* logits, void* stream, int device) {
-    check(q38m_moe_router_v1(hidden, router, tokens, logits, stream, device));
+                       std::uint32_t tokens, std::uint32_t hidden_width, float* logits,
+                       void* stream, int device) {
+    check(q38m_moe_router_v1(hidden, router, tokens, hidden_width, logits, stream, device));
 }
 
 // Shared expert (cuda_backend.cu:1573-1590): shared_output bf16 [tokens][2048]
@@ -192,10 +218,12 @@ inline void moe_router(const std::uint16_t* hidden, const std::uint16_t* router,
 inline void moe_shared_expert(const std::uint16_t* hidden, const std::uint16_t* w_gate,
                               const std::uint16_t* w_up, const std::uint16_t* w_down,
                               const std::uint16_t* w_out_gate, std::uint32_t tokens,
-                              std::uint32_t inter, void* scratch, std::uint16_t* shared_output,
-                              std::uint16_t* shared_gate, void* stream, int device) {
-    check(q38m_moe_shared_expert_v1(hidden, w_gate, w_up, w_down, w_out_gate, tokens, inter,
-                                    scratch, shared_output, shared_gate, stream, device));
+                              std::uint32_t hidden_width, std::uint32_t inter, void* scratch,
+                              std::uint16_t* shared_output, std::uint16_t* shared_gate,
+                              void* stream, int device) {
+    check(q38m_moe_shared_expert_v1(hidden, w_gate, w_up, w_down, w_out_gate, tokens,
+                                    hidden_width, inter, scratch, shared_output, shared_gate,
+                                    stream, device));
 }
 
 inline bool cuda_q38_moe_prefill_compiled() { return q38m_moe_compiled() == 1; }

@@ -10,7 +10,10 @@ import os
 import numpy as np
 
 ORACLE_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(ORACLE_DIR, "_build", "libq38m_oracle.so")
+# Q38M_ORACLE_LIB selects another build of the same source (the sanitizer
+# build of `make -C oracle check-sanitize`).
+LIB_PATH = os.environ.get("Q38M_ORACLE_LIB") or os.path.join(ORACLE_DIR, "_build",
+                                                             "libq38m_oracle.so")
 
 EXPERTS = 512
 TOPK = 10
@@ -75,6 +78,7 @@ _SIGS = {
     "q38o_gate_up": (None, [ctypes.POINTER(Weights), _U32, _U32, _P, _P, _P, _P, _P]),
     "q38o_down": (None, [ctypes.POINTER(Weights), _U32, _U32, _P, _P, _P, _P]),
     "q38o_combine": (None, [_P, _P, _P, _P, _U32, _U32, _P]),
+    "q38o_combine_shared": (None, [_P, _P, _P, _U32, _U32, _P]),
     "q38o_moe_prefill": (_INT, [ctypes.POINTER(MoeIO)]),
     "q38o_moe_per_token": (_INT, [ctypes.POINTER(MoeIO)]),
     "q38o_num_threads": (_INT, []),
@@ -369,6 +373,19 @@ def moe(hidden_bf16, gate_up, down, logits=None, ids=None, weights=None, shared_
     if rc:
         raise ValueError(f"oracle MoE step failed with status {rc}")
     return res
+
+
+def combine_shared(routed_bf16, shared_bf16, gate_bf16):
+    """Decode combine of bf16 rows (cuda/q38_moe.cu:337-350): [T][H] words,
+    gate [T] words -> bf16(fma(shared, sigmoid(gate), routed))."""
+    routed = np.ascontiguousarray(routed_bf16, dtype=np.uint16)
+    shared = np.ascontiguousarray(shared_bf16, dtype=np.uint16)
+    gate = np.ascontiguousarray(gate_bf16, dtype=np.uint16)
+    tokens, hidden = routed.shape
+    assert shared.shape == routed.shape and gate.shape == (tokens,)
+    out = np.empty_like(routed)
+    lib().q38o_combine_shared(_p(routed), _p(shared), _p(gate), tokens, hidden, _p(out))
+    return out
 
 
 def set_threads(n):

@@ -743,7 +743,9 @@ void q38o_down(const q38o_weights* down, uint32_t hidden, uint32_t inter,
 }
 
 /* Fixed rank-order reduce from 0.0f plus the optional gated shared term
- * (cuda/q38_moe_prefill.cu:601-631). */
+ * (cuda/q38_moe_prefill.cu:601-631).  The reference writes
+ * `routed + shared * multiplier`, which nvcc's default -fmad=true contracts
+ * into one fused multiply-add; the restatement uses that fma. */
 void q38o_combine(const float* route_output, const uint32_t* inverse,
                   const uint16_t* shared_output, const uint16_t* shared_gate,
                   uint32_t tokens, uint32_t hidden, uint16_t* output) {
@@ -759,12 +761,27 @@ void q38o_combine(const float* route_output, const uint32_t* inverse,
             float routed = 0.0f;
             for (uint32_t r = 0; r < Q38O_TOPK; ++r)
                 routed += route_output[(size_t)inverse[t * Q38O_TOPK + r] * hidden + c];
-            if (shared) {
-                const float term =
-                    q38o_bf16_to_f32(shared_output[(size_t)t * hidden + c]) * multiplier;
-                routed = routed + term;
-            }
+            if (shared)
+                routed = fmaf(q38o_bf16_to_f32(shared_output[(size_t)t * hidden + c]),
+                              multiplier, routed);
             output[(size_t)t * hidden + c] = q38o_f32_to_bf16(routed);
+        }
+    }
+}
+
+/* Decode combine of bf16 routed rows (cuda/q38_moe.cu:337-350):
+ * out = bf16(routed + shared * (1 / (1 + exp(-gate[t])))), the sum
+ * contracted into one fma as nvcc builds the reference expression. */
+void q38o_combine_shared(const uint16_t* routed, const uint16_t* shared_output,
+                         const uint16_t* shared_gate, uint32_t tokens, uint32_t hidden,
+                         uint16_t* output) {
+    for (uint32_t t = 0; t < tokens; ++t) {
+        const float g = q38o_bf16_to_f32(shared_gate[t]);
+        const float sigmoid = 1.0f / (1.0f + q38o_expf(-g));
+        for (uint32_t c = 0; c < hidden; ++c) {
+            const size_t i = (size_t)t * hidden + c;
+            output[i] = q38o_f32_to_bf16(
+                fmaf(q38o_bf16_to_f32(shared_output[i]), sigmoid, q38o_bf16_to_f32(routed[i])));
         }
     }
 }
@@ -875,11 +892,9 @@ int q38o_moe_per_token(q38o_moe_io* io) {
             for (uint32_t c = 0; c < H; ++c) {
                 float routed = 0.0f;
                 for (uint32_t r = 0; r < Q38O_TOPK; ++r) routed += routes[(size_t)r * H + c];
-                if (shared) {
-                    const float term =
-                        q38o_bf16_to_f32(io->shared_output[(size_t)t * H + c]) * multiplier;
-                    routed = routed + term;
-                }
+                if (shared)
+                    routed = fmaf(q38o_bf16_to_f32(io->shared_output[(size_t)t * H + c]),
+                                  multiplier, routed);
                 io->output[(size_t)t * H + c] = q38o_f32_to_bf16(routed);
             }
         }

@@ -119,6 +119,12 @@ int q38o_quantize_weights(const uint16_t* src_bf16, uint64_t rows,
                           uint32_t cols, int bits, uint32_t group,
                           uint8_t* data, uint16_t* scales, int scale_bf16);
 
+/* ---- decode combine (cuda/q38_moe.cu:337-350) ------------------------ */
+/* out[t][c] = bf16(fmaf(shared[t][c], 1/(1+exp(-gate[t])), routed[t][c])) */
+void q38o_combine_shared(const uint16_t* routed, const uint16_t* shared_output,
+                         const uint16_t* shared_gate, uint32_t tokens, uint32_t hidden,
+                         uint16_t* output);
+
 /* ---- weights -------------------------------------------------------- */
 typedef struct q38o_weights {
     const uint8_t* data;     /* canonical row-major: W4 [E][rows][cols/2]

@@ -26,6 +26,9 @@ ERR_UNSUPPORTED = 3
 ROUTE_EXPERTS = 512
 ROUTE_TOPK = 10
 MMQ_M = 16
+MODE_GROUPED_MMQ = 1
+MODE_GROUPED_MMQ_SAFE = 2
+MODE_LEGACY_ATOMIC_DIAGNOSTIC = 3
 SLAB_MAX_TOKENS = 512
 HIDDEN = 2048
 INTERMEDIATE = 512
@@ -126,9 +129,9 @@ SIGNATURES = {
     "q38m_quantize_rows_i8": (_INT, [_P, _U32, _U32, _P, _P, _P, _INT]),
     "q38m_residual_add_bf16": (_INT, [_P, _P, _P, _U64, _P, _INT]),
     "q38m_moe_grouped_gate_up_v1": (_INT, [ctypes.POINTER(ExpertWeights), _P, _P, _P, _P, _P,
-                                           _U32, _P, _P, _INT]),
+                                           _U32, _P, _U32, _P, _INT]),
     "q38m_moe_grouped_down_v1": (_INT, [ctypes.POINTER(ExpertWeights), _P, _P, _P, _U32, _P,
-                                        _P, _INT]),
+                                        _U32, _P, _INT]),
     "q38m_moe_reduce_top10_and_combine_shared_v1": (_INT, [_P, _P, _P, _P, _U32, _P, _P, _INT]),
     "q38m_moe_combine_shared_bf16": (_INT, [_P, _P, _P, _P, _U32, _P, _INT]),
     "q38m_moe_prefill_workspace_bytes": (_SZ, [_U32]),
@@ -157,9 +160,10 @@ SIGNATURES = {
                                           ctypes.POINTER(ExpertWeights), _P, _INT]),
     "q38m_quantize_expert_weights": (_INT, [_P, ctypes.POINTER(ExpertWeights), _P, _INT]),
     "q38m_dense_gemm_bf16": (_INT, [_P, _P, _U32, _U32, _U32, _P, _P, _P, _INT]),
-    "q38m_moe_router_v1": (_INT, [_P, _P, _U32, _P, _P, _INT]),
+    "q38m_moe_router_v1": (_INT, [_P, _P, _U32, _U32, _P, _P, _INT]),
     "q38m_moe_shared_expert_scratch_bytes": (_SZ, [_U32, _U32]),
-    "q38m_moe_shared_expert_v1": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _P, _P, _P, _P, _INT]),
+    "q38m_moe_shared_expert_v1": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P,
+                                         _INT]),
     "q38m_hyper_repeat_embedding_bf16": (_INT, [_P, _P, _U32, _U32, _P, _INT]),
     "q38m_hyper_group_rmsnorm_bf16": (_INT, [_P, _P, _P, _U32, _U32, _P, _INT]),
     "q38m_hyper_silu_scaled_bf16": (_INT, [_P, _P, _U32, _U32, _F, _P, _INT]),
@@ -171,6 +175,7 @@ SIGNATURES = {
     "q38m_synth_fill": (_INT, [_U32, _U64, _U64, _U64, _F, _I32, _I32, _P, _U32, _P, _P, _INT]),
     "q38m_moe_compiled": (_INT, []),
     "q38m_last_error": (ctypes.c_char_p, []),
+    # self checks (include/q38m_selftest.h)
     "q38m_debug_expf": (_INT, [_P, _U32, _P, _P, _INT]),
     "q38m_debug_mfma_16x16x32_i8": (_INT, [_P, _P, _P, _P, _INT]),
     "q38m_debug_mfma_32x32x32_i8": (_INT, [_P, _P, _P, _P, _INT]),

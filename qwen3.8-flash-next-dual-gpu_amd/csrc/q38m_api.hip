@@ -11,6 +11,7 @@
 #include <string>
 
 #include "q38m_internal.h"
+#include "q38m_selftest.h"
 
 #include <initializer_list>
 
@@ -84,6 +85,11 @@ bool valid_down(const q38m_expert_weights_v1* w) {
     return (w->format == Q38M_FORMAT_W8_SYM &&
             (w->group_size == 0u || w->group_size == 64u || w->group_size == 128u)) ||
            (w->format == Q38M_FORMAT_W4_SYM && w4_group(w->group_size));
+}
+
+// validate_grouped_mode (cuda/q38_moe_prefill.cu:64-68)
+bool valid_grouped_mode(uint32_t mode) {
+    return mode == Q38M_MOE_MODE_GROUPED_MMQ || mode == Q38M_MOE_MODE_GROUPED_MMQ_SAFE;
 }
 
 int check_weights(const q38m_expert_weights_v1* w, bool gate_up) {
@@ -249,8 +255,10 @@ int q38m_residual_add_bf16(const uint16_t* a, const uint16_t* b, uint16_t* out,
 int q38m_moe_grouped_gate_up_v1(const q38m_expert_weights_v1* gate_up, const int8_t* xq,
                                 const float* xs, const uint32_t* packed_assignment,
                                 const float* token_rank_weights, const q38m_task_v1* tasks,
-                                uint32_t task_count, uint16_t* weighted_mid, void* stream,
-                                int device) {
+                                uint32_t task_count, uint16_t* weighted_mid, uint32_t mode,
+                                void* stream, int device) {
+    if (!valid_grouped_mode(mode))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill MoE mode");
     if (int rc = check_weights(gate_up, true)) return rc;
     if (!xq || !xs || !packed_assignment || !token_rank_weights || !tasks || task_count == 0 ||
         task_count > q38m::max_tasks_v1(Q38M_PREFILL_SLAB_MAX_TOKENS) || !weighted_mid ||
@@ -264,8 +272,10 @@ int q38m_moe_grouped_gate_up_v1(const q38m_expert_weights_v1* gate_up, const int
 
 int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down, const int8_t* mid_q,
                              const float* mid_scales, const q38m_task_v1* tasks,
-                             uint32_t task_count, float* route_output, void* stream,
-                             int device) {
+                             uint32_t task_count, float* route_output, uint32_t mode,
+                             void* stream, int device) {
+    if (!valid_grouped_mode(mode))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill MoE mode");
     if (int rc = check_weights(down, false)) return rc;
     if (!mid_q || !mid_scales || !tasks || task_count == 0 ||
         task_count > q38m::max_tasks_v1(Q38M_PREFILL_SLAB_MAX_TOKENS) || !route_output ||
@@ -355,7 +365,8 @@ int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert
     if (int rc = check_weights(gate_up, true)) return rc;
     if (int rc = check_weights(down, false)) return rc;
     if (!hidden || !ws || !output || tokens == 0 || tokens > ws->max_tokens ||
-        !valid_plan(&ws->plan) || !ws->expert_ids || !ws->expert_weights || !ws->xq || !ws->xs ||
+        tokens > Q38M_PREFILL_SLAB_MAX_TOKENS || !valid_plan(&ws->plan) || !ws->expert_ids ||
+        !ws->expert_weights || !ws->xq || !ws->xs ||
         !ws->weighted_mid || !ws->mid_q || !ws->mid_s || !ws->route_output ||
         (shared_output == nullptr) != (shared_gate == nullptr) || !aligned(hidden, 16) ||
         !aligned(output, 16))
@@ -396,12 +407,23 @@ uint32_t q38m_moe_wide_max_tasks(uint32_t tokens) {
     return q38m::max_tasks_wide(tokens);
 }
 
+// Task slots of a chunk plan bound for `tokens`: the chunk plan's own bound,
+// or the V1 bound of a slab of up to 512 tokens if that is larger, so that a
+// chunk workspace also serves q38m_moe_prefill_v1 for any slab it holds.
+static size_t wide_task_slots(uint32_t tokens) {
+    const uint32_t slab = tokens < Q38M_PREFILL_SLAB_MAX_TOKENS ? tokens
+                                                                : Q38M_PREFILL_SLAB_MAX_TOKENS;
+    const uint32_t wide = q38m::max_tasks_wide(tokens);
+    const uint32_t v1 = q38m::max_tasks_v1(slab);
+    return wide > v1 ? wide : v1;
+}
+
 size_t q38m_moe_wide_plan_bytes(uint32_t tokens) {
     if (tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS) return 0;
     const size_t routes = q38m::routes_v1(tokens);
     return sizeof(q38m_route_plan_header_v1) + Q38M_ROUTE_EXPERTS * sizeof(uint16_t) +
            2u * (Q38M_ROUTE_EXPERTS + 1u) * sizeof(uint32_t) + 2u * routes * sizeof(uint32_t) +
-           static_cast<size_t>(q38m::max_tasks_wide(tokens)) * sizeof(q38m_task_v1);
+           wide_task_slots(tokens) * sizeof(q38m_task_v1);
 }
 
 size_t q38m_moe_wide_plan_scratch_bytes(uint32_t tokens) {
@@ -623,7 +645,9 @@ int q38m_dense_gemm_bf16(const uint16_t* a, const uint16_t* b, uint32_t m, uint3
 }
 
 int q38m_moe_router_v1(const uint16_t* hidden, const uint16_t* router, uint32_t tokens,
-                       float* logits, void* stream, int device) {
+                       uint32_t hidden_width, float* logits, void* stream, int device) {
+    if (hidden_width != Q38M_HIDDEN)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "router hidden width must be 2048");
     if (!hidden || !router || !logits || tokens == 0 || tokens > kDenseMaxRows ||
         !aligned(hidden, 16) || !aligned(router, 16))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid router buffers");
@@ -639,9 +663,12 @@ size_t q38m_moe_shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter) {
 
 int q38m_moe_shared_expert_v1(const uint16_t* hidden, const uint16_t* w_gate,
                               const uint16_t* w_up, const uint16_t* w_down,
-                              const uint16_t* w_out_gate, uint32_t tokens, uint32_t inter,
-                              void* scratch, uint16_t* shared_output, uint16_t* shared_gate,
-                              void* stream, int device) {
+                              const uint16_t* w_out_gate, uint32_t tokens,
+                              uint32_t hidden_width, uint32_t inter, void* scratch,
+                              uint16_t* shared_output, uint16_t* shared_gate, void* stream,
+                              int device) {
+    if (hidden_width != Q38M_HIDDEN)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "shared expert hidden width must be 2048");
     if (!hidden || !w_gate || !w_up || !w_down || !w_out_gate || !scratch || !shared_output ||
         !shared_gate || tokens == 0 || tokens > kDenseMaxRows || inter == 0 || inter % 32u != 0u ||
         !aligned(hidden, 16) || !aligned(w_gate, 16) || !aligned(w_up, 16) ||

@@ -400,7 +400,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
         if (shared_output != nullptr && shared_gate != nullptr) {
             const float g = bf16_to_f32(shared_gate[0]);
             const float multiplier = 1.0f / (1.0f + exp_q(-g));
-            total = total + bf16_to_f32(shared_output[channel]) * multiplier;
+            total = __builtin_fmaf(bf16_to_f32(shared_output[channel]), multiplier, total);
         }
         uint32_t result = f32_to_bf16(total);
         if (residual != nullptr)

@@ -528,7 +528,9 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
 
 // ---------------------------------------------------------------------------
 // Fixed rank-order reduce from 0.0f plus the optional gated shared term
-// (q38_moe_prefill.cu:601-631).  One workgroup per token, 8 columns/thread.
+// (q38_moe_prefill.cu:601-631), added as fma(shared, multiplier, routed): the
+// contraction nvcc's default -fmad applies to the reference expression.
+// One workgroup per token, 8 columns/thread.
 // ---------------------------------------------------------------------------
 template <uint32_t H>
 __global__ __launch_bounds__(256) void combine_kernel(
@@ -563,8 +565,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const uint32_t h = (i & 1) ? (sw[i >> 1] >> 16) : (sw[i >> 1] & 0xffffu);
-                const float term = bf16_to_f32(h) * multiplier;
-                acc[i] = acc[i] + term;
+                acc[i] = __builtin_fmaf(bf16_to_f32(h), multiplier, acc[i]);
             }
         }
         uint4 packed;
@@ -576,7 +577,8 @@ __global__ __launch_bounds__(256) void combine_kernel(
     }
 }
 
-// Decode combine: routed + shared * sigmoid(gate) (q38_moe.cu:337-350).
+// Decode combine: routed + shared * sigmoid(gate) (q38_moe.cu:337-350), the
+// sum contracted into one fma as nvcc builds the reference expression.
 template <uint32_t H>
 __global__ __launch_bounds__(256) void combine_shared_kernel(
     const uint16_t* __restrict__ routed, const uint16_t* __restrict__ shared,
@@ -585,8 +587,8 @@ __global__ __launch_bounds__(256) void combine_shared_kernel(
     if (index >= elements) return;
     const float g = bf16_to_f32(gate[index / H]);
     const float sigmoid = 1.0f / (1.0f + exp_q(-g));
-    const float term = bf16_to_f32(shared[index]) * sigmoid;
-    output[index] = static_cast<uint16_t>(f32_to_bf16(bf16_to_f32(routed[index]) + term));
+    output[index] = static_cast<uint16_t>(
+        f32_to_bf16(__builtin_fmaf(bf16_to_f32(shared[index]), sigmoid, bf16_to_f32(routed[index]))));
 }
 
 }  // namespace

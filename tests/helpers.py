@@ -124,14 +124,15 @@ def staged_step(q38m, layer, hidden, logits):
     mid = t.empty(R, W.INTER, dtype=t.int16, device="cuda")
     q38m.call("q38m_moe_grouped_gate_up_v1", ctypes.byref(layer.gu.desc), xq.data_ptr(),
               xs.data_ptr(), plan.packed_assignment, wts.data_ptr(), plan.tasks, tasks,
-              mid.data_ptr(), s, 0)
+              mid.data_ptr(), q38m.MODE_GROUPED_MMQ, s, 0)
     mq = t.empty(R, W.INTER, dtype=t.int8, device="cuda")
     ms = t.empty(R, dtype=t.float32, device="cuda")
     q38m.call("q38m_quantize_rows_i8", mid.data_ptr(), R, W.INTER, mq.data_ptr(), ms.data_ptr(),
               s, 0)
     route_output = t.empty(R, W.HIDDEN, dtype=t.float32, device="cuda")
     q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(layer.dn.desc), mq.data_ptr(),
-              ms.data_ptr(), plan.tasks, tasks, route_output.data_ptr(), s, 0)
+              ms.data_ptr(), plan.tasks, tasks, route_output.data_ptr(), q38m.MODE_GROUPED_MMQ_SAFE,
+              s, 0)
     out = t.empty(T, W.HIDDEN, dtype=t.int16, device="cuda")
     q38m.call("q38m_moe_reduce_top10_and_combine_shared_v1", route_output.data_ptr(),
               plan.assignment_to_packed, None, None, T, out.data_ptr(), s, 0)

@@ -12,13 +12,15 @@ import pytest
 
 from conftest import ROOT
 
-HEADER = os.path.join(ROOT, "include", "q38m.h")
+HEADERS = [os.path.join(ROOT, "include", name) for name in ("q38m.h", "q38m_selftest.h")]
 
 
-def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(q38m_[a-z0-9_]+)\s*\(", text)))
+def declared_functions(headers=HEADERS):
+    names = set()
+    for header in headers:
+        text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+        names.update(re.findall(r"\b(q38m_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol(q38m):
@@ -29,6 +31,13 @@ def test_library_exports_every_declared_symbol(q38m):
         assert hasattr(lib, name), name
     assert set(names) == set(q38m.SIGNATURES), "binding and header disagree"
     assert lib.q38m_moe_compiled() == 1
+
+
+def test_product_header_declares_no_self_checks():
+    product = declared_functions(HEADERS[:1])
+    assert not [n for n in product if n.startswith("q38m_debug")]
+    assert declared_functions(HEADERS[1:]) == ["q38m_debug_expf", "q38m_debug_mfma_16x16x32_i8",
+                                               "q38m_debug_mfma_32x32x32_i8"]
 
 
 def test_struct_layouts(q38m):
@@ -106,7 +115,7 @@ def fake_weights(q38m, fmt=2, group=32, layout=3, rows=1024, cols=2048, experts=
 
 def test_gate_up_validation(q38m):
     good = fake_weights(q38m)
-    args = [0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 800, 0x60000, None, 0]
+    args = [0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 800, 0x60000, 1, None, 0]
 
     def call(w, *override):
         a = list(args)
@@ -134,11 +143,15 @@ def test_gate_up_validation(q38m):
         call(good, (0, None))       # null activations
     with pytest.raises(q38m.InvalidArgument):
         call(good, (0, 0x10001))    # misaligned activations
+    # validate_grouped_mode (q38_moe_prefill.cu:64-68): grouped and grouped-safe only
+    for mode in (0, q38m.MODE_LEGACY_ATOMIC_DIAGNOSTIC, 4):
+        with pytest.raises(q38m.InvalidArgument, match="mode"):
+            call(good, (7, mode))
 
 
 def test_down_validation(q38m):
     w8 = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)
-    args = [0x10000, 0x20000, 0x30000, 10, 0x40000, None, 0]
+    args = [0x10000, 0x20000, 0x30000, 10, 0x40000, 2, None, 0]
     with pytest.raises(q38m.Unsupported):
         q38m.call("q38m_moe_grouped_down_v1",
                   ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=0, rows=2048, cols=512)),
@@ -160,6 +173,11 @@ def test_down_validation(q38m):
     with pytest.raises(q38m.InvalidArgument):  # transposed shape
         q38m.call("q38m_moe_grouped_down_v1",
                   ctypes.byref(fake_weights(q38m, fmt=3, group=0, layout=2, rows=512, cols=2048)), *args)
+    for mode in (0, 3):
+        bad = list(args)
+        bad[5] = mode
+        with pytest.raises(q38m.InvalidArgument, match="mode"):
+            q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(w8), *bad)
     args[2] = None
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_moe_grouped_down_v1", ctypes.byref(w8), *args)
@@ -236,17 +254,17 @@ def test_dense_validation(q38m):
             q38m.call("q38m_dense_gemm_bf16", *args, None, 0)
     with pytest.raises(q38m.InvalidArgument):  # both outputs
         q38m.call("q38m_dense_gemm_bf16", 0x1000, 0x2000, 64, 512, 2048, 0x3000, 0x4000, None, 0)
-    # hidden, router, tokens, logits
-    good = [0x1000, 0x2000, 8, 0x3000]
-    for i, bad in [(0, None), (1, None), (2, 0), (3, None), (0, 0x1004)]:
+    # hidden, router, tokens, hidden_width, logits
+    good = [0x1000, 0x2000, 8, 2048, 0x3000]
+    for i, bad in [(0, None), (1, None), (2, 0), (3, 2560), (3, 1024), (4, None), (0, 0x1004)]:
         args = list(good)
         args[i] = bad
         with pytest.raises(q38m.InvalidArgument):
             q38m.call("q38m_moe_router_v1", *args, None, 0)
-    # hidden, wg, wu, wd, wo, tokens, inter, scratch, shared_output, shared_gate
-    good = [0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 8, 512, 0x6000, 0x7000, 0x8000]
-    for i, bad in [(0, None), (4, None), (5, 0), (6, 0), (6, 520), (7, None), (8, None),
-                   (9, None), (3, 0x4008), (7, 0x6004)]:
+    # hidden, wg, wu, wd, wo, tokens, hidden_width, inter, scratch, shared_output, shared_gate
+    good = [0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 8, 2048, 512, 0x6000, 0x7000, 0x8000]
+    for i, bad in [(0, None), (4, None), (5, 0), (6, 2560), (7, 0), (7, 520), (8, None),
+                   (9, None), (10, None), (3, 0x4008), (8, 0x6004)]:
         args = list(good)
         args[i] = bad
         with pytest.raises(q38m.InvalidArgument):
@@ -307,6 +325,41 @@ def test_decode_and_step_validation(q38m):
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2000, 64,
                   ctypes.byref(ws), None, None, 0x3000, None, -1)  # negative device
+
+
+def test_slab_step_on_a_chunk_workspace(q38m):
+    """A chunk workspace holds more tokens than a slab: the slab entry point
+    (whose plan kernel and task grid are sized for <= 512 tokens) must
+    reject 513 tokens before any launch, and a chunk workspace bound for
+    <= 512 tokens has task slots for a full V1 plan."""
+    lib = q38m.lib()
+    gu = fake_weights(q38m)
+    dn = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)
+    wide = q38m.WideWorkspace()
+    base = 0x10000000
+    q38m.call("q38m_moe_wide_workspace_bind", base, lib.q38m_moe_wide_workspace_bytes(4096), 4096,
+              ctypes.byref(wide))
+    assert wide.step.max_tokens == 4096
+    for tokens in (513, 4096):
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2000,
+                      tokens, ctypes.byref(wide.step), None, None, 0x3000, None, 0)
+    for tokens in (1, 64, 300, 512, 600, 4096):
+        slab = min(tokens, 512)
+        task_bytes = lib.q38m_moe_wide_plan_bytes(tokens) - (
+            64 + 1024 + 2 * 2052 + 2 * 4 * 10 * tokens)
+        assert task_bytes >= 8 * lib.q38m_moe_prefill_max_tasks_v1(slab)
+        assert task_bytes >= 8 * lib.q38m_moe_wide_max_tasks(tokens)
+
+
+def test_combine_shared_validation(q38m):
+    # routed, shared, gate, output, tokens
+    good = [0x1000, 0x2000, 0x3000, 0x4000, 4]
+    for i, bad in [(0, None), (1, None), (2, None), (3, None), (4, 0)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_combine_shared_bf16", *args, None, 0)
 
 
 def test_repack_and_synth_validation(q38m):
@@ -380,7 +433,8 @@ int main() {
                               Q38M_LAYOUT_ROW_MAJOR, 512, 1024, 2048};
     try {
         q38m::cuda_moe_grouped_gate_up_v1(rm, nullptr, nullptr, nullptr, nullptr, nullptr, 1,
-                                          nullptr, nullptr, 0);
+                                          nullptr, q38m::Q38PrefillMoeModeV1::kGroupedMmq,
+                                          nullptr, 0);
         return 5;
     } catch (const std::invalid_argument& e) {
         std::printf("unsupported layout: %s\n", e.what());
@@ -403,3 +457,59 @@ def test_cpp_wrapper_compiles_links_and_throws(tmp_path):
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout + out.stderr
     assert "too small" in out.stdout and "MFMA16" in out.stdout and out.stdout.endswith("ok\n")
+
+
+def _function_with_comment(text, signature):
+    """The comment block above `signature` through the function's closing brace."""
+    start = text.index(signature)
+    lines = text[:start].split("\n")[:-1]
+    while lines and lines[-1].startswith("//"):
+        lines.pop()
+    begin = len("\n".join(lines)) + 1 if lines else 0
+    return text[begin:text.index("\n}\n", start) + 3]
+
+
+def test_integration_run_moe_is_the_compiled_stage_code():
+    """INTEGRATION.md shows run_moe and the slab loop verbatim from
+    include/q38m_stage.hpp, the header tests/test_gpu_stage.py compiles and
+    runs against libq38m.so."""
+    stage = open(os.path.join(ROOT, "include", "q38m_stage.hpp")).read()
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    for signature in ("inline void run_moe(", "inline std::uint16_t* run_prefill_moe("):
+        body = _function_with_comment(stage, signature)
+        assert body.count("\n") > 10
+        assert "```cpp\n" + body + "```" in doc, signature
+    assert "2560, 320" not in doc
+
+
+def test_stage_header_compiles_and_validates_workspace(tmp_path):
+    """The stage header builds with the host compiler and no vendor header;
+    its workspace binder rejects a bad allocation before any device call."""
+    import subprocess
+    src = tmp_path / "stage.cpp"
+    src.write_text(r'''
+#include "q38m_stage.hpp"
+#include <cstdio>
+int main() {
+    const std::size_t bytes = q38m::moe_stage_workspace_bytes(512);
+    if (bytes == 0 || q38m::moe_stage_workspace_bytes(513) != 0) return 2;
+    try {
+        q38m::bind_moe_stage_workspace(reinterpret_cast<void*>(0x1000), bytes - 1, 512);
+        return 3;
+    } catch (const std::invalid_argument&) {}
+    auto ws = q38m::bind_moe_stage_workspace(reinterpret_cast<void*>(0x100000), bytes, 512);
+    if (ws.max_tokens != 512 || ws.moe.max_tokens != 512) return 4;
+    const auto end = reinterpret_cast<std::uintptr_t>(ws.decode_scratch) +
+                     q38m_moe_decode_scratch_bytes();
+    if (end > 0x100000 + bytes) return 5;
+    std::printf("ok\n");
+    return 0;
+}
+''')
+    exe = tmp_path / "stage"
+    pkg = os.path.join(ROOT, "qwen3.8-flash-next-dual-gpu_amd")
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-I",
+                    os.path.join(ROOT, "include"), str(src), "-o", str(exe), "-L", pkg, "-lq38m",
+                    f"-Wl,-rpath,{pkg}", "-Wl,-rpath,/opt/rocm/lib"], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert out.returncode == 0 and out.stdout == "ok\n", out.stdout + out.stderr

@@ -68,8 +68,8 @@ def test_router_logits_and_routes(q38m, orc):
     router = bf16_matrix(orc, rng, W.EXPERTS, W.HIDDEN, 0.02)
     logits = t.empty(tokens * W.EXPERTS, dtype=t.float32, device="cuda")
     hd, rd = device(hidden), device(router)
-    q38m.call("q38m_moe_router_v1", hd.data_ptr(), rd.data_ptr(), tokens, logits.data_ptr(),
-              stream(), 0)
+    q38m.call("q38m_moe_router_v1", hd.data_ptr(), rd.data_ptr(), tokens, W.HIDDEN,
+              logits.data_ptr(), stream(), 0)
     t.cuda.synchronize()
     got = host(logits, np.float32).reshape(tokens, W.EXPERTS)
     check_close(orc, got, hidden, router, False)
@@ -104,7 +104,7 @@ def test_shared_expert(q38m, orc):
     so = t.empty(tokens * W.HIDDEN, dtype=t.int16, device="cuda")
     sg = t.empty(tokens, dtype=t.int16, device="cuda")
     devs = [device(v) for v in (x, wg, wu, wd, wo)]
-    q38m.call("q38m_moe_shared_expert_v1", *[d.data_ptr() for d in devs], tokens, inter,
+    q38m.call("q38m_moe_shared_expert_v1", *[d.data_ptr() for d in devs], tokens, W.HIDDEN, inter,
               scratch.data_ptr(), so.data_ptr(), sg.data_ptr(), stream(), 0)
     t.cuda.synchronize()
     words = host(scratch, np.uint16)
@@ -137,14 +137,15 @@ def test_moe_block_router_routed_shared(q38m, orc):
     weights = [device(bf16_matrix(orc, rng, r, c, 0.02)) for r, c in
                ((W.INTER, W.HIDDEN), (W.INTER, W.HIDDEN), (W.HIDDEN, W.INTER), (1, W.HIDDEN))]
     logits = t.empty(tokens, W.EXPERTS, dtype=t.float32, device="cuda")
-    q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), tokens,
+    q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), tokens, W.HIDDEN,
               logits.data_ptr(), stream(), 0)
     scratch = t.empty(q38m.lib().q38m_moe_shared_expert_scratch_bytes(tokens, W.INTER) // 2,
                       dtype=t.int16, device="cuda")
     so = t.empty(tokens, W.HIDDEN, dtype=t.int16, device="cuda")
     sg = t.empty(tokens, dtype=t.int16, device="cuda")
     q38m.call("q38m_moe_shared_expert_v1", hidden.data_ptr(), *[w.data_ptr() for w in weights],
-              tokens, W.INTER, scratch.data_ptr(), so.data_ptr(), sg.data_ptr(), stream(), 0)
+              tokens, W.HIDDEN, W.INTER, scratch.data_ptr(), so.data_ptr(), sg.data_ptr(), stream(),
+              0)
     ws = q38m.PrefillWorkspace_(tokens)
     out = prefill(q38m, layer, hidden, logits, ws, shared=(so, sg))
     ref = orc.moe(host(hidden, np.uint16), layer.host_gu, layer.host_dn,

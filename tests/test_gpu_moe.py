@@ -189,6 +189,32 @@ def test_shared_expert_combine(q38m, orc, layers):
     assert np.array_equal(host(out, np.uint16), ref["output"])
 
 
+def test_standalone_decode_combine_shared(q38m, orc):
+    """q38m_moe_combine_shared_bf16 (cuda_moe_combine_shared_bf16,
+    cuda/q38_moe.cu:337-350, :487-501) against the oracle bit for bit:
+    bf16 routed rows plus shared * sigmoid(gate), contracted into one fma,
+    for zero, signed-zero, saturating and ordinary gates."""
+    t = torch()
+    rng = np.random.default_rng(337)
+    gates = np.array([0.0, -0.0, 100.0, -100.0, -3.5, 2.25, 0.125, -17.0], np.float32)
+    tokens = gates.size
+    routed = orc.f32_to_bf16(rng.standard_normal((tokens, W.HIDDEN)) * 8)
+    shared = orc.f32_to_bf16(rng.standard_normal((tokens, W.HIDDEN)) * 3)
+    gate = orc.f32_to_bf16(gates)
+    out = t.empty(tokens * W.HIDDEN, dtype=t.int16, device="cuda")
+    dr, ds, dg = device(routed), device(shared), device(gate)
+    q38m.call("q38m_moe_combine_shared_bf16", dr.data_ptr(), ds.data_ptr(), dg.data_ptr(),
+              out.data_ptr(), tokens, stream(), 0)
+    got = host(out, np.uint16).reshape(tokens, W.HIDDEN)
+    want = orc.combine_shared(routed, shared, gate)
+    assert np.array_equal(got, want)
+    # saturated gates: sigmoid(100) == 1 and sigmoid(-100) == 0 exactly
+    assert np.array_equal(got[3], routed[3])
+    assert np.array_equal(orc.bf16_to_f32(got[2]),
+                          orc.bf16_to_f32(orc.f32_to_bf16(orc.bf16_to_f32(routed[2]) +
+                                                          orc.bf16_to_f32(shared[2]))))
+
+
 @pytest.mark.parametrize("config", [1, 2])
 def test_decode_equals_prefill_and_oracle(q38m, orc, layers, config):
     layer = layers(config)

@@ -137,3 +137,44 @@ def test_oracle_threads_bit_identical(orc):
 def test_logf_close(orc, x):
     got = orc.lib().q38o_logf(x)
     assert abs(got - np.log(np.float64(np.float32(x)))) <= 2 * np.spacing(np.float32(abs(got) or 1))
+
+
+def test_decode_combine_shared_is_one_fma(orc):
+    """q38o_combine_shared: bf16(routed + shared * sigmoid(gate)) with the
+    sum contracted into one fma (nvcc's default -fmad on the reference
+    expression, cuda/q38_moe.cu:348-349).  Where the float64 sum of the
+    exact product and routed is itself exact, rounding it once to float32
+    is the fma; those elements must agree.  The rows also hold pairs found
+    by search whose bf16 result differs between the fma and a separately
+    rounded multiply-then-add, so an unfused restatement fails here."""
+    rng = np.random.default_rng(348)
+    tokens, hidden = 16, 256
+    gate = orc.f32_to_bf16(rng.standard_normal(tokens) * 3)
+    g = orc.bf16_to_f32(gate)
+    sig = (np.float32(1.0) / (np.float32(1.0) + orc.expf(-g))).astype(np.float32)
+    routed = orc.f32_to_bf16(rng.standard_normal((tokens, hidden)) * 4)
+    shared = orc.f32_to_bf16(rng.standard_normal((tokens, hidden)) * 4)
+    planted = 0
+    for t in range(tokens):
+        cr = orc.f32_to_bf16(rng.standard_normal(1 << 16) * 4)
+        cs = orc.f32_to_bf16(rng.standard_normal(1 << 16) * 4)
+        rf, sf = orc.bf16_to_f32(cr), orc.bf16_to_f32(cs)
+        prod64 = sf.astype(np.float64) * np.float64(sig[t])
+        sum64 = prod64 + rf.astype(np.float64)
+        ok = ((sum64 - prod64) == rf) & ((sum64 - rf) == prod64)
+        fused = orc.f32_to_bf16(sum64.astype(np.float32))
+        unfused = orc.f32_to_bf16(rf + (sf * sig[t]).astype(np.float32))
+        hits = np.flatnonzero(ok & (fused != unfused))[:4]
+        routed[t, :hits.size], shared[t, :hits.size] = cr[hits], cs[hits]
+        planted += hits.size
+    assert planted >= 8
+    got = orc.combine_shared(routed, shared, gate)
+    r = orc.bf16_to_f32(routed).astype(np.float64)
+    p = orc.bf16_to_f32(shared).astype(np.float64) * sig.astype(np.float64)[:, None]
+    total = p + r
+    exact = ((total - p) == r) & ((total - r) == p)
+    assert exact.mean() > 0.9
+    assert np.array_equal(got[exact], orc.f32_to_bf16(total.astype(np.float32))[exact])
+    unfused = orc.f32_to_bf16(orc.bf16_to_f32(routed) +
+                              (orc.bf16_to_f32(shared) * sig[:, None]).astype(np.float32))
+    assert (got != unfused).sum() >= planted
