@@ -302,6 +302,27 @@ int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up,
                         const uint16_t* shared_gate, uint16_t* output,
                         void* stream, int device);
 
+/* ---- the same slab step without any allocation ----------------------
+ * No counterpart in the reference.  For callers that cannot allocate or
+ * pass a workspace: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  q38m_moe_prefill_v1 for a slab of at
+ * most Q38M_NOALLOC_MAX_TOKENS (64) tokens with fp32 router logits (top-k
+ * inside), bit-identical to it; its workspace is a device-resident array
+ * of q38m_moe_prefill_noalloc_scratch_bytes() bytes (6.1 MiB) that each GPU
+ * running the library holds until the process ends.  The function calls no
+ * allocator: the caller still owns every input and output.  Every call on
+ * one GPU shares that GPU's array, so calls that overlap on one GPU (other
+ * streams, other threads) race; serialise them.  More than 64 tokens:
+ * Q38M_ERR_INVALID_ARGUMENT. */
+#define Q38M_NOALLOC_MAX_TOKENS 64u
+size_t q38m_moe_prefill_noalloc_scratch_bytes(void);
+int q38m_moe_prefill_noalloc_v1(const q38m_expert_weights_v1* gate_up,
+                                const q38m_expert_weights_v1* down,
+                                const uint16_t* hidden, const float* logits,
+                                uint32_t tokens, const uint16_t* shared_output,
+                                const uint16_t* shared_gate, uint16_t* output,
+                                void* stream, int device);
+
 /* ---- one layer over a chunk of up to 32,768 tokens ------------------
  * No reference counterpart: the reference runs run_moe per slab of <= 512
  * tokens (cuda/cuda_backend.cu:1529-1559).  Same inputs, outputs and

@@ -30,6 +30,7 @@ MODE_GROUPED_MMQ = 1
 MODE_GROUPED_MMQ_SAFE = 2
 MODE_LEGACY_ATOMIC_DIAGNOSTIC = 3
 SLAB_MAX_TOKENS = 512
+NOALLOC_MAX_TOKENS = 64
 HIDDEN = 2048
 INTERMEDIATE = 512
 PLAN_MAGIC_V1 = 0x52383351
@@ -139,6 +140,10 @@ SIGNATURES = {
     "q38m_moe_prefill_v1": (_INT, [ctypes.POINTER(ExpertWeights), ctypes.POINTER(ExpertWeights),
                                    _P, _P, _U32, ctypes.POINTER(PrefillWorkspace), _P, _P, _P,
                                    _P, _INT]),
+    "q38m_moe_prefill_noalloc_scratch_bytes": (_SZ, []),
+    "q38m_moe_prefill_noalloc_v1": (_INT, [ctypes.POINTER(ExpertWeights),
+                                           ctypes.POINTER(ExpertWeights), _P, _P, _U32, _P, _P,
+                                           _P, _P, _INT]),
     "q38m_moe_wide_max_tasks": (_U32, [_U32]),
     "q38m_moe_wide_plan_bytes": (_SZ, [_U32]),
     "q38m_moe_wide_plan_scratch_bytes": (_SZ, [_U32]),

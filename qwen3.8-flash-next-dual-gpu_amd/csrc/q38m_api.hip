@@ -14,6 +14,7 @@
 #include "q38m_selftest.h"
 
 #include <initializer_list>
+#include <mutex>
 
 namespace {
 
@@ -316,16 +317,8 @@ int q38m_moe_combine_shared_bf16(const uint16_t* routed_output, const uint16_t* 
 
 size_t q38m_moe_prefill_workspace_bytes(uint32_t tokens) {
     if (tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS) return 0;
-    const size_t routes = q38m::routes_v1(tokens);
-    size_t bytes = align_up(q38m_moe_route_plan_bytes_v1(tokens), 256);
-    bytes += align_up(routes * 4u, 256) * 2u;                      // ids, weights
-    bytes += align_up(static_cast<size_t>(tokens) * Q38M_HIDDEN, 256);      // xq
-    bytes += align_up(static_cast<size_t>(tokens) * 4u, 256);               // xs
-    bytes += align_up(routes * Q38M_INTERMEDIATE * 2u, 256);                // weighted_mid
-    bytes += align_up(routes * Q38M_INTERMEDIATE, 256);                     // mid_q
-    bytes += align_up(routes * 4u, 256);                                    // mid_s
-    bytes += align_up(routes * Q38M_HIDDEN * 4u, 256);                      // route_output
-    return bytes;
+    // plan, ids, weights, xq, xs, weighted_mid, mid_q, mid_s, route_output
+    return q38m::prefill_workspace_bytes_v1(tokens);
 }
 
 int q38m_moe_prefill_workspace_bind(void* allocation, size_t bytes, uint32_t tokens,
@@ -358,6 +351,48 @@ int q38m_moe_prefill_workspace_bind(void* allocation, size_t bytes, uint32_t tok
     return Q38M_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// The run_moe sequence over one slab on a bound workspace (arguments
+// validated by the caller): top-k + int8 rows (or int8 rows of given
+// ids), plan, gate/up, mid quantisation, down, combine.
+hipError_t launch_prefill_step(const q38m_expert_weights_v1& gate_up,
+                               const q38m_expert_weights_v1& down, const uint16_t* hidden,
+                               const float* logits, uint32_t tokens,
+                               const q38m_prefill_workspace_v1& ws,
+                               const uint16_t* shared_output, const uint16_t* shared_gate,
+                               uint16_t* output, hipStream_t s) {
+    const uint32_t routes = q38m::routes_v1(tokens);
+    const uint32_t tasks = q38m::max_tasks_v1(tokens);
+    hipError_t status = hipSuccess;
+    if (logits)
+        status = q38m::launch_route_quantize(logits, hidden, tokens, Q38M_ROUTE_TOPK,
+                                             ws.expert_ids, ws.expert_weights, ws.xq, ws.xs, s);
+    else
+        status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws.xq, ws.xs, s);
+    if (status == hipSuccess)
+        status = q38m::launch_build_plan(ws.expert_ids, tokens, ws.plan, false, s);
+    if (status == hipSuccess)
+        status = q38m::launch_gate_up(gate_up, ws.xq, ws.xs, ws.plan.packed_assignment,
+                                      ws.expert_weights, ws.plan.tasks, tasks, ws.weighted_mid, s);
+    if (status == hipSuccess)
+        status = q38m::launch_quantize_rows(ws.weighted_mid, routes, Q38M_INTERMEDIATE, ws.mid_q,
+                                            ws.mid_s, s);
+    if (status == hipSuccess)
+        status = q38m::launch_down(down, ws.mid_q, ws.mid_s, ws.plan.tasks, tasks,
+                                   ws.route_output, s);
+    if (status == hipSuccess)
+        status = q38m::launch_combine(ws.route_output, ws.plan.assignment_to_packed,
+                                      shared_output, shared_gate, tokens, output, s);
+    return status;
+}
+
+}  // namespace
+
+extern "C" {
+
 int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert_weights_v1* down,
                         const uint16_t* hidden, const float* logits, uint32_t tokens,
                         const q38m_prefill_workspace_v1* ws, const uint16_t* shared_output,
@@ -372,32 +407,78 @@ int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert
         !aligned(output, 16))
         return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid prefill MoE step input");
     if (int rc = select_device(device)) return rc;
-    const hipStream_t s = as_stream(stream);
-    const uint32_t routes = q38m::routes_v1(tokens);
-    const uint32_t tasks = q38m::max_tasks_v1(tokens);
-    hipError_t status = hipSuccess;
-    if (logits)
-        status = q38m::launch_route_quantize(logits, hidden, tokens, Q38M_ROUTE_TOPK,
-                                             ws->expert_ids, ws->expert_weights, ws->xq, ws->xs,
-                                             s);
-    else
-        status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws->xq, ws->xs, s);
-    if (status == hipSuccess)
-        status = q38m::launch_build_plan(ws->expert_ids, tokens, ws->plan, false, s);
-    if (status == hipSuccess)
-        status = q38m::launch_gate_up(*gate_up, ws->xq, ws->xs, ws->plan.packed_assignment,
-                                      ws->expert_weights, ws->plan.tasks, tasks,
-                                      ws->weighted_mid, s);
-    if (status == hipSuccess)
-        status = q38m::launch_quantize_rows(ws->weighted_mid, routes, Q38M_INTERMEDIATE,
-                                            ws->mid_q, ws->mid_s, s);
-    if (status == hipSuccess)
-        status = q38m::launch_down(*down, ws->mid_q, ws->mid_s, ws->plan.tasks, tasks,
-                                   ws->route_output, s);
-    if (status == hipSuccess)
-        status = q38m::launch_combine(ws->route_output, ws->plan.assignment_to_packed,
-                                      shared_output, shared_gate, tokens, output, s);
-    return finish(status, "prefill MoE step");
+    return finish(launch_prefill_step(*gate_up, *down, hidden, logits, tokens, *ws, shared_output,
+                                      shared_gate, output, as_stream(stream)),
+                  "prefill MoE step");
+}
+
+}  // extern "C"
+
+// ---- the allocation-free slab step ---------------------------------------
+// The whole-step workspace of a slab of up to Q38M_NOALLOC_MAX_TOKENS
+// tokens, in a file-scope device array: each GPU the library runs on holds
+// its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, so its device address is looked up once per device
+// (with that device current) and only that address is used afterwards.
+static __device__ __align__(256) uint8_t
+    scratch[q38m::prefill_workspace_bytes_v1(Q38M_NOALLOC_MAX_TOKENS)];
+
+namespace {
+
+constexpr int kNoAllocDevices = 64;
+std::once_flag g_scratch_once[kNoAllocDevices];
+void* g_scratch_address[kNoAllocDevices];
+hipError_t g_scratch_status[kNoAllocDevices];
+
+// Device address of `scratch` on `device`, which the caller made current.
+int noalloc_scratch(int device, void** address) {
+    if (device >= kNoAllocDevices)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "allocation-free step: device index above 63");
+    std::call_once(g_scratch_once[device], [device] {
+        g_scratch_status[device] =
+            hipGetSymbolAddress(&g_scratch_address[device], HIP_SYMBOL(scratch));
+    });
+    if (g_scratch_status[device] != hipSuccess)
+        return device_fail(g_scratch_status[device], "hipGetSymbolAddress(scratch)");
+    *address = g_scratch_address[device];
+    return Q38M_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t q38m_moe_prefill_noalloc_scratch_bytes(void) {
+    return q38m::prefill_workspace_bytes_v1(Q38M_NOALLOC_MAX_TOKENS);
+}
+
+int q38m_moe_prefill_noalloc_v1(const q38m_expert_weights_v1* gate_up,
+                                const q38m_expert_weights_v1* down, const uint16_t* hidden,
+                                const float* logits, uint32_t tokens,
+                                const uint16_t* shared_output, const uint16_t* shared_gate,
+                                uint16_t* output, void* stream, int device) {
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (int rc = check_weights(down, false)) return rc;
+    if (tokens == 0 || tokens > Q38M_NOALLOC_MAX_TOKENS)
+        return fail(Q38M_ERR_INVALID_ARGUMENT,
+                    "q38m_moe_prefill_noalloc_v1 takes 1 to 64 tokens (its device-resident "
+                    "workspace holds a 64-token slab); use q38m_moe_prefill_v1 with a "
+                    "caller-owned workspace for more");
+    if (!hidden || !logits || !output || (shared_output == nullptr) != (shared_gate == nullptr) ||
+        !aligned(hidden, 16) || !aligned(logits, 16) || !aligned(output, 16) ||
+        (shared_output && !aligned(shared_output, 16)))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid allocation-free prefill MoE step input");
+    if (int rc = select_device(device)) return rc;
+    void* base = nullptr;
+    if (int rc = noalloc_scratch(device, &base)) return rc;
+    // binding is pointer arithmetic on the device address; nothing is touched
+    q38m_prefill_workspace_v1 ws;
+    if (int rc = q38m_moe_prefill_workspace_bind(base, q38m_moe_prefill_noalloc_scratch_bytes(),
+                                                 Q38M_NOALLOC_MAX_TOKENS, &ws))
+        return rc;
+    return finish(launch_prefill_step(*gate_up, *down, hidden, logits, tokens, ws, shared_output,
+                                      shared_gate, output, as_stream(stream)),
+                  "allocation-free prefill MoE step");
 }
 
 // ---- chunks above the slab ----------------------------------------------

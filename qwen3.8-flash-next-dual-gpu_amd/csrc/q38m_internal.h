@@ -18,11 +18,30 @@ constexpr uint32_t kSlabMaxTokens = Q38M_PREFILL_SLAB_MAX_TOKENS;
 constexpr uint32_t kHidden = Q38M_HIDDEN;
 constexpr uint32_t kInter = Q38M_INTERMEDIATE;
 
-inline uint32_t routes_v1(uint32_t tokens) { return tokens * kTopK; }
-inline uint32_t max_tasks_v1(uint32_t tokens) {
+constexpr uint32_t routes_v1(uint32_t tokens) { return tokens * kTopK; }
+constexpr uint32_t max_tasks_v1(uint32_t tokens) {
     const uint32_t routes = routes_v1(tokens);
     const uint32_t initially = routes < kExperts ? routes : kExperts;
     return initially + (routes - initially) / kMmqM;
+}
+
+// Bytes of the V1 plan image and of the whole-step workspace
+// (q38m_moe_route_plan_bytes_v1 / q38m_moe_prefill_workspace_bytes), as
+// constants for a fixed slab size.
+constexpr size_t align256(size_t v) { return (v + 255u) / 256u * 256u; }
+constexpr size_t plan_bytes_v1(uint32_t tokens) {
+    return 64u + kExperts * 2u + 2u * (kExperts + 1u) * 4u +
+           2u * static_cast<size_t>(routes_v1(tokens)) * 4u +
+           static_cast<size_t>(max_tasks_v1(tokens)) * 8u;
+}
+constexpr size_t prefill_workspace_bytes_v1(uint32_t tokens) {
+    return align256(plan_bytes_v1(tokens)) + 2u * align256(routes_v1(tokens) * 4u) +
+           align256(static_cast<size_t>(tokens) * kHidden) +
+           align256(static_cast<size_t>(tokens) * 4u) +
+           align256(static_cast<size_t>(routes_v1(tokens)) * kInter * 2u) +
+           align256(static_cast<size_t>(routes_v1(tokens)) * kInter) +
+           align256(routes_v1(tokens) * 4u) +
+           align256(static_cast<size_t>(routes_v1(tokens)) * kHidden * 4u);
 }
 
 // chunks above the slab (q38m_wide.hip): 128-row tasks, plans built from
