@@ -894,44 +894,213 @@ def bench_weight_pipeline(q38m, W, torch, reps=5):
     return out
 
 
-def cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, gpu_out, T):
-    """The CPU oracle (this repository's C + OpenMP restatement of the
-    reference's grouped MoE step; the reference ships no CPU path) timed on
-    this host over the same config-2 slab, using the very bytes the GPU
-    used; also checks the GPU output against it."""
-    import numpy as np
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle as orc
-    hg = orc.HostWeights(gu_rm.data.cpu().numpy(), gu_rm.scales.cpu().numpy().view(np.uint16), 4,
-                         32, W.EXPERTS, 2 * W.INTER, W.HIDDEN)
-    hd = orc.HostWeights(dn_rm.data.cpu().numpy(), dn_rm.scales.cpu().numpy().view(np.uint16), 8,
-                         0, W.EXPERTS, W.HIDDEN, W.INTER)
-    h = hidden.cpu().numpy().view(np.uint16)
-    lg = logits.cpu().numpy()
-    times = []
-    result = None
-    for i in range(4):
-        t0 = time.perf_counter()
-        result = orc.moe(h, hg, hd, logits=lg)
-        if i > 0:
-            times.append(time.perf_counter() - t0)
-    median = statistics.median(times)
-    match = bool(np.array_equal(result["output"], gpu_out.cpu().numpy().view(np.uint16)))
-    model = ""
+def _cpu_model():
+    """/proc/cpuinfo's model name with family/model/stepping and the host's
+    logical CPU count."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
+                key, _, value = line.partition(":")
+                key = key.strip()
+                if key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                    fields[key] = value.strip()
     except OSError:
         pass
-    return {"value": round(T / median, 1), "unit": "tok/s", "cores": orc.num_threads(),
+    return (f"{fields.get('model name', '')} (family {fields.get('cpu family', '?')}, model "
+            f"{fields.get('model', '?')}, stepping {fields.get('stepping', '?')}; "
+            f"{os.cpu_count()} logical CPUs)")
+
+
+def cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, gpu_out, T):
+    """The CPU oracle (this repository's C + OpenMP restatement of the
+    reference's grouped MoE step; the reference ships no CPU path) timed on
+    this host, with all OpenMP threads and with one, on the same bytes the
+    GPU uses, checking the GPU outputs against it.
+
+    Headline: the full config-2 slab at all threads (median of 3 after a
+    warm-up).  per_config:
+      config1  64 tokens, all-W4: full, all threads and 1 thread;
+      config2  full slab, all threads and 1 thread;
+      config3  48 decode steps (fresh router draw each) over one layer's
+               weights -- host RAM holds one layer, and 10 random experts of
+               1.14 GB miss every cache either way -- checked against the
+               decode entry point; tokens/s = 1 / (48 steps' time);
+      config4  4,096 Zipf-routed tokens as 8 slabs of 512, all threads; one
+               slab at 1 thread, extrapolated x8 (labelled);
+      config5  one mixed-policy layer over 1 slab and over all 64 slabs of
+               32,768 Zipf(0.8) tokens at all threads, and the 48-layer
+               stack extrapolated as 48 x the 64-slab layer (labelled)."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as orc
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    sh = torch.cuda.current_stream().cuda_stream
+    threads_all = orc.num_threads()
+
+    def host_weights(dev, bits, group, rows, cols):
+        return orc.HostWeights(dev.data.cpu().numpy(), dev.scales.cpu().numpy().view(np.uint16),
+                               bits, group, W.EXPERTS, rows, cols)
+
+    def layer(config, index):
+        spec = W.CONFIGS[config]
+        gfmt, dfmt = W.layer_policy(config, index)
+        gu_tag, dn_tag, _, _ = W.layer_tags(index)
+        g = q38m.synth_weights(spec["seed"], gu_tag, fmt[gfmt[1]], gfmt[2], W.EXPERTS,
+                               2 * W.INTER, W.HIDDEN, gfmt[3])
+        d = q38m.synth_weights(spec["seed"], dn_tag, fmt[dfmt[1]], dfmt[2], W.EXPERTS, W.HIDDEN,
+                               W.INTER, dfmt[3])
+        hosts = (host_weights(g, gfmt[1], gfmt[2], 2 * W.INTER, W.HIDDEN),
+                 host_weights(d, dfmt[1], dfmt[2], W.HIDDEN, W.INTER))
+        return (q38m.repack(g, paired=True), q38m.repack(d)), hosts
+
+    def inputs(config, index, tokens):
+        spec = W.CONFIGS[config]
+        _, _, h_tag, l_tag = W.layer_tags(index)
+        h = torch.empty(tokens, W.HIDDEN, dtype=torch.int16, device="cuda")
+        lg = torch.empty(tokens, W.EXPERTS, dtype=torch.float32, device="cuda")
+        bias = W.bias_for(config, index)
+        b = None if bias is None else torch.tensor(bias, dtype=torch.float32, device="cuda")
+        q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, spec["seed"], h_tag, h.numel(), h)
+        q38m.synth_fill(q38m.SYNTH_NORMAL_F32, spec["seed"], l_tag, lg.numel(), lg, bias=b)
+        return h, lg
+
+    def gpu_slabs(devs, h, lg):
+        out = torch.empty_like(h)
+        tokens = h.shape[0]
+        ws = q38m.PrefillWorkspace_(min(tokens, 512))
+        for first in range(0, tokens, 512):
+            n = min(512, tokens - first)
+            q38m.call("q38m_moe_prefill_v1", ctypes.byref(devs[0].desc),
+                      ctypes.byref(devs[1].desc), h[first].data_ptr(), lg[first].data_ptr(), n,
+                      ctypes.byref(ws.ws), None, None, out[first].data_ptr(), sh, 0)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.uint16)
+
+    def run_slabs(hosts, h, lg):
+        outs = [orc.moe(h[f:f + 512], hosts[0], hosts[1], logits=lg[f:f + 512])["output"]
+                for f in range(0, h.shape[0], 512)]
+        return np.concatenate(outs)
+
+    def timed(fn, reps, warm=True):
+        if warm:
+            fn()
+        times, result = [], None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            result = fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), result
+
+    def at_threads(n, fn):
+        orc.set_threads(n)
+        try:
+            return fn()
+        finally:
+            orc.set_threads(threads_all)
+
+    per = {}
+    # config 2 (the headline), the bytes the GPU just used
+    hg = host_weights(gu_rm, 4, 32, 2 * W.INTER, W.HIDDEN)
+    hd = host_weights(dn_rm, 8, 0, W.HIDDEN, W.INTER)
+    h2, l2 = hidden.cpu().numpy().view(np.uint16), logits.cpu().numpy()
+    t_all, res = timed(lambda: orc.moe(h2, hg, hd, logits=l2), 3)
+    match2 = bool(np.array_equal(res["output"], gpu_out.cpu().numpy().view(np.uint16)))
+    t_one, _ = at_threads(1, lambda: timed(lambda: orc.moe(h2, hg, hd, logits=l2), 1))
+    per["config2"] = {"tokens": T, "threads_all": {"tok_per_s": round(T / t_all, 1),
+                                                   "seconds": round(t_all, 4)},
+                      "threads_1": {"tok_per_s": round(T / t_one, 1), "seconds": round(t_one, 3)},
+                      "gpu_matches_cpu_bitwise": match2}
+    del hg, hd
+
+    # config 1: 64 tokens, all-W4
+    devs, hosts = layer(1, 0)
+    h, lg = inputs(1, 0, 64)
+    hh, ll = h.cpu().numpy().view(np.uint16), lg.cpu().numpy()
+    t_all, res = timed(lambda: orc.moe(hh, hosts[0], hosts[1], logits=ll), 3)
+    t_one, _ = at_threads(1, lambda: timed(lambda: orc.moe(hh, hosts[0], hosts[1], logits=ll), 1))
+    per["config1"] = {"tokens": 64, "threads_all": {"tok_per_s": round(64 / t_all, 1),
+                                                    "seconds": round(t_all, 4)},
+                      "threads_1": {"tok_per_s": round(64 / t_one, 1), "seconds": round(t_one, 4)},
+                      "gpu_matches_cpu_bitwise": bool(np.array_equal(
+                          res["output"], gpu_slabs(devs, h, lg)))}
+    del devs, hosts
+
+    # config 3: 48 decode steps over one layer's weights, fresh draws
+    devs, hosts = layer(3, 0)
+    spec = W.CONFIGS[3]
+    hs = torch.empty(48, W.HIDDEN, dtype=torch.int16, device="cuda")
+    ls = torch.empty(48, W.EXPERTS, dtype=torch.float32, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, spec["seed"], 4001, hs.numel(), hs)
+    q38m.synth_fill(q38m.SYNTH_NORMAL_F32, spec["seed"], 4002, ls.numel(), ls)
+    hh, ll = hs.cpu().numpy().view(np.uint16), ls.cpu().numpy()
+
+    def decode_all():
+        return np.stack([orc.moe(hh[i:i + 1], hosts[0], hosts[1], logits=ll[i:i + 1])["output"][0]
+                         for i in range(48)])
+    t_all, res = timed(decode_all, 1)
+    t_one, _ = at_threads(1, lambda: timed(decode_all, 1, warm=False))
+    scratch = torch.zeros(q38m.lib().q38m_moe_decode_scratch_bytes() // 2 + 64, dtype=torch.int16,
+                          device="cuda")
+    dec = torch.empty(48, W.HIDDEN, dtype=torch.int16, device="cuda")
+    for i in range(48):
+        q38m.call("q38m_moe_decode_v1", ctypes.byref(devs[0].desc), ctypes.byref(devs[1].desc),
+                  hs[i].data_ptr(), ls[i].data_ptr(), 10, None, None, None, scratch.data_ptr(),
+                  dec[i].data_ptr(), sh, 0)
+    torch.cuda.synchronize()
+    per["config3"] = {"sample": "48 decode steps (one token, fresh router draw each) over one "
+                                "layer's weights held in host RAM",
+                      "threads_all": {"tok_per_s": round(1 / t_all, 2),
+                                      "us_per_layer": round(t_all / 48 * 1e6, 1)},
+                      "threads_1": {"tok_per_s": round(1 / t_one, 2),
+                                    "us_per_layer": round(t_one / 48 * 1e6, 1)},
+                      "gpu_matches_cpu_bitwise": bool(np.array_equal(
+                          res, dec.cpu().numpy().view(np.uint16)))}
+    del devs, hosts
+
+    # config 4: 4096 Zipf-routed tokens in slabs of 512
+    devs, hosts = layer(4, 0)
+    h, lg = inputs(4, 0, 4096)
+    hh, ll = h.cpu().numpy().view(np.uint16), lg.cpu().numpy()
+    t_all, res = timed(lambda: run_slabs(hosts, hh, ll), 1)
+    t_slab, _ = at_threads(1, lambda: timed(lambda: orc.moe(hh[:512], hosts[0], hosts[1],
+                                                            logits=ll[:512]), 1, warm=False))
+    per["config4"] = {"tokens": 4096, "threads_all": {"tok_per_s": round(4096 / t_all, 1),
+                                                      "seconds": round(t_all, 3)},
+                      "threads_1_extrapolated": {
+                          "tok_per_s": round(512 / t_slab, 1),
+                          "seconds": round(8 * t_slab, 2),
+                          "sample": "first 512-token slab at 1 thread, x8 (extrapolation)"},
+                      "gpu_matches_cpu_bitwise": bool(np.array_equal(res,
+                                                                     gpu_slabs(devs, h, lg)))}
+    del devs, hosts
+
+    # config 5: one mixed-policy layer over 1 and 64 slabs; the stack by extrapolation
+    devs, hosts = layer(5, 1)
+    h, lg = inputs(5, 1, 32768)
+    hh, ll = h.cpu().numpy().view(np.uint16), lg.cpu().numpy()
+    t_slab, res1 = timed(lambda: orc.moe(hh[:512], hosts[0], hosts[1], logits=ll[:512]), 1)
+    t_layer, _ = timed(lambda: run_slabs(hosts, hh, ll), 1, warm=False)
+    per["config5"] = {"layer": "layer 1 (W4 g32 gate/up + W8 down), Zipf 0.8",
+                      "threads_all": {
+                          "one_slab_seconds": round(t_slab, 4),
+                          "layer_64_slabs_seconds": round(t_layer, 2),
+                          "layer_tok_per_s": round(32768 / t_layer, 1),
+                          "stack_48_layers_seconds_extrapolated": round(48 * t_layer, 1),
+                          "stack_tok_per_s_extrapolated": round(32768 / (48 * t_layer), 1)},
+                      "extrapolation": "48 x the measured 64-slab layer (both policies cost "
+                                       "alike per route on the CPU)",
+                      "gpu_matches_cpu_bitwise_first_slab": bool(np.array_equal(
+                          res1["output"], gpu_slabs(devs, h[:512], lg[:512])))}
+    del devs, hosts
+
+    t2 = per["config2"]["threads_all"]["seconds"]
+    return {"value": round(T / t2, 1), "unit": "tok/s", "cores": threads_all,
             "kind": "port",
             "sample": f"full config-2 slab ({T} tokens x 10 routes), median of 3 after 1 "
                       f"warm-up, gcc -O3 -fopenmp restatement in oracle/",
-            "seconds_per_slab": round(median, 4), "cpu_model": model,
-            "gpu_matches_cpu_bitwise": match}
+            "seconds_per_slab": t2, "cpu_model": _cpu_model(),
+            "gpu_matches_cpu_bitwise": match2, "per_config": per}
 
 
 if __name__ == "__main__":
