@@ -230,242 +230,229 @@ struct TileQuad {
     uint2 s;  // its scale words (4, 2 or 1 groups; load_quad_scales)
 };
 
-// Gate/up over a task of up to 128 rows.  A workgroup of 16 waves covers 8
-// gate/up tile pairs: waves 0-7 run the gate tiles, waves 8-15 the matching
-// up tiles, so each wave holds one tile's accumulators (32 VGPRs at 128
-// rows) and four waves fit on a SIMD.  Each wave runs the group chain (per
-// group one v_mfma_i32_16x16x32_i8 from a zero accumulator, then
-// y16 = fma(16*acc, s_g, y16) in group order for fp16 scales) for kTiles 16-row tiles
-// against the same unpacked weight fragment; kTiles (8, 4, 2 or 1) is
-// picked per task from its row count, so the tile loop has no branches.
-// Groups of 64 or 128 columns (kSub = 2 or 4 sub-blocks of 32): the
-// sub-blocks before a group's last chain every tile's int32 accumulator
-// through the MFMA C input, and the last one runs the pinned MFMA/fma
-// interleave from those accumulators.
-// Within a group, tile t+1's MFMA is issued before tile t's v_cvt/v_fma
-// chain, and an empty asm on each tile's accumulators keeps that order (the
-// compiler would otherwise issue every MFMA first and spill their results).
-// A is staged one quad (128 K) at a time into a double-buffered LDS image
-// [group][row tile][lane] of 8-byte MFMA fragments, the next quad loaded
-// into registers while the current one is multiplied, and a group's
-// fragments read from LDS while the previous group computes; weights run
-// two quads ahead.  The gate waves hand their y16 to the up waves through
-// LDS for the SwiGLU epilogue.
-template <uint32_t H, uint32_t I, uint32_t kThreads, uint32_t kTiles, uint32_t kSub, bool kBf16>
-__device__ __forceinline__ void gate_up_wide_rows(
-    const uint4* __restrict__ wbase, const uint16_t* __restrict__ sbase,
-    const int8_t* __restrict__ xq, const float* __restrict__ xs,
-    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
-    uint16_t* __restrict__ mid, uint2 (*a_lds)[4u * kRowTiles * 64u], float* gate_lds,
-    uint32_t rows, uint32_t p0, uint32_t pair, bool up) {
+// Gate/up, W4, over a task of up to 128 rows.  A workgroup of 16 waves
+// covers 8 gate/up channel pairs (16 channels each) of one task; wave w
+// owns pair w % 8 for rows 64 (w / 8) .. +63 (up to 4 row tiles of 16) and
+// runs both the pair's gate tile and its up tile, so each A fragment feeds
+// two MFMAs and the SwiGLU epilogue stays in registers.
+//
+// Per quad (128 columns of K) the workgroup stages into LDS the task's 128
+// int8 rows (16 KB), its 16 weight tiles (16 KB) and their scale words;
+// every thread moves one 16-byte row piece, one 16-byte weight piece and
+// one 4-byte scale piece.  Those loads are issued two quads ahead into two
+// register sets and stored one quad ahead into a double-buffered image, and
+// the barrier between quads waits only for LDS operations, so the global
+// loads of later quads stay in flight across it (a full workgroup fence
+// would wait for them).
+//
+// Arithmetic per scale group and tile: kSub v_mfma_i32_16x16x32_i8 chained
+// through the accumulator, started from the bits of 1.5 * 2^23 so that the
+// result read as a float is 12582912 + acc exactly (|acc| < 2^22); one
+// v_add_f32 recovers (float)acc and one v_fma_f32 continues the group chain
+// -- the contract's y = fmaf((float)acc_g, s_g, y) in group order.  The
+// next tile's MFMAs are issued before this tile's fp32 step.  The W4
+// nibbles sit in the high half of each int8 (16 * w); fp16 scales run the
+// chain on 16 * y, bf16 scales take s / 16.  Per-row token scale and route
+// weight are staged in LDS once for the epilogue.
+template <uint32_t H, uint32_t I, uint32_t kSub, bool kBf16>
+__global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4)))
+void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+                            const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                            const uint32_t* __restrict__ packed,
+                            const float* __restrict__ route_weights,
+                            const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kTilesAll = 2u * I / 16u;
-    constexpr uint32_t kQuadWords = kTilesAll * 64u;
-    constexpr uint32_t kQuadScales = kTilesAll * 16u;
-    constexpr uint32_t kRowScales = 4u / kSub;       // scale words per row per quad
-    constexpr uint32_t kPieces = kTiles * 16u * 8u;  // 16-byte row pieces per quad
-    constexpr uint32_t kPerThread = (kPieces + kThreads - 1u) / kThreads;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t n = lane & 15u;
-    const uint32_t q = lane >> 4;
-    const uint32_t wave_in_half = (threadIdx.x >> 6) & 7u;
-
-    auto load = [&](uint32_t kq) {
-        const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
-        return TileQuad{wbase[k * kQuadWords + lane],
-                        load_quad_scales<kSub, false>(sbase + (k * kQuadScales + n) * kRowScales)};
-    };
-
-    // Piece i: row r = i/8, 16-byte piece c = i%8 of the row's 128 bytes of
-    // the quad, i.e. group c/2, lane groups 2(c%2) and 2(c%2)+1.  Rows past
-    // valid_rows stage zeros.
-    const uint4* row_src[kPerThread];
-    uint32_t lds_at[kPerThread];
-    bool alive[kPerThread], staged[kPerThread];
-#pragma unroll
-    for (uint32_t u = 0; u < kPerThread; ++u) {
-        const uint32_t i = threadIdx.x + u * kThreads;
-        const uint32_t r = i / 8u, c = i % 8u;
-        staged[u] = i < kPieces;
-        alive[u] = staged[u] && r < rows;
-        const uint32_t token = alive[u] ? packed[p0 + r] / kTopK : 0u;
-        row_src[u] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token) * H) + c;
-        lds_at[u] = ((c >> 1) * kRowTiles + r / 16u) * 64u + (c & 1u) * 32u + r % 16u;
-    }
-    uint4 pieces[kPerThread];
-    auto load_a = [&](uint32_t kq) {
-#pragma unroll
-        for (uint32_t u = 0; u < kPerThread; ++u)
-            pieces[u] = alive[u] ? row_src[u][kq * 8u] : make_uint4(0u, 0u, 0u, 0u);
-    };
-    auto store_a = [&](uint32_t buffer) {
-#pragma unroll
-        for (uint32_t u = 0; u < kPerThread; ++u) {
-            if (!staged[u]) continue;
-            a_lds[buffer][lds_at[u]] = make_uint2(pieces[u].x, pieces[u].y);
-            a_lds[buffer][lds_at[u] + 16u] = make_uint2(pieces[u].z, pieces[u].w);
-        }
-    };
-
-    float y[kTiles][4];
-#pragma unroll
-    for (uint32_t t = 0; t < kTiles; ++t)
-#pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) y[t][i] = 0.0f;
-
-    auto multiply = [&](uint32_t kq, const TileQuad& b) {
-        const uint2* abuf = a_lds[kq & 1u] + lane;
-        const v4i zero = {0, 0, 0, 0};
-        const uint32_t ww[4] = {b.w.x, b.w.y, b.w.z, b.w.w};
-        long frag[2][kTiles];
-        v4i chain[kTiles];  // kSub > 1: the group's running int32 tiles
-#pragma unroll
-        for (uint32_t t = 0; t < kTiles; ++t) frag[0][t] = as_long(abuf[t * 64u]);
-#pragma unroll
-        for (uint32_t j = 0; j < 4u; ++j) {
-            if (j + 1u < 4u) {
-#pragma unroll
-                for (uint32_t t = 0; t < kTiles; ++t)
-                    frag[(j + 1u) & 1u][t] = as_long(abuf[((j + 1u) * kRowTiles + t) * 64u]);
-            }
-            const long* a = frag[j & 1u];
-            const long bj = unpack_w4x16(ww[j]);
-            if (j % kSub != kSub - 1u) {
-#pragma unroll
-                for (uint32_t t = 0; t < kTiles; ++t)
-                    chain[t] = mfma_i8_16x16x32(a[t], bj, j % kSub == 0u ? zero : chain[t]);
-                continue;
-            }
-            const uint32_t word = quad_scale_word(b.s, j / kSub);
-            // fp16: y16 = 16*y exactly (partial sums are multiples of 2^-24,
-            // far from the subnormal range).  bf16 words can sit near it, so
-            // they take s/16 (exact) and the chain holds y itself.
-            const float scale = kBf16 ? bf16_to_f32(word) * 0.0625f : f16_to_f32(word);
-            // the group's int32 tile t: d[t & 1] (kSub == 1) or chain[t] in place
-            v4i d[2];
-            auto issue = [&](uint32_t t) {
-                if constexpr (kSub == 1u) d[t & 1u] = mfma_i8_16x16x32(a[t], bj, zero);
-                else chain[t] = mfma_i8_16x16x32(a[t], bj, chain[t]);
-            };
-            auto tile = [&](uint32_t t) -> const v4i& {
-                if constexpr (kSub == 1u) return d[t & 1u];
-                else return chain[t];
-            };
-            issue(0);
-#pragma unroll
-            for (uint32_t t = 0; t < kTiles; ++t) {
-                if (t + 1u < kTiles) issue(t + 1u);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    y[t][i] = __builtin_fmaf(static_cast<float>(tile(t)[i]), scale, y[t][i]);
-                asm volatile("" : "+v"(y[t][0]), "+v"(y[t][1]), "+v"(y[t][2]), "+v"(y[t][3]));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-    };
-    // one quad: weights two ahead into the set just consumed, A one ahead
-    auto step = [&](uint32_t kq, const TileQuad& cur, TileQuad& refill) {
-        refill = load(kq + 2u);
-        if (kq + 1u < kQuads) load_a(kq + 1u);
-        __builtin_amdgcn_sched_barrier(0);
-        multiply(kq, cur);
-        if (kq + 1u < kQuads) store_a((kq + 1u) & 1u);
-        __syncthreads();
-    };
-
-    load_a(0);
-    TileQuad r0 = load(0), r1 = load(1), r2;
-    store_a(0);
-    __syncthreads();
-    static_assert(kQuads % 3u == 1u, "three-set rotation plus one peeled quad");
-#pragma unroll 1
-    for (uint32_t kq = 0; kq + 3u < kQuads; kq += 3u) {
-        step(kq, r0, r2);
-        step(kq + 1u, r1, r0);
-        step(kq + 2u, r2, r1);
-    }
-    multiply(kQuads - 1u, r0);
-
-    // gate waves hand y16 over: gate_lds[pair in workgroup][row][channel],
-    // over the A image, once every wave has finished reading it
-    float* handoff = gate_lds + wave_in_half * (kWideRows * 16u);
-    __syncthreads();
-    if (!up) {
-#pragma unroll
-        for (uint32_t t = 0; t < kTiles; ++t)
-#pragma unroll
-            for (uint32_t i = 0; i < 4u; ++i) handoff[(16u * t + 4u * q + i) * 16u + n] = y[t][i];
-    }
-    __syncthreads();
-    if (!up) return;
-    const uint32_t channel = pair * 16u + n;
-#pragma unroll
-    for (uint32_t t = 0; t < kTiles; ++t) {
-#pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) {
-            const uint32_t r = 16u * t + 4u * q + i;
-            if (r >= rows) continue;
-            const uint32_t p = p0 + r;
-            const uint32_t a = packed[p];
-            const float st = xs[a / kTopK];
-            const float unscale = kBf16 ? 1.0f : 0.0625f;
-            const float y_gate = (handoff[r * 16u + n] * unscale) * st;
-            const float y_up = (y[t][i] * unscale) * st;
-            mid[static_cast<size_t>(p) * I + channel] =
-                static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
-        }
-    }
-}
-
-template <uint32_t H, uint32_t I, uint32_t kPairs, uint32_t kSub, bool kBf16>
-__global__ __launch_bounds__(kPairs * 128) __attribute__((amdgpu_waves_per_eu(4)))
-void gate_up_w4_wide_kernel(
-    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
-    const int8_t* __restrict__ xq, const float* __restrict__ xs,
-    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
-    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
-    constexpr uint32_t kQuads = H / 128u;
-    constexpr uint32_t kTilesAll = 2u * I / 16u;
-    constexpr uint32_t kThreads = kPairs * 128u;
-    // the A image (two quads) and, after the K loop, the gate hand-off
-    constexpr uint32_t kABytes = 2u * 4u * kRowTiles * 64u * 8u;
-    constexpr uint32_t kHandoffBytes = kPairs * kWideRows * 16u * 4u;
-    __shared__ __align__(16) uint8_t lds[kABytes > kHandoffBytes ? kABytes : kHandoffBytes];
-    auto a_lds = reinterpret_cast<uint2 (*)[4u * kRowTiles * 64u]>(lds);
-    float* gate_lds = reinterpret_cast<float*>(lds);
+    constexpr uint32_t kRowScales = 4u / kSub;                           // words per row per quad
+    constexpr uint32_t kGroups = 4u / kSub;                              // scale groups per quad
+    constexpr uint32_t kScalePieces = 16u * 16u * kRowScales * 2u / 4u;  // 4-byte pieces per quad
+    static_assert(kQuads % 2u == 0u, "two staging register sets");
+    static_assert(kScalePieces <= 1024u, "one scale piece per thread");
+    // per buffer: A [sub-block j][row tile][lane] 8-byte MFMA fragments, the
+    // workgroup's 16 weight tiles [tile][lane] and their scale words
+    __shared__ __align__(16) uint2 a_lds[2][4u * kRowTiles * 64u];
+    __shared__ __align__(16) uint4 w_lds[2][16u * 64u];
+    __shared__ __align__(16) uint32_t s_lds[2][kScalePieces];
+    __shared__ float2 row_info[kWideRows];  // (token scale, route weight)
 
     const q38m_task_v1 task = tasks[blockIdx.y];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const bool up = wave >= kPairs;
-    const uint32_t pair = blockIdx.x * kPairs + (wave % kPairs);
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t rh = wave >> 3;
+    const uint32_t pr = wave & 7u;
+    const uint32_t n = lane & 15u, qh = lane >> 4;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
-    // Paired quad-major layout: for quad kq the gate tile of pair p is slot
-    // 2p and its up tile slot 2p+1.
-    const uint32_t slot = 2u * pair + (up ? 1u : 0u);
-    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTilesAll + slot) * 64u;
-    const uint16_t* sbase =
-        s + (static_cast<size_t>(e) * kQuads * kTilesAll + slot) * 16u * (4u / kSub);
-    const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
-    if (tiles > 4u)
-        gate_up_wide_rows<H, I, kThreads, 8, kSub, kBf16>(wbase, sbase, xq, xs, packed,
-                                                           route_weights, mid, a_lds, gate_lds,
-                                                           rows, p0, pair, up);
-    else if (tiles > 2u)
-        gate_up_wide_rows<H, I, kThreads, 4, kSub, kBf16>(wbase, sbase, xq, xs, packed,
-                                                           route_weights, mid, a_lds, gate_lds,
-                                                           rows, p0, pair, up);
-    else if (tiles == 2u)
-        gate_up_wide_rows<H, I, kThreads, 2, kSub, kBf16>(wbase, sbase, xq, xs, packed,
-                                                           route_weights, mid, a_lds, gate_lds,
-                                                           rows, p0, pair, up);
-    else
-        gate_up_wide_rows<H, I, kThreads, 1, kSub, kBf16>(wbase, sbase, xq, xs, packed,
-                                                           route_weights, mid, a_lds, gate_lds,
-                                                           rows, p0, pair, up);
+    const int here = static_cast<int>(rows) - static_cast<int>(64u * rh);
+    const uint32_t nt = here <= 0 ? 0u
+                                  : (here >= 64 ? 4u : (static_cast<uint32_t>(here) + 15u) / 16u);
+
+    // staging: row piece (row tid/8, 16-byte chunk tid%8), weight piece
+    // (slot tid/64 of the workgroup's 16, lane tid%64), scale piece tid
+    const uint32_t sr = tid >> 3, sch = tid & 7u;
+    const bool alive = sr < rows;
+    const uint32_t assignment = alive ? packed[p0 + sr] : 0u;
+    if (sch == 0u && alive)
+        row_info[sr] = make_float2(xs[assignment / kTopK], route_weights[assignment]);
+    const uint4* a_src =
+        reinterpret_cast<const uint4*>(xq + static_cast<size_t>(assignment / kTopK) * H) + sch;
+    const uint32_t a_at = ((sch >> 1) * kRowTiles + (sr >> 4)) * 64u + (sch & 1u) * 32u + (sr & 15u);
+    const size_t slot0 = static_cast<size_t>(e) * kQuads * kTilesAll + blockIdx.x * 16u;
+    const uint4* w_src = w + slot0 * 64u + tid;
+    const uint32_t* s_src = reinterpret_cast<const uint32_t*>(s) + slot0 * 16u * kRowScales / 2u + tid;
+    const bool s_thread = tid < kScalePieces;
+    struct Stage {
+        uint4 a, w;
+        uint32_t s;
+    };
+    auto load_stage = [&](uint32_t kq) {
+        Stage st;
+        st.a = alive ? a_src[kq * 8u] : make_uint4(0u, 0u, 0u, 0u);
+        st.w = w_src[static_cast<size_t>(kq) * kTilesAll * 64u];
+        st.s = s_thread ? s_src[static_cast<size_t>(kq) * kTilesAll * 16u * kRowScales / 2u] : 0u;
+        return st;
+    };
+    auto store_stage = [&](const Stage& st, uint32_t buffer) {
+        a_lds[buffer][a_at] = make_uint2(st.a.x, st.a.y);
+        a_lds[buffer][a_at + 16u] = make_uint2(st.a.z, st.a.w);
+        w_lds[buffer][tid] = st.w;
+        if (s_thread) s_lds[buffer][tid] = st.s;
+    };
+
+    float y[4][2][4];
+#pragma unroll
+    for (uint32_t t = 0; t < 4u; ++t)
+#pragma unroll
+        for (uint32_t u = 0; u < 2u; ++u)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) y[t][u][i] = 0.0f;
+    v4i bias;
+    bias.x = bias.y = bias.z = bias.w = 0x4B400000;
+    float unbias;  // -12582912.0f in a scalar register (no literal per use)
+    asm volatile("s_mov_b32 %0, 0xcb400000" : "=s"(unbias));
+
+    // One quad for kNt row tiles.  Chain k = (scale group gg, row tile t,
+    // gate/up u); the A fragments of (gg, t) are read one set ahead and a
+    // group's B fragments are unpacked once for all row tiles.
+    auto multiply = [&](auto tiles, uint32_t buffer) __attribute__((always_inline)) {
+        constexpr uint32_t kNt = decltype(tiles)::value;
+        constexpr uint32_t kSets = kGroups * kNt;
+        constexpr uint32_t kChains = kSets * 2u;
+        const uint2* abuf = a_lds[buffer] + lane;
+        const uint4 gq = w_lds[buffer][(2u * pr) * 64u + lane];
+        const uint4 uq = w_lds[buffer][(2u * pr + 1u) * 64u + lane];
+        const uint16_t* sbase = reinterpret_cast<const uint16_t*>(s_lds[buffer]);
+        const uint2 gs = load_quad_scales<kSub, false>(sbase + ((2u * pr) * 16u + n) * kRowScales);
+        const uint2 us =
+            load_quad_scales<kSub, false>(sbase + ((2u * pr + 1u) * 16u + n) * kRowScales);
+        const uint32_t gw[4] = {gq.x, gq.y, gq.z, gq.w};
+        const uint32_t uw[4] = {uq.x, uq.y, uq.z, uq.w};
+        float sc[2][kGroups];
+#pragma unroll
+        for (uint32_t gg = 0; gg < kGroups; ++gg) {
+#pragma unroll
+            for (uint32_t u = 0; u < 2u; ++u) {
+                const uint32_t word = quad_scale_word(u ? us : gs, gg);
+                sc[u][gg] = kBf16 ? bf16_to_f32(word) * 0.0625f : f16_to_f32(word);
+                asm volatile("" : "+v"(sc[u][gg]));  // a plain v_fma_f32, not v_fma_mix
+            }
+        }
+        long fa[2][kSub];
+        auto read_set = [&](uint32_t m) {
+            const uint32_t gg = m / kNt, t = m % kNt;
+#pragma unroll
+            for (uint32_t sb = 0; sb < kSub; ++sb)
+                fa[m & 1u][sb] = as_long(abuf[((gg * kSub + sb) * kRowTiles + 4u * rh + t) * 64u]);
+        };
+        long bf[2][kSub];
+        v4i d[2];
+        auto issue = [&](uint32_t k) {
+            const uint32_t m = k / 2u, u = k & 1u;
+            const uint32_t gg = m / kNt, t = m % kNt;
+            if (u == 0u) {
+                if (m + 1u < kSets) read_set(m + 1u);
+                if (t == 0u) {
+#pragma unroll
+                    for (uint32_t sb = 0; sb < kSub; ++sb) {
+                        bf[0][sb] = unpack_w4x16(gw[gg * kSub + sb]);
+                        bf[1][sb] = unpack_w4x16(uw[gg * kSub + sb]);
+                    }
+                }
+            }
+            v4i acc = bias;
+#pragma unroll
+            for (uint32_t sb = 0; sb < kSub; ++sb)
+                acc = mfma_i8_16x16x32(fa[m & 1u][sb], bf[u][sb], acc);
+            d[k & 1u] = acc;
+        };
+        auto step = [&](uint32_t k) {
+            const uint32_t m = k / 2u, u = k & 1u;
+            const uint32_t gg = m / kNt, t = m % kNt;
+            const float scale = sc[u][gg];
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i)
+                y[t][u][i] =
+                    __builtin_fmaf(__int_as_float(d[k & 1u][i]) + unbias, scale, y[t][u][i]);
+        };
+        read_set(0);
+#pragma unroll
+        for (uint32_t k = 0; k <= kChains; ++k) {
+            if (k < kChains) issue(k);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k > 0u) step(k - 1u);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto compute = [&](uint32_t buffer) __attribute__((always_inline)) {
+        // three row tiles run as four and one as two (the extra rows are zero)
+        if (nt > 2u)
+            multiply(std::integral_constant<uint32_t, 4>{}, buffer);
+        else if (nt > 0u)
+            multiply(std::integral_constant<uint32_t, 2>{}, buffer);
+    };
+    // barrier over LDS only: this wave's LDS operations are complete, its
+    // global loads (the staging of later quads) stay in flight
+    auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    // quad q: loaded at the start of quad q-2 into register set q%2, stored
+    // at the end of quad q-1 into LDS buffer q%2, multiplied during quad q
+    Stage set0 = load_stage(0), set1 = load_stage(1);
+    store_stage(set0, 0u);
+    __syncthreads();
+#pragma unroll 1
+    for (uint32_t kq = 0; kq < kQuads; kq += 2u) {
+        if (kq + 2u < kQuads) set0 = load_stage(kq + 2u);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0u);
+        store_stage(set1, 1u);
+        lds_barrier();
+        if (kq + 3u < kQuads) set1 = load_stage(kq + 3u);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(1u);
+        if (kq + 2u < kQuads) store_stage(set0, 0u);
+        lds_barrier();
+    }
+
+    // SwiGLU: D lane (qh, n) holds rows 4qh + i of each tile, channel n
+    const uint32_t channel = (blockIdx.x * 8u + pr) * 16u + n;
+    const float unscale = kBf16 ? 1.0f : 0.0625f;
+#pragma unroll
+    for (uint32_t t = 0; t < 4u; ++t) {
+        if (t >= nt) break;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 64u * rh + 16u * t + 4u * qh + i;
+            if (r >= rows) continue;
+            const float2 info = row_info[r];
+            const float yg = (y[t][0][i] * unscale) * info.x;
+            const float yu = (y[t][1][i] * unscale) * info.x;
+            mid[static_cast<size_t>(p0 + r) * I + channel] =
+                static_cast<uint16_t>(swiglu_fold(yg, yu, info.y));
+        }
+    }
 }
 
 // Gate/up, W8 (paired K-block-major layout; the reference's edge-layer
@@ -1054,12 +1041,12 @@ void launch_gate_up_wide_sub(const q38m_expert_weights_v1& w, const int8_t* xq, 
                              const uint32_t* packed, const float* route_weights,
                              const q38m_task_v1* tasks, uint32_t task_count,
                              uint16_t* weighted_mid, hipStream_t stream) {
-    constexpr uint32_t kPairs = 8;
-    const dim3 grid(kInter / 16u / kPairs, task_count);
-    gate_up_w4_wide_kernel<kHidden, kInter, kPairs, kSub, kBf16>
-        <<<grid, kPairs * 128u, 0, stream>>>(static_cast<const uint4*>(w.data),
-                                             static_cast<const uint16_t*>(w.scales), xq, xs,
-                                             packed, route_weights, tasks, weighted_mid);
+    // 8 channel pairs (256 rows of gate/up) per workgroup
+    const dim3 grid(kInter / 16u / 8u, task_count);
+    gate_up_w4_wide_kernel<kHidden, kInter, kSub, kBf16>
+        <<<grid, 1024, 0, stream>>>(static_cast<const uint4*>(w.data),
+                                    static_cast<const uint16_t*>(w.scales), xq, xs, packed,
+                                    route_weights, tasks, weighted_mid);
 }
 
 // Per channel: four tiles per wave (the tuned BASELINE shape).  Grouped:
