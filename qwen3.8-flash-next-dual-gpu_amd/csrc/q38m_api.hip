@@ -618,13 +618,15 @@ int q38m_moe_prefill_wide_v1(const q38m_expert_weights_v1* gate_up,
                                               wide->plan_scratch, s);
     if (status == hipSuccess)
         status = q38m::launch_gate_up_wide(*gate_up, ws->xq, ws->xs, ws->plan.packed_assignment,
-                                           ws->expert_weights, ws->plan.tasks, tasks,
+                                           ws->expert_weights, ws->plan.tasks,
+                                           &ws->plan.header->task_count, tasks,
                                            ws->weighted_mid, s);
     if (status == hipSuccess)
         status = q38m::launch_quantize_rows(ws->weighted_mid, routes, Q38M_INTERMEDIATE,
                                             ws->mid_q, ws->mid_s, s);
     if (status == hipSuccess)
-        status = q38m::launch_down_wide(*down, ws->mid_q, ws->mid_s, ws->plan.tasks, tasks,
+        status = q38m::launch_down_wide(*down, ws->mid_q, ws->mid_s, ws->plan.tasks,
+                                        &ws->plan.header->task_count, tasks,
                                         ws->route_output, s);
     if (status == hipSuccess)
         status = q38m::launch_combine(ws->route_output, ws->plan.assignment_to_packed,

@@ -38,16 +38,22 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h) {
     return __uint_as_float(h << 16);
 }
 
-// Round-to-nearest-even bf16 (tools/q38_artifact_compiler.py:61-66).
+// Round-to-nearest-even bf16 (tools/q38_artifact_compiler.py:61-66); a NaN
+// keeps its sign and top payload bits with the quiet bit set.  Both results
+// are formed and one selected, so the conversion runs without branches.
 __device__ __forceinline__ uint32_t f32_to_bf16(float v) {
-    uint32_t b = __float_as_uint(v);
-    if ((b & 0x7fffffffu) > 0x7f800000u) return (b >> 16) | 0x40u;
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return b >> 16;
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t rounded = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (b >> 16) | 0x40u;
+    return v != v ? quiet : rounded;
 }
 
+// the same rounding, the result widened back to fp32
 __device__ __forceinline__ float bf16_round(float v) {
-    return bf16_to_f32(f32_to_bf16(v));
+    const uint32_t b = __float_as_uint(v);
+    const uint32_t rounded = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
+    const uint32_t quiet = (b & 0xffff0000u) | 0x00400000u;
+    return __uint_as_float(v != v ? quiet : rounded);
 }
 
 // Exact binary16 -> binary32 through the hardware conversion.
@@ -82,13 +88,13 @@ __device__ __forceinline__ uint32_t f32_to_f16(float v) {
 // ---- the contract's exp ---------------------------------------------------
 // Cody & Waite reduction x = n*ln2 + r (ln2 split so n*ln2_hi is exact),
 // degree-7 Taylor polynomial of e^r in Horner form, exact 2^n scaling.
-// Results below the smallest normal are flushed to 0 (x < -87.3).
+// Results below the smallest normal are flushed to 0 (x < -87.3).  The
+// body runs on x clamped into its domain (equal to x wherever x is in it)
+// and the special cases are selected afterwards, without branches.
 __device__ __forceinline__ float exp_q(float x) {
-    if (x != x) return x + x;
-    if (x > 88.72283935546875f) return __builtin_huge_valf();
-    if (x < -87.3f) return 0.0f;
-    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
-    float r = __builtin_fmaf(n, -0.693145751953125f, x);
+    const float xb = __builtin_fminf(__builtin_fmaxf(x, -87.3f), 88.72283935546875f);
+    const float n = __builtin_rintf(xb * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(n, -0.693145751953125f, xb);
     r = __builtin_fmaf(n, -1.42860682030941723212e-6f, r);
     float p = 1.98412698412698412698e-4f;
     p = __builtin_fmaf(p, r, 1.38888888888888888889e-3f);
@@ -98,9 +104,12 @@ __device__ __forceinline__ float exp_q(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    const int e = static_cast<int>(n);
-    if (e > 127) return (p * 2.0f) * __uint_as_float(254u << 23);  // * 2^127
-    return p * __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+    const int e = static_cast<int>(n);  // -126 .. 128
+    const float scaled = e > 127 ? (p * 2.0f) * __uint_as_float(254u << 23)  // * 2^127
+                                 : p * __uint_as_float(static_cast<uint32_t>(e + 127) << 23);
+    const float ranged = x > 88.72283935546875f ? __builtin_huge_valf()
+                                                : (x < -87.3f ? 0.0f : scaled);
+    return x != x ? x + x : ranged;
 }
 
 // SwiGLU with the router-weight fold; rounding sequence of the reference

@@ -58,13 +58,15 @@ hipError_t launch_build_wide_plan(const int32_t* ids, uint32_t tokens,
                                   const q38m_route_plan_v1& plan, uint32_t* chunk_counts,
                                   hipStream_t stream);
 // the grouped GEMMs over 128-row tasks, for the formats launch_gate_up /
-// launch_down take
+// launch_down take; task_count is the number of task slots (grid rows),
+// live_tasks the device word holding how many of them the plan filled
 hipError_t launch_gate_up_wide(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
                                const uint32_t* packed, const float* route_weights,
-                               const q38m_task_v1* tasks, uint32_t task_count,
-                               uint16_t* weighted_mid, hipStream_t stream);
+                               const q38m_task_v1* tasks, const uint32_t* live_tasks,
+                               uint32_t task_count, uint16_t* weighted_mid, hipStream_t stream);
 hipError_t launch_down_wide(const q38m_expert_weights_v1& w, const int8_t* mid_q,
-                            const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+                            const float* mid_s, const q38m_task_v1* tasks,
+                            const uint32_t* live_tasks, uint32_t task_count,
                             float* route_output, hipStream_t stream);
 
 // routing (q38m_routing.hip)

@@ -223,6 +223,34 @@ __global__ __launch_bounds__(64) void wide_scatter_kernel(const int32_t* __restr
     }
 }
 
+// ---- workgroup placement -----------------------------------------------------
+
+// The grouped GEMMs below run on (slice, task) grids: gridDim.x slices of
+// the output channels times one row per task slot.  The dispatcher hands
+// workgroups to the 8 XCDs round-robin by linear id, and each XCD has its
+// own L2.  This maps the live pairs (task < the plan's task count) so that
+// each XCD runs one contiguous range of them: a task's slices read the same
+// rows, and an expert's consecutive tasks read the same weights, from one
+// L2.  Workgroups past the live pairs return at once, spread evenly over
+// the XCDs.
+struct Placement {
+    uint32_t task, slice;
+};
+
+__device__ inline bool place_on_xcds(const uint32_t* live_tasks, Placement& at) {
+    constexpr uint32_t kXcds = 8;
+    const uint32_t slices = gridDim.x;
+    const uint32_t live = min(*live_tasks, gridDim.y) * slices;
+    const uint32_t id = blockIdx.y * slices + blockIdx.x;
+    if (id >= live) return false;
+    const uint32_t per = live / kXcds, extra = live % kXcds;
+    const uint32_t xcd = id % kXcds;
+    const uint32_t j = xcd * per + min(xcd, extra) + id / kXcds;
+    at.task = j / slices;
+    at.slice = j % slices;
+    return true;
+}
+
 // ---- gate/up ----------------------------------------------------------------
 
 struct TileQuad {
@@ -260,7 +288,7 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
                             const int8_t* __restrict__ xq, const float* __restrict__ xs,
                             const uint32_t* __restrict__ packed,
                             const float* __restrict__ route_weights,
-                            const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+                            const q38m_task_v1* __restrict__ tasks, const uint32_t* __restrict__ live_tasks, uint16_t* __restrict__ mid) {
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kTilesAll = 2u * I / 16u;
     constexpr uint32_t kRowScales = 4u / kSub;                           // words per row per quad
@@ -275,7 +303,9 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
     __shared__ __align__(16) uint32_t s_lds[2][kScalePieces];
     __shared__ float2 row_info[kWideRows];  // (token scale, route weight)
 
-    const q38m_task_v1 task = tasks[blockIdx.y];
+    Placement at;
+    if (!place_on_xcds(live_tasks, at)) return;
+    const q38m_task_v1 task = tasks[at.task];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
     const uint32_t tid = threadIdx.x;
@@ -287,8 +317,8 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
     const int here = static_cast<int>(rows) - static_cast<int>(64u * rh);
-    const uint32_t nt = here <= 0 ? 0u
-                                  : (here >= 64 ? 4u : (static_cast<uint32_t>(here) + 15u) / 16u);
+    const uint32_t nt = __builtin_amdgcn_readfirstlane(
+        here <= 0 ? 0u : (here >= 64 ? 4u : (static_cast<uint32_t>(here) + 15u) / 16u));
 
     // staging: row piece (row tid/8, 16-byte chunk tid%8), weight piece
     // (slot tid/64 of the workgroup's 16, lane tid%64), scale piece tid
@@ -300,7 +330,7 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
     const uint4* a_src =
         reinterpret_cast<const uint4*>(xq + static_cast<size_t>(assignment / kTopK) * H) + sch;
     const uint32_t a_at = ((sch >> 1) * kRowTiles + (sr >> 4)) * 64u + (sch & 1u) * 32u + (sr & 15u);
-    const size_t slot0 = static_cast<size_t>(e) * kQuads * kTilesAll + blockIdx.x * 16u;
+    const size_t slot0 = static_cast<size_t>(e) * kQuads * kTilesAll + at.slice * 16u;
     const uint4* w_src = w + slot0 * 64u + tid;
     const uint32_t* s_src = reinterpret_cast<const uint32_t*>(s) + slot0 * 16u * kRowScales / 2u + tid;
     const bool s_thread = tid < kScalePieces;
@@ -308,14 +338,14 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
         uint4 a, w;
         uint32_t s;
     };
-    auto load_stage = [&](uint32_t kq) {
+    auto load_stage = [&](uint32_t kq) __attribute__((always_inline)) {
         Stage st;
         st.a = alive ? a_src[kq * 8u] : make_uint4(0u, 0u, 0u, 0u);
         st.w = w_src[static_cast<size_t>(kq) * kTilesAll * 64u];
         st.s = s_thread ? s_src[static_cast<size_t>(kq) * kTilesAll * 16u * kRowScales / 2u] : 0u;
         return st;
     };
-    auto store_stage = [&](const Stage& st, uint32_t buffer) {
+    auto store_stage = [&](const Stage& st, uint32_t buffer) __attribute__((always_inline)) {
         a_lds[buffer][a_at] = make_uint2(st.a.x, st.a.y);
         a_lds[buffer][a_at + 16u] = make_uint2(st.a.z, st.a.w);
         w_lds[buffer][tid] = st.w;
@@ -361,7 +391,7 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
             }
         }
         long fa[2][kSub];
-        auto read_set = [&](uint32_t m) {
+        auto read_set = [&](uint32_t m) __attribute__((always_inline)) {
             const uint32_t gg = m / kNt, t = m % kNt;
 #pragma unroll
             for (uint32_t sb = 0; sb < kSub; ++sb)
@@ -369,7 +399,7 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
         };
         long bf[2][kSub];
         v4i d[2];
-        auto issue = [&](uint32_t k) {
+        auto issue = [&](uint32_t k) __attribute__((always_inline)) {
             const uint32_t m = k / 2u, u = k & 1u;
             const uint32_t gg = m / kNt, t = m % kNt;
             if (u == 0u) {
@@ -388,7 +418,7 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
                 acc = mfma_i8_16x16x32(fa[m & 1u][sb], bf[u][sb], acc);
             d[k & 1u] = acc;
         };
-        auto step = [&](uint32_t k) {
+        auto step = [&](uint32_t k) __attribute__((always_inline)) {
             const uint32_t m = k / 2u, u = k & 1u;
             const uint32_t gg = m / kNt, t = m % kNt;
             const float scale = sc[u][gg];
@@ -396,6 +426,11 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
             for (uint32_t i = 0; i < 4u; ++i)
                 y[t][u][i] =
                     __builtin_fmaf(__int_as_float(d[k & 1u][i]) + unbias, scale, y[t][u][i]);
+            // keep the chain step here, between this tile's MFMAs and the next
+            // ones (otherwise it can sink to the end of the loop body, and
+            // every accumulator of the quad stays live until then)
+            asm volatile("" : "+v"(y[t][u][0]), "+v"(y[t][u][1]), "+v"(y[t][u][2]),
+                         "+v"(y[t][u][3]));
         };
         read_set(0);
 #pragma unroll
@@ -406,38 +441,44 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    auto compute = [&](uint32_t buffer) __attribute__((always_inline)) {
-        // three row tiles run as four and one as two (the extra rows are zero)
-        if (nt > 2u)
-            multiply(std::integral_constant<uint32_t, 4>{}, buffer);
-        else if (nt > 0u)
-            multiply(std::integral_constant<uint32_t, 2>{}, buffer);
-    };
     // barrier over LDS only: this wave's LDS operations are complete, its
     // global loads (the staging of later quads) stay in flight
     auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
     // quad q: loaded at the start of quad q-2 into register set q%2, stored
-    // at the end of quad q-1 into LDS buffer q%2, multiplied during quad q
+    // at the end of quad q-1 into LDS buffer q%2, multiplied during quad q.
+    // The loop is instantiated per row-tile count (three tiles run as four,
+    // one as two; the extra rows are zero), so a wave's accumulators keep
+    // one register assignment through it; every instance passes the same
+    // barriers.
     Stage set0 = load_stage(0), set1 = load_stage(1);
     store_stage(set0, 0u);
     __syncthreads();
+    auto k_loop = [&](auto tiles) __attribute__((always_inline)) {
+        constexpr uint32_t kNt = decltype(tiles)::value;
 #pragma unroll 1
-    for (uint32_t kq = 0; kq < kQuads; kq += 2u) {
-        if (kq + 2u < kQuads) set0 = load_stage(kq + 2u);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(0u);
-        store_stage(set1, 1u);
-        lds_barrier();
-        if (kq + 3u < kQuads) set1 = load_stage(kq + 3u);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(1u);
-        if (kq + 2u < kQuads) store_stage(set0, 0u);
-        lds_barrier();
-    }
+        for (uint32_t kq = 0; kq < kQuads; kq += 2u) {
+            if (kq + 2u < kQuads) set0 = load_stage(kq + 2u);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kNt > 0u) multiply(tiles, 0u);
+            store_stage(set1, 1u);
+            lds_barrier();
+            if (kq + 3u < kQuads) set1 = load_stage(kq + 3u);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (kNt > 0u) multiply(tiles, 1u);
+            if (kq + 2u < kQuads) store_stage(set0, 0u);
+            lds_barrier();
+        }
+    };
+    if (nt > 2u)
+        k_loop(std::integral_constant<uint32_t, 4>{});
+    else if (nt > 0u)
+        k_loop(std::integral_constant<uint32_t, 2>{});
+    else
+        k_loop(std::integral_constant<uint32_t, 0>{});
 
     // SwiGLU: D lane (qh, n) holds rows 4qh + i of each tile, channel n
-    const uint32_t channel = (blockIdx.x * 8u + pr) * 16u + n;
+    const uint32_t channel = (at.slice * 8u + pr) * 16u + n;
     const float unscale = kBf16 ? 1.0f : 0.0625f;
 #pragma unroll
     for (uint32_t t = 0; t < 4u; ++t) {
@@ -630,7 +671,7 @@ void gate_up_w8_wide_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
-    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    const q38m_task_v1* __restrict__ tasks, const uint32_t* __restrict__ live_tasks, uint16_t* __restrict__ mid) {
     constexpr uint32_t kBlocks = H / 64u;
     constexpr uint32_t kSlots = 2u * I / 16u;
     constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
@@ -642,12 +683,14 @@ void gate_up_w8_wide_kernel(
     auto a_lds = reinterpret_cast<uint4 (*)[kRowTiles * 64u]>(lds);
     float* gate_lds = reinterpret_cast<float*>(lds);
 
-    const q38m_task_v1 task = tasks[blockIdx.y];
+    Placement at;
+    if (!place_on_xcds(live_tasks, at)) return;
+    const q38m_task_v1 task = tasks[at.task];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool up = wave >= kPairs;
-    const uint32_t pair = blockIdx.x * kPairs + (wave % kPairs);
+    const uint32_t pair = at.slice * kPairs + (wave % kPairs);
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
     const uint32_t n = threadIdx.x & 15u;
@@ -786,7 +829,7 @@ template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave,
 __global__ __launch_bounds__(kWaves * 64) void down_w8_wide_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
-    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    const q38m_task_v1* __restrict__ tasks, const uint32_t* __restrict__ live_tasks, float* __restrict__ out) {
     constexpr uint32_t kBlocks = I / 64u;
     constexpr uint32_t kTiles = H / 16u;
     constexpr uint32_t kThreads = kWaves * 64u;
@@ -795,14 +838,16 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_wide_kernel(
     __shared__ uint4 a_lds[kBlocks * kRowTiles * 64u];
     __shared__ float row_scale[kWideRows];
 
-    const q38m_task_v1 task = tasks[blockIdx.y];
+    Placement at;
+    if (!place_on_xcds(live_tasks, at)) return;
+    const q38m_task_v1 task = tasks[at.task];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t e = task.expert;
     const uint32_t p0 = task.packed_begin;
-    const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
+    const uint32_t tile0 = (at.slice * kWaves + wave) * kTilesPerWave;
     const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
     const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
 
@@ -953,7 +998,7 @@ __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(4))
 void down_w4_wide_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ mq, const float* __restrict__ ms,
-    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    const q38m_task_v1* __restrict__ tasks, const uint32_t* __restrict__ live_tasks, float* __restrict__ out) {
     constexpr uint32_t kQuads = I / 128u;
     constexpr uint32_t kGroups = I / 32u;
     constexpr uint32_t kTiles = H / 16u;
@@ -963,7 +1008,9 @@ void down_w4_wide_kernel(
     __shared__ uint2 a_lds[kGroups * kRowTiles * 64u];
     __shared__ float row_scale[kWideRows];
 
-    const q38m_task_v1 task = tasks[blockIdx.y];
+    Placement at;
+    if (!place_on_xcds(live_tasks, at)) return;
+    const q38m_task_v1 task = tasks[at.task];
     const uint32_t rows = task.valid_rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
@@ -997,7 +1044,7 @@ void down_w4_wide_kernel(
     __syncthreads();
 
     // wave w: tiles tile0 + t * kWaves
-    const uint32_t tile0 = blockIdx.x * kWaves * kTilesPerWave + wave;
+    const uint32_t tile0 = at.slice * kWaves * kTilesPerWave + wave;
     const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile0) * 64u + lane;
     const uint16_t* st =
         s + ((static_cast<size_t>(e) * kQuads * kTiles + tile0) * 16u + n) * (4u / kSub);
@@ -1036,88 +1083,94 @@ hipError_t launch_build_wide_plan(const int32_t* ids, uint32_t tokens,
 
 namespace {
 
+// the task slots a launch covers: grid rows, and the device word with the
+// number the plan filled
+struct TaskSlots {
+    const q38m_task_v1* tasks;
+    const uint32_t* live;
+    uint32_t count;
+};
+
 template <uint32_t kSub, bool kBf16>
 void launch_gate_up_wide_sub(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
                              const uint32_t* packed, const float* route_weights,
-                             const q38m_task_v1* tasks, uint32_t task_count,
-                             uint16_t* weighted_mid, hipStream_t stream) {
+                             const TaskSlots& t, uint16_t* weighted_mid, hipStream_t stream) {
     // 8 channel pairs (256 rows of gate/up) per workgroup
-    const dim3 grid(kInter / 16u / 8u, task_count);
+    const dim3 grid(kInter / 16u / 8u, t.count);
     gate_up_w4_wide_kernel<kHidden, kInter, kSub, kBf16>
         <<<grid, 1024, 0, stream>>>(static_cast<const uint4*>(w.data),
                                     static_cast<const uint16_t*>(w.scales), xq, xs, packed,
-                                    route_weights, tasks, weighted_mid);
+                                    route_weights, t.tasks, t.live, weighted_mid);
 }
 
 // Per channel: four tiles per wave (the tuned BASELINE shape).  Grouped:
 // the fp32 chain doubles the live accumulator state, so one tile per wave.
 template <uint32_t kBlocksPerGroup, bool kBf16>
 void launch_down_w8_wide_groups(const q38m_expert_weights_v1& w, const int8_t* mid_q,
-                                const float* mid_s, const q38m_task_v1* tasks,
-                                uint32_t task_count, float* route_output, hipStream_t stream) {
+                                const float* mid_s, const TaskSlots& t, float* route_output,
+                                hipStream_t stream) {
     constexpr uint32_t kWaves = 8;
     constexpr uint32_t kTilesPerWave = kBlocksPerGroup == kInter / 64u ? 4u : 1u;
-    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
+    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), t.count);
     down_w8_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, kBf16>
         <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(w.data),
                                             static_cast<const uint16_t*>(w.scales), mid_q, mid_s,
-                                            tasks, route_output);
+                                            t.tasks, t.live, route_output);
 }
 
 template <uint32_t kSub, bool kBf16>
 void launch_down_w4_wide_sub(const q38m_expert_weights_v1& w, const int8_t* mid_q,
-                             const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
-                             float* route_output, hipStream_t stream) {
+                             const float* mid_s, const TaskSlots& t, float* route_output,
+                             hipStream_t stream) {
     constexpr uint32_t kWaves = 16, kTilesPerWave = 2;
-    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
+    const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), t.count);
     down_w4_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave, kSub, kBf16>
         <<<grid, kWaves * 64u, 0, stream>>>(static_cast<const uint4*>(w.data),
                                             static_cast<const uint16_t*>(w.scales), mid_q, mid_s,
-                                            tasks, route_output);
+                                            t.tasks, t.live, route_output);
 }
 
 template <uint32_t kBlocksPerGroup, bool kBf16>
 void launch_gate_up_w8_wide_groups(const q38m_expert_weights_v1& w, const int8_t* xq,
                                    const float* xs, const uint32_t* packed,
-                                   const float* route_weights, const q38m_task_v1* tasks,
-                                   uint32_t task_count, uint16_t* weighted_mid,
-                                   hipStream_t stream) {
+                                   const float* route_weights, const TaskSlots& t,
+                                   uint16_t* weighted_mid, hipStream_t stream) {
     constexpr uint32_t kPairs = 8;
-    const dim3 grid(kInter / 16u / kPairs, task_count);
+    const dim3 grid(kInter / 16u / kPairs, t.count);
     gate_up_w8_wide_kernel<kHidden, kInter, kPairs, kBlocksPerGroup, kBf16>
         <<<grid, kPairs * 128u, 0, stream>>>(static_cast<const uint4*>(w.data),
                                              static_cast<const uint16_t*>(w.scales), xq, xs,
-                                             packed, route_weights, tasks, weighted_mid);
+                                             packed, route_weights, t.tasks, t.live,
+                                             weighted_mid);
 }
 
 template <bool kBf16>
 hipError_t launch_gate_up_wide_dtype(const q38m_expert_weights_v1& w, const int8_t* xq,
                                      const float* xs, const uint32_t* packed,
-                                     const float* route_weights, const q38m_task_v1* tasks,
-                                     uint32_t task_count, uint16_t* weighted_mid,
-                                     hipStream_t stream) {
+                                     const float* route_weights, const TaskSlots& t,
+                                     uint16_t* mid, hipStream_t stream) {
     if (w.format == Q38M_FORMAT_W8_SYM) {
         switch (w.group_size) {
-            case 0u: launch_gate_up_w8_wide_groups<kHidden / 64u, kBf16>(
-                         w, xq, xs, packed, route_weights, tasks, task_count, weighted_mid,
-                         stream); break;
-            case 64u: launch_gate_up_w8_wide_groups<1, kBf16>(w, xq, xs, packed, route_weights,
-                                                              tasks, task_count, weighted_mid,
-                                                              stream); break;
-            case 128u: launch_gate_up_w8_wide_groups<2, kBf16>(w, xq, xs, packed, route_weights,
-                                                               tasks, task_count, weighted_mid,
-                                                               stream); break;
+            case 0u:
+                launch_gate_up_w8_wide_groups<kHidden / 64u, kBf16>(w, xq, xs, packed,
+                                                                    route_weights, t, mid, stream);
+                break;
+            case 64u:
+                launch_gate_up_w8_wide_groups<1, kBf16>(w, xq, xs, packed, route_weights, t, mid,
+                                                        stream);
+                break;
+            case 128u:
+                launch_gate_up_w8_wide_groups<2, kBf16>(w, xq, xs, packed, route_weights, t, mid,
+                                                        stream);
+                break;
             default: return hipErrorInvalidValue;
         }
         return hipGetLastError();
     }
     switch (w.group_size) {
-        case 32u: launch_gate_up_wide_sub<1, kBf16>(w, xq, xs, packed, route_weights, tasks,
-                                                    task_count, weighted_mid, stream); break;
-        case 64u: launch_gate_up_wide_sub<2, kBf16>(w, xq, xs, packed, route_weights, tasks,
-                                                    task_count, weighted_mid, stream); break;
-        case 128u: launch_gate_up_wide_sub<4, kBf16>(w, xq, xs, packed, route_weights, tasks,
-                                                     task_count, weighted_mid, stream); break;
+        case 32u: launch_gate_up_wide_sub<1, kBf16>(w, xq, xs, packed, route_weights, t, mid, stream); break;
+        case 64u: launch_gate_up_wide_sub<2, kBf16>(w, xq, xs, packed, route_weights, t, mid, stream); break;
+        case 128u: launch_gate_up_wide_sub<4, kBf16>(w, xq, xs, packed, route_weights, t, mid, stream); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1125,28 +1178,21 @@ hipError_t launch_gate_up_wide_dtype(const q38m_expert_weights_v1& w, const int8
 
 template <bool kBf16>
 hipError_t launch_down_wide_dtype(const q38m_expert_weights_v1& w, const int8_t* mid_q,
-                                  const float* mid_s, const q38m_task_v1* tasks,
-                                  uint32_t task_count, float* route_output, hipStream_t stream) {
+                                  const float* mid_s, const TaskSlots& t, float* out,
+                                  hipStream_t stream) {
     constexpr uint32_t kBlocks = kInter / 64u;
     if (w.format == Q38M_FORMAT_W8_SYM) {
         switch (w.group_size) {
-            case 0u: launch_down_w8_wide_groups<kBlocks, kBf16>(w, mid_q, mid_s, tasks,
-                                                                task_count, route_output,
-                                                                stream); break;
-            case 64u: launch_down_w8_wide_groups<1, kBf16>(w, mid_q, mid_s, tasks, task_count,
-                                                           route_output, stream); break;
-            case 128u: launch_down_w8_wide_groups<2, kBf16>(w, mid_q, mid_s, tasks, task_count,
-                                                            route_output, stream); break;
+            case 0u: launch_down_w8_wide_groups<kBlocks, kBf16>(w, mid_q, mid_s, t, out, stream); break;
+            case 64u: launch_down_w8_wide_groups<1, kBf16>(w, mid_q, mid_s, t, out, stream); break;
+            case 128u: launch_down_w8_wide_groups<2, kBf16>(w, mid_q, mid_s, t, out, stream); break;
             default: return hipErrorInvalidValue;
         }
     } else {
         switch (w.group_size) {
-            case 32u: launch_down_w4_wide_sub<1, kBf16>(w, mid_q, mid_s, tasks, task_count,
-                                                        route_output, stream); break;
-            case 64u: launch_down_w4_wide_sub<2, kBf16>(w, mid_q, mid_s, tasks, task_count,
-                                                        route_output, stream); break;
-            case 128u: launch_down_w4_wide_sub<4, kBf16>(w, mid_q, mid_s, tasks, task_count,
-                                                         route_output, stream); break;
+            case 32u: launch_down_w4_wide_sub<1, kBf16>(w, mid_q, mid_s, t, out, stream); break;
+            case 64u: launch_down_w4_wide_sub<2, kBf16>(w, mid_q, mid_s, t, out, stream); break;
+            case 128u: launch_down_w4_wide_sub<4, kBf16>(w, mid_q, mid_s, t, out, stream); break;
             default: return hipErrorInvalidValue;
         }
     }
@@ -1157,23 +1203,24 @@ hipError_t launch_down_wide_dtype(const q38m_expert_weights_v1& w, const int8_t*
 
 hipError_t launch_gate_up_wide(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
                                const uint32_t* packed, const float* route_weights,
-                               const q38m_task_v1* tasks, uint32_t task_count,
-                               uint16_t* weighted_mid, hipStream_t stream) {
+                               const q38m_task_v1* tasks, const uint32_t* live_tasks,
+                               uint32_t task_count, uint16_t* weighted_mid, hipStream_t stream) {
+    const TaskSlots t{tasks, live_tasks, task_count};
     return w.scale_dtype == Q38M_SCALE_BF16
-               ? launch_gate_up_wide_dtype<true>(w, xq, xs, packed, route_weights, tasks,
-                                                 task_count, weighted_mid, stream)
-               : launch_gate_up_wide_dtype<false>(w, xq, xs, packed, route_weights, tasks,
-                                                  task_count, weighted_mid, stream);
+               ? launch_gate_up_wide_dtype<true>(w, xq, xs, packed, route_weights, t,
+                                                 weighted_mid, stream)
+               : launch_gate_up_wide_dtype<false>(w, xq, xs, packed, route_weights, t,
+                                                  weighted_mid, stream);
 }
 
 hipError_t launch_down_wide(const q38m_expert_weights_v1& w, const int8_t* mid_q,
-                            const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+                            const float* mid_s, const q38m_task_v1* tasks,
+                            const uint32_t* live_tasks, uint32_t task_count,
                             float* route_output, hipStream_t stream) {
+    const TaskSlots t{tasks, live_tasks, task_count};
     return w.scale_dtype == Q38M_SCALE_BF16
-               ? launch_down_wide_dtype<true>(w, mid_q, mid_s, tasks, task_count, route_output,
-                                              stream)
-               : launch_down_wide_dtype<false>(w, mid_q, mid_s, tasks, task_count,
-                                               route_output, stream);
+               ? launch_down_wide_dtype<true>(w, mid_q, mid_s, t, route_output, stream)
+               : launch_down_wide_dtype<false>(w, mid_q, mid_s, t, route_output, stream);
 }
 
 }  // namespace q38m
