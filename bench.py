@@ -17,17 +17,30 @@ config-5 layer beside the slab path, config 5 end to end (32,768 tokens
 through all 48 layers, layer-major and slab-major), the hyper-connection prepare/finish
 around the MoE step (q38m_hyper_prepare_v1, q38m_hyper_inject_bf16) on the
 512-token slab, and the CPU oracle timed on this host as the baseline.
+After the timed runs, two child processes of this file run under
+rocprofv3 --pmc (config-2 slab; chunk workloads) and the line carries
+the counter-derived MFMA busy fraction and int8 rate of the headline and
+chunk GEMMs beside the algorithmic ones (skipped with --no-counters or
+without rocprofv3).  --pmc-report {slab,chunk,decode} prints the full
+counter and HBM-traffic tables of one workload instead.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
        [--no-quantizer] [--no-dense] [--no-chunks] [--no-stack] [--no-hyper]
+       [--no-formats] [--no-counters] [--pmc-report WORKLOAD]
 """
 import argparse
+import collections
+import csv
 import ctypes
 import importlib.util
 import json
 import os
+import shutil
+import signal
 import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -47,6 +60,220 @@ def load(name, path, package_dir=None):
     return module
 
 
+# ---- hardware counters (rocprofv3 --pmc over a child run of this file) ----
+#
+# One counter set per child process (rocprofv3 does not split counters over
+# passes).  Per dispatch the CSV holds each counter summed over its hardware
+# instances (SQ counters over all SIMDs, GRBM_GUI_ACTIVE over the 8 XCCs).
+PMC_MFMA = ("SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU "
+            "SQ_INSTS_MFMA SQ_ACTIVE_INST_VALU SQ_WAVES SQ_INSTS_LDS GRBM_GUI_ACTIVE")
+PMC_WAITS = ("SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_WAVE_CYCLES SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS "
+             "SQ_INST_CYCLES_VMEM_RD SQ_ACTIVE_INST_MISC SQ_INSTS_SALU GRBM_GUI_ACTIVE")
+# the child runs that each counter pass profiles
+PMC_WORKLOADS = {
+    "slab": "--no-cpu --no-decode --no-quantizer --no-dense --no-chunks --no-hyper --no-stack "
+            "--no-formats --steps 10 --warmup 2",
+    "chunk": "--no-cpu --no-decode --no-quantizer --no-dense --no-hyper --no-stack --no-formats "
+             "--steps 2 --warmup 1",
+    "decode": "--no-cpu --no-quantizer --no-dense --no-chunks --no-hyper --no-stack --no-formats "
+              "--steps 3 --warmup 1 --decode-tokens 4",
+}
+VALU_CYCLES = 4  # issue cycles of one non-packed wave64 VALU instruction on a SIMD
+
+
+def _short_kernel(name):
+    name = name.replace("void ", "").replace("q38m::(anonymous namespace)::", "")
+    return name.split("(")[0]
+
+
+def pmc_run(counters, workload, extra=""):
+    """Run this file under rocprofv3 --pmc COUNTERS as a child process on the
+    named workload; returns ({(kernel, grid): {counter: [per dispatch]},
+    "_duration_us": [...]}, agent dict), or None when rocprofv3 is absent or
+    the run fails (the parent's own results stand either way)."""
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    out = tempfile.mkdtemp(prefix="q38m_pmc_", dir="/tmp")
+    cmd = [exe, "--pmc", *counters.split(), "-f", "csv", "-d", out, "-o", "pmc", "--",
+           sys.executable, os.path.join(ROOT, "bench.py"), "--no-counters",
+           *PMC_WORKLOADS[workload].split(), *extra.split()]
+    env = dict(os.environ, TMPDIR="/tmp")
+    try:
+        proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
+                                stderr=subprocess.DEVNULL, start_new_session=True)
+        try:
+            rc = proc.wait(timeout=300)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.wait()
+            return None
+        if rc != 0:
+            return None
+        per = collections.defaultdict(lambda: collections.defaultdict(float))
+        meta = {}
+        for path, _, files in os.walk(out):
+            for f in files:
+                full = os.path.join(path, f)
+                if f.endswith("counter_collection.csv"):
+                    with open(full) as fh:
+                        for r in csv.DictReader(fh):
+                            key = (r["Kernel_Name"], int(r["Grid_Size"]), r["Dispatch_Id"])
+                            per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+                            meta[key] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                elif f.endswith("agent_info.csv"):
+                    with open(full) as fh:
+                        for r in csv.DictReader(fh):
+                            if r.get("Agent_Type") == "GPU":
+                                agent = {"simds": int(r["Simd_Count"]), "xccs": int(r["Num_Xcc"]),
+                                         "cus": int(r["Cu_Count"])}
+        agg = collections.defaultdict(lambda: collections.defaultdict(list))
+        for (name, grid, _), cs in per.items():
+            for c, v in cs.items():
+                agg[(_short_kernel(name), grid)][c].append(v)
+            agg[(_short_kernel(name), grid)]["_duration_us"].append(meta[(name, grid, _)])
+        return agg, agent
+    except (OSError, KeyError, ValueError, UnboundLocalError):
+        return None
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
+
+
+def mfma_metrics(cs, agent):
+    """Per-launch MFMA figures from one kernel's PMC_MFMA counters."""
+    m = lambda c: statistics.fmean(cs[c])
+    gui = m("GRBM_GUI_ACTIVE") / agent["xccs"]  # busy cycles of one XCC
+    mfma = m("SQ_INSTS_MFMA")
+    dur = m("_duration_us")
+    ops = m("SQ_INSTS_VALU_MFMA_MOPS_I8") * 512.0
+    valu = m("SQ_INSTS_VALU") - mfma
+    return {"launches": len(cs["_duration_us"]), "avg_us": round(dur, 2),
+            "gui_active_cycles_per_xcc": round(gui),
+            "mfma_busy_frac": round(m("SQ_VALU_MFMA_BUSY_CYCLES") / (gui * agent["simds"]), 4),
+            "int8_ops_counter": ops,
+            "int8_tops_counter": round(ops / (dur * 1e-6) / 1e12, 2),
+            "int8_peak_frac_counter": round(ops / (dur * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+            "mfma_insts": mfma,
+            "valu_insts_per_mfma": round(valu / mfma, 2) if mfma else None,
+            "valu_issue_share_est": round(valu * VALU_CYCLES / (gui * agent["simds"]), 4)}
+
+
+def pick(agg, kernel, largest_grid=False):
+    """The (kernel, grid) entry with the most launches (or the largest grid)."""
+    rows = [(g, cs) for (k, g), cs in agg.items() if k.split("<")[0] == kernel]
+    if not rows:
+        return None
+    return max(rows, key=lambda r: r[0] if largest_grid else len(r[1]["_duration_us"]))
+
+
+def counters_summary():
+    """MFMA counters of the headline slab kernels (config 2) and of the chunk
+    kernels on a config-5 layer, one child run each."""
+    out = {"source": "rocprofv3 --pmc " + PMC_MFMA + " -- python3 bench.py --no-counters <workload>",
+           "formulas": {"mfma_busy_frac": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCCs x SIMDs)",
+                        "int8_tops_counter": "SQ_INSTS_VALU_MFMA_MOPS_I8 x 512 / launch duration",
+                        "valu_issue_share_est": f"(SQ_INSTS_VALU - SQ_INSTS_MFMA) x {VALU_CYCLES} / "
+                                                "(GRBM_GUI_ACTIVE / XCCs x SIMDs)"}}
+    slab = pmc_run(PMC_MFMA, "slab")
+    if slab:
+        agg, agent = slab
+        out["workload_slab"] = PMC_WORKLOADS["slab"]
+        for k in ("gate_up_w4_kernel", "down_w8_kernel"):
+            hit = pick(agg, k)
+            if hit:
+                out[f"{k} (config 2 slab)"] = dict(grid=hit[0], **mfma_metrics(hit[1], agent))
+    chunk = pmc_run(PMC_MFMA, "chunk")
+    if chunk:
+        agg, agent = chunk
+        out["workload_chunk"] = PMC_WORKLOADS["chunk"]
+        for k in ("gate_up_w4_wide_kernel", "down_w8_wide_kernel", "down_w4_wide_kernel"):
+            hit = pick(agg, k, largest_grid=True)
+            if hit:
+                out[f"{k} (config-5 layer)"] = dict(grid=hit[0], **mfma_metrics(hit[1], agent))
+    return out if (slab or chunk) else None
+
+
+def _copy_scale(agg, counter, mib):
+    """Bytes per counted byte of FETCH_SIZE/WRITE_SIZE (KiB per dispatch),
+    from the largest __amd_rocclr_copyBuffer dispatch (a plain copy of mib MiB)."""
+    hits = [(g, cs) for (k, g), cs in agg.items() if k.startswith("__amd_rocclr_copyBuffer")]
+    if not hits:
+        return None
+    _, cs = max(hits, key=lambda h: statistics.median(h[1][counter]))
+    return (mib << 20) / (statistics.median(cs[counter]) * 1024.0)
+
+
+def pmc_report(workload):
+    """Markdown counter report of one workload: MFMA/VALU counters, wait
+    counters and calibrated HBM traffic per kernel of this library."""
+    mib = 256
+    runs = {"mfma": pmc_run(PMC_MFMA, workload), "waits": pmc_run(PMC_WAITS, workload),
+            "fetch": pmc_run("FETCH_SIZE", workload, f"--calibrate-copy-mib {mib}"),
+            "write": pmc_run("WRITE_SIZE", workload, f"--calibrate-copy-mib {mib}")}
+    lines = [f"# Hardware counters: `{workload}` workload", "",
+             f"Command (repository root on the GPU box): `python3 bench.py --pmc-report {workload}`.",
+             "It runs four child processes, one counter set each:",
+             "`rocprofv3 --pmc <set> -f csv -d <tmp> -o pmc -- python3 bench.py --no-counters "
+             f"{PMC_WORKLOADS[workload]}` (FETCH/WRITE passes add `--calibrate-copy-mib {mib}`).", "",
+             f"- set 1: `{PMC_MFMA}`", f"- set 2: `{PMC_WAITS}`", "- set 3: `FETCH_SIZE`",
+             "- set 4: `WRITE_SIZE`", ""]
+    if not any(runs.values()):
+        lines.append("rocprofv3 was not available or every pass failed.")
+        return "\n".join(lines)
+    agent = next(r[1] for r in runs.values() if r)
+    lines.append(f"Agent: {agent['cus']} CUs, {agent['simds']} SIMDs, {agent['xccs']} XCCs.  "
+                 "Counter values are per dispatch, summed over hardware instances; a kernel "
+                 "with several grids is listed per grid.")
+    fs = _copy_scale(runs["fetch"][0], "FETCH_SIZE", mib) if runs["fetch"] else None
+    ws = _copy_scale(runs["write"][0], "WRITE_SIZE", mib) if runs["write"] else None
+    lines.append(f"HBM traffic calibration ({mib} MiB copy kernel): FETCH_SIZE x "
+                 f"{fs and round(fs, 4)}, WRITE_SIZE x {ws and round(ws, 4)} bytes per counted "
+                 "byte.")
+    lines += ["", "Formulas: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCCs x "
+              "SIMDs); int8 TOP/s = SQ_INSTS_VALU_MFMA_MOPS_I8 x 512 / duration (duration from "
+              "the counter run's dispatch timestamps); VALU/MFMA = (SQ_INSTS_VALU - "
+              f"SQ_INSTS_MFMA) / SQ_INSTS_MFMA; VALU issue = (SQ_INSTS_VALU - SQ_INSTS_MFMA) x "
+              f"{VALU_CYCLES} cycles / (GRBM_GUI_ACTIVE / XCCs x SIMDs); waits = SQ_WAIT_INST_ANY "
+              "/ SQ_WAVE_CYCLES and SQ_WAIT_ANY / SQ_WAVE_CYCLES; peak int8 "
+              f"{INT8_PEAK_TOPS / 1000:.2f} POP/s.", ""]
+    keys = set()
+    for r in runs.values():
+        if r:
+            keys |= {k for k in r[0] if not k[0].startswith(("__amd", "at::", "void at::"))
+                     and not k[0].startswith(("synth", "repack", "copy_u16"))}
+    def avg(run, key, c):
+        if not run or key not in run[0] or c not in run[0][key]:
+            return None
+        return statistics.fmean(run[0][key][c])
+    rows = []
+    for key in keys:
+        mm = mfma_metrics(runs["mfma"][0][key], agent) if runs["mfma"] and key in runs["mfma"][0] \
+            else None
+        wc = avg(runs["waits"], key, "SQ_WAVE_CYCLES")
+        wi = avg(runs["waits"], key, "SQ_WAIT_INST_ANY")
+        wa = avg(runs["waits"], key, "SQ_WAIT_ANY")
+        fe = avg(runs["fetch"], key, "FETCH_SIZE")
+        wr = avg(runs["write"], key, "WRITE_SIZE")
+        rows.append((mm["avg_us"] if mm else 0.0, key, mm, wc, wi, wa,
+                     fe * 1024 * fs / 1e6 if fe is not None and fs else None,
+                     wr * 1024 * ws / 1e6 if wr is not None and ws else None))
+    rows.sort(key=lambda r: -r[0])
+    lines += ["| kernel | grid | launches | avg us | MFMA busy | int8 TOP/s | % int8 peak | "
+              "VALU/MFMA | VALU issue | wait inst | wait any | FETCH MB | WRITE MB |",
+              "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    f = lambda v, d=2: "" if v is None else (f"{v:.{d}f}" if isinstance(v, float) else str(v))
+    for _, (k, g), mm, wc, wi, wa, fe, wr in rows:
+        lines.append(
+            f"| {k} | {g} | {mm['launches'] if mm else ''} | {f(mm and mm['avg_us'])} | "
+            f"{f(mm and 100 * mm['mfma_busy_frac'], 1)}% | {f(mm and mm['int8_tops_counter'], 1)} | "
+            f"{f(mm and 100 * mm['int8_peak_frac_counter'], 2)}% | "
+            f"{f(mm and mm['valu_insts_per_mfma'])} | "
+            f"{f(mm and 100 * mm['valu_issue_share_est'], 1)}% | "
+            f"{f(wi / wc * 100 if wc else None, 1)}% | {f(wa / wc * 100 if wc else None, 1)}% | "
+            f"{f(fe, 1)} | {f(wr, 1)} |")
+    return "\n".join(lines)
+
+
 def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -62,10 +289,17 @@ def main():
     parser.add_argument("--no-formats", action="store_true")
     parser.add_argument("--no-stack", action="store_true",
                         help="skip the full 48-layer config-5 stack")
+    parser.add_argument("--no-counters", action="store_true",
+                        help="skip the rocprofv3 MFMA counter passes (child runs)")
+    parser.add_argument("--pmc-report", choices=["slab", "chunk", "decode"],
+                        help="print the counter report for one workload (markdown) and exit")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
     args = parser.parse_args()
+    if args.pmc_report:
+        print(pmc_report(args.pmc_report), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE data plane is built and measured on a single "
               f"MI355X (expert sharding is a design note only); --gpus {args.gpus} is not run.",
@@ -226,6 +460,10 @@ def main():
                               INT8_PEAK_TOPS, 4)},
         "stages_ms": {n: round(v, 5) for n, v in zip(stage_names, stage_ms)},
         "timing": {"value": "wall clock over the timed K calls of q38m_moe_prefill_v1",
+                   "plan_hashes": "the timed step builds the route plan without the FNV "
+                                  "route/plan hashes (header words route_hash and plan_hash "
+                                  "left zero, as q38m_moe_build_route_plan_v1 with hashes=0); "
+                                  "nothing in the step reads them",
                    "stages_ms": "HIP events around each entry point over a second timed run "
                                 "of K staged steps (same kernels)",
                    "staged_ms_per_step": round(staged_ms_per_step, 4)},
@@ -263,6 +501,25 @@ def main():
     if not args.no_formats:
         result["reference_formats_at_baseline_dims"] = bench_reference_formats(
             q38m, W, torch, args.steps)
+
+    if not args.no_counters:
+        counters = counters_summary()
+        result["counters"] = counters
+        head = counters and counters.get(f"{d_symbol} (config 2 slab)")
+        if head:
+            result["roofline"]["mfma_busy_frac_counter"] = head["mfma_busy_frac"]
+            result["roofline"]["int8_peak_frac_counter"] = head["int8_peak_frac_counter"]
+        wide = counters and counters.get("gate_up_w4_wide_kernel (config-5 layer)")
+        if wide and "chunks" in result:
+            result["chunks"]["gate_up_w4_wide_kernel_counters"] = {
+                k: wide[k] for k in ("avg_us", "mfma_busy_frac", "int8_peak_frac_counter",
+                                     "valu_insts_per_mfma", "valu_issue_share_est")}
+        slab_ops = [counters[k]["int8_ops_counter"] for k in
+                    ("gate_up_w4_kernel (config 2 slab)", "down_w8_kernel (config 2 slab)")
+                    if counters and k in counters]
+        if len(slab_ops) == 2:
+            result["step_roofline"]["int8_mfma_frac_counter"] = round(
+                sum(slab_ops) / step_s / 1e12 / INT8_PEAK_TOPS, 5)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,

@@ -21,6 +21,11 @@ extern "C" {
  * polynomial), the function every sigmoid / SiLU of the path uses. */
 int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream,
                     int device);
+/* All 2^32 fp32 bit patterns through the hardware bf16 conversion and the
+ * contract's integer round-to-nearest-even; result[4] (device memory, set by
+ * the caller to {0, ~0, 0, ~0}) receives {mismatches, first mismatching
+ * pattern, mismatches on non-NaN inputs, first such pattern}. */
+int q38m_debug_bf16_sweep(uint32_t* result, void* stream, int device);
 /* One int8 MFMA product d = a * b^T with a, b row-major (16x32 and 16x32,
  * or 32x32 and 32x32), through the lane layouts the grouped kernels use. */
 int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d,

@@ -182,6 +182,7 @@ SIGNATURES = {
     "q38m_last_error": (ctypes.c_char_p, []),
     # self checks (include/q38m_selftest.h)
     "q38m_debug_expf": (_INT, [_P, _U32, _P, _P, _INT]),
+    "q38m_debug_bf16_sweep": (_INT, [_P, _P, _INT]),
     "q38m_debug_mfma_16x16x32_i8": (_INT, [_P, _P, _P, _P, _INT]),
     "q38m_debug_mfma_32x32x32_i8": (_INT, [_P, _P, _P, _P, _INT]),
 }

@@ -908,6 +908,12 @@ int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream, int de
     return finish(q38m::launch_debug_expf(x, n, out, as_stream(stream)), "debug_expf_kernel");
 }
 
+int q38m_debug_bf16_sweep(uint32_t* result, void* stream, int device) {
+    if (!result) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug bf16 input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_debug_bf16(result, as_stream(stream)), "debug_bf16_kernel");
+}
+
 int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d, void* stream,
                                 int device) {
     if (!a || !b || !d) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug mfma input");

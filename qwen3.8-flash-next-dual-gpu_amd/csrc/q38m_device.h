@@ -14,6 +14,7 @@
 namespace q38m {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // ---- streaming loads -----------------------------------------------------
 
@@ -39,21 +40,26 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t h) {
 }
 
 // Round-to-nearest-even bf16 (tools/q38_artifact_compiler.py:61-66); a NaN
-// keeps its sign and top payload bits with the quiet bit set.  Both results
-// are formed and one selected, so the conversion runs without branches.
-__device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+// keeps its sign and top payload bits with the quiet bit set.  This is the
+// integer form the oracle restates; the kernels use bf16_hw below.
+__device__ __forceinline__ uint32_t f32_to_bf16_int(float v) {
     const uint32_t b = __float_as_uint(v);
     const uint32_t rounded = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
     const uint32_t quiet = (b >> 16) | 0x40u;
     return v != v ? quiet : rounded;
 }
 
+// The same rounding on the hardware conversion (v_cvt_pk_bf16_f32, what a
+// cast to __bf16 compiles to on gfx950): equal to f32_to_bf16_int for all
+// 2^32 inputs, NaNs included (q38m_debug_bf16_sweep checks every pattern
+// on the device).
+__device__ __forceinline__ uint32_t f32_to_bf16(float v) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+}
+
 // the same rounding, the result widened back to fp32
 __device__ __forceinline__ float bf16_round(float v) {
-    const uint32_t b = __float_as_uint(v);
-    const uint32_t rounded = (b + 0x7fffu + ((b >> 16) & 1u)) & 0xffff0000u;
-    const uint32_t quiet = (b & 0xffff0000u) | 0x00400000u;
-    return __uint_as_float(v != v ? quiet : rounded);
+    return bf16_to_f32(f32_to_bf16(v));
 }
 
 // Exact binary16 -> binary32 through the hardware conversion.

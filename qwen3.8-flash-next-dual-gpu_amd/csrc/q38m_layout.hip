@@ -273,6 +273,37 @@ __global__ void debug_expf_kernel(const float* __restrict__ x, uint32_t n, float
 // One v_mfma_i32_16x16x32_i8 with A (16x32) and B (32x16) given row-major
 // in memory, loaded in the operand layout the kernels assume; D (16x16) is
 // written row-major from the assumed result layout.
+// Every fp32 bit pattern through the hardware bf16 conversion
+// (v_cvt_pk_bf16_f32, what a cast to __bf16 compiles to on gfx950) and the
+// integer round-to-nearest-even of f32_to_bf16_int; result = {mismatches, first
+// mismatching pattern, mismatches on non-NaN inputs, first such pattern}.
+__global__ __launch_bounds__(256) void debug_bf16_kernel(uint32_t* __restrict__ result) {
+    uint32_t bad = 0u, first = 0xffffffffu, bad_num = 0u, first_num = 0xffffffffu;
+    const uint64_t stride = static_cast<uint64_t>(gridDim.x) * 256u;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; i < (1ull << 32);
+         i += stride) {
+        const uint32_t bits = static_cast<uint32_t>(i);
+        const float v = __uint_as_float(bits);
+        const uint32_t hw = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+        if (hw != f32_to_bf16_int(v)) {
+            ++bad;
+            first = min(first, bits);
+            if (v == v) {
+                ++bad_num;
+                first_num = min(first_num, bits);
+            }
+        }
+    }
+    if (bad != 0u) {
+        atomicAdd(&result[0], bad);
+        atomicMin(&result[1], first);
+    }
+    if (bad_num != 0u) {
+        atomicAdd(&result[2], bad_num);
+        atomicMin(&result[3], first_num);
+    }
+}
+
 __global__ void debug_mfma_kernel(const int8_t* __restrict__ a, const int8_t* __restrict__ b,
                                   int32_t* __restrict__ d) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -388,6 +419,11 @@ hipError_t launch_synth(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t cou
 
 hipError_t launch_debug_expf(const float* x, uint32_t n, float* out, hipStream_t stream) {
     debug_expf_kernel<<<blocks_for(n, 256), 256, 0, stream>>>(x, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_debug_bf16(uint32_t* result, hipStream_t stream) {
+    debug_bf16_kernel<<<4096, 256, 0, stream>>>(result);
     return hipGetLastError();
 }
 

@@ -496,6 +496,279 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
     }
 }
 
+// ---- gate/up, W4 groups of 32, on fp16 MFMA --------------------------------
+//
+// The int8 values of both operands (activations in [-127, 127], W4 nibbles
+// as 16 * w in [-128, 112]) are exact in fp16, their products (< 2^14) and
+// every partial sum of a 32-wide group (< 2^19) exact in fp32, so
+// v_mfma_f32_16x16x32_f16 returns (float)(16 * acc_g) itself -- the value
+// the int8 MFMA path recovers with one extra VALU op per accumulator element
+// and group.  The chain step is then a single v_fma_f32, and the MFMA runs
+// at the same 16 cycles as v_mfma_i32_16x16x32_i8.
+//
+// fp16 images.  Weights (MFMA16 W4 word: byte i = k_i | k_{4+i} << 4):
+// x = d ^ 0x88888888 makes each nibble w + 8; (x >> {0, 8, 4}) or (x << 4)
+// masked to bits 4-7 and 20-23 and put under the exponent bits of 1024
+// (0x6400) is 1024 + 16 * (w + 8) exactly, two values per word, and one
+// v_pk_add_f16 of -1152 leaves 16 * w.  A lane's eight K values come out
+// in the order (4, 6), (5, 7), (0, 2), (1, 3).  Activations: one
+// v_cvt_f16_i16 per sign-extended byte, written into the same order when
+// the rows are staged (a dot product does not depend on the order of its
+// K terms, only on A and B agreeing).
+__device__ __forceinline__ uint32_t pk_sub1152(uint32_t v) {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    const h2_t r = __builtin_bit_cast(h2_t, v) + h2_t{static_cast<_Float16>(-1152.0f),
+                                                       static_cast<_Float16>(-1152.0f)};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// one MFMA16 W4 word (byte i = k_i | k_{4+i} << 4) -> 16 * w as fp16, K
+// order (4, 6), (5, 7), (0, 2), (1, 3)
+__device__ __forceinline__ uint4 w4_to_f16x16(uint32_t d) {
+    constexpr uint32_t kMask = 0x00F000F0u, kExp = 0x64006400u;
+    const uint32_t x = d ^ 0x88888888u;
+    return make_uint4(pk_sub1152((x & kMask) | kExp), pk_sub1152(((x >> 8) & kMask) | kExp),
+                      pk_sub1152(((x << 4) & kMask) | kExp), pk_sub1152(((x >> 4) & kMask) | kExp));
+}
+
+// bytes 0 and 2 (or 1 and 3) of v as signed integers -> two fp16 (exact):
+// v_cvt_f16_i16 with a sign-extended byte source selected by SDWA, the
+// second conversion writing the high half and keeping the low one
+__device__ __forceinline__ uint32_t sbytes02_to_f16(uint32_t v) {
+    uint32_t r;
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_2"
+        : "=&v"(r)
+        : "v"(v));
+    return r;
+}
+__device__ __forceinline__ uint32_t sbytes13_to_f16(uint32_t v) {
+    uint32_t r;
+    asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+        : "=&v"(r)
+        : "v"(v));
+    return r;
+}
+
+// eight int8 (k 0-3 in lo, 4-7 in hi) -> fp16 in the order of w4_to_f16x16
+__device__ __forceinline__ uint4 i8_to_f16(uint32_t lo, uint32_t hi) {
+    return make_uint4(sbytes02_to_f16(hi), sbytes13_to_f16(hi), sbytes02_to_f16(lo),
+                      sbytes13_to_f16(lo));
+}
+
+__device__ __forceinline__ v4f mfma_f16_16x16x32(uint4 a, uint4 b, v4f c) {
+    typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
+                                                  __builtin_bit_cast(h8_t, b), c, 0, 0, 0);
+}
+
+// A workgroup of 8 waves covers 8 gate/up channel pairs (128 + 128
+// channels) of one task; wave p owns pair p for all of the task's row tiles
+// (1, 2, 4 or 8 of 16 rows, a compile-time choice per task), so each weight
+// fragment, converted once per wave, feeds up to 8 MFMAs.  The workgroup
+// stages half a quad (64 columns of K, two scale groups) at a time into a
+// double-buffered LDS image of 26 KB: the task's rows as fp16 MFMA
+// fragments, its 16 weight tiles and their scale words; every thread loads
+// one 16-byte row piece, two 8-byte weight pieces and (half of them) one
+// scale word a step ahead and converts the row piece when it stores it.
+// The barrier between steps waits for LDS operations only.  Two workgroups
+// share a CU (8 waves each at 4 waves per SIMD), so one's barriers,
+// prologue and epilogue overlap the other's MFMAs.  fp16 scales carry
+// 16 * y, bf16 scales take s / 16, as in the int8 kernel above; the
+// epilogue is the same.
+template <uint32_t H, uint32_t I, bool kBf16>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+                              const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                              const uint32_t* __restrict__ packed,
+                              const float* __restrict__ route_weights,
+                              const q38m_task_v1* __restrict__ tasks,
+                              const uint32_t* __restrict__ live_tasks, uint16_t* __restrict__ mid) {
+    constexpr uint32_t kHalves = H / 64u;  // staging steps
+    constexpr uint32_t kTilesAll = 2u * I / 16u;
+    constexpr uint32_t kWgTiles = 16u;  // 8 pairs
+    static_assert(kHalves % 2u == 0u, "steps run in pairs of LDS buffers");
+    // per buffer: A [K step j][row tile][lane] fp16 fragments (16 B), the
+    // workgroup's 16 weight tiles [tile][K step j][lane] (one word: eight
+    // nibbles) and their scale words [tile][channel] (two groups)
+    __shared__ __align__(16) uint4 a_lds[2][2u * kRowTiles * 64u];
+    __shared__ __align__(16) uint32_t w_lds[2][kWgTiles * 2u * 64u];
+    __shared__ __align__(16) uint32_t s_lds[2][kWgTiles * 16u];
+    __shared__ float2 row_info[kWideRows];  // (token scale, route weight)
+
+    Placement at;
+    if (!place_on_xcds(live_tasks, at)) return;
+    const q38m_task_v1 task = tasks[at.task];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t pr = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t n = lane & 15u, qh = lane >> 4;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+    const uint32_t tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
+
+    // staging: row piece (row tid/4, 16-byte chunk tid%4 of the step's 64
+    // bytes), weight pieces (tiles tid/64 and 8 + tid/64, lane tid%64: the
+    // step's two words of the quad's four), scale piece (tile, channel) =
+    // tid for tid < 256 (the step's two group words of the quad's four)
+    const uint32_t sr = tid >> 2, sch = tid & 3u;
+    const bool alive = sr < rows;
+    const uint32_t assignment = alive ? packed[p0 + sr] : 0u;
+    if (sch == 0u && alive)
+        row_info[sr] = make_float2(xs[assignment / kTopK], route_weights[assignment]);
+    const uint4* a_src =
+        reinterpret_cast<const uint4*>(xq + static_cast<size_t>(assignment / kTopK) * H) + sch;
+    const uint32_t a_at = ((sch >> 1) * kRowTiles + (sr >> 4)) * 64u + (sch & 1u) * 32u + (sr & 15u);
+    const size_t slot0 = static_cast<size_t>(e) * (H / 128u) * kTilesAll + at.slice * kWgTiles;
+    const uint2* w_src = reinterpret_cast<const uint2*>(w + slot0 * 64u + tid);
+    const uint32_t* s_src = reinterpret_cast<const uint32_t*>(s) + slot0 * 32u + 2u * tid;
+    const bool s_thread = tid < kWgTiles * 16u;
+    struct Stage {
+        uint4 a;
+        uint2 w0, w1;
+        uint32_t s;
+    };
+    // step h: quad h/2, words 2(h%2), 2(h%2)+1 of each weight piece and
+    // scale record
+    auto load_stage = [&](uint32_t h) __attribute__((always_inline)) {
+        Stage st;
+        st.a = alive ? a_src[h * 4u] : make_uint4(0u, 0u, 0u, 0u);
+        const uint2* wq = w_src + (static_cast<size_t>(h >> 1) * kTilesAll * 64u) * 2u + (h & 1u);
+        st.w0 = wq[0];
+        st.w1 = wq[8u * 64u * 2u];
+        st.s = s_thread ? s_src[static_cast<size_t>(h >> 1) * kTilesAll * 32u + (h & 1u)] : 0u;
+        return st;
+    };
+    auto store_stage = [&](const Stage& st, uint32_t buffer) __attribute__((always_inline)) {
+        a_lds[buffer][a_at] = i8_to_f16(st.a.x, st.a.y);
+        a_lds[buffer][a_at + 16u] = i8_to_f16(st.a.z, st.a.w);
+        const uint32_t w_at = (tid >> 6) * 128u + lane;
+        w_lds[buffer][w_at] = st.w0.x;
+        w_lds[buffer][w_at + 64u] = st.w0.y;
+        w_lds[buffer][w_at + 8u * 128u] = st.w1.x;
+        w_lds[buffer][w_at + 8u * 128u + 64u] = st.w1.y;
+        if (s_thread) s_lds[buffer][tid] = st.s;
+    };
+
+    float y[kRowTiles][2][4];
+#pragma unroll
+    for (uint32_t t = 0; t < kRowTiles; ++t)
+#pragma unroll
+        for (uint32_t u = 0; u < 2u; ++u)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) y[t][u][i] = 0.0f;
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    // One step for kNt row tiles: per K step (= scale group) the pair's two
+    // weight fragments are converted once; chain k = (row tile, gate/up),
+    // tile t+1's A fragment read one chain ahead, each chain's fma step
+    // issued after the next chain's MFMA.
+    auto multiply = [&](auto ntiles, uint32_t buffer) __attribute__((always_inline)) {
+        constexpr uint32_t kNt = decltype(ntiles)::value;
+        constexpr uint32_t kChains = 2u * kNt * 2u;
+        const uint4* abuf = a_lds[buffer] + lane;
+        const uint16_t* srow = reinterpret_cast<const uint16_t*>(s_lds[buffer]) +
+                               ((2u * pr) * 16u + n) * 2u;  // up: + 32 words
+        const uint32_t* wrow = w_lds[buffer] + (2u * pr) * 128u + lane;  // up: + 128
+        uint4 fa[2];
+        uint4 bf[2];
+        float sc[2];
+        v4f d[2];
+        auto issue = [&](uint32_t k) __attribute__((always_inline)) {
+            const uint32_t m = k / 2u, u = k & 1u;
+            const uint32_t j = m / kNt, t = m % kNt;
+            if (u == 0u) {
+                if (t == 0u) {
+                    bf[0] = w4_to_f16x16(wrow[j * 64u]);
+                    bf[1] = w4_to_f16x16(wrow[128u + j * 64u]);
+                }
+                if (m + 1u < 2u * kNt) {
+                    const uint32_t jn = (m + 1u) / kNt, tn = (m + 1u) % kNt;
+                    fa[(m + 1u) & 1u] = abuf[(jn * kRowTiles + tn) * 64u];
+                }
+            }
+            d[k & 1u] = mfma_f16_16x16x32(fa[m & 1u], bf[u], zero);
+        };
+        auto step = [&](uint32_t k) __attribute__((always_inline)) {
+            const uint32_t m = k / 2u, u = k & 1u;
+            const uint32_t j = m / kNt, t = m % kNt;
+            if (t == 0u) {
+                const uint32_t word = srow[u * 32u + j];
+                sc[u] = kBf16 ? bf16_to_f32(word) * 0.0625f : f16_to_f32(word);
+                asm volatile("" : "+v"(sc[u]));  // a plain v_fma_f32, not v_fma_mix
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i)
+                y[t][u][i] = __builtin_fmaf(d[k & 1u][i], sc[u], y[t][u][i]);
+            // keep the step between the MFMAs it follows and precedes
+            asm volatile("" : "+v"(y[t][u][0]), "+v"(y[t][u][1]), "+v"(y[t][u][2]),
+                         "+v"(y[t][u][3]));
+        };
+        fa[0] = abuf[0];
+#pragma unroll
+        for (uint32_t k = 0; k <= kChains; ++k) {
+            if (k < kChains) issue(k);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k > 0u) step(k - 1u);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    // step h: loaded at the start of step h-1, stored at its end into LDS
+    // buffer h%2, multiplied during step h; the loop is instantiated per
+    // row-tile count, every instance passing the same barriers
+    {
+        const Stage first = load_stage(0);
+        store_stage(first, 0u);
+    }
+    __syncthreads();
+    auto k_loop = [&](auto ntiles) __attribute__((always_inline)) {
+#pragma unroll 1
+        for (uint32_t h = 0; h < kHalves; h += 2u) {
+            Stage next = load_stage(h + 1u);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(ntiles, 0u);
+            store_stage(next, 1u);
+            lds_barrier();
+            if (h + 2u < kHalves) next = load_stage(h + 2u);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(ntiles, 1u);
+            if (h + 2u < kHalves) store_stage(next, 0u);
+            lds_barrier();
+        }
+    };
+    if (tiles > 4u)
+        k_loop(std::integral_constant<uint32_t, 8>{});
+    else if (tiles > 2u)
+        k_loop(std::integral_constant<uint32_t, 4>{});
+    else if (tiles > 1u)
+        k_loop(std::integral_constant<uint32_t, 2>{});
+    else
+        k_loop(std::integral_constant<uint32_t, 1>{});
+
+    // SwiGLU: D lane (qh, n) holds rows 4qh + i of each tile, channel n
+    const uint32_t channel = (at.slice * 8u + pr) * 16u + n;
+    const float unscale = kBf16 ? 1.0f : 0.0625f;
+#pragma unroll
+    for (uint32_t t = 0; t < kRowTiles; ++t) {
+        if (16u * t >= rows) break;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 16u * t + 4u * qh + i;
+            if (r >= rows) continue;
+            const float2 info = row_info[r];
+            const float yg = (y[t][0][i] * unscale) * info.x;
+            const float yu = (y[t][1][i] * unscale) * info.x;
+            mid[static_cast<size_t>(p0 + r) * I + channel] =
+                static_cast<uint16_t>(swiglu_fold(yg, yu, info.y));
+        }
+    }
+}
+
 // Gate/up, W8 (paired K-block-major layout; the reference's edge-layer
 // format) over a task of up to 128 rows: the W4 kernel's plan with 64-wide
 // K blocks -- 16 waves (8 gate tiles, 8 up tiles), one tile per wave for
@@ -1095,6 +1368,15 @@ template <uint32_t kSub, bool kBf16>
 void launch_gate_up_wide_sub(const q38m_expert_weights_v1& w, const int8_t* xq, const float* xs,
                              const uint32_t* packed, const float* route_weights,
                              const TaskSlots& t, uint16_t* weighted_mid, hipStream_t stream) {
+    if constexpr (kSub == 1u) {
+        // fp16 MFMA form: 8 channel pairs (256 rows of gate/up) per workgroup
+        const dim3 grid(kInter / 16u / 8u, t.count);
+        gate_up_w4g32_f16_kernel<kHidden, kInter, kBf16>
+            <<<grid, 512, 0, stream>>>(static_cast<const uint4*>(w.data),
+                                        static_cast<const uint16_t*>(w.scales), xq, xs, packed,
+                                        route_weights, t.tasks, t.live, weighted_mid);
+        return;
+    }
     // 8 channel pairs (256 rows of gate/up) per workgroup
     const dim3 grid(kInter / 16u / 8u, t.count);
     gate_up_w4_wide_kernel<kHidden, kInter, kSub, kBf16>

@@ -36,7 +36,8 @@ def test_library_exports_every_declared_symbol(q38m):
 def test_product_header_declares_no_self_checks():
     product = declared_functions(HEADERS[:1])
     assert not [n for n in product if n.startswith("q38m_debug")]
-    assert declared_functions(HEADERS[1:]) == ["q38m_debug_expf", "q38m_debug_mfma_16x16x32_i8",
+    assert declared_functions(HEADERS[1:]) == ["q38m_debug_bf16_sweep", "q38m_debug_expf",
+                                               "q38m_debug_mfma_16x16x32_i8",
                                                "q38m_debug_mfma_32x32x32_i8"]
 
 

@@ -63,6 +63,19 @@ def test_expf_bitwise(q38m, orc):
     assert np.array_equal(got.view(np.uint32), orc.expf(x).view(np.uint32))
 
 
+def test_bf16_hardware_conversion_sweep(q38m):
+    """Every fp32 bit pattern: the hardware conversion (v_cvt_pk_bf16_f32)
+    against the contract's integer round-to-nearest-even, on the device."""
+    t = torch()
+    result = device(np.array([0, 0xFFFFFFFF, 0, 0xFFFFFFFF], np.uint32).view(np.int32))
+    q38m.call("q38m_debug_bf16_sweep", result.data_ptr(), stream(), 0)
+    got = host(result, np.int32).view(np.uint32)
+    print(f"bf16 sweep: mismatches {got[0]} (first {got[1]:#010x}), "
+          f"non-NaN mismatches {got[2]} (first {got[3]:#010x})")
+    assert got[2] == 0, f"non-NaN mismatch at {got[3]:#010x}"
+    assert got[0] == 0, f"NaN mismatch at {got[1]:#010x}"
+
+
 @pytest.mark.parametrize("kind", ["normal_f32", "bias_f32", "bf16", "abs_f16", "w4", "i8"])
 def test_synth_matches_oracle(q38m, orc, kind):
     t = torch()
