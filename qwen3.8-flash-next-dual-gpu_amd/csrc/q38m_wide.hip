@@ -1336,6 +1336,189 @@ void down_w4_wide_kernel(
         run(std::integral_constant<uint32_t, 1>{});
 }
 
+// Down, W4 groups of 32, on fp16 MFMA (see the gate/up kernel above for
+// why the products are exact): a workgroup of 8 waves covers 16 output
+// tiles of one task, two adjacent tiles per wave over all of the task's row
+// tiles, so a row's 128-byte output line leaves one wave in two
+// consecutive stores.  The mid rows are staged 64 columns at a time as fp16
+// fragments in a double-buffered LDS image (16 KB per buffer); each wave
+// streams its two tiles' weights and scale words one step ahead from
+// global memory and converts each weight fragment once for all row tiles.
+// The chain is the int8 kernel's: y = fmaf((float)acc_g, s_g / 16, y) in
+// group order, then y * s_row.
+template <uint32_t H, uint32_t I, bool kBf16>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
+void down_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+                           const int8_t* __restrict__ mq, const float* __restrict__ ms,
+                           const q38m_task_v1* __restrict__ tasks,
+                           const uint32_t* __restrict__ live_tasks, float* __restrict__ out) {
+    constexpr uint32_t kSteps = I / 64u;
+    constexpr uint32_t kTiles = H / 16u;
+    static_assert(kSteps % 2u == 0u, "steps run in pairs of LDS buffers");
+    __shared__ __align__(16) uint4 a_lds[2][2u * kRowTiles * 64u];
+    __shared__ float row_scale[kWideRows];
+
+    Placement at;
+    if (!place_on_xcds(live_tasks, at)) return;
+    const q38m_task_v1 task = tasks[at.task];
+    const uint32_t rows = task.valid_rows;
+    if (rows == 0u) return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t n = lane & 15u, qh = lane >> 4;
+    const uint32_t e = task.expert;
+    const uint32_t p0 = task.packed_begin;
+    const uint32_t tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
+
+    // staging: row piece (row tid/4, 16-byte chunk tid%4 of the step's 64
+    // bytes); the task's mid rows are contiguous
+    const uint32_t sr = tid >> 2, sch = tid & 3u;
+    const bool alive = sr < rows;
+    const uint4* a_src =
+        reinterpret_cast<const uint4*>(mq + static_cast<size_t>(p0 + (alive ? sr : 0u)) * I) + sch;
+    const uint32_t a_at = ((sch >> 1) * kRowTiles + (sr >> 4)) * 64u + (sch & 1u) * 32u + (sr & 15u);
+    if (tid < kWideRows) row_scale[tid] = tid < rows ? ms[p0 + tid] : 0.0f;
+    auto load_a = [&](uint32_t h) __attribute__((always_inline)) {
+        return alive ? a_src[h * 4u] : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto store_a = [&](const uint4& v, uint32_t buffer) __attribute__((always_inline)) {
+        a_lds[buffer][a_at] = i8_to_f16(v.x, v.y);
+        a_lds[buffer][a_at + 16u] = i8_to_f16(v.z, v.w);
+    };
+
+    // this wave's tiles tile0, tile0 + 1; quad-major layout: quad kq of tile
+    // t is unit kq * kTiles + t of the expert, four K steps (one word each)
+    // per lane and four scale words per channel; step h takes words
+    // 2(h%2), 2(h%2)+1 of quad h/2
+    const uint32_t tile0 = (at.slice * 8u + wave) * 2u;
+    const size_t unit0 = static_cast<size_t>(e) * (I / 128u) * kTiles + tile0;
+    const uint2* wsrc = reinterpret_cast<const uint2*>(w + unit0 * 64u + lane);
+    const uint32_t* ssrc = reinterpret_cast<const uint32_t*>(s + (unit0 * 16u + n) * 4u);
+    struct Step {
+        uint2 w0, w1;
+        uint32_t s0, s1;
+    };
+    auto load_w = [&](uint32_t h) __attribute__((always_inline)) {
+        const size_t unit = static_cast<size_t>(h >> 1) * kTiles;
+        Step st;
+        st.w0 = wsrc[unit * 128u + (h & 1u)];
+        st.w1 = wsrc[(unit + 1u) * 128u + (h & 1u)];
+        st.s0 = ssrc[unit * 32u + (h & 1u)];
+        st.s1 = ssrc[(unit + 1u) * 32u + (h & 1u)];
+        return st;
+    };
+
+    float y[kRowTiles][2][4];
+#pragma unroll
+    for (uint32_t t = 0; t < kRowTiles; ++t)
+#pragma unroll
+        for (uint32_t u = 0; u < 2u; ++u)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) y[t][u][i] = 0.0f;
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    // one step (two groups) for kNt row tiles; chain k = (group j, row tile
+    // t, tile u) as in the gate/up kernel
+    auto multiply = [&](auto ntiles, uint32_t buffer, const Step& ws)
+                        __attribute__((always_inline)) {
+        constexpr uint32_t kNt = decltype(ntiles)::value;
+        constexpr uint32_t kChains = 2u * kNt * 2u;
+        const uint4* abuf = a_lds[buffer] + lane;
+        const uint32_t wj[2][2] = {{ws.w0.x, ws.w0.y}, {ws.w1.x, ws.w1.y}};
+        const uint32_t sj[2] = {ws.s0, ws.s1};
+        uint4 fa[2];
+        uint4 bf[2];
+        float sc[2];
+        v4f d[2];
+        auto issue = [&](uint32_t k) __attribute__((always_inline)) {
+            const uint32_t m = k / 2u, u = k & 1u;
+            const uint32_t j = m / kNt, t = m % kNt;
+            if (u == 0u) {
+                if (t == 0u) {
+                    bf[0] = w4_to_f16x16(wj[0][j]);
+                    bf[1] = w4_to_f16x16(wj[1][j]);
+                }
+                if (m + 1u < 2u * kNt) {
+                    const uint32_t jn = (m + 1u) / kNt, tn = (m + 1u) % kNt;
+                    fa[(m + 1u) & 1u] = abuf[(jn * kRowTiles + tn) * 64u];
+                }
+            }
+            d[k & 1u] = mfma_f16_16x16x32(fa[m & 1u], bf[u], zero);
+        };
+        auto step = [&](uint32_t k) __attribute__((always_inline)) {
+            const uint32_t m = k / 2u, u = k & 1u;
+            const uint32_t j = m / kNt, t = m % kNt;
+            if (t == 0u) {
+                const uint32_t word = j ? sj[u] >> 16 : sj[u] & 0xffffu;
+                sc[u] = (kBf16 ? bf16_to_f32(word) : f16_to_f32(word)) * 0.0625f;
+                asm volatile("" : "+v"(sc[u]));
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i)
+                y[t][u][i] = __builtin_fmaf(d[k & 1u][i], sc[u], y[t][u][i]);
+            asm volatile("" : "+v"(y[t][u][0]), "+v"(y[t][u][1]), "+v"(y[t][u][2]),
+                         "+v"(y[t][u][3]));
+        };
+        fa[0] = abuf[0];
+#pragma unroll
+        for (uint32_t k = 0; k <= kChains; ++k) {
+            if (k < kChains) issue(k);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k > 0u) step(k - 1u);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    store_a(load_a(0), 0u);
+    Step cur = load_w(0);
+    __syncthreads();
+    auto k_loop = [&](auto ntiles) __attribute__((always_inline)) {
+#pragma unroll 1
+        for (uint32_t h = 0; h < kSteps; h += 2u) {
+            uint4 a_next = load_a(h + 1u);
+            Step nxt = load_w(h + 1u);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(ntiles, 0u, cur);
+            store_a(a_next, 1u);
+            lds_barrier();
+            cur = nxt;
+            if (h + 2u < kSteps) {
+                a_next = load_a(h + 2u);
+                nxt = load_w(h + 2u);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(ntiles, 1u, cur);
+            if (h + 2u < kSteps) store_a(a_next, 0u);
+            lds_barrier();
+            cur = nxt;
+        }
+    };
+    if (tiles > 4u)
+        k_loop(std::integral_constant<uint32_t, 8>{});
+    else if (tiles > 2u)
+        k_loop(std::integral_constant<uint32_t, 4>{});
+    else if (tiles > 1u)
+        k_loop(std::integral_constant<uint32_t, 2>{});
+    else
+        k_loop(std::integral_constant<uint32_t, 1>{});
+
+    const uint32_t channel = tile0 * 16u + n;
+#pragma unroll
+    for (uint32_t t = 0; t < kRowTiles; ++t) {
+        if (16u * t >= rows) break;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t row = 16u * t + 4u * qh + i;
+            if (row >= rows) continue;
+            float* dst = out + static_cast<size_t>(p0 + row) * H + channel;
+            dst[0] = y[t][0][i] * row_scale[row];
+            dst[16] = y[t][1][i] * row_scale[row];
+        }
+    }
+}
+
 }  // namespace
 
 uint32_t wide_chunks(uint32_t tokens) {
@@ -1404,6 +1587,15 @@ template <uint32_t kSub, bool kBf16>
 void launch_down_w4_wide_sub(const q38m_expert_weights_v1& w, const int8_t* mid_q,
                              const float* mid_s, const TaskSlots& t, float* route_output,
                              hipStream_t stream) {
+    if constexpr (kSub == 1u) {
+        // fp16 MFMA form: 16 output tiles per 8-wave workgroup
+        const dim3 grid(kHidden / 16u / 16u, t.count);
+        down_w4g32_f16_kernel<kHidden, kInter, kBf16>
+            <<<grid, 512, 0, stream>>>(static_cast<const uint4*>(w.data),
+                                       static_cast<const uint16_t*>(w.scales), mid_q, mid_s,
+                                       t.tasks, t.live, route_output);
+        return;
+    }
     constexpr uint32_t kWaves = 16, kTilesPerWave = 2;
     const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), t.count);
     down_w4_wide_kernel<kHidden, kInter, kWaves, kTilesPerWave, kSub, kBf16>
