@@ -21,7 +21,7 @@ After the timed runs, two child processes of this file run under
 rocprofv3 --pmc (config-2 slab; chunk workloads) and the line carries
 the counter-derived MFMA busy fraction and int8 rate of the headline and
 chunk GEMMs beside the algorithmic ones (skipped with --no-counters or
-without rocprofv3).  --pmc-report {slab,chunk,decode} prints the full
+without rocprofv3).  --pmc-report {slab,chunk,decode,dense} prints the full
 counter and HBM-traffic tables of one workload instead.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
@@ -35,6 +35,7 @@ import ctypes
 import importlib.util
 import json
 import os
+import re
 import shutil
 import signal
 import statistics
@@ -65,8 +66,8 @@ def load(name, path, package_dir=None):
 # One counter set per child process (rocprofv3 does not split counters over
 # passes).  Per dispatch the CSV holds each counter summed over its hardware
 # instances (SQ counters over all SIMDs, GRBM_GUI_ACTIVE over the 8 XCCs).
-PMC_MFMA = ("SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_INSTS_VALU "
-            "SQ_INSTS_MFMA SQ_ACTIVE_INST_VALU SQ_WAVES SQ_INSTS_LDS GRBM_GUI_ACTIVE")
+PMC_MFMA = ("SQ_INSTS_VALU_MFMA_MOPS_I8 SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_VALU_MFMA_BUSY_CYCLES "
+            "SQ_BUSY_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_WAVES SQ_INSTS_LDS GRBM_GUI_ACTIVE")
 PMC_WAITS = ("SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_WAVE_CYCLES SQ_LDS_BANK_CONFLICT SQ_ACTIVE_INST_LDS "
              "SQ_INST_CYCLES_VMEM_RD SQ_ACTIVE_INST_MISC SQ_INSTS_SALU GRBM_GUI_ACTIVE")
 # the child runs that each counter pass profiles
@@ -77,25 +78,32 @@ PMC_WORKLOADS = {
              "--steps 2 --warmup 1",
     "decode": "--no-cpu --no-quantizer --no-dense --no-chunks --no-hyper --no-stack --no-formats "
               "--steps 3 --warmup 1 --decode-tokens 4",
+    "dense": "--no-cpu --no-decode --no-quantizer --no-chunks --no-stack --no-formats "
+             "--steps 10 --warmup 2",
 }
 VALU_CYCLES = 4  # issue cycles of one non-packed wave64 VALU instruction on a SIMD
 
 
 def _short_kernel(name):
-    name = name.replace("void ", "").replace("q38m::(anonymous namespace)::", "")
+    name = name.replace("void ", "")
+    # enum template arguments print as (q38m::(anonymous namespace)::Enum)N
+    name = re.sub(r"\(q38m::\(anonymous namespace\)::(\w+)\)(\d+)", r"\1=\2", name)
+    name = name.replace("q38m::(anonymous namespace)::", "")
     return name.split("(")[0]
 
 
 def pmc_run(counters, workload, extra=""):
-    """Run this file under rocprofv3 --pmc COUNTERS as a child process on the
-    named workload; returns ({(kernel, grid): {counter: [per dispatch]},
-    "_duration_us": [...]}, agent dict), or None when rocprofv3 is absent or
-    the run fails (the parent's own results stand either way)."""
+    """Run this file under rocprofv3 --pmc COUNTERS (or, for counters=None,
+    --kernel-trace) as a child process on the named workload; returns
+    ({(kernel, grid): {counter: [per dispatch]}, "_duration_us": [...]},
+    agent dict), or None when rocprofv3 is absent or the run fails (the
+    parent's own results stand either way)."""
     exe = shutil.which("rocprofv3")
     if exe is None:
         return None
     out = tempfile.mkdtemp(prefix="q38m_pmc_", dir="/tmp")
-    cmd = [exe, "--pmc", *counters.split(), "-f", "csv", "-d", out, "-o", "pmc", "--",
+    mode = ["--kernel-trace"] if counters is None else ["--pmc", *counters.split()]
+    cmd = [exe, *mode, "-f", "csv", "-d", out, "-o", "pmc", "--",
            sys.executable, os.path.join(ROOT, "bench.py"), "--no-counters",
            *PMC_WORKLOADS[workload].split(), *extra.split()]
     env = dict(os.environ, TMPDIR="/tmp")
@@ -121,6 +129,14 @@ def pmc_run(counters, workload, extra=""):
                             key = (r["Kernel_Name"], int(r["Grid_Size"]), r["Dispatch_Id"])
                             per[key][r["Counter_Name"]] += float(r["Counter_Value"])
                             meta[key] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+                elif f.endswith("kernel_trace.csv"):
+                    with open(full) as fh:
+                        for r in csv.DictReader(fh):
+                            grid = (int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) *
+                                    int(r["Grid_Size_Z"]))
+                            key = (r["Kernel_Name"], grid, r["Dispatch_Id"])
+                            per[key]["_trace"] = 1.0
+                            meta[key] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
                 elif f.endswith("agent_info.csv"):
                     with open(full) as fh:
                         for r in csv.DictReader(fh):
@@ -145,14 +161,20 @@ def mfma_metrics(cs, agent):
     gui = m("GRBM_GUI_ACTIVE") / agent["xccs"]  # busy cycles of one XCC
     mfma = m("SQ_INSTS_MFMA")
     dur = m("_duration_us")
-    ops = m("SQ_INSTS_VALU_MFMA_MOPS_I8") * 512.0
+    # the W4 g32 chunk kernels run the contract's int8 products on fp16 MFMA
+    # (exact there), so their MACs count under MOPS_F16
+    i8 = m("SQ_INSTS_VALU_MFMA_MOPS_I8") * 512.0
+    f16 = m("SQ_INSTS_VALU_MFMA_MOPS_F16") * 512.0 if "SQ_INSTS_VALU_MFMA_MOPS_F16" in cs else 0.0
+    ops = i8 + f16
     valu = m("SQ_INSTS_VALU") - mfma
     return {"launches": len(cs["_duration_us"]), "avg_us": round(dur, 2),
             "gui_active_cycles_per_xcc": round(gui),
             "mfma_busy_frac": round(m("SQ_VALU_MFMA_BUSY_CYCLES") / (gui * agent["simds"]), 4),
+            "mfma_type": "fp16" if f16 > i8 else "int8",
             "int8_ops_counter": ops,
             "int8_tops_counter": round(ops / (dur * 1e-6) / 1e12, 2),
             "int8_peak_frac_counter": round(ops / (dur * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4),
+            "fp16_peak_frac_counter": round(f16 / (dur * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4),
             "mfma_insts": mfma,
             "valu_insts_per_mfma": round(valu / mfma, 2) if mfma else None,
             "valu_issue_share_est": round(valu * VALU_CYCLES / (gui * agent["simds"]), 4)}
@@ -171,7 +193,10 @@ def counters_summary():
     kernels on a config-5 layer, one child run each."""
     out = {"source": "rocprofv3 --pmc " + PMC_MFMA + " -- python3 bench.py --no-counters <workload>",
            "formulas": {"mfma_busy_frac": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCCs x SIMDs)",
-                        "int8_tops_counter": "SQ_INSTS_VALU_MFMA_MOPS_I8 x 512 / launch duration",
+                        "int8_tops_counter": "(SQ_INSTS_VALU_MFMA_MOPS_I8 + "
+                                             "SQ_INSTS_VALU_MFMA_MOPS_F16) x 512 / launch duration "
+                                             "(the *_f16_kernel GEMMs run the int8 contract's "
+                                             "products exactly on fp16 MFMA)",
                         "valu_issue_share_est": f"(SQ_INSTS_VALU - SQ_INSTS_MFMA) x {VALU_CYCLES} / "
                                                 "(GRBM_GUI_ACTIVE / XCCs x SIMDs)"}}
     slab = pmc_run(PMC_MFMA, "slab")
@@ -186,7 +211,7 @@ def counters_summary():
     if chunk:
         agg, agent = chunk
         out["workload_chunk"] = PMC_WORKLOADS["chunk"]
-        for k in ("gate_up_w4_wide_kernel", "down_w8_wide_kernel", "down_w4_wide_kernel"):
+        for k in ("gate_up_w4g32_f16_kernel", "down_w8_wide_kernel", "down_w4g32_f16_kernel"):
             hit = pick(agg, k, largest_grid=True)
             if hit:
                 out[f"{k} (config-5 layer)"] = dict(grid=hit[0], **mfma_metrics(hit[1], agent))
@@ -203,20 +228,27 @@ def _copy_scale(agg, counter, mib):
     return (mib << 20) / (statistics.median(cs[counter]) * 1024.0)
 
 
-def pmc_report(workload):
-    """Markdown counter report of one workload: MFMA/VALU counters, wait
-    counters and calibrated HBM traffic per kernel of this library."""
+def pmc_report(workload, traffic_dir=None):
+    """Markdown report of one workload: kernel trace (durations), MFMA/VALU
+    counters, wait counters and calibrated HBM traffic per kernel of this
+    library.  With traffic_dir, the slab workload's gate/up and down traffic
+    is also written there as <kernel>_config2_traffic.json (read back by the
+    bench line's roofline.traffic)."""
     mib = 256
-    runs = {"mfma": pmc_run(PMC_MFMA, workload), "waits": pmc_run(PMC_WAITS, workload),
+    runs = {"trace": pmc_run(None, workload), "mfma": pmc_run(PMC_MFMA, workload),
+            "waits": pmc_run(PMC_WAITS, workload),
             "fetch": pmc_run("FETCH_SIZE", workload, f"--calibrate-copy-mib {mib}"),
             "write": pmc_run("WRITE_SIZE", workload, f"--calibrate-copy-mib {mib}")}
-    lines = [f"# Hardware counters: `{workload}` workload", "",
+    lines = [f"# Kernel trace and hardware counters: `{workload}` workload", "",
              f"Command (repository root on the GPU box): `python3 bench.py --pmc-report {workload}`.",
-             "It runs four child processes, one counter set each:",
-             "`rocprofv3 --pmc <set> -f csv -d <tmp> -o pmc -- python3 bench.py --no-counters "
-             f"{PMC_WORKLOADS[workload]}` (FETCH/WRITE passes add `--calibrate-copy-mib {mib}`).", "",
+             "It runs five child processes: `rocprofv3 --kernel-trace -f csv -d <tmp> -o pmc -- "
+             f"python3 bench.py --no-counters {PMC_WORKLOADS[workload]}`, then the same with "
+             "`--pmc <set>` for each counter set (FETCH/WRITE passes add "
+             f"`--calibrate-copy-mib {mib}`).", "",
              f"- set 1: `{PMC_MFMA}`", f"- set 2: `{PMC_WAITS}`", "- set 3: `FETCH_SIZE`",
-             "- set 4: `WRITE_SIZE`", ""]
+             "- set 4: `WRITE_SIZE`", "",
+             "Durations (launches, avg/min/max us) come from the kernel-trace run; the counter "
+             "runs serialise dispatches and are used for ratios only.", ""]
     if not any(runs.values()):
         lines.append("rocprofv3 was not available or every pass failed.")
         return "\n".join(lines)
@@ -230,10 +262,15 @@ def pmc_report(workload):
                  f"{fs and round(fs, 4)}, WRITE_SIZE x {ws and round(ws, 4)} bytes per counted "
                  "byte.")
     lines += ["", "Formulas: MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / XCCs x "
-              "SIMDs); int8 TOP/s = SQ_INSTS_VALU_MFMA_MOPS_I8 x 512 / duration (duration from "
-              "the counter run's dispatch timestamps); VALU/MFMA = (SQ_INSTS_VALU - "
+              "SIMDs); int8 TOP/s = (SQ_INSTS_VALU_MFMA_MOPS_I8 + SQ_INSTS_VALU_MFMA_MOPS_F16) x "
+              "512 / duration (duration from the counter run's dispatch timestamps; the "
+              "*_f16_kernel GEMMs run the contract's int8 products on fp16 MFMA, exactly, so "
+              "their MACs count under MOPS_F16 -- against the fp16 peak of "
+              f"{BF16_PEAK_TFLOPS / 1000:.1f} PFLOP/s their fraction is twice the int8 one); "
+              "VALU/MFMA = (SQ_INSTS_VALU - "
               f"SQ_INSTS_MFMA) / SQ_INSTS_MFMA; VALU issue = (SQ_INSTS_VALU - SQ_INSTS_MFMA) x "
-              f"{VALU_CYCLES} cycles / (GRBM_GUI_ACTIVE / XCCs x SIMDs); waits = SQ_WAIT_INST_ANY "
+              f"{VALU_CYCLES} cycles / (GRBM_GUI_ACTIVE / XCCs x SIMDs), an estimate (values "
+              "above 100 % mean some instructions issued in fewer cycles); waits = SQ_WAIT_INST_ANY "
               "/ SQ_WAVE_CYCLES and SQ_WAIT_ANY / SQ_WAVE_CYCLES; peak int8 "
               f"{INT8_PEAK_TOPS / 1000:.2f} POP/s.", ""]
     keys = set()
@@ -249,28 +286,46 @@ def pmc_report(workload):
     for key in keys:
         mm = mfma_metrics(runs["mfma"][0][key], agent) if runs["mfma"] and key in runs["mfma"][0] \
             else None
+        tr = runs["trace"][0].get(key) if runs["trace"] else None
+        td = tr["_duration_us"] if tr else None
         wc = avg(runs["waits"], key, "SQ_WAVE_CYCLES")
         wi = avg(runs["waits"], key, "SQ_WAIT_INST_ANY")
         wa = avg(runs["waits"], key, "SQ_WAIT_ANY")
         fe = avg(runs["fetch"], key, "FETCH_SIZE")
         wr = avg(runs["write"], key, "WRITE_SIZE")
-        rows.append((mm["avg_us"] if mm else 0.0, key, mm, wc, wi, wa,
-                     fe * 1024 * fs / 1e6 if fe is not None and fs else None,
-                     wr * 1024 * ws / 1e6 if wr is not None and ws else None))
+        fb = fe * 1024 * fs if fe is not None and fs else None
+        wb = wr * 1024 * ws if wr is not None and ws else None
+        mean_us = statistics.fmean(td) if td else (mm["avg_us"] if mm else 0.0)
+        rows.append((mean_us, key, mm, td, wc, wi, wa, fb, wb))
     rows.sort(key=lambda r: -r[0])
-    lines += ["| kernel | grid | launches | avg us | MFMA busy | int8 TOP/s | % int8 peak | "
-              "VALU/MFMA | VALU issue | wait inst | wait any | FETCH MB | WRITE MB |",
-              "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    lines += ["| kernel | grid | launches | avg us | min us | max us | MFMA busy | int8 TOP/s | "
+              "% int8 peak | VALU/MFMA | VALU issue | wait inst | wait any | FETCH MB | WRITE MB |",
+              "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
     f = lambda v, d=2: "" if v is None else (f"{v:.{d}f}" if isinstance(v, float) else str(v))
-    for _, (k, g), mm, wc, wi, wa, fe, wr in rows:
+    traffic = {}
+    for mean_us, (k, g), mm, td, wc, wi, wa, fb, wb in rows:
         lines.append(
-            f"| {k} | {g} | {mm['launches'] if mm else ''} | {f(mm and mm['avg_us'])} | "
+            f"| {k} | {g} | {len(td) if td else ''} | {f(mean_us)} | {f(td and min(td))} | "
+            f"{f(td and max(td))} | "
             f"{f(mm and 100 * mm['mfma_busy_frac'], 1)}% | {f(mm and mm['int8_tops_counter'], 1)} | "
             f"{f(mm and 100 * mm['int8_peak_frac_counter'], 2)}% | "
             f"{f(mm and mm['valu_insts_per_mfma'])} | "
             f"{f(mm and 100 * mm['valu_issue_share_est'], 1)}% | "
             f"{f(wi / wc * 100 if wc else None, 1)}% | {f(wa / wc * 100 if wc else None, 1)}% | "
-            f"{f(fe, 1)} | {f(wr, 1)} |")
+            f"{f(fb and fb / 1e6, 1)} | {f(wb and wb / 1e6, 1)} |")
+        base = k.split("<")[0]
+        if workload == "slab" and base in ("gate_up_w4_kernel", "down_w8_kernel") and fb and wb:
+            # the headline slab's grids have the most launches
+            if base not in traffic or len(td or []) > traffic[base][0]:
+                traffic[base] = (len(td or []), fb, wb)
+    if traffic_dir:
+        for base, (_, fb, wb) in traffic.items():
+            with open(os.path.join(traffic_dir, f"{base}_config2_traffic.json"), "w") as fh:
+                json.dump({"kernel": base, "workload": "config2",
+                           "hbm_bytes_per_launch": round(fb + wb), "fetch_bytes": round(fb),
+                           "write_bytes": round(wb), "fetch_scale": round(fs, 4),
+                           "write_scale": round(ws, 4),
+                           "source": "profiles/counters_config2_slab.md"}, fh, indent=1)
     return "\n".join(lines)
 
 
@@ -291,14 +346,18 @@ def main():
                         help="skip the full 48-layer config-5 stack")
     parser.add_argument("--no-counters", action="store_true",
                         help="skip the rocprofv3 MFMA counter passes (child runs)")
-    parser.add_argument("--pmc-report", choices=["slab", "chunk", "decode"],
-                        help="print the counter report for one workload (markdown) and exit")
+    parser.add_argument("--pmc-report", choices=["slab", "chunk", "decode", "dense"],
+                        help="print the trace and counter report for one workload (markdown) "
+                             "and exit")
+    parser.add_argument("--traffic-json-dir", default=None,
+                        help="with --pmc-report slab: also write the headline kernels' "
+                             "<kernel>_config2_traffic.json files into this directory")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
     args = parser.parse_args()
     if args.pmc_report:
-        print(pmc_report(args.pmc_report), flush=True)
+        print(pmc_report(args.pmc_report, args.traffic_json_dir), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE data plane is built and measured on a single "
@@ -509,11 +568,12 @@ def main():
         if head:
             result["roofline"]["mfma_busy_frac_counter"] = head["mfma_busy_frac"]
             result["roofline"]["int8_peak_frac_counter"] = head["int8_peak_frac_counter"]
-        wide = counters and counters.get("gate_up_w4_wide_kernel (config-5 layer)")
+        wide = counters and counters.get("gate_up_w4g32_f16_kernel (config-5 layer)")
         if wide and "chunks" in result:
-            result["chunks"]["gate_up_w4_wide_kernel_counters"] = {
+            result["chunks"]["gate_up_w4g32_f16_kernel_counters"] = {
                 k: wide[k] for k in ("avg_us", "mfma_busy_frac", "int8_peak_frac_counter",
-                                     "valu_insts_per_mfma", "valu_issue_share_est")}
+                                     "fp16_peak_frac_counter", "valu_insts_per_mfma",
+                                     "valu_issue_share_est")}
         slab_ops = [counters[k]["int8_ops_counter"] for k in
                     ("gate_up_w4_kernel (config 2 slab)", "down_w8_kernel (config 2 slab)")
                     if counters and k in counters]
