@@ -506,29 +506,43 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
 // and group.  The chain step is then a single v_fma_f32, and the MFMA runs
 // at the same 16 cycles as v_mfma_i32_16x16x32_i8.
 //
-// fp16 images.  Weights (MFMA16 W4 word: byte i = k_i | k_{4+i} << 4):
-// x = d ^ 0x88888888 makes each nibble w + 8; (x >> {0, 8, 4}) or (x << 4)
-// masked to bits 4-7 and 20-23 and put under the exponent bits of 1024
-// (0x6400) is 1024 + 16 * (w + 8) exactly, two values per word, and one
-// v_pk_add_f16 of -1152 leaves 16 * w.  A lane's eight K values come out
-// in the order (4, 6), (5, 7), (0, 2), (1, 3).  Activations: one
-// v_cvt_f16_i16 per sign-extended byte, written into the same order when
-// the rows are staged (a dot product does not depend on the order of its
-// K terms, only on A and B agreeing).
-__device__ __forceinline__ uint32_t pk_sub1152(uint32_t v) {
+// fp16 images.  Weights (MFMA16 W4 word: byte i = k_i | k_{4+i} << 4): a
+// nibble u' = w + 8 (offset binary: the nibble's top bit inverted) placed
+// under the exponent bits of 1024 (0x6400) is the fp16 1024 + 16 u' (nibble
+// in bits 4-7) or 1024 + u' (bits 0-3), exact; one v_pk_add_f16 of -1152 or
+// -1032 leaves 16 w or w.  One v_bitop3_b32 forms two such values from a
+// word (or the word shifted right by 8): per bit, field bits pass (sign bit
+// inverted), exponent bits are set, the rest cleared.  A lane's eight K
+// values come out as (4, 6) and (5, 7) times 16, (0, 2) and (1, 3) times 1;
+// the activations are staged in the same K order with the (0, 2), (1, 3)
+// pairs times 16 (one v_cvt_f16_i16 per sign-extended byte, one v_pk_mul_f16
+// per pair), so every product is 16 a w, as on the int8 path.  A dot
+// product does not depend on the order of its K terms, only on A and B
+// agreeing; every value and product here is an integer below 2^14.
+__device__ __forceinline__ uint32_t pk_add_f16(uint32_t v, float c) {
     typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
-    const h2_t r = __builtin_bit_cast(h2_t, v) + h2_t{static_cast<_Float16>(-1152.0f),
-                                                       static_cast<_Float16>(-1152.0f)};
-    return __builtin_bit_cast(uint32_t, r);
+    const _Float16 h = static_cast<_Float16>(c);
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, v) + h2_t{h, h});
+}
+__device__ __forceinline__ uint32_t pk_times16_f16(uint32_t v) {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    const _Float16 h = static_cast<_Float16>(16.0f);
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, v) * h2_t{h, h});
 }
 
-// one MFMA16 W4 word (byte i = k_i | k_{4+i} << 4) -> 16 * w as fp16, K
-// order (4, 6), (5, 7), (0, 2), (1, 3)
+// one MFMA16 W4 word -> fp16 K order (4, 6)x16, (5, 7)x16, (0, 2), (1, 3)
 __device__ __forceinline__ uint4 w4_to_f16x16(uint32_t d) {
-    constexpr uint32_t kMask = 0x00F000F0u, kExp = 0x64006400u;
-    const uint32_t x = d ^ 0x88888888u;
-    return make_uint4(pk_sub1152((x & kMask) | kExp), pk_sub1152(((x >> 8) & kMask) | kExp),
-                      pk_sub1152(((x << 4) & kMask) | kExp), pk_sub1152(((x >> 4) & kMask) | kExp));
+    // bitop3 truth table (index = S0*4 + S1*2 + S2): out = S0 where S1 & !S2,
+    // !S0 where S1 & S2, 1 where !S1 & S2, 0 elsewhere
+    constexpr uint32_t kTable = 0x6A;
+    constexpr uint32_t kHiField = 0x00F000F0u, kHiConst = 0x64806480u;
+    constexpr uint32_t kLoField = 0x000F000Fu, kLoConst = 0x64086408u;
+    const uint32_t t = d >> 8;
+    return make_uint4(
+        pk_add_f16(__builtin_amdgcn_bitop3_b32(d, kHiField, kHiConst, kTable), -1152.0f),
+        pk_add_f16(__builtin_amdgcn_bitop3_b32(t, kHiField, kHiConst, kTable), -1152.0f),
+        pk_add_f16(__builtin_amdgcn_bitop3_b32(d, kLoField, kLoConst, kTable), -1032.0f),
+        pk_add_f16(__builtin_amdgcn_bitop3_b32(t, kLoField, kLoConst, kTable), -1032.0f));
 }
 
 // bytes 0 and 2 (or 1 and 3) of v as signed integers -> two fp16 (exact):
@@ -551,10 +565,11 @@ __device__ __forceinline__ uint32_t sbytes13_to_f16(uint32_t v) {
     return r;
 }
 
-// eight int8 (k 0-3 in lo, 4-7 in hi) -> fp16 in the order of w4_to_f16x16
+// eight int8 (k 0-3 in lo, 4-7 in hi) -> fp16 in the order and scaling of
+// w4_to_f16x16's partners: (4, 6), (5, 7), 16 (0, 2), 16 (1, 3)
 __device__ __forceinline__ uint4 i8_to_f16(uint32_t lo, uint32_t hi) {
-    return make_uint4(sbytes02_to_f16(hi), sbytes13_to_f16(hi), sbytes02_to_f16(lo),
-                      sbytes13_to_f16(lo));
+    return make_uint4(sbytes02_to_f16(hi), sbytes13_to_f16(hi),
+                      pk_times16_f16(sbytes02_to_f16(lo)), pk_times16_f16(sbytes13_to_f16(lo)));
 }
 
 __device__ __forceinline__ v4f mfma_f16_16x16x32(uint4 a, uint4 b, v4f c) {
