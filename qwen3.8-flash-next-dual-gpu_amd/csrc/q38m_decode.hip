@@ -75,7 +75,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
         num_lds[lane] = weights_in[lane];
     }
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
-    if (wave < 4u) row_absmax_partial(hw, amax_lds);
+    // the selection first: the token row's absmax waits for its load, the
+    // selection only for the logits
     if (fused) {
         block_topk512(logit, select_lds, ids_lds, num_lds);
         if (blockIdx.x == 0 && threadIdx.x < top_k) ids_out[threadIdx.x] = ids_lds[threadIdx.x];
@@ -124,7 +125,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
             sw = s[row * (kBlocks / 2u) + kq];
     }
 
-    // int8 token (same arithmetic as the row quantiser)
+    // int8 token (same arithmetic as the row quantiser); the barrier waits
+    // for LDS only, so the weight loads above stay in flight
+    if (wave < 4u) row_absmax_partial(hw, amax_lds);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const float xs = row_scale(amax_lds);
     if (wave < 4u) {
         const uint32_t k = 8u * threadIdx.x;
