@@ -4,10 +4,14 @@
 // Order: value descending, expert id ascending on ties (the order of the
 // reference's sort, cuda/q38_kernels.cu:431-458), expressed as unique
 // 64-bit keys (order key << 32 | 511 - id) so that "larger key" is "ranked
-// first".  Two levels of rank counting:
-//   1. each of waves 0-7 ranks its 64 keys among themselves; ranks 0-9 of
-//      every wave (80 candidates in eight sorted lists) contain the top 10,
-//      because every key above a top-10 key is itself in its wave's top 10;
+// first".  Two levels:
+//   1. each of waves 0-7 finds the 10th largest 32-bit order key of its 64
+//      logits by a radix search on the wave's ballots (bit 31 down to 0:
+//      keep the bit if at least ten keys reach the prefix with it set), then
+//      takes every key above it and, among the keys equal to it, the lowest
+//      lanes (lowest ids) up to ten: the wave's top 10, written unordered to
+//      LDS -- 80 candidates in eight lists that contain the top 10, because
+//      every key above a top-10 key is itself in its wave's top 10;
 //   2. eight threads per candidate count the larger keys in one list each
 //      and a DPP sum adds the eight counts: the global rank.
 // The thread holding rank r writes id_r and exp(l_r - l_0); values come
@@ -23,9 +27,9 @@ namespace q38m {
 
 constexpr uint32_t kSelectThreads = 64u * kTopK;  // ten waves
 
-struct SelectLds {
-    uint64_t key[kExperts];
+struct alignas(16) SelectLds {
     uint64_t cand[8u * kTopK];
+    uint32_t wave_max[8];  // each wave's largest order key
 };
 
 // Monotonic unsigned key of a float: larger key = larger value; -0 and +0
@@ -55,24 +59,6 @@ __device__ __forceinline__ float wave_max_f32(float x) {
     return x;
 }
 
-// Rank of `mine` among `count` unique keys in LDS: the number of larger keys
-// (four independent counts so the compares pipeline).
-template <uint32_t kCount>
-__device__ __forceinline__ uint32_t rank_among(const uint64_t* keys, uint64_t mine) {
-    static_assert(kCount % 4u == 0u, "keys in groups of four");
-    uint32_t r[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (uint32_t j = 0; j < kCount; j += 4u) {
-        const ulonglong2 a = *reinterpret_cast<const ulonglong2*>(keys + j);
-        const ulonglong2 b = *reinterpret_cast<const ulonglong2*>(keys + j + 2u);
-        r[0] += a.x > mine ? 1u : 0u;
-        r[1] += a.y > mine ? 1u : 0u;
-        r[2] += b.x > mine ? 1u : 0u;
-        r[3] += b.y > mine ? 1u : 0u;
-    }
-    return (r[0] + r[1]) + (r[2] + r[3]);
-}
-
 // Called by all kSelectThreads threads of the block; `logit` is the row
 // entry of threads 0..511.  LDS writes the caller made before the call are
 // visible to the whole block on return.  On return ids[r] and num[r]
@@ -80,18 +66,35 @@ __device__ __forceinline__ uint32_t rank_among(const uint64_t* keys, uint64_t mi
 __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32_t* ids,
                                               float* num) {
     const uint32_t t = threadIdx.x;
-    uint64_t key = 0;
+    const uint32_t lane = t & 63u;
     if (t < kExperts) {
-        key = (static_cast<uint64_t>(order_key(logit)) << 32) | (kExperts - 1u - t);
-        lds.key[t] = key;
-    }
-    __syncthreads();
-    if (t < kExperts) {
-        const uint32_t rank = rank_among<64>(lds.key + (t & ~63u), key);
-        if (rank < kTopK) lds.cand[kTopK * (t >> 6) + rank] = key;
+        // 1. the wave's top 10 (wave-uniform control flow: ballots only)
+        const uint32_t k32 = order_key(logit);
+        uint32_t prefix = 0u;
+        for (int b = 31; b >= 0; --b) {
+            const uint32_t cand = prefix | (1u << b);
+            if (__popcll(__ballot(k32 >= cand)) >= kTopK) prefix = cand;
+        }
+        const uint64_t below = (1ull << lane) - 1ull;
+        const uint64_t above = __ballot(k32 > prefix);
+        const uint64_t equal = __ballot(k32 == prefix);
+        const uint32_t need = kTopK - static_cast<uint32_t>(__popcll(above));
+        const bool mine_eq = k32 == prefix &&
+                             static_cast<uint32_t>(__popcll(equal & below)) < need;
+        const uint64_t chosen = above | __ballot(mine_eq);
+        if (k32 > prefix || mine_eq) {
+            const uint32_t at = static_cast<uint32_t>(__popcll(chosen & below));
+            lds.cand[kTopK * (t >> 6) + at] = (static_cast<uint64_t>(k32) << 32) | (kExperts - 1u - t);
+        }
+        uint32_t kmax = k32;
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1)
+            kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), offset, 64)));
+        if (lane == 0u) lds.wave_max[t >> 6] = kmax;
     }
     __syncthreads();
     {
+        // 2. global ranks of the 80 candidates
         const uint32_t c = t >> 3, list = t & 7u;
         const uint64_t mine = lds.cand[c];
         const uint64_t* other = lds.cand + kTopK * list;
@@ -102,17 +105,15 @@ __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32
             larger += pr.x > mine ? 1u : 0u;
             larger += pr.y > mine ? 1u : 0u;
         }
-        uint64_t top = lds.cand[0];
-#pragma unroll
-        for (uint32_t w8 = 1; w8 < 8u; ++w8) {
-            const uint64_t head = lds.cand[kTopK * w8];
-            top = head > top ? head : top;
-        }
+        // l_0's order key: the largest of the eight wave maxima
+        const uint4 m0 = *reinterpret_cast<const uint4*>(lds.wave_max);
+        const uint4 m1 = *reinterpret_cast<const uint4*>(lds.wave_max + 4);
+        const uint32_t top = max(max(max(m0.x, m0.y), max(m0.z, m0.w)),
+                                 max(max(m1.x, m1.y), max(m1.z, m1.w)));
         const uint32_t rank = group8_sum(larger);
         if (list == 7u && rank < kTopK) {
             ids[rank] = static_cast<int32_t>(kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu));
-            num[rank] = exp_q(key_value(static_cast<uint32_t>(mine >> 32)) -
-                              key_value(static_cast<uint32_t>(top >> 32)));
+            num[rank] = exp_q(key_value(static_cast<uint32_t>(mine >> 32)) - key_value(top));
         }
     }
     __syncthreads();
