@@ -24,44 +24,72 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast
 
 constexpr uint32_t kDenseWaves = 4;
 
-// Lane pointer into a 16-row panel starting at `row`: lane l reads row l%16
-// (clamped to the last row, never stored) at k = 8*(l/16) .. +7 of each
-// 32-wide K step, one 16-byte load per step, which is the bf16 MFMA
-// operand layout.
-__device__ __forceinline__ const uint4* panel_ptr(const uint16_t* base, uint32_t row,
-                                                  uint32_t rows, uint32_t k, uint32_t lane) {
-    const uint32_t r = min(row + (lane & 15u), rows - 1u);
-    return reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * k + (lane >> 4) * 8u);
+// Operands reach the MFMAs through a per-wave LDS slab.  A wave's panels
+// (16 rows each: its A panels, then its B panels) are stacked into one list
+// of rows; staging instruction i loads rows 8i .. 8i+7 of that list, lane l
+// reading row 8i + l/8 at the 16-byte chunk l%8 of the current 64-wide K
+// chunk, so each instruction reads eight whole 128-byte lines.  (Loading
+// the MFMA layout straight from memory -- lane l at row l%16 -- reads
+// sixteen half lines per instruction and runs at a third of the rate from
+// L2.)  In LDS, row r keeps its chunk c in slot c ^ (r%8): both the row
+// writes and the MFMA-layout reads (eight rows, one chunk) fall in distinct
+// banks.
+
+// Lane pointer of staging instruction `half` (0/1) of the 16-row panel at
+// `row`: row row + 8 half + l/8 (clamped to the last row, never stored),
+// column 8 (l%8).
+__device__ __forceinline__ const uint4* stage_ptr(const uint16_t* base, uint32_t row,
+                                                  uint32_t rows, uint32_t k, uint32_t half,
+                                                  uint32_t lane) {
+    const uint32_t r = min(row + 8u * half + (lane >> 3), rows - 1u);
+    return reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * k + (lane & 7u) * 8u);
 }
 
-// One wave's partial products over K steps [s0, s1) for kTM A panels
-// against kNB x kTN B panels.  Steps go in batches of kBatch with the next
-// batch's loads issued before the current batch's MFMAs, so a wave has a
-// batch of loads in flight while it multiplies.
-template <uint32_t kTM, uint32_t kTN, uint32_t kNB, uint32_t kBatch>
-__device__ __forceinline__ void wave_partial(const uint4* const (&pa)[kTM],
-                                             const uint4* const (&pb)[kNB][kTN], uint32_t s0,
+// One wave's partial products over 32-wide K steps [s0, s1) for kTM A
+// panels against kNB x kTN B panels; ga[2p + half] are the panel p staging
+// pointers (p < kTM: A panel p; then B panel (v, j) at kTM + v kTN + j).
+// Steps go in pairs (one 64-wide chunk, a half chunk at an odd end); two
+// chunks are in flight in registers while the wave multiplies the one in
+// its slab.  The slab is private to the wave and a wave's LDS operations
+// complete in program order, so no barrier is needed.  Each accumulator
+// receives its K steps in increasing order, lane l contributing
+// k = 32 s + 8 (l/16) .. +7 of step s.
+template <uint32_t kTM, uint32_t kTN, uint32_t kNB>
+__device__ __forceinline__ void wave_partial(const uint4* const (&ga)[2 * (kTM + kNB * kTN)],
+                                             uint4* slab, uint32_t lane, uint32_t s0,
                                              uint32_t s1, f32x4 (&acc)[kNB][kTM][kTN]) {
-    struct Batch {
-        uint4 a[kBatch][kTM];
-        uint4 b[kBatch][kNB][kTN];
+    constexpr uint32_t kL = 2u * (kTM + kNB * kTN);
+    struct Chunk {
+        uint4 v[kL];
     };
-    auto load = [&](Batch& x, uint32_t s, uint32_t count) {
+    const uint32_t write_at = 8u * (lane >> 3) + ((lane & 7u) ^ (lane >> 3));
+    const uint32_t read_at = 8u * (lane & 15u);
+    const uint32_t read_slot[2] = {(lane >> 4) ^ (lane & 7u), (4u + (lane >> 4)) ^ (lane & 7u)};
+    const uint32_t chunks = (s1 - s0 + 1u) / 2u;
+    auto load = [&](Chunk& x, uint32_t c) {
+        const uint32_t s = s0 + 2u * c;
+        const bool whole = s + 1u < s1 || (lane & 7u) < 4u;
 #pragma unroll
-        for (uint32_t q = 0; q < kBatch; ++q) {
-            if (q >= count) break;
+        for (uint32_t i = 0; i < kL; ++i)
+            x.v[i] = whole ? ga[i][4u * s] : make_uint4(0u, 0u, 0u, 0u);
+    };
+    auto stage = [&](const Chunk& x) {
 #pragma unroll
-            for (uint32_t i = 0; i < kTM; ++i) x.a[q][i] = pa[i][4u * (s + q)];
+        for (uint32_t i = 0; i < kL; ++i) slab[64u * i + write_at] = x.v[i];
+    };
+    auto multiply = [&](uint32_t c) {
+        const uint32_t steps = min(2u, s1 - s0 - 2u * c);
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; ++h) {
+            if (h >= steps) break;
+            uint4 a[kTM], b[kNB][kTN];
+#pragma unroll
+            for (uint32_t i = 0; i < kTM; ++i) a[i] = slab[128u * i + read_at + read_slot[h]];
 #pragma unroll
             for (uint32_t v = 0; v < kNB; ++v)
 #pragma unroll
-                for (uint32_t j = 0; j < kTN; ++j) x.b[q][v][j] = pb[v][j][4u * (s + q)];
-        }
-    };
-    auto multiply = [&](const Batch& x, uint32_t count) {
-#pragma unroll
-        for (uint32_t q = 0; q < kBatch; ++q) {
-            if (q >= count) break;
+                for (uint32_t j = 0; j < kTN; ++j)
+                    b[v][j] = slab[128u * (kTM + v * kTN + j) + read_at + read_slot[h]];
 #pragma unroll
             for (uint32_t v = 0; v < kNB; ++v)
 #pragma unroll
@@ -69,33 +97,22 @@ __device__ __forceinline__ void wave_partial(const uint4* const (&pa)[kTM],
 #pragma unroll
                     for (uint32_t j = 0; j < kTN; ++j)
                         acc[v][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            as_bf16x8(x.a[q][i]), as_bf16x8(x.b[q][v][j]), acc[v][i][j], 0, 0,
-                            0);
+                            as_bf16x8(a[i]), as_bf16x8(b[v][j]), acc[v][i][j], 0, 0, 0);
         }
     };
-    uint32_t s = s0;
-    if (s + kBatch <= s1) {
-        Batch cur;
-        load(cur, s, kBatch);
-        s += kBatch;
-        while (s + kBatch <= s1) {
-            Batch next;
-            load(next, s, kBatch);
-            multiply(cur, kBatch);
-            cur = next;
-            s += kBatch;
-        }
-        multiply(cur, kBatch);
+    if (chunks == 0u) return;
+    Chunk x0, x1;
+    load(x0, 0u);
+    if (chunks > 1u) load(x1, 1u);
+    for (uint32_t c = 0; c < chunks; c += 2u) {
+        stage(x0);
+        if (c + 2u < chunks) load(x0, c + 2u);
+        multiply(c);
+        if (c + 1u >= chunks) break;
+        stage(x1);
+        if (c + 3u < chunks) load(x1, c + 3u);
+        multiply(c + 1u);
     }
-    for (; s < s1; ++s) {
-        Batch one;
-        load(one, s, 1u);
-        multiply(one, 1u);
-    }
-}
-
-constexpr uint32_t batch_for(uint32_t loads_per_step) {
-    return loads_per_step <= 2u ? 8u : (loads_per_step <= 4u ? 4u : 2u);
 }
 
 // The four waves of a block split K; their partial tiles meet in LDS and
@@ -145,25 +162,30 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(
     const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m, uint32_t n,
     uint32_t k, float* __restrict__ c_f32, uint16_t* __restrict__ c_bf16, float divisor,
     float scale) {
+    constexpr uint32_t kL = 2u * (kTM + kTN);
+    __shared__ uint4 slab[kDenseWaves * kL * 64];
     __shared__ f32x4 lds[kDenseWaves * kTM * kTN * 64];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t m0 = blockIdx.y * 16u * kTM;
     const uint32_t n0 = blockIdx.x * 16u * kTN;
-    const uint4* pa[kTM];
-    const uint4* pb[1][kTN];
+    const uint4* ga[kL];
 #pragma unroll
-    for (uint32_t i = 0; i < kTM; ++i) pa[i] = panel_ptr(a, m0 + 16u * i, m, k, lane);
+    for (uint32_t h = 0; h < 2u; ++h) {
 #pragma unroll
-    for (uint32_t j = 0; j < kTN; ++j) pb[0][j] = panel_ptr(b, n0 + 16u * j, n, k, lane);
+        for (uint32_t i = 0; i < kTM; ++i) ga[2u * i + h] = stage_ptr(a, m0 + 16u * i, m, k, h, lane);
+#pragma unroll
+        for (uint32_t j = 0; j < kTN; ++j)
+            ga[2u * (kTM + j) + h] = stage_ptr(b, n0 + 16u * j, n, k, h, lane);
+    }
     f32x4 acc[1][kTM][kTN];
 #pragma unroll
     for (uint32_t i = 0; i < kTM; ++i)
 #pragma unroll
         for (uint32_t j = 0; j < kTN; ++j) acc[0][i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t steps = k / 32u;
-    wave_partial<kTM, kTN, 1, batch_for(kTM + kTN)>(pa, pb, wave * steps / kDenseWaves,
-                                                    (wave + 1u) * steps / kDenseWaves, acc);
+    wave_partial<kTM, kTN, 1>(ga, slab + wave * kL * 64u, lane, wave * steps / kDenseWaves,
+                              (wave + 1u) * steps / kDenseWaves, acc);
     reduce_waves<kTM * kTN, kTM * kTN>(lds, &acc[0][0][0], wave, lane,
                                        [&](uint32_t o, uint32_t, f32x4 sum) {
         const uint32_t col = n0 + 16u * (o % kTN) + (lane & 15u);
@@ -197,21 +219,28 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
     uint32_t inter, uint16_t* __restrict__ g_out, uint16_t* __restrict__ u_out,
     uint16_t* __restrict__ h_out, uint16_t* __restrict__ gate_out) {
     constexpr uint32_t kTM = 2, kTN = 2;
+    constexpr uint32_t kL = 2u * (kTM + 2u * kTN);
+    __shared__ uint4 slab[kDenseWaves * kL * 64];
     __shared__ f32x4 lds[kDenseWaves * 2 * kTM * kTN * 64];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t m0 = blockIdx.y * 16u * kTM;
     const uint32_t steps = kHidden / 32u;
     const uint32_t s0 = wave * steps / kDenseWaves, s1 = (wave + 1u) * steps / kDenseWaves;
-    const uint4* pa[kTM];
-#pragma unroll
-    for (uint32_t i = 0; i < kTM; ++i) pa[i] = panel_ptr(x, m0 + 16u * i, m, kHidden, lane);
+    uint4* const wave_slab = slab + wave * kL * 64u;
     if (blockIdx.x == gridDim.x - 1u) {
-        const uint4* pb[1][1] = {{panel_ptr(w_out_gate, 0, 1, kHidden, lane)}};
+        const uint4* ga[2u * (kTM + 1u)];
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; ++h) {
+#pragma unroll
+            for (uint32_t i = 0; i < kTM; ++i)
+                ga[2u * i + h] = stage_ptr(x, m0 + 16u * i, m, kHidden, h, lane);
+            ga[2u * kTM + h] = stage_ptr(w_out_gate, 0u, 1u, kHidden, h, lane);
+        }
         f32x4 acc[1][kTM][1];
 #pragma unroll
         for (uint32_t i = 0; i < kTM; ++i) acc[0][i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        wave_partial<kTM, 1, 1, batch_for(kTM + 1)>(pa, pb, s0, s1, acc);
+        wave_partial<kTM, 1, 1>(ga, wave_slab, lane, s0, s1, acc);
         reduce_waves<kTM, kTM>(lds, &acc[0][0][0], wave, lane,
                                [&](uint32_t o, uint32_t, f32x4 sum) {
             if ((lane & 15u) != 0u) return;  // column 0 holds the gate
@@ -224,11 +253,17 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
         return;
     }
     const uint32_t n0 = blockIdx.x * 16u * kTN;
-    const uint4* pb[2][kTN];
+    const uint4* ga[kL];
 #pragma unroll
-    for (uint32_t j = 0; j < kTN; ++j) {
-        pb[0][j] = panel_ptr(w_gate, n0 + 16u * j, inter, kHidden, lane);
-        pb[1][j] = panel_ptr(w_up, n0 + 16u * j, inter, kHidden, lane);
+    for (uint32_t h = 0; h < 2u; ++h) {
+#pragma unroll
+        for (uint32_t i = 0; i < kTM; ++i)
+            ga[2u * i + h] = stage_ptr(x, m0 + 16u * i, m, kHidden, h, lane);
+#pragma unroll
+        for (uint32_t j = 0; j < kTN; ++j) {
+            ga[2u * (kTM + j) + h] = stage_ptr(w_gate, n0 + 16u * j, inter, kHidden, h, lane);
+            ga[2u * (kTM + kTN + j) + h] = stage_ptr(w_up, n0 + 16u * j, inter, kHidden, h, lane);
+        }
     }
     f32x4 acc[2][kTM][kTN];
 #pragma unroll
@@ -237,7 +272,7 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
         for (uint32_t i = 0; i < kTM; ++i)
 #pragma unroll
             for (uint32_t j = 0; j < kTN; ++j) acc[v][i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    wave_partial<kTM, kTN, 2, batch_for(kTM + 2 * kTN)>(pa, pb, s0, s1, acc);
+    wave_partial<kTM, kTN, 2>(ga, wave_slab, lane, s0, s1, acc);
     uint32_t g_bits[4] = {0u, 0u, 0u, 0u};
     reduce_waves<2 * kTM * kTN, kTM * kTN>(lds, &acc[0][0][0], wave, lane,
                                            [&](uint32_t o, uint32_t v, f32x4 sum) {
