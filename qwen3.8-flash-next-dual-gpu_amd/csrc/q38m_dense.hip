@@ -19,8 +19,12 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 16 bytes as a native vector: loads and stores of it stay plain vector
+// moves (a HIP_vector_type copy is a memcpy the compiler may keep in
+// scratch memory)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 constexpr uint32_t kDenseWaves = 4;
 
@@ -38,11 +42,11 @@ constexpr uint32_t kDenseWaves = 4;
 // Lane pointer of staging instruction `half` (0/1) of the 16-row panel at
 // `row`: row row + 8 half + l/8 (clamped to the last row, never stored),
 // column 8 (l%8).
-__device__ __forceinline__ const uint4* stage_ptr(const uint16_t* base, uint32_t row,
+__device__ __forceinline__ const u32x4* stage_ptr(const uint16_t* base, uint32_t row,
                                                   uint32_t rows, uint32_t k, uint32_t half,
                                                   uint32_t lane) {
     const uint32_t r = min(row + 8u * half + (lane >> 3), rows - 1u);
-    return reinterpret_cast<const uint4*>(base + static_cast<size_t>(r) * k + (lane & 7u) * 8u);
+    return reinterpret_cast<const u32x4*>(base + static_cast<size_t>(r) * k + (lane & 7u) * 8u);
 }
 
 // One wave's partial products over 32-wide K steps [s0, s1) for kTM A
@@ -55,34 +59,40 @@ __device__ __forceinline__ const uint4* stage_ptr(const uint16_t* base, uint32_t
 // receives its K steps in increasing order, lane l contributing
 // k = 32 s + 8 (l/16) .. +7 of step s.
 template <uint32_t kTM, uint32_t kTN, uint32_t kNB>
-__device__ __forceinline__ void wave_partial(const uint4* const (&ga)[2 * (kTM + kNB * kTN)],
-                                             uint4* slab, uint32_t lane, uint32_t s0,
+__device__ __forceinline__ void wave_partial(const u32x4* const (&ga)[2 * (kTM + kNB * kTN)],
+                                             u32x4* slab, uint32_t lane, uint32_t s0,
                                              uint32_t s1, f32x4 (&acc)[kNB][kTM][kTN]) {
     constexpr uint32_t kL = 2u * (kTM + kNB * kTN);
     struct Chunk {
-        uint4 v[kL];
+        u32x4 v[kL];
     };
     const uint32_t write_at = 8u * (lane >> 3) + ((lane & 7u) ^ (lane >> 3));
     const uint32_t read_at = 8u * (lane & 15u);
     const uint32_t read_slot[2] = {(lane >> 4) ^ (lane & 7u), (4u + (lane >> 4)) ^ (lane & 7u)};
     const uint32_t chunks = (s1 - s0 + 1u) / 2u;
-    auto load = [&](Chunk& x, uint32_t c) {
+    // At a half chunk, lanes l%8 >= 4 load their row's first half again
+    // instead of the next step (which may lie past the matrix): every lane
+    // loads, so the loads stay outside divergent control flow, and the
+    // duplicated slots are never read.
+    // (ga[i] points at the lane's 16 bytes l%8 of its row, so stepping back
+    // four vectors from step s stays within the row)
+    const uint32_t back = (lane & 7u) < 4u ? 0u : 4u;
+    auto load = [&](Chunk& x, uint32_t c) __attribute__((always_inline)) {
         const uint32_t s = s0 + 2u * c;
-        const bool whole = s + 1u < s1 || (lane & 7u) < 4u;
+        const size_t shift = s + 1u < s1 ? 0u : back;
 #pragma unroll
-        for (uint32_t i = 0; i < kL; ++i)
-            x.v[i] = whole ? ga[i][4u * s] : make_uint4(0u, 0u, 0u, 0u);
+        for (uint32_t i = 0; i < kL; ++i) x.v[i] = *(ga[i] + 4u * s - shift);
     };
-    auto stage = [&](const Chunk& x) {
+    auto stage = [&](const Chunk& x) __attribute__((always_inline)) {
 #pragma unroll
         for (uint32_t i = 0; i < kL; ++i) slab[64u * i + write_at] = x.v[i];
     };
-    auto multiply = [&](uint32_t c) {
-        const uint32_t steps = min(2u, s1 - s0 - 2u * c);
+    // the MFMAs of the staged chunk over `steps` (1 or 2) K steps
+    auto multiply = [&](uint32_t steps) __attribute__((always_inline)) {
 #pragma unroll
         for (uint32_t h = 0; h < 2u; ++h) {
             if (h >= steps) break;
-            uint4 a[kTM], b[kNB][kTN];
+            u32x4 a[kTM], b[kNB][kTN];
 #pragma unroll
             for (uint32_t i = 0; i < kTM; ++i) a[i] = slab[128u * i + read_at + read_slot[h]];
 #pragma unroll
@@ -101,17 +111,44 @@ __device__ __forceinline__ void wave_partial(const uint4* const (&ga)[2 * (kTM +
         }
     };
     if (chunks == 0u) return;
+    const uint32_t last_steps = s1 - s0 - 2u * (chunks - 1u);  // 1 or 2
     Chunk x0, x1;
     load(x0, 0u);
-    if (chunks > 1u) load(x1, 1u);
-    for (uint32_t c = 0; c < chunks; c += 2u) {
+    if (chunks == 1u) {
         stage(x0);
-        if (c + 2u < chunks) load(x0, c + 2u);
-        multiply(c);
-        if (c + 1u >= chunks) break;
+        multiply(last_steps);
+        return;
+    }
+    load(x1, 1u);
+    // steady state: every load in the loop is taken, so the wait for a
+    // chunk leaves the next chunk's loads in flight
+    uint32_t c = 0;
+    for (; c + 3u < chunks; c += 2u) {
+        stage(x0);
+        load(x0, c + 2u);
+        // keep the scheduler from sinking the loads below the next stage
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(2u);
         stage(x1);
-        if (c + 3u < chunks) load(x1, c + 3u);
-        multiply(c + 1u);
+        load(x1, c + 3u);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(2u);
+    }
+    // two or three chunks left; only the last may be a half chunk
+    if (chunks - c == 3u) {
+        stage(x0);
+        load(x0, c + 2u);
+        __builtin_amdgcn_sched_barrier(0);
+        multiply(2u);
+        stage(x1);
+        multiply(2u);
+        stage(x0);
+        multiply(last_steps);
+    } else {
+        stage(x0);
+        multiply(2u);
+        stage(x1);
+        multiply(last_steps);
     }
 }
 
@@ -163,13 +200,13 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(
     uint32_t k, float* __restrict__ c_f32, uint16_t* __restrict__ c_bf16, float divisor,
     float scale) {
     constexpr uint32_t kL = 2u * (kTM + kTN);
-    __shared__ uint4 slab[kDenseWaves * kL * 64];
+    __shared__ u32x4 slab[kDenseWaves * kL * 64];
     __shared__ f32x4 lds[kDenseWaves * kTM * kTN * 64];
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t m0 = blockIdx.y * 16u * kTM;
     const uint32_t n0 = blockIdx.x * 16u * kTN;
-    const uint4* ga[kL];
+    const u32x4* ga[kL];
 #pragma unroll
     for (uint32_t h = 0; h < 2u; ++h) {
 #pragma unroll
@@ -220,16 +257,16 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
     uint16_t* __restrict__ h_out, uint16_t* __restrict__ gate_out) {
     constexpr uint32_t kTM = 2, kTN = 2;
     constexpr uint32_t kL = 2u * (kTM + 2u * kTN);
-    __shared__ uint4 slab[kDenseWaves * kL * 64];
+    __shared__ u32x4 slab[kDenseWaves * kL * 64];
     __shared__ f32x4 lds[kDenseWaves * 2 * kTM * kTN * 64];
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t m0 = blockIdx.y * 16u * kTM;
     const uint32_t steps = kHidden / 32u;
     const uint32_t s0 = wave * steps / kDenseWaves, s1 = (wave + 1u) * steps / kDenseWaves;
-    uint4* const wave_slab = slab + wave * kL * 64u;
+    u32x4* const wave_slab = slab + wave * kL * 64u;
     if (blockIdx.x == gridDim.x - 1u) {
-        const uint4* ga[2u * (kTM + 1u)];
+        const u32x4* ga[2u * (kTM + 1u)];
 #pragma unroll
         for (uint32_t h = 0; h < 2u; ++h) {
 #pragma unroll
@@ -253,7 +290,7 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
         return;
     }
     const uint32_t n0 = blockIdx.x * 16u * kTN;
-    const uint4* ga[kL];
+    const u32x4* ga[kL];
 #pragma unroll
     for (uint32_t h = 0; h < 2u; ++h) {
 #pragma unroll
