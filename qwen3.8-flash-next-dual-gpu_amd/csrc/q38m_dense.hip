@@ -58,14 +58,24 @@ __device__ __forceinline__ const u32x4* stage_ptr(const uint16_t* base, uint32_t
 // complete in program order, so no barrier is needed.  Each accumulator
 // receives its K steps in increasing order, lane l contributing
 // k = 32 s + 8 (l/16) .. +7 of step s.
-template <uint32_t kTM, uint32_t kTN, uint32_t kNB>
+//
+// With kGate, the wave also multiplies its A panels by one extra B row
+// (`gate`, the lane's pointer at k = 8 (l/16) of that row) into
+// acc_gate[i]: the row rides in the MFMA B operand of lanes l%16 == 0 and
+// the other fifteen columns are zero, so column 0 of acc_gate holds the dot
+// products, summed exactly as in a 16-row panel.
+template <uint32_t kTM, uint32_t kTN, uint32_t kNB, bool kGate = false>
 __device__ __forceinline__ void wave_partial(const u32x4* const (&ga)[2 * (kTM + kNB * kTN)],
                                              u32x4* slab, uint32_t lane, uint32_t s0,
-                                             uint32_t s1, f32x4 (&acc)[kNB][kTM][kTN]) {
+                                             uint32_t s1, f32x4 (&acc)[kNB][kTM][kTN],
+                                             const u32x4* gate = nullptr,
+                                             f32x4* acc_gate = nullptr) {
     constexpr uint32_t kL = 2u * (kTM + kNB * kTN);
     struct Chunk {
         u32x4 v[kL];
+        u32x4 g[kGate ? 2 : 1];  // the gate row's two steps
     };
+    const bool gate_lane = (lane & 15u) == 0u;
     const uint32_t write_at = 8u * (lane >> 3) + ((lane & 7u) ^ (lane >> 3));
     const uint32_t read_at = 8u * (lane & 15u);
     const uint32_t read_slot[2] = {(lane >> 4) ^ (lane & 7u), (4u + (lane >> 4)) ^ (lane & 7u)};
@@ -79,13 +89,24 @@ __device__ __forceinline__ void wave_partial(const u32x4* const (&ga)[2 * (kTM +
     const uint32_t back = (lane & 7u) < 4u ? 0u : 4u;
     auto load = [&](Chunk& x, uint32_t c) __attribute__((always_inline)) {
         const uint32_t s = s0 + 2u * c;
-        const size_t shift = s + 1u < s1 ? 0u : back;
+        const bool whole = s + 1u < s1;  // uniform: both steps lie in the range
+        const size_t shift = whole ? 0u : back;
 #pragma unroll
         for (uint32_t i = 0; i < kL; ++i) x.v[i] = *(ga[i] + 4u * s - shift);
+        if constexpr (kGate) {
+            x.g[0] = gate[4u * s];
+            x.g[1] = gate[4u * (whole ? s + 1u : s)];
+        }
     };
+    u32x4 staged_gate[2];
     auto stage = [&](const Chunk& x) __attribute__((always_inline)) {
 #pragma unroll
         for (uint32_t i = 0; i < kL; ++i) slab[64u * i + write_at] = x.v[i];
+        if constexpr (kGate) {
+            const u32x4 zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (uint32_t h = 0; h < 2u; ++h) staged_gate[h] = gate_lane ? x.g[h] : zero;
+        }
     };
     // the MFMAs of the staged chunk over `steps` (1 or 2) K steps
     auto multiply = [&](uint32_t steps) __attribute__((always_inline)) {
@@ -108,6 +129,12 @@ __device__ __forceinline__ void wave_partial(const u32x4* const (&ga)[2 * (kTM +
                     for (uint32_t j = 0; j < kTN; ++j)
                         acc[v][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                             as_bf16x8(a[i]), as_bf16x8(b[v][j]), acc[v][i][j], 0, 0, 0);
+            if constexpr (kGate) {
+#pragma unroll
+                for (uint32_t i = 0; i < kTM; ++i)
+                    acc_gate[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        as_bf16x8(a[i]), as_bf16x8(staged_gate[h]), acc_gate[i], 0, 0, 0);
+            }
         }
     };
     if (chunks == 0u) return;
@@ -246,10 +273,10 @@ __device__ __forceinline__ uint32_t silu_multiply(uint32_t g_bits, uint32_t u_bi
     return f32_to_bf16((g / (1.0f + exp_q(-g))) * bf16_to_f32(u_bits));
 }
 
-// The shared expert's first half in one launch: block (x, y) with x below
-// the last column computes the 32 x 32 tiles (y, x) of g = bf16(X Wg^T) and
-// u = bf16(X Wu^T) and h = silu_multiply(g, u) from them; the last column
-// of blocks computes the scalar output gate bf16(X wo^T) of its 32 rows.
+// The shared expert's first half in one launch: block (x, y) computes the
+// 32 x 32 tiles (y, x) of g = bf16(X Wg^T) and u = bf16(X Wu^T) and
+// h = silu_multiply(g, u) from them; the blocks of column 0 also compute
+// the scalar output gate bf16(X wo^T) of their 32 rows.
 __global__ __launch_bounds__(256) void shared_gate_up_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w_gate,
     const uint16_t* __restrict__ w_up, const uint16_t* __restrict__ w_out_gate, uint32_t m,
@@ -259,37 +286,13 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
     constexpr uint32_t kL = 2u * (kTM + 2u * kTN);
     __shared__ u32x4 slab[kDenseWaves * kL * 64];
     __shared__ f32x4 lds[kDenseWaves * 2 * kTM * kTN * 64];
+    __shared__ float gate_lds[kDenseWaves][16 * kTM];
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t m0 = blockIdx.y * 16u * kTM;
+    const uint32_t n0 = blockIdx.x * 16u * kTN;
     const uint32_t steps = kHidden / 32u;
     const uint32_t s0 = wave * steps / kDenseWaves, s1 = (wave + 1u) * steps / kDenseWaves;
-    u32x4* const wave_slab = slab + wave * kL * 64u;
-    if (blockIdx.x == gridDim.x - 1u) {
-        const u32x4* ga[2u * (kTM + 1u)];
-#pragma unroll
-        for (uint32_t h = 0; h < 2u; ++h) {
-#pragma unroll
-            for (uint32_t i = 0; i < kTM; ++i)
-                ga[2u * i + h] = stage_ptr(x, m0 + 16u * i, m, kHidden, h, lane);
-            ga[2u * kTM + h] = stage_ptr(w_out_gate, 0u, 1u, kHidden, h, lane);
-        }
-        f32x4 acc[1][kTM][1];
-#pragma unroll
-        for (uint32_t i = 0; i < kTM; ++i) acc[0][i][0] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        wave_partial<kTM, 1, 1>(ga, wave_slab, lane, s0, s1, acc);
-        reduce_waves<kTM, kTM>(lds, &acc[0][0][0], wave, lane,
-                               [&](uint32_t o, uint32_t, f32x4 sum) {
-            if ((lane & 15u) != 0u) return;  // column 0 holds the gate
-#pragma unroll
-            for (uint32_t e = 0; e < 4u; ++e) {
-                const uint32_t row = m0 + 16u * o + 4u * (lane >> 4) + e;
-                if (row < m) gate_out[row] = static_cast<uint16_t>(f32_to_bf16(sum[e]));
-            }
-        });
-        return;
-    }
-    const uint32_t n0 = blockIdx.x * 16u * kTN;
     const u32x4* ga[kL];
 #pragma unroll
     for (uint32_t h = 0; h < 2u; ++h) {
@@ -309,7 +312,25 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
         for (uint32_t i = 0; i < kTM; ++i)
 #pragma unroll
             for (uint32_t j = 0; j < kTN; ++j) acc[v][i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    wave_partial<kTM, kTN, 2>(ga, wave_slab, lane, s0, s1, acc);
+    f32x4 acc_gate[kTM];
+#pragma unroll
+    for (uint32_t i = 0; i < kTM; ++i) acc_gate[i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    u32x4* const wave_slab = slab + wave * kL * 64u;
+    const bool with_gate = blockIdx.x == 0u;
+    if (with_gate) {
+        const u32x4* gate = reinterpret_cast<const u32x4*>(w_out_gate + 8u * (lane >> 4));
+        wave_partial<kTM, kTN, 2, true>(ga, wave_slab, lane, s0, s1, acc, gate, acc_gate);
+        // column 0 of the gate tiles: lane 16 q holds rows 4 q + e of panel i
+        if ((lane & 15u) == 0u) {
+#pragma unroll
+            for (uint32_t i = 0; i < kTM; ++i)
+#pragma unroll
+                for (uint32_t e = 0; e < 4u; ++e)
+                    gate_lds[wave][16u * i + 4u * (lane >> 4) + e] = acc_gate[i][e];
+        }
+    } else {
+        wave_partial<kTM, kTN, 2>(ga, wave_slab, lane, s0, s1, acc);
+    }
     uint32_t g_bits[4] = {0u, 0u, 0u, 0u};
     reduce_waves<2 * kTM * kTN, kTM * kTN>(lds, &acc[0][0][0], wave, lane,
                                            [&](uint32_t o, uint32_t v, f32x4 sum) {
@@ -329,6 +350,15 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
             h_out[at] = static_cast<uint16_t>(silu_multiply(g_bits[e], bits));
         }
     });
+    // reduce_waves' barrier has made gate_lds visible; the gate's partials
+    // are summed in wave order like every other tile
+    if (with_gate && wave == 0u && lane < 16u * kTM) {
+        float sum = gate_lds[0][lane];
+#pragma unroll
+        for (uint32_t w = 1; w < kDenseWaves; ++w) sum += gate_lds[w][lane];
+        const uint32_t row = m0 + lane;
+        if (row < m) gate_out[row] = static_cast<uint16_t>(f32_to_bf16(sum));
+    }
 }
 
 }  // namespace
@@ -389,7 +419,7 @@ hipError_t launch_shared_expert(const uint16_t* hidden, const uint16_t* w_gate,
     uint16_t* g = static_cast<uint16_t*>(scratch);
     uint16_t* u = g + elements;
     uint16_t* h = u + elements;
-    const dim3 grid(inter / 32u + 1u, (tokens + 31u) / 32u);
+    const dim3 grid(inter / 32u, (tokens + 31u) / 32u);
     shared_gate_up_kernel<<<grid, 256, 0, stream>>>(hidden, w_gate, w_up, w_out_gate, tokens,
                                                     inter, g, u, h, shared_gate);
     hipError_t e = hipGetLastError();
