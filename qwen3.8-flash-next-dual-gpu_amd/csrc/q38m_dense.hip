@@ -27,6 +27,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 constexpr uint32_t kDenseWaves = 4;
+// the 64 x 64 workgroup tile serves K up to this and grids of at least
+// this many tiles
+constexpr uint32_t kTile64MaxK = 1024;
+constexpr uint32_t kTile64MinTiles = 192;
 
 // Operands reach the MFMAs through a per-wave LDS slab.  A wave's panels
 // (16 rows each: its A panels, then its B panels) are stacked into one list
@@ -266,6 +270,141 @@ __global__ __launch_bounds__(256) void dense_gemm_kernel(
     });
 }
 
+// C[M][N] = A[M][K] * B[N][K]^T for a 64 x 64 tile of C per workgroup, for
+// short K (the products whose grid of 64 x 64 tiles fills the GPU): the
+// four waves share each 64-wide K chunk of the tile's 64 A rows and 64 B
+// rows (16 KB, four whole-line loads per thread) in a double-buffered LDS
+// stage, and wave w multiplies its 32 x 32 quarter (rows 32 (w/2), columns
+// 32 (w%2)) over all of K, the K steps in increasing order.  Two chunks are
+// in flight in registers; the barriers wait for LDS only.
+template <DenseOut kOut>
+__global__ __launch_bounds__(256) void dense_tile64_kernel(
+    const uint16_t* __restrict__ a, const uint16_t* __restrict__ b, uint32_t m, uint32_t n,
+    uint32_t k, float* __restrict__ c_f32, uint16_t* __restrict__ c_bf16, float divisor,
+    float scale) {
+    constexpr uint32_t kRows = 128;  // 64 A rows, then 64 B rows
+    __shared__ u32x4 stage_lds[2][kRows * 8];
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t m0 = blockIdx.y * 64u, n0 = blockIdx.x * 64u;
+    // staging instruction i: stacked row 32 i + t/8, 16-byte chunk t%8,
+    // kept in slot (t%8) ^ (row%8)
+    const u32x4* gp[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        const uint32_t row = 32u * i + (t >> 3);
+        const uint16_t* base = row < 64u ? a + static_cast<size_t>(min(m0 + row, m - 1u)) * k
+                                         : b + static_cast<size_t>(min(n0 + row - 64u, n - 1u)) * k;
+        gp[i] = reinterpret_cast<const u32x4*>(base + (t & 7u) * 8u);
+    }
+    const uint32_t write_at = 8u * (t >> 3) + ((t & 7u) ^ ((t >> 3) & 7u));
+    const uint32_t read_at = 8u * (lane & 15u);
+    const uint32_t read_slot[2] = {(lane >> 4) ^ (lane & 7u), (4u + (lane >> 4)) ^ (lane & 7u)};
+    const uint32_t a_row = 32u * (wave >> 1), b_row = 64u + 32u * (wave & 1u);
+    const uint32_t steps = k / 32u;
+    const uint32_t chunks = (steps + 1u) / 2u;
+    const uint32_t last_steps = steps - 2u * (chunks - 1u);
+    const size_t back = (t & 7u) < 4u ? 0u : 4u;
+    struct Chunk {
+        u32x4 v[4];
+    };
+    auto load = [&](Chunk& x, uint32_t c) __attribute__((always_inline)) {
+        const uint32_t s = 2u * c;
+        const size_t shift = s + 1u < steps ? 0u : back;  // a half chunk re-reads its step
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) x.v[i] = *(gp[i] + 4u * s - shift);
+    };
+    auto stage = [&](const Chunk& x, uint32_t slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) stage_lds[slot][256u * i + write_at] = x.v[i];
+    };
+    auto lds_barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    f32x4 acc[2][2];
+#pragma unroll
+    for (uint32_t i = 0; i < 2u; ++i)
+#pragma unroll
+        for (uint32_t j = 0; j < 2u; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto multiply = [&](uint32_t slot, uint32_t count) __attribute__((always_inline)) {
+        const u32x4* lds = stage_lds[slot];
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; ++h) {
+            if (h >= count) break;
+            u32x4 av[2], bv[2];
+#pragma unroll
+            for (uint32_t i = 0; i < 2u; ++i) {
+                av[i] = lds[8u * (a_row + 16u * i) + read_at + read_slot[h]];
+                bv[i] = lds[8u * (b_row + 16u * i) + read_at + read_slot[h]];
+            }
+#pragma unroll
+            for (uint32_t i = 0; i < 2u; ++i)
+#pragma unroll
+                for (uint32_t j = 0; j < 2u; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        as_bf16x8(av[i]), as_bf16x8(bv[j]), acc[i][j], 0, 0, 0);
+        }
+    };
+    Chunk x0, x1;
+    load(x0, 0u);
+    if (chunks == 1u) {
+        stage(x0, 0u);
+        lds_barrier();
+        multiply(0u, last_steps);
+    } else {
+        load(x1, 1u);
+        stage(x0, 0u);
+        lds_barrier();
+        // at the top of each pass: chunk c in slot 0, chunk c + 1 in flight in x1
+        uint32_t c = 0;
+        for (; c + 3u < chunks; c += 2u) {
+            load(x0, c + 2u);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(0u, 2u);
+            stage(x1, 1u);
+            lds_barrier();
+            load(x1, c + 3u);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(1u, 2u);
+            stage(x0, 0u);
+            lds_barrier();
+        }
+        if (chunks - c == 3u) {
+            load(x0, c + 2u);
+            __builtin_amdgcn_sched_barrier(0);
+            multiply(0u, 2u);
+            stage(x1, 1u);
+            lds_barrier();
+            multiply(1u, 2u);
+            stage(x0, 0u);
+            lds_barrier();
+            multiply(0u, last_steps);
+        } else {
+            multiply(0u, 2u);
+            stage(x1, 1u);
+            lds_barrier();
+            multiply(1u, last_steps);
+        }
+    }
+    // D layout: lane l holds rows 4 (l/16) + e of column l%16 of each tile
+#pragma unroll
+    for (uint32_t i = 0; i < 2u; ++i)
+#pragma unroll
+        for (uint32_t j = 0; j < 2u; ++j) {
+            const uint32_t col = n0 + 32u * (wave & 1u) + 16u * j + (lane & 15u);
+#pragma unroll
+            for (uint32_t e = 0; e < 4u; ++e) {
+                const uint32_t row = m0 + a_row + 16u * i + 4u * (lane >> 4) + e;
+                if (row >= m || col >= n) continue;
+                const size_t at = static_cast<size_t>(row) * n + col;
+                if constexpr (kOut == DenseOut::kF32)
+                    c_f32[at] = acc[i][j][e];
+                else
+                    c_bf16[at] =
+                        static_cast<uint16_t>(dense_epilogue(kOut, acc[i][j][e], divisor, scale));
+            }
+        }
+}
+
 // h = bf16(g / (1 + exp(-g)) * u) on bf16 g and u (q38_kernels.cu:286-296,
 // with this library's exp).
 __device__ __forceinline__ uint32_t silu_multiply(uint32_t g_bits, uint32_t u_bits) {
@@ -369,6 +508,15 @@ template <DenseOut kOut>
 void launch_dense_tiles(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n, uint32_t k,
                         float* c_f32, uint16_t* c_bf16, float divisor, float scale,
                         hipStream_t stream) {
+    // short K with a 64 x 64 grid that fills the GPU: workgroup-shared
+    // tiles read half the bytes per output of the K-split 32 x 32 tiles
+    const uint32_t tiles64 = ((m + 63u) / 64u) * ((n + 63u) / 64u);
+    if (k <= kTile64MaxK && tiles64 >= kTile64MinTiles) {
+        const dim3 grid((n + 63u) / 64u, (m + 63u) / 64u);
+        dense_tile64_kernel<kOut><<<grid, 256, 0, stream>>>(a, b, m, n, k, c_f32, c_bf16, divisor,
+                                                            scale);
+        return;
+    }
     const uint32_t tm = m <= 16u ? 1u : 2u;
     const uint32_t tn = (m <= 16u || n <= 16u) ? 1u : 2u;
     const dim3 grid((n + 16u * tn - 1u) / (16u * tn), (m + 16u * tm - 1u) / (16u * tm));
