@@ -87,6 +87,17 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     // every lane's weights: lane = kq + 16*(c + 2u), u = gate/up, c = channel
     const uint32_t route = wave;
     const int32_t id = route < top_k ? ids_lds[route] : -1;
+    // the route's weight, while the weights stream: given, or
+    // exp(l_r - l_0) over the rank-order sum (q38_kernels.cu:460-479)
+    float wr = 0.0f;
+    if (route < top_k) {
+        wr = num_lds[route];
+        if (fused) {
+            float denominator = 0.0f;
+            for (uint32_t r = 0; r < top_k; ++r) denominator += num_lds[r];
+            wr = wr / denominator;
+        }
+    }
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
     const uint32_t kq = lane & 15u;
@@ -195,9 +206,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
             }
         if constexpr (kPer == H / 64u) {
             // per channel: one int32 over the row (16 lanes), y = (float)acc * s
+            // the row's 16 lanes by DPP rotations (row_ror 8, 4, 2, 1)
             int sum = acc[0] + acc[1];
-#pragma unroll
-            for (int offset = 8; offset > 0; offset >>= 1) sum += __shfl_xor(sum, offset, 16);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x128, 0xf, 0xf, false);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x124, 0xf, 0xf, false);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x122, 0xf, 0xf, false);
+            sum += __builtin_amdgcn_update_dpp(0, sum, 0x121, 0xf, 0xf, false);
             y = static_cast<float>(sum) * scale_to_f32(sw, bf16);
         } else {
             float gs[2];
@@ -226,18 +240,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 31));
     const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 47));
     const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 63));
-    if (lane == 0 && route < top_k) {
-        float wr = num_lds[route];
-        if (fused) {
-            // exp(l_r - l_0) over the rank-order sum (q38_kernels.cu:460-479)
-            float denominator = 0.0f;
-            for (uint32_t r = 0; r < top_k; ++r) denominator += num_lds[r];
-            wr = wr / denominator;
-        }
-        const uint32_t m0 = valid ? swiglu_fold(g0 * xs, u0 * xs, wr) : 0u;
-        const uint32_t m1 = valid ? swiglu_fold(g1 * xs, u1 * xs, wr) : 0u;
-        *reinterpret_cast<uint32_t*>(mid + static_cast<size_t>(route) * I + 16u * pair + n0) =
-            m0 | (m1 << 16);
+    // lane n computes channel n0 + n (n = 0, 1)
+    if (lane < 2u && route < top_k) {
+        const float g = lane == 0u ? g0 : g1;
+        const float up = lane == 0u ? u0 : u1;
+        const uint32_t m = valid ? swiglu_fold(g * xs, up * xs, wr) : 0u;
+        mid[static_cast<size_t>(route) * I + 16u * pair + n0 + lane] = static_cast<uint16_t>(m);
     }
 }
 
@@ -376,9 +384,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
             acc = __builtin_amdgcn_sdot4(static_cast<int>(bq[q].w), static_cast<int>(xv.w), acc, false);
         }
         if constexpr (kPerGroup == kBlocks) {
-            acc += __shfl_xor(acc, 8, 64);
-            acc += __shfl_xor(acc, 16, 64);
-            acc += __shfl_xor(acc, 32, 64);
+            // lanes c + 8 kb, kb = 0..7: row_ror 8 within the row, then the
+            // row pairs and the halves by the permlane swaps
+            acc += __builtin_amdgcn_update_dpp(0, acc, 0x128, 0xf, 0xf, false);
+            const auto rows = __builtin_amdgcn_permlane16_swap(acc, acc, false, false);
+            acc = static_cast<int>(rows[0]) + static_cast<int>(rows[1]);
+            const auto halves = __builtin_amdgcn_permlane32_swap(acc, acc, false, false);
+            acc = static_cast<int>(halves[0]) + static_cast<int>(halves[1]);
             o = (static_cast<float>(acc) * ws) * sm;
         } else {
             // group g = kb / kPerGroup: its blocks' sum, then the chain over

@@ -53,10 +53,32 @@ __device__ __forceinline__ uint32_t group8_sum(uint32_t x) {
     return x;
 }
 
+// Reductions over the 64 lanes of a wave without LDS round trips: the quad
+// and row steps by DPP (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror), then row pairs and wave halves by the permlane swaps (with
+// both operands x, permlane16_swap returns rows [0,0,2,2] and [1,1,3,3],
+// permlane32_swap the halves [lo,lo] and [hi,hi]).  Every lane receives the
+// result.  For max and integer sums the order of the steps does not matter.
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t x, Op op) {
+    x = op(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0xb1, 0xf, 0xf, false)));
+    x = op(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x4e, 0xf, 0xf, false)));
+    x = op(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x141, 0xf, 0xf, false)));
+    x = op(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x140, 0xf, 0xf, false)));
+    const auto rows = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    x = op(static_cast<uint32_t>(rows[0]), static_cast<uint32_t>(rows[1]));
+    const auto halves = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return op(static_cast<uint32_t>(halves[0]), static_cast<uint32_t>(halves[1]));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+    return wave_reduce_u32(x, [](uint32_t a, uint32_t b) { return max(a, b); });
+}
+
 __device__ __forceinline__ float wave_max_f32(float x) {
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) x = fmaxf(x, __shfl_xor(x, offset, 64));
-    return x;
+    return __uint_as_float(wave_reduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    }));
 }
 
 // Called by all kSelectThreads threads of the block; `logit` is the row
@@ -71,9 +93,17 @@ __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32
         // 1. the wave's top 10 (wave-uniform control flow: ballots only)
         const uint32_t k32 = order_key(logit);
         uint32_t prefix = 0u;
+#pragma unroll
         for (int b = 31; b >= 0; --b) {
+            // four scalar instructions per bit (count, compare, select,
+            // next candidate): the eight waves share the CU's scalar unit,
+            // and the compiler's own popcount of a 64-bit ballot adds a
+            // 64-bit vector compare and an exec mask step
             const uint32_t cand = prefix | (1u << b);
-            if (__popcll(__ballot(k32 >= cand)) >= kTopK) prefix = cand;
+            const uint64_t reach = __builtin_amdgcn_ballot_w64(k32 >= cand);
+            uint32_t count;
+            asm("s_bcnt1_i32_b64 %0, %1" : "=s"(count) : "s"(reach));
+            prefix = count >= kTopK ? cand : prefix;
         }
         const uint64_t below = (1ull << lane) - 1ull;
         const uint64_t above = __ballot(k32 > prefix);
@@ -86,10 +116,7 @@ __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32
             const uint32_t at = static_cast<uint32_t>(__popcll(chosen & below));
             lds.cand[kTopK * (t >> 6) + at] = (static_cast<uint64_t>(k32) << 32) | (kExperts - 1u - t);
         }
-        uint32_t kmax = k32;
-#pragma unroll
-        for (int offset = 32; offset > 0; offset >>= 1)
-            kmax = max(kmax, static_cast<uint32_t>(__shfl_xor(static_cast<int>(kmax), offset, 64)));
+        const uint32_t kmax = wave_max_u32(k32);
         if (lane == 0u) lds.wave_max[t >> 6] = kmax;
     }
     __syncthreads();
