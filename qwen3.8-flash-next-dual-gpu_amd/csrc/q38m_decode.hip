@@ -262,7 +262,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     static_assert(I == 64u * 8u, "one 8-element chunk of the mid row per lane");
     static_assert(kTiles * 2u == kDecodeBlocks, "eight output channels per workgroup");
     __shared__ uint4 mq_lds[kTopK][I / 16u];
-    __shared__ float o_lds[kTopK][8];
+    // route partials per output channel, ten routes padded to 12 floats
+    __shared__ float4 o_lds[8][3];
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t route = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -270,6 +271,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     const uint32_t tile = 16u * (blockIdx.x & 7u) + (slot8 >> 1);
     const uint32_t n0 = 8u * (slot8 & 1u);
     const bool active = route < top_k;
+
+    // the epilogue's operands, requested first: they depend on nothing
+    const uint32_t channel = 16u * tile + n0 + (threadIdx.x & 7u);
+    const bool finisher = threadIdx.x < 8u;
+    uint32_t residual_bits = 0u, shared_bits = 0u, gate_bits = 0u;
+    if (finisher) {
+        if (residual != nullptr) residual_bits = residual[channel];
+        if (shared_output != nullptr && shared_gate != nullptr) {
+            shared_bits = shared_output[channel];
+            gate_bits = shared_gate[0];
+        }
+    }
 
     const int32_t id = active ? ids[route] : -1;
     uint4 mv = make_uint4(0u, 0u, 0u, 0u);
@@ -407,20 +420,26 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
             o = __shfl(y, static_cast<int>(8u * kPerGroup * (kW8Groups - 1u) + c), 64) * sm;
         }
     }
-    if (lane < 8u) o_lds[route][lane] = valid ? o : 0.0f;
+    if (lane < 8u) reinterpret_cast<float*>(o_lds[lane])[route] = valid ? o : 0.0f;
     __syncthreads();
-    if (threadIdx.x < 8u) {
-        const uint32_t channel = 16u * tile + n0 + threadIdx.x;
+    if (finisher) {
+        // routes summed in rank order
+        const float4 p0 = o_lds[threadIdx.x][0], p1 = o_lds[threadIdx.x][1];
+        const float4 p2 = o_lds[threadIdx.x][2];
+        const float part[12] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w,
+                                p2.x, p2.y, p2.z, p2.w};
         float total = 0.0f;
-        for (uint32_t r = 0; r < top_k; ++r) total += o_lds[r][threadIdx.x];
+#pragma unroll
+        for (uint32_t r = 0; r < kTopK; ++r)
+            if (r < top_k) total += part[r];
         if (shared_output != nullptr && shared_gate != nullptr) {
-            const float g = bf16_to_f32(shared_gate[0]);
+            const float g = bf16_to_f32(gate_bits);
             const float multiplier = 1.0f / (1.0f + exp_q(-g));
-            total = __builtin_fmaf(bf16_to_f32(shared_output[channel]), multiplier, total);
+            total = __builtin_fmaf(bf16_to_f32(shared_bits), multiplier, total);
         }
         uint32_t result = f32_to_bf16(total);
         if (residual != nullptr)
-            result = f32_to_bf16(bf16_to_f32(residual[channel]) + bf16_to_f32(result));
+            result = f32_to_bf16(bf16_to_f32(residual_bits) + bf16_to_f32(result));
         out[channel] = static_cast<uint16_t>(result);
     }
 }
