@@ -87,17 +87,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     // every lane's weights: lane = kq + 16*(c + 2u), u = gate/up, c = channel
     const uint32_t route = wave;
     const int32_t id = route < top_k ? ids_lds[route] : -1;
-    // the route's weight, while the weights stream: given, or
-    // exp(l_r - l_0) over the rank-order sum (q38_kernels.cu:460-479)
-    float wr = 0.0f;
-    if (route < top_k) {
-        wr = num_lds[route];
-        if (fused) {
-            float denominator = 0.0f;
-            for (uint32_t r = 0; r < top_k; ++r) denominator += num_lds[r];
-            wr = wr / denominator;
-        }
-    }
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
     const uint32_t kq = lane & 15u;
@@ -134,6 +123,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
             sw = *reinterpret_cast<const uint32_t*>(s + row * kBlocks + 2u * kq);
         else
             sw = s[row * (kBlocks / 2u) + kq];
+    }
+
+    // the route's weight, while the weights stream: given, or
+    // exp(l_r - l_0) over the rank-order sum (q38_kernels.cu:460-479)
+    float wr = 0.0f;
+    if (route < top_k) {
+        wr = num_lds[route];
+        if (fused) {
+            float denominator = 0.0f;
+            for (uint32_t r = 0; r < top_k; ++r) denominator += num_lds[r];
+            wr = wr / denominator;
+        }
     }
 
     // int8 token (same arithmetic as the row quantiser); the barrier waits
