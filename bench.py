@@ -895,6 +895,20 @@ def bench_router_shared(q38m, W, torch, hidden, steps):
         q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), T, W.HIDDEN,
                   logits.data_ptr(), sh, 0)
 
+    ids = torch.empty(T, W.TOPK, dtype=torch.int32, device="cuda")
+    wts = torch.empty(T, W.TOPK, dtype=torch.float32, device="cuda")
+    topk_ws_bytes = q38m.lib().q38m_moe_router_topk_workspace_bytes(T)
+    topk_ws = torch.empty(topk_ws_bytes, dtype=torch.uint8, device="cuda")
+
+    def run_router_then_topk():
+        run_router()
+        q38m.call("q38m_topk_router_f32", logits.data_ptr(), ids.data_ptr(), wts.data_ptr(), T,
+                  W.EXPERTS, W.TOPK, 1, sh, 0)
+
+    def run_router_topk():
+        q38m.call("q38m_moe_router_topk_v1", hidden.data_ptr(), router.data_ptr(), T, W.HIDDEN,
+                  W.TOPK, topk_ws.data_ptr(), topk_ws_bytes, ids.data_ptr(), wts.data_ptr(), sh, 0)
+
     def run_shared():
         q38m.call("q38m_moe_shared_expert_v1", hidden.data_ptr(), wg.data_ptr(), wu.data_ptr(),
                   wd.data_ptr(), wo.data_ptr(), T, W.HIDDEN, I, scratch.data_ptr(), so.data_ptr(),
@@ -913,6 +927,7 @@ def bench_router_shared(q38m, W, torch, hidden, steps):
         return start.elapsed_time(stop) / steps
 
     r_ms, s_ms = timed(run_router), timed(run_shared)
+    rt_ms, rtk_ms = timed(run_router_then_topk), timed(run_router_topk)
     r_flops = 2 * T * W.EXPERTS * W.HIDDEN
     r_bytes = 2 * T * W.HIDDEN + 2 * W.EXPERTS * W.HIDDEN + 4 * T * W.EXPERTS
     s_flops = 2 * T * W.HIDDEN * (3 * I + 1)
@@ -926,6 +941,12 @@ def bench_router_shared(q38m, W, torch, hidden, steps):
                      "bf16_mfma_frac": round(flops / s / 1e12 / BF16_PEAK_TFLOPS, 4),
                      "GBps": round(nbytes / s / 1e9, 1),
                      "hbm_frac": round(nbytes / s / 1e9 / HBM_PEAK_GBPS, 4)}
+    out["router_then_topk_ms"] = round(rt_ms, 5)
+    out["router_topk_fused_ms"] = round(rtk_ms, 5)
+    out["router_topk_note"] = ("q38m_moe_router_v1 + q38m_topk_router_f32 (fp32 logits written "
+                               "and re-read) vs q38m_moe_router_topk_v1 (level-1 selection in "
+                               "the GEMM epilogue, 80 candidate keys per token); same ids and "
+                               "weights")
     out["tokens"] = T
     return out
 

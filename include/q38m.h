@@ -459,6 +459,24 @@ int q38m_moe_router_v1(const uint16_t* hidden, const uint16_t* router,
                        uint32_t tokens, uint32_t hidden_width, float* logits,
                        void* stream, int device);
 
+/* Router GEMM and top-k selection without the fp32 logits in memory: the
+ * router step of run_moe (cuda/cuda_backend.cu:1518-1525: the router GEMM,
+ * then cuda_topk_router_bf16 with 512 experts and normalize_top_k = true,
+ * include/q38/cuda_kernels.h:83-91) in two launches.  The first computes
+ * the logits exactly as q38m_moe_router_v1 does and keeps each 64-expert
+ * block's top 10 per token (keys in the workspace); the second ranks the
+ * 80 candidates per token.  expert_ids / expert_weights [T][top_k] equal
+ * q38m_topk_router_f32 (512 experts, normalised) on q38m_moe_router_v1's
+ * logits, bit for bit.  hidden_width must be Q38M_HIDDEN; 1 <= top_k <= 10;
+ * workspace (16-byte aligned) of q38m_moe_router_topk_workspace_bytes(T).
+ * No single reference function: the reference runs these as two calls. */
+size_t q38m_moe_router_topk_workspace_bytes(uint32_t tokens);
+int q38m_moe_router_topk_v1(const uint16_t* hidden, const uint16_t* router,
+                            uint32_t tokens, uint32_t hidden_width,
+                            uint32_t top_k, void* workspace,
+                            size_t workspace_bytes, int32_t* expert_ids,
+                            float* expert_weights, void* stream, int device);
+
 /* Shared expert of the MoE block (cuda/cuda_backend.cu:1573-1590), bf16
  * weights: g = bf16(x Wg^T), u = bf16(x Wu^T) [T][inter],
  * h = bf16(g / (1 + exp(-g)) * u) (cuda_silu_multiply_bf16,

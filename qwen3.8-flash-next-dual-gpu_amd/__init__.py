@@ -166,6 +166,8 @@ SIGNATURES = {
     "q38m_quantize_expert_weights": (_INT, [_P, ctypes.POINTER(ExpertWeights), _P, _INT]),
     "q38m_dense_gemm_bf16": (_INT, [_P, _P, _U32, _U32, _U32, _P, _P, _P, _INT]),
     "q38m_moe_router_v1": (_INT, [_P, _P, _U32, _U32, _P, _P, _INT]),
+    "q38m_moe_router_topk_workspace_bytes": (_SZ, [_U32]),
+    "q38m_moe_router_topk_v1": (_INT, [_P, _P, _U32, _U32, _U32, _P, _SZ, _P, _P, _P, _INT]),
     "q38m_moe_shared_expert_scratch_bytes": (_SZ, [_U32, _U32]),
     "q38m_moe_shared_expert_v1": (_INT, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _P, _P, _P, _P,
                                          _INT]),

@@ -740,6 +740,28 @@ int q38m_moe_router_v1(const uint16_t* hidden, const uint16_t* router, uint32_t 
                   "router GEMM");
 }
 
+size_t q38m_moe_router_topk_workspace_bytes(uint32_t tokens) {
+    return q38m::router_topk_workspace_bytes(tokens);
+}
+
+int q38m_moe_router_topk_v1(const uint16_t* hidden, const uint16_t* router, uint32_t tokens,
+                            uint32_t hidden_width, uint32_t top_k, void* workspace,
+                            size_t workspace_bytes, int32_t* expert_ids, float* expert_weights,
+                            void* stream, int device) {
+    if (hidden_width != Q38M_HIDDEN)
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "router hidden width must be 2048");
+    // the selection grid's y dimension holds one 16-token block per workgroup
+    if (!hidden || !router || !workspace || !expert_ids || !expert_weights || tokens == 0 ||
+        tokens > 65535u * 16u || top_k == 0 || top_k > Q38M_ROUTE_TOPK ||
+        !aligned(hidden, 16) || !aligned(router, 16) || !aligned(workspace, 16) ||
+        workspace_bytes < q38m::router_topk_workspace_bytes(tokens))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid router top-k buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_router_topk(hidden, router, tokens, top_k, workspace, expert_ids,
+                                           expert_weights, as_stream(stream)),
+                  "router top-k kernels");
+}
+
 size_t q38m_moe_shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter) {
     return q38m::shared_expert_scratch_bytes(tokens, inter);
 }

@@ -13,6 +13,7 @@
 // partial sums is fixed, so a launch's results are the same on every run.
 #include "q38m_device.h"
 #include "q38m_internal.h"
+#include "q38m_select.h"
 
 namespace q38m {
 namespace {
@@ -405,6 +406,92 @@ __global__ __launch_bounds__(256) void dense_tile64_kernel(
         }
 }
 
+// Router logits with the first level of the top-10 selection in the
+// epilogue (the router GEMM, cuda_backend.cu:1518-1519, fused with level 1
+// of cuda_topk_router_bf16's selection, q38_kernels.cu:406-458): workgroup
+// (b, y) computes tokens 16y .. 16y+15 against experts 64b .. 64b+63 with
+// the four waves splitting K exactly as dense_gemm_kernel does, so every
+// logit is the value q38m_moe_router_v1 writes, bit for bit; the 16 x 64
+// logits then stay in LDS, and wave w selects the top 10 of tokens 4w ..
+// 4w+3 over its block (wave_top10), writing ten keys per (token, block)
+// and the block's largest order key.  The fp32 logits never leave the CU.
+__global__ __launch_bounds__(256) void router_select_kernel(
+    const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ router, uint32_t m,
+    uint64_t* __restrict__ cand, uint32_t* __restrict__ block_max) {
+    constexpr uint32_t kTM = 1, kTN = 4;
+    constexpr uint32_t kL = 2u * (kTM + kTN);
+    constexpr uint32_t kBlocks = kExperts / 64u;
+    __shared__ u32x4 slab[kDenseWaves * kL * 64];
+    __shared__ f32x4 lds[kDenseWaves * kTM * kTN * 64];
+    __shared__ float logit_lds[16][64];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t m0 = blockIdx.y * 16u;
+    const uint32_t n0 = blockIdx.x * 64u;
+    const u32x4* ga[kL];
+#pragma unroll
+    for (uint32_t h = 0; h < 2u; ++h) {
+        ga[h] = stage_ptr(hidden, m0, m, kHidden, h, lane);
+#pragma unroll
+        for (uint32_t j = 0; j < kTN; ++j)
+            ga[2u * (kTM + j) + h] = stage_ptr(router, n0 + 16u * j, kExperts, kHidden, h, lane);
+    }
+    f32x4 acc[1][kTM][kTN];
+#pragma unroll
+    for (uint32_t j = 0; j < kTN; ++j) acc[0][0][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr uint32_t steps = kHidden / 32u;
+    wave_partial<kTM, kTN, 1>(ga, slab + wave * kL * 64u, lane, wave * steps / kDenseWaves,
+                              (wave + 1u) * steps / kDenseWaves, acc);
+    // tile o: tokens 4 (l/16) + e, experts 16 o + l%16
+    reduce_waves<kTM * kTN, kTM * kTN>(lds, &acc[0][0][0], wave, lane,
+                                       [&](uint32_t o, uint32_t, f32x4 sum) {
+#pragma unroll
+        for (uint32_t e = 0; e < 4u; ++e) logit_lds[4u * (lane >> 4) + e][16u * o + (lane & 15u)] = sum[e];
+    });
+    __syncthreads();
+    // wave w: tokens 4w .. 4w+3, their four selections interleaved (rows
+    // past the last token select over their clamped copies and store nothing)
+    uint32_t k32[4], kmax[4];
+#pragma unroll
+    for (uint32_t r = 0; r < 4u; ++r) k32[r] = order_key(logit_lds[4u * wave + r][lane]);
+    const size_t slot0 = static_cast<size_t>(m0 + 4u * wave) * kBlocks + blockIdx.x;
+    wave_top10_rows<4>(k32, n0 + lane, [&](uint32_t r, uint32_t at, uint64_t key) {
+        if (m0 + 4u * wave + r < m) cand[(slot0 + r * kBlocks) * kTopK + at] = key;
+    }, kmax);
+    if (lane < 4u && m0 + 4u * wave + lane < m) {
+        const uint32_t mine = lane == 0u ? kmax[0] : lane == 1u ? kmax[1] : lane == 2u ? kmax[2] : kmax[3];
+        block_max[slot0 + lane * kBlocks] = mine;
+    }
+}
+
+// Level 2 of the fused router selection, one workgroup per token: the
+// eight blocks' candidate lists and maxima into LDS, rank_candidates, then
+// the rank-order denominator over the first top_k ranks and the weights
+// (q38_kernels.cu:460-479), as q38m_topk_router_f32 computes them.
+__global__ __launch_bounds__(kSelectThreads) void router_merge_kernel(
+    const uint64_t* __restrict__ cand, const uint32_t* __restrict__ block_max, uint32_t top_k,
+    int32_t* __restrict__ ids, float* __restrict__ weights) {
+    constexpr uint32_t kBlocks = kExperts / 64u;
+    __shared__ SelectLds select_lds;
+    __shared__ int32_t ids_lds[kTopK];
+    __shared__ float num_lds[kTopK];
+    const uint32_t token = blockIdx.x;
+    const uint32_t t = threadIdx.x;
+    if (t < kBlocks * kTopK) select_lds.cand[t] = cand[static_cast<size_t>(token) * kBlocks * kTopK + t];
+    if (t < kBlocks) select_lds.wave_max[t] = block_max[static_cast<size_t>(token) * kBlocks + t];
+    __syncthreads();
+    rank_candidates<kBlocks>(select_lds, ids_lds, num_lds);
+    __syncthreads();
+    if (t < 64u) {
+        float denominator = 0.0f;
+        for (uint32_t r = 0; r < top_k; ++r) denominator += num_lds[r];
+        if (t < top_k) {
+            ids[static_cast<size_t>(token) * top_k + t] = ids_lds[t];
+            weights[static_cast<size_t>(token) * top_k + t] = num_lds[t] / denominator;
+        }
+    }
+}
+
 // h = bf16(g / (1 + exp(-g)) * u) on bf16 g and u (q38_kernels.cu:286-296,
 // with this library's exp).
 __device__ __forceinline__ uint32_t silu_multiply(uint32_t g_bits, uint32_t u_bits) {
@@ -552,6 +639,26 @@ hipError_t launch_dense_gemm_act(const uint16_t* a, const uint16_t* b, uint32_t 
         launch_dense_tiles<DenseOut::kBf16Sigmoid>(a, b, m, n, k, nullptr, c_bf16, divisor,
                                                    scale, stream);
     return hipGetLastError();
+}
+
+size_t router_topk_workspace_bytes(uint32_t tokens) {
+    constexpr uint32_t kBlocks = kExperts / 64u;
+    return static_cast<size_t>(tokens) * kBlocks * (kTopK * sizeof(uint64_t) + sizeof(uint32_t));
+}
+
+hipError_t launch_router_topk(const uint16_t* hidden, const uint16_t* router, uint32_t tokens,
+                              uint32_t top_k, void* workspace, int32_t* ids, float* weights,
+                              hipStream_t stream) {
+    constexpr uint32_t kBlocks = kExperts / 64u;
+    uint64_t* cand = static_cast<uint64_t*>(workspace);
+    uint32_t* block_max = reinterpret_cast<uint32_t*>(cand + static_cast<size_t>(tokens) * kBlocks * kTopK);
+    router_select_kernel<<<dim3(kBlocks, (tokens + 15u) / 16u), 256, 0, stream>>>(
+        hidden, router, tokens, cand, block_max);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess)
+        router_merge_kernel<<<tokens, kSelectThreads, 0, stream>>>(cand, block_max, top_k, ids,
+                                                                   weights);
+    return e == hipSuccess ? hipGetLastError() : e;
 }
 
 size_t shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter) {

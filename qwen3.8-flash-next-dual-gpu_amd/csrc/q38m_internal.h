@@ -137,6 +137,12 @@ hipError_t launch_dense_gemm(const uint16_t* a, const uint16_t* b, uint32_t m, u
 hipError_t launch_dense_gemm_act(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n,
                                  uint32_t k, bool silu, float divisor, float scale,
                                  uint16_t* c_bf16, hipStream_t stream);
+// router logits with the top-10 selection: level 1 in the GEMM epilogue,
+// level 2 in a second launch; the workspace holds the candidate keys
+size_t router_topk_workspace_bytes(uint32_t tokens);
+hipError_t launch_router_topk(const uint16_t* hidden, const uint16_t* router, uint32_t tokens,
+                              uint32_t top_k, void* workspace, int32_t* ids, float* weights,
+                              hipStream_t stream);
 size_t shared_expert_scratch_bytes(uint32_t tokens, uint32_t inter);
 hipError_t launch_shared_expert(const uint16_t* hidden, const uint16_t* w_gate,
                                 const uint16_t* w_up, const uint16_t* w_down,

@@ -4,7 +4,8 @@
 // Order: value descending, expert id ascending on ties (the order of the
 // reference's sort, cuda/q38_kernels.cu:431-458), expressed as unique
 // 64-bit keys (order key << 32 | 511 - id) so that "larger key" is "ranked
-// first".  Two levels:
+// first".  Two levels (wave_top10, rank_candidates; the fused router GEMM
+// runs level 1 in its epilogue and level 2 in a second kernel):
 //   1. each of waves 0-7 finds the 10th largest 32-bit order key of its 64
 //      logits by a radix search on the wave's ballots (bit 31 down to 0:
 //      keep the bit if at least ten keys reach the prefix with it set), then
@@ -81,68 +82,131 @@ __device__ __forceinline__ float wave_max_f32(float x) {
     }));
 }
 
-// Called by all kSelectThreads threads of the block; `logit` is the row
-// entry of threads 0..511.  LDS writes the caller made before the call are
-// visible to the whole block on return.  On return ids[r] and num[r]
-// (r < 10) hold the rank-r expert and exp(l_r - l_0).
+// Level 1 for one wave: the wave's top 10 of its 64 order keys (k32 of
+// lane l, expert `expert`), found by a radix search on the wave's ballots
+// (bit 31 down to 0: keep the bit if at least ten keys reach the prefix
+// with it set), then every key above the threshold and, among the keys
+// equal to it, the lowest lanes up to ten.  Lanes must hold ascending
+// expert ids.  store(position, key64) receives the ten unique keys
+// (k32 << 32 | 511 - expert) in positions 0..9, unordered; returns the
+// wave's largest order key (in every lane).  Wave-uniform control flow.
+template <typename Store>
+__device__ __forceinline__ uint32_t wave_top10(uint32_t k32, uint32_t expert, Store store) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        // four scalar instructions per bit (count, compare, select, next
+        // candidate): the waves share the CU's scalar unit, and the
+        // compiler's own popcount of a 64-bit ballot adds a 64-bit vector
+        // compare and an exec mask step
+        const uint32_t cand = prefix | (1u << b);
+        const uint64_t reach = __builtin_amdgcn_ballot_w64(k32 >= cand);
+        uint32_t count;
+        asm("s_bcnt1_i32_b64 %0, %1" : "=s"(count) : "s"(reach));
+        prefix = count >= kTopK ? cand : prefix;
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    const uint64_t above = __ballot(k32 > prefix);
+    const uint64_t equal = __ballot(k32 == prefix);
+    const uint32_t need = kTopK - static_cast<uint32_t>(__popcll(above));
+    const bool mine_eq = k32 == prefix && static_cast<uint32_t>(__popcll(equal & below)) < need;
+    const uint64_t chosen = above | __ballot(mine_eq);
+    if (k32 > prefix || mine_eq)
+        store(static_cast<uint32_t>(__popcll(chosen & below)),
+              (static_cast<uint64_t>(k32) << 32) | (kExperts - 1u - expert));
+    return wave_max_u32(k32);
+}
+
+// wave_top10 over kRows independent rows at once (row r: k32[r] of lane
+// l, expert `expert`): the rows' radix searches advance together, one bit
+// per pass, so their scalar chains overlap.  store(row, position, key64);
+// kmax[r] receives row r's largest order key.
+template <uint32_t kRows, typename Store>
+__device__ __forceinline__ void wave_top10_rows(const uint32_t (&k32)[kRows], uint32_t expert,
+                                                Store store, uint32_t (&kmax)[kRows]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t prefix[kRows];
+#pragma unroll
+    for (uint32_t r = 0; r < kRows; ++r) prefix[r] = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+#pragma unroll
+        for (uint32_t r = 0; r < kRows; ++r) {
+            const uint32_t cand = prefix[r] | (1u << b);
+            const uint64_t reach = __builtin_amdgcn_ballot_w64(k32[r] >= cand);
+            uint32_t count;
+            asm("s_bcnt1_i32_b64 %0, %1" : "=s"(count) : "s"(reach));
+            prefix[r] = count >= kTopK ? cand : prefix[r];
+        }
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+#pragma unroll
+    for (uint32_t r = 0; r < kRows; ++r) {
+        const uint64_t above = __ballot(k32[r] > prefix[r]);
+        const uint64_t equal = __ballot(k32[r] == prefix[r]);
+        const uint32_t need = kTopK - static_cast<uint32_t>(__popcll(above));
+        const bool mine_eq =
+            k32[r] == prefix[r] && static_cast<uint32_t>(__popcll(equal & below)) < need;
+        const uint64_t chosen = above | __ballot(mine_eq);
+        if (k32[r] > prefix[r] || mine_eq)
+            store(r, static_cast<uint32_t>(__popcll(chosen & below)),
+                  (static_cast<uint64_t>(k32[r]) << 32) | (kExperts - 1u - expert));
+        kmax[r] = wave_max_u32(k32[r]);
+    }
+}
+
+// Level 2: lds.cand holds kLists lists of ten keys that contain the top 10
+// (every key above a top-10 key is in its list's top 10), lds.wave_max the
+// lists' largest order keys, visible to the block.  kLists threads per
+// candidate (threads t < 10 kLists^2) count the larger keys in one list
+// each and a DPP sum adds the counts: the global rank.  The thread holding
+// rank r writes ids[r] and num[r] = exp(l_r - l_0); values come back from
+// the keys (exactly, -0 as +0, which leaves every difference unchanged).
+template <uint32_t kLists>
+__device__ __forceinline__ void rank_candidates(const SelectLds& lds, int32_t* ids, float* num) {
+    static_assert(kLists == 8u, "groups of eight lanes");
+    const uint32_t t = threadIdx.x;
+    if (t >= kTopK * kLists * kLists) return;
+    const uint32_t c = t / kLists, list = t % kLists;
+    const uint64_t mine = lds.cand[c];
+    const uint64_t* other = lds.cand + kTopK * list;
+    uint32_t larger = 0;
+#pragma unroll
+    for (uint32_t j = 0; j < kTopK; j += 2u) {
+        const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(other + j);
+        larger += pr.x > mine ? 1u : 0u;
+        larger += pr.y > mine ? 1u : 0u;
+    }
+    // l_0's order key: the largest of the list maxima
+    const uint4 m0 = *reinterpret_cast<const uint4*>(lds.wave_max);
+    const uint4 m1 = *reinterpret_cast<const uint4*>(lds.wave_max + 4);
+    const uint32_t top = max(max(max(m0.x, m0.y), max(m0.z, m0.w)),
+                             max(max(m1.x, m1.y), max(m1.z, m1.w)));
+    const uint32_t rank = group8_sum(larger);
+    if (list == kLists - 1u && rank < kTopK) {
+        ids[rank] = static_cast<int32_t>(kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu));
+        num[rank] = exp_q(key_value(static_cast<uint32_t>(mine >> 32)) - key_value(top));
+    }
+}
+
+// Block-wide top-k of one 512-logit row: called by all kSelectThreads
+// threads of the block; `logit` is the row entry of threads 0..511.  LDS
+// writes the caller made before the call are visible to the whole block on
+// return.  On return ids[r] and num[r] (r < 10) hold the rank-r expert and
+// exp(l_r - l_0).
 __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32_t* ids,
                                               float* num) {
     const uint32_t t = threadIdx.x;
-    const uint32_t lane = t & 63u;
     if (t < kExperts) {
-        // 1. the wave's top 10 (wave-uniform control flow: ballots only)
-        const uint32_t k32 = order_key(logit);
-        uint32_t prefix = 0u;
-#pragma unroll
-        for (int b = 31; b >= 0; --b) {
-            // four scalar instructions per bit (count, compare, select,
-            // next candidate): the eight waves share the CU's scalar unit,
-            // and the compiler's own popcount of a 64-bit ballot adds a
-            // 64-bit vector compare and an exec mask step
-            const uint32_t cand = prefix | (1u << b);
-            const uint64_t reach = __builtin_amdgcn_ballot_w64(k32 >= cand);
-            uint32_t count;
-            asm("s_bcnt1_i32_b64 %0, %1" : "=s"(count) : "s"(reach));
-            prefix = count >= kTopK ? cand : prefix;
-        }
-        const uint64_t below = (1ull << lane) - 1ull;
-        const uint64_t above = __ballot(k32 > prefix);
-        const uint64_t equal = __ballot(k32 == prefix);
-        const uint32_t need = kTopK - static_cast<uint32_t>(__popcll(above));
-        const bool mine_eq = k32 == prefix &&
-                             static_cast<uint32_t>(__popcll(equal & below)) < need;
-        const uint64_t chosen = above | __ballot(mine_eq);
-        if (k32 > prefix || mine_eq) {
-            const uint32_t at = static_cast<uint32_t>(__popcll(chosen & below));
-            lds.cand[kTopK * (t >> 6) + at] = (static_cast<uint64_t>(k32) << 32) | (kExperts - 1u - t);
-        }
-        const uint32_t kmax = wave_max_u32(k32);
-        if (lane == 0u) lds.wave_max[t >> 6] = kmax;
+        uint64_t* list = lds.cand + kTopK * (t >> 6);
+        const uint32_t kmax = wave_top10(order_key(logit), t, [&](uint32_t at, uint64_t key) {
+            list[at] = key;
+        });
+        if ((t & 63u) == 0u) lds.wave_max[t >> 6] = kmax;
     }
     __syncthreads();
-    {
-        // 2. global ranks of the 80 candidates
-        const uint32_t c = t >> 3, list = t & 7u;
-        const uint64_t mine = lds.cand[c];
-        const uint64_t* other = lds.cand + kTopK * list;
-        uint32_t larger = 0;
-#pragma unroll
-        for (uint32_t j = 0; j < kTopK; j += 2u) {
-            const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(other + j);
-            larger += pr.x > mine ? 1u : 0u;
-            larger += pr.y > mine ? 1u : 0u;
-        }
-        // l_0's order key: the largest of the eight wave maxima
-        const uint4 m0 = *reinterpret_cast<const uint4*>(lds.wave_max);
-        const uint4 m1 = *reinterpret_cast<const uint4*>(lds.wave_max + 4);
-        const uint32_t top = max(max(max(m0.x, m0.y), max(m0.z, m0.w)),
-                                 max(max(m1.x, m1.y), max(m1.z, m1.w)));
-        const uint32_t rank = group8_sum(larger);
-        if (list == 7u && rank < kTopK) {
-            ids[rank] = static_cast<int32_t>(kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu));
-            num[rank] = exp_q(key_value(static_cast<uint32_t>(mine >> 32)) - key_value(top));
-        }
-    }
+    rank_candidates<8>(lds, ids, num);
     __syncthreads();
 }
 

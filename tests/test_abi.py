@@ -271,6 +271,16 @@ def test_dense_validation(q38m):
         with pytest.raises(q38m.InvalidArgument):
             q38m.call("q38m_moe_shared_expert_v1", *args, None, 0)
     assert q38m.lib().q38m_moe_shared_expert_scratch_bytes(8, 512) == 3 * 8 * 512 * 2
+    # hidden, router, tokens, hidden_width, top_k, workspace, workspace_bytes, ids, weights
+    ws = q38m.lib().q38m_moe_router_topk_workspace_bytes(8)
+    assert ws == 8 * 8 * (10 * 8 + 4)
+    good = [0x1000, 0x2000, 8, 2048, 10, 0x3000, ws, 0x4000, 0x5000]
+    for i, bad in [(0, None), (1, None), (2, 0), (2, 65535 * 16 + 1), (3, 2560), (4, 0), (4, 11),
+                   (5, None), (6, ws - 1), (7, None), (8, None), (0, 0x1004), (5, 0x3008)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_router_topk_v1", *args, None, 0)
 
 
 def test_hyper_validation(q38m):

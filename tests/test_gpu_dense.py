@@ -95,6 +95,49 @@ def test_router_logits_and_routes(q38m, orc):
     assert decided >= tokens * 0.9
 
 
+@pytest.mark.parametrize("tokens,top_k", [(1, 10), (37, 10), (512, 10), (96, 7)])
+def test_router_topk_fused(q38m, orc, tokens, top_k):
+    """q38m_moe_router_topk_v1 (logits kept on the CU, level-1 selection in
+    the GEMM epilogue) equals q38m_moe_router_v1 -> q38m_topk_router_f32 and
+    the oracle's top-k of those logits, bit for bit.  Experts 5 and 300 share
+    a router row (exact ties, lower id first) and token 0 is all zeros (every
+    logit 0: experts 0..9)."""
+    t = torch()
+    rng = np.random.default_rng(tokens * 31 + top_k)
+    hidden = bf16_matrix(orc, rng, tokens, W.HIDDEN, 1.0)
+    hidden[0] = 0
+    router = bf16_matrix(orc, rng, W.EXPERTS, W.HIDDEN, 0.02)
+    router[300] = router[5]
+    hd, rd = device(hidden), device(router)
+    logits = t.empty(tokens * W.EXPERTS, dtype=t.float32, device="cuda")
+    q38m.call("q38m_moe_router_v1", hd.data_ptr(), rd.data_ptr(), tokens, W.HIDDEN,
+              logits.data_ptr(), stream(), 0)
+    ref_ids = t.empty(tokens * top_k, dtype=t.int32, device="cuda")
+    ref_w = t.empty(tokens * top_k, dtype=t.float32, device="cuda")
+    q38m.call("q38m_topk_router_f32", logits.data_ptr(), ref_ids.data_ptr(), ref_w.data_ptr(),
+              tokens, W.EXPERTS, top_k, 1, stream(), 0)
+    ws_bytes = q38m.lib().q38m_moe_router_topk_workspace_bytes(tokens)
+    ws = t.empty(ws_bytes, dtype=t.uint8, device="cuda")
+    ids = t.full((tokens * top_k,), -7, dtype=t.int32, device="cuda")
+    w = t.full((tokens * top_k,), -1.0, dtype=t.float32, device="cuda")
+    q38m.call("q38m_moe_router_topk_v1", hd.data_ptr(), rd.data_ptr(), tokens, W.HIDDEN, top_k,
+              ws.data_ptr(), ws_bytes, ids.data_ptr(), w.data_ptr(), stream(), 0)
+    t.cuda.synchronize()
+    got_ids = host(ids, np.int32).reshape(tokens, top_k)
+    got_w = host(w, np.float32).reshape(tokens, top_k)
+    assert np.array_equal(got_ids, host(ref_ids, np.int32).reshape(tokens, top_k))
+    assert np.array_equal(got_w.view(np.uint32),
+                          host(ref_w, np.float32).reshape(tokens, top_k).view(np.uint32))
+    orc_ids, orc_w = orc.topk(host(logits, np.float32).reshape(tokens, W.EXPERTS), top_k)
+    assert np.array_equal(got_ids, orc_ids)
+    assert np.array_equal(got_w.view(np.uint32), orc_w.view(np.uint32))
+    assert list(got_ids[0]) == list(range(top_k))
+    # the tie: wherever both tied experts are selected, 5 ranks directly above 300
+    for row in got_ids:
+        if 5 in row and 300 in row:
+            assert list(row).index(300) == list(row).index(5) + 1
+
+
 def test_shared_expert(q38m, orc):
     t = torch()
     rng = np.random.default_rng(9)
