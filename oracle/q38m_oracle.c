@@ -477,9 +477,11 @@ void q38o_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
         float s = amax / 127.0f;
         if (s == 0.0f) s = 1.0f;
         for (uint32_t k = 0; k < width; ++k) {
-            float v = rintf(q38o_bf16_to_f32(row[k]) / s);
-            if (v > 127.0f) v = 127.0f;
-            if (v < -127.0f) v = -127.0f;
+            /* fmaxf / fminf return the other operand for a NaN quotient
+             * (an infinite element of a row whose absmax is infinite:
+             * inf / inf), so it quantises to -127, defined, as the device
+             * clamp does; a plain cast of NaN would be undefined */
+            const float v = fminf(fmaxf(rintf(q38o_bf16_to_f32(row[k]) / s), -127.0f), 127.0f);
             q[(size_t)r * width + k] = (int8_t)v;
         }
         scales[r] = s;
@@ -513,9 +515,9 @@ int q38o_quantize_weights(const uint16_t* src_bf16, uint64_t rows, uint32_t cols
             if (s == 0.0f) s = 1.0f;
             scales[(size_t)r * groups + gi] = scale_bf16 ? q38o_f32_to_bf16(s) : q38o_f32_to_f16(s);
             for (uint32_t k = 0; k < g; ++k) {
-                float v = rintf(q38o_bf16_to_f32(w[k]) / s);
-                if (v > qmax) v = qmax;
-                if (v < -qmax) v = -qmax;
+                /* NaN quotients clamp to -qmax (fmaxf returns the other
+                 * operand), as the device quantiser does */
+                const float v = fminf(fmaxf(rintf(q38o_bf16_to_f32(w[k]) / s), -qmax), qmax);
                 const int q = (int)v;
                 const size_t col = (size_t)gi * g + k;
                 if (bits == 8) {

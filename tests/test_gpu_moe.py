@@ -12,7 +12,8 @@ the reference's one-hot KAT (cuda_kernel_tests.cu:613-868) restated;
 double runs over poisoned workspaces; the gated shared-expert combine;
 decode == prefill(tokens=1) == oracle; the fused logits-in decode (ids,
 ties, signed zeros, fewer routes, shared term, residual); a reduced
-config-3 decode stack (routed and fused), a
+config-3 decode stack (routed and fused) and the full 48-layer config-3
+stack on the fused path, a
 config-4 Zipf 4096-token chunk as 8 slabs (oracle on a token sample) and a
 reduced config-5 alternating-policy stack with residual adds.
 """
@@ -358,6 +359,86 @@ def test_config3_decode_stack_reduced(q38m, orc, layers):
                                      orc.bf16_to_f32(ref["output"].ravel()))
         assert np.array_equal(host(state, np.uint16).ravel(), host_state.ravel())
         assert np.array_equal(host(fused_state, np.uint16).ravel(), host_state.ravel())
+
+
+def canonical_nan(words):
+    """bf16 words with every NaN as 0x7fc0: a NaN's sign and payload depend
+    on the instruction set that produced it (x86 and the GPU differ), not on
+    the arithmetic, and nothing downstream reads them."""
+    w = np.array(words, dtype=np.uint16, copy=True)
+    w[((w & 0x7f80) == 0x7f80) & ((w & 0x007f) != 0)] = 0x7fc0
+    return w
+
+
+def test_config3_decode_stack_full_depth(q38m, orc):
+    """Config 3 at full depth on the fused decode path the bench times:
+    every one of the 48 layers (its own weights and fresh router draw)
+    against the oracle bit for bit, on a fresh N(0,1) token; and the
+    chained stack (residual add between layers) layer by layer.  The
+    synthetic stack has no norm between layers and the MoE output grows
+    about quadratically with its input, so the chained state overflows
+    after a few layers; from there its words are compared with NaNs
+    canonicalised (the oracle's and the device's agree on every finite and
+    infinite word).  The oracle evaluates each layer on the ten routed
+    experts only: their row-major weights are gathered on the device and
+    given to it as a ten-expert layer, routes renumbered 0..9 in rank
+    order."""
+    t = torch()
+    seed = W.CONFIGS[3]["seed"]
+    scratch = decode_scratch(q38m)
+    state = synth_hidden(q38m, seed, 1, 1)
+    host_state = host(state, np.uint16).copy().reshape(1, W.HIDDEN)
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+
+    def subset(weights, ids, bits, group, rows, cols):
+        per_data = weights.data.numel() // W.EXPERTS
+        per_scale = weights.scales.numel() // W.EXPERTS
+        index = t.as_tensor(ids, device="cuda", dtype=t.long)
+        data = weights.data.view(W.EXPERTS, per_data).index_select(0, index)
+        scales = weights.scales.view(W.EXPERTS, per_scale).index_select(0, index)
+        return orc.HostWeights(host(data, np.uint8), host(scales, np.uint16), bits, group,
+                               len(ids), rows, cols)
+
+    class Repacked:
+        pass
+
+    finite_layers = 0
+    for layer_index in range(48):
+        gfmt, dfmt = W.layer_policy(3, layer_index)
+        gu_tag, dn_tag, _, l_tag = W.layer_tags(layer_index)
+        gu_rm = q38m.synth_weights(seed, gu_tag, fmt[gfmt[1]], gfmt[2], W.EXPERTS, 2 * W.INTER,
+                                   W.HIDDEN, gfmt[3])
+        dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dfmt[1]], dfmt[2], W.EXPERTS, W.HIDDEN,
+                                   W.INTER, dfmt[3])
+        layer = Repacked()
+        layer.gu, layer.dn = q38m.repack(gu_rm, paired=True), q38m.repack(dn_rm)
+        logits = synth_logits(q38m, seed, l_tag, 1)
+        ids, w = orc.topk(host(logits, np.float32))
+        gu_sub = subset(gu_rm, ids[0], gfmt[1], gfmt[2], 2 * W.INTER, W.HIDDEN)
+        dn_sub = subset(dn_rm, ids[0], dfmt[1], dfmt[2], W.HIDDEN, W.INTER)
+        routes = np.arange(10, dtype=np.int32)[None]
+
+        # the layer on a fresh finite token
+        fresh = synth_hidden(q38m, seed, 1000 + layer_index, 1)
+        got = decode_fused(q38m, layer, fresh, logits, scratch)
+        ref = orc.moe(host(fresh, np.uint16).reshape(1, W.HIDDEN), gu_sub, dn_sub, ids=routes,
+                      weights=w, grouped=False)
+        assert np.array_equal(host(got, np.uint16).reshape(1, W.HIDDEN), ref["output"]), (
+            f"layer {layer_index}, fresh token")
+
+        # the chained stack
+        state = decode_fused(q38m, layer, state, logits, scratch, output=t.empty_like(state),
+                             residual=state)
+        ref = orc.moe(host_state, gu_sub, dn_sub, ids=routes, weights=w, grouped=False)
+        host_state = orc.f32_to_bf16(orc.bf16_to_f32(host_state) +
+                                     orc.bf16_to_f32(ref["output"])).reshape(1, W.HIDDEN)
+        got_state = host(state, np.uint16).reshape(1, W.HIDDEN)
+        assert np.array_equal(canonical_nan(got_state), canonical_nan(host_state)), (
+            f"layer {layer_index}, chained state")
+        finite_layers += int(np.isfinite(orc.bf16_to_f32(host_state)).all())
+        host_state = got_state.copy()  # carry the device's words (NaN payloads included)
+        del gu_rm, dn_rm, layer
+    assert finite_layers >= 4
 
 
 def test_decode_graph_replays(q38m, orc, layers):

@@ -114,6 +114,10 @@ def test_quantize_rows_bitwise(q38m, orc, width):
     x = (rng.standard_normal((rows, width)) * rng.uniform(1e-3, 100, (rows, 1))).astype(np.float32)
     x[5] = 0.0
     x[9, 3] = 3e38
+    # non-finite rows (an overflowed decode state): inf elements, a NaN
+    x[11, 4], x[11, 8] = np.inf, -np.inf
+    x[12, 6] = np.nan
+    x[13] = np.inf
     h = orc.f32_to_bf16(x)
     t = torch()
     q = t.empty(rows * width, dtype=t.int8, device="cuda")

@@ -53,6 +53,30 @@ def test_quantize_rows_numpy_and_invariants(orc):
     assert (np.abs(q[np.arange(64), arg]) == 127)[np.arange(64) != 3].all()
 
 
+def test_quantize_rows_non_finite(orc):
+    """Rows the synthetic 48-layer decode stack reaches once its state
+    overflows: an infinite element makes the scale infinite, finite values
+    then quantise to 0 and the infinite ones (inf / inf = NaN) to -127; a
+    NaN element is ignored by the absmax and quantises to -127.  numpy's
+    fmax / fmin, like C's fmaxf / fminf and the device's v_max / v_min,
+    return the other operand for a NaN."""
+    x = np.zeros((3, 64), dtype=np.float32)
+    x[0, :] = np.linspace(-3, 3, 64)
+    x[0, 5], x[0, 9] = np.inf, -np.inf
+    x[1, :] = np.linspace(-3, 3, 64)
+    x[1, 7] = np.nan
+    x[2, 0] = np.inf
+    h = orc.f32_to_bf16(x)
+    q, s = orc.quantize_rows(h, 64)
+    xf = orc.bf16_to_f32(h)
+    assert np.isinf(s[0]) and np.isinf(s[2]) and np.isfinite(s[1])
+    with np.errstate(invalid="ignore"):
+        want = np.fmin(np.fmax(np.rint(xf / s[:, None]), -127), 127).astype(np.int8)
+    assert np.array_equal(q, want)
+    assert q[0, 5] == -127 and q[0, 9] == -127 and q[1, 7] == -127 and q[2, 0] == -127
+    assert not q[0, [0, 1, 63]].any() and not q[2, 1:].any()
+
+
 def decode_scales(w, expert):
     """float64 [rows][groups] from the scale words, without the oracle."""
     g = w.cols // w.group if w.group else 1
