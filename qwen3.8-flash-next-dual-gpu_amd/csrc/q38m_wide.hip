@@ -32,6 +32,17 @@ constexpr uint32_t kWideRows = Q38M_WIDE_TASK_ROWS;
 constexpr uint32_t kRowTiles = kWideRows / 16u;
 constexpr uint32_t kCountSlots = kExperts + 1u;  // slot 512 counts invalid ids
 
+// The contract's SwiGLU gate, silu(g) = g / (1 + exp(-g)), for every bf16 g:
+// entry h holds the fp32 word of silu(bits h << 16).  The gate enters SwiGLU
+// rounded to bf16 (q38_moe_prefill.cu:449-461), so silu depends on g's 16
+// bits only; the table is written at build time by q38m_silu_gen.c (the
+// contract's exp and one IEEE division, equal to swiglu_fold's evaluation
+// for every g), and one gather replaces ~40 VALU instructions per element
+// in the compute-bound gate/up epilogue.  256 KiB, read through L2.
+__device__ const uint32_t kSiluTable[65536] = {
+#include "q38m_silu_table.inc"
+};
+
 // ---- plan -------------------------------------------------------------------
 
 __global__ __launch_bounds__(256) void wide_count_kernel(const int32_t* __restrict__ ids,
@@ -639,22 +650,28 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
     const uint32_t a_at = ((sch >> 1) * kRowTiles + (sr >> 4)) * 64u + (sch & 1u) * 32u + (sr & 15u);
     const size_t slot0 = static_cast<size_t>(e) * (H / 128u) * kTilesAll + at.slice * kWgTiles;
     const uint2* w_src = reinterpret_cast<const uint2*>(w + slot0 * 64u + tid);
-    const uint32_t* s_src = reinterpret_cast<const uint32_t*>(s) + slot0 * 32u + 2u * tid;
-    const bool s_thread = tid < kWgTiles * 16u;
+    // threads past the scale piece re-read thread tid % 256's word and
+    // store the same value to the same LDS word
+    const uint32_t s_at = tid % (kWgTiles * 16u);
+    const uint32_t* s_src =
+        reinterpret_cast<const uint32_t*>(s) + slot0 * 32u + 2u * s_at;
     struct Stage {
         uint4 a;
         uint2 w0, w1;
         uint32_t s;
     };
     // step h: quad h/2, words 2(h%2), 2(h%2)+1 of each weight piece and
-    // scale record
+    // scale record.  Every thread issues the same loads unconditionally (a
+    // row past the task reads token 0's row, whose products land in rows
+    // that are never stored), so the wait before each LDS store covers
+    // exactly that step's loads and nothing waits on a prefetch early.
     auto load_stage = [&](uint32_t h) __attribute__((always_inline)) {
         Stage st;
-        st.a = alive ? a_src[h * 4u] : make_uint4(0u, 0u, 0u, 0u);
+        st.a = a_src[h * 4u];
         const uint2* wq = w_src + (static_cast<size_t>(h >> 1) * kTilesAll * 64u) * 2u + (h & 1u);
         st.w0 = wq[0];
         st.w1 = wq[8u * 64u * 2u];
-        st.s = s_thread ? s_src[static_cast<size_t>(h >> 1) * kTilesAll * 32u + (h & 1u)] : 0u;
+        st.s = s_src[static_cast<size_t>(h >> 1) * kTilesAll * 32u + (h & 1u)];
         return st;
     };
     auto store_stage = [&](const Stage& st, uint32_t buffer) __attribute__((always_inline)) {
@@ -665,7 +682,7 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
         w_lds[buffer][w_at + 64u] = st.w0.y;
         w_lds[buffer][w_at + 8u * 128u] = st.w1.x;
         w_lds[buffer][w_at + 8u * 128u + 64u] = st.w1.y;
-        if (s_thread) s_lds[buffer][tid] = st.s;
+        s_lds[buffer][s_at] = st.s;
     };
 
     float y[kRowTiles][2][4];
@@ -749,10 +766,13 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
             multiply(ntiles, 0u);
             store_stage(next, 1u);
             lds_barrier();
-            if (h + 2u < kHalves) next = load_stage(h + 2u);
+            // the last pair's second load repeats step h + 1 into buffer 0,
+            // which nothing reads after it (unconditional, so the loads stay
+            // ahead of the multiply instead of sinking into a branch)
+            next = load_stage(h + 2u < kHalves ? h + 2u : h + 1u);
             __builtin_amdgcn_sched_barrier(0);
             multiply(ntiles, 1u);
-            if (h + 2u < kHalves) store_stage(next, 0u);
+            store_stage(next, 0u);
             lds_barrier();
         }
     };
@@ -765,22 +785,37 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
     else
         k_loop(std::integral_constant<uint32_t, 1>{});
 
-    // SwiGLU: D lane (qh, n) holds rows 4qh + i of each tile, channel n
+    // SwiGLU (swiglu_fold's rounding sequence with silu(g) from the table):
+    // D lane (qh, n) holds rows 4qh + i of each tile, channel n.  Four
+    // tiles' gathers are in flight before their first store.
     const uint32_t channel = (at.slice * 8u + pr) * 16u + n;
     const float unscale = kBf16 ? 1.0f : 0.0625f;
+    constexpr uint32_t kBatch = 4u;
 #pragma unroll
-    for (uint32_t t = 0; t < kRowTiles; ++t) {
-        if (16u * t >= rows) break;
+    for (uint32_t t0 = 0; t0 < kRowTiles; t0 += kBatch) {
+        if (16u * t0 >= rows) break;
+        uint32_t silu_word[kBatch][4];
+        float up_value[kBatch][4];
 #pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) {
-            const uint32_t r = 16u * t + 4u * qh + i;
-            if (r >= rows) continue;
-            const float2 info = row_info[r];
-            const float yg = (y[t][0][i] * unscale) * info.x;
-            const float yu = (y[t][1][i] * unscale) * info.x;
-            mid[static_cast<size_t>(p0 + r) * I + channel] =
-                static_cast<uint16_t>(swiglu_fold(yg, yu, info.y));
-        }
+        for (uint32_t b = 0; b < kBatch; ++b)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) {
+                const uint32_t r = 16u * (t0 + b) + 4u * qh + i;
+                const float st = row_info[r < rows ? r : 0u].x;
+                const float yg = (y[t0 + b][0][i] * unscale) * st;
+                up_value[b][i] = bf16_round((y[t0 + b][1][i] * unscale) * st);
+                silu_word[b][i] = kSiluTable[f32_to_bf16(yg)];
+            }
+#pragma unroll
+        for (uint32_t b = 0; b < kBatch; ++b)
+#pragma unroll
+            for (uint32_t i = 0; i < 4u; ++i) {
+                const uint32_t r = 16u * (t0 + b) + 4u * qh + i;
+                if (r >= rows) continue;
+                const float h = bf16_round(__uint_as_float(silu_word[b][i]) * up_value[b][i]);
+                mid[static_cast<size_t>(p0 + r) * I + channel] =
+                    static_cast<uint16_t>(f32_to_bf16(h * row_info[r].y));
+            }
     }
 }
 
