@@ -8,7 +8,9 @@ to 32,768 tokens with 128-row tasks).
 - the whole step bit-exact against the slab path on the same inputs (every
   token of a 4096-token Zipf chunk) and against the oracle token by token
   on samples; at T = 512 every intermediate equals the slab path's;
-- all-W4 layers (W4 down), the gated shared term and ragged sizes.
+- all-W4 layers (W4 down), the gated shared term and ragged sizes;
+- the most skewed routing (every token to the same ten experts), plan and
+  step.
 """
 import ctypes
 
@@ -89,12 +91,20 @@ def zipf_ids(seed, tokens, s=1.1):
     return out
 
 
+HOT_EXPERTS = np.array([3, 77, 150, 151, 260, 311, 400, 401, 402, 511], np.int32)
+
+
 @pytest.mark.parametrize("tokens,kind", [(1, "uniform"), (3, "uniform"), (512, "uniform"),
-                                         (2053, "zipf"), (4096, "zipf"), (32768, "uniform")])
+                                         (2053, "zipf"), (4096, "zipf"), (32768, "uniform"),
+                                         (32768, "hot")])
 def test_wide_plan_matches_stable_sort(q38m, orc, tokens, kind):
     rng = np.random.default_rng(tokens)
     if kind == "zipf":
         ids = zipf_ids(tokens, tokens)
+    elif kind == "hot":
+        # every token routes to the same ten experts (in its own order):
+        # ten 32,768-route segments of 256 full tasks each
+        ids = np.stack([rng.permutation(HOT_EXPERTS) for _ in range(tokens)]).astype(np.int32)
     else:
         ids = np.stack([rng.choice(512, 10, replace=False) for _ in range(tokens)]).astype(np.int32)
     got = wide_plan(q38m, ids, tokens)
@@ -234,6 +244,37 @@ def test_wide_all_w4_layer_and_shared(q38m, orc, wide_layers, tokens):
                   shared_output=host(so, np.uint16)[sample],
                   shared_gate=host(sg, np.uint16)[sample], grouped=False)
     assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
+
+
+def test_wide_hot_experts_chunk(q38m, orc, wide_layers):
+    """The most skewed routing: a +40 logit bias on ten experts sends every
+    token of a 2,048-token chunk to the same ten (each expert 2,048 rows,
+    16 full 128-row tasks).  Every token equals the slab path's result and
+    a sample equals the oracle."""
+    t = torch()
+    layer = wide_layers(4)
+    seed = W.CONFIGS[4]["seed"]
+    tokens = 2048
+    bias = np.zeros(512, np.float32)
+    bias[HOT_EXPERTS] = 40.0
+    hidden = synth_hidden(q38m, seed, 51, tokens)
+    logits = synth_logits(q38m, seed, 52, tokens, bias)
+    wsw = q38m.WideWorkspace_(tokens)
+    outw = prefill_wide(q38m, layer, hidden, logits, wsw)
+    counts = wide_plan_counts(wsw)
+    assert np.array_equal(np.flatnonzero(counts), np.sort(HOT_EXPERTS))
+    assert (counts[HOT_EXPERTS] == tokens).all()
+    ws1 = q38m.PrefillWorkspace_(512)
+    out1 = t.empty(tokens, W.HIDDEN, dtype=t.int16, device="cuda")
+    for s in range(tokens // 512):
+        sl = slice(s * 512, (s + 1) * 512)
+        prefill(q38m, layer, hidden[sl], logits[sl], ws1, output=out1[sl])
+    got = host(outw, np.uint16)
+    assert np.array_equal(got, host(out1, np.uint16))
+    sample = np.arange(0, tokens, 97)
+    ref = orc.moe(host(hidden[sample.tolist()], np.uint16), layer.host_gu, layer.host_dn,
+                  logits=host(logits[sample.tolist()], np.float32), grouped=False)
+    assert np.array_equal(got[sample], ref["output"])
 
 
 def test_wide_config5_layer_full_chunk(q38m, orc, wide_layers):
