@@ -202,3 +202,12 @@ def ws_arrays(ws, tokens):
         "route_output": grab(w.route_output, r * W.HIDDEN, 4, np.float32).reshape(r, W.HIDDEN),
         "plan": grab(w.plan.header, load_product().route_plan_bytes(ws.max_tokens), 1, np.uint8),
     }
+
+
+def canonical_nan(words):
+    """bf16 words with every NaN as 0x7fc0: a NaN's sign and payload depend
+    on the instruction set that produced it (x86 and the GPU differ), not on
+    the arithmetic, and nothing downstream reads them."""
+    w = np.array(words, dtype=np.uint16, copy=True)
+    w[((w & 0x7f80) == 0x7f80) & ((w & 0x007f) != 0)] = 0x7fc0
+    return w

@@ -24,9 +24,9 @@ import numpy as np
 import pytest
 
 from conftest import GOLDEN_DIR
-from helpers import (Layer, W, decode, decode_fused, decode_scratch, device, host, prefill,
-                     scratch_ids, staged_step, stream, synth_hidden, synth_logits, torch,
-                     ws_arrays)
+from helpers import (Layer, W, canonical_nan, decode, decode_fused, decode_scratch, device,
+                     host, prefill, scratch_ids, staged_step, stream, synth_hidden,
+                     synth_logits, torch, ws_arrays)
 
 pytestmark = pytest.mark.gpu
 
@@ -359,15 +359,6 @@ def test_config3_decode_stack_reduced(q38m, orc, layers):
                                      orc.bf16_to_f32(ref["output"].ravel()))
         assert np.array_equal(host(state, np.uint16).ravel(), host_state.ravel())
         assert np.array_equal(host(fused_state, np.uint16).ravel(), host_state.ravel())
-
-
-def canonical_nan(words):
-    """bf16 words with every NaN as 0x7fc0: a NaN's sign and payload depend
-    on the instruction set that produced it (x86 and the GPU differ), not on
-    the arithmetic, and nothing downstream reads them."""
-    w = np.array(words, dtype=np.uint16, copy=True)
-    w[((w & 0x7f80) == 0x7f80) & ((w & 0x007f) != 0)] = 0x7fc0
-    return w
 
 
 def test_config3_decode_stack_full_depth(q38m, orc):

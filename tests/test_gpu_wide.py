@@ -17,7 +17,8 @@ import ctypes
 import numpy as np
 import pytest
 
-from helpers import (Layer, W, host, prefill, stream, synth_hidden, synth_logits, torch,
+from helpers import (Layer, W, canonical_nan, host, prefill, stream, synth_hidden, synth_logits,
+                     torch,
                      ws_arrays)
 
 pytestmark = pytest.mark.gpu
@@ -292,3 +293,74 @@ def test_wide_config5_layer_full_chunk(q38m, orc, wide_layers):
     ref = orc.moe(host(hidden[sample.tolist()], np.uint16), layer.host_gu, layer.host_dn,
                   logits=host(logits[sample.tolist()], np.float32), grouped=False)
     assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
+
+
+def test_config5_stack_full_depth_chunk(q38m, orc):
+    """Config 5 at full depth on the chunk path: all 48 layers (alternating
+    all-W4 / W4-W8 policy, each with its own weights and Zipf s=0.8 router
+    draw) over a 2,048-token chunk with the residual add between layers.
+    At every layer, a fresh N(0,1) chunk through the layer equals the oracle
+    on sampled tokens bit for bit, and so does the chained state (the
+    device's input words for those tokens, NaNs canonicalised once the
+    synthetic stack overflows).  The oracle evaluates a token on its ten
+    routed experts only, gathered on the device, routes renumbered 0..9 in
+    rank order."""
+    t = torch()
+    seed = W.CONFIGS[5]["seed"]
+    tokens = 2048
+    sample = np.array([0, 517, 1303, 2047])
+    fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
+    wsw = q38m.WideWorkspace_(tokens)
+    state = synth_hidden(q38m, seed, 1, tokens)
+
+    def subset(weights, ids, bits, group, rows, cols):
+        per_data = weights.data.numel() // W.EXPERTS
+        per_scale = weights.scales.numel() // W.EXPERTS
+        index = t.as_tensor(ids, device="cuda", dtype=t.long)
+        data = weights.data.view(W.EXPERTS, per_data).index_select(0, index)
+        scales = weights.scales.view(W.EXPERTS, per_scale).index_select(0, index)
+        return orc.HostWeights(host(data, np.uint8), host(scales, np.uint16), bits, group,
+                               len(ids), rows, cols)
+
+    class Repacked:
+        pass
+
+    routes = np.arange(10, dtype=np.int32)[None]
+    finite_layers = 0
+    for layer_index in range(48):
+        gfmt, dfmt = W.layer_policy(5, layer_index)
+        gu_tag, dn_tag, _, l_tag = W.layer_tags(layer_index)
+        gu_rm = q38m.synth_weights(seed, gu_tag, fmt[gfmt[1]], gfmt[2], W.EXPERTS, 2 * W.INTER,
+                                   W.HIDDEN, gfmt[3])
+        dn_rm = q38m.synth_weights(seed, dn_tag, fmt[dfmt[1]], dfmt[2], W.EXPERTS, W.HIDDEN,
+                                   W.INTER, dfmt[3])
+        layer = Repacked()
+        layer.gu, layer.dn = q38m.repack(gu_rm, paired=True), q38m.repack(dn_rm)
+        logits = synth_logits(q38m, seed, l_tag, tokens, W.bias_for(5, layer_index))
+        host_logits = host(logits, np.float32)[sample]
+        fresh = synth_hidden(q38m, seed, 2000 + layer_index, tokens)
+        got_fresh = host(prefill_wide(q38m, layer, fresh, logits, wsw), np.uint16)
+        host_fresh = host(fresh, np.uint16)[sample]
+        host_in = host(state, np.uint16)[sample]
+        out = prefill_wide(q38m, layer, state, logits, wsw)
+        got_out = host(out, np.uint16)
+        for k, token in enumerate(sample):
+            ids, w = orc.topk(host_logits[k:k + 1])
+            gu_sub = subset(gu_rm, ids[0], gfmt[1], gfmt[2], 2 * W.INTER, W.HIDDEN)
+            dn_sub = subset(dn_rm, ids[0], dfmt[1], dfmt[2], W.HIDDEN, W.INTER)
+            ref = orc.moe(host_fresh[k:k + 1], gu_sub, dn_sub, ids=routes, weights=w,
+                          grouped=False)
+            assert np.array_equal(got_fresh[token:token + 1], ref["output"]), (
+                f"layer {layer_index}, fresh token {token}")
+            ref = orc.moe(host_in[k:k + 1], gu_sub, dn_sub, ids=routes, weights=w,
+                          grouped=False)
+            assert np.array_equal(canonical_nan(got_out[token:token + 1]),
+                                  canonical_nan(ref["output"])), (
+                f"layer {layer_index}, chained token {token}")
+        finite_layers += int(np.isfinite(orc.bf16_to_f32(got_out[sample])).all())
+        new_state = t.empty_like(state)
+        q38m.call("q38m_residual_add_bf16", state.data_ptr(), out.data_ptr(),
+                  new_state.data_ptr(), tokens * W.HIDDEN, stream(), 0)
+        state = new_state
+        del gu_rm, dn_rm, layer
+    assert finite_layers >= 3
