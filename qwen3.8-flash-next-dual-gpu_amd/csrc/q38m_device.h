@@ -33,6 +33,22 @@ __device__ __forceinline__ uint2 load_stream(const uint2* p) {
     return make_uint2(v.x, v.y);
 }
 
+// ---- plan tasks ------------------------------------------------------------
+// A task record (q38m_task_v1: packed_begin, expert, valid_rows, flags) read
+// as one 8-byte load of its two words: with a uniform index that is a single
+// scalar load, where the struct's 16- and 8-bit fields would otherwise come
+// from separate vector loads, a round trip each, before the first weight
+// address of the task exists.
+struct TaskRecord {
+    uint32_t begin, expert, rows;
+};
+
+__device__ __forceinline__ TaskRecord read_task(const q38m_task_v1* __restrict__ tasks,
+                                                uint32_t index) {
+    const uint2 w = reinterpret_cast<const uint2*>(tasks)[index];
+    return TaskRecord{w.x, w.y & 0xffffu, (w.y >> 16) & 0xffu};
+}
+
 // ---- conversions ---------------------------------------------------------
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) {

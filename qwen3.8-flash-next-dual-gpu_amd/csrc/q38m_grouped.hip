@@ -93,8 +93,8 @@ void gate_up_w4_kernel(
     constexpr uint32_t kThreads = kWaves * 64u;
     __shared__ uint2 a_lds[kGroups * 64u];
 
-    const q38m_task_v1 task = tasks[blockIdx.y];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, blockIdx.y);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -102,7 +102,7 @@ void gate_up_w4_kernel(
     const uint32_t q = lane >> 4;
     const uint32_t gate_tile = blockIdx.x * kWaves + wave;  // = the gate/up pair index
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
 
     // Paired quad-major layout: for quad kq the gate tile of pair p is slot
     // 2p and its up tile slot 2p+1, so a workgroup's step reads one
@@ -225,8 +225,8 @@ void gate_up_w8_kernel(
     constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
     __shared__ uint4 a_lds[kBlocks * 64u];
 
-    const q38m_task_v1 task = tasks[blockIdx.y];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, blockIdx.y);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -234,7 +234,7 @@ void gate_up_w8_kernel(
     const uint32_t q = lane >> 4;
     const uint32_t pair = blockIdx.x * kWaves + wave;
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
 
     constexpr uint32_t kBlockWords = kTiles * 64u;  // uint4 per K block of one expert
     const uint4* wbase = w + (static_cast<size_t>(e) * kBlocks * kTiles + 2u * pair) * 64u;
@@ -366,15 +366,15 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     static_assert(kPerChannel || kHalf % kBlocksPerGroup == 0u, "groups within half tiles");
     __shared__ uint4 a_lds[kBlocks * 64u];
 
-    const q38m_task_v1 task = tasks[blockIdx.y];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, blockIdx.y);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
     const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
     const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
 
@@ -471,15 +471,15 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
     constexpr uint32_t kQuads = I / 128u;
     constexpr uint32_t kTiles = H / 16u;
     constexpr uint32_t kRowScales = 4u / kSub;
-    const q38m_task_v1 task = tasks[blockIdx.y];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, blockIdx.y);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
     const uint32_t a_row = n < rows ? n : 0u;
     const uint2* xa = reinterpret_cast<const uint2*>(mq + static_cast<size_t>(p0 + a_row) * I) + q;
     long a[kQuads * 4u];

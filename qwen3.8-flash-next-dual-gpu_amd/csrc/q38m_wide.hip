@@ -316,8 +316,8 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
 
     Placement at;
     if (!place_on_xcds(live_tasks, at)) return;
-    const q38m_task_v1 task = tasks[at.task];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, at.task);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
@@ -326,7 +326,7 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
     const uint32_t pr = wave & 7u;
     const uint32_t n = lane & 15u, qh = lane >> 4;
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
     const int here = static_cast<int>(rows) - static_cast<int>(64u * rh);
     const uint32_t nt = __builtin_amdgcn_readfirstlane(
         here <= 0 ? 0u : (here >= 64 ? 4u : (static_cast<uint32_t>(here) + 15u) / 16u));
@@ -625,15 +625,15 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
 
     Placement at;
     if (!place_on_xcds(live_tasks, at)) return;
-    const q38m_task_v1 task = tasks[at.task];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, at.task);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t pr = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 15u, qh = lane >> 4;
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
     const uint32_t tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
 
     // staging: row piece (row tid/4, 16-byte chunk tid%4 of the step's 64
@@ -1008,14 +1008,14 @@ void gate_up_w8_wide_kernel(
 
     Placement at;
     if (!place_on_xcds(live_tasks, at)) return;
-    const q38m_task_v1 task = tasks[at.task];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, at.task);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool up = wave >= kPairs;
     const uint32_t pair = at.slice * kPairs + (wave % kPairs);
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
     const uint32_t n = threadIdx.x & 15u;
     // paired K-block-major layout: for block kb the gate tile of pair p is
     // slot 2p and its up tile slot 2p+1
@@ -1163,13 +1163,13 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_wide_kernel(
 
     Placement at;
     if (!place_on_xcds(live_tasks, at)) return;
-    const q38m_task_v1 task = tasks[at.task];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, at.task);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
     const uint32_t tile0 = (at.slice * kWaves + wave) * kTilesPerWave;
     const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
     const uint32_t tiles = (rows + 15u) / 16u;  // uniform per workgroup
@@ -1333,14 +1333,14 @@ void down_w4_wide_kernel(
 
     Placement at;
     if (!place_on_xcds(live_tasks, at)) return;
-    const q38m_task_v1 task = tasks[at.task];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, at.task);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
 
     // Piece i: row r, 16-byte piece c = group c/2, lane groups 2(c%2),
     // 2(c%2)+1; all loads before the first store.
@@ -1410,15 +1410,15 @@ void down_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __restri
 
     Placement at;
     if (!place_on_xcds(live_tasks, at)) return;
-    const q38m_task_v1 task = tasks[at.task];
-    const uint32_t rows = task.valid_rows;
+    const TaskRecord task = read_task(tasks, at.task);
+    const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t n = lane & 15u, qh = lane >> 4;
     const uint32_t e = task.expert;
-    const uint32_t p0 = task.packed_begin;
+    const uint32_t p0 = task.begin;
     const uint32_t tiles = __builtin_amdgcn_readfirstlane((rows + 15u) / 16u);
 
     // staging: row piece (row tid/4, 16-byte chunk tid%4 of the step's 64
