@@ -273,21 +273,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     const uint32_t n0 = 8u * (slot8 & 1u);
     const bool active = route < top_k;
 
-    // the epilogue's operands, requested first: they depend on nothing
+    // the epilogue's operands, requested first: they depend on nothing.
+    // Every thread loads them in straight-line code (an absent operand reads
+    // the mid row's first word instead and is never used), so no branch
+    // holds a wait for them ahead of the weight requests.
     const uint32_t channel = 16u * tile + n0 + (threadIdx.x & 7u);
     const bool finisher = threadIdx.x < 8u;
-    uint32_t residual_bits = 0u, shared_bits = 0u, gate_bits = 0u;
-    if (finisher) {
-        if (residual != nullptr) residual_bits = residual[channel];
-        if (shared_output != nullptr && shared_gate != nullptr) {
-            shared_bits = shared_output[channel];
-            gate_bits = shared_gate[0];
-        }
-    }
+    const bool has_residual = residual != nullptr;
+    const bool has_shared = shared_output != nullptr && shared_gate != nullptr;
+    const uint32_t residual_bits = (has_residual ? residual : mid)[has_residual ? channel : 0u];
+    const uint32_t shared_bits = (has_shared ? shared_output : mid)[has_shared ? channel : 0u];
+    const uint32_t gate_bits = (has_shared ? shared_gate : mid)[0];
 
     const int32_t id = active ? ids[route] : -1;
-    uint4 mv = make_uint4(0u, 0u, 0u, 0u);
-    if (active) mv = reinterpret_cast<const uint4*>(mid + static_cast<size_t>(route) * I)[lane];
+    // the scratch holds ten mid rows, so a route past top_k reads one too
+    // (straight-line, no wait at a branch join); its partial is dropped
+    const uint4 mv = reinterpret_cast<const uint4*>(mid + static_cast<size_t>(route) * I)[lane];
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
 
@@ -296,7 +297,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     constexpr uint32_t kW8Groups = kBlocks / kPerGroup;
     uint4 bq[4];
     uint2 sc = make_uint2(0u, 0u);
-    float ws = 0.0f;
+    uint32_t ws_bits = 0u;
     if constexpr (kW4) {
         // lane = c + 8*(kq + 4*qh): quad kq, chunks q = 2qh, 2qh+1
         constexpr uint32_t kQuads = I / 128u;
@@ -314,11 +315,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
         bq[1] = wp[16];
         bq[2] = wp[32];
         bq[3] = wp[48];
-        // this lane's group (per channel: the one scale), artifact order
-        ws = scale_to_f32(s[(static_cast<size_t>(e) * H + 16u * tile + n0 + c) * kW8Groups +
-                            kb / kPerGroup],
-                          bf16);
+        // this lane's group (per channel: the one scale), artifact order; a
+        // relaxed atomic load, which the compiler keeps here instead of
+        // sinking it to its use after the barrier (a full round trip there)
+        ws_bits = __hip_atomic_load(
+            s + (static_cast<size_t>(e) * H + 16u * tile + n0 + c) * kW8Groups + kb / kPerGroup,
+            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     }
+    // every request above is out before the quantisation below waits for
+    // the mid row
+    __builtin_amdgcn_sched_barrier(0);
 
     // quantise this route's mid row (8 elements per lane)
     const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
@@ -388,6 +394,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     } else {
         const uint32_t kb = lane >> 3;
         const uint4* mrow = mq_lds[route] + 4u * kb;
+        const float ws = scale_to_f32(ws_bits, bf16);
         int acc = 0;
 #pragma unroll
         for (uint32_t q = 0; q < 4u; ++q) {
@@ -433,13 +440,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
 #pragma unroll
         for (uint32_t r = 0; r < kTopK; ++r)
             if (r < top_k) total += part[r];
-        if (shared_output != nullptr && shared_gate != nullptr) {
+        if (has_shared) {
             const float g = bf16_to_f32(gate_bits);
             const float multiplier = 1.0f / (1.0f + exp_q(-g));
             total = __builtin_fmaf(bf16_to_f32(shared_bits), multiplier, total);
         }
         uint32_t result = f32_to_bf16(total);
-        if (residual != nullptr)
+        if (has_residual)
             result = f32_to_bf16(bf16_to_f32(residual_bits) + bf16_to_f32(result));
         out[channel] = static_cast<uint16_t>(result);
     }
