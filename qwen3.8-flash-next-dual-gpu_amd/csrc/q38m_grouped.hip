@@ -378,18 +378,28 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
     const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
 
-    // first half-tile in flight while A is staged
+    // Stage A: 16-byte chunk c of mid row r is K block c/4, lane group c%4.
+    // The row chunks are requested first, then the first half-tile of
+    // weights, so the LDS stores wait for the rows only.
+    constexpr uint32_t kStage = 16u * (I / 16u) / kThreads;
+    static_assert(16u * (I / 16u) % kThreads == 0u, "whole row chunks per thread");
+    uint4 av[kStage];
+#pragma unroll
+    for (uint32_t u = 0; u < kStage; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
+        const uint32_t r = i / (I / 16u);
+        av[u] = reinterpret_cast<const uint4*>(
+            mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[i % (I / 16u)];
+    }
     uint4 b[kHalf];
 #pragma unroll
     for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
-
-    // Stage A: 16-byte chunk c of mid row r is K block c/4, lane group c%4.
-    for (uint32_t i = threadIdx.x; i < 16u * (I / 16u); i += kThreads) {
-        const uint32_t r = i / (I / 16u);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t u = 0; u < kStage; ++u) {
+        const uint32_t i = threadIdx.x + u * kThreads;
         const uint32_t chunk = i % (I / 16u);
-        const uint4 v = reinterpret_cast<const uint4*>(
-            mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[chunk];
-        a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + r] = v;
+        a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + i / (I / 16u)] = av[u];
     }
     float row_scale[4];
 #pragma unroll
@@ -407,16 +417,16 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
         uint4 nb[kHalf];
 #pragma unroll
         for (uint32_t kb = 0; kb < kHalf; ++kb) nb[kb] = load_stream(wtile + (kHalf + kb) * 64u);
-        // grouped: the row's group scales up front; per channel: after the
-        // K loop (fewer live registers across it)
-        float gs[kGroups];
-        auto load_scales = [&]() {
+        // the row's scale words, requested with the tile's weights and
+        // widened where they are used: relaxed atomic loads stay here (a
+        // plain load would be sunk to its use after the K loop, and its wait
+        // would then also cover the next tile's weight requests)
+        uint32_t gbits[kGroups];
 #pragma unroll
-            for (uint32_t g = 0; g < kGroups; ++g)
-                gs[g] = scale_to_f32(
-                    s[(static_cast<size_t>(e) * H + tile * 16u + n) * kGroups + g], kBf16);
-        };
-        if constexpr (!kPerChannel) load_scales();
+        for (uint32_t g = 0; g < kGroups; ++g)
+            gbits[g] = __hip_atomic_load(
+                s + (static_cast<size_t>(e) * H + tile * 16u + n) * kGroups + g, __ATOMIC_RELAXED,
+                __HIP_MEMORY_SCOPE_WORKGROUP);
         __builtin_amdgcn_sched_barrier(0);
         v4i acc = zero;
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -427,10 +437,10 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
                                    kb % kBlocksPerGroup == 0u ? zero : acc);
             if constexpr (!kPerChannel) {
                 if (kb % kBlocksPerGroup == kBlocksPerGroup - 1u) {
+                    const float gs = scale_to_f32(gbits[kb / kBlocksPerGroup], kBf16);
 #pragma unroll
                     for (uint32_t i = 0; i < 4u; ++i)
-                        y[i] = __builtin_fmaf(static_cast<float>(acc[i]), gs[kb / kBlocksPerGroup],
-                                              y[i]);
+                        y[i] = __builtin_fmaf(static_cast<float>(acc[i]), gs, y[i]);
                 }
             }
         };
@@ -445,13 +455,13 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (uint32_t kb = 0; kb < kHalf; ++kb) block(kHalf + kb, nb[kb]);
-        if constexpr (kPerChannel) load_scales();
+        const float cs = scale_to_f32(gbits[0], kBf16);  // per channel: the one scale
         const uint32_t channel = tile * 16u + n;
 #pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) {
             const uint32_t r = 4u * q + i;
             if (r >= rows) continue;
-            const float o = kPerChannel ? (static_cast<float>(acc[i]) * gs[0]) * row_scale[i]
+            const float o = kPerChannel ? (static_cast<float>(acc[i]) * cs) * row_scale[i]
                                         : y[i] * row_scale[i];
             out[static_cast<size_t>(p0 + r) * H + channel] = o;
         }
