@@ -7,6 +7,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "q38m.h"
@@ -42,6 +43,9 @@ __device__ __forceinline__ uint2 load_stream(const uint2* p) {
 struct TaskRecord {
     uint32_t begin, expert, rows;
 };
+static_assert(sizeof(q38m_task_v1) == 8 && offsetof(q38m_task_v1, expert) == 4 &&
+                  offsetof(q38m_task_v1, valid_rows) == 6,
+              "read_task unpacks the record's second word as expert | valid_rows << 16");
 
 __device__ __forceinline__ TaskRecord read_task(const q38m_task_v1* __restrict__ tasks,
                                                 uint32_t index) {
