@@ -141,11 +141,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
     // for LDS only, so the weight loads above stay in flight
     if (wave < 4u) row_absmax_partial(hw, amax_lds);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const float xs = row_scale(amax_lds);
+    const QuantScale row_q = row_scale(amax_lds);
+    const float xs = row_q.s;
     if (wave < 4u) {
         const uint32_t k = 8u * threadIdx.x;
         reinterpret_cast<uint2*>(x_lds)[(k >> 7) * (2u * kQuadPad) + ((k & 127u) >> 3)] =
-            quantize8(hw, xs);
+            quantize8(hw, row_q);
     }
     __syncthreads();
 
@@ -334,20 +335,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
         amax = fmaxf(amax, fabsf(bf16_to_f32(mw[i] & 0xffffu)));
         amax = fmaxf(amax, fabsf(bf16_to_f32(mw[i] >> 16)));
     }
-    amax = wave_max_f32(amax);
-    float sm = amax / 127.0f;
-    if (sm == 0.0f) sm = 1.0f;
-    {
-        uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t h = (i & 1) ? (mw[i >> 1] >> 16) : (mw[i >> 1] & 0xffffu);
-            float r = __builtin_rintf(bf16_to_f32(h) / sm);
-            r = fminf(fmaxf(r, -127.0f), 127.0f);
-            packed[i >> 2] |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * (i & 3));
-        }
-        reinterpret_cast<uint2*>(mq_lds[route])[lane] = make_uint2(packed[0], packed[1]);
-    }
+    const QuantScale mid_q = quant_scale(wave_max_f32(amax));
+    const float sm = mid_q.s;
+    reinterpret_cast<uint2*>(mq_lds[route])[lane] = quantize8(mw, mid_q);
     __syncthreads();
 
     float o = 0.0f;

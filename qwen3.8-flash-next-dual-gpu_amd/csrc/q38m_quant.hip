@@ -1,6 +1,7 @@
 // Per-row int8 activation quantisation and the bf16 hidden gather.
 #include "q38m_device.h"
 #include "q38m_internal.h"
+#include "q38m_select.h"
 
 namespace q38m {
 namespace {
@@ -8,7 +9,8 @@ namespace {
 // One wave per row; lane l owns elements [8l + 512c, 8l + 512c + 8) so
 // every load is a coalesced 16-byte vector.  s = absmax/127 (IEEE
 // division), zero -> 1, q = clamp(rint(x/s), -127, 127): the convention of
-// tools/q38_artifact_compiler.py:214-222 applied per token row.
+// tools/q38_artifact_compiler.py:214-222 applied per token row (quotients
+// through quant_scale / quantize8).
 template <uint32_t kChunks>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(
     const uint16_t* __restrict__ x, uint32_t rows, int8_t* __restrict__ q,
@@ -31,27 +33,14 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
             amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] >> 16)));
         }
     }
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1)
-        amax = fmaxf(amax, __shfl_xor(amax, offset, 64));
-    float s = amax / 127.0f;
-    if (s == 0.0f) s = 1.0f;
+    const QuantScale qs = quant_scale(wave_max_f32(amax));
     uint2* dst = reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * kWidth);
 #pragma unroll
     for (uint32_t c = 0; c < kChunks; ++c) {
         const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-        uint32_t packed[2] = {0u, 0u};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t h = (i & 1) ? (w[i >> 1] >> 16) : (w[i >> 1] & 0xffffu);
-            float r = __builtin_rintf(bf16_to_f32(h) / s);
-            r = fminf(fmaxf(r, -127.0f), 127.0f);
-            const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
-            packed[i >> 2] |= b << (8 * (i & 3));
-        }
-        dst[c * 64u + lane] = make_uint2(packed[0], packed[1]);
+        dst[c * 64u + lane] = quantize8(w, qs);
     }
-    if (lane == 0) scales[row] = s;
+    if (lane == 0) scales[row] = qs.s;
 }
 
 // Gather hidden[token(packed)] -> packed order (q38_moe_prefill.cu:292-306).

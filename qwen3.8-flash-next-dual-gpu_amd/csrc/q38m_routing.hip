@@ -151,16 +151,14 @@ __global__ __launch_bounds__(256) void route_quantize_wave_kernel(
         const uint32_t w[4] = {h[c].x, h[c].y, h[c].z, h[c].w};
         amax = fmaxf(amax, row_absmax8(w));
     }
-    amax = wave_max_f32(amax);
-    float s = amax / 127.0f;
-    if (s == 0.0f) s = 1.0f;
+    const QuantScale qs = quant_scale(wave_max_f32(amax));
     uint2* dst = reinterpret_cast<uint2*>(xq + static_cast<size_t>(token) * kHidden);
 #pragma unroll
     for (uint32_t c = 0; c < kChunks; ++c) {
         const uint32_t w[4] = {h[c].x, h[c].y, h[c].z, h[c].w};
-        dst[c * 64u + lane] = quantize8(w, s);
+        dst[c * 64u + lane] = quantize8(w, qs);
     }
-    if (lane == 0) xs[token] = s;
+    if (lane == 0) xs[token] = qs.s;
 }
 
 // ---------------------------------------------------------------------------
@@ -192,9 +190,9 @@ __global__ __launch_bounds__(kSelectThreads) void route_quantize_kernel(
     if (quantize && wave < 4u) row_absmax_partial(hw, amax_lds);
     block_topk512(logit, select_lds, ids_lds, num_lds);
     if (quantize && wave < 4u) {
-        const float s = row_scale(amax_lds);
-        reinterpret_cast<uint2*>(xq + static_cast<size_t>(token) * kHidden)[t] = quantize8(hw, s);
-        if (t == 0) xs[token] = s;
+        const QuantScale qs = row_scale(amax_lds);
+        reinterpret_cast<uint2*>(xq + static_cast<size_t>(token) * kHidden)[t] = quantize8(hw, qs);
+        if (t == 0) xs[token] = qs.s;
     }
     if (wave == kTopK - 1u) {
         const uint32_t lane = t & 63u;
