@@ -583,6 +583,15 @@ __device__ __forceinline__ uint4 i8_to_f16(uint32_t lo, uint32_t hi) {
                       pk_times16_f16(sbytes02_to_f16(lo)), pk_times16_f16(sbytes13_to_f16(lo)));
 }
 
+// Staging swizzle of the fp16 A image: in fragment (group j, row tile t)
+// the slot of row r (0..15) in 16-byte chunk c (0..3) is c*16 + (r ^ f(s)),
+// s = (c >> 1) + 2j, f = {0, 6, 10, 12}.  A staging store instruction writes
+// four rows x the four chunk pairs of a 64-column step: unswizzled, its
+// eight- and sixteen-lane groups land on two and four bank groups (2- and
+// 4-way conflicts); with f every group hits distinct banks, and the MFMA
+// reads (one chunk, sixteen rows) stay conflict-free.
+__device__ __forceinline__ uint32_t a_swizzle(uint32_t s) { return (0xCA60u >> (4u * s)) & 15u; }
+
 __device__ __forceinline__ v4f mfma_f16_16x16x32(uint4 a, uint4 b, v4f c) {
     typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8_t, a),
@@ -647,7 +656,8 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
         row_info[sr] = make_float2(xs[assignment / kTopK], route_weights[assignment]);
     const uint4* a_src =
         reinterpret_cast<const uint4*>(xq + static_cast<size_t>(assignment / kTopK) * H) + sch;
-    const uint32_t a_at = ((sch >> 1) * kRowTiles + (sr >> 4)) * 64u + (sch & 1u) * 32u + (sr & 15u);
+    const uint32_t a_at = ((sch >> 1) * kRowTiles + (sr >> 4)) * 64u + (sch & 1u) * 32u +
+                          ((sr & 15u) ^ a_swizzle(sch));
     const size_t slot0 = static_cast<size_t>(e) * (H / 128u) * kTilesAll + at.slice * kWgTiles;
     const uint2* w_src = reinterpret_cast<const uint2*>(w + slot0 * 64u + tid);
     // threads past the scale piece re-read thread tid % 256's word and
@@ -701,7 +711,9 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
     auto multiply = [&](auto ntiles, uint32_t buffer) __attribute__((always_inline)) {
         constexpr uint32_t kNt = decltype(ntiles)::value;
         constexpr uint32_t kChains = 2u * kNt * 2u;
-        const uint4* abuf = a_lds[buffer] + lane;
+        // lane l reads row l%16 of chunk l/16, through the staging swizzle
+        const uint4* abuf0 = a_lds[buffer] + ((lane & 48u) | ((lane & 15u) ^ a_swizzle(lane >> 5)));
+        const uint4* abuf1 = a_lds[buffer] + ((lane & 48u) | ((lane & 15u) ^ a_swizzle((lane >> 5) + 2u)));
         const uint16_t* srow = reinterpret_cast<const uint16_t*>(s_lds[buffer]) +
                                ((2u * pr) * 16u + n) * 2u;  // up: + 32 words
         const uint32_t* wrow = w_lds[buffer] + (2u * pr) * 128u + lane;  // up: + 128
@@ -719,7 +731,7 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
                 }
                 if (m + 1u < 2u * kNt) {
                     const uint32_t jn = (m + 1u) / kNt, tn = (m + 1u) % kNt;
-                    fa[(m + 1u) & 1u] = abuf[(jn * kRowTiles + tn) * 64u];
+                    fa[(m + 1u) & 1u] = (jn == 0u ? abuf0 : abuf1)[(jn * kRowTiles + tn) * 64u];
                 }
             }
             d[k & 1u] = mfma_f16_16x16x32(fa[m & 1u], bf[u], zero);
@@ -739,7 +751,7 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
             asm volatile("" : "+v"(y[t][u][0]), "+v"(y[t][u][1]), "+v"(y[t][u][2]),
                          "+v"(y[t][u][3]));
         };
-        fa[0] = abuf[0];
+        fa[0] = abuf0[0];
 #pragma unroll
         for (uint32_t k = 0; k <= kChains; ++k) {
             if (k < kChains) issue(k);
