@@ -129,26 +129,24 @@ void gate_up_w4_kernel(
     // row indices are loaded first, then the first two quads of weights and
     // all row chunks, so A costs two round trips and the weights stay in
     // flight meanwhile.
+    // Piece i is row i % 16, chunk i / 16: consecutive lanes take
+    // consecutive rows, so a store instruction spreads over the banks (a
+    // row's chunks all fall in its bank pair; row-major pieces put 32 lanes
+    // on one), and every piece of a thread is in the same row (one index).
     constexpr uint32_t kChunks = 16u * (H / 16u) / kThreads;
-    static_assert(16u * (H / 16u) % kThreads == 0u, "whole chunks per thread");
-    uint32_t token[kChunks];
-#pragma unroll
-    for (uint32_t c = 0; c < kChunks; ++c) {
-        const uint32_t r = (threadIdx.x + c * kThreads) / (H / 16u);
-        token[c] = packed[p0 + (r < rows ? r : 0u)];
-    }
+    static_assert(16u * (H / 16u) % kThreads == 0u && kThreads % 16u == 0u,
+                  "whole chunks per thread, one row per thread");
+    const uint32_t srow = threadIdx.x % 16u;
+    const uint32_t token = packed[p0 + (srow < rows ? srow : 0u)];
     QuadWeights r0 = load(0), r1 = load(1), r2;
+    const uint4* arow = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token / kTopK) * H);
     uint4 v[kChunks];
 #pragma unroll
-    for (uint32_t c = 0; c < kChunks; ++c) {
-        const uint32_t chunk = (threadIdx.x + c * kThreads) % (H / 16u);
-        v[c] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token[c] / kTopK) * H)[chunk];
-    }
+    for (uint32_t c = 0; c < kChunks; ++c) v[c] = arow[(threadIdx.x + c * kThreads) / 16u];
 #pragma unroll
     for (uint32_t c = 0; c < kChunks; ++c) {
-        const uint32_t i = threadIdx.x + c * kThreads;
-        const uint32_t chunk = i % (H / 16u);
-        const uint32_t base = (chunk >> 1) * 64u + (chunk & 1u) * 32u + i / (H / 16u);
+        const uint32_t chunk = (threadIdx.x + c * kThreads) / 16u;
+        const uint32_t base = (chunk >> 1) * 64u + (chunk & 1u) * 32u + srow;
         a_lds[base] = make_uint2(v[c].x, v[c].y);
         a_lds[base + 16u] = make_uint2(v[c].z, v[c].w);
     }
@@ -383,13 +381,15 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     // weights, so the LDS stores wait for the rows only.
     constexpr uint32_t kStage = 16u * (I / 16u) / kThreads;
     static_assert(16u * (I / 16u) % kThreads == 0u, "whole row chunks per thread");
+    // piece i: row i % 16, chunk i / 16 (consecutive lanes, consecutive
+    // rows: the LDS stores fall in distinct banks)
     uint4 av[kStage];
 #pragma unroll
     for (uint32_t u = 0; u < kStage; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
-        const uint32_t r = i / (I / 16u);
+        const uint32_t r = i % 16u;
         av[u] = reinterpret_cast<const uint4*>(
-            mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[i % (I / 16u)];
+            mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[i / 16u];
     }
     uint4 b[kHalf];
 #pragma unroll
@@ -398,8 +398,8 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
 #pragma unroll
     for (uint32_t u = 0; u < kStage; ++u) {
         const uint32_t i = threadIdx.x + u * kThreads;
-        const uint32_t chunk = i % (I / 16u);
-        a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + i / (I / 16u)] = av[u];
+        const uint32_t chunk = i / 16u;
+        a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + i % 16u] = av[u];
     }
     float row_scale[4];
 #pragma unroll
