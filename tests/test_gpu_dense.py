@@ -48,13 +48,14 @@ def check_close(orc, got, a, b, out_bf16):
     assert np.all(np.abs(got - exact) <= bound)
 
 
-# K-split 32 x 32 tiles, and (K <= 1024 with at least 192 tiles of 64 x 64)
+# K-split 32 x 32 tiles (long K too: the hyper mix-down's 8192, and a
+# ragged odd-step K), and (K <= 1024 with at least 192 tiles of 64 x 64)
 # workgroup-shared 64 x 64 tiles: ragged edges, a trailing half K chunk, a
 # single half chunk, the largest K of that form
 @pytest.mark.parametrize("m,n,k", [(40, 512, 2048), (512, 2048, 512), (1, 512, 2048),
                                    (33, 1, 2048), (64, 96, 64), (130, 70, 96),
                                    (1000, 1000, 160), (640, 1600, 32), (1024, 768, 1024),
-                                   (512, 2048, 320)])
+                                   (512, 2048, 320), (512, 320, 8192), (70, 100, 4128)])
 @pytest.mark.parametrize("out_bf16", [False, True])
 def test_dense_gemm(q38m, orc, m, n, k, out_bf16):
     rng = np.random.default_rng(m * 7 + n * 3 + k)
