@@ -82,29 +82,41 @@ __global__ __launch_bounds__(512) void wide_scan_kernel(uint32_t* __restrict__ c
 
     // 1. running count of expert e over the chunks, in chunk order; each
     // chunk's slot becomes the expert's count in the chunks before it.  The
-    // loads of 32 chunks are issued before their sums.
+    // loads of 80 chunks (two passes for the largest plan, 160 chunks) are
+    // issued before their sums, unconditionally (a chunk past the last
+    // re-reads the last one and adds nothing), so no branch sits between a
+    // load and the wait for it.
+    constexpr uint32_t kBatch = 80;
     uint32_t count = 0;
-    for (uint32_t c0 = 0; c0 < chunks; c0 += 32u) {
-        uint32_t v[32];
+    for (uint32_t c0 = 0; c0 < chunks; c0 += kBatch) {
+        uint32_t v[kBatch];
 #pragma unroll
-        for (uint32_t j = 0; j < 32u; ++j)
-            v[j] = c0 + j < chunks ? chunk_counts[static_cast<size_t>(c0 + j) * kCountSlots + e]
-                                   : 0u;
+        for (uint32_t j = 0; j < kBatch; ++j)
+            v[j] = chunk_counts[static_cast<size_t>(min(c0 + j, chunks - 1u)) * kCountSlots + e];
 #pragma unroll
-        for (uint32_t j = 0; j < 32u; ++j) {
-            if (c0 + j < chunks)
-                chunk_counts[static_cast<size_t>(c0 + j) * kCountSlots + e] = count;
-            count += v[j];
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const bool live = c0 + j < chunks;
+            if (live) chunk_counts[static_cast<size_t>(c0 + j) * kCountSlots + e] = count;
+            count += live ? v[j] : 0u;
         }
     }
-    // invalid ids: wave 0 sums slot 512 of every chunk
+    // invalid ids: wave 0 sums slot 512 of every chunk (at most 160, three
+    // unconditional loads per lane, one round trip)
+    constexpr uint32_t kMaxChunks = (Q38M_WIDE_MAX_TOKENS * kTopK + kWideChunkRoutes - 1u) /
+                                    kWideChunkRoutes;
+    static_assert(kMaxChunks <= 192u, "three invalid-slot loads per lane");
     if (wave == 0u) {
-        uint32_t bad = 0;
-        for (uint32_t c = lane; c < chunks; c += 64u)
-            bad += chunk_counts[static_cast<size_t>(c) * kCountSlots + kExperts];
+        uint32_t bad[3];
 #pragma unroll
-        for (int offset = 32; offset > 0; offset >>= 1) bad += __shfl_xor(bad, offset, 64);
-        if (lane == 0u) invalid = bad;
+        for (uint32_t j = 0; j < 3u; ++j)
+            bad[j] = chunk_counts[static_cast<size_t>(min(lane + 64u * j, chunks - 1u)) *
+                                      kCountSlots + kExperts];
+        uint32_t sum = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < 3u; ++j) sum += lane + 64u * j < chunks ? bad[j] : 0u;
+#pragma unroll
+        for (int offset = 32; offset > 0; offset >>= 1) sum += __shfl_xor(sum, offset, 64);
+        if (lane == 0u) invalid = sum;
     }
     plan.expert_counts[e] = static_cast<uint16_t>(count);
 
@@ -200,16 +212,32 @@ __global__ __launch_bounds__(64) void wide_scatter_kernel(const int32_t* __restr
     __shared__ unsigned long long table[kCountSlots];
     const uint32_t lane = threadIdx.x;
     const uint32_t* base = bases + static_cast<size_t>(blockIdx.x) * kCountSlots;
-    for (uint32_t i = lane; i < kExperts; i += 64u) running[i] = plan.expert_offsets[i] + base[i];
+    const uint32_t begin = blockIdx.x * kWideChunkRoutes;
+    const uint32_t end = min(begin + kWideChunkRoutes, routes);
+    // every load of the chunk is issued before the first use: the segment
+    // bases and the chunk's ids (clamped to its last route, unused past it)
+    constexpr uint32_t kPerLane = kExperts / 64u, kSteps = kWideChunkRoutes / 64u;
+    static_assert(kExperts % 64u == 0u && kWideChunkRoutes % 64u == 0u, "whole waves");
+    uint32_t offset[kPerLane], chunk_base[kPerLane];
+    int32_t idv[kSteps];
+#pragma unroll
+    for (uint32_t k = 0; k < kPerLane; ++k) {
+        offset[k] = plan.expert_offsets[lane + 64u * k];
+        chunk_base[k] = base[lane + 64u * k];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kSteps; ++j) idv[j] = ids[min(begin + 64u * j + lane, end - 1u)];
+#pragma unroll
+    for (uint32_t k = 0; k < kPerLane; ++k) running[lane + 64u * k] = offset[k] + chunk_base[k];
     for (uint32_t i = lane; i < kCountSlots; i += 64u) table[i] = 0ull;
     __syncthreads();
     const uint64_t below_mask = (1ull << lane) - 1ull;
-    const uint32_t begin = blockIdx.x * kWideChunkRoutes;
-    const uint32_t end = min(begin + kWideChunkRoutes, routes);
-    for (uint32_t a0 = begin; a0 < end; a0 += 64u) {
-        const uint32_t a = a0 + lane;
+#pragma unroll
+    for (uint32_t j = 0; j < kSteps; ++j) {
+        const uint32_t a = begin + 64u * j + lane;
+        if (begin + 64u * j >= end) break;  // uniform
         const bool in = a < end;
-        const int32_t id = in ? ids[a] : -1;
+        const int32_t id = in ? idv[j] : -1;
         const bool valid = in && id >= 0 && id < static_cast<int32_t>(kExperts);
         const uint32_t slot = valid ? static_cast<uint32_t>(id) : kExperts;
         atomicOr(&table[slot], 1ull << lane);
