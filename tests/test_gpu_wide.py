@@ -128,11 +128,16 @@ def test_wide_plan_matches_stable_sort(q38m, orc, tokens, kind):
         assert np.array_equal(got["inverse"], v1["inverse"])
 
 
-def test_wide_plan_invalid_ids_fail_closed(q38m):
-    tokens = 300
+# 300 tokens: two 2048-route chunks; 32,768 tokens: 160 chunks, with
+# invalid ids in chunks past 64 and 128 (the scan sums each chunk's
+# invalid count in lane c % 64, pass c / 64)
+@pytest.mark.parametrize("tokens,bad", [(300, {4: -1, 2500: 600}),
+                                        (32768, {4: -1, 2500: 600, 131079: 512,
+                                                 307203: -5})])
+def test_wide_plan_invalid_ids_fail_closed(q38m, tokens, bad):
     ids = ((np.arange(tokens * 10) * 19 + 5) % 512).astype(np.int32)
-    ids[4] = -1
-    ids[2500] = 600
+    for at, v in bad.items():
+        ids[at] = v
     got = wide_plan(q38m, ids, tokens)
     assert got["status"] == 1
     valid = (ids >= 0) & (ids < 512)
@@ -140,7 +145,8 @@ def test_wide_plan_invalid_ids_fail_closed(q38m):
     nvalid = valid.sum()
     assert np.array_equal(got["packed"][:nvalid], order)
     assert np.array_equal(got["packed"][nvalid:], np.arange(nvalid, tokens * 10))
-    assert got["inverse"][4] == 4 and got["inverse"][2500] == 2500
+    for at in bad:
+        assert got["inverse"][at] == at
 
 
 def prefill_wide(q38m, layer, hidden, logits, ws, output=None, shared=None):
