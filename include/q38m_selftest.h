@@ -1,12 +1,14 @@
 /*
  * q38m self-check entry points -- not part of the MoE operator surface.
  *
- * libq38m.so exports these for its own test suite: each runs one
+ * libq38m_selftest.so, a library of their own next to libq38m.so (which
+ * exports none of them), holds these for the test suite: each runs one
  * instruction-level building block of the kernels on the device so the
  * tests can pin it in isolation (the contract's exp against libm, the
  * int8 MFMA lane layouts against an integer matrix product).  A caller of
  * the MoE data plane never needs them; they allocate nothing and follow the
- * conventions of q38m.h (device pointers, opaque stream, status codes).
+ * conventions of q38m.h (device pointers, opaque stream, status codes,
+ * without a message: q38m_last_error belongs to libq38m.so).
  */
 #ifndef Q38M_SELFTEST_H
 #define Q38M_SELFTEST_H

@@ -182,29 +182,71 @@ SIGNATURES = {
     "q38m_synth_fill": (_INT, [_U32, _U64, _U64, _U64, _F, _I32, _I32, _P, _U32, _P, _P, _INT]),
     "q38m_moe_compiled": (_INT, []),
     "q38m_last_error": (ctypes.c_char_p, []),
-    # self checks (include/q38m_selftest.h)
+}
+
+# The test suite's self checks (include/q38m_selftest.h), in their own
+# library: libq38m.so exports none of them.
+SELFTEST_LIB_PATH = os.path.join(PACKAGE_DIR, "libq38m_selftest.so")
+SELFTEST_SIGNATURES = {
     "q38m_debug_expf": (_INT, [_P, _U32, _P, _P, _INT]),
     "q38m_debug_bf16_sweep": (_INT, [_P, _P, _INT]),
     "q38m_debug_mfma_16x16x32_i8": (_INT, [_P, _P, _P, _P, _INT]),
     "q38m_debug_mfma_32x32x32_i8": (_INT, [_P, _P, _P, _P, _INT]),
 }
 
+# The timing build (include/q38m_phase.h): the product entry points plus
+# the phase log.
+TIMED_LIB_PATH = os.path.join(PACKAGE_DIR, "libq38m_timed.so")
+PHASE_SIGNATURES = {
+    "q38m_phase_log_v1": (_INT, [_P, _U32, _INT]),
+    "q38m_phase_calls_v1": (_U32, []),
+}
+
+
+class PhaseRecord(ctypes.Structure):
+    _fields_ = [("stamp", ctypes.c_uint64 * 16), ("kernel", ctypes.c_uint32),
+                ("block", ctypes.c_uint32), ("call", ctypes.c_uint32), ("valid", ctypes.c_uint32)]
+
+
 _lib = None
+_selftest_lib = None
+_timed_lib = None
+
+
+def _open(path, signatures):
+    if not os.path.exists(path):
+        raise Q38MError(f"{path} is not built; run __graft_entry__.build()")
+    handle = ctypes.CDLL(path)
+    for name, (restype, argtypes) in signatures.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return handle
 
 
 def lib():
     """Loads libq38m.so (raises OSError/Q38MError when it is not built)."""
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
-            raise Q38MError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
-        handle = ctypes.CDLL(LIB_PATH)
-        for name, (restype, argtypes) in SIGNATURES.items():
-            fn = getattr(handle, name)
-            fn.restype = restype
-            fn.argtypes = argtypes
-        _lib = handle
+        _lib = _open(LIB_PATH, SIGNATURES)
     return _lib
+
+
+def selftest_lib():
+    """Loads libq38m_selftest.so, the test suite's self-check kernels."""
+    global _selftest_lib
+    if _selftest_lib is None:
+        _selftest_lib = _open(SELFTEST_LIB_PATH, SELFTEST_SIGNATURES)
+    return _selftest_lib
+
+
+def timed_lib():
+    """Loads libq38m_timed.so, the timing build (its own copy of every entry
+    point, with phase timestamps in the decode kernels)."""
+    global _timed_lib
+    if _timed_lib is None:
+        _timed_lib = _open(TIMED_LIB_PATH, {**SIGNATURES, **PHASE_SIGNATURES})
+    return _timed_lib
 
 
 def _check(rc):
@@ -221,6 +263,24 @@ def _check(rc):
 def call(name, *args):
     """Calls an int-returning entry point and raises on a non-OK status."""
     _check(getattr(lib(), name)(*args))
+
+
+def call_selftest(name, *args):
+    """Calls a self-check entry point of libq38m_selftest.so."""
+    rc = getattr(selftest_lib(), name)(*args)
+    if rc == ERR_INVALID_ARGUMENT:
+        raise InvalidArgument(f"{name}: invalid argument")
+    if rc != OK:
+        raise DeviceError(f"{name}: status {rc}")
+
+
+def call_timed(name, *args):
+    """Calls an entry point of the timing build and raises on a non-OK status."""
+    handle = timed_lib()
+    rc = getattr(handle, name)(*args)
+    if rc != OK:
+        message = handle.q38m_last_error().decode(errors="replace")
+        raise (InvalidArgument if rc == ERR_INVALID_ARGUMENT else DeviceError)(message)
 
 
 # ---------------------------------------------------------------------------

@@ -11,7 +11,6 @@
 #include <string>
 
 #include "q38m_internal.h"
-#include "q38m_selftest.h"
 
 #include <initializer_list>
 #include <mutex>
@@ -922,32 +921,6 @@ int q38m_hyper_prepare_v1(const uint16_t* hyper, const uint16_t* norm_weight,
                                              hidden, low_rank, scratch, mixed, injection,
                                              as_stream(stream)),
                   "hyper prepare kernels");
-}
-
-int q38m_debug_expf(const float* x, uint32_t n, float* out, void* stream, int device) {
-    if (!x || !out || n == 0) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug expf input");
-    if (int rc = select_device(device)) return rc;
-    return finish(q38m::launch_debug_expf(x, n, out, as_stream(stream)), "debug_expf_kernel");
-}
-
-int q38m_debug_bf16_sweep(uint32_t* result, void* stream, int device) {
-    if (!result) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug bf16 input");
-    if (int rc = select_device(device)) return rc;
-    return finish(q38m::launch_debug_bf16(result, as_stream(stream)), "debug_bf16_kernel");
-}
-
-int q38m_debug_mfma_16x16x32_i8(const int8_t* a, const int8_t* b, int32_t* d, void* stream,
-                                int device) {
-    if (!a || !b || !d) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug mfma input");
-    if (int rc = select_device(device)) return rc;
-    return finish(q38m::launch_debug_mfma(a, b, d, as_stream(stream)), "debug_mfma_kernel");
-}
-
-int q38m_debug_mfma_32x32x32_i8(const int8_t* a, const int8_t* b, int32_t* d, void* stream,
-                                int device) {
-    if (!a || !b || !d) return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid debug mfma input");
-    if (int rc = select_device(device)) return rc;
-    return finish(q38m::launch_debug_mfma32(a, b, d, as_stream(stream)), "debug_mfma32_kernel");
 }
 
 }  // extern "C"

@@ -29,11 +29,85 @@
 #include "q38m_internal.h"
 #include "q38m_select.h"
 
+#ifdef Q38M_PHASE_TIMESTAMPS
+#include <atomic>
+
+#include "q38m_phase.h"
+#endif
+
 namespace q38m {
 namespace {
 
+// ---- phase timestamps (include/q38m_phase.h) ------------------------------
+// PhaseStamps reads the constant 100 MHz clock at a kernel's phase
+// boundaries in the timing build (-DQ38M_PHASE_TIMESTAMPS) and is empty in
+// the product build, where every call on it compiles to nothing.  PhaseCall
+// carries the host's call counter (always 0 in the product build).
+struct PhaseCall {
+    uint32_t index;
+};
+
+#ifdef Q38M_PHASE_TIMESTAMPS
+__device__ q38m_phase_record_v1* g_phase_records;
+__device__ uint32_t g_phase_calls_held;  // log capacity / 512
+std::atomic<uint32_t> g_phase_calls{0};
+
+struct PhaseStamps {
+    static constexpr uint32_t kStamps = 16u;
+    uint64_t t[kStamps];
+    __device__ PhaseStamps() {
+#pragma unroll
+        for (uint32_t i = 1; i < kStamps; ++i) t[i] = 0u;
+        t[0] = __builtin_amdgcn_s_memrealtime();
+        // the start stays ahead of the kernel-argument loads and their wait
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __device__ void mark(uint32_t i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+    // after this wave's outstanding vector loads have arrived
+    __device__ void mark_loaded(uint32_t i) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        mark(i);
+    }
+    // thread 0 writes the record (a vector store under a lane branch)
+    __device__ void finish(uint32_t kernel, PhaseCall call) {
+        q38m_phase_record_v1* log = g_phase_records;
+        const uint32_t held = g_phase_calls_held;
+        if (threadIdx.x != 0u || log == nullptr || held == 0u) return;
+        q38m_phase_record_v1& r = log[(call.index % held) * 512u + 256u * kernel + blockIdx.x];
+#pragma unroll
+        for (uint32_t i = 0; i < kStamps; ++i) r.stamp[i] = t[i];
+        r.kernel = kernel;
+        r.block = blockIdx.x;
+        r.call = call.index;
+        r.valid = 1u;
+    }
+};
+
+PhaseCall next_phase_call() { return PhaseCall{g_phase_calls.fetch_add(1u)}; }
+#else
+struct PhaseStamps {
+    __device__ void mark(uint32_t) {}
+    __device__ void mark_loaded(uint32_t) {}
+    __device__ void finish(uint32_t, PhaseCall) {}
+};
+
+PhaseCall next_phase_call() { return PhaseCall{0u}; }
+#endif
+
 constexpr uint32_t kDecodeBlocks = 256;
 constexpr uint32_t kDecodeThreads = kSelectThreads;
+
+// gate/up: 12 waves, three route slots x four quarters of K.
+constexpr uint32_t kGateUpThreads = 768u;
+constexpr uint32_t kRouteSlots = 3u;
+static_assert(kGateUpThreads >= kSelectThreads, "the block top-k needs ten waves");
+static_assert(kRouteSlots * 64u * 4u == kGateUpThreads, "wave = route slot x K quarter");
+
+// Routes of workgroup group g (0..3): {0,1,2}, {3,4,5}, {6,7}, {8,9}.
+__device__ __forceinline__ uint32_t route_group_first(uint32_t g) {
+    return g < 2u ? 3u * g : 2u * g + 2u;
+}
+__device__ __forceinline__ uint32_t route_group_count(uint32_t g) { return g < 2u ? 3u : 2u; }
 
 // W4 (kW8 false): kPer = 32-column sub-blocks per group (1, 2 or 4: groups
 // of 32, 64, 128), the MFMA16 quad-major layout.  W8: kPer = 64-column K
@@ -41,29 +115,43 @@ constexpr uint32_t kDecodeThreads = kSelectThreads;
 // K-block-major layout, scales in the artifact order.  A group's partial
 // accumulators add exactly in int32 before the fp32 chain; bf16: scale
 // words are bf16 (else fp16).
+//
+// Workgroup b owns channels 16p + 8h .. +7 (gate and up rows) of pair tile
+// p for one group of routes; the two halves h of a (p, group) sit on one XCD
+// (b % 8), so each 128-byte line of scale words crosses HBM once.  Load
+// layout: wave = (route slot rs, K quarter), lane = n + 8u + 16kq' (row
+// 8h + n of the tile's gate (u = 0) or up (u = 1) slot, quad 4 quarter +
+// kq'): every load instruction reads 8 whole 128-byte lines, 8 consecutive
+// lanes per line.  The int32 group sums and their scales then move through
+// LDS into the chain layout: wave = route slot x two channels, lane =
+// quad + 16 (2 n' + u), where the fp32 chain runs along each 16-lane row.
 template <uint32_t H, uint32_t I, bool kW8, uint32_t kPer>
-__global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
+__global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, bool bf16,
     const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
     const int32_t* __restrict__ ids_in, const float* __restrict__ weights_in, uint32_t top_k,
-    int32_t* __restrict__ ids_out, uint16_t* __restrict__ mid) {
+    int32_t* __restrict__ ids_out, uint16_t* __restrict__ mid, PhaseCall call) {
+    PhaseStamps stamps;
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kSlots = 2u * I / 16u;
     constexpr uint32_t kPairs = I / 16u;
     constexpr uint32_t kQuadPad = 9u;  // 144-byte rows: the 16 quads hit disjoint banks
+    constexpr uint32_t kChains = kRouteSlots * 16u;  // (route slot, channel, gate/up)
     static_assert(H == 256u * 8u && kQuads == 16u, "16 quads, one 8-element token chunk per thread");
-    static_assert(kPairs * 8u == kDecodeBlocks, "eight workgroups per pair tile");
+    static_assert(kPairs * 2u * 4u == kDecodeBlocks, "pair tile x half x route group");
     __shared__ int32_t ids_lds[kTopK];
     __shared__ float num_lds[kTopK];
     __shared__ float amax_lds[4];
     __shared__ uint4 x_lds[kQuads * kQuadPad];
     __shared__ SelectLds select_lds;
+    // [chain][quad]: int32 group sums, then their fp32 scales
+    __shared__ uint4 xch[kChains * kQuads][2];
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t slot8 = blockIdx.x >> 3;
-    const uint32_t pair = 4u * (blockIdx.x & 7u) + (slot8 >> 3);
-    const uint32_t n0 = 2u * (slot8 & 7u);
+    const uint32_t xcd = blockIdx.x & 7u, within = blockIdx.x >> 3;
+    const uint32_t pg = 16u * xcd + (within >> 1);
+    const uint32_t pair = pg % kPairs, group = pg / kPairs, half = within & 1u;
     const bool fused = logits != nullptr;
 
     uint4 hv = make_uint4(0u, 0u, 0u, 0u);
@@ -75,60 +163,74 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
         num_lds[lane] = weights_in[lane];
     }
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    stamps.mark_loaded(1);
     // the selection first: the token row's absmax waits for its load, the
     // selection only for the logits
     if (fused) {
-        block_topk512(logit, select_lds, ids_lds, num_lds);
+        block_topk512(logit, select_lds, ids_lds, num_lds,
+                      [&](uint32_t level) { stamps.mark(10u + level); });
         if (blockIdx.x == 0 && threadIdx.x < top_k) ids_out[threadIdx.x] = ids_lds[threadIdx.x];
     } else {
         __syncthreads();
     }
+    stamps.mark(2);
 
-    // every lane's weights: lane = kq + 16*(c + 2u), u = gate/up, c = channel
-    const uint32_t route = wave;
-    const int32_t id = route < top_k ? ids_lds[route] : -1;
+    // this wave's route (the same in the load and the chain layout)
+    const uint32_t slot_rs = wave >> 2;
+    const uint32_t route = route_group_first(group) + slot_rs;
+    const bool active = slot_rs < route_group_count(group) && route < top_k;
+    const int32_t id = active ? ids_lds[route] : -1;
     const bool valid = id >= 0 && id < static_cast<int32_t>(kExperts);
     const uint32_t e = valid ? static_cast<uint32_t>(id) : 0u;
-    const uint32_t kq = lane & 15u;
-    const uint32_t c = (lane >> 4) & 1u;
-    const uint32_t u = lane >> 5;
+
+    // load layout
+    const uint32_t n = lane & 7u, u = (lane >> 3) & 1u;
+    const uint32_t kq = 4u * (wave & 3u) + (lane >> 4);
+    const uint32_t row = 8u * half + n;
+    const uint32_t slot = 2u * pair + u;
     // W4: quad kq of the slot's tile, 16 bytes per row per 32-column group.
     // W8: blocks 2kq and 2kq+1 (the same 128 columns), 16 bytes per row and
-    // lane group q: bq[4*block + q].
+    // lane group q: bq[4*block + q].  A wave without a route reads one
+    // common kilobyte instead (an L2 hit), so every load stays unconditional.
     uint4 bq[kW8 ? 8 : 4];
     uint2 sc = make_uint2(0u, 0u);
     uint32_t sw = 0;
     if constexpr (!kW8) {
-        const size_t tile = (static_cast<size_t>(e) * kQuads + kq) * kSlots + 2u * pair + u;
-        const uint4* wp = w + tile * 64u + n0 + c;
+        const size_t tile = (static_cast<size_t>(e) * kQuads + kq) * kSlots + slot;
+        const uint4* wp = active ? w + tile * 64u + row : w + lane;
         bq[0] = wp[0];
         bq[1] = wp[16];
         bq[2] = wp[32];
         bq[3] = wp[48];
-        sc = load_quad_scales<kPer, false>(s + (tile * 16u + n0 + c) * (4u / kPer));
+        sc = load_quad_scales<kPer, false>(s + (active ? (tile * 16u + row) * (4u / kPer) : 0u));
     } else {
         constexpr uint32_t kBlocks = H / 64u;
-        const uint32_t slot = 2u * pair + u;
 #pragma unroll
         for (uint32_t b = 0; b < 2u; ++b) {
-            const uint4* wp = w + ((static_cast<size_t>(e) * kBlocks + 2u * kq + b) * kSlots + slot) *
-                                      64u + n0 + c;
+            const uint4* wp =
+                active ? w + ((static_cast<size_t>(e) * kBlocks + 2u * kq + b) * kSlots + slot) *
+                                 64u + row
+                       : w + lane;
 #pragma unroll
             for (uint32_t q = 0; q < 4u; ++q) bq[4u * b + q] = wp[16u * q];
         }
-        const size_t row = static_cast<size_t>(e) * 2u * I + (u ? I : 0u) + 16u * pair + n0 + c;
+        const size_t srow = active ? static_cast<size_t>(e) * 2u * I + (u ? I : 0u) +
+                                         16u * pair + row
+                                   : 0u;
         if constexpr (kPer == kBlocks)
-            sw = s[row];
+            sw = s[srow];
         else if constexpr (kPer == 1u)
-            sw = *reinterpret_cast<const uint32_t*>(s + row * kBlocks + 2u * kq);
+            sw = *reinterpret_cast<const uint32_t*>(s + srow * kBlocks + 2u * kq);
         else
-            sw = s[row * (kBlocks / 2u) + kq];
+            sw = s[srow * (kBlocks / 2u) + kq];
     }
+
+    stamps.mark(3);
 
     // the route's weight, while the weights stream: given, or
     // exp(l_r - l_0) over the rank-order sum (q38_kernels.cu:460-479)
     float wr = 0.0f;
-    if (route < top_k) {
+    if (active) {
         wr = num_lds[route];
         if (fused) {
             float denominator = 0.0f;
@@ -149,49 +251,44 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
             quantize8(hw, row_q);
     }
     __syncthreads();
+    stamps.mark(4);
+    stamps.mark_loaded(5);
 
-    float y = 0.0f;
+    // this lane's group sums (int32) and their scales (fp32 words)
+    uint4 xa = make_uint4(0u, 0u, 0u, 0u), xf = make_uint4(0u, 0u, 0u, 0u);
     if constexpr (!kW8) {
-    // group j of quad kq, chunk q: k = 32(4kq+j) + 8q + {0..3} (low nibbles)
-    // and + {4..7} (high nibbles); nibbles sit in the high half of each byte
-    // (16*w), so acc is 16x the group accumulator.
-    uint32_t xw[32];
+        // group j of quad kq, chunk q: k = 32(4kq+j) + 8q + {0..3} (low
+        // nibbles) and + {4..7} (high nibbles); nibbles sit in the high half
+        // of each byte (16*w), so acc is 16x the group accumulator.
+        uint32_t xw[32];
 #pragma unroll
-    for (uint32_t i = 0; i < 8u; ++i) {
-        const uint4 xv = x_lds[kq * kQuadPad + i];
-        xw[4 * i] = xv.x; xw[4 * i + 1] = xv.y; xw[4 * i + 2] = xv.z; xw[4 * i + 3] = xv.w;
-    }
-    int acc[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (uint32_t q = 0; q < 4u; ++q) {
-        const uint32_t wq[4] = {bq[q].x, bq[q].y, bq[q].z, bq[q].w};
-#pragma unroll
-        for (uint32_t j = 0; j < 4u; ++j) {
-            const uint32_t lo = (wq[j] << 4) & 0xf0f0f0f0u;
-            const uint32_t hi = wq[j] & 0xf0f0f0f0u;
-            acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(xw[8u * j + 2u * q]), acc[j], false);
-            acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xw[8u * j + 2u * q + 1u]), acc[j], false);
+        for (uint32_t i = 0; i < 8u; ++i) {
+            const uint4 xv = x_lds[kq * kQuadPad + i];
+            xw[4 * i] = xv.x; xw[4 * i + 1] = xv.y; xw[4 * i + 2] = xv.z; xw[4 * i + 3] = xv.w;
         }
-    }
-    float gs[4u / kPer];
-    int gacc[4u / kPer];
+        int acc[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (uint32_t gi = 0; gi < 4u / kPer; ++gi) {
-        gs[gi] = scale_to_f32(quad_scale_word(sc, gi), bf16) * 0.0625f;
-        gacc[gi] = acc[gi * kPer];
+        for (uint32_t q = 0; q < 4u; ++q) {
+            const uint32_t wq[4] = {bq[q].x, bq[q].y, bq[q].z, bq[q].w};
 #pragma unroll
-        for (uint32_t j = 1; j < kPer; ++j) gacc[gi] += acc[gi * kPer + j];
-    }
-    // fp32 chain in group order: lane kq continues lane kq-1's value (row_shr:1
-    // inside each 16-lane row); after 16 steps lane 15 holds the row's y.
+            for (uint32_t j = 0; j < 4u; ++j) {
+                const uint32_t lo = (wq[j] << 4) & 0xf0f0f0f0u;
+                const uint32_t hi = wq[j] & 0xf0f0f0f0u;
+                acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(lo), static_cast<int>(xw[8u * j + 2u * q]), acc[j], false);
+                acc[j] = __builtin_amdgcn_sdot4(static_cast<int>(hi), static_cast<int>(xw[8u * j + 2u * q + 1u]), acc[j], false);
+            }
+        }
+        uint32_t ga[4] = {0u, 0u, 0u, 0u}, gf[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (uint32_t step = 0; step < kQuads; ++step) {
-        float t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
+        for (uint32_t gi = 0; gi < 4u / kPer; ++gi) {
+            gf[gi] = __float_as_uint(scale_to_f32(quad_scale_word(sc, gi), bf16) * 0.0625f);
+            int sum = acc[gi * kPer];
 #pragma unroll
-        for (uint32_t gi = 0; gi < 4u / kPer; ++gi)
-            t = __builtin_fmaf(static_cast<float>(gacc[gi]), gs[gi], t);
-        y = t;
-    }
+            for (uint32_t j = 1; j < kPer; ++j) sum += acc[gi * kPer + j];
+            ga[gi] = static_cast<uint32_t>(sum);
+        }
+        xa = make_uint4(ga[0], ga[1], ga[2], ga[3]);
+        xf = make_uint4(gf[0], gf[1], gf[2], gf[3]);
     } else {
         // block b (= 2kq + b), lane group q: columns 64(2kq+b) + 16q .. +15
         int acc[2] = {0, 0};
@@ -206,49 +303,74 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_gate_up_kernel(
                 acc[b] = __builtin_amdgcn_sdot4(static_cast<int>(wv.z), static_cast<int>(xv.z), acc[b], false);
                 acc[b] = __builtin_amdgcn_sdot4(static_cast<int>(wv.w), static_cast<int>(xv.w), acc[b], false);
             }
-        if constexpr (kPer == H / 64u) {
-            // per channel: one int32 over the row (16 lanes), y = (float)acc * s
-            // the row's 16 lanes by DPP rotations (row_ror 8, 4, 2, 1)
-            int sum = acc[0] + acc[1];
-            sum += __builtin_amdgcn_update_dpp(0, sum, 0x128, 0xf, 0xf, false);
-            sum += __builtin_amdgcn_update_dpp(0, sum, 0x124, 0xf, 0xf, false);
-            sum += __builtin_amdgcn_update_dpp(0, sum, 0x122, 0xf, 0xf, false);
-            sum += __builtin_amdgcn_update_dpp(0, sum, 0x121, 0xf, 0xf, false);
-            y = static_cast<float>(sum) * scale_to_f32(sw, bf16);
+        if constexpr (kPer == 1u) {
+            xa = make_uint4(static_cast<uint32_t>(acc[0]), static_cast<uint32_t>(acc[1]), 0u, 0u);
+            xf = make_uint4(__float_as_uint(scale_to_f32(sw & 0xffffu, bf16)),
+                            __float_as_uint(scale_to_f32(sw >> 16, bf16)), 0u, 0u);
         } else {
-            float gs[2];
-            int gacc[2];
-            if constexpr (kPer == 1u) {
-                gs[0] = scale_to_f32(sw & 0xffffu, bf16);
-                gs[1] = scale_to_f32(sw >> 16, bf16);
-                gacc[0] = acc[0];
-                gacc[1] = acc[1];
-            } else {
-                gs[0] = scale_to_f32(sw, bf16);
-                gacc[0] = acc[0] + acc[1];
-            }
-            // the same chain over the 16 lanes of the row, 128 columns per lane
+            // per channel: this lane's 128-column part of the row's one
+            // int32; groups of 128: the group's sum
+            xa.x = static_cast<uint32_t>(acc[0] + acc[1]);
+            xf.x = __float_as_uint(scale_to_f32(sw, bf16));
+        }
+    }
+    stamps.mark(6);
+    {
+        const uint32_t chain = 16u * slot_rs + 2u * n + u;
+        xch[chain * kQuads + kq][0] = xa;
+        xch[chain * kQuads + kq][1] = xf;
+    }
+    __syncthreads();
+    stamps.mark(7);
+
+    // chain layout: lane = quad + 16 c, chain 4 wave + c = (route slot,
+    // channel 2 (wave % 4) + c / 2, gate/up c % 2)
+    const uint32_t cq = lane & 15u;
+    const uint4 ca = xch[(4u * wave + (lane >> 4)) * kQuads + cq][0];
+    const uint4 cf = xch[(4u * wave + (lane >> 4)) * kQuads + cq][1];
+    const int ga[4] = {static_cast<int>(ca.x), static_cast<int>(ca.y), static_cast<int>(ca.z),
+                       static_cast<int>(ca.w)};
+    const float gs[4] = {__uint_as_float(cf.x), __uint_as_float(cf.y), __uint_as_float(cf.z),
+                         __uint_as_float(cf.w)};
+    constexpr uint32_t kChainTerms = kW8 ? (kPer == 1u ? 2u : 1u) : 4u / kPer;
+    float y = 0.0f;
+    if constexpr (kW8 && kPer == H / 64u) {
+        // per channel: one int32 over the row (16 lanes) by DPP rotations
+        // (row_ror 8, 4, 2, 1), y = (float)acc * s
+        int sum = ga[0];
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0x128, 0xf, 0xf, false);
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0x124, 0xf, 0xf, false);
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0x122, 0xf, 0xf, false);
+        sum += __builtin_amdgcn_update_dpp(0, sum, 0x121, 0xf, 0xf, false);
+        y = static_cast<float>(sum) * gs[0];
+    } else {
+        // fp32 chain in group order: lane cq continues lane cq-1's value
+        // (row_shr:1 inside each 16-lane row); after 16 steps lane 15 of
+        // the row holds the channel's y.
 #pragma unroll
-            for (uint32_t step = 0; step < kQuads; ++step) {
-                float t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
+        for (uint32_t step = 0; step < kQuads; ++step) {
+            float t = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(y), 0x111, 0xf, 0xf, true));
 #pragma unroll
-                for (uint32_t gi = 0; gi < 2u / kPer; ++gi)
-                    t = __builtin_fmaf(static_cast<float>(gacc[gi]), gs[gi], t);
-                y = t;
-            }
+            for (uint32_t gi = 0; gi < kChainTerms; ++gi)
+                t = __builtin_fmaf(static_cast<float>(ga[gi]), gs[gi], t);
+            y = t;
         }
     }
     const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 15));
-    const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 31));
-    const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 47));
+    const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 31));
+    const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 47));
     const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(y), 63));
-    // lane n computes channel n0 + n (n = 0, 1)
-    if (lane < 2u && route < top_k) {
+    stamps.mark(8);
+    // lane c computes channel 2 (wave % 4) + c (c = 0, 1)
+    if (lane < 2u && active) {
         const float g = lane == 0u ? g0 : g1;
         const float up = lane == 0u ? u0 : u1;
         const uint32_t m = valid ? swiglu_fold(g * xs, up * xs, wr) : 0u;
-        mid[static_cast<size_t>(route) * I + 16u * pair + n0 + lane] = static_cast<uint16_t>(m);
+        mid[static_cast<size_t>(route) * I + 16u * pair + 8u * half + 2u * (wave & 3u) + lane] =
+            static_cast<uint16_t>(m);
     }
+    stamps.mark(9);
+    stamps.finish(0u, call);
 }
 
 // kPerGroup: W4, 32-column sub-blocks per group (1, 2, 4); W8, 64-column
@@ -259,7 +381,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     const uint16_t* __restrict__ mid,
     const int32_t* __restrict__ ids, uint32_t top_k, const uint16_t* __restrict__ shared_output,
     const uint16_t* __restrict__ shared_gate, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, PhaseCall call) {
+    PhaseStamps stamps;
     constexpr uint32_t kTiles = H / 16u;
     static_assert(I == 64u * 8u, "one 8-element chunk of the mid row per lane");
     static_assert(kTiles * 2u == kDecodeBlocks, "eight output channels per workgroup");
@@ -326,6 +449,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     // every request above is out before the quantisation below waits for
     // the mid row
     __builtin_amdgcn_sched_barrier(0);
+    stamps.mark(1);
 
     // quantise this route's mid row (8 elements per lane)
     const uint32_t mw[4] = {mv.x, mv.y, mv.z, mv.w};
@@ -339,6 +463,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     const float sm = mid_q.s;
     reinterpret_cast<uint2*>(mq_lds[route])[lane] = quantize8(mw, mid_q);
     __syncthreads();
+    stamps.mark(2);
+    stamps.mark_loaded(3);
 
     float o = 0.0f;
     if constexpr (kW4) {
@@ -418,8 +544,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
             o = __shfl(y, static_cast<int>(8u * kPerGroup * (kW8Groups - 1u) + c), 64) * sm;
         }
     }
+    stamps.mark(4);
     if (lane < 8u) reinterpret_cast<float*>(o_lds[lane])[route] = valid ? o : 0.0f;
     __syncthreads();
+    stamps.mark(5);
     if (finisher) {
         // routes summed in rank order
         const float4 p0 = o_lds[threadIdx.x][0], p1 = o_lds[threadIdx.x][1];
@@ -440,6 +568,8 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
             result = f32_to_bf16(bf16_to_f32(residual_bits) + bf16_to_f32(result));
         out[channel] = static_cast<uint16_t>(result);
     }
+    stamps.mark(6);
+    stamps.finish(1u, call);
 }
 
 }  // namespace
@@ -454,11 +584,11 @@ template <bool kW4, uint32_t kPerGroup>
 void launch_decode_down(const q38m_expert_weights_v1& down, const uint16_t* mid,
                         const int32_t* ids, uint32_t top_k, const uint16_t* shared_output,
                         const uint16_t* shared_gate, const uint16_t* residual, uint16_t* output,
-                        hipStream_t stream) {
+                        PhaseCall call, hipStream_t stream) {
     decode_down_kernel<kHidden, kInter, kW4, kPerGroup><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
         static_cast<const uint4*>(down.data), static_cast<const uint16_t*>(down.scales),
         down.scale_dtype == Q38M_SCALE_BF16, mid, ids, top_k, shared_output, shared_gate,
-        residual, output);
+        residual, output, call);
 }
 
 }  // namespace
@@ -475,10 +605,11 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
     const uint16_t* gs = static_cast<const uint16_t*>(gate_up.scales);
     const bool gbf16 = gate_up.scale_dtype == Q38M_SCALE_BF16;
     int32_t* ids_out = logits != nullptr ? scratch_ids : nullptr;
+    const PhaseCall call = next_phase_call();
     auto gate_up_launch = [&](auto w8, auto per) {
         decode_gate_up_kernel<kHidden, kInter, decltype(w8)::value, decltype(per)::value>
-            <<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(gw, gs, gbf16, hidden, logits, ids,
-                                                           weights, top_k, ids_out, mid);
+            <<<kDecodeBlocks, kGateUpThreads, 0, stream>>>(gw, gs, gbf16, hidden, logits, ids,
+                                                           weights, top_k, ids_out, mid, call);
     };
     using W4 = std::false_type;
     using W8 = std::true_type;
@@ -504,28 +635,28 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
         case 0u:
             if (!w8) return hipErrorInvalidValue;
             launch_decode_down<false, kBlocks>(down, mid, down_ids, top_k, shared_output,
-                                               shared_gate, residual, output, stream);
+                                               shared_gate, residual, output, call, stream);
             break;
         case 32u:
             if (w8) return hipErrorInvalidValue;
             launch_decode_down<true, 1>(down, mid, down_ids, top_k, shared_output, shared_gate,
-                                        residual, output, stream);
+                                        residual, output, call, stream);
             break;
         case 64u:
             if (w8)
                 launch_decode_down<false, 1>(down, mid, down_ids, top_k, shared_output,
-                                             shared_gate, residual, output, stream);
+                                             shared_gate, residual, output, call, stream);
             else
                 launch_decode_down<true, 2>(down, mid, down_ids, top_k, shared_output,
-                                            shared_gate, residual, output, stream);
+                                            shared_gate, residual, output, call, stream);
             break;
         case 128u:
             if (w8)
                 launch_decode_down<false, 2>(down, mid, down_ids, top_k, shared_output,
-                                             shared_gate, residual, output, stream);
+                                             shared_gate, residual, output, call, stream);
             else
                 launch_decode_down<true, 4>(down, mid, down_ids, top_k, shared_output,
-                                            shared_gate, residual, output, stream);
+                                            shared_gate, residual, output, call, stream);
             break;
         default: return hipErrorInvalidValue;
     }
@@ -533,3 +664,24 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
 }
 
 }  // namespace q38m
+
+#ifdef Q38M_PHASE_TIMESTAMPS
+extern "C" {
+
+int q38m_phase_log_v1(q38m_phase_record_v1* records, uint32_t capacity, int device) {
+    if (capacity % 512u != 0u || (records == nullptr) != (capacity == 0u) || device < 0)
+        return Q38M_ERR_INVALID_ARGUMENT;
+    if (hipSetDevice(device) != hipSuccess) return Q38M_ERR_DEVICE;
+    const uint32_t held = capacity / 512u;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(q38m::g_phase_records), &records, sizeof(records)) !=
+            hipSuccess ||
+        hipMemcpyToSymbol(HIP_SYMBOL(q38m::g_phase_calls_held), &held, sizeof(held)) != hipSuccess)
+        return Q38M_ERR_DEVICE;
+    q38m::g_phase_calls.store(0u);
+    return Q38M_OK;
+}
+
+uint32_t q38m_phase_calls_v1(void) { return q38m::g_phase_calls.load(); }
+
+}  // extern "C"
+#endif

@@ -179,12 +179,5 @@ hipError_t launch_quantize_weights(const uint16_t* src, const q38m_expert_weight
 hipError_t launch_synth(uint32_t kind, uint64_t seed, uint64_t tag, uint64_t count,
                         float sigma, int32_t lo, int32_t hi, const float* bias,
                         uint32_t bias_len, void* out, hipStream_t stream);
-hipError_t launch_debug_expf(const float* x, uint32_t n, float* out,
-                             hipStream_t stream);
-hipError_t launch_debug_bf16(uint32_t* result, hipStream_t stream);
-hipError_t launch_debug_mfma(const int8_t* a, const int8_t* b, int32_t* d,
-                             hipStream_t stream);
-hipError_t launch_debug_mfma32(const int8_t* a, const int8_t* b, int32_t* d,
-                               hipStream_t stream);
 
 }  // namespace q38m

@@ -94,17 +94,25 @@ template <typename Store>
 __device__ __forceinline__ uint32_t wave_top10(uint32_t k32, uint32_t expert, Store store) {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t prefix = 0u;
+    // Unrolled, so the prefix stays in scalar registers (a rolled loop
+    // carries it and the bit index in vector registers): per bit, scalar
+    // count, compare, select, next candidate and exit test -- the waves share
+    // the CU's scalar unit, and the compiler's own popcount of a 64-bit
+    // ballot adds a 64-bit vector compare and an exec mask step.
 #pragma unroll
     for (int b = 31; b >= 0; --b) {
-        // four scalar instructions per bit (count, compare, select, next
-        // candidate): the waves share the CU's scalar unit, and the
-        // compiler's own popcount of a 64-bit ballot adds a 64-bit vector
-        // compare and an exec mask step
         const uint32_t cand = prefix | (1u << b);
         const uint64_t reach = __builtin_amdgcn_ballot_w64(k32 >= cand);
         uint32_t count;
         asm("s_bcnt1_i32_b64 %0, %1" : "=s"(count) : "s"(reach));
         prefix = count >= kTopK ? cand : prefix;
+        // exactly ten keys reach the prefix: they are the wave's top 10
+        // (below, "above" and the ties at the prefix make up exactly that
+        // set whether or not the prefix is itself a key), so the remaining
+        // bits cannot change the selection.  Distinct logits usually get
+        // here once the prefix separates the 10th key from the 11th, about
+        // half way down.
+        if (count == kTopK) break;
     }
     const uint64_t below = (1ull << lane) - 1ull;
     const uint64_t above = __ballot(k32 > prefix);
@@ -195,8 +203,11 @@ __device__ __forceinline__ void rank_candidates(const SelectLds& lds, int32_t* i
 // writes the caller made before the call are visible to the whole block on
 // return.  On return ids[r] and num[r] (r < 10) hold the rank-r expert and
 // exp(l_r - l_0).
+// phase(i) is called after level 1 (i = 0), after the barrier that joins
+// the lists (1) and after level 2 (2); the plain form passes a no-op.
+template <typename Phase>
 __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32_t* ids,
-                                              float* num) {
+                                              float* num, Phase phase) {
     const uint32_t t = threadIdx.x;
     if (t < kExperts) {
         uint64_t* list = lds.cand + kTopK * (t >> 6);
@@ -205,9 +216,17 @@ __device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32
         });
         if ((t & 63u) == 0u) lds.wave_max[t >> 6] = kmax;
     }
+    phase(0u);
     __syncthreads();
+    phase(1u);
     rank_candidates<8>(lds, ids, num);
+    phase(2u);
     __syncthreads();
+}
+
+__device__ __forceinline__ void block_topk512(float logit, SelectLds& lds, int32_t* ids,
+                                              float* num) {
+    block_topk512(logit, lds, ids, num, [](uint32_t) {});
 }
 
 // max |x| over eight bf16 values (one 16-byte chunk)

@@ -7,20 +7,30 @@ touching a device."""
 import ctypes
 import os
 import re
+import subprocess
 
 import pytest
 
 from conftest import ROOT
 
-HEADERS = [os.path.join(ROOT, "include", name) for name in ("q38m.h", "q38m_selftest.h")]
+HEADERS = [os.path.join(ROOT, "include", name)
+           for name in ("q38m.h", "q38m_selftest.h", "q38m_phase.h")]
 
 
-def declared_functions(headers=HEADERS):
+def declared_functions(headers=HEADERS[:1]):
     names = set()
     for header in headers:
         text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
         names.update(re.findall(r"\b(q38m_[a-z0-9_]+)\s*\(", text))
     return sorted(names)
+
+
+def exported_functions(path):
+    """The q38m_ functions a shared library's dynamic symbol table defines."""
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True,
+                         text=True).stdout
+    return sorted({line.split()[-1] for line in out.splitlines()
+                   if line.split()[-1].startswith("q38m_") and line.split()[1] in "TW"})
 
 
 def test_library_exports_every_declared_symbol(q38m):
@@ -33,12 +43,32 @@ def test_library_exports_every_declared_symbol(q38m):
     assert lib.q38m_moe_compiled() == 1
 
 
-def test_product_header_declares_no_self_checks():
-    product = declared_functions(HEADERS[:1])
-    assert not [n for n in product if n.startswith("q38m_debug")]
-    assert declared_functions(HEADERS[1:]) == ["q38m_debug_bf16_sweep", "q38m_debug_expf",
-                                               "q38m_debug_mfma_16x16x32_i8",
-                                               "q38m_debug_mfma_32x32x32_i8"]
+def test_product_library_exports_exactly_its_header(q38m):
+    """libq38m.so exports the operator surface of q38m.h and nothing else:
+    the self checks and the phase log live in their own libraries."""
+    assert exported_functions(q38m.LIB_PATH) == declared_functions()
+
+
+def test_selftest_library_exports_its_header(q38m):
+    names = declared_functions(HEADERS[1:2])
+    assert names == ["q38m_debug_bf16_sweep", "q38m_debug_expf", "q38m_debug_mfma_16x16x32_i8",
+                     "q38m_debug_mfma_32x32x32_i8"]
+    assert exported_functions(q38m.SELFTEST_LIB_PATH) == names
+    assert set(names) == set(q38m.SELFTEST_SIGNATURES)
+    q38m.selftest_lib()
+    with pytest.raises(q38m.InvalidArgument):
+        q38m.call_selftest("q38m_debug_expf", None, 0, None, None, 0)
+
+
+def test_timed_library_is_the_product_plus_the_phase_log(q38m):
+    phase = declared_functions(HEADERS[2:])
+    assert phase == ["q38m_phase_calls_v1", "q38m_phase_log_v1"]
+    assert exported_functions(q38m.TIMED_LIB_PATH) == sorted(declared_functions() + phase)
+    assert ctypes.sizeof(q38m.PhaseRecord) == 144
+    lib = q38m.timed_lib()
+    # capacity must be a multiple of 512 records, and null with zero
+    assert lib.q38m_phase_log_v1(None, 512, 0) == q38m.ERR_INVALID_ARGUMENT
+    assert lib.q38m_phase_log_v1(None, 0, -1) == q38m.ERR_INVALID_ARGUMENT
 
 
 def test_struct_layouts(q38m):

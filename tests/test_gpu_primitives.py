@@ -29,7 +29,7 @@ def test_mfma_i8_lane_layout(q38m):
     t = torch()
     d = t.zeros(256, dtype=t.int32, device="cuda")
     da, db = device(a), device(b)  # keep both alive until the kernel has run
-    q38m.call("q38m_debug_mfma_16x16x32_i8", da.data_ptr(), db.data_ptr(), d.data_ptr(),
+    q38m.call_selftest("q38m_debug_mfma_16x16x32_i8", da.data_ptr(), db.data_ptr(), d.data_ptr(),
               stream(), 0)
     got = host(d, np.int32).reshape(16, 16)
     assert np.array_equal(got, a.astype(np.int64) @ b.astype(np.int64))
@@ -42,7 +42,7 @@ def test_mfma_i8_32x32_lane_layout(q38m):
     t = torch()
     d = t.zeros(1024, dtype=t.int32, device="cuda")
     da, db = device(a), device(b)
-    q38m.call("q38m_debug_mfma_32x32x32_i8", da.data_ptr(), db.data_ptr(), d.data_ptr(),
+    q38m.call_selftest("q38m_debug_mfma_32x32x32_i8", da.data_ptr(), db.data_ptr(), d.data_ptr(),
               stream(), 0)
     got = host(d, np.int32).reshape(32, 32)
     assert np.array_equal(got, a.astype(np.int64) @ b.astype(np.int64))
@@ -58,7 +58,7 @@ def test_expf_bitwise(q38m, orc):
     t = torch()
     xd = device(x)
     out = t.empty_like(xd)
-    q38m.call("q38m_debug_expf", xd.data_ptr(), x.size, out.data_ptr(), stream(), 0)
+    q38m.call_selftest("q38m_debug_expf", xd.data_ptr(), x.size, out.data_ptr(), stream(), 0)
     got = host(out, np.float32)
     assert np.array_equal(got.view(np.uint32), orc.expf(x).view(np.uint32))
 
@@ -68,7 +68,7 @@ def test_bf16_hardware_conversion_sweep(q38m):
     against the contract's integer round-to-nearest-even, on the device."""
     t = torch()
     result = device(np.array([0, 0xFFFFFFFF, 0, 0xFFFFFFFF], np.uint32).view(np.int32))
-    q38m.call("q38m_debug_bf16_sweep", result.data_ptr(), stream(), 0)
+    q38m.call_selftest("q38m_debug_bf16_sweep", result.data_ptr(), stream(), 0)
     got = host(result, np.int32).view(np.uint32)
     print(f"bf16 sweep: mismatches {got[0]} (first {got[1]:#010x}), "
           f"non-NaN mismatches {got[2]} (first {got[3]:#010x})")
