@@ -587,14 +587,111 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
     }
 }
 
+// ---- one activation row (m = 1: the batch-1 decode step) --------------
+// At m = 1 a GEMM is a GEMV: every weight byte is used once, so the bound is
+// how fast the weight rows stream, and a 16 x 16 MFMA tile would waste 15 of
+// its 16 rows.  One wave per output row: lane l reads the row's 16-byte
+// chunks l, l + 64, ... (each load instruction eight whole 128-byte lines)
+// and the activation's matching chunks (an L2 hit after the first wave),
+// four chunks in flight per lane, each chunk's eight products accumulated
+// into its own fp32 partial in k order, the partials added in chunk order,
+// then the lanes summed by a fixed DPP / permlane tree.  The order of every
+// addition is fixed, so the results are the same on every run.
+
+// fp32 dot product of one weight row with the activation row over k
+// (k % 8 == 0), the sum in every lane of the wave.
+__device__ __forceinline__ float wave_dot_bf16(const uint16_t* __restrict__ a,
+                                               const uint16_t* __restrict__ row, uint32_t k,
+                                               uint32_t lane) {
+    const u32x4* av = reinterpret_cast<const u32x4*>(a);
+    const u32x4* bv = reinterpret_cast<const u32x4*>(row);
+    const uint32_t chunks = k / 8u;
+    float total = 0.0f;
+    for (uint32_t base = 0; base < chunks; base += 256u) {
+        u32x4 wa[4], xa[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t c = base + 64u * i + lane;
+            const bool in = c < chunks;
+            wa[i] = in ? bv[c] : u32x4{0u, 0u, 0u, 0u};
+            xa[i] = in ? av[c] : u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            float part = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j) {
+                part = __builtin_fmaf(bf16_to_f32(xa[i][j] & 0xffffu), bf16_to_f32(wa[i][j] & 0xffffu), part);
+                part = __builtin_fmaf(bf16_to_f32(xa[i][j] >> 16), bf16_to_f32(wa[i][j] >> 16), part);
+            }
+            total += part;
+        }
+    }
+    return __uint_as_float(wave_reduce_u32(__float_as_uint(total), [](uint32_t x, uint32_t y) {
+        return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
+    }));
+}
+
+// C[n] = a . B[n], four waves (rows) per workgroup.
+template <DenseOut kOut>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ a,
+                                                   const uint16_t* __restrict__ b, uint32_t n,
+                                                   uint32_t k, float* __restrict__ c_f32,
+                                                   uint16_t* __restrict__ c_bf16, float divisor,
+                                                   float scale) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row = blockIdx.x * 4u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (row >= n) return;
+    const float acc = wave_dot_bf16(a, b + static_cast<size_t>(row) * k, k, lane);
+    if (lane != 0u) return;
+    if constexpr (kOut == DenseOut::kF32)
+        c_f32[row] = acc;
+    else
+        c_bf16[row] = static_cast<uint16_t>(dense_epilogue(kOut, acc, divisor, scale));
+}
+
+// The shared expert's first half for one token: wave c < inter computes
+// channel c's g = bf16(x Wg[c]) and u = bf16(x Wu[c]) (both rows' loads in
+// flight together) and h = silu_multiply(g, u); wave `inter` computes the
+// scalar output gate bf16(x wo).  Two waves per workgroup.
+__global__ __launch_bounds__(128) void shared_gate_up_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w_gate,
+    const uint16_t* __restrict__ w_up, const uint16_t* __restrict__ w_out_gate, uint32_t inter,
+    uint16_t* __restrict__ g_out, uint16_t* __restrict__ u_out, uint16_t* __restrict__ h_out,
+    uint16_t* __restrict__ gate_out) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t c = blockIdx.x * 2u + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (c > inter) return;
+    if (c == inter) {
+        const float gate = wave_dot_bf16(x, w_out_gate, kHidden, lane);
+        if (lane == 0u) gate_out[0] = static_cast<uint16_t>(f32_to_bf16(gate));
+        return;
+    }
+    const float g = wave_dot_bf16(x, w_gate + static_cast<size_t>(c) * kHidden, kHidden, lane);
+    const float u = wave_dot_bf16(x, w_up + static_cast<size_t>(c) * kHidden, kHidden, lane);
+    if (lane != 0u) return;
+    const uint32_t g_bits = f32_to_bf16(g), u_bits = f32_to_bf16(u);
+    g_out[c] = static_cast<uint16_t>(g_bits);
+    u_out[c] = static_cast<uint16_t>(u_bits);
+    h_out[c] = static_cast<uint16_t>(silu_multiply(g_bits, u_bits));
+}
+
 }  // namespace
 
 namespace {
+
+// one activation row: the GEMV form (grids of up to 65535 workgroups)
+constexpr uint32_t kGemvMaxRows = 65535u * 4u;
 
 template <DenseOut kOut>
 void launch_dense_tiles(const uint16_t* a, const uint16_t* b, uint32_t m, uint32_t n, uint32_t k,
                         float* c_f32, uint16_t* c_bf16, float divisor, float scale,
                         hipStream_t stream) {
+    if (m == 1u && n <= kGemvMaxRows) {
+        gemv_kernel<kOut><<<(n + 3u) / 4u, 256, 0, stream>>>(a, b, n, k, c_f32, c_bf16, divisor,
+                                                             scale);
+        return;
+    }
     // short K with a 64 x 64 grid that fills the GPU: workgroup-shared
     // tiles read half the bytes per output of the K-split 32 x 32 tiles
     const uint32_t tiles64 = ((m + 63u) / 64u) * ((n + 63u) / 64u);
@@ -643,6 +740,8 @@ hipError_t launch_dense_gemm_act(const uint16_t* a, const uint16_t* b, uint32_t 
 
 size_t router_topk_workspace_bytes(uint32_t tokens) {
     constexpr uint32_t kBlocks = kExperts / 64u;
+    // one token: the GEMV's fp32 logits
+    if (tokens == 1u) return kExperts * sizeof(float);
     return static_cast<size_t>(tokens) * kBlocks * (kTopK * sizeof(uint64_t) + sizeof(uint32_t));
 }
 
@@ -650,6 +749,18 @@ hipError_t launch_router_topk(const uint16_t* hidden, const uint16_t* router, ui
                               uint32_t top_k, void* workspace, int32_t* ids, float* weights,
                               hipStream_t stream) {
     constexpr uint32_t kBlocks = kExperts / 64u;
+    if (tokens == 1u) {
+        // one token: a GEMM tile would waste 15 of its 16 rows, so the
+        // logits come from the GEMV (the same words q38m_moe_router_v1
+        // writes for one token) and the block top-k ranks them
+        float* logits = static_cast<float*>(workspace);
+        gemv_kernel<DenseOut::kF32><<<kExperts / 4u, 256, 0, stream>>>(
+            hidden, router, kExperts, kHidden, logits, nullptr, 1.0f, 1.0f);
+        hipError_t e = hipGetLastError();
+        return e == hipSuccess ? launch_topk(logits, ids, weights, 1u, kExperts, top_k, true,
+                                             stream)
+                               : e;
+    }
     uint64_t* cand = static_cast<uint64_t*>(workspace);
     uint32_t* block_max = reinterpret_cast<uint32_t*>(cand + static_cast<size_t>(tokens) * kBlocks * kTopK);
     router_select_kernel<<<dim3(kBlocks, (tokens + 15u) / 16u), 256, 0, stream>>>(
@@ -674,9 +785,14 @@ hipError_t launch_shared_expert(const uint16_t* hidden, const uint16_t* w_gate,
     uint16_t* g = static_cast<uint16_t*>(scratch);
     uint16_t* u = g + elements;
     uint16_t* h = u + elements;
-    const dim3 grid(inter / 32u, (tokens + 31u) / 32u);
-    shared_gate_up_kernel<<<grid, 256, 0, stream>>>(hidden, w_gate, w_up, w_out_gate, tokens,
-                                                    inter, g, u, h, shared_gate);
+    if (tokens == 1u) {
+        shared_gate_up_gemv_kernel<<<(inter + 2u) / 2u, 128, 0, stream>>>(
+            hidden, w_gate, w_up, w_out_gate, inter, g, u, h, shared_gate);
+    } else {
+        const dim3 grid(inter / 32u, (tokens + 31u) / 32u);
+        shared_gate_up_kernel<<<grid, 256, 0, stream>>>(hidden, w_gate, w_up, w_out_gate, tokens,
+                                                        inter, g, u, h, shared_gate);
+    }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess)
         e = launch_dense_gemm(h, w_down, tokens, kHidden, inter, nullptr, shared_output, stream);

@@ -11,7 +11,8 @@ outputs additionally within one bf16 step (2^-8 relative)."""
 import numpy as np
 import pytest
 
-from helpers import Layer, W, device, host, prefill, stream, synth_hidden, torch
+from helpers import (Layer, W, decode_fused, decode_scratch, device, host, prefill, stream,
+                     synth_hidden, torch)
 
 pytestmark = pytest.mark.gpu
 
@@ -49,13 +50,17 @@ def check_close(orc, got, a, b, out_bf16):
 
 
 # K-split 32 x 32 tiles (long K too: the hyper mix-down's 8192, and a
-# ragged odd-step K), and (K <= 1024 with at least 192 tiles of 64 x 64)
+# ragged odd-step K), (K <= 1024 with at least 192 tiles of 64 x 64)
 # workgroup-shared 64 x 64 tiles: ragged edges, a trailing half K chunk, a
-# single half chunk, the largest K of that form
+# single half chunk, the largest K of that form; and one activation row
+# (the GEMV form: the router and the shared down projection at one token,
+# a row count that is not a multiple of the workgroup's four, a K whose
+# last pass of chunks is partial, a single row)
 @pytest.mark.parametrize("m,n,k", [(40, 512, 2048), (512, 2048, 512), (1, 512, 2048),
                                    (33, 1, 2048), (64, 96, 64), (130, 70, 96),
                                    (1000, 1000, 160), (640, 1600, 32), (1024, 768, 1024),
-                                   (512, 2048, 320), (512, 320, 8192), (70, 100, 4128)])
+                                   (512, 2048, 320), (512, 320, 8192), (70, 100, 4128),
+                                   (1, 2048, 512), (1, 1001, 4128), (1, 1, 32), (1, 320, 8192)])
 @pytest.mark.parametrize("out_bf16", [False, True])
 def test_dense_gemm(q38m, orc, m, n, k, out_bf16):
     rng = np.random.default_rng(m * 7 + n * 3 + k)
@@ -139,10 +144,12 @@ def test_router_topk_fused(q38m, orc, tokens, top_k):
             assert list(row).index(300) == list(row).index(5) + 1
 
 
-def test_shared_expert(q38m, orc):
+@pytest.mark.parametrize("tokens", [40, 1])
+def test_shared_expert(q38m, orc, tokens):
+    """Tiled at 40 tokens, the GEMV form at one token."""
     t = torch()
-    rng = np.random.default_rng(9)
-    tokens, inter = 40, W.INTER
+    rng = np.random.default_rng(9 + tokens)
+    inter = W.INTER
     x = bf16_matrix(orc, rng, tokens, W.HIDDEN, 1.0)
     wg = bf16_matrix(orc, rng, inter, W.HIDDEN, 0.02)
     wu = bf16_matrix(orc, rng, inter, W.HIDDEN, 0.02)
@@ -172,15 +179,17 @@ def test_shared_expert(q38m, orc):
     check_close(orc, host(sg, np.uint16).reshape(tokens, 1), x, wo, True)
 
 
-def test_moe_block_router_routed_shared(q38m, orc):
+@pytest.mark.parametrize("tokens", [64, 1])
+def test_moe_block_router_routed_shared(q38m, orc, tokens):
     """The whole MoE block on the device -- router logits, the routed
     experts, the shared expert and the gated combine -- equals the oracle's
-    step on the same logits and shared inputs, bit for bit."""
+    step on the same logits and shared inputs, bit for bit; at one token
+    (the GEMV router and shared expert) through the decode entry point as
+    well as the prefill one."""
     t = torch()
     gfmt, dfmt = W.layer_policy(2, 0)
     layer = Layer(q38m, orc, W.CONFIGS[2]["seed"], 0, gfmt, dfmt)
-    rng = np.random.default_rng(17)
-    tokens = 64
+    rng = np.random.default_rng(17 + tokens)
     hidden = synth_hidden(q38m, 17, 1, tokens)
     router = device(bf16_matrix(orc, rng, W.EXPERTS, W.HIDDEN, 0.02))
     weights = [device(bf16_matrix(orc, rng, r, c, 0.02)) for r, c in
@@ -201,3 +210,13 @@ def test_moe_block_router_routed_shared(q38m, orc):
                   logits=host(logits, np.float32), shared_output=host(so, np.uint16),
                   shared_gate=host(sg, np.uint16))
     assert np.array_equal(host(out, np.uint16), ref["output"])
+    if tokens == 1:
+        dec = decode_fused(q38m, layer, hidden, logits, decode_scratch(q38m), shared=(so, sg))
+        assert np.array_equal(host(dec, np.uint16).ravel(), ref["output"].ravel())
+        # the logits, shared output and gate themselves against float64
+        check_close(orc, host(logits, np.float32).reshape(1, W.EXPERTS),
+                    host(hidden, np.uint16).reshape(1, W.HIDDEN), host(router, np.uint16)
+                    .reshape(W.EXPERTS, W.HIDDEN), False)
+        check_close(orc, host(sg, np.uint16).reshape(1, 1),
+                    host(hidden, np.uint16).reshape(1, W.HIDDEN),
+                    host(weights[3], np.uint16).reshape(1, W.HIDDEN), True)
