@@ -22,11 +22,14 @@ rocprofv3 --pmc (config-2 slab; chunk workloads) and the line carries
 the counter-derived MFMA busy fraction and int8 rate of the headline and
 chunk GEMMs beside the algorithmic ones (skipped with --no-counters or
 without rocprofv3).  --pmc-report {slab,chunk,decode,dense} prints the full
-counter and HBM-traffic tables of one workload instead.
+counter and HBM-traffic tables of one workload instead; --phase-report
+decode prints the batch-1 decode's per-phase timeline from the timing
+build (libq38m_timed.so).  The JSON line ends with the roofline, the CPU
+baseline and a summary of the decode half of the metric.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
        [--no-quantizer] [--no-dense] [--no-chunks] [--no-stack] [--no-hyper]
-       [--no-formats] [--no-counters] [--pmc-report WORKLOAD]
+       [--no-formats] [--no-counters] [--pmc-report WORKLOAD] [--phase-report decode]
 """
 import argparse
 import collections
@@ -82,6 +85,11 @@ PMC_WORKLOADS = {
              "--steps 10 --warmup 2",
 }
 VALU_CYCLES = 4  # issue cycles of one non-packed wave64 VALU instruction on a SIMD
+# Algorithmic bytes per launch of the decode kernels (config 3: ten routes,
+# W4 g32 fp16-scaled gate/up, W8 per-channel down): the selected experts'
+# weights and scale words.
+DECODE_KERNEL_BYTES = {"decode_gate_up_kernel": 10 * (1048576 + 131072),
+                       "decode_down_kernel": 10 * (1048576 + 4096)}
 
 
 def _short_kernel(name):
@@ -113,9 +121,15 @@ def pmc_run(counters, workload, extra=""):
         try:
             rc = proc.wait(timeout=300)
         except subprocess.TimeoutExpired:
-            os.killpg(proc.pid, signal.SIGKILL)
+            rc = None
+        finally:
+            # the profiler runs in its own session: whatever it started there
+            # ends with it, whether it exited or timed out
+            try:
+                os.killpg(proc.pid, signal.SIGKILL)
+            except ProcessLookupError:
+                pass
             proc.wait()
-            return None
         if rc != 0:
             return None
         per = collections.defaultdict(lambda: collections.defaultdict(float))
@@ -318,7 +332,24 @@ def pmc_report(workload, traffic_dir=None):
             # the headline slab's grids have the most launches
             if base not in traffic or len(td or []) > traffic[base][0]:
                 traffic[base] = (len(td or []), fb, wb)
-    if traffic_dir:
+        if workload == "decode" and base in DECODE_KERNEL_BYTES and td and fb and wb:
+            if base not in traffic or len(td) > traffic[base][0]:
+                traffic[base] = (len(td), fb, wb, statistics.fmean(td))
+    if traffic_dir and workload == "decode":
+        kernels = {}
+        for base, (launches, fb, wb, us) in traffic.items():
+            alg = DECODE_KERNEL_BYTES[base]
+            kernels[base] = {"launches": launches, "avg_us": round(us, 3),
+                             "algorithmic_bytes": alg, "fetch_bytes": round(fb),
+                             "write_bytes": round(wb), "fetch_over_algorithmic": round(fb / alg, 3),
+                             "GBps": round(alg / (us * 1e-6) / 1e9, 1),
+                             "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+        with open(os.path.join(traffic_dir, "decode_kernels_config3.json"), "w") as fh:
+            json.dump({"workload": "config3 decode (" + PMC_WORKLOADS["decode"] + ")",
+                       "kernels": kernels, "fetch_scale": fs and round(fs, 4),
+                       "write_scale": ws and round(ws, 4),
+                       "source": "profiles/counters_decode_config3.md"}, fh, indent=1)
+    elif traffic_dir:
         for base, (_, fb, wb) in traffic.items():
             with open(os.path.join(traffic_dir, f"{base}_config2_traffic.json"), "w") as fh:
                 json.dump({"kernel": base, "workload": "config2",
@@ -349,15 +380,22 @@ def main():
     parser.add_argument("--pmc-report", choices=["slab", "chunk", "decode", "dense"],
                         help="print the trace and counter report for one workload (markdown) "
                              "and exit")
+    parser.add_argument("--phase-report", choices=["decode"],
+                        help="print the batch-1 decode phase table from the timing build "
+                             "(libq38m_timed.so) and exit")
     parser.add_argument("--traffic-json-dir", default=None,
                         help="with --pmc-report slab: also write the headline kernels' "
-                             "<kernel>_config2_traffic.json files into this directory")
+                             "<kernel>_config2_traffic.json files into this directory; with "
+                             "--pmc-report decode: decode_kernels_config3.json")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="after the run, copy a buffer of this many MiB 5 times (a plain "
                              "copy kernel of known size, to scale rocprofv3 FETCH/WRITE_SIZE)")
     args = parser.parse_args()
     if args.pmc_report:
         print(pmc_report(args.pmc_report, args.traffic_json_dir), flush=True)
+        return
+    if args.phase_report:
+        print(phase_report(), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the MoE data plane is built and measured on a single "
@@ -584,17 +622,68 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
                                               T)
-    print(json.dumps(result), flush=True)
+    print(json.dumps(ordered_line(result)), flush=True)
 
 
-def bench_decode(q38m, W, torch, tokens):
-    """Config 3: one token through 48 MoE layers (W4 g32 gate/up + W8 down),
-    a fresh router draw per layer, residual add between layers, through the
-    fused q38m_moe_decode_v1 (top-k + experts + residual, two launches per
-    layer).  Timed eagerly and as one HIP graph holding every layer of
-    `tokens` tokens; reports HBM GB/s over the selected experts' weights."""
-    spec = W.CONFIGS[3]
-    seed, layers = spec["seed"], spec["layers"]
+def decode_summary(dec):
+    """The decode half of the metric in a few fields: the graph-replayed
+    config-3 layer, its floor, the whole MoE block at tokens == 1 and the
+    decode kernels' rocprof durations (profiles/decode_kernels_config3.json,
+    written by --pmc-report decode)."""
+    s = {"workload": "config3: 1 token x 48 layers, top-10 of 512, W4 g32 gate/up + W8 down",
+         "us_per_layer": dec["us_per_layer"], "GBps": dec["GBps"], "hbm_frac": dec["hbm_frac"],
+         "floor_us_per_layer": dec["floor"]["layer_us"],
+         "two_launch_floor_us": dec["floor"]["two_launch_us"],
+         "floor_over_measured": round(dec["floor"]["layer_us"] / dec["us_per_layer"], 4)}
+    block = dec.get("moe_block")
+    if block:
+        s["moe_block_us_per_layer"] = block["us_per_layer"]
+        s["moe_block_hbm_frac"] = block["hbm_frac"]
+        s["router_t1_us"] = block["router_t1"]["us"]
+        s["shared_expert_t1_us"] = block["shared_expert_t1"]["us"]
+    path = os.path.join(ROOT, "profiles", "decode_kernels_config3.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            kernels = json.load(f)["kernels"]
+        if kernels:
+            name = max(kernels, key=lambda k: kernels[k]["avg_us"])
+            k = kernels[name]
+            s["dominant_kernel"] = {"kernel": name, "avg_us": k["avg_us"],
+                                    "algorithmic_bytes": k["algorithmic_bytes"],
+                                    "GBps": k["GBps"], "frac": k["hbm_frac"],
+                                    "fetch_over_algorithmic": k["fetch_over_algorithmic"],
+                                    "source": "profiles/decode_kernels_config3.json"}
+    return s
+
+
+def ordered_line(result):
+    """The bench line with the contract's fields first, the detail sections
+    next, and the roofline, the CPU baseline and the decode summary last (a
+    reader of the line's tail sees both halves of the metric)."""
+    head = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step",
+            "higher_is_better", "scaling", "vs_baseline", "dtype", "data", "config")
+    line = {k: result[k] for k in head if k in result}
+    cpu = result.get("cpu_baseline")
+    if cpu and "per_config" in cpu:
+        cpu = dict(cpu)
+        result["cpu_baseline_per_config"] = cpu.pop("per_config")
+    if "decode" in result:
+        result["decode_detail"] = result["decode"]
+    for k, v in result.items():
+        if k not in head and k not in ("roofline", "cpu_baseline", "decode"):
+            line[k] = v
+    line["roofline"] = result["roofline"]
+    if cpu:
+        line["cpu_baseline"] = cpu
+    if "decode" in result:
+        line["decode"] = decode_summary(result["decode"])
+    return line
+
+
+def decode_stack(q38m, W, layers):
+    """Config 3's resident layers: W4 g32 gate/up (paired MFMA16 layout) and
+    W8 per-channel down, distinct seeded weights per layer."""
+    seed = W.CONFIGS[3]["seed"]
     fmt = {4: q38m.FORMAT_W4_SYM, 8: q38m.FORMAT_W8_SYM}
     stack = []
     for layer in range(layers):
@@ -607,6 +696,121 @@ def bench_decode(q38m, W, torch, tokens):
         dn = q38m.repack(dn_rm)
         del dn_rm
         stack.append((gu, dn))
+    return stack
+
+
+GATE_UP_PHASES = ("start", "token row and logits arrived", "top-k done", "weight loads issued",
+                  "token quantised", "weights arrived", "group sums formed",
+                  "group sums exchanged (all waves)", "fp32 chains done", "end",
+                  "top-k level 1 done (first wave)", "top-k lists joined", "top-k level 2 done")
+DOWN_PHASES = ("start", "ids arrived, weight loads issued", "mid rows quantised",
+               "weights arrived", "route partial formed", "route partials in LDS (all waves)",
+               "end")
+
+
+def phase_report(tokens=8):
+    """Markdown table of the batch-1 decode's phases (config 3, 48 layers,
+    one graph of `tokens` tokens) from the timing build libq38m_timed.so
+    (include/q38m_phase.h): per phase, the median over a launch's 256
+    workgroups of the first wave's clock read, in us from the gate/up
+    launch's first workgroup start, then the median over every layer and
+    token.  The timing build's final state is checked against the product
+    library's."""
+    import numpy as np
+    import torch
+    q38m = load("q38m_amd", os.path.join(PACKAGE_DIR, "__init__.py"), PACKAGE_DIR)
+    W = load("q38m_workloads", os.path.join(PACKAGE_DIR, "workloads.py"))
+    torch.cuda.set_device(0)
+    spec = W.CONFIGS[3]
+    seed, layers = spec["seed"], spec["layers"]
+    stack = decode_stack(q38m, W, layers)
+    logits = torch.empty(tokens, layers, W.EXPERTS, dtype=torch.float32, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_F32, seed, 2, logits.numel(), logits)
+    state = torch.empty(layers + 1, W.HIDDEN, dtype=torch.int16, device="cuda")
+    q38m.synth_fill(q38m.SYNTH_NORMAL_BF16, seed, 1, W.HIDDEN, state[0])
+    first = state[0].clone()
+    scratch = torch.zeros(q38m.lib().q38m_moe_decode_scratch_bytes(), dtype=torch.uint8,
+                          device="cuda")
+
+    def run(call):
+        sh = torch.cuda.current_stream().cuda_stream
+        for t in range(tokens):
+            for layer, (gu, dn) in enumerate(stack):
+                call("q38m_moe_decode_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                     state[layer].data_ptr(), logits[t, layer].data_ptr(), W.TOPK, None, None,
+                     state[layer].data_ptr(), scratch.data_ptr(), state[layer + 1].data_ptr(),
+                     sh, 0)
+
+    run(q38m.call)
+    torch.cuda.synchronize()
+    product_final = state[layers].clone()
+    calls = tokens * layers
+    records = torch.zeros(calls * 512 * ctypes.sizeof(q38m.PhaseRecord), dtype=torch.uint8,
+                          device="cuda")
+    timed = q38m.timed_lib()
+    if timed.q38m_phase_log_v1(records.data_ptr(), calls * 512, 0) != q38m.OK:
+        raise RuntimeError("q38m_phase_log_v1 failed")
+    state[0].copy_(first)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(q38m.call_timed)
+    for _ in range(3):
+        state[0].copy_(first)
+        graph.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(state[layers], product_final):
+        raise RuntimeError("timing build's decode differs from the product library's")
+    timed.q38m_phase_log_v1(None, 0, 0)
+    rec = np.frombuffer(records.cpu().numpy().tobytes(), dtype=np.dtype(
+        [("stamp", "<u8", 16), ("kernel", "<u4"), ("block", "<u4"), ("call", "<u4"),
+         ("valid", "<u4")])).reshape(calls, 2, 256)
+    if not rec["valid"].all():
+        raise RuntimeError("phase log incomplete")
+    t0 = rec["stamp"][:, 0, :, 0].min(axis=1).astype(np.int64)  # per call
+    rel = (rec["stamp"].astype(np.int64) - t0[:, None, None, None]) * 10 / 1000.0  # us
+    layer_us = (rel[:, 1, :, len(DOWN_PHASES) - 1].max(axis=1))
+    lines = ["# Batch-1 decode phases (config 3)", "",
+             "Command (repository root on the GPU box): `python3 bench.py --phase-report decode`.",
+             "", f"The timing build `libq38m_timed.so` (the product library with "
+             "`-DQ38M_PHASE_TIMESTAMPS` in the decode kernels, `make timed`) runs "
+             f"{tokens} tokens x {layers} layers of config 3 (W4 g32 gate/up, W8 per-channel "
+             "down, fresh router draw per layer, residual add) as one HIP graph; its final state "
+             "equals the product library's bit for bit.  Each workgroup's first wave reads "
+             "s_memrealtime (100 MHz) at the phase boundaries.  Per phase: the median over a "
+             "launch's 256 workgroups, in us from that layer's first gate/up workgroup start, "
+             f"then the median over the {calls} layer calls; `last` is the median of the "
+             "launch's latest workgroup.", "",
+             "| kernel | phase | median us | last us |", "|---|---|---:|---:|"]
+    summary = {}
+    for k, names in ((0, GATE_UP_PHASES), (1, DOWN_PHASES)):
+        for i, name in enumerate(names):
+            med = float(np.median(np.median(rel[:, k, :, i], axis=1)))
+            last = float(np.median(rel[:, k, :, i].max(axis=1)))
+            kname = "decode_gate_up_kernel" if k == 0 else "decode_down_kernel"
+            lines.append(f"| {kname} | {name} | {med:.2f} | {last:.2f} |")
+            summary[f"{k}:{i}"] = med
+    gu_end = rel[:, 0, :, 9].max(axis=1)
+    dn_start = rel[:, 1, :, 0].min(axis=1)
+    period = np.diff(t0) * 10 / 1000.0
+    layer_period = period[(np.arange(calls - 1) + 1) % layers != 0]  # within a token
+    lines += ["", f"Layer (first gate/up start to last down end), median over calls: "
+              f"{float(np.median(layer_us)):.2f} us.  Launch boundaries (medians): gate/up's last "
+              f"workgroup end to down's first start {float(np.median(dn_start - gu_end)):.2f} us; "
+              "down's last workgroup end to the next layer's first gate/up start "
+              f"{float(np.median(layer_period - layer_us[:-1][(np.arange(calls - 1) + 1) % layers != 0])):.2f}"
+              f" us; layer-to-layer period {float(np.median(layer_period)):.2f} us."]
+    return "\n".join(lines)
+
+
+def bench_decode(q38m, W, torch, tokens):
+    """Config 3: one token through 48 MoE layers (W4 g32 gate/up + W8 down),
+    a fresh router draw per layer, residual add between layers, through the
+    fused q38m_moe_decode_v1 (top-k + experts + residual, two launches per
+    layer).  Timed eagerly and as one HIP graph holding every layer of
+    `tokens` tokens; reports HBM GB/s over the selected experts' weights."""
+    spec = W.CONFIGS[3]
+    seed, layers = spec["seed"], spec["layers"]
+    stack = decode_stack(q38m, W, layers)
     resident = sum(gu.nbytes + dn.nbytes for gu, dn in stack)
     # one fresh router draw per (token, layer); the first two tokens warm up
     logits = torch.empty(tokens + 2, layers, W.EXPERTS, dtype=torch.float32, device="cuda")
@@ -658,17 +862,124 @@ def bench_decode(q38m, W, torch, tokens):
 
     bytes_token = layers * W.TOPK * W.algorithmic_bytes_per_expert(W.W4, W.W8)
 
-    def rate(ms):
-        gbps = bytes_token / (ms * 1e-3) / 1e9
+    def rate(ms, nbytes=bytes_token):
+        gbps = nbytes / (ms * 1e-3) / 1e9
         return {"us_per_token": round(ms * 1e3, 2), "us_per_layer": round(ms * 1e3 / layers, 3),
                 "GBps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
+    def graph_ms(fn, count):
+        """ms per call of fn() (which launches `count` items) replayed as one graph"""
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(replays):
+            g.replay()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / (replays * count)
+
+    # the launch floor: two dependent single-workgroup launches per layer in
+    # a graph (no memory traffic), the kernel-boundary cost a two-launch
+    # layer pays before any of its bytes
+    tick = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def empty_layers():
+        for _ in range(layers):
+            tick.add_(1)
+            tick.add_(1)
+
+    launch_floor_us = graph_ms(empty_layers, layers) * 1e3
     graph_rate = rate(ms_graph)
-    return {"workload": spec["name"], "tokens": tokens, "layers": layers,
-            "resident_weight_GB": round(resident / 1e9, 2),
-            "algorithmic_bytes_per_token": bytes_token, "launches_per_layer": 2,
-            "entry_point": "q38m_moe_decode_v1", **graph_rate, "mode": "hip_graph",
-            "eager": rate(ms_eager)}
+    hbm_floor_us = bytes_token / layers / (HBM_PEAK_GBPS * 1e3)
+    out = {"workload": spec["name"], "tokens": tokens, "layers": layers,
+           "resident_weight_GB": round(resident / 1e9, 2),
+           "algorithmic_bytes_per_token": bytes_token, "launches_per_layer": 2,
+           "entry_point": "q38m_moe_decode_v1", **graph_rate, "mode": "hip_graph",
+           "eager": rate(ms_eager),
+           "floor": {"two_launch_us": round(launch_floor_us, 3),
+                     "hbm_us": round(hbm_floor_us, 3),
+                     "layer_us": round(launch_floor_us + hbm_floor_us, 3),
+                     "note": "two dependent empty launches per layer in a graph (measured here) "
+                             "+ the ten experts' bytes at 8 TB/s"}}
+
+    # the whole MoE block of a decode step: router GEMV over the bf16 router,
+    # the bf16 shared expert and the routed experts with the gated shared
+    # term and the residual (cuda_backend.cu:1516-1605 at tokens == 1)
+    dense = []
+    rng = torch.Generator(device="cuda").manual_seed(spec["seed"])
+
+    def bf16_weight(rows, cols, scale):
+        return (torch.randn(rows, cols, generator=rng, device="cuda") * scale).to(
+            torch.bfloat16).view(torch.int16)
+
+    for _ in range(layers):
+        dense.append((bf16_weight(W.EXPERTS, W.HIDDEN, 0.02), bf16_weight(W.INTER, W.HIDDEN, 0.02),
+                      bf16_weight(W.INTER, W.HIDDEN, 0.02), bf16_weight(W.HIDDEN, W.INTER, 0.02),
+                      bf16_weight(1, W.HIDDEN, 0.02)))
+    dense_bytes = 2 * (W.EXPERTS * W.HIDDEN + 3 * W.INTER * W.HIDDEN + W.HIDDEN)
+    block_logits = torch.empty(layers, W.EXPERTS, dtype=torch.float32, device="cuda")
+    sscratch = torch.empty(q38m.lib().q38m_moe_shared_expert_scratch_bytes(1, W.INTER) // 2 + 64,
+                           dtype=torch.int16, device="cuda")
+    s_out = torch.empty(layers, W.HIDDEN, dtype=torch.int16, device="cuda")
+    s_gate = torch.empty(layers, 8, dtype=torch.int16, device="cuda")
+
+    def block_token():
+        sh = torch.cuda.current_stream().cuda_stream
+        for layer, (gu, dn) in enumerate(stack):
+            router, wg, wu, wd, wo = dense[layer]
+            q38m.call("q38m_moe_router_v1", state[layer].data_ptr(), router.data_ptr(), 1,
+                      W.HIDDEN, block_logits[layer].data_ptr(), sh, 0)
+            q38m.call("q38m_moe_shared_expert_v1", state[layer].data_ptr(), wg.data_ptr(),
+                      wu.data_ptr(), wd.data_ptr(), wo.data_ptr(), 1, W.HIDDEN, W.INTER,
+                      sscratch.data_ptr(), s_out[layer].data_ptr(), s_gate[layer].data_ptr(), sh,
+                      0)
+            q38m.call("q38m_moe_decode_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
+                      state[layer].data_ptr(), block_logits[layer].data_ptr(), W.TOPK,
+                      s_out[layer].data_ptr(), s_gate[layer].data_ptr(), state[layer].data_ptr(),
+                      scratch.data_ptr(), state[layer + 1].data_ptr(), sh, 0)
+
+    def router_only():
+        sh = torch.cuda.current_stream().cuda_stream
+        for layer in range(layers):
+            q38m.call("q38m_moe_router_v1", state[layer].data_ptr(), dense[layer][0].data_ptr(), 1,
+                      W.HIDDEN, block_logits[layer].data_ptr(), sh, 0)
+
+    def shared_only():
+        sh = torch.cuda.current_stream().cuda_stream
+        for layer in range(layers):
+            _, wg, wu, wd, wo = dense[layer]
+            q38m.call("q38m_moe_shared_expert_v1", state[layer].data_ptr(), wg.data_ptr(),
+                      wu.data_ptr(), wd.data_ptr(), wo.data_ptr(), 1, W.HIDDEN, W.INTER,
+                      sscratch.data_ptr(), s_out[layer].data_ptr(), s_gate[layer].data_ptr(), sh,
+                      0)
+
+    block_token()
+    torch.cuda.synchronize()
+    block_us = graph_ms(block_token, layers) * 1e3
+    router_us = graph_ms(router_only, layers) * 1e3
+    shared_us = graph_ms(shared_only, layers) * 1e3
+    block_bytes = W.TOPK * W.algorithmic_bytes_per_expert(W.W4, W.W8) + dense_bytes
+
+    def dense_rate(us, nbytes):
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"us": round(us, 3), "bytes": nbytes, "GBps": round(gbps, 1),
+                "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+    out["moe_block"] = {
+        "what": "per layer: q38m_moe_router_v1 (T=1) + q38m_moe_shared_expert_v1 (T=1) + "
+                "q38m_moe_decode_v1 with the gated shared term and residual, 48 layers of "
+                "distinct weights in one graph",
+        "us_per_layer": round(block_us, 3),
+        "bytes_per_layer": block_bytes,
+        "GBps": round(block_bytes / (block_us * 1e-6) / 1e9, 1),
+        "hbm_frac": round(block_bytes / (block_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "router_t1": dense_rate(router_us, 2 * W.EXPERTS * W.HIDDEN + 4 * W.HIDDEN + 4 * W.EXPERTS),
+        "shared_expert_t1": dense_rate(shared_us, 2 * (3 * W.INTER * W.HIDDEN + W.HIDDEN) +
+                                       4 * W.HIDDEN + 2)}
+    return out
 
 
 # The reference artifact's routed-expert number formats (tools/
