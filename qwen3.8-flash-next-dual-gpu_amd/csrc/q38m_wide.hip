@@ -1080,6 +1080,16 @@ void gate_up_w8_wide_kernel(
 
 // ---- down -------------------------------------------------------------------
 
+// The route outputs of a chunk (fp32 [R][H], 2.68 GB for a config-5 layer)
+// are written once here and read once by the combine, far more than the
+// L2s hold: stored with ordinary stores they are allocated in L2 and evict
+// the expert weights and mid rows that an expert's later tasks re-read
+// (the W8 down kernel fetched 1.44x its unique bytes), so they are stored
+// non-temporally.
+__device__ __forceinline__ void store_route_output(float* p, float v) {
+    __builtin_nontemporal_store(v, p);
+}
+
 // Down, W8 per output channel, over a task of up to 128 rows: the mid rows
 // (contiguous in packed order) are staged once into LDS as [K block][row
 // tile][lane] 16-byte MFMA fragments.  Each wave owns kTilesPerWave
@@ -1182,8 +1192,9 @@ __device__ __forceinline__ void down_w8_wide_rows(const uint4* __restrict__ wt,
             float* dst = out + static_cast<size_t>(p0 + row) * H + tile0 * 16u + n;
 #pragma unroll
             for (uint32_t t = 0; t < kTilesPerWave; ++t)
-                dst[16u * t] = kPerChannel ? (static_cast<float>(acc[t][r][i]) * ws[t][0]) * sm
-                                           : y[t][r][i] * sm;
+                store_route_output(dst + 16u * t,
+                                   kPerChannel ? (static_cast<float>(acc[t][r][i]) * ws[t][0]) * sm
+                                               : y[t][r][i] * sm);
         }
 }
 
@@ -1350,7 +1361,8 @@ __device__ __forceinline__ void down_w4_wide_rows(const uint4* __restrict__ wt,
             for (uint32_t i = 0; i < 4u; ++i) {
                 const uint32_t row = 16u * r + lane_row + i;
                 if (row >= rows) continue;
-                out[static_cast<size_t>(p0 + row) * H + channel] = y[r][i] * row_scale[row];
+                store_route_output(out + static_cast<size_t>(p0 + row) * H + channel,
+                                   y[r][i] * row_scale[row]);
             }
     }
 }
@@ -1603,8 +1615,8 @@ void down_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __restri
             const uint32_t row = 16u * t + 4u * qh + i;
             if (row >= rows) continue;
             float* dst = out + static_cast<size_t>(p0 + row) * H + channel;
-            dst[0] = y[t][0][i] * row_scale[row];
-            dst[16] = y[t][1][i] * row_scale[row];
+            store_route_output(dst, y[t][0][i] * row_scale[row]);
+            store_route_output(dst + 16, y[t][1][i] * row_scale[row]);
         }
     }
 }
