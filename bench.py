@@ -612,6 +612,8 @@ def main():
                 k: wide[k] for k in ("avg_us", "mfma_busy_frac", "int8_peak_frac_counter",
                                      "fp16_peak_frac_counter", "valu_insts_per_mfma",
                                      "valu_issue_share_est")}
+        if wide and "config5_stack" in result:
+            result["config5_stack"]["contract_ceilings"] = contract_ceilings(wide)
         slab_ops = [counters[k]["int8_ops_counter"] for k in
                     ("gate_up_w4_kernel (config 2 slab)", "down_w8_kernel (config 2 slab)")
                     if counters and k in counters]
@@ -623,6 +625,26 @@ def main():
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,
                                               T)
     print(json.dumps(ordered_line(result)), flush=True)
+
+
+def contract_ceilings(gate_up):
+    """What the int8 contract lets the config-5 W4 g32 GEMMs reach: they run
+    its products exactly on fp16 MFMA (v_mfma_f32_16x16x32_f16, half the
+    int8 MAC rate), and every 32-wide group of every output element needs
+    one fp32 fma of the contract's chain y = fmaf((float)acc_g, s_g, y) on
+    the VALU -- 4 wave64 instructions (16 VALU cycles) per 16-cycle MFMA.
+    chain_only: the chain alone already fills the VALU at full fp16 MFMA
+    rate, i.e. half the int8 peak; valu_issue: the kernel's measured VALU
+    instructions per MFMA (counters) over the same 16-cycle budget."""
+    per_mfma = gate_up["valu_insts_per_mfma"]
+    fp16_over_int8 = BF16_PEAK_TFLOPS / INT8_PEAK_TOPS
+    return {"kernel": "gate_up_w4g32_f16_kernel", "mfma_type": "fp16",
+            "chain_only_int8_frac": round(fp16_over_int8 * min(1.0, 16.0 / (4 * VALU_CYCLES)), 4),
+            "valu_insts_per_mfma_counter": per_mfma,
+            "valu_issue_int8_frac": round(fp16_over_int8 * min(1.0, 16.0 / (per_mfma * VALU_CYCLES)), 4),
+            "achieved_int8_frac_counter": gate_up["int8_peak_frac_counter"],
+            "note": "int8 peak fractions; the W4 g32 kernels run the int8 contract on fp16 "
+                    "MFMA (exact), whose dense peak is half the int8 one"}
 
 
 def decode_summary(dec):

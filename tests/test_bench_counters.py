@@ -92,3 +92,30 @@ def test_counter_sets_fit_one_pass(bench):
         assert sum(n.startswith("SQ_") for n in names) <= 8
         assert sum(n.startswith("GRBM_") for n in names) <= 2
         assert len(set(names)) == len(names)
+
+
+def test_contract_ceilings(bench):
+    """The chain alone (4 VALU per fp16 MFMA) caps the W4 g32 path at half
+    the int8 peak; 8 VALU per MFMA halves that again."""
+    c = bench.contract_ceilings({"valu_insts_per_mfma": 8.0, "int8_peak_frac_counter": 0.15})
+    assert c["chain_only_int8_frac"] == 0.5
+    assert c["valu_issue_int8_frac"] == 0.25
+    assert c["mfma_type"] == "fp16"
+    assert bench.contract_ceilings({"valu_insts_per_mfma": 2.0,
+                                    "int8_peak_frac_counter": 0.1})["valu_issue_int8_frac"] == 0.5
+
+
+def test_ordered_line_ends_with_both_halves_of_the_metric(bench):
+    result = {"metric": "m", "value": 1.0, "unit": "tok/s", "config": {}, "extra": 1,
+              "roofline": {"frac": 0.7},
+              "cpu_baseline": {"value": 2.0, "per_config": {"config1": {}}},
+              "decode": {"us_per_layer": 10.0, "GBps": 2000.0, "hbm_frac": 0.25,
+                         "floor": {"layer_us": 6.0, "two_launch_us": 3.2}}}
+    line = bench.ordered_line(result)
+    keys = list(line)
+    assert keys[:4] == ["metric", "value", "unit", "config"]
+    assert keys[-3:] == ["roofline", "cpu_baseline", "decode"]
+    assert "per_config" not in line["cpu_baseline"]
+    assert line["cpu_baseline_per_config"] == {"config1": {}}
+    assert line["decode_detail"]["us_per_layer"] == 10.0
+    assert line["decode"]["floor_over_measured"] == 0.6
