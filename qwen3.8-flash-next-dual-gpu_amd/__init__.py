@@ -16,7 +16,9 @@ import ctypes
 import os
 
 PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PACKAGE_DIR, "libq38m.so")
+# Q38M_LIB_PATH names another build of the same library (the host-sanitized
+# one of the ABI tests); there is no fallback either way.
+LIB_PATH = os.environ.get("Q38M_LIB_PATH") or os.path.join(PACKAGE_DIR, "libq38m.so")
 
 OK = 0
 ERR_INVALID_ARGUMENT = 1
@@ -203,6 +205,16 @@ PHASE_SIGNATURES = {
 }
 
 
+# The checked build (include/q38m_checked.h): the product entry points with
+# the device index checks compiled in, plus their status word.
+CHECKED_LIB_PATH = os.path.join(PACKAGE_DIR, "libq38m_checked.so")
+CHECKED_SIGNATURES = {"q38m_checked_status_v1": (_INT, [_P, _INT, _INT])}
+CHECK_EXPERT = 1
+CHECK_TASK_ROWS = 2
+CHECK_ROUTE = 4
+CHECK_TOKEN = 8
+
+
 class PhaseRecord(ctypes.Structure):
     _fields_ = [("stamp", ctypes.c_uint64 * 16), ("kernel", ctypes.c_uint32),
                 ("block", ctypes.c_uint32), ("call", ctypes.c_uint32), ("valid", ctypes.c_uint32)]
@@ -211,6 +223,7 @@ class PhaseRecord(ctypes.Structure):
 _lib = None
 _selftest_lib = None
 _timed_lib = None
+_checked_lib = None
 
 
 def _open(path, signatures):
@@ -260,9 +273,34 @@ def _check(rc):
     raise DeviceError(message)
 
 
+def checked_lib():
+    """Loads libq38m_checked.so, the checked build (its own copy of every
+    entry point, with the device index checks compiled in)."""
+    global _checked_lib
+    if _checked_lib is None:
+        _checked_lib = _open(CHECKED_LIB_PATH, {**SIGNATURES, **CHECKED_SIGNATURES})
+    return _checked_lib
+
+
 def call(name, *args):
     """Calls an int-returning entry point and raises on a non-OK status."""
     _check(getattr(lib(), name)(*args))
+
+
+def call_checked(name, *args):
+    """Calls an entry point of the checked build and raises on a non-OK status."""
+    handle = checked_lib()
+    rc = getattr(handle, name)(*args)
+    if rc != OK:
+        message = handle.q38m_last_error().decode(errors="replace")
+        raise (InvalidArgument if rc == ERR_INVALID_ARGUMENT else DeviceError)(message)
+
+
+def checked_status(reset=True, device=0):
+    """The checked build's status bits (CHECK_*) since the last reset."""
+    word = ctypes.c_uint32(0)
+    call_checked("q38m_checked_status_v1", ctypes.byref(word), 1 if reset else 0, device)
+    return word.value
 
 
 def call_selftest(name, *args):

@@ -15,6 +15,26 @@
 #include <initializer_list>
 #include <mutex>
 
+#ifdef Q38M_CHECKED
+#include <vector>
+
+#include "q38m_checked.h"
+
+namespace q38m {
+using CheckedReader = hipError_t (*)(uint32_t*, int, hipStream_t);
+// every translation unit's status-word reader (q38m_device.h), registered
+// at load
+std::vector<CheckedReader>& checked_readers() {
+    static std::vector<CheckedReader> readers;
+    return readers;
+}
+bool register_checked_status(CheckedReader read) {
+    checked_readers().push_back(read);
+    return true;
+}
+}  // namespace q38m
+#endif
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -922,5 +942,28 @@ int q38m_hyper_prepare_v1(const uint16_t* hyper, const uint16_t* norm_weight,
                                              as_stream(stream)),
                   "hyper prepare kernels");
 }
+
+#ifdef Q38M_CHECKED
+int q38m_checked_status_v1(uint32_t* status, int reset, int device) {
+    if (!status) return fail(Q38M_ERR_INVALID_ARGUMENT, "null checked status");
+    if (int rc = select_device(device)) return rc;
+    // a diagnostic of the checked build: it allocates its own 4 bytes
+    uint32_t* word = nullptr;
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMalloc(&word, sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(word, 0, sizeof(uint32_t));
+    for (q38m::CheckedReader read : q38m::checked_readers())
+        if (e == hipSuccess) e = read(word, reset, nullptr);
+    uint32_t all = 0u;
+    if (e == hipSuccess) e = hipMemcpy(&all, word, sizeof(all), hipMemcpyDeviceToHost);
+    if (word != nullptr) {
+        const hipError_t freed = hipFree(word);
+        if (e == hipSuccess) e = freed;
+    }
+    if (e != hipSuccess) return device_fail(e, "checked status");
+    *status = all;
+    return finish(hipSuccess, "checked status");
+}
+#endif
 
 }  // extern "C"

@@ -34,6 +34,56 @@ __device__ __forceinline__ uint2 load_stream(const uint2* p) {
     return make_uint2(v.x, v.y);
 }
 
+// ---- checked build (-DQ38M_CHECKED: libq38m_checked.so) -------------------
+// Index checks on values the kernels read from memory: the expert and row
+// count of a task record, the plan's packed and inverse route indices.  In
+// the checked build a value outside its range sets a bit of the status word
+// of this translation unit (each unit has its own; q38m_checked_status_v1
+// ORs them) and is replaced by 0, an in-range value, so the kernel completes
+// without touching memory outside its buffers -- it never traps.  In the
+// product build checked() is the value itself.
+enum CheckBit : uint32_t {
+    kCheckExpert = 1u,    // task expert >= 512
+    kCheckTaskRows = 2u,  // task rows > the largest task (128)
+    kCheckRoute = 4u,     // inverse (assignment -> packed) index >= routes
+    kCheckToken = 8u,     // packed route index past the largest chunk
+};
+
+#ifdef Q38M_CHECKED
+// Each unit registers a reader of its status word with the host
+// (q38m_api.hip): a one-thread kernel that ORs the word into *out and, on
+// reset, clears it (the word itself is internal to the unit, so no symbol
+// lookup is involved).
+bool register_checked_status(hipError_t (*read)(uint32_t* out, int reset, hipStream_t stream));
+namespace {
+__device__ uint32_t g_checked_status;
+__global__ void checked_status_kernel(uint32_t* out, int reset) {
+    if (threadIdx.x == 0u) {
+        out[0] |= g_checked_status;
+        if (reset) g_checked_status = 0u;
+    }
+}
+hipError_t read_checked_status(uint32_t* out, int reset, hipStream_t stream) {
+    checked_status_kernel<<<1, 64, 0, stream>>>(out, reset);
+    return hipGetLastError();
+}
+[[maybe_unused]] const bool g_checked_registered = register_checked_status(&read_checked_status);
+}  // namespace
+#endif
+
+__device__ __forceinline__ uint32_t checked(uint32_t v, uint32_t limit, CheckBit bit) {
+#ifdef Q38M_CHECKED
+    if (v >= limit) {
+        atomicOr(&g_checked_status, static_cast<uint32_t>(bit));
+        return 0u;
+    }
+#else
+    (void)limit;
+    (void)bit;
+#endif
+    return v;
+}
+
 // ---- plan tasks ------------------------------------------------------------
 // A task record (q38m_task_v1: packed_begin, expert, valid_rows, flags) read
 // as one 8-byte load of its two words: with a uniform index that is a single
@@ -50,7 +100,8 @@ static_assert(sizeof(q38m_task_v1) == 8 && offsetof(q38m_task_v1, expert) == 4 &
 __device__ __forceinline__ TaskRecord read_task(const q38m_task_v1* __restrict__ tasks,
                                                 uint32_t index) {
     const uint2 w = reinterpret_cast<const uint2*>(tasks)[index];
-    return TaskRecord{w.x, w.y & 0xffffu, (w.y >> 16) & 0xffu};
+    return TaskRecord{w.x, checked(w.y & 0xffffu, Q38M_ROUTE_EXPERTS, kCheckExpert),
+                      checked((w.y >> 16) & 0xffu, Q38M_WIDE_TASK_ROWS + 1u, kCheckTaskRows)};
 }
 
 // ---- conversions ---------------------------------------------------------

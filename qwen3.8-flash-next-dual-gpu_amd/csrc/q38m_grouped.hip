@@ -137,7 +137,7 @@ void gate_up_w4_kernel(
     static_assert(16u * (H / 16u) % kThreads == 0u && kThreads % 16u == 0u,
                   "whole chunks per thread, one row per thread");
     const uint32_t srow = threadIdx.x % 16u;
-    const uint32_t token = packed[p0 + (srow < rows ? srow : 0u)];
+    const uint32_t token = checked(packed[p0 + (srow < rows ? srow : 0u)], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
     QuadWeights r0 = load(0), r1 = load(1), r2;
     const uint4* arow = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token / kTopK) * H);
     uint4 v[kChunks];
@@ -180,7 +180,7 @@ void gate_up_w4_kernel(
         const uint32_t r = 4u * q + i;
         if (r >= rows) continue;
         const uint32_t p = p0 + r;
-        const uint32_t a = packed[p];
+        const uint32_t a = checked(packed[p], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
         const float st = xs[a / kTopK];
         const float unscale = kBf16 ? 1.0f : 0.0625f;
         const float y_gate = (yg[i] * unscale) * st;
@@ -255,7 +255,7 @@ void gate_up_w8_kernel(
 #pragma unroll
     for (uint32_t c = 0; c < kChunks; ++c) {
         const uint32_t r = (threadIdx.x + c * kThreads) / (H / 16u);
-        token[c] = packed[p0 + (r < rows ? r : 0u)];
+        token[c] = checked(packed[p0 + (r < rows ? r : 0u)], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
     }
     BlockWeights r0 = load(0), r1 = load(1), r2;
     uint4 v[kChunks];
@@ -324,7 +324,7 @@ void gate_up_w8_kernel(
         const uint32_t r = 4u * q + i;
         if (r >= rows) continue;
         const uint32_t p = p0 + r;
-        const uint32_t a = packed[p];
+        const uint32_t a = checked(packed[p], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
         const float st = xs[a / kTopK];
         mid[static_cast<size_t>(p) * I + channel] =
             static_cast<uint16_t>(swiglu_fold(yg[i] * st, yu[i] * st, route_weights[a]));
@@ -556,7 +556,8 @@ __global__ __launch_bounds__(256) void combine_kernel(
     }
     uint32_t rows[kTopK];
 #pragma unroll
-    for (uint32_t r = 0; r < kTopK; ++r) rows[r] = inverse[token * kTopK + r];
+    for (uint32_t r = 0; r < kTopK; ++r)
+        rows[r] = checked(inverse[token * kTopK + r], gridDim.x * kTopK, kCheckRoute);
     for (uint32_t c0 = threadIdx.x * 8u; c0 < H; c0 += 256u * 8u) {
         float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256) void pack_hidden_kernel(
     const uint16_t* __restrict__ hidden, const uint32_t* __restrict__ packed,
     uint32_t width, uint16_t* __restrict__ out) {
     const uint32_t p = blockIdx.x;
-    const uint32_t token = packed[p] / kTopK;
+    const uint32_t token = checked(packed[p], Q38M_WIDE_MAX_TOKENS * kTopK, kCheckToken) / kTopK;
     const uint4* src = reinterpret_cast<const uint4*>(hidden + static_cast<size_t>(token) * width);
     uint4* dst = reinterpret_cast<uint4*>(out + static_cast<size_t>(p) * width);
     for (uint32_t i = threadIdx.x; i < width / 8u; i += blockDim.x) dst[i] = src[i];

@@ -363,7 +363,7 @@ void gate_up_w4_wide_kernel(const uint4* __restrict__ w, const uint16_t* __restr
     // (slot tid/64 of the workgroup's 16, lane tid%64), scale piece tid
     const uint32_t sr = tid >> 3, sch = tid & 7u;
     const bool alive = sr < rows;
-    const uint32_t assignment = alive ? packed[p0 + sr] : 0u;
+    const uint32_t assignment = alive ? checked(packed[p0 + sr], Q38M_WIDE_MAX_TOKENS * kTopK, kCheckToken) : 0u;
     if (sch == 0u && alive)
         row_info[sr] = make_float2(xs[assignment / kTopK], route_weights[assignment]);
     const uint4* a_src =
@@ -679,7 +679,7 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
     // tid for tid < 256 (the step's two group words of the quad's four)
     const uint32_t sr = tid >> 2, sch = tid & 3u;
     const bool alive = sr < rows;
-    const uint32_t assignment = alive ? packed[p0 + sr] : 0u;
+    const uint32_t assignment = alive ? checked(packed[p0 + sr], Q38M_WIDE_MAX_TOKENS * kTopK, kCheckToken) : 0u;
     if (sch == 0u && alive)
         row_info[sr] = make_float2(xs[assignment / kTopK], route_weights[assignment]);
     const uint4* a_src =
@@ -910,7 +910,7 @@ __device__ __forceinline__ void gate_up_w8_wide_rows(
         const uint32_t r = i / 4u, c = i % 4u;
         staged[u] = i < kPieces;
         alive[u] = staged[u] && r < rows;
-        const uint32_t token = alive[u] ? packed[p0 + r] / kTopK : 0u;
+        const uint32_t token = alive[u] ? checked(packed[p0 + r], Q38M_WIDE_MAX_TOKENS * kTopK, kCheckToken) / kTopK : 0u;
         row_src[u] = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token) * H) + c;
         lds_at[u] = (r / 16u) * 64u + c * 16u + r % 16u;
     }
@@ -1020,7 +1020,7 @@ __device__ __forceinline__ void gate_up_w8_wide_rows(
             const uint32_t r = 16u * t + 4u * q + i;
             if (r >= rows) continue;
             const uint32_t p = p0 + r;
-            const uint32_t a = packed[p];
+            const uint32_t a = checked(packed[p], Q38M_WIDE_MAX_TOKENS * kTopK, kCheckToken);
             const float st = xs[a / kTopK];
             mid[static_cast<size_t>(p) * I + channel] = static_cast<uint16_t>(
                 swiglu_fold(handoff[r * 16u + n] * st, y[t][i] * st, route_weights[a]));

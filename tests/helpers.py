@@ -85,14 +85,15 @@ def synth_logits(q38m, seed, tag, tokens, bias=None):
     return out.view(tokens, W.EXPERTS)
 
 
-def prefill(q38m, layer, hidden, logits, ws, output=None, shared=None):
-    """Runs q38m_moe_prefill_v1 on device tensors; returns the bf16 output."""
+def prefill(q38m, layer, hidden, logits, ws, output=None, shared=None, call=None):
+    """Runs q38m_moe_prefill_v1 on device tensors (through `call`, by
+    default the product library's); returns the bf16 output."""
     t = torch()
     tokens = hidden.shape[0]
     if output is None:
         output = t.empty(tokens, W.HIDDEN, dtype=t.int16, device="cuda")
     so, sg = (None, None) if shared is None else shared
-    q38m.call("q38m_moe_prefill_v1", ctypes.byref(layer.gu.desc), ctypes.byref(layer.dn.desc),
+    (call or q38m.call)("q38m_moe_prefill_v1", ctypes.byref(layer.gu.desc), ctypes.byref(layer.dn.desc),
               hidden.data_ptr(), None if logits is None else logits.data_ptr(), tokens,
               ctypes.byref(ws.ws), None if so is None else so.data_ptr(),
               None if sg is None else sg.data_ptr(), output.data_ptr(), stream(), 0)
@@ -150,14 +151,14 @@ def decode(q38m, layer, hidden, ids, weights, scratch, output=None, top_k=10):
 
 
 def decode_fused(q38m, layer, hidden, logits, scratch, output=None, top_k=10, shared=None,
-                 residual=None):
+                 residual=None, call=None):
     """Runs q38m_moe_decode_v1 (top-k from logits, routed experts, optional
     gated shared term and residual) on device tensors."""
     t = torch()
     if output is None:
         output = t.empty(1, W.HIDDEN, dtype=t.int16, device="cuda")
     so, sg = (None, None) if shared is None else shared
-    q38m.call("q38m_moe_decode_v1", ctypes.byref(layer.gu.desc), ctypes.byref(layer.dn.desc),
+    (call or q38m.call)("q38m_moe_decode_v1", ctypes.byref(layer.gu.desc), ctypes.byref(layer.dn.desc),
               hidden.data_ptr(), logits.data_ptr(), top_k,
               None if so is None else so.data_ptr(), None if sg is None else sg.data_ptr(),
               None if residual is None else residual.data_ptr(), scratch.data_ptr(),

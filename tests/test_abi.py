@@ -14,7 +14,7 @@ import pytest
 from conftest import ROOT
 
 HEADERS = [os.path.join(ROOT, "include", name)
-           for name in ("q38m.h", "q38m_selftest.h", "q38m_phase.h")]
+           for name in ("q38m.h", "q38m_selftest.h", "q38m_phase.h", "q38m_checked.h")]
 
 
 def declared_functions(headers=HEADERS[:1]):
@@ -61,7 +61,7 @@ def test_selftest_library_exports_its_header(q38m):
 
 
 def test_timed_library_is_the_product_plus_the_phase_log(q38m):
-    phase = declared_functions(HEADERS[2:])
+    phase = declared_functions(HEADERS[2:3])
     assert phase == ["q38m_phase_calls_v1", "q38m_phase_log_v1"]
     assert exported_functions(q38m.TIMED_LIB_PATH) == sorted(declared_functions() + phase)
     assert ctypes.sizeof(q38m.PhaseRecord) == 144
@@ -554,3 +554,13 @@ int main() {
                     f"-Wl,-rpath,{pkg}", "-Wl,-rpath,/opt/rocm/lib"], check=True)
     out = subprocess.run([str(exe)], capture_output=True, text=True)
     assert out.returncode == 0 and out.stdout == "ok\n", out.stdout + out.stderr
+
+
+def test_checked_library_is_the_product_plus_the_status_word(q38m):
+    checked = declared_functions(HEADERS[3:])
+    assert checked == ["q38m_checked_status_v1"]
+    assert exported_functions(q38m.CHECKED_LIB_PATH) == sorted(declared_functions() + checked)
+    lib = q38m.checked_lib()
+    assert lib.q38m_checked_status_v1(None, 0, 0) == q38m.ERR_INVALID_ARGUMENT
+    # the checked build rejects the same arguments as the product library
+    assert lib.q38m_moe_prefill_max_tasks_v1(512) == 800
