@@ -657,7 +657,9 @@ static inline float bf16_round(float v) {
 
 /* SwiGLU and router-weight fold, the rounding sequence of
  * cuda/q38_moe_prefill.cu:449-461: g=bf16(y_g), u=bf16(y_u),
- * h=bf16(g/(1+exp(-g))*u), m=bf16(h*w). */
+ * h=bf16(g/(1+exp(-g))*u), m=bf16(h*w).  A NaN m is written as the quiet
+ * NaN 0x7fc0 (its sign and payload would otherwise follow the instruction
+ * set; the GPU's epilogues write the same word). */
 static inline uint16_t swiglu_fold(float y_gate, float y_up, float weight) {
     const float g = bf16_round(y_gate);
     const float u = bf16_round(y_up);
@@ -665,7 +667,8 @@ static inline uint16_t swiglu_fold(float y_gate, float y_up, float weight) {
     const float den = 1.0f + e;
     const float silu = g / den;
     const float h = bf16_round(silu * u);
-    return q38o_f32_to_bf16(h * weight);
+    const uint16_t m = q38o_f32_to_bf16(h * weight);
+    return (m & 0x7fffu) > 0x7f80u ? (uint16_t)0x7fc0u : m;
 }
 
 /* Grouped gate/up over the plan's M=16 tasks (q38_moe_prefill.cu:308-464)

@@ -189,8 +189,16 @@ __device__ __forceinline__ float exp_q(float x) {
     return x != x ? x + x : ranged;
 }
 
+// Every NaN bf16 word as the quiet NaN 0x7fc0.  A NaN's sign and payload
+// follow the instruction set that produced it (the host table behind the
+// chunk path's silu and the device's own exp and division differ), so the
+// SwiGLU epilogues write NaN in this one form.
+__device__ __forceinline__ uint32_t bf16_canonical_nan(uint32_t word) {
+    return (word & 0x7fffu) > 0x7f80u ? 0x7fc0u : word;
+}
+
 // SwiGLU with the router-weight fold; rounding sequence of the reference
-// gate/up epilogue (cuda/q38_moe_prefill.cu:449-461).
+// gate/up epilogue (cuda/q38_moe_prefill.cu:449-461); NaN as 0x7fc0.
 __device__ __forceinline__ uint32_t swiglu_fold(float y_gate, float y_up,
                                                 float weight) {
     const float g = bf16_round(y_gate);
@@ -199,7 +207,7 @@ __device__ __forceinline__ uint32_t swiglu_fold(float y_gate, float y_up,
     const float den = 1.0f + e;
     const float silu = g / den;
     const float h = bf16_round(silu * u);
-    return f32_to_bf16(h * weight);
+    return bf16_canonical_nan(f32_to_bf16(h * weight));
 }
 
 // ---- int8 MFMA -------------------------------------------------------------

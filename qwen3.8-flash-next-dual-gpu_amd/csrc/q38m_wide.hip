@@ -825,7 +825,8 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
     else
         k_loop(std::integral_constant<uint32_t, 1>{});
 
-    // SwiGLU (swiglu_fold's rounding sequence with silu(g) from the table):
+    // SwiGLU (swiglu_fold's rounding sequence with silu(g) from the table,
+    // NaN written as 0x7fc0 like swiglu_fold):
     // D lane (qh, n) holds rows 4qh + i of each tile, channel n.  Four
     // tiles' gathers are in flight before their first store.
     const uint32_t channel = (at.slice * 8u + pr) * 16u + n;
@@ -853,8 +854,8 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
                 const uint32_t r = 16u * (t0 + b) + 4u * qh + i;
                 if (r >= rows) continue;
                 const float h = bf16_round(__uint_as_float(silu_word[b][i]) * up_value[b][i]);
-                mid[static_cast<size_t>(p0 + r) * I + channel] =
-                    static_cast<uint16_t>(f32_to_bf16(h * row_info[r].y));
+                mid[static_cast<size_t>(p0 + r) * I + channel] = static_cast<uint16_t>(
+                    bf16_canonical_nan(f32_to_bf16(h * row_info[r].y)));
             }
     }
 }

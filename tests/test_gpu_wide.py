@@ -178,22 +178,45 @@ def wide_layers(q38m, orc):
     cache.clear()
 
 
-def test_wide_slab_equals_v1_with_intermediates(q38m, orc, wide_layers):
+@pytest.mark.parametrize("values", ["finite", "non-finite"])
+def test_wide_slab_equals_v1_with_intermediates(q38m, orc, wide_layers, values):
     """At T = 512 the chunk plan's packed order is the V1 order, so every
-    intermediate of the chunk path equals the slab path's."""
+    intermediate of the chunk path equals the slab path's -- also word for
+    word where tokens carry +inf, -inf or NaN (their gates go infinite or
+    NaN: the chunk path's silu comes from a host-built table, the slab's
+    from the device's exp and division, and both write NaN mid words as
+    0x7fc0)."""
     layer = wide_layers(2)
     seed = W.CONFIGS[2]["seed"]
     hidden = synth_hidden(q38m, seed, 7, 512)
     logits = synth_logits(q38m, seed, 8, 512)
+    if values == "non-finite":
+        t = torch()
+        bad = t.tensor([0x7f80, 0xff80, 0x7fc1, 0xffa0], dtype=t.int32).to(t.int16)
+        for k, token in enumerate((3, 100, 101, 511)):
+            hidden[token, 17 + 5 * k] = bad[k].item()
+        hidden[200, :] = bad[2].item()  # a whole row of NaN
     ws1 = q38m.PrefillWorkspace_(512)
     out1 = prefill(q38m, layer, hidden, logits, ws1)
     wsw = q38m.WideWorkspace_(512)
     outw = prefill_wide(q38m, layer, hidden, logits, wsw)
     a, b = ws_arrays(ws1, 512), ws_arrays(wsw, 512)
-    for name in ("ids", "xq", "weighted_mid", "mid_q", "route_output"):
+    for name in ("ids", "xq", "weighted_mid", "mid_q"):
         assert np.array_equal(a[name], b[name]), name
+    assert np.array_equal(a["route_output"].view(np.uint32), b["route_output"].view(np.uint32))
     assert np.array_equal(a["weights"].view(np.uint32), b["weights"].view(np.uint32))
     assert np.array_equal(host(out1, np.uint16), host(outw, np.uint16))
+    if values == "non-finite":
+        mid = a["weighted_mid"]
+        nan = ((mid & 0x7f80) == 0x7f80) & ((mid & 0x7f) != 0)
+        assert nan.any() and np.all(mid[nan] == 0x7fc0)
+        # and the oracle writes the same mid words (NaN included) and output
+        ref = orc.moe(host(hidden, np.uint16).reshape(512, W.HIDDEN), layer.host_gu,
+                      layer.host_dn, logits=host(logits, np.float32).reshape(512, W.EXPERTS),
+                      intermediates=True)
+        assert np.array_equal(ref["weighted_mid"], mid)
+        assert np.array_equal(canonical_nan(ref["output"]),
+                              canonical_nan(host(out1, np.uint16).reshape(512, W.HIDDEN)))
 
 
 def test_wide_config4_chunk(q38m, orc, wide_layers):
