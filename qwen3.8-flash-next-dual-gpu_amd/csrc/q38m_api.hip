@@ -12,6 +12,7 @@
 
 #include "q38m_internal.h"
 
+#include <atomic>
 #include <initializer_list>
 #include <mutex>
 
@@ -445,21 +446,28 @@ static __device__ __align__(256) uint8_t
 namespace {
 
 constexpr int kNoAllocDevices = 64;
-std::once_flag g_scratch_once[kNoAllocDevices];
-void* g_scratch_address[kNoAllocDevices];
-hipError_t g_scratch_status[kNoAllocDevices];
+// a successful lookup is kept per device; a failed one is not, so a later
+// call (say, once the device's context exists) looks again
+std::atomic<void*> g_scratch_address[kNoAllocDevices];
+std::mutex g_scratch_mutex;
 
 // Device address of `scratch` on `device`, which the caller made current.
 int noalloc_scratch(int device, void** address) {
     if (device >= kNoAllocDevices)
         return fail(Q38M_ERR_INVALID_ARGUMENT, "allocation-free step: device index above 63");
-    std::call_once(g_scratch_once[device], [device] {
-        g_scratch_status[device] =
-            hipGetSymbolAddress(&g_scratch_address[device], HIP_SYMBOL(scratch));
-    });
-    if (g_scratch_status[device] != hipSuccess)
-        return device_fail(g_scratch_status[device], "hipGetSymbolAddress(scratch)");
-    *address = g_scratch_address[device];
+    void* known = g_scratch_address[device].load(std::memory_order_acquire);
+    if (known == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mutex);
+        known = g_scratch_address[device].load(std::memory_order_relaxed);
+        if (known == nullptr) {
+            const hipError_t status = hipGetSymbolAddress(&known, HIP_SYMBOL(scratch));
+            if (status != hipSuccess || known == nullptr)
+                return device_fail(status != hipSuccess ? status : hipErrorInvalidSymbol,
+                                   "hipGetSymbolAddress(scratch)");
+            g_scratch_address[device].store(known, std::memory_order_release);
+        }
+    }
+    *address = known;
     return Q38M_OK;
 }
 
