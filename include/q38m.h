@@ -392,6 +392,32 @@ int q38m_moe_decode_v1(const q38m_expert_weights_v1* gate_up,
                        void* scratch, uint16_t* output, void* stream,
                        int device);
 
+/* The whole MoE block of one decode step from the hidden row: the tokens
+ * == 1 branch of run_moe (cuda/cuda_backend.cu:1516-1605) -- the router
+ * GEMV over the bf16 router (:1518-1519), cuda_topk_router_bf16 (512
+ * experts, normalised), cuda_moe_routed_bf16 (include/q38/cuda_moe.h:
+ * 17-29), the bf16 shared expert (cuda_backend.cu:1573-1590) and
+ * cuda_moe_combine_shared_bf16 (cuda_moe.h:31-37) -- in three launches
+ * instead of five: the router GEMV; the routed gate/up with the top-k and
+ * the shared gate/up; the routed down with the shared down, the gated
+ * combine and the optional residual.  Bit-identical to
+ * q38m_moe_router_v1 -> q38m_moe_shared_expert_v1 -> q38m_moe_decode_v1
+ * on the same token.  router [512][2048], w_gate / w_up [shared_inter][2048],
+ * w_down [2048][shared_inter], w_out_gate [2048], bf16, 16-byte aligned;
+ * shared_inter must be Q38M_INTERMEDIATE (512).  residual: null, or
+ * output = bf16(residual + moe).  scratch: 16-byte aligned,
+ * q38m_moe_decode_block_scratch_bytes() bytes; the chosen ids are left in
+ * its first 40 bytes. */
+size_t q38m_moe_decode_block_scratch_bytes(void);
+int q38m_moe_decode_block_v1(const q38m_expert_weights_v1* gate_up,
+                             const q38m_expert_weights_v1* down,
+                             const uint16_t* hidden, const uint16_t* router,
+                             const uint16_t* w_gate, const uint16_t* w_up,
+                             const uint16_t* w_down, const uint16_t* w_out_gate,
+                             uint32_t shared_inter, uint32_t top_k,
+                             const uint16_t* residual, void* scratch,
+                             uint16_t* output, void* stream, int device);
+
 /* ---- hyper-connection prepare/finish around the MoE step -------------
  * include/q38/cuda_hyper.h:15-58 (kernels cuda/q38_hyper.cu:52-114; call
  * sequence cuda_backend.cu:1219-1252).  The hidden state is

@@ -207,6 +207,23 @@ inline void run_moe_prefill(const ExpertWeightsV1& gate_up, const ExpertWeightsV
 
 // Router logits (cuda_backend.cu:1518-1519): fp32 [tokens][512] from
 // hidden rows of hidden_width (must be 2048) values.
+// The whole MoE block of one decode step (run_moe's tokens == 1 branch,
+// cuda_backend.cu:1516-1605): router GEMV, routed experts, bf16 shared
+// expert, gated combine and optional residual in three launches; equal to
+// moe_router + moe_shared_expert + moe_decode bit for bit.
+inline void moe_decode_block(const q38m_expert_weights_v1& gate_up_experts,
+                             const q38m_expert_weights_v1& down_experts,
+                             const std::uint16_t* hidden, const std::uint16_t* router,
+                             const std::uint16_t* w_gate, const std::uint16_t* w_up,
+                             const std::uint16_t* w_down, const std::uint16_t* w_out_gate,
+                             std::uint32_t shared_inter, std::uint32_t top_k,
+                             const std::uint16_t* residual, void* scratch,
+                             std::uint16_t* output, void* stream, int device) {
+    check(q38m_moe_decode_block_v1(&gate_up_experts, &down_experts, hidden, router, w_gate,
+                                   w_up, w_down, w_out_gate, shared_inter, top_k, residual,
+                                   scratch, output, stream, device));
+}
+
 inline void moe_router(const std::uint16_t* hidden, const std::uint16_t* router,
                        std::uint32_t tokens, std::uint32_t hidden_width, float* logits,
                        void* stream, int device) {

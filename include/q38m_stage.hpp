@@ -82,7 +82,7 @@ inline void stage_regions(std::uint32_t t, std::uint32_t shared_inter, std::uint
     out[6] = t * h * 2u;
     out[7] = q38m_moe_shared_expert_scratch_bytes(t, shared_inter);
     out[8] = q38m_hyper_prepare_scratch_bytes(t, Q38M_HIDDEN, low_rank);
-    out[9] = q38m_moe_decode_scratch_bytes();
+    out[9] = q38m_moe_decode_block_scratch_bytes();  // covers the plain decode's too
 }
 }  // namespace detail
 
@@ -136,6 +136,15 @@ inline void run_moe(const MoeLayerWeights& m, std::uint32_t tokens, MoeStageWork
                     void* stream, int device) {
     if (tokens == 0 || tokens > ws.max_tokens)
         throw std::invalid_argument("run_moe: tokens outside the bound workspace");
+    if (tokens == 1 && m.shared_inter == Q38M_INTERMEDIATE) {
+        // the decode step: router, top-k, routed experts, shared expert and
+        // the gated combine (:1518-1601) in three launches
+        moe_decode_block(m.gate_up, m.down, ws.mixed, m.router, m.shared_gate, m.shared_up,
+                         m.shared_down, m.shared_output_gate, m.shared_inter, Q38M_ROUTE_TOPK,
+                         /*residual=*/nullptr, ws.decode_scratch, ws.block_output, stream,
+                         device);
+        return;
+    }
     // router logits (:1518) and the shared expert with its output gate
     // (:1573-1590), both reading the 2048-wide mixed rows
     moe_router(ws.mixed, m.router, tokens, Q38M_HIDDEN, ws.logits, stream, device);

@@ -162,6 +162,10 @@ SIGNATURES = {
                                          _P, _INT]),
     "q38m_moe_decode_v1": (_INT, [ctypes.POINTER(ExpertWeights), ctypes.POINTER(ExpertWeights),
                                   _P, _P, _U32, _P, _P, _P, _P, _P, _P, _INT]),
+    "q38m_moe_decode_block_scratch_bytes": (_SZ, []),
+    "q38m_moe_decode_block_v1": (_INT, [ctypes.POINTER(ExpertWeights),
+                                        ctypes.POINTER(ExpertWeights), _P, _P, _P, _P, _P, _P,
+                                        _U32, _U32, _P, _P, _P, _P, _INT]),
     "q38m_expert_weights_bytes": (_SZ, [ctypes.POINTER(ExpertWeights), ctypes.POINTER(_SZ)]),
     "q38m_repack_expert_weights": (_INT, [ctypes.POINTER(ExpertWeights),
                                           ctypes.POINTER(ExpertWeights), _P, _INT]),

@@ -69,6 +69,13 @@ bool aligned(const void* p, uintptr_t alignment) {
     return (reinterpret_cast<uintptr_t>(p) % alignment) == 0u;
 }
 
+// every pointer non-null and 16-byte aligned
+bool all16(std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs)
+        if (!p || !aligned(p, 16)) return false;
+    return true;
+}
+
 size_t align_up(size_t value, size_t alignment) {
     return (value + alignment - 1u) / alignment * alignment;
 }
@@ -698,6 +705,31 @@ int q38m_moe_decode_v1(const q38m_expert_weights_v1* gate_up, const q38m_expert_
                   "decode MoE kernels");
 }
 
+size_t q38m_moe_decode_block_scratch_bytes(void) { return q38m::decode_block_scratch_bytes(); }
+
+int q38m_moe_decode_block_v1(const q38m_expert_weights_v1* gate_up,
+                             const q38m_expert_weights_v1* down, const uint16_t* hidden,
+                             const uint16_t* router, const uint16_t* w_gate, const uint16_t* w_up,
+                             const uint16_t* w_down, const uint16_t* w_out_gate,
+                             uint32_t shared_inter, uint32_t top_k, const uint16_t* residual,
+                             void* scratch, uint16_t* output, void* stream, int device) {
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (int rc = check_weights(down, false)) return rc;
+    if (shared_inter != Q38M_INTERMEDIATE)
+        return fail(Q38M_ERR_INVALID_ARGUMENT,
+                    "decode block: the shared expert's intermediate size must be 512 (two "
+                    "channels per gate/up workgroup)");
+    if (!all16({hidden, router, w_gate, w_up, w_down, w_out_gate, scratch}) || !output ||
+        top_k == 0 || top_k > Q38M_ROUTE_TOPK || (residual != nullptr && !aligned(residual, 2)) ||
+        !aligned(output, 2))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid decode block buffers");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_decode_block(*gate_up, *down, hidden, router, w_gate, w_up, w_down,
+                                            w_out_gate, top_k, residual, scratch, output,
+                                            as_stream(stream)),
+                  "decode block kernels");
+}
+
 size_t q38m_expert_weights_bytes(const q38m_expert_weights_v1* w, size_t* scale_bytes) {
     if (!w || (w->format != Q38M_FORMAT_W4_SYM && w->format != Q38M_FORMAT_W8_SYM)) {
         if (scale_bytes) *scale_bytes = 0;
@@ -856,11 +888,6 @@ const char* q38m_last_error(void) { return g_last_error.c_str(); }
 
 namespace {
 bool valid_hidden(uint32_t hidden) { return hidden != 0u && hidden % 8u == 0u && hidden <= 8192u; }
-bool all16(std::initializer_list<const void*> ptrs) {
-    for (const void* p : ptrs)
-        if (!p || !aligned(p, 16)) return false;
-    return true;
-}
 }  // namespace
 
 int q38m_hyper_repeat_embedding_bf16(const uint16_t* embedding, uint16_t* hyper, uint32_t tokens,

@@ -97,6 +97,28 @@ PhaseCall next_phase_call() { return PhaseCall{0u}; }
 constexpr uint32_t kDecodeBlocks = 256;
 constexpr uint32_t kDecodeThreads = kSelectThreads;
 
+// The whole MoE block of a decode step (q38m_moe_decode_block_v1) adds the
+// bf16 shared expert to the two routed launches: gate/up workgroup b also
+// computes channels 2b and 2b + 1 of g = bf16(x Wg^T), u = bf16(x Wu^T)
+// and h = silu_multiply(g, u) (workgroup 0 also the output gate
+// bf16(x wo)), and down workgroup b computes its eight channels of
+// bf16(h Wd^T) before the gated combine.  Every dot product is
+// wave_dot_bf16's (one wave per row, the same summation order as the GEMV
+// entry points), so the block equals q38m_moe_router_v1 +
+// q38m_moe_shared_expert_v1 + q38m_moe_decode_v1 bit for bit.
+struct SharedGateUp {
+    const uint16_t* w_gate;
+    const uint16_t* w_up;
+    const uint16_t* w_out_gate;
+    uint16_t* h;     // [I] bf16
+    uint16_t* gate;  // the output gate word
+};
+struct SharedDown {
+    const uint16_t* w_down;  // [H][I] bf16
+    const uint16_t* h;       // [I] bf16, from the gate/up launch
+    const uint16_t* gate;    // the output gate word
+};
+
 // gate/up: 12 waves, three route slots x four quarters of K.
 constexpr uint32_t kGateUpThreads = 768u;
 constexpr uint32_t kRouteSlots = 3u;
@@ -125,12 +147,17 @@ __device__ __forceinline__ uint32_t route_group_count(uint32_t g) { return g < 2
 // lanes per line.  The int32 group sums and their scales then move through
 // LDS into the chain layout: wave = route slot x two channels, lane =
 // quad + 16 (2 n' + u), where the fp32 chain runs along each 16-lane row.
-template <uint32_t H, uint32_t I, bool kW8, uint32_t kPer>
+//
+// kShared (the decode block): waves 8-11, which hold no logits, issue their
+// shared-expert row (gate and up rows of channels 2b, 2b + 1) before the
+// selection and finish the dot products while the routed weights stream.
+template <uint32_t H, uint32_t I, bool kW8, uint32_t kPer, bool kShared = false>
 __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, bool bf16,
     const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
     const int32_t* __restrict__ ids_in, const float* __restrict__ weights_in, uint32_t top_k,
-    int32_t* __restrict__ ids_out, uint16_t* __restrict__ mid, PhaseCall call) {
+    int32_t* __restrict__ ids_out, uint16_t* __restrict__ mid, PhaseCall call,
+    SharedGateUp shared) {
     PhaseStamps stamps;
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kSlots = 2u * I / 16u;
@@ -146,6 +173,7 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     __shared__ SelectLds select_lds;
     // [chain][quad]: int32 group sums, then their fp32 scales
     __shared__ uint4 xch[kChains * kQuads][2];
+    __shared__ float shared_dot[4];  // kShared: g, u of channel 2b; g, u of 2b + 1
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -163,6 +191,17 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
         num_lds[lane] = weights_in[lane];
     }
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    Bf16RowPass shared_row, gate_row;
+    if constexpr (kShared) {
+        if (wave >= 8u) {
+            const uint32_t c = 2u * blockIdx.x + ((wave - 8u) >> 1);
+            const uint16_t* rowp = ((wave & 1u) ? shared.w_up : shared.w_gate) +
+                                   static_cast<size_t>(c) * H;
+            shared_row = bf16_row_load(hidden, rowp, H / 8u, 0u, lane);
+            if (blockIdx.x == 0u && wave == 8u)
+                gate_row = bf16_row_load(hidden, shared.w_out_gate, H / 8u, 0u, lane);
+        }
+    }
     stamps.mark_loaded(1);
     // the selection first: the token row's absmax waits for its load, the
     // selection only for the logits
@@ -226,6 +265,18 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     }
 
     stamps.mark(3);
+
+    if constexpr (kShared) {
+        // the shared rows' products, while the routed weights stream
+        if (wave >= 8u) {
+            const float dot = wave_sum_f32(bf16_row_accumulate(shared_row, 0.0f));
+            if (lane == 0u) shared_dot[wave - 8u] = dot;
+        }
+        if (blockIdx.x == 0u && wave == 8u) {
+            const float gate = wave_sum_f32(bf16_row_accumulate(gate_row, 0.0f));
+            if (lane == 0u) shared.gate[0] = static_cast<uint16_t>(f32_to_bf16(gate));
+        }
+    }
 
     // the route's weight, while the weights stream: given, or
     // exp(l_r - l_0) over the rank-order sum (q38_kernels.cu:460-479)
@@ -322,6 +373,15 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     }
     __syncthreads();
     stamps.mark(7);
+    if constexpr (kShared) {
+        // the exchange barrier made shared_dot visible
+        if (threadIdx.x < 2u) {
+            const uint32_t g_bits = f32_to_bf16(shared_dot[2u * threadIdx.x]);
+            const uint32_t u_bits = f32_to_bf16(shared_dot[2u * threadIdx.x + 1u]);
+            shared.h[2u * blockIdx.x + threadIdx.x] =
+                static_cast<uint16_t>(silu_multiply(g_bits, u_bits));
+        }
+    }
 
     // chain layout: lane = quad + 16 c, chain 4 wave + c = (route slot,
     // channel 2 (wave % 4) + c / 2, gate/up c % 2)
@@ -375,13 +435,18 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
 
 // kPerGroup: W4, 32-column sub-blocks per group (1, 2, 4); W8, 64-column
 // K blocks per group (1, 2; I/64 = per output channel).
-template <uint32_t H, uint32_t I, bool kW4, uint32_t kPerGroup>
-__global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
+// kShared (the decode block): two more waves compute the workgroup's
+// eight channels of the shared down projection bf16(h Wd^T) and meet the
+// route waves at their two barriers; the finisher takes those words and the
+// output gate from the gate/up launch.
+template <uint32_t H, uint32_t I, bool kW4, uint32_t kPerGroup, bool kShared = false>
+__global__ __launch_bounds__(kShared ? kDecodeThreads + 128u : kDecodeThreads)
+void decode_down_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, bool bf16,
     const uint16_t* __restrict__ mid,
     const int32_t* __restrict__ ids, uint32_t top_k, const uint16_t* __restrict__ shared_output,
     const uint16_t* __restrict__ shared_gate, const uint16_t* __restrict__ residual,
-    uint16_t* __restrict__ out, PhaseCall call) {
+    uint16_t* __restrict__ out, PhaseCall call, SharedDown shared) {
     PhaseStamps stamps;
     constexpr uint32_t kTiles = H / 16u;
     static_assert(I == 64u * 8u, "one 8-element chunk of the mid row per lane");
@@ -389,6 +454,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     __shared__ uint4 mq_lds[kTopK][I / 16u];
     // route partials per output channel, ten routes padded to 12 floats
     __shared__ float4 o_lds[8][3];
+    __shared__ uint32_t shared_lds[8];  // kShared: the eight shared-down words
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t route = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -397,6 +463,27 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     const uint32_t n0 = 8u * (slot8 & 1u);
     const bool active = route < top_k;
 
+    if constexpr (kShared) {
+        if (route >= kTopK) {
+            // wave 10: channels n0 + 0..3 of the tile, wave 11: n0 + 4..7
+            const uint32_t c0 = 4u * (route - kTopK);
+            Bf16RowPass rows[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j)
+                rows[j] = bf16_row_load(shared.h,
+                                        shared.w_down + static_cast<size_t>(16u * tile + n0 + c0 + j) * I,
+                                        I / 8u, 0u, lane);
+#pragma unroll
+            for (uint32_t j = 0; j < 4u; ++j) {
+                const float dot = wave_sum_f32(bf16_row_accumulate(rows[j], 0.0f));
+                if (lane == 0u) shared_lds[c0 + j] = f32_to_bf16(dot);
+            }
+            __syncthreads();  // the route waves' mid-row barrier
+            __syncthreads();  // their partials barrier (the finisher reads shared_lds after it)
+            return;
+        }
+    }
+
     // the epilogue's operands, requested first: they depend on nothing.
     // Every thread loads them in straight-line code (an absent operand reads
     // the mid row's first word instead and is never used), so no branch
@@ -404,10 +491,15 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
     const uint32_t channel = 16u * tile + n0 + (threadIdx.x & 7u);
     const bool finisher = threadIdx.x < 8u;
     const bool has_residual = residual != nullptr;
-    const bool has_shared = shared_output != nullptr && shared_gate != nullptr;
+    const bool has_shared = kShared || (shared_output != nullptr && shared_gate != nullptr);
     const uint32_t residual_bits = (has_residual ? residual : mid)[has_residual ? channel : 0u];
-    const uint32_t shared_bits = (has_shared ? shared_output : mid)[has_shared ? channel : 0u];
-    const uint32_t gate_bits = (has_shared ? shared_gate : mid)[0];
+    uint32_t shared_bits = 0u, gate_bits = 0u;
+    if constexpr (kShared) {
+        gate_bits = shared.gate[0];
+    } else {
+        shared_bits = (has_shared ? shared_output : mid)[has_shared ? channel : 0u];
+        gate_bits = (has_shared ? shared_gate : mid)[0];
+    }
 
     const int32_t id = active ? ids[route] : -1;
     // the scratch holds ten mid rows, so a route past top_k reads one too
@@ -559,6 +651,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_down_kernel(
         for (uint32_t r = 0; r < kTopK; ++r)
             if (r < top_k) total += part[r];
         if (has_shared) {
+            if constexpr (kShared) shared_bits = shared_lds[threadIdx.x];
             const float g = bf16_to_f32(gate_bits);
             const float multiplier = 1.0f / (1.0f + exp_q(-g));
             total = __builtin_fmaf(bf16_to_f32(shared_bits), multiplier, total);
@@ -578,27 +671,36 @@ size_t decode_scratch_bytes() {
     return 256u + static_cast<size_t>(kTopK) * kInter * sizeof(uint16_t);
 }
 
+// The decode block's scratch: the decode scratch (ids, mid rows), then the
+// router's fp32 logits, the shared expert's h (bf16) and its output gate.
+constexpr size_t kBlockLogits = 256u + static_cast<size_t>(kTopK) * kInter * sizeof(uint16_t);
+constexpr size_t kBlockH = kBlockLogits + kExperts * sizeof(float);
+constexpr size_t kBlockGate = kBlockH + kInter * sizeof(uint16_t);
+size_t decode_block_scratch_bytes() { return kBlockGate + 256u; }
+
 namespace {
 
-template <bool kW4, uint32_t kPerGroup>
+template <bool kW4, uint32_t kPerGroup, bool kShared>
 void launch_decode_down(const q38m_expert_weights_v1& down, const uint16_t* mid,
                         const int32_t* ids, uint32_t top_k, const uint16_t* shared_output,
                         const uint16_t* shared_gate, const uint16_t* residual, uint16_t* output,
-                        PhaseCall call, hipStream_t stream) {
-    decode_down_kernel<kHidden, kInter, kW4, kPerGroup><<<kDecodeBlocks, kDecodeThreads, 0, stream>>>(
-        static_cast<const uint4*>(down.data), static_cast<const uint16_t*>(down.scales),
-        down.scale_dtype == Q38M_SCALE_BF16, mid, ids, top_k, shared_output, shared_gate,
-        residual, output, call);
+                        PhaseCall call, SharedDown shared, hipStream_t stream) {
+    decode_down_kernel<kHidden, kInter, kW4, kPerGroup, kShared>
+        <<<kDecodeBlocks, kShared ? kDecodeThreads + 128u : kDecodeThreads, 0, stream>>>(
+            static_cast<const uint4*>(down.data), static_cast<const uint16_t*>(down.scales),
+            down.scale_dtype == Q38M_SCALE_BF16, mid, ids, top_k, shared_output, shared_gate,
+            residual, output, call, shared);
 }
 
-}  // namespace
-
-hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
-                         const q38m_expert_weights_v1& down, const uint16_t* hidden,
-                         const float* logits, const int32_t* ids, const float* weights,
-                         uint32_t top_k, const uint16_t* shared_output,
-                         const uint16_t* shared_gate, const uint16_t* residual, void* scratch,
-                         uint16_t* output, hipStream_t stream) {
+// the two routed launches; kShared: with the shared expert (the decode block)
+template <bool kShared>
+hipError_t launch_decode_routed(const q38m_expert_weights_v1& gate_up,
+                                const q38m_expert_weights_v1& down, const uint16_t* hidden,
+                                const float* logits, const int32_t* ids, const float* weights,
+                                uint32_t top_k, const uint16_t* shared_output,
+                                const uint16_t* shared_gate, const uint16_t* residual,
+                                void* scratch, uint16_t* output, SharedGateUp sgu,
+                                SharedDown sdn, hipStream_t stream) {
     int32_t* scratch_ids = static_cast<int32_t*>(scratch);
     uint16_t* mid = reinterpret_cast<uint16_t*>(static_cast<char*>(scratch) + 256);
     const uint4* gw = static_cast<const uint4*>(gate_up.data);
@@ -607,9 +709,10 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
     int32_t* ids_out = logits != nullptr ? scratch_ids : nullptr;
     const PhaseCall call = next_phase_call();
     auto gate_up_launch = [&](auto w8, auto per) {
-        decode_gate_up_kernel<kHidden, kInter, decltype(w8)::value, decltype(per)::value>
+        decode_gate_up_kernel<kHidden, kInter, decltype(w8)::value, decltype(per)::value, kShared>
             <<<kDecodeBlocks, kGateUpThreads, 0, stream>>>(gw, gs, gbf16, hidden, logits, ids,
-                                                           weights, top_k, ids_out, mid, call);
+                                                           weights, top_k, ids_out, mid, call,
+                                                           sgu);
     };
     using W4 = std::false_type;
     using W8 = std::true_type;
@@ -631,36 +734,68 @@ hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
     const int32_t* down_ids = logits != nullptr ? scratch_ids : ids;
     constexpr uint32_t kBlocks = kInter / 64u;
     const bool w8 = down.format == Q38M_FORMAT_W8_SYM;
+    auto down_launch = [&](auto w4, auto per) {
+        launch_decode_down<decltype(w4)::value, decltype(per)::value, kShared>(
+            down, mid, down_ids, top_k, shared_output, shared_gate, residual, output, call, sdn,
+            stream);
+    };
     switch (down.group_size) {
         case 0u:
             if (!w8) return hipErrorInvalidValue;
-            launch_decode_down<false, kBlocks>(down, mid, down_ids, top_k, shared_output,
-                                               shared_gate, residual, output, call, stream);
+            down_launch(std::false_type{}, std::integral_constant<uint32_t, kBlocks>{});
             break;
         case 32u:
             if (w8) return hipErrorInvalidValue;
-            launch_decode_down<true, 1>(down, mid, down_ids, top_k, shared_output, shared_gate,
-                                        residual, output, call, stream);
+            down_launch(std::true_type{}, std::integral_constant<uint32_t, 1>{});
             break;
         case 64u:
             if (w8)
-                launch_decode_down<false, 1>(down, mid, down_ids, top_k, shared_output,
-                                             shared_gate, residual, output, call, stream);
+                down_launch(std::false_type{}, std::integral_constant<uint32_t, 1>{});
             else
-                launch_decode_down<true, 2>(down, mid, down_ids, top_k, shared_output,
-                                            shared_gate, residual, output, call, stream);
+                down_launch(std::true_type{}, std::integral_constant<uint32_t, 2>{});
             break;
         case 128u:
             if (w8)
-                launch_decode_down<false, 2>(down, mid, down_ids, top_k, shared_output,
-                                             shared_gate, residual, output, call, stream);
+                down_launch(std::false_type{}, std::integral_constant<uint32_t, 2>{});
             else
-                launch_decode_down<true, 4>(down, mid, down_ids, top_k, shared_output,
-                                            shared_gate, residual, output, call, stream);
+                down_launch(std::true_type{}, std::integral_constant<uint32_t, 4>{});
             break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
+                         const q38m_expert_weights_v1& down, const uint16_t* hidden,
+                         const float* logits, const int32_t* ids, const float* weights,
+                         uint32_t top_k, const uint16_t* shared_output,
+                         const uint16_t* shared_gate, const uint16_t* residual, void* scratch,
+                         uint16_t* output, hipStream_t stream) {
+    return launch_decode_routed<false>(gate_up, down, hidden, logits, ids, weights, top_k,
+                                       shared_output, shared_gate, residual, scratch, output,
+                                       SharedGateUp{}, SharedDown{}, stream);
+}
+
+hipError_t launch_decode_block(const q38m_expert_weights_v1& gate_up,
+                               const q38m_expert_weights_v1& down, const uint16_t* hidden,
+                               const uint16_t* router, const uint16_t* w_gate,
+                               const uint16_t* w_up, const uint16_t* w_down,
+                               const uint16_t* w_out_gate, uint32_t top_k,
+                               const uint16_t* residual, void* scratch, uint16_t* output,
+                               hipStream_t stream) {
+    char* base = static_cast<char*>(scratch);
+    float* logits = reinterpret_cast<float*>(base + kBlockLogits);
+    uint16_t* h = reinterpret_cast<uint16_t*>(base + kBlockH);
+    uint16_t* gate = reinterpret_cast<uint16_t*>(base + kBlockGate);
+    // the router GEMV (the same launch as q38m_moe_router_v1 at one token)
+    hipError_t e = launch_dense_gemm(hidden, router, 1u, kExperts, kHidden, logits, nullptr, stream);
+    if (e != hipSuccess) return e;
+    return launch_decode_routed<true>(gate_up, down, hidden, logits, nullptr, nullptr, top_k,
+                                      nullptr, nullptr, residual, scratch, output,
+                                      SharedGateUp{w_gate, w_up, w_out_gate, h, gate},
+                                      SharedDown{w_down, h, gate}, stream);
 }
 
 }  // namespace q38m

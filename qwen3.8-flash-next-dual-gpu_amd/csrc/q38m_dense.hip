@@ -20,10 +20,9 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-// 16 bytes as a native vector: loads and stores of it stay plain vector
-// moves (a HIP_vector_type copy is a memcpy the compiler may keep in
-// scratch memory)
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// u32x4 (q38m_select.h): 16 bytes as a native vector, so loads and stores
+// of it stay plain vector moves (a HIP_vector_type copy is a memcpy the
+// compiler may keep in scratch memory)
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -492,12 +491,6 @@ __global__ __launch_bounds__(kSelectThreads) void router_merge_kernel(
     }
 }
 
-// h = bf16(g / (1 + exp(-g)) * u) on bf16 g and u (q38_kernels.cu:286-296,
-// with this library's exp).
-__device__ __forceinline__ uint32_t silu_multiply(uint32_t g_bits, uint32_t u_bits) {
-    const float g = bf16_to_f32(g_bits);
-    return f32_to_bf16((g / (1.0f + exp_q(-g))) * bf16_to_f32(u_bits));
-}
 
 // The shared expert's first half in one launch: block (x, y) computes the
 // 32 x 32 tiles (y, x) of g = bf16(X Wg^T) and u = bf16(X Wu^T) and
@@ -590,47 +583,9 @@ __global__ __launch_bounds__(256) void shared_gate_up_kernel(
 // ---- one activation row (m = 1: the batch-1 decode step) --------------
 // At m = 1 a GEMM is a GEMV: every weight byte is used once, so the bound is
 // how fast the weight rows stream, and a 16 x 16 MFMA tile would waste 15 of
-// its 16 rows.  One wave per output row: lane l reads the row's 16-byte
-// chunks l, l + 64, ... (each load instruction eight whole 128-byte lines)
-// and the activation's matching chunks (an L2 hit after the first wave),
-// four chunks in flight per lane, each chunk's eight products accumulated
-// into its own fp32 partial in k order, the partials added in chunk order,
-// then the lanes summed by a fixed DPP / permlane tree.  The order of every
-// addition is fixed, so the results are the same on every run.
-
-// fp32 dot product of one weight row with the activation row over k
-// (k % 8 == 0), the sum in every lane of the wave.
-__device__ __forceinline__ float wave_dot_bf16(const uint16_t* __restrict__ a,
-                                               const uint16_t* __restrict__ row, uint32_t k,
-                                               uint32_t lane) {
-    const u32x4* av = reinterpret_cast<const u32x4*>(a);
-    const u32x4* bv = reinterpret_cast<const u32x4*>(row);
-    const uint32_t chunks = k / 8u;
-    float total = 0.0f;
-    for (uint32_t base = 0; base < chunks; base += 256u) {
-        u32x4 wa[4], xa[4];
-#pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) {
-            const uint32_t c = base + 64u * i + lane;
-            const bool in = c < chunks;
-            wa[i] = in ? bv[c] : u32x4{0u, 0u, 0u, 0u};
-            xa[i] = in ? av[c] : u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (uint32_t i = 0; i < 4u; ++i) {
-            float part = 0.0f;
-#pragma unroll
-            for (uint32_t j = 0; j < 4u; ++j) {
-                part = __builtin_fmaf(bf16_to_f32(xa[i][j] & 0xffffu), bf16_to_f32(wa[i][j] & 0xffffu), part);
-                part = __builtin_fmaf(bf16_to_f32(xa[i][j] >> 16), bf16_to_f32(wa[i][j] >> 16), part);
-            }
-            total += part;
-        }
-    }
-    return __uint_as_float(wave_reduce_u32(__float_as_uint(total), [](uint32_t x, uint32_t y) {
-        return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
-    }));
-}
+// its 16 rows.  One wave per output row (wave_dot_bf16, q38m_select.h: four
+// 16-byte chunks in flight per lane, fixed summation order); the
+// activation's chunks are L2 hits after the first wave.
 
 // C[n] = a . B[n], four waves (rows) per workgroup.
 template <DenseOut kOut>

@@ -210,6 +210,13 @@ __device__ __forceinline__ uint32_t swiglu_fold(float y_gate, float y_up,
     return bf16_canonical_nan(f32_to_bf16(h * weight));
 }
 
+// The shared expert's h = bf16(g / (1 + exp(-g)) * u) on bf16 g and u
+// (cuda_silu_multiply_bf16, q38_kernels.cu:286-296, with this library's exp).
+__device__ __forceinline__ uint32_t silu_multiply(uint32_t g_bits, uint32_t u_bits) {
+    const float g = bf16_to_f32(g_bits);
+    return f32_to_bf16((g / (1.0f + exp_q(-g))) * bf16_to_f32(u_bits));
+}
+
 // ---- int8 MFMA -------------------------------------------------------------
 // v_mfma_i32_16x16x32_i8: A 16x32 (lane l: row l%16, k 8*(l/16)..+7),
 // B 32x16 (lane l: column l%16, same k), D lane l: rows 4*(l/16)+i,

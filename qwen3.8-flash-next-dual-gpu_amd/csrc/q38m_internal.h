@@ -122,6 +122,16 @@ hipError_t launch_combine_shared(const uint16_t* routed, const uint16_t* shared,
 
 // decode (q38m_decode.hip)
 size_t decode_scratch_bytes();
+size_t decode_block_scratch_bytes();
+// the whole MoE block of one decode step: router GEMV, routed experts and
+// the bf16 shared expert (shared intermediate kInter) in three launches
+hipError_t launch_decode_block(const q38m_expert_weights_v1& gate_up,
+                               const q38m_expert_weights_v1& down, const uint16_t* hidden,
+                               const uint16_t* router, const uint16_t* w_gate,
+                               const uint16_t* w_up, const uint16_t* w_down,
+                               const uint16_t* w_out_gate, uint32_t top_k,
+                               const uint16_t* residual, void* scratch, uint16_t* output,
+                               hipStream_t stream);
 // logits != null: top-k inside the gate/up launch; else ids/weights given
 hipError_t launch_decode(const q38m_expert_weights_v1& gate_up,
                          const q38m_expert_weights_v1& down, const uint16_t* hidden,

@@ -76,6 +76,72 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
     return wave_reduce_u32(x, [](uint32_t a, uint32_t b) { return max(a, b); });
 }
 
+// ---- bf16 row dot products, one wave per row (the GEMV form) --------------
+// fp32 dot product of a bf16 weight row with a bf16 activation row: lane l
+// takes the 16-byte chunks l, l + 64, l + 128, l + 192 of each pass of 256
+// chunks (every load instruction eight whole 128-byte lines), each chunk's
+// eight products accumulated into its own fp32 partial in k order, the
+// partials added to the running total in chunk order, then the lanes summed
+// by wave_reduce_u32's fixed DPP / permlane tree.  Every addition is in a
+// fixed order, so the result is the same on every run and in every kernel
+// that uses these helpers (the dense GEMV, the decode block's shared
+// expert).  A pass's loads (bf16_row_load) can be issued well before its
+// products (bf16_row_accumulate).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct Bf16RowPass {
+    u32x4 w[4], x[4];
+};
+
+// chunks [base, base + 256) of a row of `chunks` 16-byte chunks
+__device__ __forceinline__ Bf16RowPass bf16_row_load(const uint16_t* __restrict__ a,
+                                                     const uint16_t* __restrict__ row,
+                                                     uint32_t chunks, uint32_t base,
+                                                     uint32_t lane) {
+    const u32x4* av = reinterpret_cast<const u32x4*>(a);
+    const u32x4* bv = reinterpret_cast<const u32x4*>(row);
+    Bf16RowPass p;
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        const uint32_t c = base + 64u * i + lane;
+        const bool in = c < chunks;
+        p.w[i] = in ? bv[c] : u32x4{0u, 0u, 0u, 0u};
+        p.x[i] = in ? av[c] : u32x4{0u, 0u, 0u, 0u};
+    }
+    return p;
+}
+
+__device__ __forceinline__ float bf16_row_accumulate(const Bf16RowPass& p, float total) {
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; ++i) {
+        float part = 0.0f;
+#pragma unroll
+        for (uint32_t j = 0; j < 4u; ++j) {
+            part = __builtin_fmaf(bf16_to_f32(p.x[i][j] & 0xffffu), bf16_to_f32(p.w[i][j] & 0xffffu), part);
+            part = __builtin_fmaf(bf16_to_f32(p.x[i][j] >> 16), bf16_to_f32(p.w[i][j] >> 16), part);
+        }
+        total += part;
+    }
+    return total;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float total) {
+    return __uint_as_float(wave_reduce_u32(__float_as_uint(total), [](uint32_t x, uint32_t y) {
+        return __float_as_uint(__uint_as_float(x) + __uint_as_float(y));
+    }));
+}
+
+// the whole dot product over k (k % 8 == 0), the sum in every lane
+__device__ __forceinline__ float wave_dot_bf16(const uint16_t* __restrict__ a,
+                                               const uint16_t* __restrict__ row, uint32_t k,
+                                               uint32_t lane) {
+    const uint32_t chunks = k / 8u;
+    float total = 0.0f;
+    for (uint32_t base = 0; base < chunks; base += 256u)
+        total = bf16_row_accumulate(bf16_row_load(a, row, chunks, base, lane), total);
+    return wave_sum_f32(total);
+}
+
 __device__ __forceinline__ float wave_max_f32(float x) {
     return __uint_as_float(wave_reduce_u32(__float_as_uint(x), [](uint32_t a, uint32_t b) {
         return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));

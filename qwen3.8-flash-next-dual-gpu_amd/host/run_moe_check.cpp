@@ -173,6 +173,17 @@ int main(int argc, char** argv) {
                 q38m::prepare_hyper(layers[l].moe_hyper, current, tokens, ws, s, 0);
                 dump(stem + "mixed.bin", ws.mixed, std::size_t(tokens) * H * 2, s);
                 q38m::run_moe(layers[l].moe, tokens, ws, s, 0);
+                if (tokens == 1) {
+                    // the decode block keeps its logits and shared-expert
+                    // words internal; the separate entry points (equal to
+                    // them bit for bit) produce the oracle's inputs
+                    const q38m::MoeLayerWeights& m = layers[l].moe;
+                    q38m::moe_router(ws.mixed, m.router, 1, H, ws.logits, s, 0);
+                    q38m::moe_shared_expert(ws.mixed, m.shared_gate, m.shared_up, m.shared_down,
+                                            m.shared_output_gate, 1, H, m.shared_inter,
+                                            ws.shared_scratch, ws.shared_output, ws.shared_gate,
+                                            s, 0);
+                }
                 dump(stem + "logits.bin", ws.logits,
                      std::size_t(tokens) * Q38M_ROUTE_EXPERTS * 4, s);
                 dump(stem + "shared_output.bin", ws.shared_output, std::size_t(tokens) * H * 2,

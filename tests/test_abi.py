@@ -564,3 +564,24 @@ def test_checked_library_is_the_product_plus_the_status_word(q38m):
     assert lib.q38m_checked_status_v1(None, 0, 0) == q38m.ERR_INVALID_ARGUMENT
     # the checked build rejects the same arguments as the product library
     assert lib.q38m_moe_prefill_max_tasks_v1(512) == 800
+
+
+def test_decode_block_validation(q38m):
+    gu = fake_weights(q38m)
+    dn = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)
+    # gu, dn, hidden, router, w_gate, w_up, w_down, w_out_gate, shared_inter, top_k,
+    # residual, scratch, output
+    good = [ctypes.byref(gu), ctypes.byref(dn), 0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 0x6000,
+            512, 10, None, 0x7000, 0x8000]
+    for i, bad in [(2, None), (3, None), (4, None), (5, None), (6, None), (7, None),
+                   (8, 256), (8, 1024), (9, 0), (9, 11), (11, None), (12, None),
+                   (2, 0x1008), (3, 0x2002), (11, 0x7004), (10, 0x9001)]:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_decode_block_v1", *args, None, 0)
+    with pytest.raises(q38m.Unsupported):  # row-major gate/up
+        rm = fake_weights(q38m, layout=0)
+        q38m.call("q38m_moe_decode_block_v1", ctypes.byref(rm), *good[1:], None, 0)
+    assert q38m.lib().q38m_moe_decode_block_scratch_bytes() >= (
+        q38m.lib().q38m_moe_decode_scratch_bytes() + 512 * 4 + 512 * 2 + 2)

@@ -8,6 +8,8 @@ Tolerances: an fp32 accumulation of K products is within
 TOL_SUM * sum_k |a_k b_k| of the exact value (TOL_SUM = 2^-16, far above
 the ~sqrt(K) * 2^-24 typical error, far below any layout mistake); bf16
 outputs additionally within one bf16 step (2^-8 relative)."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -220,3 +222,69 @@ def test_moe_block_router_routed_shared(q38m, orc, tokens):
         check_close(orc, host(sg, np.uint16).reshape(1, 1),
                     host(hidden, np.uint16).reshape(1, W.HIDDEN),
                     host(weights[3], np.uint16).reshape(1, W.HIDDEN), True)
+
+
+@pytest.mark.parametrize("policy,top_k,with_residual", [
+    ("config", 10, False), ("config", 10, True), ("config", 7, True), ("interior", 10, True)])
+def test_decode_block_equals_router_shared_decode(q38m, orc, policy, top_k, with_residual):
+    """q38m_moe_decode_block_v1 (router GEMV; routed gate/up with the top-k
+    and the shared gate/up; routed down with the shared down, the gated
+    combine and the residual -- three launches) equals
+    q38m_moe_router_v1 -> q38m_moe_shared_expert_v1 -> q38m_moe_decode_v1
+    on the same token bit for bit, and the oracle fed the GPU's logits and
+    shared inputs.  Formats: config 2's (W4 g32 gate/up, W8 down) and the
+    reference artifact's interior layers (W4 g128, bf16 scales)."""
+    t = torch()
+    if policy == "config":
+        gfmt, dfmt = W.layer_policy(2, 0)
+        layer = Layer(q38m, orc, W.CONFIGS[2]["seed"], 0, gfmt, dfmt)
+    else:
+        fmt = ("w4", 4, 128, 0.02)
+        layer = Layer(q38m, orc, W.CONFIGS[2]["seed"], 3, fmt, fmt, gate_up_bf16=True,
+                      down_bf16=True)
+    rng = np.random.default_rng(23 + top_k)
+    hidden = synth_hidden(q38m, 23, 1, 1)
+    router = device(bf16_matrix(orc, rng, W.EXPERTS, W.HIDDEN, 0.02))
+    wg, wu, wd, wo = [device(bf16_matrix(orc, rng, r, c, 0.02)) for r, c in
+                      ((W.INTER, W.HIDDEN), (W.INTER, W.HIDDEN), (W.HIDDEN, W.INTER),
+                       (1, W.HIDDEN))]
+    residual = synth_hidden(q38m, 23, 5, 1) if with_residual else None
+    s = stream()
+
+    logits = t.empty(1, W.EXPERTS, dtype=t.float32, device="cuda")
+    q38m.call("q38m_moe_router_v1", hidden.data_ptr(), router.data_ptr(), 1, W.HIDDEN,
+              logits.data_ptr(), s, 0)
+    scratch = t.empty(q38m.lib().q38m_moe_shared_expert_scratch_bytes(1, W.INTER) // 2 + 8,
+                      dtype=t.int16, device="cuda")
+    so = t.empty(1, W.HIDDEN, dtype=t.int16, device="cuda")
+    sg = t.empty(8, dtype=t.int16, device="cuda")
+    q38m.call("q38m_moe_shared_expert_v1", hidden.data_ptr(), wg.data_ptr(), wu.data_ptr(),
+              wd.data_ptr(), wo.data_ptr(), 1, W.HIDDEN, W.INTER, scratch.data_ptr(),
+              so.data_ptr(), sg.data_ptr(), s, 0)
+    want = decode_fused(q38m, layer, hidden, logits, decode_scratch(q38m), top_k=top_k,
+                        shared=(so, sg), residual=residual)
+
+    bscratch = t.full((q38m.lib().q38m_moe_decode_block_scratch_bytes() // 2,), -1,
+                      dtype=t.int16, device="cuda")
+    got = t.empty(1, W.HIDDEN, dtype=t.int16, device="cuda")
+    q38m.call("q38m_moe_decode_block_v1", ctypes.byref(layer.gu.desc),
+              ctypes.byref(layer.dn.desc), hidden.data_ptr(), router.data_ptr(), wg.data_ptr(),
+              wu.data_ptr(), wd.data_ptr(), wo.data_ptr(), W.INTER, top_k,
+              None if residual is None else residual.data_ptr(), bscratch.data_ptr(),
+              got.data_ptr(), s, 0)
+    t.cuda.synchronize()
+    assert t.equal(got, want)
+    ref = orc.moe(host(hidden, np.uint16).reshape(1, W.HIDDEN), layer.host_gu, layer.host_dn,
+                  ids=None, logits=host(logits, np.float32).reshape(1, W.EXPERTS),
+                  shared_output=host(so, np.uint16).reshape(1, W.HIDDEN),
+                  shared_gate=host(sg, np.uint16)[:1]) if top_k == 10 else None
+    if ref is not None:
+        out = ref["output"]
+        if residual is not None:
+            out = orc.f32_to_bf16(orc.bf16_to_f32(host(residual, np.uint16).reshape(1, W.HIDDEN)) +
+                                  orc.bf16_to_f32(out))
+        assert np.array_equal(host(got, np.uint16).reshape(1, W.HIDDEN), out)
+    ids = host(bscratch[:2 * top_k], np.int32)
+    assert np.array_equal(ids, orc.topk(host(logits, np.float32).reshape(1, W.EXPERTS),
+                                        top_k)[0].ravel())
+
