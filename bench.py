@@ -785,7 +785,8 @@ def phase_report(tokens=8):
         raise RuntimeError("timing build's decode differs from the product library's")
     timed.q38m_phase_log_v1(None, 0, 0)
     rec = np.frombuffer(records.cpu().numpy().tobytes(), dtype=np.dtype(
-        [("stamp", "<u8", 16), ("kernel", "<u4"), ("block", "<u4"), ("call", "<u4"),
+        [("stamp", "<u8", 16), ("wave_stamp", "<u8", 16), ("kernel", "<u4"), ("block", "<u4"),
+         ("call", "<u4"),
          ("valid", "<u4")])).reshape(calls, 2, 256)
     if not rec["valid"].all():
         raise RuntimeError("phase log incomplete")
@@ -812,6 +813,27 @@ def phase_report(tokens=8):
             kname = "decode_gate_up_kernel" if k == 0 else "decode_down_kernel"
             lines.append(f"| {kname} | {name} | {med:.2f} | {last:.2f} |")
             summary[f"{k}:{i}"] = med
+    # every wave's weight arrival (gate/up: wave = route slot x K quarter,
+    # route groups {0,1,2} {3,4,5} {6,7} {8,9} on XCD pairs 0-1, 2-3, 4-5,
+    # 6-7; down: wave = route), per wave and per XCD (block % 8)
+    wave_rel = (rec["wave_stamp"].astype(np.int64) - t0[:, None, None, None]) * 10 / 1000.0
+    lines += ["", "Weight arrival per wave (each wave's own loads complete): median over "
+              "workgroups, then over calls; per XCD: the median over calls of the XCD's "
+              "latest wave.", "", "| kernel | wave | median us |", "|---|---|---:|"]
+    for k, waves in ((0, 12), (1, 10)):
+        kname = "decode_gate_up_kernel" if k == 0 else "decode_down_kernel"
+        for wv in range(waves):
+            med = float(np.median(np.median(wave_rel[:, k, :, wv], axis=1)))
+            lines.append(f"| {kname} | {wv} | {med:.2f} |")
+    lines += ["", "| kernel | XCD | latest wave us | median block's latest wave us |",
+              "|---|---|---:|---:|"]
+    for k, waves in ((0, 12), (1, 10)):
+        kname = "decode_gate_up_kernel" if k == 0 else "decode_down_kernel"
+        block_last = wave_rel[:, k, :, :waves].max(axis=2)  # [call, block]
+        for x in range(8):
+            xb = block_last[:, x::8]
+            lines.append(f"| {kname} | {x} | {float(np.median(xb.max(axis=1))):.2f} | "
+                         f"{float(np.median(np.median(xb, axis=1))):.2f} |")
     gu_end = rel[:, 0, :, 9].max(axis=1)
     dn_start = rel[:, 1, :, 0].min(axis=1)
     period = np.diff(t0) * 10 / 1000.0

@@ -28,6 +28,9 @@
  * weight loads issued, 2 mid rows quantised, 3 weights arrived, 4 route
  * partial formed, 5 route partials in LDS (every wave's), 6 end; 7-15
  * unused.
+ * wave_stamp[w]: the clock as wave w's own weight loads have all arrived
+ * (gate/up: after phase 5's barrier, 12 waves; down: after phase 3, 10
+ * waves, 12 in the decode block); 0 past the launch's last wave.
  */
 #ifndef Q38M_PHASE_H
 #define Q38M_PHASE_H
@@ -39,8 +42,9 @@ extern "C" {
 #endif
 
 typedef struct q38m_phase_record_v1 {
-    uint64_t stamp[16]; /* s_memrealtime ticks (10 ns) */
-    uint32_t kernel;    /* 0 gate/up, 1 down */
+    uint64_t stamp[16];      /* s_memrealtime ticks (10 ns) */
+    uint64_t wave_stamp[16]; /* wave w's weights arrived (0 past the last wave) */
+    uint32_t kernel;         /* 0 gate/up, 1 down */
     uint32_t block;     /* workgroup id */
     uint32_t call;      /* the call counter value */
     uint32_t valid;     /* 1 once written */

@@ -220,7 +220,8 @@ CHECK_TOKEN = 8
 
 
 class PhaseRecord(ctypes.Structure):
-    _fields_ = [("stamp", ctypes.c_uint64 * 16), ("kernel", ctypes.c_uint32),
+    _fields_ = [("stamp", ctypes.c_uint64 * 16), ("wave_stamp", ctypes.c_uint64 * 16),
+                ("kernel", ctypes.c_uint32),
                 ("block", ctypes.c_uint32), ("call", ctypes.c_uint32), ("valid", ctypes.c_uint32)]
 
 

@@ -384,14 +384,14 @@ namespace {
 
 // The run_moe sequence over one slab on a bound workspace (arguments
 // validated by the caller): top-k + int8 rows (or int8 rows of given
-// ids), plan, gate/up, mid quantisation, down, combine.
+// ids), plan, gate/up, down (quantising the mid rows as it stages them),
+// combine.
 hipError_t launch_prefill_step(const q38m_expert_weights_v1& gate_up,
                                const q38m_expert_weights_v1& down, const uint16_t* hidden,
                                const float* logits, uint32_t tokens,
                                const q38m_prefill_workspace_v1& ws,
                                const uint16_t* shared_output, const uint16_t* shared_gate,
                                uint16_t* output, hipStream_t s) {
-    const uint32_t routes = q38m::routes_v1(tokens);
     const uint32_t tasks = q38m::max_tasks_v1(tokens);
     hipError_t status = hipSuccess;
     if (logits)
@@ -405,11 +405,8 @@ hipError_t launch_prefill_step(const q38m_expert_weights_v1& gate_up,
         status = q38m::launch_gate_up(gate_up, ws.xq, ws.xs, ws.plan.packed_assignment,
                                       ws.expert_weights, ws.plan.tasks, tasks, ws.weighted_mid, s);
     if (status == hipSuccess)
-        status = q38m::launch_quantize_rows(ws.weighted_mid, routes, Q38M_INTERMEDIATE, ws.mid_q,
-                                            ws.mid_s, s);
-    if (status == hipSuccess)
-        status = q38m::launch_down(down, ws.mid_q, ws.mid_s, ws.plan.tasks, tasks,
-                                   ws.route_output, s);
+        status = q38m::launch_down_quantize(down, ws.weighted_mid, ws.mid_q, ws.mid_s,
+                                            ws.plan.tasks, tasks, ws.route_output, s);
     if (status == hipSuccess)
         status = q38m::launch_combine(ws.route_output, ws.plan.assignment_to_packed,
                                       shared_output, shared_gate, tokens, output, s);

@@ -53,7 +53,8 @@ __device__ uint32_t g_phase_calls_held;  // log capacity / 512
 std::atomic<uint32_t> g_phase_calls{0};
 
 struct PhaseStamps {
-    static constexpr uint32_t kStamps = 16u;
+    static constexpr uint32_t kStamps = 16u;  // the first wave's phases
+    static constexpr uint32_t kWaveStamps = 16u;  // one per wave: its weights arrived
     uint64_t t[kStamps];
     __device__ PhaseStamps() {
 #pragma unroll
@@ -68,14 +69,24 @@ struct PhaseStamps {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         mark(i);
     }
-    // thread 0 writes the record (a vector store under a lane branch)
-    __device__ void finish(uint32_t kernel, PhaseCall call) {
+    // every wave: the time its own loads have all arrived, into wave_lds
+    __device__ void mark_wave_loaded(uint64_t* wave_lds) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint64_t now = __builtin_amdgcn_s_memrealtime();
+        if ((threadIdx.x & 63u) == 0u) wave_lds[threadIdx.x >> 6] = now;
+    }
+    // thread 0 writes the record (a vector store under a lane branch);
+    // wave_lds (the per-wave stamps, visible after a barrier) may be null
+    __device__ void finish(uint32_t kernel, PhaseCall call, const uint64_t* wave_lds = nullptr) {
         q38m_phase_record_v1* log = g_phase_records;
         const uint32_t held = g_phase_calls_held;
         if (threadIdx.x != 0u || log == nullptr || held == 0u) return;
         q38m_phase_record_v1& r = log[(call.index % held) * 512u + 256u * kernel + blockIdx.x];
 #pragma unroll
         for (uint32_t i = 0; i < kStamps; ++i) r.stamp[i] = t[i];
+        const uint32_t waves = blockDim.x / 64u;
+        for (uint32_t i = 0; i < kWaveStamps; ++i)
+            r.wave_stamp[i] = wave_lds != nullptr && i < waves ? wave_lds[i] : 0u;
         r.kernel = kernel;
         r.block = blockIdx.x;
         r.call = call.index;
@@ -88,7 +99,8 @@ PhaseCall next_phase_call() { return PhaseCall{g_phase_calls.fetch_add(1u)}; }
 struct PhaseStamps {
     __device__ void mark(uint32_t) {}
     __device__ void mark_loaded(uint32_t) {}
-    __device__ void finish(uint32_t, PhaseCall) {}
+    __device__ void mark_wave_loaded(uint64_t*) {}
+    __device__ void finish(uint32_t, PhaseCall, const uint64_t* = nullptr) {}
 };
 
 PhaseCall next_phase_call() { return PhaseCall{0u}; }
@@ -174,6 +186,11 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     // [chain][quad]: int32 group sums, then their fp32 scales
     __shared__ uint4 xch[kChains * kQuads][2];
     __shared__ float shared_dot[4];  // kShared: g, u of channel 2b; g, u of 2b + 1
+#ifdef Q38M_PHASE_TIMESTAMPS
+    __shared__ uint64_t wave_stamp_lds[kGateUpThreads / 64u];
+#else
+    uint64_t* const wave_stamp_lds = nullptr;
+#endif
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -304,6 +321,7 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     __syncthreads();
     stamps.mark(4);
     stamps.mark_loaded(5);
+    stamps.mark_wave_loaded(wave_stamp_lds);
 
     // this lane's group sums (int32) and their scales (fp32 words)
     uint4 xa = make_uint4(0u, 0u, 0u, 0u), xf = make_uint4(0u, 0u, 0u, 0u);
@@ -430,7 +448,7 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
             static_cast<uint16_t>(m);
     }
     stamps.mark(9);
-    stamps.finish(0u, call);
+    stamps.finish(0u, call, wave_stamp_lds);
 }
 
 // kPerGroup: W4, 32-column sub-blocks per group (1, 2, 4); W8, 64-column
@@ -455,6 +473,11 @@ void decode_down_kernel(
     // route partials per output channel, ten routes padded to 12 floats
     __shared__ float4 o_lds[8][3];
     __shared__ uint32_t shared_lds[8];  // kShared: the eight shared-down words
+#ifdef Q38M_PHASE_TIMESTAMPS
+    __shared__ uint64_t wave_stamp_lds[kDecodeThreads / 64u + 2u];
+#else
+    uint64_t* const wave_stamp_lds = nullptr;
+#endif
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t route = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -473,6 +496,7 @@ void decode_down_kernel(
                 rows[j] = bf16_row_load(shared.h,
                                         shared.w_down + static_cast<size_t>(16u * tile + n0 + c0 + j) * I,
                                         I / 8u, 0u, lane);
+            stamps.mark_wave_loaded(wave_stamp_lds);
 #pragma unroll
             for (uint32_t j = 0; j < 4u; ++j) {
                 const float dot = wave_sum_f32(bf16_row_accumulate(rows[j], 0.0f));
@@ -557,6 +581,7 @@ void decode_down_kernel(
     __syncthreads();
     stamps.mark(2);
     stamps.mark_loaded(3);
+    stamps.mark_wave_loaded(wave_stamp_lds);
 
     float o = 0.0f;
     if constexpr (kW4) {
@@ -662,7 +687,7 @@ void decode_down_kernel(
         out[channel] = static_cast<uint16_t>(result);
     }
     stamps.mark(6);
-    stamps.finish(1u, call);
+    stamps.finish(1u, call, wave_stamp_lds);
 }
 
 }  // namespace

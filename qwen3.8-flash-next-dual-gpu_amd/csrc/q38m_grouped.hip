@@ -3,59 +3,74 @@
 //
 // Work decomposition: one workgroup per (task, output slice), where a task
 // is one M=16 tile of one expert from the V1 route plan.  Each wave owns a
-// 16-channel tile (gate/up: a gate tile and its matching up tile, so the
-// SwiGLU pair sits in the same lane) and streams the expert's weights
+// 16-channel tile (W4 gate/up: a gate or an up tile, the pair meeting in
+// LDS for the SwiGLU; W8 gate/up: a gate tile and its matching up tile, so
+// the SwiGLU pair sits in the same lane) and streams the expert's weights
 // straight from HBM into VGPRs in the MFMA16 layout: every wave-wide
 // 16-byte load is 1 KiB contiguous.  Tasks beyond the plan's task_count
 // carry valid_rows == 0 and exit at once (q38_moe_prefill.cu:316-317).
 #include "q38m_device.h"
 #include "q38m_internal.h"
+#include "q38m_select.h"
 
 namespace q38m {
 namespace {
 
-struct QuadWeights {
-    uint4 g, u;    // gate and up tile data of one quad
-    uint2 sg, su;  // their scale words (load_quad_scales)
+// The down kernels' A operand: the int8 mid rows and their scales (the
+// staged entry point), or -- kQuantize, the one-call step -- the bf16 mid
+// rows, which the kernel quantises itself while its first weights stream:
+// one wave per row, lane l holding elements [8l, 8l + 8), the arithmetic of
+// quantize_rows_kernel<1> (row_absmax8, wave_max_f32, quant_scale,
+// quantize8), so the int8 rows and scales are the same bit for bit.  The
+// workgroups of output slice 0 also store them to q / s, where the caller's
+// workspace keeps them.
+struct MidRows {
+    const int8_t* q;        // [routes][I] int8 (written by slice 0 when kQuantize)
+    const float* s;         // [routes] scales (likewise)
+    const uint16_t* bf16;   // kQuantize: [routes][I] bf16 rows
 };
 
-// One quad (128 columns) of the gate/up chain for one gate tile and its up
-// tile.  Per 32-wide sub-block one MFMA per tile; the kSub sub-blocks of a
-// group chain through the int32 accumulator input (the first from zero),
-// giving the group's exact 16*acc; then the fp32 chain
-// y16 = fma(16*acc, s_g, y16) (fp16 scales) or y = fma(16*acc, s_g/16, y)
-// (bf16 scales).
+// Quantise one 512-wide bf16 row held as lane l's elements [8l, 8l + 8).
+__device__ __forceinline__ uint2 quantize_mid_row(uint4 v, float& scale) {
+    const uint32_t hw[4] = {v.x, v.y, v.z, v.w};
+    const QuantScale qs = quant_scale(wave_max_f32(row_absmax8(hw)));
+    scale = qs.s;
+    return quantize8(hw, qs);
+}
+
+struct TileWeights {
+    uint4 w;   // one quad of the wave's tile
+    uint2 s;   // its scale words (load_quad_scales)
+};
+
+// One quad (128 columns) of the chain for one 16-channel tile.  Per 32-wide
+// sub-block one MFMA; the kSub sub-blocks of a group chain through the
+// int32 accumulator input (the first from zero), giving the group's exact
+// 16*acc; then the fp32 chain y16 = fma(16*acc, s_g, y16) (fp16 scales) or
+// y = fma(16*acc, s_g/16, y) (bf16 scales).
 template <uint32_t kSub, bool kBf16>
-__device__ __forceinline__ void gate_up_quad(const uint2* __restrict__ a_quad, uint4 wg, uint4 wu,
-                                             uint2 sg, uint2 su, float (&yg)[4],
-                                             float (&yu)[4]) {
+__device__ __forceinline__ void tile_quad(const uint2* __restrict__ a_quad, uint4 wt, uint2 sc,
+                                          float (&y)[4]) {
     const v4i zero = {0, 0, 0, 0};
-    const uint32_t wgw[4] = {wg.x, wg.y, wg.z, wg.w};
-    const uint32_t wuw[4] = {wu.x, wu.y, wu.z, wu.w};
-    v4i cg = zero, cu = zero;  // kSub > 1: the group's running int32 tiles
+    const uint32_t ww[4] = {wt.x, wt.y, wt.z, wt.w};
+    v4i c = zero;  // kSub > 1: the group's running int32 tile
 #pragma unroll
     for (uint32_t j = 0; j < 4u; ++j) {
         const long a = as_long(a_quad[j * 64u]);
-        const v4i dg = mfma_i8_16x16x32(a, unpack_w4x16(wgw[j]), j % kSub == 0u ? zero : cg);
-        const v4i du = mfma_i8_16x16x32(a, unpack_w4x16(wuw[j]), j % kSub == 0u ? zero : cu);
+        const v4i d = mfma_i8_16x16x32(a, unpack_w4x16(ww[j]), j % kSub == 0u ? zero : c);
         if (j % kSub != kSub - 1u) {
-            cg = dg;
-            cu = du;
+            c = d;
             continue;
         }
-        const uint32_t wsg = quad_scale_word(sg, j / kSub), wsu = quad_scale_word(su, j / kSub);
-        const float scale_g = kBf16 ? bf16_to_f32(wsg) * 0.0625f : f16_to_f32(wsg);
-        const float scale_u = kBf16 ? bf16_to_f32(wsu) * 0.0625f : f16_to_f32(wsu);
+        const uint32_t ws = quad_scale_word(sc, j / kSub);
+        const float scale = kBf16 ? bf16_to_f32(ws) * 0.0625f : f16_to_f32(ws);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            yg[i] = __builtin_fmaf(static_cast<float>(dg[i]), scale_g, yg[i]);
-            yu[i] = __builtin_fmaf(static_cast<float>(du[i]), scale_u, yu[i]);
-        }
+        for (int i = 0; i < 4; ++i) y[i] = __builtin_fmaf(static_cast<float>(d[i]), scale, y[i]);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Gate/up, W4 group-32 fp16 scales, MFMA16 layout.
+// Gate/up, W4 in groups of 32 (64, 128), MFMA16 layout.
 //   acc[r][j][g] = sum_{k in g} xq[token(r)][k] * W[e][j][k]        (int32)
 //   y[r][j]      = fmaf-chain over g = 0..H/32-1 of acc * s[e][j][g]  (fp32)
 //   then y * xs[token(r)] and the SwiGLU fold of the reference epilogue.
@@ -63,14 +78,20 @@ __device__ __forceinline__ void gate_up_quad(const uint2* __restrict__ a_quad, u
 // tile (zero accumulator), so the fp32 chain runs in group order in the
 // same lanes that hold the accumulators.
 //
-// Memory plan: a workgroup of kWaves waves covers kWaves gate tiles and
-// their up tiles of one task.  The task's 16 int8 token rows (32 KiB) are
-// staged into LDS once in the MFMA A-operand order ([group][lane], 8 bytes
-// per lane), so the waves read activations with conflict-free 512-byte
-// ds_read_b64 instead of each re-reading them from L2.  Every wave streams
-// its two weight tiles two quads ahead (4.6 KB in flight per wave); at ~70
-// VGPRs three 8-wave workgroups per CU keep ~110 KB of weights in flight,
-// what ~2 us of loaded HBM latency needs at full bandwidth.
+// Work: a workgroup of kWaves waves covers kWaves/2 channel pairs of one
+// task; wave w streams one tile -- the gate tile (w even) or the up tile (w
+// odd) of pair blockIdx.x * kWaves/2 + w/2 -- two quads ahead through three
+// register sets, and the up wave hands its chain to the gate wave through
+// LDS for the SwiGLU epilogue.  One tile per wave (not a gate + up pair)
+// halves a wave's stream (16 KiB of weights), so the slab's last
+// workgroups drain in half the time, and at ~57 VGPRs and 36 KiB of LDS
+// four workgroups (32 waves) fit per CU: config 2's step 0.2247 -> 0.2216
+// ms against the pair-per-wave form (bit-identical; two or four quads
+// ahead, or 4 / 16 waves per workgroup, measured slower).
+// The task's 16 int8 token rows (32 KiB) are staged into LDS once in the
+// MFMA A-operand order ([group][lane], 8 bytes per lane), so the waves read
+// activations with conflict-free 512-byte ds_read_b64 instead of each
+// re-reading them from L2.
 //
 // The MFMA gives 16*acc (nibbles in the high half of each byte).  fp16
 // scales: the raw scale feeds the fma, so y16 = 16*y exactly at every step
@@ -91,7 +112,10 @@ void gate_up_w4_kernel(
     constexpr uint32_t kGroups = H / 32u;
     constexpr uint32_t kTiles = 2u * I / 16u;
     constexpr uint32_t kThreads = kWaves * 64u;
+    constexpr uint32_t kDepth = 2u, kSets = kDepth + 1u;
+    static_assert(kWaves % 2u == 0u, "gate and up waves in pairs");
     __shared__ uint2 a_lds[kGroups * 64u];
+    __shared__ float up_lds[kWaves / 2u][4][64];
 
     const TaskRecord task = read_task(tasks, blockIdx.y);
     const uint32_t rows = task.rows;
@@ -100,28 +124,26 @@ void gate_up_w4_kernel(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
-    const uint32_t gate_tile = blockIdx.x * kWaves + wave;  // = the gate/up pair index
+    const uint32_t pair = blockIdx.x * (kWaves / 2u) + (wave >> 1);
+    const uint32_t up = wave & 1u;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.begin;
 
     // Paired quad-major layout: for quad kq the gate tile of pair p is slot
-    // 2p and its up tile slot 2p+1, so a workgroup's step reads one
-    // contiguous span of 2*kWaves KiB of weights and 256*kWaves B of scales.
+    // 2p and its up tile slot 2p+1 (1 KiB each, 256 B of scale words)
     constexpr uint32_t kQuadWords = kTiles * 64u;  // uint4 per quad of one expert
     constexpr uint32_t kRowScales = 4u / kSub;     // scale words per row and quad
     constexpr uint32_t kSlotScales = 16u * kRowScales;
     constexpr uint32_t kQuadScales = kTiles * kSlotScales;
     // uniform bases (scalar registers) plus 32-bit per-lane offsets
-    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * 64u;
+    const uint32_t slot = 2u * pair + up;
+    const uint4* wbase = w + (static_cast<size_t>(e) * kQuads * kTiles + slot) * 64u;
     const uint16_t* sbase =
-        s + (static_cast<size_t>(e) * kQuads * kTiles + 2u * gate_tile) * kSlotScales;
+        s + (static_cast<size_t>(e) * kQuads * kTiles + slot) * kSlotScales;
     auto load = [&](uint32_t kq) {
         const uint32_t k = kq < kQuads ? kq : kQuads - 1u;  // past the end: re-read (L1 hit)
-        const uint32_t wi = k * kQuadWords + lane;
-        const uint32_t si = k * kQuadScales + n * kRowScales;
-        return QuadWeights{load_stream(wbase + wi), load_stream(wbase + wi + 64u),
-                           load_quad_scales<kSub>(sbase + si),
-                           load_quad_scales<kSub>(sbase + si + kSlotScales)};
+        return TileWeights{load_stream(wbase + k * kQuadWords + lane),
+                           load_quad_scales<kSub>(sbase + k * kQuadScales + n * kRowScales)};
     };
 
     // Stage A: 16-byte chunk c of token row r holds group c/2 for lane groups
@@ -137,8 +159,11 @@ void gate_up_w4_kernel(
     static_assert(16u * (H / 16u) % kThreads == 0u && kThreads % 16u == 0u,
                   "whole chunks per thread, one row per thread");
     const uint32_t srow = threadIdx.x % 16u;
-    const uint32_t token = checked(packed[p0 + (srow < rows ? srow : 0u)], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
-    QuadWeights r0 = load(0), r1 = load(1), r2;
+    const uint32_t token = checked(packed[p0 + (srow < rows ? srow : 0u)],
+                                   Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
+    TileWeights r[kSets];
+#pragma unroll
+    for (uint32_t i = 0; i < kDepth; ++i) r[i] = load(i);
     const uint4* arow = reinterpret_cast<const uint4*>(xq + static_cast<size_t>(token / kTopK) * H);
     uint4 v[kChunks];
 #pragma unroll
@@ -152,39 +177,48 @@ void gate_up_w4_kernel(
     }
     __syncthreads();
 
-    float yg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float yu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    // Two quads ahead through three register sets in a fixed rotation: each
-    // load lands in the set consumed one step earlier, so no register with a
-    // load in flight is ever copied (a copy would wait for the load).  Each
-    // step issues its load before any of its math (scheduling barrier).
-    static_assert(kQuads % 3u == 1u, "three-set rotation plus one peeled quad");
+    // kDepth quads ahead through kSets register sets in a fixed rotation:
+    // each load lands in the set consumed one step earlier, so no register
+    // with a load in flight is ever copied (a copy would wait for the
+    // load).  Each step issues its load before any of its math (scheduling
+    // barrier).
+    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const uint2* a_base = a_lds + lane;
+    constexpr uint32_t kFull = kQuads / kSets * kSets;
 #pragma unroll 1
-    for (uint32_t kq = 0; kq + 3u < kQuads; kq += 3u) {
-        r2 = load(kq + 2u);
-        __builtin_amdgcn_sched_barrier(0);
-        gate_up_quad<kSub, kBf16>(a_base + 4u * kq * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
-        r0 = load(kq + 3u);
-        __builtin_amdgcn_sched_barrier(0);
-        gate_up_quad<kSub, kBf16>(a_base + 4u * (kq + 1u) * 64u, r1.g, r1.u, r1.sg, r1.su, yg, yu);
-        r1 = load(kq + 4u);
-        __builtin_amdgcn_sched_barrier(0);
-        gate_up_quad<kSub, kBf16>(a_base + 4u * (kq + 2u) * 64u, r2.g, r2.u, r2.sg, r2.su, yg, yu);
+    for (uint32_t kq = 0; kq < kFull; kq += kSets) {
+#pragma unroll
+        for (uint32_t i = 0; i < kSets; ++i) {
+            r[(i + kDepth) % kSets] = load(kq + i + kDepth);
+            __builtin_amdgcn_sched_barrier(0);
+            tile_quad<kSub, kBf16>(a_base + 4u * (kq + i) * 64u, r[i].w, r[i].s, y);
+        }
     }
-    gate_up_quad<kSub, kBf16>(a_base + 4u * (kQuads - 1u) * 64u, r0.g, r0.u, r0.sg, r0.su, yg, yu);
+#pragma unroll
+    for (uint32_t i = 0; i < kQuads - kFull; ++i) {
+        if (kFull + i + kDepth < kQuads) r[(i + kDepth) % kSets] = load(kFull + i + kDepth);
+        __builtin_amdgcn_sched_barrier(0);
+        tile_quad<kSub, kBf16>(a_base + 4u * (kFull + i) * 64u, r[i].w, r[i].s, y);
+    }
 
-    const uint32_t channel = gate_tile * 16u + n;
+    // the up wave's chain to its gate wave
+    if (up) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) up_lds[wave >> 1][i][lane] = y[i];
+    }
+    __syncthreads();
+    if (up) return;
+    const uint32_t channel = pair * 16u + n;
 #pragma unroll
     for (uint32_t i = 0; i < 4u; ++i) {
-        const uint32_t r = 4u * q + i;
-        if (r >= rows) continue;
-        const uint32_t p = p0 + r;
+        const uint32_t rr = 4u * q + i;
+        if (rr >= rows) continue;
+        const uint32_t p = p0 + rr;
         const uint32_t a = checked(packed[p], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
         const float st = xs[a / kTopK];
         const float unscale = kBf16 ? 1.0f : 0.0625f;
-        const float y_gate = (yg[i] * unscale) * st;
-        const float y_up = (yu[i] * unscale) * st;
+        const float y_gate = (y[i] * unscale) * st;
+        const float y_up = (up_lds[wave >> 1][i][lane] * unscale) * st;
         mid[static_cast<size_t>(p) * I + channel] =
             static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
     }
@@ -349,10 +383,9 @@ void gate_up_w8_kernel(
 // per SIMD keep ~128 KB of weights in flight per CU.
 // ---------------------------------------------------------------------------
 template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave,
-          uint32_t kBlocksPerGroup, bool kBf16>
+          uint32_t kBlocksPerGroup, bool kBf16, bool kQuantize>
 __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
-    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
-    const int8_t* __restrict__ mq, const float* __restrict__ ms,
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s, MidRows mid,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
     constexpr uint32_t kBlocks = I / 64u;
     constexpr uint32_t kHalf = kBlocks / 2u;
@@ -363,6 +396,7 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     static_assert(kBlocks % 2u == 0u, "half-tile units");
     static_assert(kPerChannel || kHalf % kBlocksPerGroup == 0u, "groups within half tiles");
     __shared__ uint4 a_lds[kBlocks * 64u];
+    __shared__ float scale_lds[16];  // kQuantize: the rows' scales
 
     const TaskRecord task = read_task(tasks, blockIdx.y);
     const uint32_t rows = task.rows;
@@ -381,33 +415,67 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     // weights, so the LDS stores wait for the rows only.
     constexpr uint32_t kStage = 16u * (I / 16u) / kThreads;
     static_assert(16u * (I / 16u) % kThreads == 0u, "whole row chunks per thread");
-    // piece i: row i % 16, chunk i / 16 (consecutive lanes, consecutive
-    // rows: the LDS stores fall in distinct banks)
-    uint4 av[kStage];
-#pragma unroll
-    for (uint32_t u = 0; u < kStage; ++u) {
-        const uint32_t i = threadIdx.x + u * kThreads;
-        const uint32_t r = i % 16u;
-        av[u] = reinterpret_cast<const uint4*>(
-            mq + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[i / 16u];
-    }
-    uint4 b[kHalf];
-#pragma unroll
-    for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (uint32_t u = 0; u < kStage; ++u) {
-        const uint32_t i = threadIdx.x + u * kThreads;
-        const uint32_t chunk = i / 16u;
-        a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + i % 16u] = av[u];
-    }
+    constexpr uint32_t kRowsPerWave = 16u / kWaves;  // kQuantize: whole rows per wave
+    static_assert(!kQuantize || (I == 512u && 16u % kWaves == 0u), "one wave per 512-wide row");
     float row_scale[4];
+    uint4 b[kHalf];
+    if constexpr (kQuantize) {
+        uint4 mv[kRowsPerWave];
 #pragma unroll
-    for (uint32_t i = 0; i < 4u; ++i) {
-        const uint32_t r = 4u * q + i;
-        row_scale[i] = ms[p0 + (r < rows ? r : 0u)];
+        for (uint32_t j = 0; j < kRowsPerWave; ++j) {
+            const uint32_t r = wave * kRowsPerWave + j;
+            mv[j] = reinterpret_cast<const uint4*>(
+                mid.bf16 + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[lane];
+        }
+#pragma unroll
+        for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t j = 0; j < kRowsPerWave; ++j) {
+            const uint32_t r = wave * kRowsPerWave + j;
+            float scale;
+            const uint2 qv = quantize_mid_row(mv[j], scale);
+            // lane l holds half of 16-byte chunk l/2
+            const uint32_t chunk = lane >> 1;
+            reinterpret_cast<uint2*>(a_lds)[2u * ((chunk >> 2) * 64u + (chunk & 3u) * 16u + r) +
+                                            (lane & 1u)] = qv;
+            if (lane == 0u) scale_lds[r] = scale;
+            if (blockIdx.x == 0u && r < rows) {
+                reinterpret_cast<uint2*>(const_cast<int8_t*>(mid.q) +
+                                         static_cast<size_t>(p0 + r) * I)[lane] = qv;
+                if (lane == 0u) const_cast<float*>(mid.s)[p0 + r] = scale;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) row_scale[i] = scale_lds[4u * q + i];
+    } else {
+        // piece i: row i % 16, chunk i / 16 (consecutive lanes, consecutive
+        // rows: the LDS stores fall in distinct banks)
+        uint4 av[kStage];
+#pragma unroll
+        for (uint32_t u = 0; u < kStage; ++u) {
+            const uint32_t i = threadIdx.x + u * kThreads;
+            const uint32_t r = i % 16u;
+            av[u] = reinterpret_cast<const uint4*>(
+                mid.q + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[i / 16u];
+        }
+#pragma unroll
+        for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t u = 0; u < kStage; ++u) {
+            const uint32_t i = threadIdx.x + u * kThreads;
+            const uint32_t chunk = i / 16u;
+            a_lds[(chunk >> 2) * 64u + (chunk & 3u) * 16u + i % 16u] = av[u];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 4u * q + i;
+            row_scale[i] = mid.s[p0 + (r < rows ? r : 0u)];
+        }
+        __syncthreads();
     }
-    __syncthreads();
 
     const v4i zero = {0, 0, 0, 0};
 #pragma unroll
@@ -473,14 +541,19 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
 // group; the all-W4 layer policy): the gate/up group chain over K = I, then
 // * sm[r].
 // ---------------------------------------------------------------------------
-template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kSub, bool kBf16>
+template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kSub, bool kBf16,
+          bool kQuantize>
 __global__ __launch_bounds__(256) void down_w4_kernel(
-    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
-    const int8_t* __restrict__ mq, const float* __restrict__ ms,
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s, MidRows mid,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
     constexpr uint32_t kQuads = I / 128u;
     constexpr uint32_t kTiles = H / 16u;
     constexpr uint32_t kRowScales = 4u / kSub;
+    constexpr uint32_t kGroups = kQuads * 4u;  // 32-wide K groups
+    // kQuantize: the int8 rows in the MFMA A order, [group][lane] (lane
+    // n + 16q: row n, columns 32g + 8q ..+7), and the rows' scales
+    __shared__ uint2 a_lds[kQuantize ? kGroups * 64u : 1u];
+    __shared__ float scale_lds[16];
     const TaskRecord task = read_task(tasks, blockIdx.y);
     const uint32_t rows = task.rows;
     if (rows == 0u) return;
@@ -490,16 +563,48 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
     const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.begin;
-    const uint32_t a_row = n < rows ? n : 0u;
-    const uint2* xa = reinterpret_cast<const uint2*>(mq + static_cast<size_t>(p0 + a_row) * I) + q;
-    long a[kQuads * 4u];
-#pragma unroll
-    for (uint32_t g = 0; g < kQuads * 4u; ++g) a[g] = as_long(xa[g * 4u]);
+    long a[kGroups];
     float row_scale[4];
+    if constexpr (kQuantize) {
+        static_assert(I == 512u, "one wave per 512-wide row");
+        constexpr uint32_t kRowsPerWave = 4u;  // 16 rows over 4 waves
+        uint4 mv[kRowsPerWave];
 #pragma unroll
-    for (uint32_t i = 0; i < 4u; ++i) {
-        const uint32_t r = 4u * q + i;
-        row_scale[i] = ms[p0 + (r < rows ? r : 0u)];
+        for (uint32_t j = 0; j < kRowsPerWave; ++j) {
+            const uint32_t r = wave * kRowsPerWave + j;
+            mv[j] = reinterpret_cast<const uint4*>(
+                mid.bf16 + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[lane];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kRowsPerWave; ++j) {
+            const uint32_t r = wave * kRowsPerWave + j;
+            float scale;
+            const uint2 qv = quantize_mid_row(mv[j], scale);
+            // lane l holds columns 8l..8l+7: group l/4, lane group l%4
+            a_lds[(lane >> 2) * 64u + 16u * (lane & 3u) + r] = qv;
+            if (lane == 0u) scale_lds[r] = scale;
+            if (blockIdx.x == 0u && r < rows) {
+                reinterpret_cast<uint2*>(const_cast<int8_t*>(mid.q) +
+                                         static_cast<size_t>(p0 + r) * I)[lane] = qv;
+                if (lane == 0u) const_cast<float*>(mid.s)[p0 + r] = scale;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t g = 0; g < kGroups; ++g) a[g] = as_long(a_lds[g * 64u + lane]);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) row_scale[i] = scale_lds[4u * q + i];
+    } else {
+        const uint32_t a_row = n < rows ? n : 0u;
+        const uint2* xa =
+            reinterpret_cast<const uint2*>(mid.q + static_cast<size_t>(p0 + a_row) * I) + q;
+#pragma unroll
+        for (uint32_t g = 0; g < kGroups; ++g) a[g] = as_long(xa[g * 4u]);
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t r = 4u * q + i;
+            row_scale[i] = mid.s[p0 + (r < rows ? r : 0u)];
+        }
     }
     const v4i zero = {0, 0, 0, 0};
     const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
@@ -612,7 +717,7 @@ void launch_gate_up_sub(const q38m_expert_weights_v1& w, const int8_t* xq, const
                         const q38m_task_v1* tasks, uint32_t task_count, uint16_t* weighted_mid,
                         hipStream_t stream) {
     constexpr uint32_t kWaves = 8;
-    const dim3 grid(kInter / 16u / kWaves, task_count);
+    const dim3 grid(kInter / 16u / (kWaves / 2u), task_count);
     const auto* data = static_cast<const uint4*>(w.data);
     const auto* scales = static_cast<const uint16_t*>(w.scales);
     if (w.scale_dtype == Q38M_SCALE_BF16)
@@ -642,36 +747,65 @@ void launch_gate_up_w8_groups(const q38m_expert_weights_v1& w, const int8_t* xq,
                                                 weighted_mid);
 }
 
-template <uint32_t kBlocksPerGroup>
-void launch_down_w8_groups(const q38m_expert_weights_v1& w, const int8_t* mid_q,
-                           const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+template <uint32_t kBlocksPerGroup, bool kQuantize>
+void launch_down_w8_groups(const q38m_expert_weights_v1& w, const MidRows& mid,
+                           const q38m_task_v1* tasks, uint32_t task_count,
                            float* route_output, hipStream_t stream) {
     constexpr uint32_t kWaves = 8, kTilesPerWave = 2;
     const dim3 grid(kHidden / 16u / (kWaves * kTilesPerWave), task_count);
     const auto* data = static_cast<const uint4*>(w.data);
     const auto* scales = static_cast<const uint16_t*>(w.scales);
     if (w.scale_dtype == Q38M_SCALE_BF16)
-        down_w8_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, true>
-            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid_q, mid_s, tasks, route_output);
+        down_w8_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, true, kQuantize>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid, tasks, route_output);
     else
-        down_w8_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, false>
-            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid_q, mid_s, tasks, route_output);
+        down_w8_kernel<kHidden, kInter, kWaves, kTilesPerWave, kBlocksPerGroup, false, kQuantize>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid, tasks, route_output);
 }
 
-template <uint32_t kSub>
-void launch_down_w4_sub(const q38m_expert_weights_v1& w, const int8_t* mid_q,
-                        const float* mid_s, const q38m_task_v1* tasks, uint32_t task_count,
+template <uint32_t kSub, bool kQuantize>
+void launch_down_w4_sub(const q38m_expert_weights_v1& w, const MidRows& mid,
+                        const q38m_task_v1* tasks, uint32_t task_count,
                         float* route_output, hipStream_t stream) {
     constexpr uint32_t kTilesPerWave = 4;
     const dim3 grid(kHidden / 16u / (4u * kTilesPerWave), task_count);
     const auto* data = static_cast<const uint4*>(w.data);
     const auto* scales = static_cast<const uint16_t*>(w.scales);
     if (w.scale_dtype == Q38M_SCALE_BF16)
-        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, true><<<grid, 256, 0, stream>>>(
-            data, scales, mid_q, mid_s, tasks, route_output);
+        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, true, kQuantize>
+            <<<grid, 256, 0, stream>>>(data, scales, mid, tasks, route_output);
     else
-        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, false><<<grid, 256, 0, stream>>>(
-            data, scales, mid_q, mid_s, tasks, route_output);
+        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, false, kQuantize>
+            <<<grid, 256, 0, stream>>>(data, scales, mid, tasks, route_output);
+}
+
+template <bool kQuantize>
+hipError_t launch_down_rows(const q38m_expert_weights_v1& w, const MidRows& mid,
+                            const q38m_task_v1* tasks, uint32_t task_count,
+                            float* route_output, hipStream_t stream) {
+    constexpr uint32_t kBlocks = kInter / 64u;
+    if (w.format == Q38M_FORMAT_W8_SYM) {
+        switch (w.group_size) {
+            case 0u: launch_down_w8_groups<kBlocks, kQuantize>(w, mid, tasks, task_count,
+                                                               route_output, stream); break;
+            case 64u: launch_down_w8_groups<1, kQuantize>(w, mid, tasks, task_count,
+                                                          route_output, stream); break;
+            case 128u: launch_down_w8_groups<2, kQuantize>(w, mid, tasks, task_count,
+                                                           route_output, stream); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        switch (w.group_size) {
+            case 32u: launch_down_w4_sub<1, kQuantize>(w, mid, tasks, task_count, route_output,
+                                                       stream); break;
+            case 64u: launch_down_w4_sub<2, kQuantize>(w, mid, tasks, task_count, route_output,
+                                                       stream); break;
+            case 128u: launch_down_w4_sub<4, kQuantize>(w, mid, tasks, task_count, route_output,
+                                                        stream); break;
+            default: return hipErrorInvalidValue;
+        }
+    }
+    return hipGetLastError();
 }
 
 }  // namespace
@@ -708,29 +842,15 @@ hipError_t launch_gate_up(const q38m_expert_weights_v1& w, const int8_t* xq, con
 hipError_t launch_down(const q38m_expert_weights_v1& w, const int8_t* mid_q, const float* mid_s,
                        const q38m_task_v1* tasks, uint32_t task_count, float* route_output,
                        hipStream_t stream) {
-    constexpr uint32_t kBlocks = kInter / 64u;
-    if (w.format == Q38M_FORMAT_W8_SYM) {
-        switch (w.group_size) {
-            case 0u: launch_down_w8_groups<kBlocks>(w, mid_q, mid_s, tasks, task_count,
-                                                    route_output, stream); break;
-            case 64u: launch_down_w8_groups<1>(w, mid_q, mid_s, tasks, task_count, route_output,
-                                               stream); break;
-            case 128u: launch_down_w8_groups<2>(w, mid_q, mid_s, tasks, task_count, route_output,
-                                                stream); break;
-            default: return hipErrorInvalidValue;
-        }
-    } else {
-        switch (w.group_size) {
-            case 32u: launch_down_w4_sub<1>(w, mid_q, mid_s, tasks, task_count, route_output,
-                                            stream); break;
-            case 64u: launch_down_w4_sub<2>(w, mid_q, mid_s, tasks, task_count, route_output,
-                                            stream); break;
-            case 128u: launch_down_w4_sub<4>(w, mid_q, mid_s, tasks, task_count, route_output,
-                                             stream); break;
-            default: return hipErrorInvalidValue;
-        }
-    }
-    return hipGetLastError();
+    return launch_down_rows<false>(w, MidRows{mid_q, mid_s, nullptr}, tasks, task_count,
+                                   route_output, stream);
+}
+
+hipError_t launch_down_quantize(const q38m_expert_weights_v1& w, const uint16_t* weighted_mid,
+                                int8_t* mid_q, float* mid_s, const q38m_task_v1* tasks,
+                                uint32_t task_count, float* route_output, hipStream_t stream) {
+    return launch_down_rows<true>(w, MidRows{mid_q, mid_s, weighted_mid}, tasks, task_count,
+                                  route_output, stream);
 }
 
 hipError_t launch_combine(const float* route_output, const uint32_t* inverse,

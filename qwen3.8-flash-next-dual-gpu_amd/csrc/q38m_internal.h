@@ -113,6 +113,12 @@ hipError_t launch_gate_up(const q38m_expert_weights_v1& w, const int8_t* xq, con
 hipError_t launch_down(const q38m_expert_weights_v1& w, const int8_t* mid_q, const float* mid_s,
                        const q38m_task_v1* tasks, uint32_t task_count, float* route_output,
                        hipStream_t stream);
+// down from the bf16 mid rows: each task's rows quantised inside the kernel
+// (the same int8 rows and scales as launch_quantize_rows, also stored to
+// mid_q / mid_s)
+hipError_t launch_down_quantize(const q38m_expert_weights_v1& w, const uint16_t* weighted_mid,
+                                int8_t* mid_q, float* mid_s, const q38m_task_v1* tasks,
+                                uint32_t task_count, float* route_output, hipStream_t stream);
 hipError_t launch_combine(const float* route_output, const uint32_t* inverse,
                           const uint16_t* shared_output, const uint16_t* shared_gate,
                           uint32_t tokens, uint16_t* output, hipStream_t stream);

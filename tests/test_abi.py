@@ -64,7 +64,7 @@ def test_timed_library_is_the_product_plus_the_phase_log(q38m):
     phase = declared_functions(HEADERS[2:3])
     assert phase == ["q38m_phase_calls_v1", "q38m_phase_log_v1"]
     assert exported_functions(q38m.TIMED_LIB_PATH) == sorted(declared_functions() + phase)
-    assert ctypes.sizeof(q38m.PhaseRecord) == 144
+    assert ctypes.sizeof(q38m.PhaseRecord) == 272
     lib = q38m.timed_lib()
     # capacity must be a multiple of 512 records, and null with zero
     assert lib.q38m_phase_log_v1(None, 512, 0) == q38m.ERR_INVALID_ARGUMENT
