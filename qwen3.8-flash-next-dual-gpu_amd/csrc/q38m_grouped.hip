@@ -563,6 +563,21 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
     const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.begin;
+    // quad-major layout: quad kq of tile t is unit (e*kQuads + kq)*kTiles + t;
+    // a tile's four quads are requested together, one tile ahead, the first
+    // tile's before the A rows are staged
+    const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
+    auto load_tile = [&](uint32_t t, uint4 (&b)[kQuads], uint2 (&c)[kQuads]) {
+        const size_t unit = static_cast<size_t>(e) * kQuads * kTiles + tile0 + t;
+#pragma unroll
+        for (uint32_t kq = 0; kq < kQuads; ++kq) {
+            b[kq] = load_stream(w + (unit + kq * kTiles) * 64u + lane);
+            c[kq] = load_quad_scales<kSub>(s + ((unit + kq * kTiles) * 16u + n) * kRowScales);
+        }
+    };
+    uint4 wb[kTilesPerWave][kQuads];
+    uint2 wc[kTilesPerWave][kQuads];
+    load_tile(0, wb[0], wc[0]);
     long a[kGroups];
     float row_scale[4];
     if constexpr (kQuantize) {
@@ -607,31 +622,26 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
         }
     }
     const v4i zero = {0, 0, 0, 0};
-    const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
+#pragma unroll
     for (uint32_t t = 0; t < kTilesPerWave; ++t) {
-        const uint32_t tile = tile0 + t;
-        // quad-major layout: quad kq of tile t is unit (e*kQuads + kq)*kTiles + t
-        const uint4* wt = w + (static_cast<size_t>(e) * kQuads * kTiles + tile) * 64u + lane;
-        const uint16_t* st =
-            s + ((static_cast<size_t>(e) * kQuads * kTiles + tile) * 16u + n) * kRowScales;
+        if (t + 1u < kTilesPerWave) load_tile(t + 1u, wb[t + 1u], wc[t + 1u]);
         float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (uint32_t kq = 0; kq < kQuads; ++kq) {
-            const uint4 b = load_stream(wt + kq * kTiles * 64u);
-            const uint2 c = load_quad_scales<kSub>(st + kq * kTiles * 16u * kRowScales);
-            const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+            const uint32_t bw[4] = {wb[t][kq].x, wb[t][kq].y, wb[t][kq].z, wb[t][kq].w};
             v4i d = zero;
 #pragma unroll
             for (uint32_t j = 0; j < 4u; ++j) {
                 d = mfma_i8_16x16x32(a[kq * 4u + j], unpack_w4x16(bw[j]), j % kSub == 0u ? zero : d);
                 if (j % kSub != kSub - 1u) continue;
-                const float scale = scale_to_f32(quad_scale_word(c, j / kSub), kBf16) * 0.0625f;
+                const float scale =
+                    scale_to_f32(quad_scale_word(wc[t][kq], j / kSub), kBf16) * 0.0625f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     y[i] = __builtin_fmaf(static_cast<float>(d[i]), scale, y[i]);
             }
         }
-        const uint32_t channel = tile * 16u + n;
+        const uint32_t channel = (tile0 + t) * 16u + n;
 #pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) {
             const uint32_t r = 4u * q + i;
