@@ -210,12 +210,13 @@ __global__ __launch_bounds__(kSelectThreads) void route_quantize_kernel(
 // expert over every route (O(routes * experts) LDS compares, then a serial
 // prefix on lane 0; q38_moe_prefill.cu:198-233).  Here:
 //   1. each wave owns a contiguous segment of assignments and, 64 at a time,
-//      finds lanes with equal expert ids with nine ballots (one per id bit);
-//      the stable rank inside the segment is the popcount of equal lanes
-//      below plus the wave's running per-expert count in LDS;
+//      finds the lanes with equal expert ids through an LDS table of lane
+//      masks (each lane ORs its bit into its id's slot, reads it back and
+//      clears it); the stable rank inside the segment is the popcount of
+//      equal lanes below plus the wave's running per-expert count in LDS;
 //   2. a per-expert exclusive scan over the 16 wave histograms gives each
 //      wave's base inside its expert;
-//   3. a 512-wide scan (wave prefix + wave totals) gives expert and task
+//   3. a 512-wide scan (DPP wave prefix + wave totals) gives expert and task
 //      offsets;
 //   4. scatter: packed = offset[e] + wave_base[w][e] + local rank.
 // The result is the stable counting sort of the reference, byte for byte.
@@ -223,6 +224,8 @@ __global__ __launch_bounds__(kSelectThreads) void route_quantize_kernel(
 constexpr uint32_t kPlanThreads = 1024;
 constexpr uint32_t kPlanWaves = kPlanThreads / 64;
 constexpr uint32_t kMaxRoutes = kSlabMaxTokens * kTopK;
+static_assert(kMaxRoutes / kPlanWaves <= 512u && kPlanWaves <= 128u,
+              "a local rank and its wave share 16 bits");
 
 __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     const int32_t* __restrict__ expert_ids, uint32_t tokens,
@@ -243,13 +246,8 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     const uint32_t wave = tid >> 6;
     const uint32_t routes = tokens * kTopK;
 
-    if (tid == 0) invalid = 0u;
-    static_assert(kPlanWaves * kExperts * 2u == kPlanThreads * 16u, "one 16-byte clear per thread");
-    reinterpret_cast<uint4*>(&hist[0][0])[tid] = make_uint4(0u, 0u, 0u, 0u);
-    for (uint32_t i = tid; i < kPlanWaves * (kExperts + 1u); i += kPlanThreads)
-        (&peers[0][0])[i] = 0ull;
-    __syncthreads();
-    // every id load is issued before the first is used (one round trip)
+    // every id load is issued first (one round trip), the LDS tables are
+    // cleared while they are in flight
     constexpr uint32_t kPerThread = (kMaxRoutes + kPlanThreads - 1u) / kPlanThreads;
     int32_t loaded[kPerThread];
 #pragma unroll
@@ -257,6 +255,13 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
         const uint32_t a = tid + i * kPlanThreads;
         loaded[i] = a < routes ? expert_ids[a] : 0;
     }
+    if (tid == 0) invalid = 0u;
+    static_assert(kPlanWaves * kExperts * 2u == kPlanThreads * 16u, "one 16-byte clear per thread");
+    reinterpret_cast<uint4*>(&hist[0][0])[tid] = make_uint4(0u, 0u, 0u, 0u);
+    for (uint32_t i = tid; i < kPlanWaves * (kExperts + 1u); i += kPlanThreads)
+        (&peers[0][0])[i] = 0ull;
+    // LDS only: the id loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
     for (uint32_t i = 0; i < kPerThread; ++i) {
         const uint32_t a = tid + i * kPlanThreads;
@@ -298,7 +303,8 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
         table[slot] = 0ull;
         const uint32_t below = __popcll(equal & below_mask);
         const uint32_t running = valid ? hist[wave][k] : 0u;
-        if (valid) local_rank[a] = static_cast<uint16_t>(running + below);
+        // the rank inside the segment (< 512) and the wave above it
+        if (valid) local_rank[a] = static_cast<uint16_t>((wave << 9) | (running + below));
         if (valid && below == 0u)
             hist[wave][k] = static_cast<uint16_t>(running + __popcll(equal));
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -327,17 +333,8 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     if (tid < kExperts) {
         count = counts[tid];
         tasks = (count + kMmqM - 1u) / kMmqM;
-        inc_count = count;
-        inc_tasks = tasks;
-#pragma unroll
-        for (int offset = 1; offset < 64; offset <<= 1) {
-            const uint32_t oc = __shfl_up(inc_count, offset, 64);
-            const uint32_t ot = __shfl_up(inc_tasks, offset, 64);
-            if (lane >= static_cast<uint32_t>(offset)) {
-                inc_count += oc;
-                inc_tasks += ot;
-            }
-        }
+        inc_count = wave_inclusive_sum(count);
+        inc_tasks = wave_inclusive_sum(tasks);
         const uint64_t active = __ballot(count != 0u);
         if (lane == 63u) {
             wave_totals[0][wave] = inc_count;
@@ -402,8 +399,8 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
             plan.assignment_to_packed[a] = a;
             continue;
         }
-        const uint32_t w = a / segment;
-        const uint32_t position = offsets[k] + hist[w][k] + local_rank[a];
+        const uint32_t lr = local_rank[a];
+        const uint32_t position = offsets[k] + hist[lr >> 9][k] + (lr & 511u);
         plan.packed_assignment[position] = a;
         plan.assignment_to_packed[a] = position;
     }

@@ -54,6 +54,20 @@ __device__ __forceinline__ uint32_t group8_sum(uint32_t x) {
     return x;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave by DPP alone: row_shr
+// 1, 2, 4, 8 within each 16-lane row (lanes shifted in from outside the
+// row add 0), then row_bcast:15 (each row's last lane into the next row,
+// rows 1 and 3) and row_bcast:31 (lane 31 into rows 2 and 3).
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t x) {
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x111, 0xf, 0xf, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x112, 0xf, 0xf, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x114, 0xf, 0xf, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x118, 0xf, 0xf, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x142, 0xa, 0xf, false));
+    x += static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x143, 0xc, 0xf, false));
+    return x;
+}
+
 // Reductions over the 64 lanes of a wave without LDS round trips: the quad
 // and row steps by DPP (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
 // row_mirror), then row pairs and wave halves by the permlane swaps (with
