@@ -24,6 +24,7 @@
 // kernel is VALU-bound (~1/4 of int8 MFMA peak); down W8 is MFMA/HBM-bound.
 #include "q38m_device.h"
 #include "q38m_internal.h"
+#include "q38m_select.h"
 
 namespace q38m {
 namespace {
@@ -66,6 +67,9 @@ __global__ __launch_bounds__(256) void wide_count_kernel(const int32_t* __restri
 // One workgroup of 512 threads, thread e = expert e.  Turns the per-chunk
 // counts into per-chunk bases within each expert's segment (in place) and
 // writes the plan's counts, offsets, task offsets, tasks and header.
+constexpr uint32_t kMaxChunks = (Q38M_WIDE_MAX_TOKENS * kTopK + kWideChunkRoutes - 1u) /
+                                kWideChunkRoutes;
+
 __global__ __launch_bounds__(512) void wide_scan_kernel(uint32_t* __restrict__ chunk_counts,
                                                         uint32_t chunks, uint32_t tokens,
                                                         q38m_route_plan_v1 plan,
@@ -76,34 +80,46 @@ __global__ __launch_bounds__(512) void wide_scan_kernel(uint32_t* __restrict__ c
     __shared__ uint32_t task_offsets[kExperts + 1u];
     __shared__ uint32_t invalid;
     const uint32_t e = threadIdx.x;
+    const uint32_t tid = e;
     const uint32_t lane = e & 63u;
     const uint32_t wave = e >> 6;
     const uint32_t routes = tokens * kTopK;
 
     // 1. running count of expert e over the chunks, in chunk order; each
-    // chunk's slot becomes the expert's count in the chunks before it.  The
-    // loads of 32 chunks are issued before their sums, unconditionally (a
-    // chunk past the last re-reads the last one and adds nothing), so no
-    // branch sits between a load and the wait for it.  (Passes of 80 save
-    // ~2 µs at 160 chunks and cost ~2.6 µs at 20.)
+    // chunk's slot becomes the expert's count in the chunks before it.
+    // Batches of 32 chunks, the next batch's loads issued before this
+    // batch's sums (two batches in flight), unconditionally (a chunk past
+    // the last re-reads the last one and adds nothing), so no branch sits
+    // between a load and the wait for it.  (One batch at a time: ~9.5 us at
+    // 160 chunks, a round trip each.)
     constexpr uint32_t kBatch = 32;
-    uint32_t count = 0;
-    for (uint32_t c0 = 0; c0 < chunks; c0 += kBatch) {
-        uint32_t v[kBatch];
+    auto load_batch = [&](uint32_t c0, uint32_t (&v)[kBatch]) {
 #pragma unroll
         for (uint32_t j = 0; j < kBatch; ++j)
             v[j] = chunk_counts[static_cast<size_t>(min(c0 + j, chunks - 1u)) * kCountSlots + e];
+    };
+    uint32_t count = 0;
+    uint32_t va[kBatch], vb[kBatch];
+    load_batch(0u, va);
+    for (uint32_t c0 = 0; c0 < chunks; c0 += 2u * kBatch) {
+        load_batch(c0 + kBatch, vb);
 #pragma unroll
         for (uint32_t j = 0; j < kBatch; ++j) {
             const bool live = c0 + j < chunks;
             if (live) chunk_counts[static_cast<size_t>(c0 + j) * kCountSlots + e] = count;
-            count += live ? v[j] : 0u;
+            count += live ? va[j] : 0u;
+        }
+        if (c0 + kBatch >= chunks) break;  // uniform
+        load_batch(c0 + 2u * kBatch, va);
+#pragma unroll
+        for (uint32_t j = 0; j < kBatch; ++j) {
+            const bool live = c0 + kBatch + j < chunks;
+            if (live) chunk_counts[static_cast<size_t>(c0 + kBatch + j) * kCountSlots + e] = count;
+            count += live ? vb[j] : 0u;
         }
     }
     // invalid ids: wave 0 sums slot 512 of every chunk (at most 160, three
     // unconditional loads per lane, one round trip)
-    constexpr uint32_t kMaxChunks = (Q38M_WIDE_MAX_TOKENS * kTopK + kWideChunkRoutes - 1u) /
-                                    kWideChunkRoutes;
     static_assert(kMaxChunks <= 192u, "three invalid-slot loads per lane");
     if (wave == 0u) {
         uint32_t bad[3];
@@ -114,67 +130,79 @@ __global__ __launch_bounds__(512) void wide_scan_kernel(uint32_t* __restrict__ c
         uint32_t sum = 0;
 #pragma unroll
         for (uint32_t j = 0; j < 3u; ++j) sum += lane + 64u * j < chunks ? bad[j] : 0u;
-#pragma unroll
-        for (int offset = 32; offset > 0; offset >>= 1) sum += __shfl_xor(sum, offset, 64);
-        if (lane == 0u) invalid = sum;
+        sum = wave_inclusive_sum(sum);
+        if (lane == 63u) invalid = sum;
     }
-    plan.expert_counts[e] = static_cast<uint16_t>(count);
+    const uint32_t tasks = (count + kWideRows - 1u) / kWideRows;
 
     // 2. exclusive scans of counts and task counts over experts
-    const uint32_t tasks = (count + kWideRows - 1u) / kWideRows;
-    uint32_t inc_count = count, inc_tasks = tasks;
+    {
+        plan.expert_counts[e] = static_cast<uint16_t>(count);
+        const uint32_t inc_count = wave_inclusive_sum(count);
+        const uint32_t inc_tasks = wave_inclusive_sum(tasks);
+        const uint64_t active = __ballot(count != 0u);
+        if (lane == 63u) {
+            wave_totals[0][wave] = inc_count;
+            wave_totals[1][wave] = inc_tasks;
+        }
+        if (lane == 0u) wave_active[wave] = __popcll(active);
+        // inclusive values kept for after the barrier
+        offsets[e] = inc_count;
+        task_offsets[e] = inc_tasks;
+    }
+    __syncthreads();
+    {
+        uint32_t prefix_count = 0, prefix_tasks = 0;
 #pragma unroll
-    for (int offset = 1; offset < 64; offset <<= 1) {
-        const uint32_t oc = __shfl_up(inc_count, offset, 64);
-        const uint32_t ot = __shfl_up(inc_tasks, offset, 64);
-        if (lane >= static_cast<uint32_t>(offset)) {
-            inc_count += oc;
-            inc_tasks += ot;
+        for (uint32_t w = 0; w < 8u; ++w) {
+            prefix_count += w < wave ? wave_totals[0][w] : 0u;
+            prefix_tasks += w < wave ? wave_totals[1][w] : 0u;
+        }
+        const uint32_t offset = prefix_count + offsets[e] - count;
+        const uint32_t task_offset = prefix_tasks + task_offsets[e] - tasks;
+        plan.expert_offsets[e] = offset;
+        plan.expert_task_offsets[e] = task_offset;
+        if (e == kExperts - 1u) {
+            plan.expert_offsets[kExperts] = prefix_count + offsets[e];
+            plan.expert_task_offsets[kExperts] = prefix_tasks + task_offsets[e];
+        }
+        // every read of offsets[] above precedes the writes below (one
+        // thread reads and writes only its own slot)
+        offsets[e] = offset;
+        task_offsets[e] = task_offset;
+        if (e == kExperts - 1u) {
+            offsets[kExperts] = offset + count;
+            task_offsets[kExperts] = task_offset + tasks;
         }
     }
-    const uint64_t active = __ballot(count != 0u);
-    if (lane == 63u) {
-        wave_totals[0][wave] = inc_count;
-        wave_totals[1][wave] = inc_tasks;
-    }
-    if (lane == 0u) wave_active[wave] = __popcll(active);
     __syncthreads();
-    uint32_t prefix_count = 0, prefix_tasks = 0;
-#pragma unroll
-    for (uint32_t w = 0; w < 8u; ++w) {
-        prefix_count += w < wave ? wave_totals[0][w] : 0u;
-        prefix_tasks += w < wave ? wave_totals[1][w] : 0u;
-    }
-    const uint32_t offset = prefix_count + inc_count - count;
-    const uint32_t task_offset = prefix_tasks + inc_tasks - tasks;
-    offsets[e] = offset;
-    task_offsets[e] = task_offset;
-    if (e == kExperts - 1u) {
-        offsets[kExperts] = prefix_count + inc_count;
-        task_offsets[kExperts] = prefix_tasks + inc_tasks;
-    }
-    __syncthreads();
-    plan.expert_offsets[e] = offset;
-    plan.expert_task_offsets[e] = task_offset;
-    if (e == 0u) {
-        plan.expert_offsets[kExperts] = offsets[kExperts];
-        plan.expert_task_offsets[kExperts] = task_offsets[kExperts];
-    }
     const uint32_t total = offsets[kExperts];
     const uint32_t task_total = task_offsets[kExperts];
 
-    // 3. tasks: 128-row tiles of each expert's segment, zero past the count
+    // 3. tasks: 128-row tiles of each expert's segment, zero past the count.
+    // Spread over the threads (a Zipf-hot expert has hundreds of tasks, and
+    // one thread per expert took ~12 us at 32,768 tokens): task t's expert
+    // is the last e with task_offsets[e] <= t, by binary search in LDS.
     uint2* task_words = reinterpret_cast<uint2*>(plan.tasks);
-    for (uint32_t t = 0; t < tasks; ++t) {
-        const uint32_t remaining = count - t * kWideRows;
-        const uint32_t rows = remaining < kWideRows ? remaining : kWideRows;
-        task_words[task_offset + t] = make_uint2(offset + t * kWideRows, e | (rows << 16));
+    for (uint32_t t = tid; t < max_tasks; t += 512u) {
+        uint2 word = make_uint2(0u, 0u);
+        if (t < task_total) {
+            uint32_t lo = 0u, hi = kExperts - 1u;  // task_offsets[lo] <= t < task_offsets[lo + 1]
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi + 1u) >> 1;
+                if (task_offsets[mid] <= t) lo = mid; else hi = mid - 1u;
+            }
+            const uint32_t tile = t - task_offsets[lo];
+            const uint32_t remaining = (offsets[lo + 1u] - offsets[lo]) - tile * kWideRows;
+            const uint32_t rows = remaining < kWideRows ? remaining : kWideRows;
+            word = make_uint2(offsets[lo] + tile * kWideRows, lo | (rows << 16));
+        }
+        task_words[t] = word;
     }
-    for (uint32_t t = task_total + e; t < max_tasks; t += 512u) task_words[t] = make_uint2(0u, 0u);
     // packed positions no valid route fills hold their own index
-    for (uint32_t p = total + e; p < routes; p += 512u) plan.packed_assignment[p] = p;
+    for (uint32_t p = total + tid; p < routes; p += 512u) plan.packed_assignment[p] = p;
 
-    if (e == 0u) {
+    if (tid == 0u) {
         uint32_t active_experts = 0;
         for (uint32_t w = 0; w < 8u; ++w) active_experts += wave_active[w];
         uint32_t status = Q38M_PLAN_OK;
