@@ -108,19 +108,10 @@ __global__ __launch_bounds__(256) void topk_kernel(
 
 // ---------------------------------------------------------------------------
 // Routing + activation quantisation for chunks, one wave per token (four per
-// workgroup), lane l holding the logits of experts l + 64j (j = 0..7):
-//   1. the 10th largest 32-bit order key of the 512 by a radix search on
-//      the wave's ballots (bit 31 down: keep the bit if at least ten keys
-//      reach the prefix with it set; stop once exactly ten do), eight
-//      ballots and scalar popcounts per bit -- no cross-lane data movement;
-//   2. every key above it and, among the keys equal to it, the lowest
-//      expert ids up to ten: the top 10, written as unique 64-bit keys
-//      (order key << 32 | 511 - id) to ten LDS slots of the wave;
-//   3. lanes 0-9 rank their slot's key among the ten (the count of larger
-//      keys) -- the order (value desc, id asc) of the reference's sort,
-//      cuda/q38_kernels.cu:431-458 -- and form exp(l_r - l_0), summed in
-//      rank order for the normalisation (cuda/q38_kernels.cu:460-479);
-// then the int8 quantisation of its 2048-wide row, lane l owning elements
+// workgroup): the top 10 of the token's 512 logits by wave_top10_of_512 (a
+// ballot radix search, the order of the reference's sort,
+// cuda/q38_kernels.cu:431-458), exp(l_r - l_0) summed in rank order for
+// the normalisation (cuda/q38_kernels.cu:460-479); then the int8 quantisation of its 2048-wide row, lane l owning elements
 // 8l + 512c .. +7 (c = 0..3).  The logit and hidden loads go out together.
 // Same ids, weights and int8 rows as route_quantize_kernel (block_topk512's
 // keys and order) bit for bit; at tens of thousands of tokens it keeps 32
@@ -129,18 +120,6 @@ __global__ __launch_bounds__(256) void topk_kernel(
 // six shuffle steps through the LDS crossbar, took 88 us per 32,768-token
 // layer, VALU-bound.)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t scalar_popcount(uint64_t mask) {
-    uint32_t count;
-    asm("s_bcnt1_i32_b64 %0, %1" : "=s"(count) : "s"(mask));
-    return count;
-}
-
-// popcount of mask's bits below this lane
-__device__ __forceinline__ uint32_t count_below(uint64_t mask) {
-    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
-}
-
 __global__ __launch_bounds__(256) void route_quantize_wave_kernel(
     const float* __restrict__ logits, const uint16_t* __restrict__ hidden, uint32_t tokens,
     int32_t* __restrict__ ids, float* __restrict__ weights, int8_t* __restrict__ xq,
@@ -162,65 +141,22 @@ __global__ __launch_bounds__(256) void route_quantize_wave_kernel(
 #pragma unroll
     for (uint32_t c = 0; c < kChunks; ++c) h[c] = src[c * 64u + lane];
 
-    uint32_t key[kPerLane];
-#pragma unroll
-    for (uint32_t j = 0; j < kPerLane; ++j) key[j] = order_key(v[j]);
-    // 1. the threshold (unrolled, so the prefix stays in scalar registers)
-    uint32_t prefix = 0u;
-#pragma unroll
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t cand = prefix | (1u << b);
-        uint32_t count = 0u;
-#pragma unroll
-        for (uint32_t j = 0; j < kPerLane; ++j)
-            count += scalar_popcount(__builtin_amdgcn_ballot_w64(key[j] >= cand));
-        prefix = count >= kTopK ? cand : prefix;
-        // exactly ten keys reach the prefix: they are the top 10
-        if (count == kTopK) break;
-    }
-    // 2. the ten, in (j, lane) = expert id order among equal keys
-    uint32_t above = 0u;
-#pragma unroll
-    for (uint32_t j = 0; j < kPerLane; ++j)
-        above += scalar_popcount(__builtin_amdgcn_ballot_w64(key[j] > prefix));
-    const uint32_t need = kTopK - above;
-    uint32_t equal_before = 0u, taken = 0u;
-#pragma unroll
-    for (uint32_t j = 0; j < kPerLane; ++j) {
-        const uint64_t equal = __builtin_amdgcn_ballot_w64(key[j] == prefix);
-        const bool mine = key[j] > prefix ||
-                          (key[j] == prefix && equal_before + count_below(equal) < need);
-        const uint64_t chosen = __builtin_amdgcn_ballot_w64(mine);
-        if (mine)
-            top_lds[wave][taken + count_below(chosen)] =
-                (static_cast<uint64_t>(key[j]) << 32) | (kExperts - 1u - (lane + 64u * j));
-        taken += scalar_popcount(chosen);
-        equal_before += scalar_popcount(equal);
-    }
-    // the wave's own LDS writes are visible to its later reads
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    // 3. ranks, l_0 and the rank-order normalisation
-    uint64_t mine = 0u, top = 0u;
-    uint32_t rank = 0u;
-#pragma unroll
-    for (uint32_t i = 0; i < kTopK; ++i) {
-        const uint64_t other = top_lds[wave][i];
-        if (i == (lane < kTopK ? lane : 0u)) mine = other;
-        top = other > top ? other : top;
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < kTopK; ++i) rank += top_lds[wave][i] > mine ? 1u : 0u;
-    const float numerator =
-        exp_q(key_value(static_cast<uint32_t>(mine >> 32)) - key_value(static_cast<uint32_t>(top >> 32)));
-    if (lane < kTopK) num_lds[wave][rank] = numerator;
+    int32_t my_id = 0;
+    uint32_t my_rank = 0u;
+    float numerator = 0.0f;
+    wave_top10_of_512(v, top_lds[wave], [&](uint32_t rank, int32_t id, float num) {
+        my_rank = rank;
+        my_id = id;
+        numerator = num;
+        num_lds[wave][rank] = num;
+    });
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     float denominator = 0.0f;
 #pragma unroll
     for (uint32_t r = 0; r < kTopK; ++r) denominator += num_lds[wave][r];
     if (lane < kTopK) {
-        ids[static_cast<size_t>(token) * kTopK + rank] =
-            static_cast<int32_t>(kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu));
-        weights[static_cast<size_t>(token) * kTopK + rank] = numerator / denominator;
+        ids[static_cast<size_t>(token) * kTopK + my_rank] = my_id;
+        weights[static_cast<size_t>(token) * kTopK + my_rank] = numerator / denominator;
     }
 
     float amax = 0.0f;

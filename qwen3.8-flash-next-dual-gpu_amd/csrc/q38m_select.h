@@ -278,6 +278,92 @@ __device__ __forceinline__ void rank_candidates(const SelectLds& lds, int32_t* i
     }
 }
 
+// popcount of a wave-uniform 64-bit mask, on the scalar unit
+__device__ __forceinline__ uint32_t scalar_popcount(uint64_t mask) {
+    uint32_t count;
+    asm("s_bcnt1_i32_b64 %0, %1" : "=s"(count) : "s"(mask));
+    return count;
+}
+
+// popcount of mask's bits below this lane
+__device__ __forceinline__ uint32_t count_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
+}
+
+// Top-10 of one 512-logit row by ONE wave, lane l holding the logits of
+// experts l + 64j (j = 0..7):
+//   1. the 10th largest 32-bit order key of the 512 by a radix search on
+//      the wave's ballots (bit 31 down: keep the bit if at least ten keys
+//      reach the prefix with it set; stop once exactly ten do), eight
+//      ballots and scalar popcounts per bit -- no cross-lane data movement;
+//   2. every key above it and, among the keys equal to it, the lowest
+//      expert ids up to ten: the top 10, written as unique 64-bit keys
+//      (order key << 32 | 511 - id) to the wave's ten slots top_lds[0..9];
+//   3. lanes 0-9 rank their slot's key among the ten (the count of larger
+//      keys): the order (value desc, id asc) of block_topk512.
+// emit(rank, id, exp(l_rank - l_0)) runs in lanes 0-9, each rank once; the
+// values come back from the keys as in rank_candidates.  Wave-uniform
+// control flow; top_lds is the calling wave's own.
+template <typename Emit>
+__device__ __forceinline__ void wave_top10_of_512(const float (&v)[kExperts / 64u],
+                                                  uint64_t* top_lds, Emit emit) {
+    constexpr uint32_t kPerLane = kExperts / 64u;
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t key[kPerLane];
+#pragma unroll
+    for (uint32_t j = 0; j < kPerLane; ++j) key[j] = order_key(v[j]);
+    // 1. the threshold (unrolled, so the prefix stays in scalar registers)
+    uint32_t prefix = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t cand = prefix | (1u << b);
+        uint32_t count = 0u;
+#pragma unroll
+        for (uint32_t j = 0; j < kPerLane; ++j)
+            count += scalar_popcount(__builtin_amdgcn_ballot_w64(key[j] >= cand));
+        prefix = count >= kTopK ? cand : prefix;
+        // exactly ten keys reach the prefix: they are the top 10
+        if (count == kTopK) break;
+    }
+    // 2. the ten, in (j, lane) = expert id order among equal keys
+    uint32_t above = 0u;
+#pragma unroll
+    for (uint32_t j = 0; j < kPerLane; ++j)
+        above += scalar_popcount(__builtin_amdgcn_ballot_w64(key[j] > prefix));
+    const uint32_t need = kTopK - above;
+    uint32_t equal_before = 0u, taken = 0u;
+#pragma unroll
+    for (uint32_t j = 0; j < kPerLane; ++j) {
+        const uint64_t equal = __builtin_amdgcn_ballot_w64(key[j] == prefix);
+        const bool mine = key[j] > prefix ||
+                          (key[j] == prefix && equal_before + count_below(equal) < need);
+        const uint64_t chosen = __builtin_amdgcn_ballot_w64(mine);
+        if (mine)
+            top_lds[taken + count_below(chosen)] =
+                (static_cast<uint64_t>(key[j]) << 32) | (kExperts - 1u - (lane + 64u * j));
+        taken += scalar_popcount(chosen);
+        equal_before += scalar_popcount(equal);
+    }
+    // the wave's own LDS writes are visible to its later reads
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // 3. ranks and l_0
+    uint64_t mine = 0u, top = 0u;
+    uint32_t rank = 0u;
+#pragma unroll
+    for (uint32_t i = 0; i < kTopK; ++i) {
+        const uint64_t other = top_lds[i];
+        if (i == (lane < kTopK ? lane : 0u)) mine = other;
+        top = other > top ? other : top;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kTopK; ++i) rank += top_lds[i] > mine ? 1u : 0u;
+    if (lane < kTopK)
+        emit(rank, static_cast<int32_t>(kExperts - 1u - static_cast<uint32_t>(mine & 0xffffffffu)),
+             exp_q(key_value(static_cast<uint32_t>(mine >> 32)) -
+                   key_value(static_cast<uint32_t>(top >> 32))));
+}
+
 // Block-wide top-k of one 512-logit row: called by all kSelectThreads
 // threads of the block; `logit` is the row entry of threads 0..511.  LDS
 // writes the caller made before the call are visible to the whole block on
