@@ -212,3 +212,19 @@ def canonical_nan(words):
     w = np.array(words, dtype=np.uint16, copy=True)
     w[((w & 0x7f80) == 0x7f80) & ((w & 0x007f) != 0)] = 0x7fc0
     return w
+
+
+def pow2_normalize(orc, words):
+    """Scales each row of bf16 words by 2^-k, k = floor(log2(row rms)),
+    which brings every row's rms into [1, 2).  Only exponents change, so the
+    scaling is exact; it is the chained tests' deterministic stand-in for
+    the norm a model applies between its MoE layers (the product has none:
+    the reference's layer ends at the residual add)."""
+    w = np.ascontiguousarray(words, dtype=np.uint16)
+    f = orc.bf16_to_f32(w)
+    rms = np.sqrt(np.mean(f.astype(np.float64) ** 2, axis=-1, keepdims=True))
+    assert np.isfinite(rms).all() and (rms > 0).all()
+    scaled = f * np.exp2(-np.floor(np.log2(rms))).astype(np.float32)
+    out = orc.f32_to_bf16(scaled).reshape(w.shape)
+    assert np.array_equal(orc.bf16_to_f32(out), scaled)  # exact
+    return out

@@ -25,8 +25,8 @@ import pytest
 
 from conftest import GOLDEN_DIR
 from helpers import (Layer, W, canonical_nan, decode, decode_fused, decode_scratch, device,
-                     host, prefill, scratch_ids, staged_step, stream, synth_hidden,
-                     synth_logits, torch, ws_arrays)
+                     host, pow2_normalize, prefill, scratch_ids, staged_step, stream,
+                     synth_hidden, synth_logits, torch, ws_arrays)
 
 pytestmark = pytest.mark.gpu
 
@@ -361,19 +361,15 @@ def test_config3_decode_stack_reduced(q38m, orc, layers):
         assert np.array_equal(host(fused_state, np.uint16).ravel(), host_state.ravel())
 
 
-def test_config3_decode_stack_full_depth(q38m, orc):
-    """Config 3 at full depth on the fused decode path the bench times:
-    every one of the 48 layers (its own weights and fresh router draw)
-    against the oracle bit for bit, on a fresh N(0,1) token; and the
-    chained stack (residual add between layers) layer by layer.  The
-    synthetic stack has no norm between layers and the MoE output grows
-    about quadratically with its input, so the chained state overflows
-    after a few layers; from there its words are compared with NaNs
-    canonicalised (the oracle's and the device's agree on every finite and
-    infinite word).  The oracle evaluates each layer on the ten routed
-    experts only: their row-major weights are gathered on the device and
-    given to it as a ten-expert layer, routes renumbered 0..9 in rank
-    order."""
+def _decode_stack(q38m, orc, normalize=False, fresh_tokens=True):
+    """Config 3's 48 layers on the fused decode path (q38m_moe_decode_v1
+    with the residual add), each layer's chained state against the oracle
+    word for word (NaNs canonicalised); optionally also each layer on a
+    fresh N(0,1) token.  With normalize, the state is rescaled by a power
+    of two after every layer (pow2_normalize) before it enters the next.
+    The oracle evaluates each layer on the ten routed experts only: their row-major weights are gathered on the device
+    and given to it as a ten-expert layer, routes renumbered 0..9 in rank
+    order.  Returns the number of layers whose chained state is finite."""
     t = torch()
     seed = W.CONFIGS[3]["seed"]
     scratch = decode_scratch(q38m)
@@ -409,15 +405,14 @@ def test_config3_decode_stack_full_depth(q38m, orc):
         dn_sub = subset(dn_rm, ids[0], dfmt[1], dfmt[2], W.HIDDEN, W.INTER)
         routes = np.arange(10, dtype=np.int32)[None]
 
-        # the layer on a fresh finite token
-        fresh = synth_hidden(q38m, seed, 1000 + layer_index, 1)
-        got = decode_fused(q38m, layer, fresh, logits, scratch)
-        ref = orc.moe(host(fresh, np.uint16).reshape(1, W.HIDDEN), gu_sub, dn_sub, ids=routes,
-                      weights=w, grouped=False)
-        assert np.array_equal(host(got, np.uint16).reshape(1, W.HIDDEN), ref["output"]), (
-            f"layer {layer_index}, fresh token")
+        if fresh_tokens:
+            fresh = synth_hidden(q38m, seed, 1000 + layer_index, 1)
+            got = decode_fused(q38m, layer, fresh, logits, scratch)
+            ref = orc.moe(host(fresh, np.uint16).reshape(1, W.HIDDEN), gu_sub, dn_sub,
+                          ids=routes, weights=w, grouped=False)
+            assert np.array_equal(host(got, np.uint16).reshape(1, W.HIDDEN), ref["output"]), (
+                f"layer {layer_index}, fresh token")
 
-        # the chained stack
         state = decode_fused(q38m, layer, state, logits, scratch, output=t.empty_like(state),
                              residual=state)
         ref = orc.moe(host_state, gu_sub, dn_sub, ids=routes, weights=w, grouped=False)
@@ -428,8 +423,33 @@ def test_config3_decode_stack_full_depth(q38m, orc):
             f"layer {layer_index}, chained state")
         finite_layers += int(np.isfinite(orc.bf16_to_f32(host_state)).all())
         host_state = got_state.copy()  # carry the device's words (NaN payloads included)
+        if normalize:
+            host_state = pow2_normalize(orc, host_state)
+            state = device(host_state).view(1, W.HIDDEN)
         del gu_rm, dn_rm, layer
-    assert finite_layers >= 4
+    return finite_layers
+
+
+def test_config3_decode_stack_full_depth(q38m, orc):
+    """Config 3 at full depth on the fused decode path the bench times:
+    every one of the 48 layers (its own weights and fresh router draw)
+    against the oracle bit for bit, on a fresh N(0,1) token; and the
+    chained stack (residual add between layers) layer by layer.  The
+    synthetic stack has no norm between layers and the MoE output grows
+    about quadratically with its input (an N(0,1) token gives an output of
+    rms about 16), so the chained state overflows after a few layers; from
+    there its words are compared with NaNs canonicalised (the oracle's and
+    the device's agree on every finite and infinite word)."""
+    assert _decode_stack(q38m, orc) >= 4
+
+
+def test_config3_decode_stack_normalized_all_finite(q38m, orc):
+    """The chained 48-layer decode with config 3's weights and routes and a
+    power-of-two rescale of the state between layers (rms back into
+    [1, 2), exact in bf16; a stand-in for the norm of a real stack): every
+    layer's chained state stays finite and equals the oracle's word for
+    word, so the whole depth is compared on finite values."""
+    assert _decode_stack(q38m, orc, normalize=True, fresh_tokens=False) == 48
 
 
 def test_decode_graph_replays(q38m, orc, layers):

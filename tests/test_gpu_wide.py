@@ -17,9 +17,8 @@ import ctypes
 import numpy as np
 import pytest
 
-from helpers import (Layer, W, canonical_nan, host, prefill, stream, synth_hidden, synth_logits,
-                     torch,
-                     ws_arrays)
+from helpers import (Layer, W, canonical_nan, device, host, pow2_normalize, prefill, stream,
+                     synth_hidden, synth_logits, torch, ws_arrays)
 
 pytestmark = pytest.mark.gpu
 
@@ -324,16 +323,18 @@ def test_wide_config5_layer_full_chunk(q38m, orc, wide_layers):
     assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
 
 
-def test_config5_stack_full_depth_chunk(q38m, orc):
-    """Config 5 at full depth on the chunk path: all 48 layers (alternating
-    all-W4 / W4-W8 policy, each with its own weights and Zipf s=0.8 router
-    draw) over a 2,048-token chunk with the residual add between layers.
-    At every layer, a fresh N(0,1) chunk through the layer equals the oracle
-    on sampled tokens bit for bit, and so does the chained state (the
-    device's input words for those tokens, NaNs canonicalised once the
-    synthetic stack overflows).  The oracle evaluates a token on its ten
+def _chunk_stack(q38m, orc, normalize=False, fresh_tokens=True):
+    """Config 5's 48 layers (alternating all-W4 / W4-W8 policy, each with
+    its own weights and Zipf s=0.8 router draw) on the chunk path over a
+    2,048-token chunk with the residual add between layers.  At every
+    layer the chained output equals the oracle on sampled tokens bit for
+    bit (the device's input words for those tokens, NaNs canonicalised);
+    optionally a fresh N(0,1) chunk through the layer does too.  With
+    normalize, every token's state is rescaled by a power of two after the
+    residual add (pow2_normalize).  The oracle evaluates a token on its ten
     routed experts only, gathered on the device, routes renumbered 0..9 in
-    rank order."""
+    rank order.  Returns the number of layers whose sampled outputs are
+    finite."""
     t = torch()
     seed = W.CONFIGS[5]["seed"]
     tokens = 2048
@@ -367,9 +368,10 @@ def test_config5_stack_full_depth_chunk(q38m, orc):
         layer.gu, layer.dn = q38m.repack(gu_rm, paired=True), q38m.repack(dn_rm)
         logits = synth_logits(q38m, seed, l_tag, tokens, W.bias_for(5, layer_index))
         host_logits = host(logits, np.float32)[sample]
-        fresh = synth_hidden(q38m, seed, 2000 + layer_index, tokens)
-        got_fresh = host(prefill_wide(q38m, layer, fresh, logits, wsw), np.uint16)
-        host_fresh = host(fresh, np.uint16)[sample]
+        if fresh_tokens:
+            fresh = synth_hidden(q38m, seed, 2000 + layer_index, tokens)
+            got_fresh = host(prefill_wide(q38m, layer, fresh, logits, wsw), np.uint16)
+            host_fresh = host(fresh, np.uint16)[sample]
         host_in = host(state, np.uint16)[sample]
         out = prefill_wide(q38m, layer, state, logits, wsw)
         got_out = host(out, np.uint16)
@@ -377,10 +379,11 @@ def test_config5_stack_full_depth_chunk(q38m, orc):
             ids, w = orc.topk(host_logits[k:k + 1])
             gu_sub = subset(gu_rm, ids[0], gfmt[1], gfmt[2], 2 * W.INTER, W.HIDDEN)
             dn_sub = subset(dn_rm, ids[0], dfmt[1], dfmt[2], W.HIDDEN, W.INTER)
-            ref = orc.moe(host_fresh[k:k + 1], gu_sub, dn_sub, ids=routes, weights=w,
-                          grouped=False)
-            assert np.array_equal(got_fresh[token:token + 1], ref["output"]), (
-                f"layer {layer_index}, fresh token {token}")
+            if fresh_tokens:
+                ref = orc.moe(host_fresh[k:k + 1], gu_sub, dn_sub, ids=routes, weights=w,
+                              grouped=False)
+                assert np.array_equal(got_fresh[token:token + 1], ref["output"]), (
+                    f"layer {layer_index}, fresh token {token}")
             ref = orc.moe(host_in[k:k + 1], gu_sub, dn_sub, ids=routes, weights=w,
                           grouped=False)
             assert np.array_equal(canonical_nan(got_out[token:token + 1]),
@@ -391,5 +394,25 @@ def test_config5_stack_full_depth_chunk(q38m, orc):
         q38m.call("q38m_residual_add_bf16", state.data_ptr(), out.data_ptr(),
                   new_state.data_ptr(), tokens * W.HIDDEN, stream(), 0)
         state = new_state
+        if normalize:
+            state = device(pow2_normalize(orc, host(state, np.uint16))).view(tokens, W.HIDDEN)
         del gu_rm, dn_rm, layer
-    assert finite_layers >= 3
+    return finite_layers
+
+
+def test_config5_stack_full_depth_chunk(q38m, orc):
+    """Config 5 at full depth on the chunk path, on a fresh N(0,1) chunk
+    and on the chained state.  The synthetic stack has no norm between
+    layers and the MoE output grows about quadratically with its input, so
+    the chained state overflows after a few layers; from there its words
+    are compared with NaNs canonicalised."""
+    assert _chunk_stack(q38m, orc) >= 3
+
+
+def test_config5_stack_normalized_chunk_all_finite(q38m, orc):
+    """The chained 48-layer chunk stack with config 5's weights and routes
+    and a power-of-two rescale of every token's state between layers (rms
+    back into [1, 2), exact in bf16; a stand-in for the norm of a real
+    stack): every layer's sampled outputs stay finite and equal the
+    oracle's word for word."""
+    assert _chunk_stack(q38m, orc, normalize=True, fresh_tokens=False) == 48
