@@ -88,8 +88,18 @@ VALU_CYCLES = 4  # issue cycles of one non-packed wave64 VALU instruction on a S
 # Algorithmic bytes per launch of the decode kernels (config 3: ten routes,
 # W4 g32 fp16-scaled gate/up, W8 per-channel down): the selected experts'
 # weights and scale words.
-DECODE_KERNEL_BYTES = {"decode_gate_up_kernel": 10 * (1048576 + 131072),
-                       "decode_down_kernel": 10 * (1048576 + 4096)}
+# Algorithmic bytes per decode launch (config 3): the gate/up launch reads its
+# ten experts' W4 g32 rows and, once they are in, touches the down launch's
+# lines (ten W8 experts) so that they sit in L2; the down launch then reads
+# those same bytes from L2.
+DECODE_GATE_UP_BYTES = 10 * (1048576 + 131072)
+DECODE_DOWN_BYTES = 10 * (1048576 + 4096)
+DECODE_KERNEL_BYTES = {"decode_gate_up_kernel": DECODE_GATE_UP_BYTES + DECODE_DOWN_BYTES,
+                       "decode_down_kernel": DECODE_DOWN_BYTES}
+DECODE_KERNEL_NOTES = {"decode_gate_up_kernel": "HBM: its own weights plus the down launch's "
+                                                "lines, which it prefetches into L2",
+                       "decode_down_kernel": "its weights come from L2 (prefetched by the "
+                                             "gate/up launch); GBps is its operand rate"}
 
 
 def _short_kernel(name):
@@ -343,7 +353,8 @@ def pmc_report(workload, traffic_dir=None):
                              "algorithmic_bytes": alg, "fetch_bytes": round(fb),
                              "write_bytes": round(wb), "fetch_over_algorithmic": round(fb / alg, 3),
                              "GBps": round(alg / (us * 1e-6) / 1e9, 1),
-                             "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+                             "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                             "note": DECODE_KERNEL_NOTES[base]}
         with open(os.path.join(traffic_dir, "decode_kernels_config3.json"), "w") as fh:
             json.dump({"workload": "config3 decode (" + PMC_WORKLOADS["decode"] + ")",
                        "kernels": kernels, "fetch_scale": fs and round(fs, 4),

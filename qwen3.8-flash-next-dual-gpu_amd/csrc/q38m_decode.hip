@@ -20,6 +20,8 @@
 //            together).  Workgroup b owns channels 16p+n0, 16p+n0+1 of all
 //            routes; the eight workgroups sharing a pair tile's 128-byte
 //            lines sit on one XCD (b % 8), so each line crosses HBM once.
+//            Once its weights are in, each wave requests the lines the
+//            down launch's workgroup b will read, into the same XCD's L2.
 //   down     256 workgroups x 10 waves.  Each wave loads the ids and its
 //            route's mid row together, quantises the row in registers, and
 //            streams 8 output channels x 512 columns; int32 partials meet by
@@ -131,6 +133,52 @@ struct SharedDown {
     const uint16_t* gate;    // the output gate word
 };
 
+// The down launch's weight and scale lines, requested by the gate/up launch
+// once its own weights have arrived: gate/up workgroup b touches every
+// 64-byte piece that down workgroup b will read (both grids have 256
+// workgroups, and workgroup b runs on XCD b % 8 in both), so the down
+// launch finds its weights in that XCD's L2 instead of waiting a full HBM
+// round trip after its ids arrive.  The loaded words are only folded into a
+// value the wave keeps live to its end; nothing is computed from them.
+struct DownPrefetch {
+    const uint8_t* w;       // the down weights
+    const uint16_t* s;      // their scale words
+    uint32_t w4;            // 1: W4 (MFMA16 quad-major), 0: W8 (K-block-major)
+    uint32_t scale_words;   // W8: scale words per channel; W4: per row and quad
+};
+
+// wave `route` of gate/up workgroup b: the route's pieces of down workgroup
+// b (decode_down_kernel's load addresses), one 4-byte load per 64 bytes
+__device__ __forceinline__ uint32_t prefetch_down(const DownPrefetch& pf, uint32_t e,
+                                                  uint32_t lane) {
+    constexpr uint32_t kTiles = kHidden / 16u;
+    const uint32_t slot8 = blockIdx.x >> 3;
+    const uint32_t tile = 16u * (blockIdx.x & 7u) + (slot8 >> 1);
+    const uint32_t n0 = 8u * (slot8 & 1u);
+    size_t piece;  // 16-byte index into the weights
+    size_t scale;  // scale word index
+    if (pf.w4) {
+        // lanes 0-31: (quad kq, half qh, chunk x, 64-byte half hs) of the
+        // route's 16 lines; lanes 32-63: the scale words of (kq, channel)
+        constexpr uint32_t kQuads = kInter / 128u;
+        const uint32_t kq = (lane >> 3) & 3u;
+        const size_t t = (static_cast<size_t>(e) * kQuads + kq) * kTiles + tile;
+        piece = t * 64u + 32u * ((lane >> 2) & 1u) + 16u * ((lane >> 1) & 1u) + n0 +
+                4u * (lane & 1u);
+        scale = (t * 16u + n0 + (lane & 7u)) * pf.scale_words;
+    } else {
+        // (K block kb, chunk q, 64-byte half hs) of the route's 32 lines;
+        // the channel's scale words
+        constexpr uint32_t kBlocks = kInter / 64u;
+        piece = ((static_cast<size_t>(e) * kTiles + tile) * kBlocks + (lane >> 3)) * 64u + n0 +
+                16u * ((lane >> 1) & 3u) + 4u * (lane & 1u);
+        scale = (static_cast<size_t>(e) * kHidden + 16u * tile + n0 + (lane & 7u)) *
+                pf.scale_words;
+    }
+    const uint32_t word = *reinterpret_cast<const uint32_t*>(pf.w + 16u * piece);
+    return word ^ static_cast<uint32_t>(pf.s[scale]);
+}
+
 // gate/up: 12 waves, three route slots x four quarters of K.
 constexpr uint32_t kGateUpThreads = 768u;
 constexpr uint32_t kRouteSlots = 3u;
@@ -169,7 +217,7 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     const uint16_t* __restrict__ hidden, const float* __restrict__ logits,
     const int32_t* __restrict__ ids_in, const float* __restrict__ weights_in, uint32_t top_k,
     int32_t* __restrict__ ids_out, uint16_t* __restrict__ mid, PhaseCall call,
-    SharedGateUp shared) {
+    SharedGateUp shared, DownPrefetch prefetch) {
     PhaseStamps stamps;
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kSlots = 2u * I / 16u;
@@ -318,10 +366,25 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
         reinterpret_cast<uint2*>(x_lds)[(k >> 7) * (2u * kQuadPad) + ((k & 127u) >> 3)] =
             quantize8(hw, row_q);
     }
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     stamps.mark(4);
     stamps.mark_loaded(5);
     stamps.mark_wave_loaded(wave_stamp_lds);
+
+    // Once this wave's weights and scales are in, the down launch's pieces
+    // of route `wave` (waves 10 and 11 repeat expert 0's): issued earlier,
+    // they share HBM with the other workgroups' gate/up weights and delay
+    // them more than they save.  Every barrier after this point waits for
+    // LDS only, so the prefetch stays in flight until the kernel's end.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    uint32_t prefetched;
+    {
+        const int32_t pid = wave < top_k ? ids_lds[wave] : -1;
+        const uint32_t pe =
+            pid >= 0 && pid < static_cast<int32_t>(kExperts) ? static_cast<uint32_t>(pid) : 0u;
+        prefetched = prefetch_down(prefetch, pe, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     // this lane's group sums (int32) and their scales (fp32 words)
     uint4 xa = make_uint4(0u, 0u, 0u, 0u), xf = make_uint4(0u, 0u, 0u, 0u);
@@ -389,7 +452,7 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
         xch[chain * kQuads + kq][0] = xa;
         xch[chain * kQuads + kq][1] = xf;
     }
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     stamps.mark(7);
     if constexpr (kShared) {
         // the exchange barrier made shared_dot visible
@@ -449,6 +512,8 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     }
     stamps.mark(9);
     stamps.finish(0u, call, wave_stamp_lds);
+    // the prefetch's words are consumed here, after everything else
+    asm volatile("" ::"v"(prefetched));
 }
 
 // kPerGroup: W4, 32-column sub-blocks per group (1, 2, 4); W8, 64-column
@@ -733,11 +798,19 @@ hipError_t launch_decode_routed(const q38m_expert_weights_v1& gate_up,
     const bool gbf16 = gate_up.scale_dtype == Q38M_SCALE_BF16;
     int32_t* ids_out = logits != nullptr ? scratch_ids : nullptr;
     const PhaseCall call = next_phase_call();
+    // the down weights' scale words per channel (W8) or per row and quad
+    // (W4); the descriptor's format and group size were validated
+    const bool down_w4 = down.format == Q38M_FORMAT_W4_SYM;
+    const uint32_t down_scale_words =
+        down_w4 ? 128u / down.group_size : (down.group_size == 0u ? 1u : kInter / down.group_size);
+    const DownPrefetch prefetch{static_cast<const uint8_t*>(down.data),
+                                static_cast<const uint16_t*>(down.scales), down_w4 ? 1u : 0u,
+                                down_scale_words};
     auto gate_up_launch = [&](auto w8, auto per) {
         decode_gate_up_kernel<kHidden, kInter, decltype(w8)::value, decltype(per)::value, kShared>
             <<<kDecodeBlocks, kGateUpThreads, 0, stream>>>(gw, gs, gbf16, hidden, logits, ids,
                                                            weights, top_k, ids_out, mid, call,
-                                                           sgu);
+                                                           sgu, prefetch);
     };
     using W4 = std::false_type;
     using W8 = std::true_type;

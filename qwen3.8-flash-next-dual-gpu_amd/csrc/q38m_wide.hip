@@ -770,8 +770,10 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
         // lane l reads row l%16 of chunk l/16, through the staging swizzle
         const uint4* abuf0 = a_lds[buffer] + ((lane & 48u) | ((lane & 15u) ^ a_swizzle(lane >> 5)));
         const uint4* abuf1 = a_lds[buffer] + ((lane & 48u) | ((lane & 15u) ^ a_swizzle((lane >> 5) + 2u)));
-        const uint16_t* srow = reinterpret_cast<const uint16_t*>(s_lds[buffer]) +
-                               ((2u * pr) * 16u + n) * 2u;  // up: + 32 words
+        const uint32_t* srow = s_lds[buffer] + (2u * pr) * 16u + n;  // up: + 16 words
+        // the step's scale words (gate, up; two groups each), read before
+        // the first MFMA instead of one LDS round trip per group
+        const uint32_t sword[2] = {srow[0], srow[16u]};
         const uint32_t* wrow = w_lds[buffer] + (2u * pr) * 128u + lane;  // up: + 128
         uint4 fa[2];
         uint4 bf[2];
@@ -796,7 +798,7 @@ void gate_up_w4g32_f16_kernel(const uint4* __restrict__ w, const uint16_t* __res
             const uint32_t m = k / 2u, u = k & 1u;
             const uint32_t j = m / kNt, t = m % kNt;
             if (t == 0u) {
-                const uint32_t word = srow[u * 32u + j];
+                const uint32_t word = (sword[u] >> (16u * j)) & 0xFFFFu;
                 sc[u] = kBf16 ? bf16_to_f32(word) * 0.0625f : f16_to_f32(word);
                 asm volatile("" : "+v"(sc[u]));  // a plain v_fma_f32, not v_fma_mix
             }
