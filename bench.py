@@ -90,16 +90,16 @@ VALU_CYCLES = 4  # issue cycles of one non-packed wave64 VALU instruction on a S
 # weights and scale words.
 # Algorithmic bytes per decode launch (config 3): the gate/up launch reads its
 # ten experts' W4 g32 rows and, once they are in, touches the down launch's
-# lines (ten W8 experts) so that they sit in L2; the down launch then reads
-# those same bytes from L2.
+# lines (ten W8 experts) so that they are cached; the down launch then reads
+# those same bytes from the cache.
 DECODE_GATE_UP_BYTES = 10 * (1048576 + 131072)
 DECODE_DOWN_BYTES = 10 * (1048576 + 4096)
 DECODE_KERNEL_BYTES = {"decode_gate_up_kernel": DECODE_GATE_UP_BYTES + DECODE_DOWN_BYTES,
                        "decode_down_kernel": DECODE_DOWN_BYTES}
 DECODE_KERNEL_NOTES = {"decode_gate_up_kernel": "HBM: its own weights plus the down launch's "
-                                                "lines, which it prefetches into L2",
-                       "decode_down_kernel": "its weights come from L2 (prefetched by the "
-                                             "gate/up launch); GBps is its operand rate"}
+                                                "lines, which it prefetches",
+                       "decode_down_kernel": "its weights were prefetched by the gate/up "
+                                             "launch; GBps is its operand rate"}
 
 
 def _short_kernel(name):

@@ -21,7 +21,7 @@
 //            routes; the eight workgroups sharing a pair tile's 128-byte
 //            lines sit on one XCD (b % 8), so each line crosses HBM once.
 //            Once its weights are in, each wave requests the lines the
-//            down launch's workgroup b will read, into the same XCD's L2.
+//            down launch's workgroup b will read, so they are cached.
 //   down     256 workgroups x 10 waves.  Each wave loads the ids and its
 //            route's mid row together, quantises the row in registers, and
 //            streams 8 output channels x 512 columns; int32 partials meet by
@@ -137,8 +137,8 @@ struct SharedDown {
 // once its own weights have arrived: gate/up workgroup b touches every
 // 64-byte piece that down workgroup b will read (both grids have 256
 // workgroups, and workgroup b runs on XCD b % 8 in both), so the down
-// launch finds its weights in that XCD's L2 instead of waiting a full HBM
-// round trip after its ids arrive.  The loaded words are only folded into a
+// launch finds its weights in a cache (that XCD's L2 or the memory-side
+// Infinity Cache) instead of streaming them from HBM after its ids arrive.  The loaded words are only folded into a
 // value the wave keeps live to its end; nothing is computed from them.
 struct DownPrefetch {
     const uint8_t* w;       // the down weights
