@@ -655,13 +655,26 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
 // Fixed rank-order reduce from 0.0f plus the optional gated shared term
 // (q38_moe_prefill.cu:601-631), added as fma(shared, multiplier, routed): the
 // contraction nvcc's default -fmad applies to the reference expression.
-// One workgroup per token, 8 columns/thread.
+// One workgroup per token; thread t sums columns 4t..4t+3 of each 1024-column
+// half, so every load instruction reads 1 KB of whole 128-byte lines.
+// kStream: the route outputs are read with non-temporal loads (for route
+// outputs larger than the memory-side cache, read once from HBM).
 // ---------------------------------------------------------------------------
-template <uint32_t H>
+__device__ __forceinline__ float4 load_f4(const float* p, std::true_type) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float4 load_f4(const float* p, std::false_type) {
+    return *reinterpret_cast<const float4*>(p);
+}
+
+template <uint32_t H, bool kStream>
 __global__ __launch_bounds__(256) void combine_kernel(
     const float* __restrict__ route_output, const uint32_t* __restrict__ inverse,
     const uint16_t* __restrict__ shared_output, const uint16_t* __restrict__ shared_gate,
     uint16_t* __restrict__ output) {
+    static_assert(H == 2u * 1024u, "two 1024-column halves, four columns per thread");
     const uint32_t token = blockIdx.x;
     const bool shared = shared_output != nullptr && shared_gate != nullptr;
     float multiplier = 0.0f;
@@ -673,33 +686,34 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
     for (uint32_t r = 0; r < kTopK; ++r)
         rows[r] = checked(inverse[token * kTopK + r], gridDim.x * kTopK, kCheckRoute);
-    for (uint32_t c0 = threadIdx.x * 8u; c0 < H; c0 += 256u * 8u) {
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t c = 4u * threadIdx.x;
+    float acc[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
 #pragma unroll
-        for (uint32_t r = 0; r < kTopK; ++r) {
-            const float4* src = reinterpret_cast<const float4*>(
-                route_output + static_cast<size_t>(rows[r]) * H + c0);
-            const float4 v0 = src[0];
-            const float4 v1 = src[1];
-            acc[0] += v0.x; acc[1] += v0.y; acc[2] += v0.z; acc[3] += v0.w;
-            acc[4] += v1.x; acc[5] += v1.y; acc[6] += v1.z; acc[7] += v1.w;
+    for (uint32_t r = 0; r < kTopK; ++r) {
+        const float* row = route_output + static_cast<size_t>(rows[r]) * H + c;
+#pragma unroll
+        for (uint32_t h = 0; h < 2u; ++h) {
+            const float4 v = load_f4(row + 1024u * h, std::integral_constant<bool, kStream>{});
+            acc[h][0] += v.x; acc[h][1] += v.y; acc[h][2] += v.z; acc[h][3] += v.w;
         }
-        if (shared) {
-            const uint4 sv = *reinterpret_cast<const uint4*>(
-                shared_output + static_cast<size_t>(token) * H + c0);
-            const uint32_t sw[4] = {sv.x, sv.y, sv.z, sv.w};
+    }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const uint32_t h = (i & 1) ? (sw[i >> 1] >> 16) : (sw[i >> 1] & 0xffffu);
-                acc[i] = __builtin_fmaf(bf16_to_f32(h), multiplier, acc[i]);
+    for (uint32_t h = 0; h < 2u; ++h) {
+        const uint32_t col = c + 1024u * h;
+        if (shared) {
+            const uint2 sv = *reinterpret_cast<const uint2*>(
+                shared_output + static_cast<size_t>(token) * H + col);
+            const uint32_t sw[2] = {sv.x, sv.y};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t bits = (i & 1) ? (sw[i >> 1] >> 16) : (sw[i >> 1] & 0xffffu);
+                acc[h][i] = __builtin_fmaf(bf16_to_f32(bits), multiplier, acc[h][i]);
             }
         }
-        uint4 packed;
-        packed.x = f32_to_bf16(acc[0]) | (f32_to_bf16(acc[1]) << 16);
-        packed.y = f32_to_bf16(acc[2]) | (f32_to_bf16(acc[3]) << 16);
-        packed.z = f32_to_bf16(acc[4]) | (f32_to_bf16(acc[5]) << 16);
-        packed.w = f32_to_bf16(acc[6]) | (f32_to_bf16(acc[7]) << 16);
-        *reinterpret_cast<uint4*>(output + static_cast<size_t>(token) * H + c0) = packed;
+        uint2 packed;
+        packed.x = f32_to_bf16(acc[h][0]) | (f32_to_bf16(acc[h][1]) << 16);
+        packed.y = f32_to_bf16(acc[h][2]) | (f32_to_bf16(acc[h][3]) << 16);
+        *reinterpret_cast<uint2*>(output + static_cast<size_t>(token) * H + col) = packed;
     }
 }
 
@@ -866,8 +880,19 @@ hipError_t launch_down_quantize(const q38m_expert_weights_v1& w, const uint16_t*
 hipError_t launch_combine(const float* route_output, const uint32_t* inverse,
                           const uint16_t* shared_output, const uint16_t* shared_gate,
                           uint32_t tokens, uint16_t* output, hipStream_t stream) {
-    combine_kernel<kHidden><<<tokens, 256, 0, stream>>>(route_output, inverse,
-                                                        shared_output, shared_gate, output);
+    // route outputs beyond the 256 MB memory-side cache (a chunk's: 80 KB per
+    // token) are read once from HBM, with non-temporal loads (config-5 layer:
+    // 523 -> 480 us); a slab's were just written and are read through the caches
+    constexpr size_t kCachedRouteBytes = size_t(256) << 20;
+    const size_t bytes = static_cast<size_t>(tokens) * kTopK * kHidden * sizeof(float);
+    if (bytes > kCachedRouteBytes)
+        combine_kernel<kHidden, true><<<tokens, 256, 0, stream>>>(route_output, inverse,
+                                                                  shared_output, shared_gate,
+                                                                  output);
+    else
+        combine_kernel<kHidden, false><<<tokens, 256, 0, stream>>>(route_output, inverse,
+                                                                   shared_output, shared_gate,
+                                                                   output);
     return hipGetLastError();
 }
 
