@@ -228,3 +228,18 @@ def pow2_normalize(orc, words):
     out = orc.f32_to_bf16(scaled).reshape(w.shape)
     assert np.array_equal(orc.bf16_to_f32(out), scaled)  # exact
     return out
+
+
+def oracle_chunk(orc, hidden, logits, gate_up, down, slab=512):
+    """The oracle over a chunk of any size, evaluated as consecutive slabs
+    through its grouped path (T <= 512 per call): a token's output depends
+    only on its own row, logits and routes (per-token and per-route
+    quantisation, rank-order combine), so the slabs' outputs are the
+    chunk's.  hidden: bf16 words [T][H]; logits: fp32 [T][E]."""
+    tokens = hidden.shape[0]
+    out = np.empty(hidden.shape, dtype=np.uint16)
+    for s0 in range(0, tokens, slab):
+        sl = slice(s0, min(tokens, s0 + slab))
+        out[sl] = orc.moe(np.ascontiguousarray(hidden[sl]), gate_up, down,
+                          logits=np.ascontiguousarray(logits[sl]), grouped=True)["output"]
+    return out

@@ -17,8 +17,8 @@ import ctypes
 import numpy as np
 import pytest
 
-from helpers import (Layer, W, canonical_nan, device, host, pow2_normalize, prefill, stream,
-                     synth_hidden, synth_logits, torch, ws_arrays)
+from helpers import (Layer, W, canonical_nan, device, host, oracle_chunk, pow2_normalize,
+                     prefill, stream, synth_hidden, synth_logits, torch, ws_arrays)
 
 pytestmark = pytest.mark.gpu
 
@@ -220,7 +220,8 @@ def test_wide_slab_equals_v1_with_intermediates(q38m, orc, wide_layers, values):
 
 def test_wide_config4_chunk(q38m, orc, wide_layers):
     """Config 4 (4096 tokens, Zipf s=1.1) in one chunk: every token equals
-    the slab path's result, and a sample equals the oracle token by token."""
+    the slab path's result and the oracle's (evaluated slab by slab), and a
+    sample equals the oracle's token-by-token evaluation."""
     t = torch()
     layer = wide_layers(4)
     seed = W.CONFIGS[4]["seed"]
@@ -236,6 +237,9 @@ def test_wide_config4_chunk(q38m, orc, wide_layers):
         prefill(q38m, layer, hidden[sl], logits[sl], ws1, output=out1[sl])
     got = host(outw, np.uint16)
     assert np.array_equal(got, host(out1, np.uint16))
+    full = oracle_chunk(orc, host(hidden, np.uint16), host(logits, np.float32),
+                        layer.host_gu, layer.host_dn)
+    assert np.array_equal(got, full)
     rng = np.random.default_rng(44)
     sample = np.sort(rng.choice(4096, 64, replace=False))
     ref = orc.moe(host(hidden, np.uint16)[sample], layer.host_gu, layer.host_dn,
@@ -279,7 +283,7 @@ def test_wide_hot_experts_chunk(q38m, orc, wide_layers):
     """The most skewed routing: a +40 logit bias on ten experts sends every
     token of a 2,048-token chunk to the same ten (each expert 2,048 rows,
     16 full 128-row tasks).  Every token equals the slab path's result and
-    a sample equals the oracle."""
+    the oracle's."""
     t = torch()
     layer = wide_layers(4)
     seed = W.CONFIGS[4]["seed"]
@@ -300,15 +304,15 @@ def test_wide_hot_experts_chunk(q38m, orc, wide_layers):
         prefill(q38m, layer, hidden[sl], logits[sl], ws1, output=out1[sl])
     got = host(outw, np.uint16)
     assert np.array_equal(got, host(out1, np.uint16))
-    sample = np.arange(0, tokens, 97)
-    ref = orc.moe(host(hidden[sample.tolist()], np.uint16), layer.host_gu, layer.host_dn,
-                  logits=host(logits[sample.tolist()], np.float32), grouped=False)
-    assert np.array_equal(got[sample], ref["output"])
+    full = oracle_chunk(orc, host(hidden, np.uint16), host(logits, np.float32),
+                        layer.host_gu, layer.host_dn)
+    assert np.array_equal(got, full)
 
 
 def test_wide_config5_layer_full_chunk(q38m, orc, wide_layers):
     """One config-5 layer (W4/W8) over all 32,768 tokens of the stack in one
-    chunk, against the oracle on a 64-token sample."""
+    chunk: every token against the oracle (evaluated slab by slab), and a
+    64-token sample against its token-by-token evaluation."""
     layer = wide_layers(5, 1)
     seed = W.CONFIGS[5]["seed"]
     tokens = 32768
@@ -317,13 +321,18 @@ def test_wide_config5_layer_full_chunk(q38m, orc, wide_layers):
     logits = synth_logits(q38m, seed, l_tag, tokens, W.bias_for(5, 1))
     wsw = q38m.WideWorkspace_(tokens)
     out = prefill_wide(q38m, layer, hidden, logits, wsw)
+    got = host(out, np.uint16)
+    full = oracle_chunk(orc, host(hidden, np.uint16), host(logits, np.float32),
+                        layer.host_gu, layer.host_dn)
+    mismatched = np.flatnonzero((got != full).any(axis=1))
+    assert mismatched.size == 0, f"{mismatched.size} tokens differ, first {mismatched[:8]}"
     sample = np.arange(0, tokens, 512) + np.arange(64) % 7
     ref = orc.moe(host(hidden[sample.tolist()], np.uint16), layer.host_gu, layer.host_dn,
                   logits=host(logits[sample.tolist()], np.float32), grouped=False)
-    assert np.array_equal(host(out, np.uint16)[sample], ref["output"])
+    assert np.array_equal(got[sample], ref["output"])
 
 
-def _chunk_stack(q38m, orc, normalize=False, fresh_tokens=True):
+def _chunk_stack(q38m, orc, normalize=False, fresh_tokens=True, every_token=False):
     """Config 5's 48 layers (alternating all-W4 / W4-W8 policy, each with
     its own weights and Zipf s=0.8 router draw) on the chunk path over a
     2,048-token chunk with the residual add between layers.  At every
@@ -333,8 +342,10 @@ def _chunk_stack(q38m, orc, normalize=False, fresh_tokens=True):
     normalize, every token's state is rescaled by a power of two after the
     residual add (pow2_normalize).  The oracle evaluates a token on its ten
     routed experts only, gathered on the device, routes renumbered 0..9 in
-    rank order.  Returns the number of layers whose sampled outputs are
-    finite."""
+    rank order.  With every_token, each layer's whole chained output is also
+    compared with the oracle over all 2,048 tokens (the layer's full
+    512-expert weights, slab by slab).  Returns the number of layers whose
+    sampled outputs are finite."""
     t = torch()
     seed = W.CONFIGS[5]["seed"]
     tokens = 2048
@@ -389,6 +400,16 @@ def _chunk_stack(q38m, orc, normalize=False, fresh_tokens=True):
             assert np.array_equal(canonical_nan(got_out[token:token + 1]),
                                   canonical_nan(ref["output"])), (
                 f"layer {layer_index}, chained token {token}")
+        if every_token:
+            full = oracle_chunk(
+                orc, host(state, np.uint16), host(logits, np.float32),
+                orc.HostWeights(host(gu_rm.data, np.uint8), host(gu_rm.scales, np.uint16),
+                                gfmt[1], gfmt[2], W.EXPERTS, 2 * W.INTER, W.HIDDEN),
+                orc.HostWeights(host(dn_rm.data, np.uint8), host(dn_rm.scales, np.uint16),
+                                dfmt[1], dfmt[2], W.EXPERTS, W.HIDDEN, W.INTER))
+            mismatched = np.flatnonzero((canonical_nan(got_out) != canonical_nan(full)).any(axis=1))
+            assert mismatched.size == 0, (
+                f"layer {layer_index}: {mismatched.size} tokens differ, first {mismatched[:8]}")
         finite_layers += int(np.isfinite(orc.bf16_to_f32(got_out[sample])).all())
         new_state = t.empty_like(state)
         q38m.call("q38m_residual_add_bf16", state.data_ptr(), out.data_ptr(),
@@ -413,6 +434,6 @@ def test_config5_stack_normalized_chunk_all_finite(q38m, orc):
     """The chained 48-layer chunk stack with config 5's weights and routes
     and a power-of-two rescale of every token's state between layers (rms
     back into [1, 2), exact in bf16; a stand-in for the norm of a real
-    stack): every layer's sampled outputs stay finite and equal the
-    oracle's word for word."""
-    assert _chunk_stack(q38m, orc, normalize=True, fresh_tokens=False) == 48
+    stack): at every layer all 2,048 tokens' outputs equal the oracle's
+    word for word, and they stay finite."""
+    assert _chunk_stack(q38m, orc, normalize=True, fresh_tokens=False, every_token=True) == 48
