@@ -539,20 +539,27 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
 // ---------------------------------------------------------------------------
 // Down, W4 in groups of 32, 64 or 128 columns (kSub sub-blocks of 32 per
 // group; the all-W4 layer policy): the gate/up group chain over K = I, then
-// * sm[r].
+// * sm[r].  A workgroup covers 16 output tiles of one task: kWaves waves of
+// kTilesPerWave tiles (8 x 2, or 16 x 1 for groups of 128, whose chain is
+// light enough that more waves with one tile each stream faster); the
+// task's 16 rows are staged once in LDS as int8 MFMA fragments (quantised
+// there, kQuantize, 16 / kWaves rows per wave) and read from LDS by every
+// MFMA, which keeps the waves small enough for 4-8 per SIMD.
 // ---------------------------------------------------------------------------
 template <uint32_t H, uint32_t I, uint32_t kTilesPerWave, uint32_t kSub, bool kBf16,
-          bool kQuantize>
-__global__ __launch_bounds__(256) void down_w4_kernel(
+          bool kQuantize, uint32_t kWaves>
+__global__ __launch_bounds__(kWaves * 64) void down_w4_kernel(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, MidRows mid,
     const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
     constexpr uint32_t kQuads = I / 128u;
     constexpr uint32_t kTiles = H / 16u;
     constexpr uint32_t kRowScales = 4u / kSub;
     constexpr uint32_t kGroups = kQuads * 4u;  // 32-wide K groups
-    // kQuantize: the int8 rows in the MFMA A order, [group][lane] (lane
-    // n + 16q: row n, columns 32g + 8q ..+7), and the rows' scales
-    __shared__ uint2 a_lds[kQuantize ? kGroups * 64u : 1u];
+    static_assert(kWaves * kTilesPerWave == 16u && 16u % kWaves == 0u,
+                  "16 tiles and 16 rows per workgroup");
+    // the int8 rows in the MFMA A order, [group][lane] (lane n + 16q: row n,
+    // columns 32g + 8q ..+7), and (kQuantize) the rows' scales
+    __shared__ uint2 a_lds[kGroups * 64u];
     __shared__ float scale_lds[16];
     const TaskRecord task = read_task(tasks, blockIdx.y);
     const uint32_t rows = task.rows;
@@ -566,7 +573,7 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
     // quad-major layout: quad kq of tile t is unit (e*kQuads + kq)*kTiles + t;
     // a tile's four quads are requested together, one tile ahead, the first
     // tile's before the A rows are staged
-    const uint32_t tile0 = (blockIdx.x * 4u + wave) * kTilesPerWave;
+    const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
     auto load_tile = [&](uint32_t t, uint4 (&b)[kQuads], uint2 (&c)[kQuads]) {
         const size_t unit = static_cast<size_t>(e) * kQuads * kTiles + tile0 + t;
 #pragma unroll
@@ -578,11 +585,10 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
     uint4 wb[kTilesPerWave][kQuads];
     uint2 wc[kTilesPerWave][kQuads];
     load_tile(0, wb[0], wc[0]);
-    long a[kGroups];
     float row_scale[4];
     if constexpr (kQuantize) {
         static_assert(I == 512u, "one wave per 512-wide row");
-        constexpr uint32_t kRowsPerWave = 4u;  // 16 rows over 4 waves
+        constexpr uint32_t kRowsPerWave = 16u / kWaves;
         uint4 mv[kRowsPerWave];
 #pragma unroll
         for (uint32_t j = 0; j < kRowsPerWave; ++j) {
@@ -606,20 +612,23 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
         }
         __syncthreads();
 #pragma unroll
-        for (uint32_t g = 0; g < kGroups; ++g) a[g] = as_long(a_lds[g * 64u + lane]);
-#pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) row_scale[i] = scale_lds[4u * q + i];
     } else {
-        const uint32_t a_row = n < rows ? n : 0u;
-        const uint2* xa =
-            reinterpret_cast<const uint2*>(mid.q + static_cast<size_t>(p0 + a_row) * I) + q;
+        // row n, lane group q of every group, through LDS like the
+        // quantising path
+        if (wave == 0u) {
+            const uint32_t a_row = n < rows ? n : 0u;
+            const uint2* xa =
+                reinterpret_cast<const uint2*>(mid.q + static_cast<size_t>(p0 + a_row) * I) + q;
 #pragma unroll
-        for (uint32_t g = 0; g < kGroups; ++g) a[g] = as_long(xa[g * 4u]);
+            for (uint32_t g = 0; g < kGroups; ++g) a_lds[g * 64u + lane] = xa[g * 4u];
+        }
 #pragma unroll
         for (uint32_t i = 0; i < 4u; ++i) {
             const uint32_t r = 4u * q + i;
             row_scale[i] = mid.s[p0 + (r < rows ? r : 0u)];
         }
+        __syncthreads();
     }
     const v4i zero = {0, 0, 0, 0};
 #pragma unroll
@@ -632,7 +641,7 @@ __global__ __launch_bounds__(256) void down_w4_kernel(
             v4i d = zero;
 #pragma unroll
             for (uint32_t j = 0; j < 4u; ++j) {
-                d = mfma_i8_16x16x32(a[kq * 4u + j], unpack_w4x16(bw[j]), j % kSub == 0u ? zero : d);
+                d = mfma_i8_16x16x32(as_long(a_lds[(kq * 4u + j) * 64u + lane]), unpack_w4x16(bw[j]), j % kSub == 0u ? zero : d);
                 if (j % kSub != kSub - 1u) continue;
                 const float scale =
                     scale_to_f32(quad_scale_word(wc[t][kq], j / kSub), kBf16) * 0.0625f;
@@ -791,16 +800,19 @@ template <uint32_t kSub, bool kQuantize>
 void launch_down_w4_sub(const q38m_expert_weights_v1& w, const MidRows& mid,
                         const q38m_task_v1* tasks, uint32_t task_count,
                         float* route_output, hipStream_t stream) {
-    constexpr uint32_t kTilesPerWave = 4;
-    const dim3 grid(kHidden / 16u / (4u * kTilesPerWave), task_count);
+    // groups of 128: 16 waves x 1 tile (interior reference format, slab
+    // step 0.1818 -> 0.1759 ms); 32 and 64: 8 waves x 2 tiles
+    constexpr uint32_t kWaves = kSub == 4u ? 16u : 8u;
+    constexpr uint32_t kTilesPerWave = 16u / kWaves;
+    const dim3 grid(kHidden / 16u / 16u, task_count);
     const auto* data = static_cast<const uint4*>(w.data);
     const auto* scales = static_cast<const uint16_t*>(w.scales);
     if (w.scale_dtype == Q38M_SCALE_BF16)
-        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, true, kQuantize>
-            <<<grid, 256, 0, stream>>>(data, scales, mid, tasks, route_output);
+        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, true, kQuantize, kWaves>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid, tasks, route_output);
     else
-        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, false, kQuantize>
-            <<<grid, 256, 0, stream>>>(data, scales, mid, tasks, route_output);
+        down_w4_kernel<kHidden, kInter, kTilesPerWave, kSub, false, kQuantize, kWaves>
+            <<<grid, kWaves * 64u, 0, stream>>>(data, scales, mid, tasks, route_output);
 }
 
 template <bool kQuantize>
