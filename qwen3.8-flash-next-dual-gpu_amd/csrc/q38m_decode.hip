@@ -371,20 +371,6 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
     stamps.mark_loaded(5);
     stamps.mark_wave_loaded(wave_stamp_lds);
 
-    // Once this wave's weights and scales are in, the down launch's pieces
-    // of route `wave` (waves 10 and 11 repeat expert 0's): issued earlier,
-    // they share HBM with the other workgroups' gate/up weights and delay
-    // them more than they save.  Every barrier after this point waits for
-    // LDS only, so the prefetch stays in flight until the kernel's end.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    uint32_t prefetched;
-    {
-        const int32_t pid = wave < top_k ? ids_lds[wave] : -1;
-        const uint32_t pe =
-            pid >= 0 && pid < static_cast<int32_t>(kExperts) ? static_cast<uint32_t>(pid) : 0u;
-        prefetched = prefetch_down(prefetch, pe, lane);
-    }
-    __builtin_amdgcn_sched_barrier(0);
 
     // this lane's group sums (int32) and their scales (fp32 words)
     uint4 xa = make_uint4(0u, 0u, 0u, 0u), xf = make_uint4(0u, 0u, 0u, 0u);
@@ -446,6 +432,23 @@ __global__ __launch_bounds__(kGateUpThreads) void decode_gate_up_kernel(
             xf.x = __float_as_uint(scale_to_f32(sw, bf16));
         }
     }
+    // This wave's weights and scales are consumed: now the down launch's
+    // pieces of route `wave` (waves 10 and 11 repeat expert 0's), issued
+    // while the waves wait for each other at the exchange.  Issued right
+    // behind this launch's own weight requests they share HBM with the other
+    // workgroups' gate/up weights and delay them more than they save; issued
+    // before the group sums they hold those up.  Every barrier after this
+    // point waits for LDS only, so the prefetch stays in flight until the
+    // kernel's end.
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t prefetched;
+    {
+        const int32_t pid = wave < top_k ? ids_lds[wave] : -1;
+        const uint32_t pe =
+            pid >= 0 && pid < static_cast<int32_t>(kExperts) ? static_cast<uint32_t>(pid) : 0u;
+        prefetched = prefetch_down(prefetch, pe, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     stamps.mark(6);
     {
         const uint32_t chain = 16u * slot_rs + 2u * n + u;
