@@ -43,6 +43,41 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(
     if (lane == 0) scales[row] = qs.s;
 }
 
+// 512-wide rows (the mid rows), kRows rows per wave with all their loads
+// issued together and non-temporal (each row is read once; 327,680 rows:
+// 101 -> 94 us against one row per wave); the same per-row arithmetic as
+// quantize_rows_kernel.
+template <uint32_t kRows>
+__global__ __launch_bounds__(256) void quantize_rows512_kernel(
+    const uint16_t* __restrict__ x, uint32_t rows, int8_t* __restrict__ q,
+    float* __restrict__ scales) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row0 = (blockIdx.x * 4u + (threadIdx.x >> 6)) * kRows;
+    u4v v[kRows];
+#pragma unroll
+    for (uint32_t j = 0; j < kRows; ++j) {
+        const uint32_t row = row0 + j < rows ? row0 + j : rows - 1u;
+        v[j] = __builtin_nontemporal_load(
+            reinterpret_cast<const u4v*>(x + static_cast<size_t>(row) * 512u) + lane);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kRows; ++j) {
+        const uint32_t row = row0 + j;
+        if (row >= rows) break;
+        const uint32_t w[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] & 0xffffu)));
+            amax = fmaxf(amax, fabsf(bf16_to_f32(w[i] >> 16)));
+        }
+        const QuantScale qs = quant_scale(wave_max_f32(amax));
+        reinterpret_cast<uint2*>(q + static_cast<size_t>(row) * 512u)[lane] = quantize8(w, qs);
+        if (lane == 0) scales[row] = qs.s;
+    }
+}
+
 // Gather hidden[token(packed)] -> packed order (q38_moe_prefill.cu:292-306).
 __global__ __launch_bounds__(256) void pack_hidden_kernel(
     const uint16_t* __restrict__ hidden, const uint32_t* __restrict__ packed,
@@ -54,13 +89,17 @@ __global__ __launch_bounds__(256) void pack_hidden_kernel(
     for (uint32_t i = threadIdx.x; i < width / 8u; i += blockDim.x) dst[i] = src[i];
 }
 
-// out = bf16(a + b) in fp32, 8 elements per thread.
+// out = bf16(a + b) in fp32, 8 elements per thread; both inputs are read
+// once, with non-temporal loads (32,768 x 2048: 71 -> 62 us).
 __global__ __launch_bounds__(256) void residual_add_kernel(
     const uint4* __restrict__ a, const uint4* __restrict__ b, uint4* __restrict__ out,
     uint64_t vectors) {
     const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= vectors) return;
-    const uint4 va = a[i], vb = b[i];
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const u4v na = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(a) + i);
+    const u4v nb = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(b) + i);
+    const uint4 va = make_uint4(na.x, na.y, na.z, na.w), vb = make_uint4(nb.x, nb.y, nb.z, nb.w);
     const uint32_t wa[4] = {va.x, va.y, va.z, va.w};
     const uint32_t wb[4] = {vb.x, vb.y, vb.z, vb.w};
     uint32_t r[4];
@@ -88,7 +127,9 @@ hipError_t launch_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width
                                 int8_t* q, float* scales, hipStream_t stream) {
     const dim3 grid((rows + 3u) / 4u);
     switch (width / 512u) {
-        case 1: quantize_rows_kernel<1><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
+        case 1:
+            quantize_rows512_kernel<4><<<(rows + 15u) / 16u, 256, 0, stream>>>(x, rows, q, scales);
+            break;
         case 2: quantize_rows_kernel<2><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
         case 4: quantize_rows_kernel<4><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
         case 8: quantize_rows_kernel<8><<<grid, 256, 0, stream>>>(x, rows, q, scales); break;
