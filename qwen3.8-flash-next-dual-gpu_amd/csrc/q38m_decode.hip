@@ -13,13 +13,14 @@
 // so the layer is two launches and every byte of each launch is requested
 // as early as its address is known.
 //
-//   gate/up  256 workgroups x 10 waves (one wave per route).  Waves 0-7
-//            rank the 512 router logits (or wave 9 reads the given ids) while
-//            waves 0-3 also load the token; then every lane issues its 72 bytes of weights
-//            at once (46 KB per workgroup, the layer's 11.8 MB in flight
-//            together).  Workgroup b owns channels 16p+n0, 16p+n0+1 of all
-//            routes; the eight workgroups sharing a pair tile's 128-byte
-//            lines sit on one XCD (b % 8), so each line crosses HBM once.
+//   gate/up  256 workgroups x 12 waves (three route slots x four quarters
+//            of K).  Waves 0-7 rank the 512 router logits (or wave 9 reads
+//            the given ids) while waves 0-3 also load the token; then every
+//            lane issues its weight loads at once (46 KB per workgroup, the
+//            layer's 11.8 MB in flight together).  Workgroup b owns eight
+//            channels (gate and up rows) of one pair tile for a group of 2-3
+//            routes; the two halves of a pair tile's group sit on one XCD
+//            (b % 8), so each scale line crosses HBM once.
 //            Once its weights are in, each wave requests the lines the
 //            down launch's workgroup b will read, so they are cached.
 //   down     256 workgroups x 10 waves.  Each wave loads the ids and its

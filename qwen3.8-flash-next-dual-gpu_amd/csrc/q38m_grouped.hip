@@ -379,8 +379,9 @@ void gate_up_w8_kernel(
 // output tiles of one task.  The task's 16 int8 mid rows (8 KiB) are staged
 // into LDS once in the MFMA A-operand order ([k block][lane], 16 bytes per
 // lane).  Each wave streams its tiles in half-tile units (4 K blocks = 4 KiB
-// per wave) with a pinned one-unit-ahead prefetch; at ~60 VGPRs eight waves
-// per SIMD keep ~128 KB of weights in flight per CU.
+// per wave) with a pinned one-unit-ahead prefetch; the launch uses 16 waves
+// of one tile each, and at ~51-71 VGPRs seven or eight waves per SIMD keep
+// ~128 KB of weights in flight per CU.
 // ---------------------------------------------------------------------------
 template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave,
           uint32_t kBlocksPerGroup, bool kBf16, bool kQuantize>
