@@ -234,14 +234,13 @@ void gate_up_w4_kernel(
 // Scales stay in the artifact order [E][rows][K/G] (gate rows 0..I-1, up
 // rows I..2I-1).  Then y * s_t and the SwiGLU fold, as the W4 kernel.
 // Same plan as the W4 kernel: the task's 16 token rows (32 KiB) staged once
-// in LDS in the A-operand order ([block][lane], 16 bytes per lane), weights
-// two blocks ahead through three register sets, one contiguous span of
-// 2*kWaves KiB per step.
+// in LDS in the A-operand order ([block][lane], 16 bytes per lane); each
+// wave streams ONE tile (the gate tile, w even, or the up tile, w odd, of
+// pair blockIdx.x * kWaves/2 + w/2) two blocks ahead through three register
+// sets, and the up wave hands its y to the gate wave through LDS for the
+// SwiGLU (against a gate + up pair per wave: edge-format slab step 0.3162
+// -> 0.3116 ms; 16 waves per workgroup 0.324 ms).
 // ---------------------------------------------------------------------------
-struct BlockWeights {
-    uint4 g, u;       // gate and up tile data of one K block
-    uint32_t sg, su;  // their scale words for the block's group
-};
 
 template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kBlocksPerGroup, bool kBf16>
 __global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6, 8)))
@@ -256,6 +255,7 @@ void gate_up_w8_kernel(
     constexpr bool kPerChannel = kBlocksPerGroup == kBlocks;
     constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
     __shared__ uint4 a_lds[kBlocks * 64u];
+    __shared__ float up_lds[kWaves / 2u][4][64];
 
     const TaskRecord task = read_task(tasks, blockIdx.y);
     const uint32_t rows = task.rows;
@@ -264,21 +264,25 @@ void gate_up_w8_kernel(
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
-    const uint32_t pair = blockIdx.x * kWaves + wave;
+    const uint32_t pair = blockIdx.x * (kWaves / 2u) + (wave >> 1);
+    const uint32_t up = wave & 1u;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.begin;
 
     constexpr uint32_t kBlockWords = kTiles * 64u;  // uint4 per K block of one expert
-    const uint4* wbase = w + (static_cast<size_t>(e) * kBlocks * kTiles + 2u * pair) * 64u;
-    // this lane's gate row 16p+n and up row I+16p+n
-    const uint16_t* sg_row = s + (static_cast<size_t>(e) * 2u * I + pair * 16u + n) * kGroups;
-    const uint16_t* su_row = sg_row + static_cast<size_t>(I) * kGroups;
+    const uint4* wbase = w + (static_cast<size_t>(e) * kBlocks * kTiles + 2u * pair + up) * 64u;
+    // this lane's row: gate 16p+n or up I+16p+n
+    const uint16_t* s_row =
+        s + (static_cast<size_t>(e) * 2u * I + (up ? I : 0u) + pair * 16u + n) * kGroups;
+    struct TileBlock {
+        uint4 w;
+        uint32_t s;
+    };
     auto load = [&](uint32_t kb) {
         const uint32_t k = kb < kBlocks ? kb : kBlocks - 1u;  // past the end: re-read (L1 hit)
         const uint32_t wi = k * kBlockWords + lane;
         const uint32_t g = kPerChannel ? 0u : k / kBlocksPerGroup;
-        return BlockWeights{load_stream(wbase + wi), load_stream(wbase + wi + 64u),
-                            static_cast<uint32_t>(sg_row[g]), static_cast<uint32_t>(su_row[g])};
+        return TileBlock{load_stream(wbase + wi), static_cast<uint32_t>(s_row[g])};
     };
 
     // Stage A: 16-byte chunk c of token row r is K block c/4, lane group c%4;
@@ -291,7 +295,7 @@ void gate_up_w8_kernel(
         const uint32_t r = (threadIdx.x + c * kThreads) / (H / 16u);
         token[c] = checked(packed[p0 + (r < rows ? r : 0u)], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
     }
-    BlockWeights r0 = load(0), r1 = load(1), r2;
+    TileBlock r0 = load(0), r1 = load(1), r2;
     uint4 v[kChunks];
 #pragma unroll
     for (uint32_t c = 0; c < kChunks; ++c) {
@@ -307,23 +311,18 @@ void gate_up_w8_kernel(
     __syncthreads();
 
     const v4i zero = {0, 0, 0, 0};
-    v4i cg = zero, cu = zero;
-    float yg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float yu[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    auto block = [&](uint32_t kb, const BlockWeights& b) {
+    v4i c = zero;
+    float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto block = [&](uint32_t kb, const TileBlock& b) {
         const v4i a = as_v4i(a_lds[kb * 64u + lane]);
         const bool first = kb % kBlocksPerGroup == 0u;
-        cg = mfma_i8_16x16x64(a, as_v4i(b.g), first ? zero : cg);
-        cu = mfma_i8_16x16x64(a, as_v4i(b.u), first ? zero : cu);
+        c = mfma_i8_16x16x64(a, as_v4i(b.w), first ? zero : c);
         if constexpr (!kPerChannel) {
             if (kb % kBlocksPerGroup == kBlocksPerGroup - 1u) {
-                const float scale_g = scale_to_f32(b.sg, kBf16);
-                const float scale_u = scale_to_f32(b.su, kBf16);
+                const float scale = scale_to_f32(b.s, kBf16);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    yg[i] = __builtin_fmaf(static_cast<float>(cg[i]), scale_g, yg[i]);
-                    yu[i] = __builtin_fmaf(static_cast<float>(cu[i]), scale_u, yu[i]);
-                }
+                for (int i = 0; i < 4; ++i)
+                    y[i] = __builtin_fmaf(static_cast<float>(c[i]), scale, y[i]);
             }
         }
     };
@@ -343,15 +342,18 @@ void gate_up_w8_kernel(
     block(kBlocks - 2u, r0);
     block(kBlocks - 1u, r1);
     if constexpr (kPerChannel) {
-        const float scale_g = scale_to_f32(r1.sg, kBf16);
-        const float scale_u = scale_to_f32(r1.su, kBf16);
+        const float scale = scale_to_f32(r1.s, kBf16);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            yg[i] = static_cast<float>(cg[i]) * scale_g;
-            yu[i] = static_cast<float>(cu[i]) * scale_u;
-        }
+        for (int i = 0; i < 4; ++i) y[i] = static_cast<float>(c[i]) * scale;
     }
 
+    // the up wave's y to its gate wave
+    if (up) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) up_lds[wave >> 1][i][lane] = y[i];
+    }
+    __syncthreads();
+    if (up) return;
     const uint32_t channel = pair * 16u + n;
 #pragma unroll
     for (uint32_t i = 0; i < 4u; ++i) {
@@ -361,7 +363,7 @@ void gate_up_w8_kernel(
         const uint32_t a = checked(packed[p], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
         const float st = xs[a / kTopK];
         mid[static_cast<size_t>(p) * I + channel] =
-            static_cast<uint16_t>(swiglu_fold(yg[i] * st, yu[i] * st, route_weights[a]));
+            static_cast<uint16_t>(swiglu_fold(y[i] * st, up_lds[wave >> 1][i][lane] * st, route_weights[a]));
     }
 }
 
@@ -769,7 +771,7 @@ void launch_gate_up_w8_groups(const q38m_expert_weights_v1& w, const int8_t* xq,
                               const q38m_task_v1* tasks, uint32_t task_count,
                               uint16_t* weighted_mid, hipStream_t stream) {
     constexpr uint32_t kWaves = 8;
-    const dim3 grid(kInter / 16u / kWaves, task_count);
+    const dim3 grid(kInter / 16u / (kWaves / 2u), task_count);
     const auto* data = static_cast<const uint4*>(w.data);
     const auto* scales = static_cast<const uint16_t*>(w.scales);
     if (w.scale_dtype == Q38M_SCALE_BF16)
