@@ -227,7 +227,7 @@ def counters_summary():
     if slab:
         agg, agent = slab
         out["workload_slab"] = PMC_WORKLOADS["slab"]
-        for k in ("gate_up_w4_kernel", "down_w8_kernel"):
+        for k in ("gate_up_down_kernel", "gate_up_w4_kernel", "down_w8_kernel"):
             hit = pick(agg, k)
             if hit:
                 out[f"{k} (config 2 slab)"] = dict(grid=hit[0], **mfma_metrics(hit[1], agent))
@@ -338,7 +338,8 @@ def pmc_report(workload, traffic_dir=None):
             f"{f(wi / wc * 100 if wc else None, 1)}% | {f(wa / wc * 100 if wc else None, 1)}% | "
             f"{f(fb and fb / 1e6, 1)} | {f(wb and wb / 1e6, 1)} |")
         base = k.split("<")[0]
-        if workload == "slab" and base in ("gate_up_w4_kernel", "down_w8_kernel") and fb and wb:
+        if workload == "slab" and base in ("gate_up_down_kernel", "gate_up_w4_kernel",
+                                           "down_w8_kernel") and fb and wb:
             # the headline slab's grids have the most launches
             if base not in traffic or len(td or []) > traffic[base][0]:
                 traffic[base] = (len(td or []), fb, wb)
@@ -472,12 +473,37 @@ def main():
         if events is not None:
             events[-1].record(stream)
 
+    # the one-call step's kernels one entry point at a time: gate/up, the mid
+    # quantisation and down as the one launch q38m_moe_prefill_v1 makes of
+    # them (q38m_moe_grouped_gate_up_down_v1, whose hand-off flags are
+    # cleared once here and left zero by every call)
+    fused_names = ["route_quant", "plan", "gate_up_down", "combine"]
+    header_status = ws.plan.header + 24  # q38m_route_plan_header_v1.status
+
+    def launch_fused_stage(i):
+        if i == 2:
+            q38m.call("q38m_moe_grouped_gate_up_down_v1", ctypes.byref(gu.desc),
+                      ctypes.byref(dn.desc), ws.xq, ws.xs, ws.plan.packed_assignment,
+                      ws.expert_weights, ws.plan.tasks, max_tasks, ws.weighted_mid, ws.mid_q,
+                      ws.mid_s, ws.task_flags, header_status, ws.route_output,
+                      q38m.MODE_GROUPED_MMQ, sh, 0)
+        else:
+            launch_stage({0: 0, 1: 1, 3: 5}[i])
+
+    def fused_stages(events=None):
+        for i in range(len(fused_names)):
+            if events is not None:
+                events[i].record(stream)
+            launch_fused_stage(i)
+        if events is not None:
+            events[-1].record(stream)
+
     def fused_step():
         q38m.call("q38m_moe_prefill_v1", ctypes.byref(gu.desc), ctypes.byref(dn.desc),
                   hidden.data_ptr(), logits.data_ptr(), T, ctypes.byref(ws), None, None,
                   out.data_ptr(), sh, 0)
 
-    # the fused entry point must agree with the stage sequence
+    # the fused entry point must agree with both stage sequences
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -485,6 +511,12 @@ def main():
     fused_step()
     torch.cuda.synchronize()
     assert torch.equal(staged, out), "fused and staged prefill disagree"
+    out.zero_()
+    q38m.call("q38m_moe_clear_task_flags_v1", ws.task_flags, max_tasks, sh, 0)
+    for _ in range(args.warmup):
+        fused_stages()
+    torch.cuda.synchronize()
+    assert torch.equal(staged, out), "one-launch gate/up + down stages and staged prefill disagree"
     for _ in range(args.warmup):
         fused_step()
 
@@ -511,6 +543,19 @@ def main():
     stage_ms = [statistics.fmean(events[k][i].elapsed_time(events[k][i + 1])
                                  for k in range(args.steps)) for i in range(len(stage_names))]
 
+    # timed region 3: the one-call step's own kernels, one entry point at a
+    # time (per-kernel durations of the headline step: the roofline)
+    fevents = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fused_names) + 1)]
+               for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t2 = time.perf_counter()
+    for k in range(args.steps):
+        fused_stages(fevents[k])
+    torch.cuda.synchronize()
+    fused_stages_ms_per_step = (time.perf_counter() - t2) * 1e3 / args.steps
+    fused_ms = [statistics.fmean(fevents[k][i].elapsed_time(fevents[k][i + 1])
+                                 for k in range(args.steps)) for i in range(len(fused_names))]
+
     # algorithmic counts (per launch / per step)
     ids = torch.empty(routes, dtype=torch.int32, device="cuda")
     base = wsb.buffer.data_ptr()
@@ -522,9 +567,16 @@ def main():
                      routes * W.INTER * 2)
     down_bytes = (active * dn_bytes_expert + routes * W.INTER + routes * 4 +
                   routes * W.HIDDEN * 4)
+    # the headline step's kernels: gate/up + down is one launch
+    # (gate_up_down_kernel); the separate kernels of the staged entry points
+    # are reported beside it
     kernels = {
-        "gate_up": (stage_ms[stage_names.index("gate_up")], gate_up_bytes, "gate_up_w4_kernel"),
-        "down": (stage_ms[stage_names.index("down")], down_bytes, "down_w8_kernel"),
+        "gate_up_down": (fused_ms[fused_names.index("gate_up_down")], gate_up_bytes + down_bytes,
+                         "gate_up_down_kernel"),
+    }
+    separate = {
+        "gate_up_w4_kernel": (stage_ms[stage_names.index("gate_up")], gate_up_bytes),
+        "down_w8_kernel": (stage_ms[stage_names.index("down")], down_bytes),
     }
     dominant = max(kernels, key=lambda k: kernels[k][0])
     d_ms, d_bytes, d_symbol = kernels[dominant]
@@ -566,14 +618,23 @@ def main():
                           "hbm_bound_mfma_ceiling": round(
                               (step_ops / (step_bytes / (HBM_PEAK_GBPS * 1e9))) / 1e12 /
                               INT8_PEAK_TOPS, 4)},
-        "stages_ms": {n: round(v, 5) for n, v in zip(stage_names, stage_ms)},
+        "stages_ms": {n: round(v, 5) for n, v in zip(fused_names, fused_ms)},
+        "separate_kernels": {
+            "stages_ms": {n: round(v, 5) for n, v in zip(stage_names, stage_ms)},
+            "rooflines": {k: {"avg_ms": round(ms_, 5), "algorithmic_bytes": b,
+                              "hbm_frac": round(b / (ms_ * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+                          for k, (ms_, b) in separate.items()},
+            "note": "the reference's staged boundary (grouped gate/up, mid quantisation, "
+                    "grouped down as three launches); q38m_moe_prefill_v1 runs them as one"},
         "timing": {"value": "wall clock over the timed K calls of q38m_moe_prefill_v1",
                    "plan_hashes": "the timed step builds the route plan without the FNV "
                                   "route/plan hashes (header words route_hash and plan_hash "
                                   "left zero, as q38m_moe_build_route_plan_v1 with hashes=0); "
                                   "nothing in the step reads them",
-                   "stages_ms": "HIP events around each entry point over a second timed run "
-                                "of K staged steps (same kernels)",
+                   "stages_ms": "HIP events around each entry point over a timed run of K "
+                                "steps through the step's own kernels (route + quantise, plan, "
+                                "q38m_moe_grouped_gate_up_down_v1, combine)",
+                   "stages_ms_per_step": round(fused_stages_ms_per_step, 4),
                    "staged_ms_per_step": round(staged_ms_per_step, 4)},
     }
 
@@ -625,12 +686,10 @@ def main():
                                      "valu_issue_share_est")}
         if wide and "config5_stack" in result:
             result["config5_stack"]["contract_ceilings"] = contract_ceilings(wide)
-        slab_ops = [counters[k]["int8_ops_counter"] for k in
-                    ("gate_up_w4_kernel (config 2 slab)", "down_w8_kernel (config 2 slab)")
-                    if counters and k in counters]
-        if len(slab_ops) == 2:
+        fused_ops = counters and counters.get("gate_up_down_kernel (config 2 slab)")
+        if fused_ops:
             result["step_roofline"]["int8_mfma_frac_counter"] = round(
-                sum(slab_ops) / step_s / 1e12 / INT8_PEAK_TOPS, 5)
+                fused_ops["int8_ops_counter"] / step_s / 1e12 / INT8_PEAK_TOPS, 5)
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(q38m, W, torch, gu_rm, dn_rm, hidden, logits, out,

@@ -64,6 +64,12 @@ extern "C" {
 #define Q38M_PLAN_OK 0u
 #define Q38M_PLAN_INVALID_EXPERT 1u
 #define Q38M_PLAN_INVALID_SHAPE 2u
+/* No reference counterpart: ORed into the plan status by the one-launch
+ * gate/up + down (q38m_moe_prefill_v1, q38m_moe_grouped_gate_up_down_v1)
+ * when a down workgroup's bounded wait for its task's gate/up workgroups
+ * ran out; that step's outputs are then invalid.  Not expected to occur
+ * (see q38m_moe_grouped_gate_up_down_v1). */
+#define Q38M_PLAN_STEP_TIMEOUT 4u
 
 /* Q38PrefillMoeModeV1, include/q38/cuda_moe_prefill.h:67-71.  The grouped
  * gate/up and down entry points take the mode argument of the reference and
@@ -252,6 +258,40 @@ int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down,
                              const q38m_task_v1* tasks, uint32_t task_count,
                              float* route_output, uint32_t mode, void* stream, int device);
 
+/* No reference counterpart: cuda_moe_grouped_gate_up_v1, the mid
+ * quantisation (q38m_quantize_rows_i8) and cuda_moe_grouped_down_v1
+ * (include/q38/cuda_moe_prefill.h:112-125) as one call, with their
+ * results bit for bit (weighted_mid, mid_q/mid_scales, route_output).  W4
+ * gate/up with per-channel W8 down of one scale dtype run as ONE launch
+ * whose down workgroups start while the last gate/up workgroups still
+ * stream; other format pairs run the three kernels.  task_flags:
+ * 9 * task_count words (8 hand-off flags and a counter per task) that must
+ * be ZERO on entry: clear them once with q38m_moe_clear_task_flags_v1
+ * after allocating them; the call leaves them zero (the last down
+ * workgroup of each task clears the task's words).  plan_status (normally
+ * &plan.header->status): a down workgroup ORs Q38M_PLAN_STEP_TIMEOUT into
+ * it if its bounded wait for its task's gate/up workgroups runs out --
+ * that call's outputs are invalid and the flags must be cleared again.
+ * Workgroups are dispatched in block order and every gate/up workgroup
+ * precedes every down workgroup, so the wait always ends within a gate/up
+ * workgroup's lifetime; the bound only caps a broken dispatch order.
+ * mode as for gate/up. */
+int q38m_moe_grouped_gate_up_down_v1(const q38m_expert_weights_v1* gate_up,
+                                     const q38m_expert_weights_v1* down,
+                                     const int8_t* xq, const float* xs,
+                                     const uint32_t* packed_assignment,
+                                     const float* token_rank_weights,
+                                     const q38m_task_v1* tasks, uint32_t task_count,
+                                     uint16_t* weighted_mid, int8_t* mid_q,
+                                     float* mid_scales, uint32_t* task_flags,
+                                     uint32_t* plan_status, float* route_output,
+                                     uint32_t mode, void* stream, int device);
+
+/* No reference counterpart: zeroes the 9 * task_count words of a
+ * q38m_moe_grouped_gate_up_down_v1 task_flags buffer (a fill kernel). */
+int q38m_moe_clear_task_flags_v1(uint32_t* task_flags, uint32_t task_count, void* stream,
+                                 int device);
+
 /* cuda_moe_reduce_top10_and_combine_shared_v1,
  * include/q38/cuda_moe_prefill.h:127-131.  shared_output/shared_gate may
  * both be NULL (no shared expert). */
@@ -281,6 +321,11 @@ typedef struct q38m_prefill_workspace_v1 {
     int8_t* mid_q;           /* [T*10][I] */
     float* mid_s;            /* [T*10] */
     float* route_output;     /* [T*10][H] */
+    /* No reference counterpart: the gate/up -> down hand-off flags of the
+     * one-launch gate/up + down (8 flags and a counter per task slot),
+     * cleared by the step's plan kernel.  NULL: the step runs gate/up and
+     * down as two launches. */
+    uint32_t* task_flags;    /* [max_tasks(T)*9] */
 } q38m_prefill_workspace_v1;
 
 /* Bytes of one contiguous workspace for `tokens` (<= 512) and its binding
@@ -293,7 +338,10 @@ int q38m_moe_prefill_workspace_bind(void* allocation, size_t bytes,
 /* One MoE layer over a slab of <= 512 tokens: top-k (when logits is not
  * NULL; else expert_ids/expert_weights in the workspace are inputs),
  * route plan, int8 quantisation, grouped gate/up, mid quantisation,
- * grouped down, fixed-order combine. */
+ * grouped down, fixed-order combine.  With W4 gate/up and per-channel W8
+ * down weights of one scale dtype (and ws->task_flags set), gate/up, the mid
+ * quantisation and down run as one launch (q38m_moe_grouped_gate_up_down_v1);
+ * the results are the same bit for bit. */
 int q38m_moe_prefill_v1(const q38m_expert_weights_v1* gate_up,
                         const q38m_expert_weights_v1* down,
                         const uint16_t* hidden, const float* logits,

@@ -128,6 +128,32 @@ inline void cuda_moe_grouped_down_v1(const ExpertWeightsV1& down_experts,
                                    device));
 }
 
+// No reference counterpart: the gate/up, mid quantisation and down calls
+// above as one (one launch for W4 gate/up with per-channel W8 down), same
+// results; task_flags (9 * task_count words) zero on entry, see q38m.h.
+inline void moe_clear_task_flags_v1(std::uint32_t* task_flags, std::uint32_t task_count,
+                                    void* stream, int device) {
+    check(q38m_moe_clear_task_flags_v1(task_flags, task_count, stream, device));
+}
+
+inline void moe_grouped_gate_up_down_v1(const ExpertWeightsV1& gate_up_experts,
+                                        const ExpertWeightsV1& down_experts,
+                                        const std::int8_t* xq, const float* xs,
+                                        const std::uint32_t* packed_assignment,
+                                        const float* token_rank_weights,
+                                        const Q38ExpertMmqTaskV1* tasks,
+                                        std::uint32_t task_count, std::uint16_t* weighted_mid,
+                                        std::int8_t* mid_q, float* mid_scales,
+                                        std::uint32_t* task_flags, std::uint32_t* plan_status,
+                                        float* route_output, Q38PrefillMoeModeV1 mode,
+                                        void* stream, int device) {
+    check(q38m_moe_grouped_gate_up_down_v1(&gate_up_experts, &down_experts, xq, xs,
+                                           packed_assignment, token_rank_weights, tasks,
+                                           task_count, weighted_mid, mid_q, mid_scales,
+                                           task_flags, plan_status, route_output,
+                                           static_cast<std::uint32_t>(mode), stream, device));
+}
+
 inline void cuda_moe_reduce_top10_and_combine_shared_v1(
     const float* route_output, const std::uint32_t* assignment_to_packed,
     const std::uint16_t* shared_output, const std::uint16_t* shared_gate, std::uint32_t tokens,

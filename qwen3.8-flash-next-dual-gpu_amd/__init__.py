@@ -103,7 +103,8 @@ class PrefillWorkspace(ctypes.Structure):
                 ("expert_ids", ctypes.c_void_p), ("expert_weights", ctypes.c_void_p),
                 ("xq", ctypes.c_void_p), ("xs", ctypes.c_void_p),
                 ("weighted_mid", ctypes.c_void_p), ("mid_q", ctypes.c_void_p),
-                ("mid_s", ctypes.c_void_p), ("route_output", ctypes.c_void_p)]
+                ("mid_s", ctypes.c_void_p), ("route_output", ctypes.c_void_p),
+                ("task_flags", ctypes.c_void_p)]
 
 
 class WideWorkspace(ctypes.Structure):
@@ -135,6 +136,10 @@ SIGNATURES = {
                                            _U32, _P, _U32, _P, _INT]),
     "q38m_moe_grouped_down_v1": (_INT, [ctypes.POINTER(ExpertWeights), _P, _P, _P, _U32, _P,
                                         _U32, _P, _INT]),
+    "q38m_moe_grouped_gate_up_down_v1": (_INT, [ctypes.POINTER(ExpertWeights),
+                                                ctypes.POINTER(ExpertWeights), _P, _P, _P, _P, _P,
+                                                _U32, _P, _P, _P, _P, _P, _P, _U32, _P, _INT]),
+    "q38m_moe_clear_task_flags_v1": (_INT, [_P, _U32, _P, _INT]),
     "q38m_moe_reduce_top10_and_combine_shared_v1": (_INT, [_P, _P, _P, _P, _U32, _P, _P, _INT]),
     "q38m_moe_combine_shared_bf16": (_INT, [_P, _P, _P, _P, _U32, _P, _INT]),
     "q38m_moe_prefill_workspace_bytes": (_SZ, [_U32]),

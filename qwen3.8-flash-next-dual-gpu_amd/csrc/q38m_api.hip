@@ -315,6 +315,44 @@ int q38m_moe_grouped_down_v1(const q38m_expert_weights_v1* down, const int8_t* m
                   "grouped down kernel");
 }
 
+int q38m_moe_grouped_gate_up_down_v1(const q38m_expert_weights_v1* gate_up,
+                                     const q38m_expert_weights_v1* down, const int8_t* xq,
+                                     const float* xs, const uint32_t* packed_assignment,
+                                     const float* token_rank_weights,
+                                     const q38m_task_v1* tasks, uint32_t task_count,
+                                     uint16_t* weighted_mid, int8_t* mid_q, float* mid_scales,
+                                     uint32_t* task_flags, uint32_t* plan_status,
+                                     float* route_output, uint32_t mode, void* stream,
+                                     int device) {
+    if (!valid_grouped_mode(mode))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill MoE mode");
+    if (int rc = check_weights(gate_up, true)) return rc;
+    if (int rc = check_weights(down, false)) return rc;
+    if (!xq || !xs || !packed_assignment || !token_rank_weights || !tasks || task_count == 0 ||
+        task_count > q38m::max_tasks_v1(Q38M_PREFILL_SLAB_MAX_TOKENS) || !weighted_mid ||
+        !mid_q || !mid_scales || !task_flags || !plan_status || !route_output ||
+        !aligned(xq, 8) || !aligned(tasks, 8) || !aligned(mid_q, 16) || !aligned(task_flags, 4) ||
+        !aligned(plan_status, 4))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid grouped prefill gate/up + down input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_gate_up_down(*gate_up, *down, xq, xs, packed_assignment,
+                                            token_rank_weights, tasks, task_count, weighted_mid,
+                                            mid_q, mid_scales, route_output, task_flags,
+                                            plan_status, as_stream(stream)),
+                  "grouped gate/up + down kernels");
+}
+
+int q38m_moe_clear_task_flags_v1(uint32_t* task_flags, uint32_t task_count, void* stream,
+                                 int device) {
+    if (!task_flags || task_count == 0 ||
+        task_count > q38m::max_tasks_v1(Q38M_PREFILL_SLAB_MAX_TOKENS) || !aligned(task_flags, 4))
+        return fail(Q38M_ERR_INVALID_ARGUMENT, "invalid task-flag clear input");
+    if (int rc = select_device(device)) return rc;
+    return finish(q38m::launch_clear_words(task_flags, q38m::task_flag_words(task_count),
+                                           as_stream(stream)),
+                  "clear_words_kernel");
+}
+
 int q38m_moe_reduce_top10_and_combine_shared_v1(const float* route_output,
                                                 const uint32_t* assignment_to_packed,
                                                 const uint16_t* shared_output,
@@ -344,7 +382,8 @@ int q38m_moe_combine_shared_bf16(const uint16_t* routed_output, const uint16_t* 
 
 size_t q38m_moe_prefill_workspace_bytes(uint32_t tokens) {
     if (tokens == 0 || tokens > Q38M_PREFILL_SLAB_MAX_TOKENS) return 0;
-    // plan, ids, weights, xq, xs, weighted_mid, mid_q, mid_s, route_output
+    // plan, ids, weights, xq, xs, weighted_mid, mid_q, mid_s, route_output,
+    // task_flags
     return q38m::prefill_workspace_bytes_v1(tokens);
 }
 
@@ -374,6 +413,8 @@ int q38m_moe_prefill_workspace_bind(void* allocation, size_t bytes, uint32_t tok
     out->mid_s = reinterpret_cast<float*>(cursor);
     cursor += align_up(routes * 4u, 256);
     out->route_output = reinterpret_cast<float*>(cursor);
+    cursor += align_up(routes * Q38M_HIDDEN * 4u, 256);
+    out->task_flags = reinterpret_cast<uint32_t*>(cursor);
     g_last_error.clear();
     return Q38M_OK;
 }
@@ -385,7 +426,8 @@ namespace {
 // The run_moe sequence over one slab on a bound workspace (arguments
 // validated by the caller): top-k + int8 rows (or int8 rows of given
 // ids), plan, gate/up, down (quantising the mid rows as it stages them),
-// combine.
+// combine; gate/up and down as one launch where the formats allow
+// (launch_gate_up_down), its hand-off flags cleared by the plan kernel.
 hipError_t launch_prefill_step(const q38m_expert_weights_v1& gate_up,
                                const q38m_expert_weights_v1& down, const uint16_t* hidden,
                                const float* logits, uint32_t tokens,
@@ -393,6 +435,8 @@ hipError_t launch_prefill_step(const q38m_expert_weights_v1& gate_up,
                                const uint16_t* shared_output, const uint16_t* shared_gate,
                                uint16_t* output, hipStream_t s) {
     const uint32_t tasks = q38m::max_tasks_v1(tokens);
+    // one launch for gate/up and down: the plan kernel clears its flags
+    const bool fused = ws.task_flags != nullptr && q38m::gate_up_down_fusable(gate_up, down);
     hipError_t status = hipSuccess;
     if (logits)
         status = q38m::launch_route_quantize(logits, hidden, tokens, Q38M_ROUTE_TOPK,
@@ -400,11 +444,19 @@ hipError_t launch_prefill_step(const q38m_expert_weights_v1& gate_up,
     else
         status = q38m::launch_quantize_rows(hidden, tokens, Q38M_HIDDEN, ws.xq, ws.xs, s);
     if (status == hipSuccess)
-        status = q38m::launch_build_plan(ws.expert_ids, tokens, ws.plan, false, s);
-    if (status == hipSuccess)
+        status = q38m::launch_build_plan(ws.expert_ids, tokens, ws.plan, false, s,
+                                         fused ? ws.task_flags : nullptr,
+                                         fused ? q38m::task_flag_words(tasks) : 0u);
+    if (status == hipSuccess && fused)
+        status = q38m::launch_gate_up_down(gate_up, down, ws.xq, ws.xs,
+                                           ws.plan.packed_assignment, ws.expert_weights,
+                                           ws.plan.tasks, tasks, ws.weighted_mid, ws.mid_q,
+                                           ws.mid_s, ws.route_output, ws.task_flags,
+                                           &ws.plan.header->status, s);
+    if (status == hipSuccess && !fused)
         status = q38m::launch_gate_up(gate_up, ws.xq, ws.xs, ws.plan.packed_assignment,
                                       ws.expert_weights, ws.plan.tasks, tasks, ws.weighted_mid, s);
-    if (status == hipSuccess)
+    if (status == hipSuccess && !fused)
         status = q38m::launch_down_quantize(down, ws.weighted_mid, ws.mid_q, ws.mid_s,
                                             ws.plan.tasks, tasks, ws.route_output, s);
     if (status == hipSuccess)
@@ -569,6 +621,13 @@ int q38m_moe_build_route_plan_wide(const int32_t* expert_ids, uint32_t tokens,
                   "chunk route-plan kernels");
 }
 
+// hand-off flags for q38m_moe_prefill_v1 on a chunk workspace: the V1 task
+// slots of the largest slab it holds
+static uint32_t slab_flag_words(uint32_t tokens) {
+    return q38m::task_flag_words(q38m::max_tasks_v1(
+        tokens < Q38M_PREFILL_SLAB_MAX_TOKENS ? tokens : Q38M_PREFILL_SLAB_MAX_TOKENS));
+}
+
 size_t q38m_moe_wide_workspace_bytes(uint32_t tokens) {
     if (tokens == 0 || tokens > Q38M_WIDE_MAX_TOKENS) return 0;
     const size_t routes = q38m::routes_v1(tokens);
@@ -581,6 +640,7 @@ size_t q38m_moe_wide_workspace_bytes(uint32_t tokens) {
     bytes += align_up(routes * Q38M_INTERMEDIATE, 256);                     // mid_q
     bytes += align_up(routes * 4u, 256);                                    // mid_s
     bytes += align_up(routes * Q38M_HIDDEN * 4u, 256);                      // route_output
+    bytes += align_up(static_cast<size_t>(slab_flag_words(tokens)) * 4u, 256);  // task_flags
     return bytes;
 }
 
@@ -612,6 +672,8 @@ int q38m_moe_wide_workspace_bind(void* allocation, size_t bytes, uint32_t tokens
     w.mid_s = reinterpret_cast<float*>(cursor);
     cursor += align_up(routes * 4u, 256);
     w.route_output = reinterpret_cast<float*>(cursor);
+    cursor += align_up(routes * Q38M_HIDDEN * 4u, 256);
+    w.task_flags = reinterpret_cast<uint32_t*>(cursor);
     g_last_error.clear();
     return Q38M_OK;
 }

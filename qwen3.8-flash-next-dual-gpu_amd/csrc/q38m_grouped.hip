@@ -38,6 +38,17 @@ __device__ __forceinline__ uint2 quantize_mid_row(uint4 v, float& scale) {
     return quantize8(hw, qs);
 }
 
+// Device-coherent (agent-scope) loads and stores: seen by every XCD
+// without a cache writeback or invalidation around them.
+template <typename T>
+__device__ __forceinline__ T load_device(const T* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void store_device(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct TileWeights {
     uint4 w;   // one quad of the wave's tile
     uint2 s;   // its scale words (load_quad_scales)
@@ -100,31 +111,33 @@ __device__ __forceinline__ void tile_quad(const uint2* __restrict__ a_quad, uint
 // bf16 scale words can sit near the subnormal range, so the fma takes s/16
 // (exact in fp32, subnormals included; |16*acc| < 2^24): each product is
 // acc*s exactly and the chain holds y itself.  Then y * s_t.
+//
+// gate_up_w4_item is one (task, channel slice) item of this plan, shared by
+// gate_up_w4_kernel (one item per workgroup) and gate_up_down_kernel: a_lds
+// holds H / 32 * 64 uint2, up_lds kWaves / 2 blocks of 4 x 64 floats.
+// kPublish (the fused launch): the mid words are stored device-coherently
+// and, once every wave's stores are complete, *flag is set to 1.
 // ---------------------------------------------------------------------------
-template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kSub, bool kBf16>
-__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6, 8)))
-void gate_up_w4_kernel(
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kSub, bool kBf16, bool kPublish>
+__device__ __forceinline__ void gate_up_w4_item(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s,
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
-    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    const TaskRecord task, const uint32_t slice, uint16_t* __restrict__ mid, uint2* a_lds,
+    float (*up_lds)[4][64], uint32_t* flag) {
     constexpr uint32_t kQuads = H / 128u;
-    constexpr uint32_t kGroups = H / 32u;
     constexpr uint32_t kTiles = 2u * I / 16u;
     constexpr uint32_t kThreads = kWaves * 64u;
     constexpr uint32_t kDepth = 2u, kSets = kDepth + 1u;
     static_assert(kWaves % 2u == 0u, "gate and up waves in pairs");
-    __shared__ uint2 a_lds[kGroups * 64u];
-    __shared__ float up_lds[kWaves / 2u][4][64];
 
-    const TaskRecord task = read_task(tasks, blockIdx.y);
     const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t n = lane & 15u;
     const uint32_t q = lane >> 4;
-    const uint32_t pair = blockIdx.x * (kWaves / 2u) + (wave >> 1);
+    const uint32_t pair = slice * (kWaves / 2u) + (wave >> 1);
     const uint32_t up = wave & 1u;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.begin;
@@ -207,21 +220,50 @@ void gate_up_w4_kernel(
         for (uint32_t i = 0; i < 4u; ++i) up_lds[wave >> 1][i][lane] = y[i];
     }
     __syncthreads();
-    if (up) return;
-    const uint32_t channel = pair * 16u + n;
-#pragma unroll
-    for (uint32_t i = 0; i < 4u; ++i) {
-        const uint32_t rr = 4u * q + i;
-        if (rr >= rows) continue;
-        const uint32_t p = p0 + rr;
-        const uint32_t a = checked(packed[p], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
-        const float st = xs[a / kTopK];
-        const float unscale = kBf16 ? 1.0f : 0.0625f;
-        const float y_gate = (y[i] * unscale) * st;
-        const float y_up = (up_lds[wave >> 1][i][lane] * unscale) * st;
-        mid[static_cast<size_t>(p) * I + channel] =
-            static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
+    if constexpr (!kPublish) {
+        if (up) return;
     }
+    if (!up) {
+        const uint32_t channel = pair * 16u + n;
+#pragma unroll
+        for (uint32_t i = 0; i < 4u; ++i) {
+            const uint32_t rr = 4u * q + i;
+            if (rr >= rows) continue;
+            const uint32_t p = p0 + rr;
+            const uint32_t a =
+                checked(packed[p], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
+            const float st = xs[a / kTopK];
+            const float unscale = kBf16 ? 1.0f : 0.0625f;
+            const float y_gate = (y[i] * unscale) * st;
+            const float y_up = (up_lds[wave >> 1][i][lane] * unscale) * st;
+            const uint16_t m = static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
+            if constexpr (kPublish)
+                store_device(mid + static_cast<size_t>(p) * I + channel, m);
+            else
+                mid[static_cast<size_t>(p) * I + channel] = m;
+        }
+    }
+    if constexpr (kPublish) {
+        // every wave's mid words have reached the device coherence point
+        // before the flag is set
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0u) store_device(flag, 1u);
+    }
+}
+
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kSub, bool kBf16>
+__global__ __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(6, 8)))
+void gate_up_w4_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s,
+    const int8_t* __restrict__ xq, const float* __restrict__ xs,
+    const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
+    const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
+    __shared__ uint2 a_lds[H / 32u * 64u];
+    __shared__ float up_lds[kWaves / 2u][4][64];
+    gate_up_w4_item<H, I, kWaves, kSub, kBf16, false>(w, s, xq, xs, packed, route_weights,
+                                                      read_task(tasks, blockIdx.y), blockIdx.x,
+                                                      mid, a_lds, up_lds, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -384,12 +426,55 @@ void gate_up_w8_kernel(
 // per wave) with a pinned one-unit-ahead prefetch; the launch uses 16 waves
 // of one tile each, and at ~51-71 VGPRs seven or eight waves per SIMD keep
 // ~128 KB of weights in flight per CU.
+//
+// down_w8_item is one (task, output slice) item, shared by down_w8_kernel
+// and gate_up_down_kernel: a_lds holds I / 64 * 64 uint4, scale_lds 16
+// floats.  kAwait (the fused launch, kQuantize only): every wave requests
+// its first weights, then wave 0 waits for the task's gate/up items
+// (await_gate_up) and the workgroup reads the mid rows once they are
+// complete; each item then counts itself in the task's counter, and the
+// last of the task's eight down items clears the task's flags and counter
+// at its end, so the flags are zero again when the launch ends.
 // ---------------------------------------------------------------------------
+
+// Poll budget of a down item waiting for its task's eight gate/up items:
+// each poll is one device-coherent load (~1-5 us under load) and a short
+// sleep.  Workgroups are dispatched in block order, so by the time a down
+// item waits, every gate/up item is resident or done and the wait ends
+// within a gate/up item's lifetime (~20 us); the budget only bounds it.
+constexpr uint32_t kAwaitPolls = 1u << 14;
+
+// Wave 0 of a down item: wait until the task's eight gate/up flags are set;
+// if the budget runs out, record Q38M_PLAN_STEP_TIMEOUT in *status and tell
+// the workgroup (expired_lds) to skip the item.
+__device__ __forceinline__ void await_gate_up(const uint32_t* flags, uint32_t* status,
+                                              uint32_t* expired_lds) {
+    const uint32_t lane = threadIdx.x & 63u;
+    bool expired = false;
+    for (uint32_t polls = 1u;; ++polls) {
+        const uint32_t v = lane < 8u ? load_device(flags + lane) : 1u;
+        if (__all(v == 1u)) break;
+        if (polls >= kAwaitPolls) {
+            expired = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    if (lane == 0u) {
+        *expired_lds = expired ? 1u : 0u;
+        if (expired)
+            __hip_atomic_fetch_or(status, Q38M_PLAN_STEP_TIMEOUT, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave,
-          uint32_t kBlocksPerGroup, bool kBf16, bool kQuantize>
-__global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
+          uint32_t kBlocksPerGroup, bool kBf16, bool kQuantize, bool kAwait>
+__device__ __forceinline__ void down_w8_item(
     const uint4* __restrict__ w, const uint16_t* __restrict__ s, MidRows mid,
-    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    const TaskRecord task, const uint32_t slice, float* __restrict__ out, uint4* a_lds,
+    float* scale_lds, uint32_t* flags, uint32_t* counter, uint32_t* status,
+    uint32_t* expired_lds) {
     constexpr uint32_t kBlocks = I / 64u;
     constexpr uint32_t kHalf = kBlocks / 2u;
     constexpr uint32_t kTiles = H / 16u;
@@ -398,10 +483,8 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     constexpr uint32_t kGroups = kBlocks / kBlocksPerGroup;
     static_assert(kBlocks % 2u == 0u, "half-tile units");
     static_assert(kPerChannel || kHalf % kBlocksPerGroup == 0u, "groups within half tiles");
-    __shared__ uint4 a_lds[kBlocks * 64u];
-    __shared__ float scale_lds[16];  // kQuantize: the rows' scales
+    static_assert(!kAwait || kQuantize, "the fused launch quantises the mid rows");
 
-    const TaskRecord task = read_task(tasks, blockIdx.y);
     const uint32_t rows = task.rows;
     if (rows == 0u) return;
     const uint32_t lane = threadIdx.x & 63u;
@@ -410,7 +493,7 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     const uint32_t q = lane >> 4;
     const uint32_t e = task.expert;
     const uint32_t p0 = task.begin;
-    const uint32_t tile0 = (blockIdx.x * kWaves + wave) * kTilesPerWave;
+    const uint32_t tile0 = (slice * kWaves + wave) * kTilesPerWave;
     const uint4* wt = w + static_cast<size_t>(e * kTiles + tile0) * kBlocks * 64u + lane;
 
     // Stage A: 16-byte chunk c of mid row r is K block c/4, lane group c%4.
@@ -421,17 +504,41 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
     static_assert(!kQuantize || (I == 512u && 16u % kWaves == 0u), "one wave per 512-wide row");
     float row_scale[4];
     uint4 b[kHalf];
+    uint32_t ticket = 0u;  // kAwait, wave 0 lane 0: the items of the task counted before this one
     if constexpr (kQuantize) {
         uint4 mv[kRowsPerWave];
+        auto load_rows = [&] {
 #pragma unroll
-        for (uint32_t j = 0; j < kRowsPerWave; ++j) {
-            const uint32_t r = wave * kRowsPerWave + j;
-            mv[j] = reinterpret_cast<const uint4*>(
-                mid.bf16 + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[lane];
+            for (uint32_t j = 0; j < kRowsPerWave; ++j) {
+                const uint32_t r = wave * kRowsPerWave + j;
+                mv[j] = reinterpret_cast<const uint4*>(
+                    mid.bf16 + static_cast<size_t>(p0 + (r < rows ? r : 0u)) * I)[lane];
+            }
+        };
+        if constexpr (kAwait) {
+            // the first weights stream while wave 0 waits; the rows are read
+            // (ordinary loads) only once every line of them is final: the
+            // fused launch started with no line of them in any L2, and the
+            // gate/up items wrote each 128-byte line of a row whole, through
+            // to the coherence point, before their flags
+#pragma unroll
+            for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
+            __builtin_amdgcn_sched_barrier(0);
+            if (wave == 0u) await_gate_up(flags, status, expired_lds);
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (*expired_lds != 0u) return;
+            // this item is past its wait: count it (the result is read at
+            // the item's end)
+            if (wave == 0u && lane == 0u)
+                ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+            load_rows();
+        } else {
+            load_rows();
+#pragma unroll
+            for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
+            __builtin_amdgcn_sched_barrier(0);
         }
-#pragma unroll
-        for (uint32_t kb = 0; kb < kHalf; ++kb) b[kb] = load_stream(wt + kb * 64u);
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (uint32_t j = 0; j < kRowsPerWave; ++j) {
             const uint32_t r = wave * kRowsPerWave + j;
@@ -442,7 +549,7 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
             reinterpret_cast<uint2*>(a_lds)[2u * ((chunk >> 2) * 64u + (chunk & 3u) * 16u + r) +
                                             (lane & 1u)] = qv;
             if (lane == 0u) scale_lds[r] = scale;
-            if (blockIdx.x == 0u && r < rows) {
+            if (slice == 0u && r < rows) {
                 reinterpret_cast<uint2*>(const_cast<int8_t*>(mid.q) +
                                          static_cast<size_t>(p0 + r) * I)[lane] = qv;
                 if (lane == 0u) const_cast<float*>(mid.s)[p0 + r] = scale;
@@ -538,6 +645,99 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
             out[static_cast<size_t>(p0 + r) * H + channel] = o;
         }
     }
+    if constexpr (kAwait) {
+        // the task's eighth down item: every item of the task is past its
+        // wait, so nothing reads the flags any more
+        if (wave == 0u && lane == 0u && ticket == 7u) {
+#pragma unroll
+            for (uint32_t i = 0; i < 8u; ++i) store_device(flags + i, 0u);
+            store_device(counter, 0u);
+        }
+    }
+}
+
+template <uint32_t H, uint32_t I, uint32_t kWaves, uint32_t kTilesPerWave,
+          uint32_t kBlocksPerGroup, bool kBf16, bool kQuantize>
+__global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
+    const uint4* __restrict__ w, const uint16_t* __restrict__ s, MidRows mid,
+    const q38m_task_v1* __restrict__ tasks, float* __restrict__ out) {
+    __shared__ uint4 a_lds[I / 64u * 64u];
+    __shared__ float scale_lds[16];  // kQuantize: the rows' scales
+    down_w8_item<H, I, kWaves, kTilesPerWave, kBlocksPerGroup, kBf16, kQuantize, false>(
+        w, s, mid, read_task(tasks, blockIdx.y), blockIdx.x, out, a_lds, scale_lds, nullptr,
+        nullptr, nullptr, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// Gate/up (W4) and down (W8) of a slab in ONE launch of 8-wave workgroups,
+// so that the down items start while the last gate/up items still stream
+// instead of after the launch boundary (config-2 step 0.2201 -> 0.2143 ms,
+// bit-identical).  Blocks [0, 8 * slots): gate/up items (task b / 8,
+// channel slice b % 8; gate_up_w4_item with kPublish); blocks
+// [8 * slots, 16 * slots): down items (task, 256 output channels;
+// down_w8_item as 8 waves x 2 tiles, kQuantize and kAwait).  Block b runs
+// on XCD b % 8, so both kinds keep their slice-to-XCD placement.
+//
+// The hand-off: a gate/up item stores its mid words device-coherently,
+// waits for them, then sets flags[8 * task + slice]; a down item's wave 0
+// polls the task's eight flags (device-coherent loads) while the first
+// weights stream, and the item then reads the mid rows.  The flags and the
+// per-task counters (flags[8 * slots + task]) are zero at the launch -- the
+// step's plan kernel clears them, and every launch leaves them zero (the
+// last down item of a task clears the task's words) -- unless a wait ran
+// out.  Workgroups are dispatched in block order, so every gate/up item has
+// been dispatched -- and, never waiting on anything, will finish -- before
+// any down item polls.
+// ---------------------------------------------------------------------------
+struct GateUpDownArgs {
+    const uint4* gate_up_w;
+    const uint16_t* gate_up_s;
+    const int8_t* xq;
+    const float* xs;
+    const uint32_t* packed;
+    const float* route_weights;
+    const q38m_task_v1* tasks;
+    uint16_t* weighted_mid;
+    const uint4* down_w;
+    const uint16_t* down_s;
+    int8_t* mid_q;
+    float* mid_s;
+    float* route_output;
+    uint32_t* flags;   // [9 * slots]: 8 flags per task, then a counter per task; zero
+    uint32_t* status;  // Q38M_PLAN_STEP_TIMEOUT on a wait that ran out
+    uint32_t slots;
+};
+
+template <uint32_t H, uint32_t I, uint32_t kSub, bool kGuBf16, uint32_t kDnBlocksPerGroup,
+          bool kDnBf16>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6, 8)))
+void gate_up_down_kernel(GateUpDownArgs a) {
+    constexpr uint32_t kWaves = 8u;
+    constexpr uint32_t kGateUpLds = H / 32u * 64u * 8u + kWaves / 2u * 4u * 64u * 4u;
+    constexpr uint32_t kDownLds = I / 64u * 64u * 16u + 16u * 4u + 4u;
+    __shared__ __align__(16) uint8_t lds[kGateUpLds > kDownLds ? kGateUpLds : kDownLds];
+    const uint32_t b = blockIdx.x;
+    if (b < 8u * a.slots) {
+        const uint32_t task = b >> 3, slice = b & 7u;
+        gate_up_w4_item<H, I, kWaves, kSub, kGuBf16, true>(
+            a.gate_up_w, a.gate_up_s, a.xq, a.xs, a.packed, a.route_weights,
+            read_task(a.tasks, task), slice, a.weighted_mid, reinterpret_cast<uint2*>(lds),
+            reinterpret_cast<float(*)[4][64]>(lds + H / 32u * 64u * 8u), a.flags + 8u * task + slice);
+        return;
+    }
+    const uint32_t task = (b - 8u * a.slots) >> 3, slice = b & 7u;
+    down_w8_item<H, I, kWaves, 2u, kDnBlocksPerGroup, kDnBf16, true, true>(
+        a.down_w, a.down_s, MidRows{a.mid_q, a.mid_s, a.weighted_mid}, read_task(a.tasks, task),
+        slice, a.route_output, reinterpret_cast<uint4*>(lds),
+        reinterpret_cast<float*>(lds + I / 64u * 64u * 16u), a.flags + 8u * task,
+        a.flags + 8u * a.slots + task, a.status,
+        reinterpret_cast<uint32_t*>(lds + I / 64u * 64u * 16u + 16u * 4u));
+}
+
+__global__ __launch_bounds__(256) void clear_words_kernel(uint32_t* __restrict__ p,
+                                                          uint32_t count) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < count) p[i] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -878,6 +1078,73 @@ hipError_t launch_gate_up(const q38m_expert_weights_v1& w, const int8_t* xq, con
                                          weighted_mid, stream); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+// W4 gate/up with per-channel W8 down, one scale dtype: at <= 64 VGPRs the
+// fused kernel keeps the gate/up kernel's four workgroups per CU (the
+// grouped W8 down items take 69-80)
+bool gate_up_down_fusable(const q38m_expert_weights_v1& gate_up,
+                          const q38m_expert_weights_v1& down) {
+    const bool gu = gate_up.format == Q38M_FORMAT_W4_SYM &&
+                    (gate_up.group_size == 32u || gate_up.group_size == 64u ||
+                     gate_up.group_size == 128u);
+    const bool dn = down.format == Q38M_FORMAT_W8_SYM && down.group_size == 0u;
+    return gu && dn && gate_up.scale_dtype == down.scale_dtype;
+}
+
+namespace {
+
+template <uint32_t kSub, bool kGuBf16, uint32_t kDnBlocksPerGroup, bool kDnBf16>
+void launch_gate_up_down_as(const GateUpDownArgs& a, hipStream_t stream) {
+    gate_up_down_kernel<kHidden, kInter, kSub, kGuBf16, kDnBlocksPerGroup, kDnBf16>
+        <<<16u * a.slots, 512, 0, stream>>>(a);
+}
+
+// one scale dtype for both projections, per-channel down (gate_up_down_fusable)
+template <uint32_t kSub>
+void launch_gate_up_down_gu(const q38m_expert_weights_v1& gate_up, const GateUpDownArgs& a,
+                            hipStream_t stream) {
+    constexpr uint32_t kBlocks = kInter / 64u;
+    if (gate_up.scale_dtype == Q38M_SCALE_BF16)
+        launch_gate_up_down_as<kSub, true, kBlocks, true>(a, stream);
+    else
+        launch_gate_up_down_as<kSub, false, kBlocks, false>(a, stream);
+}
+
+}  // namespace
+
+hipError_t launch_gate_up_down(const q38m_expert_weights_v1& gate_up,
+                               const q38m_expert_weights_v1& down, const int8_t* xq,
+                               const float* xs, const uint32_t* packed,
+                               const float* route_weights, const q38m_task_v1* tasks,
+                               uint32_t task_count, uint16_t* weighted_mid, int8_t* mid_q,
+                               float* mid_s, float* route_output, uint32_t* task_flags,
+                               uint32_t* status, hipStream_t stream) {
+    if (!gate_up_down_fusable(gate_up, down)) {
+        hipError_t rc = launch_gate_up(gate_up, xq, xs, packed, route_weights, tasks, task_count,
+                                       weighted_mid, stream);
+        if (rc == hipSuccess)
+            rc = launch_down_quantize(down, weighted_mid, mid_q, mid_s, tasks, task_count,
+                                      route_output, stream);
+        return rc;
+    }
+    const GateUpDownArgs a{static_cast<const uint4*>(gate_up.data),
+                           static_cast<const uint16_t*>(gate_up.scales),
+                           xq, xs, packed, route_weights, tasks, weighted_mid,
+                           static_cast<const uint4*>(down.data),
+                           static_cast<const uint16_t*>(down.scales),
+                           mid_q, mid_s, route_output, task_flags, status, task_count};
+    switch (gate_up.group_size) {
+        case 32u: launch_gate_up_down_gu<1>(gate_up, a, stream); break;
+        case 64u: launch_gate_up_down_gu<2>(gate_up, a, stream); break;
+        default: launch_gate_up_down_gu<4>(gate_up, a, stream); break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_clear_words(uint32_t* words, uint32_t count, hipStream_t stream) {
+    clear_words_kernel<<<(count + 255u) / 256u, 256, 0, stream>>>(words, count);
     return hipGetLastError();
 }
 

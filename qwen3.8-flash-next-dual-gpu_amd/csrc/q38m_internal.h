@@ -41,7 +41,8 @@ constexpr size_t prefill_workspace_bytes_v1(uint32_t tokens) {
            align256(static_cast<size_t>(routes_v1(tokens)) * kInter * 2u) +
            align256(static_cast<size_t>(routes_v1(tokens)) * kInter) +
            align256(routes_v1(tokens) * 4u) +
-           align256(static_cast<size_t>(routes_v1(tokens)) * kHidden * 4u);
+           align256(static_cast<size_t>(routes_v1(tokens)) * kHidden * 4u) +
+           align256(static_cast<size_t>(max_tasks_v1(tokens)) * 9u * 4u);
 }
 
 // chunks above the slab (q38m_wide.hip): 128-row tasks, plans built from
@@ -89,9 +90,12 @@ hipError_t launch_route_bf16(const uint16_t* logits, uint32_t tokens, uint32_t t
 hipError_t launch_route_quantize(const float* logits, const uint16_t* hidden, uint32_t tokens,
                                 uint32_t top_k, int32_t* ids, float* weights, int8_t* xq,
                                 float* xs, hipStream_t stream);
+// task_flags (may be null): flag_words words cleared while the ids load,
+// the hand-off flags of the fused gate/up + down launch that follows
 hipError_t launch_build_plan(const int32_t* ids, uint32_t tokens,
                              const q38m_route_plan_v1& plan, bool hashes,
-                             hipStream_t stream);
+                             hipStream_t stream, uint32_t* task_flags = nullptr,
+                             uint32_t flag_words = 0);
 
 // quantisation and gathers (q38m_quant.hip)
 hipError_t launch_quantize_rows(const uint16_t* x, uint32_t rows, uint32_t width,
@@ -119,6 +123,23 @@ hipError_t launch_down(const q38m_expert_weights_v1& w, const int8_t* mid_q, con
 hipError_t launch_down_quantize(const q38m_expert_weights_v1& w, const uint16_t* weighted_mid,
                                 int8_t* mid_q, float* mid_s, const q38m_task_v1* tasks,
                                 uint32_t task_count, float* route_output, hipStream_t stream);
+// gate/up and down (with the mid quantisation) in one launch when
+// gate_up_down_fusable (W4 gate/up, per-channel W8 down, one scale dtype);
+// otherwise launch_gate_up + launch_down_quantize.  task_flags:
+// task_flag_words(task_count) words, zero at the launch and left zero
+// (unless a wait ran out); status: where a down item whose wait ran out ORs
+// Q38M_PLAN_STEP_TIMEOUT.
+constexpr uint32_t task_flag_words(uint32_t task_count) { return 9u * task_count; }
+bool gate_up_down_fusable(const q38m_expert_weights_v1& gate_up,
+                          const q38m_expert_weights_v1& down);
+hipError_t launch_gate_up_down(const q38m_expert_weights_v1& gate_up,
+                               const q38m_expert_weights_v1& down, const int8_t* xq,
+                               const float* xs, const uint32_t* packed,
+                               const float* route_weights, const q38m_task_v1* tasks,
+                               uint32_t task_count, uint16_t* weighted_mid, int8_t* mid_q,
+                               float* mid_s, float* route_output, uint32_t* task_flags,
+                               uint32_t* status, hipStream_t stream);
+hipError_t launch_clear_words(uint32_t* words, uint32_t count, hipStream_t stream);
 hipError_t launch_combine(const float* route_output, const uint32_t* inverse,
                           const uint16_t* shared_output, const uint16_t* shared_gate,
                           uint32_t tokens, uint16_t* output, hipStream_t stream);

@@ -243,7 +243,8 @@ static_assert(kMaxRoutes / kPlanWaves <= 512u && kPlanWaves <= 128u,
 
 __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
     const int32_t* __restrict__ expert_ids, uint32_t tokens,
-    q38m_route_plan_v1 plan, uint32_t max_tasks) {
+    q38m_route_plan_v1 plan, uint32_t max_tasks, uint32_t* __restrict__ task_flags,
+    uint32_t flag_words) {
     __shared__ uint16_t key[kMaxRoutes];
     __shared__ uint16_t local_rank[kMaxRoutes];
     __shared__ uint16_t hist[kPlanWaves][kExperts];
@@ -269,6 +270,9 @@ __global__ __launch_bounds__(kPlanThreads) void build_plan_kernel(
         const uint32_t a = tid + i * kPlanThreads;
         loaded[i] = a < routes ? expert_ids[a] : 0;
     }
+    // the one-launch gate/up + down that follows in the step waits on these
+    // (q38m_grouped.hip, gate_up_down_kernel): cleared every call
+    for (uint32_t i = tid; i < flag_words; i += kPlanThreads) task_flags[i] = 0u;
     if (tid == 0) invalid = 0u;
     static_assert(kPlanWaves * kExperts * 2u == kPlanThreads * 16u, "one 16-byte clear per thread");
     reinterpret_cast<uint4*>(&hist[0][0])[tid] = make_uint4(0u, 0u, 0u, 0u);
@@ -534,9 +538,9 @@ hipError_t launch_route_bf16(const uint16_t* logits, uint32_t tokens, uint32_t t
 
 hipError_t launch_build_plan(const int32_t* ids, uint32_t tokens,
                              const q38m_route_plan_v1& plan, bool hashes,
-                             hipStream_t stream) {
-    build_plan_kernel<<<1, kPlanThreads, 0, stream>>>(ids, tokens, plan,
-                                                      max_tasks_v1(tokens));
+                             hipStream_t stream, uint32_t* task_flags, uint32_t flag_words) {
+    build_plan_kernel<<<1, kPlanThreads, 0, stream>>>(ids, tokens, plan, max_tasks_v1(tokens),
+                                                      task_flags, flag_words);
     if (hashes) plan_hash_kernel<<<1, 64, 0, stream>>>(ids, plan);
     return hipGetLastError();
 }

@@ -131,9 +131,10 @@ def test_workspace_binding(q38m):
     q38m.call("q38m_moe_prefill_workspace_bind", base, sizes[2], 512, ctypes.byref(ws))
     assert ws.max_tokens == 512 and ws.plan.header == base
     ptrs = [ws.expert_ids, ws.expert_weights, ws.xq, ws.xs, ws.weighted_mid, ws.mid_q,
-            ws.mid_s, ws.route_output]
+            ws.mid_s, ws.route_output, ws.task_flags]
     assert ptrs == sorted(ptrs) and all(p % 256 == 0 for p in ptrs)
-    assert ws.route_output + 5120 * 2048 * 4 <= base + sizes[2]
+    assert ws.route_output + 5120 * 2048 * 4 <= ws.task_flags
+    assert ws.task_flags + 9 * q38m.max_tasks(512) * 4 <= base + sizes[2]
     with pytest.raises(q38m.InvalidArgument):
         q38m.call("q38m_moe_prefill_workspace_bind", base + 16, sizes[2], 512, ctypes.byref(ws))
 
@@ -391,6 +392,39 @@ def test_slab_step_on_a_chunk_workspace(q38m):
             64 + 1024 + 2 * 2052 + 2 * 4 * 10 * tokens)
         assert task_bytes >= 8 * lib.q38m_moe_prefill_max_tasks_v1(slab)
         assert task_bytes >= 8 * lib.q38m_moe_wide_max_tasks(tokens)
+    # the slab step's hand-off flags: a V1 plan's task slots, inside the workspace
+    for tokens in (64, 4096):
+        q38m.call("q38m_moe_wide_workspace_bind", base, lib.q38m_moe_wide_workspace_bytes(tokens),
+                  tokens, ctypes.byref(wide))
+        step = wide.step
+        assert step.route_output + 10 * tokens * 2048 * 4 <= step.task_flags
+        assert (step.task_flags + 36 * lib.q38m_moe_prefill_max_tasks_v1(min(tokens, 512)) <=
+                base + lib.q38m_moe_wide_workspace_bytes(tokens))
+
+
+def test_gate_up_down_validation(q38m):
+    """q38m_moe_grouped_gate_up_down_v1 rejects what either staged entry
+    point rejects, and missing flags or status, before any launch."""
+    gu = fake_weights(q38m)
+    dn = fake_weights(q38m, fmt=3, group=0, layout=2, rows=2048, cols=512)
+    # xq, xs, packed, weights, tasks, task_count, mid, mid_q, mid_s, flags, status, out, mode
+    good = [0x1000, 0x2000, 0x3000, 0x4000, 0x5000, 16, 0x6000, 0x7000, 0x8000, 0x9000,
+            0xa000, 0xb000, q38m.MODE_GROUPED_MMQ]
+    bad_values = [(0, None), (1, None), (2, None), (3, None), (4, None), (5, 0),
+                  (5, q38m.max_tasks(512) + 1), (6, None), (7, None), (8, None), (9, None),
+                  (10, None), (11, None), (12, 3), (9, 0x9002), (0, 0x1004)]
+    for i, bad in bad_values:
+        args = list(good)
+        args[i] = bad
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_grouped_gate_up_down_v1", ctypes.byref(gu), ctypes.byref(dn),
+                      *args, None, 0)
+    with pytest.raises(q38m.InvalidArgument):  # down given as gate/up
+        q38m.call("q38m_moe_grouped_gate_up_down_v1", ctypes.byref(dn), ctypes.byref(dn), *good,
+                  None, 0)
+    for args in ([None, 16], [0x9000, 0], [0x9000, q38m.max_tasks(512) + 1], [0x9002, 16]):
+        with pytest.raises(q38m.InvalidArgument):
+            q38m.call("q38m_moe_clear_task_flags_v1", *args, None, 0)
 
 
 def test_combine_shared_validation(q38m):

@@ -24,13 +24,17 @@ def noalloc(q38m, layer, hidden, logits, tokens, shared=None):
     return out
 
 
-def test_noalloc_equals_prefill_on_two_calls(q38m, orc):
+@pytest.mark.parametrize("config", [1, 2])
+def test_noalloc_equals_prefill_on_two_calls(q38m, orc, config):
+    """config 1 (all-W4) runs gate/up and down as two launches, config 2
+    (W4 + per-channel W8) as one, whose hand-off flags live in the
+    device-resident workspace too."""
     t = torch()
-    gfmt, dfmt = W.layer_policy(1, 0)
-    layer = Layer(q38m, orc, W.CONFIGS[1]["seed"], 0, gfmt, dfmt, with_host=False)
+    gfmt, dfmt = W.layer_policy(config, 0)
+    layer = Layer(q38m, orc, W.CONFIGS[config]["seed"], 0, gfmt, dfmt, with_host=False)
     ws = q38m.PrefillWorkspace_(64)
     for tokens, tag in ((64, 11), (17, 12)):
-        print(f"noalloc: {tokens} tokens", flush=True)
+        print(f"noalloc: config {config}, {tokens} tokens", flush=True)
         hidden = synth_hidden(q38m, 5, tag, tokens)
         logits = synth_logits(q38m, 5, tag + 100, tokens)
         so = synth_hidden(q38m, 5, tag + 200, tokens)
