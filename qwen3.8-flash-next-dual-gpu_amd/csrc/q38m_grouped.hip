@@ -671,7 +671,7 @@ __global__ __launch_bounds__(kWaves * 64) void down_w8_kernel(
 // ---------------------------------------------------------------------------
 // Gate/up (W4) and down (W8) of a slab in ONE launch of 8-wave workgroups,
 // so that the down items start while the last gate/up items still stream
-// instead of after the launch boundary (config-2 step 0.2201 -> 0.2143 ms,
+// instead of after the launch boundary (config-2 step 0.2199 -> 0.2163 ms,
 // bit-identical).  Blocks [0, 8 * slots): gate/up items (task b / 8,
 // channel slice b % 8; gate_up_w4_item with kPublish); blocks
 // [8 * slots, 16 * slots): down items (task, 256 output channels;
