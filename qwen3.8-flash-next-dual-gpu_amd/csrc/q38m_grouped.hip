@@ -703,7 +703,7 @@ struct GateUpDownArgs {
     int8_t* mid_q;
     float* mid_s;
     float* route_output;
-    uint32_t* flags;   // [9 * slots]: 8 flags per task, then a counter per task; zero
+    uint32_t* flags;   // [9 * slots]: 8 flags per task, then a counter per task
     uint32_t* status;  // Q38M_PLAN_STEP_TIMEOUT on a wait that ran out
     uint32_t slots;
 };
@@ -722,7 +722,8 @@ void gate_up_down_kernel(GateUpDownArgs a) {
         gate_up_w4_item<H, I, kWaves, kSub, kGuBf16, true>(
             a.gate_up_w, a.gate_up_s, a.xq, a.xs, a.packed, a.route_weights,
             read_task(a.tasks, task), slice, a.weighted_mid, reinterpret_cast<uint2*>(lds),
-            reinterpret_cast<float(*)[4][64]>(lds + H / 32u * 64u * 8u), a.flags + 8u * task + slice);
+            reinterpret_cast<float(*)[4][64]>(lds + H / 32u * 64u * 8u),
+            a.flags + 8u * task + slice);
         return;
     }
     const uint32_t task = (b - 8u * a.slots) >> 3, slice = b & 7u;
