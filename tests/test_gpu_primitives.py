@@ -279,14 +279,20 @@ def run_plan(q38m, ids, tokens, hashes, poison=None):
 
 
 def reference_pattern(tokens, repeated):
+    """Distinct ids within every token (what top-k gives), all one id
+    ("all"), or distinct except one token that repeats an id ("one")."""
     a = np.arange(tokens * 10, dtype=np.int64)
-    if repeated:
+    if repeated == "all":
         return np.full(a.size, 7, np.int32)
-    return ((a * 73 + (a // 10) * 17) % 512).astype(np.int32)
+    ids = ((a * 73 + (a // 10) * 17) % 512).astype(np.int32)
+    if repeated == "one":
+        ids[10 * (tokens // 2) + 7] = ids[10 * (tokens // 2) + 3]
+    return ids
 
 
-@pytest.mark.parametrize("tokens,repeated", [(1, False), (2, False), (3, False), (128, False),
-                                             (512, False), (512, True), (100, False)])
+@pytest.mark.parametrize("tokens,repeated", [(1, None), (2, None), (3, None), (128, None),
+                                             (512, None), (512, "all"), (100, None),
+                                             (300, "one"), (512, "one")])
 @pytest.mark.parametrize("hashes", [False, True])
 def test_plan_bitwise(q38m, orc, tokens, repeated, hashes):
     ids = reference_pattern(tokens, repeated)
