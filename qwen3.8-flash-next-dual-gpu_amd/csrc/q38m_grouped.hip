@@ -114,7 +114,9 @@ __device__ __forceinline__ void tile_quad(const uint2* __restrict__ a_quad, uint
 //
 // gate_up_w4_item is one (task, channel slice) item of this plan, shared by
 // gate_up_w4_kernel (one item per workgroup) and gate_up_down_kernel: a_lds
-// holds H / 32 * 64 uint2, up_lds kWaves / 2 blocks of 4 x 64 floats.
+// holds H / 32 * 64 uint2, up_lds kWaves / 2 blocks of 4 x 64 floats,
+// row_info the task's 16 (token scale, route weight) pairs, read while the
+// rows stage so that the epilogue makes no global round trip.
 // kPublish (the fused launch): the mid words are stored device-coherently
 // and, once every wave's stores are complete, *flag is set to 1.
 // ---------------------------------------------------------------------------
@@ -124,7 +126,7 @@ __device__ __forceinline__ void gate_up_w4_item(
     const int8_t* __restrict__ xq, const float* __restrict__ xs,
     const uint32_t* __restrict__ packed, const float* __restrict__ route_weights,
     const TaskRecord task, const uint32_t slice, uint16_t* __restrict__ mid, uint2* a_lds,
-    float (*up_lds)[4][64], uint32_t* flag) {
+    float (*up_lds)[4][64], float2* row_info, uint32_t* flag) {
     constexpr uint32_t kQuads = H / 128u;
     constexpr uint32_t kTiles = 2u * I / 16u;
     constexpr uint32_t kThreads = kWaves * 64u;
@@ -174,6 +176,7 @@ __device__ __forceinline__ void gate_up_w4_item(
     const uint32_t srow = threadIdx.x % 16u;
     const uint32_t token = checked(packed[p0 + (srow < rows ? srow : 0u)],
                                    Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
+    if (threadIdx.x < 16u) row_info[srow] = make_float2(xs[token / kTopK], route_weights[token]);
     TileWeights r[kSets];
 #pragma unroll
     for (uint32_t i = 0; i < kDepth; ++i) r[i] = load(i);
@@ -230,13 +233,11 @@ __device__ __forceinline__ void gate_up_w4_item(
             const uint32_t rr = 4u * q + i;
             if (rr >= rows) continue;
             const uint32_t p = p0 + rr;
-            const uint32_t a =
-                checked(packed[p], Q38M_PREFILL_SLAB_MAX_TOKENS * kTopK, kCheckToken);
-            const float st = xs[a / kTopK];
+            const float2 info = row_info[rr];  // (token scale, route weight)
             const float unscale = kBf16 ? 1.0f : 0.0625f;
-            const float y_gate = (y[i] * unscale) * st;
-            const float y_up = (up_lds[wave >> 1][i][lane] * unscale) * st;
-            const uint16_t m = static_cast<uint16_t>(swiglu_fold(y_gate, y_up, route_weights[a]));
+            const float y_gate = (y[i] * unscale) * info.x;
+            const float y_up = (up_lds[wave >> 1][i][lane] * unscale) * info.x;
+            const uint16_t m = static_cast<uint16_t>(swiglu_fold(y_gate, y_up, info.y));
             if constexpr (kPublish)
                 store_device(mid + static_cast<size_t>(p) * I + channel, m);
             else
@@ -261,9 +262,10 @@ void gate_up_w4_kernel(
     const q38m_task_v1* __restrict__ tasks, uint16_t* __restrict__ mid) {
     __shared__ uint2 a_lds[H / 32u * 64u];
     __shared__ float up_lds[kWaves / 2u][4][64];
+    __shared__ float2 row_info[16];
     gate_up_w4_item<H, I, kWaves, kSub, kBf16, false>(w, s, xq, xs, packed, route_weights,
                                                       read_task(tasks, blockIdx.y), blockIdx.x,
-                                                      mid, a_lds, up_lds, nullptr);
+                                                      mid, a_lds, up_lds, row_info, nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -713,7 +715,7 @@ template <uint32_t H, uint32_t I, uint32_t kSub, bool kGuBf16, uint32_t kDnBlock
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6, 8)))
 void gate_up_down_kernel(GateUpDownArgs a) {
     constexpr uint32_t kWaves = 8u;
-    constexpr uint32_t kGateUpLds = H / 32u * 64u * 8u + kWaves / 2u * 4u * 64u * 4u;
+    constexpr uint32_t kGateUpLds = H / 32u * 64u * 8u + kWaves / 2u * 4u * 64u * 4u + 16u * 8u;
     constexpr uint32_t kDownLds = I / 64u * 64u * 16u + 16u * 4u + 4u;
     __shared__ __align__(16) uint8_t lds[kGateUpLds > kDownLds ? kGateUpLds : kDownLds];
     const uint32_t b = blockIdx.x;
@@ -723,6 +725,7 @@ void gate_up_down_kernel(GateUpDownArgs a) {
             a.gate_up_w, a.gate_up_s, a.xq, a.xs, a.packed, a.route_weights,
             read_task(a.tasks, task), slice, a.weighted_mid, reinterpret_cast<uint2*>(lds),
             reinterpret_cast<float(*)[4][64]>(lds + H / 32u * 64u * 8u),
+            reinterpret_cast<float2*>(lds + H / 32u * 64u * 8u + kWaves / 2u * 4u * 64u * 4u),
             a.flags + 8u * task + slice);
         return;
     }
