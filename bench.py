@@ -1631,7 +1631,8 @@ def bench_config5_stack(q38m, W, torch, passes=2):
 
 
 def bench_weight_pipeline(q38m, W, torch, reps=5):
-    """The load-time weight path of one layer: bf16
+    """The load-time weight path of one layer (the artifact compiler's
+    quantisation, tools/q38_artifact_compiler.py:193-253): bf16
     expert weights quantised on the device (quantize_groupwise: W4 g32
     gate/up, W8 per-channel down, fp16 scales) and repacked into the MFMA
     layouts.  HBM-bound; bytes = read + written."""

@@ -1,5 +1,6 @@
-"""The dense bf16 GEMMs on either side of the routed experts (SURVEY 8(f)
-ranks 1 and 2): the router logits and the shared expert.  They are
+"""The dense bf16 GEMMs on either side of the routed experts
+(cuda/cuda_backend.cu:1518-1525, 1573-1601): the router logits and the
+shared expert.  They are
 floating-point results, checked against a float64 CPU evaluation within a
 tolerance written here; the shared expert's SiLU multiply and everything
 downstream of the logits / shared inputs are bit-exact.
